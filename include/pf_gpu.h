@@ -1,0 +1,221 @@
+/*
+ * pf_gpu.h -- C ABI of libpocketforge_amd.so, the MI355X (gfx950) drop-in
+ * for PocketForge's MTP speculative-decoding hot path.
+ *
+ * Plain pointers and sizes only; no C++ or torch types cross this boundary.
+ * Every call returns PF_OK (0) or a negative pf_status; pf_last_error()
+ * gives the message (pf_last_error(NULL) for a failed pf_init).  Pointers named *_dev are device (HBM) pointers; all
+ * other pointers are host pointers.  Work is issued on the context's own
+ * HIP stream (default priority); calls that return host data synchronize
+ * that stream.  A context is not re-entrant: one host thread per context,
+ * as the reference's engine assumes (one Engine per process,
+ * src/forge_server.cpp:11).
+ *
+ * Reference interfaces replaced (reference file:line):
+ *   matmul kernels   include/forge/matmul_neon.hpp:20-92
+ *   3-tier KV cache  include/forge/kv_cache.hpp:33-56
+ *   MTP heads        include/forge/mtp.hpp:31-53
+ *   engine           include/forge/engine.hpp:15-74
+ *   types            include/forge/types.hpp:36-41, 220-268
+ */
+#ifndef PF_GPU_H
+#define PF_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t pf_status;
+#define PF_OK 0
+#define PF_ERR_ARG -1          /* invalid argument or shape */
+#define PF_ERR_HIP -2          /* HIP runtime error (message has the code) */
+#define PF_ERR_RANGE -3        /* block scales outside the exact-sum range */
+#define PF_ERR_UNSUPPORTED -4  /* shape outside what the kernels support */
+#define PF_ERR_STATE -5        /* call out of order (e.g. model incomplete) */
+#define PF_ERR_CAPACITY -6     /* position/token capacity exceeded */
+
+typedef struct pf_ctx pf_ctx;
+typedef struct pf_model pf_model;
+typedef struct pf_engine pf_engine;
+typedef struct pf_kv pf_kv;
+typedef struct pf_matrix pf_matrix;
+
+/* Weight formats: 32-element blocks with an fp16 scale d.
+ * Interchange layout (host): codes [rows][cols/32][16 (Q4) | 8 (Q2, Q1.5)]
+ * with the reference's element order (Q4: byte j = elements 2j (low
+ * nibble) and 2j+1, code = nibble - 8; Q2: byte j = elements 4j..4j+3 at
+ * bits 0,2,4,6, code = c - 2; Q1.5: same packing, code = c - 1 for
+ * c in {0,1,2}), scales [rows][cols/32] as IEEE binary16 bits. */
+#define PF_FMT_Q4 0
+#define PF_FMT_Q2 1
+#define PF_FMT_Q15 2
+
+/* Matrix ids within a layer follow the .squeeze matrix ids of
+ * src/quant_tool.cpp (0-6 = Q K V O gate up down). */
+#define PF_MAT_Q 0
+#define PF_MAT_K 1
+#define PF_MAT_V 2
+#define PF_MAT_O 3
+#define PF_MAT_GATE 4
+#define PF_MAT_UP 5
+#define PF_MAT_DOWN 6
+
+/* ------------------------------------------------------------ context */
+pf_status pf_init(int device, pf_ctx** out);
+void pf_destroy(pf_ctx* ctx);
+const char* pf_last_error(const pf_ctx* ctx);
+/* Device name and compute units, for reports. */
+pf_status pf_device_info(pf_ctx* ctx, char* name, size_t name_len, int* compute_units);
+pf_status pf_synchronize(pf_ctx* ctx);
+/* Device bytes currently held by all objects of this context. */
+size_t pf_device_bytes(const pf_ctx* ctx);
+/* Device memory for the *_dev arguments (plumbing for callers without
+ * their own allocator).  pf_memcpy kind: 0 host->device, 1 device->host,
+ * 2 device->device; it synchronizes the context's stream. */
+pf_status pf_malloc(pf_ctx* ctx, size_t bytes, void** out_dev);
+pf_status pf_free(pf_ctx* ctx, void* dev, size_t bytes);
+pf_status pf_memcpy(pf_ctx* ctx, void* dst, const void* src, size_t bytes, int32_t kind);
+
+/* ------------------------------------- weights (host side, no GPU use) */
+/* N(0, std^2) weights from Philox4x32-10 + Box-Muller (seed, stream), then
+ * the reference's block code rules (src/quant_format.cpp:77-154, with a
+ * multiplicative fp16 scale and Q1.5 threshold 0.35*amax). */
+pf_status pf_gen_matrix(uint64_t seed, uint32_t stream, float stddev, uint32_t rows, uint32_t cols,
+                        int32_t fmt, uint8_t* codes, uint16_t* scales);
+/* Quantizes given float weights with the same code rules. */
+pf_status pf_quantize_matrix(const float* w, uint32_t rows, uint32_t cols, int32_t fmt,
+                             uint8_t* codes, uint16_t* scales);
+
+/* ---------------------------- matmul_neon.hpp (device pointers, stream) */
+/* quantize_activation_row (include/forge/matmul_neon.hpp:20-25) on M rows. */
+pf_status pf_quantize_activation_rows(pf_ctx* ctx, const float* src_dev, int8_t* dst_dev,
+                                      float* scales_dev, uint32_t M, uint32_t K);
+/* matmul_int8 (include/forge/matmul_neon.hpp:55-62): C = A * B^T, int32. */
+pf_status pf_matmul_int8(pf_ctx* ctx, const int8_t* A_dev, const int8_t* B_dev, int32_t* C_dev,
+                         uint32_t M, uint32_t N, uint32_t K);
+/* matmul_quantized (include/forge/matmul_neon.hpp:68-77): per-row fp32
+ * weight scales; act_scales_dev may be NULL (computed per row). */
+pf_status pf_matmul_quantized(pf_ctx* ctx, const float* A_dev, const int8_t* B_dev, float* C_dev,
+                              uint32_t M, uint32_t N, uint32_t K, const float* w_scales_dev,
+                              const float* act_scales_dev);
+
+/* Block-quantized matrices resident in HBM. */
+pf_status pf_matrix_upload(pf_ctx* ctx, int32_t fmt, uint32_t rows, uint32_t cols, const uint8_t* codes,
+                           const uint16_t* scales, int32_t rowmajor, pf_matrix** out);
+void pf_matrix_free(pf_matrix* m);
+/* y[M][rows] = quantize_activation_row(x[m]) x W (tiled matrices), the
+ * fused matmul_quantized path with per-block scales. */
+pf_status pf_gemv_q(pf_ctx* ctx, const pf_matrix* W, const float* x_dev, float* y_dev, uint32_t M);
+/* y[M][rows] = fp32 x[m] . dequantized W rows (row-major Q4 matrices). */
+pf_status pf_gemv_f32(pf_ctx* ctx, const pf_matrix* W, const float* x_dev, float* y_dev, uint32_t M);
+
+/* ----------------------------------------------- kv_cache.hpp (3-tier) */
+typedef struct {
+    uint32_t n_layers, n_kv_heads, head_dim;
+    uint32_t sink_size, window_size, pool_block, max_context;
+} pf_kv_config;   /* KVCacheConfig, include/forge/kv_cache.hpp:23-31 */
+
+pf_status pf_kv_create(pf_ctx* ctx, const pf_kv_config* cfg, pf_kv** out);
+void pf_kv_destroy(pf_kv* kv);
+/* KVCache::store (include/forge/kv_cache.hpp:37-38); key/value are host
+ * pointers of head_dim floats. */
+pf_status pf_kv_store(pf_kv* kv, uint32_t layer, uint32_t head, uint32_t pos, const float* key,
+                      const float* value);
+/* KVCache::attention_scores (kv_cache.hpp:41-45): writes *count scores. */
+pf_status pf_kv_attention_scores(pf_kv* kv, uint32_t layer, uint32_t head, const float* query,
+                                 float* scores_out, uint32_t* count);
+/* KVCache::attention_weighted_sum (kv_cache.hpp:47-52), 64-entry chunks. */
+pf_status pf_kv_attention_weighted_sum(pf_kv* kv, uint32_t layer, uint32_t head, const float* scores,
+                                       float* output, uint32_t count);
+uint32_t pf_kv_size(const pf_kv* kv);
+pf_status pf_kv_clear(pf_kv* kv);
+size_t pf_kv_memory_usage(const pf_kv* kv);
+
+/* --------------------------------------------------------------- model */
+typedef struct {
+    uint32_t n_layers, n_embd, n_heads, head_dim, n_ff, n_vocab, n_mtp;
+} pf_model_desc;  /* ModelConfig subset, include/forge/types.hpp:220-254 (MHA) */
+
+pf_status pf_model_create(pf_ctx* ctx, const pf_model_desc* desc, pf_model** out);
+void pf_model_destroy(pf_model* m);
+/* Layer matrix `id` (PF_MAT_*), interchange layout.  Q/K/V must share a
+ * format, as must gate/up. */
+pf_status pf_model_set_matrix(pf_model* m, uint32_t layer, int32_t id, int32_t fmt, const uint8_t* codes,
+                              const uint16_t* scales);
+/* Tied embedding / unembedding table [n_vocab][n_embd], Q4. */
+pf_status pf_model_set_embedding(pf_model* m, const uint8_t* codes, const uint16_t* scales);
+/* MTP head k matrix which (0 gate, 1 up, 2 down), n_embd x n_embd Q4. */
+pf_status pf_model_set_mtp(pf_model* m, uint32_t head, int32_t which, const uint8_t* codes,
+                           const uint16_t* scales);
+/* RMSNorm weights: which 7 = attention, 8 = FFN (default 1.0). */
+pf_status pf_model_set_norm(pf_model* m, uint32_t layer, int32_t which, const float* w);
+
+/* -------------------------------------------------------------- engine */
+typedef struct {
+    float temperature;
+    float top_p;
+    uint32_t top_k;
+    int32_t greedy;
+} pf_sampling;  /* SamplingConfig, include/forge/types.hpp:36-41 */
+
+typedef struct {
+    uint32_t n_tokens;        /* tokens written (prompt included) */
+    int32_t mtp_accepted;
+    int32_t mtp_rejected;
+    int32_t oom_protected;
+    uint32_t rounds;          /* MTP rounds */
+    uint32_t passes;          /* forward passes issued (prefill excluded) */
+    double prefill_seconds;
+    double decode_seconds;
+} pf_gen_result;  /* GenerationResult, include/forge/types.hpp:260-268 */
+
+typedef struct {
+    uint32_t sink_size, window_size, pool_block, max_context;
+} pf_cache_desc;
+
+pf_status pf_engine_create(pf_model* m, const pf_cache_desc* cache, pf_engine** out);
+void pf_engine_destroy(pf_engine* e);
+/* Clears the cache and the position counter. */
+pf_status pf_engine_reset(pf_engine* e);
+uint32_t pf_engine_position(const pf_engine* e);
+/* Engine::forward_with_hidden (engine.hpp:38-41) for n <= 8 consecutive
+ * tokens in one pass; row j equals the j-th of n sequential forwards.
+ * logits [n][n_vocab] and hidden [n][n_embd] may be NULL. */
+pf_status pf_forward(pf_engine* e, const int32_t* tokens, uint32_t n, float* logits, float* hidden);
+/* MTPHeads::forward (mtp.hpp:40-43) with the tied table: logits
+ * [n_mtp][n_vocab] from a pre-norm hidden state. */
+pf_status pf_mtp_forward(pf_engine* e, const float* hidden, float* logits);
+/* Engine::sample (engine.hpp:54-60) on a host logits row; *draw_index is
+ * the stochastic draw counter (incremented when a uniform is used). */
+pf_status pf_sample(pf_engine* e, const float* logits, const pf_sampling* cfg, uint64_t seed,
+                    uint64_t* draw_index, int32_t* token);
+/* Engine::generate (engine.hpp:27-32) with the sampling configuration
+ * passed explicitly.  tokens_out receives prompt + generated tokens. */
+pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n_prompt, uint32_t max_new_tokens,
+                      const pf_sampling* cfg, uint64_t seed, int32_t* tokens_out, uint32_t tokens_cap,
+                      pf_gen_result* result);
+/* Engine::set_max_memory (engine.hpp:25): generate stops with
+ * oom_protected when the context's device bytes exceed this (0 = off). */
+pf_status pf_engine_set_max_memory(pf_engine* e, size_t bytes);
+
+/* Timing hook for benchmarks: average device time in microseconds of the
+ * verify passes (M = n_mtp + 1) and base passes (M = 1) issued by the last
+ * pf_generate, measured with HIP events on the engine's stream. */
+pf_status pf_engine_pass_times(const pf_engine* e, double* verify_us, double* base_us,
+                               uint32_t* verify_n, uint32_t* base_n);
+
+/* Profiling mode: brackets every int8 GEMV launch of the verify passes of
+ * pf_generate with HIP events on the engine's stream. */
+pf_status pf_engine_profile(pf_engine* e, int32_t enable);
+/* Launch count, average duration (us) and average algorithmic bytes
+ * (packed weights + int8 activations + fp32 outputs) of the GEMV launches
+ * recorded by the last pf_generate in profiling mode. */
+pf_status pf_engine_gemv_stats(pf_engine* e, uint32_t* launches, double* avg_us, double* avg_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -949,6 +949,16 @@ int32_t orc_sample(const float* logits, uint32_t V, const orc_sampling* cfg,
 
 /* ============================================================ generate */
 
+#include <time.h>
+static double g_last_decode_seconds = 0.0;
+static double now_s(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+/* Wall time of the decode loop (after the prompt) of the last orc_generate. */
+double orc_last_decode_seconds(void) { return g_last_decode_seconds; }
+
 /* Engine::generate, src/engine.cpp:276-396, MTP branch :304-373 and the
  * fallback :377-386, with the sampling configuration passed explicitly.
  * Returns 0, or -1 when tokens_cap is too small. */
@@ -968,6 +978,7 @@ int32_t orc_generate(orc_engine* e, const int32_t* prompt, uint32_t n_prompt,
 #define PUSH(t) do { if (nt >= cap) { nt = cap + 1; goto done; } tokens[nt++] = (t); } while (0)
     for (uint32_t i = 0; i < n_prompt; i++) orc_forward(e, prompt[i], NULL, NULL);
     for (uint32_t i = 0; i < n_prompt; i++) PUSH(prompt[i]);
+    double t_dec = now_s();
     uint32_t n_gen = 0;
     int32_t cur = n_prompt ? prompt[n_prompt - 1] : 0;
     while (n_gen < max_new) {
@@ -1000,6 +1011,7 @@ int32_t orc_generate(orc_engine* e, const int32_t* prompt, uint32_t n_prompt,
     }
 done:
 #undef PUSH
+    g_last_decode_seconds = now_s() - t_dec;
     free(logits); free(mtp_logits); free(hid); free(preds);
     *n_tokens = nt > cap ? cap : nt;
     *mtp_accepted = acc_total; *mtp_rejected = rej_total;

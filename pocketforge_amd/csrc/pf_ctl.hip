@@ -1,0 +1,332 @@
+// Sampling, acceptance and decode-round control on the device.
+//
+// Engine::sample's dispatch (src/engine.cpp:881-916): greedy when
+// cfg.greedy or temperature <= 0; else top-p when 0 < top_p < 1 (top-k is
+// then ignored); else top-k when 0 < top_k < V; else full-vocabulary
+// temperature sampling.  One uniform per stochastic call, drawn from
+// Philox4x32-10 keyed by the run seed with the draw index as counter.
+//
+// The decode round (src/engine.cpp:304-373) runs as: sample T1 from the
+// base logits, sample one draft per MTP head, one verify pass over
+// [T1, d0..d{n-1}], greedy argmax of every verify row, accept the longest
+// matching prefix, sample the corrective from the first mismatching row.
+// Every token decision is made here; the host reads one 32-bit word per
+// round (accepted count | corrective pushed << 8).
+#include "pf_device.h"
+
+namespace pf {
+
+struct ArgBest { float v; int32_t i; };
+
+__device__ __forceinline__ ArgBest arg_better(ArgBest a, ArgBest b) {
+    if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+    return a;
+}
+
+// First index of the maximum (src/engine.cpp:918-928) of a row, computed by
+// a 1024-thread block.  Result valid in thread 0.
+__device__ ArgBest block_argmax(const float* __restrict__ x, uint32_t V) {
+    __shared__ float sv[16];
+    __shared__ int32_t si[16];
+    ArgBest b{-__builtin_inff(), 0x7FFFFFFF};
+    for (uint32_t i = threadIdx.x; i < V; i += blockDim.x) b = arg_better(b, ArgBest{x[i], (int32_t)i});
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        ArgBest o{__shfl_xor(b.v, off, 64), __shfl_xor(b.i, off, 64)};
+        b = arg_better(b, o);
+    }
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = b.v; si[threadIdx.x >> 6] = b.i; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (uint32_t w = 1; w < blockDim.x / 64; w++) b = arg_better(b, ArgBest{sv[w], si[w]});
+        if (b.i == 0x7FFFFFFF) b.i = 0;
+    }
+    __syncthreads();
+    return b;
+}
+
+// row_argmax[m] for every row of a pass.  Grid M, 1024 threads.
+__global__ __launch_bounds__(1024) void k_argmax_rows(const float* __restrict__ logits, uint32_t stride,
+                                                      uint32_t V, const PassDesc* __restrict__ pd,
+                                                      int32_t* __restrict__ out) {
+    if (blockIdx.x >= pd->m) return;
+    ArgBest b = block_argmax(logits + (size_t)blockIdx.x * stride, V);
+    if (threadIdx.x == 0) out[blockIdx.x] = b.i;
+}
+
+// ----------------------------------------------------- stochastic sampler
+
+__device__ __forceinline__ uint32_t ord_f(float f) {
+    uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Bitonic sort of n (power of two) 64-bit keys in LDS, ascending.
+__device__ void lds_bitonic(uint64_t* a, uint32_t n) {
+    for (uint32_t k = 2; k <= n; k <<= 1) {
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+                uint32_t l = i ^ j;
+                if (l > i) {
+                    uint64_t x = a[i], y = a[l];
+                    bool up = (i & k) == 0;
+                    if ((x > y) == up) { a[i] = y; a[l] = x; }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// LDS arena for the sampler: 16384 64-bit slots (128 KiB).
+constexpr uint32_t SAMPLE_MAX_V = 16384;
+
+// Sorted (logit desc, index asc) order into `a` (hi = ord bits, lo = idx);
+// returns the padded power-of-two size.
+__device__ uint32_t sort_desc(const float* __restrict__ x, uint32_t V, uint64_t* a) {
+    uint32_t n = 1;
+    while (n < V) n <<= 1;
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x)
+        a[i] = i < V ? (((uint64_t)(~ord_f(x[i]))) << 32) | i : ~0ull;
+    __syncthreads();
+    lds_bitonic(a, n);
+    return n;
+}
+
+__device__ __forceinline__ float key_val(uint64_t k) {
+    uint32_t o = ~(uint32_t)(k >> 32);
+    uint32_t u = (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o;
+    return __uint_as_float(u);
+}
+
+// Chunk-of-64 sum and scan over p[0..n) held in the high words of `a`
+// (float bits) by wave 0: chunk totals left to right, running prefix from
+// the chunk's offset.  Returns the first index with cum >= thr1 (or n) and
+// the first index with thr2 <= cum (or n).  Valid in wave 0.
+struct ScanHit { uint32_t first_ge1, first_ge2; };
+
+__device__ __forceinline__ float slot_f(uint64_t k) { return __uint_as_float((uint32_t)(k >> 32)); }
+
+__device__ float chunk64_total(const uint64_t* a, uint32_t n, float* tot_lds) {
+    const uint32_t lane = threadIdx.x, cl = (n + 63u) / 64u;
+    float t = 0.0f;
+    for (uint32_t i = lane * cl; i < n && i < (lane + 1) * cl; i++) t = t + slot_f(a[i]);
+    tot_lds[lane] = t;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    float s = 0.0f;
+    for (uint32_t b = 0; b < 64; b++) s = s + tot_lds[b];
+    return s;
+}
+
+__device__ ScanHit chunk64_scan(const uint64_t* a, uint32_t n, float thr1, float thr2, float* tot_lds) {
+    const uint32_t lane = threadIdx.x, cl = (n + 63u) / 64u;
+    float t = 0.0f;
+    for (uint32_t i = lane * cl; i < n && i < (lane + 1) * cl; i++) t = t + slot_f(a[i]);
+    tot_lds[lane] = t;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    float off = 0.0f;
+    for (uint32_t b = 0; b < lane; b++) off = off + tot_lds[b];
+    uint32_t h1 = n, h2 = n;
+    float c = off;
+    for (uint32_t i = lane * cl; i < n && i < (lane + 1) * cl; i++) {
+        c = c + slot_f(a[i]);
+        if (h1 == n && c >= thr1) h1 = i;
+        if (h2 == n && thr2 <= c) h2 = i;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        h1 = min(h1, (uint32_t)__shfl_xor((int)h1, o, 64));
+        h2 = min(h2, (uint32_t)__shfl_xor((int)h2, o, 64));
+    }
+    return ScanHit{h1, h2};
+}
+
+// Engine::sample of one logits row.  1024 threads.  Returns the token in
+// thread 0.  `draw` is the draw index to use for a stochastic call.
+__device__ int32_t sample_row(const float* __restrict__ x, uint32_t V, const SamplingCfg& cfg, uint64_t seed,
+                              uint64_t draw, bool* used_draw) {
+    __shared__ uint64_t arena[SAMPLE_MAX_V];
+    __shared__ float tot[64];
+    __shared__ float bcast[2];
+    *used_draw = false;
+    if (cfg.greedy || cfg.temperature <= 0.0f) return block_argmax(x, V).i;
+    *used_draw = true;
+    const float temp = cfg.temperature > 0.001f ? cfg.temperature : 0.001f;
+    const float r = uniform(seed, draw);
+    int32_t result = 0;
+    if (cfg.top_p < 1.0f && cfg.top_p > 0.0f) {            // src/engine.cpp:961-1003
+        sort_desc(x, V, arena);
+        const float mx = key_val(arena[0]);
+        for (uint32_t i = threadIdx.x; i < V; i += blockDim.x) {
+            uint64_t k = arena[i];
+            float p = expf_c((key_val(k) - mx) / temp);
+            arena[i] = ((uint64_t)__float_as_uint(p) << 32) | (uint32_t)k;
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            float sum = chunk64_total(arena, V, tot);
+            if (threadIdx.x == 0) bcast[0] = sum;
+        }
+        __syncthreads();
+        const float sum = bcast[0];
+        for (uint32_t i = threadIdx.x; i < V; i += blockDim.x) {
+            uint64_t k = arena[i];
+            float p = slot_f(k) / sum;
+            arena[i] = ((uint64_t)__float_as_uint(p) << 32) | (uint32_t)k;
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            ScanHit h = chunk64_scan(arena, V, cfg.top_p, r, tot);
+            uint32_t cutoff = h.first_ge1 < V ? h.first_ge1 + 1 : V;
+            uint32_t pick = h.first_ge2 < cutoff ? h.first_ge2 : cutoff - 1;
+            if (threadIdx.x == 0) result = (int32_t)(uint32_t)arena[pick];
+        }
+    } else if (cfg.top_k > 0 && cfg.top_k < V) {           // src/engine.cpp:930-959
+        sort_desc(x, V, arena);
+        if (threadIdx.x == 0) {
+            const uint32_t k = cfg.top_k;
+            const float mx = key_val(arena[0]);
+            float sum = 0.0f;
+            for (uint32_t i = 0; i < k; i++) sum = sum + expf_c((key_val(arena[i]) - mx) / temp);
+            float cum = 0.0f;
+            result = (int32_t)(uint32_t)arena[k - 1];
+            for (uint32_t i = 0; i < k; i++) {
+                cum = cum + expf_c((key_val(arena[i]) - mx) / temp) / sum;
+                if (r <= cum) { result = (int32_t)(uint32_t)arena[i]; break; }
+            }
+        }
+    } else {                                               // src/engine.cpp:895-915
+        float* fa = reinterpret_cast<float*>(arena);
+        float mx = -__builtin_inff();
+        {
+            ArgBest b = block_argmax(x, V);
+            if (threadIdx.x == 0) bcast[1] = b.v;
+            __syncthreads();
+            mx = bcast[1];
+        }
+        for (uint32_t i = threadIdx.x; i < V; i += blockDim.x) {
+            float p = expf_c((x[i] - mx) / temp);
+            arena[i] = ((uint64_t)__float_as_uint(p) << 32) | i;
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            float sum = chunk64_total(arena, V, tot);
+            if (threadIdx.x == 0) bcast[0] = sum;
+        }
+        __syncthreads();
+        const float sum = bcast[0];
+        for (uint32_t i = threadIdx.x; i < V; i += blockDim.x) {
+            uint64_t k = arena[i];
+            float p = slot_f(k) / sum;
+            arena[i] = ((uint64_t)__float_as_uint(p) << 32) | (uint32_t)k;
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            ScanHit h = chunk64_scan(arena, V, 2.0f, r, tot);
+            if (threadIdx.x == 0) result = h.first_ge2 < V ? (int32_t)h.first_ge2 : (int32_t)V - 1;
+        }
+        (void)fa;
+    }
+    __syncthreads();
+    return result;
+}
+
+// Roles of a sample call inside the decode round.
+enum SampleRole : int32_t {
+    ROLE_PLAIN = 0,       // write the token to *out
+    ROLE_T1 = 1,          // push; it is row 0 of the verify pass
+    ROLE_DRAFT = 2,       // draft of head `k`: row k+1 of the verify pass
+    ROLE_CORRECTIVE = 3,  // corrective of the first mismatching verify row
+    ROLE_FALLBACK = 4,    // single-token path: push, becomes `cur`
+};
+
+__device__ __forceinline__ void push_token(DecodeState* st, int32_t* tokens, uint32_t cap, int32_t t) {
+    if (st->n_tokens < cap) tokens[st->n_tokens] = t;
+    st->n_tokens++;
+    st->n_gen++;
+    st->cur = t;
+}
+
+// One Engine::sample call.  Row `row` of `logits` (row < 0: the verify row
+// of the first mismatch, st->round_acc).  Grid 1, 1024 threads.
+__global__ __launch_bounds__(1024) void k_sample(const float* __restrict__ logits, uint32_t stride, int32_t row,
+                                                 uint32_t V, SamplingCfg cfg, uint64_t seed, DecodeState* st,
+                                                 int32_t* tokens, uint32_t cap, PassDesc* pdB, int32_t role,
+                                                 int32_t k, int32_t* out) {
+    __shared__ uint32_t skip;
+    if (threadIdx.x == 0) {
+        uint32_t n_mtp = pdB ? pdB->m - 1 : 0;
+        skip = (role == ROLE_CORRECTIVE && st->round_acc >= n_mtp) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (skip) return;
+    const uint32_t r = row >= 0 ? (uint32_t)row : st->round_acc;
+    bool used = false;
+    const int32_t t = sample_row(logits + (size_t)r * stride, V, cfg, seed, st->draw, &used);
+    if (threadIdx.x != 0) return;
+    if (used) st->draw++;
+    switch (role) {
+        case ROLE_T1:
+            push_token(st, tokens, cap, t);
+            pdB->tok[0] = t;
+            pdB->pos0 = st->pos;
+            break;
+        case ROLE_DRAFT:
+            st->draft[k] = t;
+            pdB->tok[k + 1] = t;
+            break;
+        case ROLE_CORRECTIVE: {
+            uint32_t a = st->round_acc;
+            uint32_t pushed = 0;
+            if (t != st->draft[a]) { push_token(st, tokens, cap, t); st->rejected++; pushed = 1; }
+            st->round_word = a | (pushed << 8);
+            break;
+        }
+        case ROLE_FALLBACK:
+            push_token(st, tokens, cap, t);
+            break;
+        default:
+            if (out) *out = t;
+    }
+}
+
+// Pass A setup: forward `cur` at the next position.
+__global__ void k_ctl_pass_a(DecodeState* st, PassDesc* pdA) {
+    pdA->pos0 = st->pos;
+    pdA->m = 1;
+    pdA->tok[0] = st->cur;
+    st->pos += 1;
+    st->have_row4 = 0;
+}
+
+// The last verify row already holds F(cur) at position st->pos.
+__global__ void k_ctl_reuse_row(DecodeState* st) {
+    st->pos += 1;
+    st->have_row4 = 0;
+}
+
+// Acceptance (src/engine.cpp:333-365) given the greedy argmax of every
+// verify row: accepted prefix pushed, positions committed.
+__global__ void k_ctl_accept(DecodeState* st, const PassDesc* pdB, int32_t* tokens, uint32_t cap) {
+    const uint32_t n_mtp = pdB->m - 1;
+    uint32_t a = 0;
+    while (a < n_mtp && st->row_argmax[a] == st->draft[a]) {
+        push_token(st, tokens, cap, st->draft[a]);
+        a++;
+    }
+    st->round_acc = a;
+    st->accepted += a;
+    if (a < n_mtp) {
+        st->pos = pdB->pos0 + a + 1;
+        st->have_row4 = 0;
+    } else {
+        st->pos = pdB->pos0 + n_mtp;
+        st->have_row4 = 1;
+    }
+    st->round_word = a;
+}
+
+}  // namespace pf

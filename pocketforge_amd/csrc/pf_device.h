@@ -1,0 +1,235 @@
+// Device-side helpers shared by the gfx950 kernels.
+//
+// Float results of the hot path must be bit-identical to the CPU restatement,
+// so every reduction here has one fixed association order and every fused
+// multiply-add is written explicitly (the library is compiled with
+// -ffp-contract=off).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "pf_layout.h"
+
+#define PF_WAVE 64
+
+namespace pf {
+
+__device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
+
+// exp(x): Cody-Waite reduction x = k*ln2 + r with ln2 split into a 16-bit
+// head and a tail, degree-7 Taylor polynomial of exp(r) in Horner form,
+// scaling by 2^k through the exponent field.  x < -86 gives 0 and x > 88
+// gives +inf, so no subnormal result is formed.
+__device__ __forceinline__ float expf_c(float x) {
+    if (x != x) return x;
+    if (x < -86.0f) return 0.0f;
+    if (x > 88.0f) return __builtin_inff();
+    float kf = __builtin_rintf(x * 1.44269502162933349609375f);
+    float r = __builtin_fmaf(kf, -0.693145751953125f, x);
+    r = __builtin_fmaf(kf, -1.42860676533018704503775e-06f, r);
+    float p = 1.98412698412698412698e-4f;
+    p = __builtin_fmaf(p, r, 1.38888888888888888889e-3f);
+    p = __builtin_fmaf(p, r, 8.33333333333333333333e-3f);
+    p = __builtin_fmaf(p, r, 4.16666666666666666667e-2f);
+    p = __builtin_fmaf(p, r, 1.66666666666666666667e-1f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    int k = (int)kf;
+    return p * u2f((uint32_t)(k + 127) << 23);
+}
+
+// IEEE binary16 bits -> float (exact).
+__device__ __forceinline__ float h2f(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    if (e == 0) {
+        float v = (float)m * 0x1p-24f;
+        return sign ? -v : v;
+    }
+    if (e == 31) return u2f(sign | 0x7F800000u | (m << 13));
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+// Philox4x32-10 (Salmon et al., SC'11).
+__device__ __forceinline__ void philox(uint32_t c[4], uint32_t k0, uint32_t k1) {
+    for (int r = 0; r < 10; r++) {
+        if (r > 0) { k0 += 0x9E3779B9u; k1 += 0xBB67AE85u; }
+        uint32_t lo0 = 0xD2511F53u * c[0], hi0 = __umulhi(0xD2511F53u, c[0]);
+        uint32_t lo1 = 0xCD9E8D57u * c[2], hi1 = __umulhi(0xCD9E8D57u, c[2]);
+        uint32_t n0 = hi1 ^ c[1] ^ k0, n2 = hi0 ^ c[3] ^ k1;
+        c[0] = n0; c[1] = lo1; c[2] = n2; c[3] = lo0;
+    }
+}
+
+// Uniform in [0,1) for stochastic draw number idx of a run seeded `seed`.
+__device__ __forceinline__ float uniform(uint64_t seed, uint64_t idx) {
+    uint32_t c[4] = {(uint32_t)idx, (uint32_t)(idx >> 32), 0x53414D50u, 0u};
+    philox(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+    return (float)(c[0] >> 8) * 0x1p-24f;
+}
+
+// ---------------------------------------------------------------- waves
+
+__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, PF_WAVE); }
+__device__ __forceinline__ double shfl_xor(double v, int m) { return __shfl_xor(v, m, PF_WAVE); }
+
+// Halving tree over the 64 lanes of a wave: after the butterfly every lane
+// holds ((P0+P32)+(P16+P48)) ... in the order offsets 32,16,8,4,2,1.
+__device__ __forceinline__ float wave_tree_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = v + shfl_xor(v, off);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, shfl_xor(v, off));
+    return v;
+}
+
+// Canonical sum over a block of W waves where each thread has already
+// accumulated its strided partial: wave trees, then a halving tree over the
+// wave totals (offsets W/2 .. 1).  `red` is __shared__ float[W].  All threads
+// return the total.
+template <int W>
+__device__ __forceinline__ float block_canon_sum(float part, float* red) {
+    float w = wave_tree_sum(part);
+    int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wid] = w;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t[W];
+#pragma unroll
+        for (int i = 0; i < W; i++) t[i] = red[i];
+#pragma unroll
+        for (int off = W / 2; off >= 1; off >>= 1)
+#pragma unroll
+            for (int i = 0; i < off; i++) t[i] = t[i] + t[i + off];
+        red[0] = t[0];
+    }
+    __syncthreads();
+    float r = red[0];
+    __syncthreads();
+    return r;
+}
+
+template <int W>
+__device__ __forceinline__ float block_max(float v, float* red) {
+    float w = wave_max(v);
+    int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wid] = w;
+    __syncthreads();
+    float m = red[0];
+#pragma unroll
+    for (int i = 1; i < W; i++) m = fmaxf(m, red[i]);
+    __syncthreads();
+    return m;
+}
+
+// quantize_activation_row / KVCache::quantize_row arithmetic for one value.
+__device__ __forceinline__ int8_t quant_code(float x, float inv) {
+    return (int8_t)(int)__builtin_roundf(x * inv);
+}
+
+// ------------------------------------------------------- 3-tier KV views
+
+// Visible entries of a query, from the plane's sink count and the number of
+// window stores so far (src/kv_cache.cpp:59-127 keeps exactly this state
+// per (layer, head)): sink rows, pooled rows, window entries oldest ->
+// newest (src/kv_cache.cpp:137-155).
+struct KvView {
+    uint32_t sink, pool, win_lo, win_hi;
+    __device__ __host__ uint32_t count() const { return sink + pool + (win_hi - win_lo); }
+};
+
+__device__ __host__ __forceinline__ KvView kv_view_counts(const KvGeom& g, uint32_t sink, uint32_t nw) {
+    KvView v;
+    v.sink = sink;
+    v.win_hi = nw;
+    v.win_lo = nw > g.window ? nw - g.window : 0u;
+    v.pool = v.win_lo / g.pool_block;
+    return v;
+}
+
+// The engine stores every position once, in order, in every plane: a query
+// at position p sees the stores of positions [0, min(p, max_context)).
+__device__ __host__ __forceinline__ KvView kv_view(const KvGeom& g, uint32_t p) {
+    uint32_t n = p < g.max_context ? p : g.max_context;
+    uint32_t s_eff = g.sink_size < KV_SINK_ROWS ? g.sink_size : KV_SINK_ROWS;
+    uint32_t nw = n > g.sink_size ? n - g.sink_size : 0u;
+    return kv_view_counts(g, n < s_eff ? n : s_eff, nw);
+}
+
+// Destination row of the store of position p, or UINT32_MAX when the
+// reference stores nothing (p >= max_context, or a sink position >= 8).
+__device__ __host__ __forceinline__ uint32_t kv_store_row(const KvGeom& g, uint32_t p) {
+    if (p >= g.max_context) return 0xFFFFFFFFu;
+    if (p < g.sink_size) return p < KV_SINK_ROWS ? p : 0xFFFFFFFFu;
+    return KV_SINK_ROWS + (p - g.sink_size) % g.ring;
+}
+
+// Row index (within one (layer, head) plane) of visible entry j.
+__device__ __forceinline__ uint32_t kv_row(const KvGeom& g, const KvView& v, uint32_t j) {
+    if (j < v.sink) return j;
+    j -= v.sink;
+    if (j < v.pool) return KV_SINK_ROWS + g.ring + j;
+    j -= v.pool;
+    return KV_SINK_ROWS + (v.win_lo + j) % g.ring;
+}
+
+// ------------------------------------------------- GEMV partial sums
+
+// y = (float)(sum_s part[s][m][n] * (double)a_scale[m]).
+__device__ __forceinline__ float gemv_out(const double* __restrict__ part, uint32_t splits,
+                                          uint32_t M, uint32_t N, uint32_t m, uint32_t n, float as) {
+    double S = 0.0;
+    for (uint32_t s = 0; s < splits; s++) S += part[((size_t)s * M + m) * N + n];
+    return (float)(S * (double)as);
+}
+
+// ------------------------------------------------------ quantized rows
+
+// Block sums of int8 codes over 32-element blocks for a 256-thread block
+// where thread t handles elements t, t+256, ...: the 32 elements of a block
+// sit in 32 consecutive lanes of one wave.
+__device__ __forceinline__ int half_wave_isum(int v) {
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Quantize rows (src/matmul_neon.cpp:16-29).  Grid M, 256 threads, K <=
+// 256 * PER.  Writes codes, scale and block sums (when bsum != null).
+template <int PER>
+__device__ __forceinline__ void quantize_row_block(const float (&x)[PER], uint32_t K, int8_t* q,
+                                                   float* scale_out, int32_t* bsum, float* red) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        uint32_t i = threadIdx.x + 256u * k;
+        if (i < K) amax = fmaxf(amax, fabsf(x[k]));
+    }
+    amax = block_max<4>(amax, red);
+    const float inv = (amax == 0.0f) ? 1.0f : 127.0f / amax;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        uint32_t i = threadIdx.x + 256u * k;
+        int code = 0;
+        if (i < K) {
+            int8_t c = quant_code(x[k], inv);
+            q[i] = c;
+            code = c;
+        }
+        if (bsum) {
+            int s = half_wave_isum(code);
+            if (i < K && (i & 31u) == 0) bsum[i >> 5] = s;
+        }
+    }
+    if (threadIdx.x == 0) *scale_out = (amax == 0.0f) ? 1.0f : amax / 127.0f;
+}
+
+}  // namespace pf

@@ -1,0 +1,319 @@
+// GEMV / GEMM kernels for gfx950.
+//
+//  * k_gemv_i8     int8 activations x block-quantized (Q4/Q2/Q1.5, 32-wide
+//                  blocks, fp16 scale) tiled matrix, M <= 8 activation rows.
+//                  One lane per output row, wave-uniform activations in
+//                  SGPRs, v_dot4 int32 block dots, exact fp64 accumulation of
+//                  d_b * p_b.  HBM bound: every weight byte is read once.
+//  * k_gemv_f32    fp32 activations x dequantized Q4 row-major matrix (tied
+//                  unembedding, MTP heads) in the canonical 64-lane order.
+//  * row prologues quantize_activation_row, residual + RMSNorm + quantize,
+//                  SwiGLU + quantize, all producing int8 rows, the row scale
+//                  and per-32-block sums of the codes.
+//  * k_matmul_int8 / k_mm_epilogue: the reference's plain int8 matmul API.
+#include "pf_device.h"
+
+namespace pf {
+
+// ===================================================== int8 x block GEMV
+
+template <int FMT>
+__device__ __forceinline__ void unpack_codes(const uint8_t* tile, uint32_t t, uint32_t lane,
+                                             uint32_t u[8]) {
+    if constexpr (FMT == FMT_Q4) {
+        uint4 c = *reinterpret_cast<const uint4*>(tile + t * 1024u + lane * 16u);
+        const uint32_t m = 0x0F0F0F0Fu;
+        u[0] = c.x & m; u[1] = c.y & m; u[2] = c.z & m; u[3] = c.w & m;
+        u[4] = (c.x >> 4) & m; u[5] = (c.y >> 4) & m; u[6] = (c.z >> 4) & m; u[7] = (c.w >> 4) & m;
+    } else {
+        uint2 c = *reinterpret_cast<const uint2*>(tile + (t >> 1) * 1024u + lane * 16u + (t & 1u) * 8u);
+        const uint32_t m = 0x03030303u;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            u[2 * p] = (c.x >> (2 * p)) & m;
+            u[2 * p + 1] = (c.y >> (2 * p)) & m;
+        }
+    }
+}
+
+// part[s][m][n] = sum over the blocks of split s of d_b * p_b (exact), where
+// p_b = sum_i a[m][32b+i] * code[n][32b+i].  Grid (N/64, splits), 256
+// threads; wave w of split s covers blocks [(4s+w)*bpw, (4s+w+1)*bpw).
+template <int FMT, int M>
+__global__ __launch_bounds__(256) void k_gemv_i8(const uint8_t* __restrict__ W, uint32_t K,
+                                                 const int8_t* __restrict__ act, uint32_t act_stride,
+                                                 const int32_t* __restrict__ bsum, uint32_t bsum_stride,
+                                                 uint32_t bpw, uint32_t N, double* __restrict__ part) {
+    constexpr uint32_t TB = tile_bytes(FMT);
+    constexpr uint32_t CODES = TILE_ROWS * TILE_BLOCKS * code_bytes(FMT);
+    constexpr int OFF = code_offset(FMT);
+    const uint32_t g = blockIdx.x, s = blockIdx.y;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nb = K >> 5, chunks = K >> 8;
+    const uint32_t b0 = (s * 4u + wid) * bpw;
+    const uint32_t b1 = min(b0 + bpw, nb);
+    const uint8_t* tiles = W + (size_t)g * chunks * TB;
+
+    double S[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) S[m] = 0.0;
+
+    for (uint32_t b = b0; b < b1; b++) {
+        const uint32_t c = b >> 3, t = b & 7u;
+        const uint8_t* tile = tiles + (size_t)c * TB;
+        uint32_t u[8];
+        unpack_codes<FMT>(tile, t, lane, u);
+        const uint16_t sc = *reinterpret_cast<const uint16_t*>(tile + CODES + lane * 16u + t * 2u);
+        const double d = (double)h2f(sc);
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const int32_t* a = reinterpret_cast<const int32_t*>(act + (size_t)m * act_stride + (size_t)b * 32u);
+            int acc = -OFF * bsum[(size_t)m * bsum_stride + b];
+#pragma unroll
+            for (int k = 0; k < 8; k++) acc = __builtin_amdgcn_sdot4((int)u[k], a[k], acc, false);
+            S[m] = __builtin_fma(d, (double)acc, S[m]);
+        }
+    }
+
+    __shared__ double red[4][M][64];
+#pragma unroll
+    for (int m = 0; m < M; m++) red[wid][m][lane] = S[m];
+    __syncthreads();
+    if (threadIdx.x < 64) {
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            double v = red[0][m][lane] + red[1][m][lane] + red[2][m][lane] + red[3][m][lane];
+            part[((size_t)s * M + m) * N + (size_t)g * 64u + lane] = v;
+        }
+    }
+}
+
+__global__ void k_gemv_finish(const double* __restrict__ part, uint32_t splits, uint32_t M, uint32_t N,
+                              const float* __restrict__ as, float* __restrict__ y, uint32_t y_stride) {
+    uint32_t n = blockIdx.x * blockDim.x + threadIdx.x, m = blockIdx.y;
+    if (n >= N) return;
+    y[(size_t)m * y_stride + n] = gemv_out(part, splits, M, N, m, n, as[m]);
+}
+
+// ============================================ fp32 x dequantized Q4 GEMV
+
+// y[m][n] (+= y_in[m][n] when resid) = canonical fp32 dot of h[m] with row n:
+// lane l holds block l (K <= 2048), fmaf chain over the block's elements,
+// halving tree over the 64 lanes.  Each wave walks rows n = wave, wave +
+// total_waves, ...
+template <int M>
+__global__ __launch_bounds__(256) void k_gemv_f32(const uint8_t* __restrict__ codes,
+                                                  const uint16_t* __restrict__ scales,
+                                                  uint32_t N, uint32_t K,
+                                                  const float* __restrict__ h, uint32_t h_stride,
+                                                  float* __restrict__ y, uint32_t y_stride,
+                                                  const float* __restrict__ y_in) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
+    const uint32_t nb = K >> 5;
+    const bool live = lane < nb;
+    float hv[M][32];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+            float4 v = live ? *reinterpret_cast<const float4*>(h + (size_t)m * h_stride + lane * 32u + i)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+            hv[m][i] = v.x; hv[m][i + 1] = v.y; hv[m][i + 2] = v.z; hv[m][i + 3] = v.w;
+        }
+    }
+    for (uint32_t n = wave; n < N; n += nwaves) {
+        float acc[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) acc[m] = 0.0f;
+        if (live) {
+            uint4 c = *reinterpret_cast<const uint4*>(codes + ((size_t)n * nb + lane) * 16u);
+            float d = h2f(scales[(size_t)n * nb + lane]);
+            float nd = -8.0f * d;
+            uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                uint32_t byte = (cw[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+                float w0 = __builtin_fmaf((float)(byte & 15u), d, nd);
+                float w1 = __builtin_fmaf((float)(byte >> 4), d, nd);
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+                    acc[m] = __builtin_fmaf(hv[m][2 * j], w0, acc[m]);
+                    acc[m] = __builtin_fmaf(hv[m][2 * j + 1], w1, acc[m]);
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            float t = wave_tree_sum(acc[m]);
+            if (lane == 0) {
+                size_t o = (size_t)m * y_stride + n;
+                y[o] = y_in ? (y_in[o] + t) : t;
+            }
+        }
+    }
+}
+
+// ============================================================ prologues
+
+template <int PER>
+__global__ __launch_bounds__(256) void k_quant_rows(const float* __restrict__ x, uint32_t x_stride,
+                                                    uint32_t K, int8_t* __restrict__ q, uint32_t q_stride,
+                                                    float* __restrict__ as, int32_t* __restrict__ bsum,
+                                                    uint32_t bsum_stride) {
+    __shared__ float red[4];
+    const uint32_t m = blockIdx.x;
+    float v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        uint32_t i = threadIdx.x + 256u * k;
+        v[k] = i < K ? x[(size_t)m * x_stride + i] : 0.0f;
+    }
+    quantize_row_block<PER>(v, K, q + (size_t)m * q_stride, as + m,
+                            bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
+}
+
+// x[m] += (float)(GEMV partial sum * as_prev[m])   (when part != null),
+// then RMSNorm (src/matmul_neon.cpp:231-239, CANON(4) sum of squares) with
+// weight w, then quantize_activation_row of the normed row.
+template <int PER>
+__global__ __launch_bounds__(256) void k_resid_norm_quant(float* __restrict__ x, uint32_t K,
+                                                          const double* __restrict__ part, uint32_t splits,
+                                                          uint32_t M, const float* __restrict__ as_prev,
+                                                          const float* __restrict__ w,
+                                                          int8_t* __restrict__ q, uint32_t q_stride,
+                                                          float* __restrict__ as, int32_t* __restrict__ bsum,
+                                                          uint32_t bsum_stride) {
+    __shared__ float red[4];
+    const uint32_t m = blockIdx.x;
+    float v[PER];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        uint32_t i = threadIdx.x + 256u * k;
+        float xi = 0.0f;
+        if (i < K) {
+            xi = x[(size_t)m * K + i];
+            if (part) {
+                xi = xi + gemv_out(part, splits, M, K, m, i, as_prev[m]);
+                x[(size_t)m * K + i] = xi;
+            }
+            ss = __builtin_fmaf(xi, xi, ss);
+        }
+        v[k] = xi;
+    }
+    ss = block_canon_sum<4>(ss, red);
+    const float rms = __builtin_sqrtf(ss / (float)K + 1e-6f);
+    const float inv = 1.0f / rms;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        uint32_t i = threadIdx.x + 256u * k;
+        if (i < K) v[k] = v[k] * inv * w[i];
+    }
+    quantize_row_block<PER>(v, K, q + (size_t)m * q_stride, as + m,
+                            bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
+}
+
+// x[m] += (float)(GEMV partial sum * as_prev[m]) only (the last layer's
+// down projection residual).
+__global__ void k_resid_add(float* __restrict__ x, uint32_t K, const double* __restrict__ part,
+                            uint32_t splits, uint32_t M, const float* __restrict__ as_prev) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, m = blockIdx.y;
+    if (i >= K) return;
+    x[(size_t)m * K + i] = x[(size_t)m * K + i] + gemv_out(part, splits, M, K, m, i, as_prev[m]);
+}
+
+// SwiGLU of src/engine.cpp:832-838 on the fused gate|up GEMV (rows [0,ff) =
+// gate, [ff, 2ff) = up), then quantize_activation_row of the result.
+template <int PER>
+__global__ __launch_bounds__(256) void k_swiglu_quant(const double* __restrict__ part, uint32_t splits,
+                                                      uint32_t M, uint32_t ff, const float* __restrict__ as_in,
+                                                      int8_t* __restrict__ q, uint32_t q_stride,
+                                                      float* __restrict__ as, int32_t* __restrict__ bsum,
+                                                      uint32_t bsum_stride) {
+    __shared__ float red[4];
+    const uint32_t m = blockIdx.x;
+    const float a = as_in[m];
+    float v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        uint32_t i = threadIdx.x + 256u * k;
+        float f = 0.0f;
+        if (i < ff) {
+            float g = gemv_out(part, splits, M, 2 * ff, m, i, a);
+            float u = gemv_out(part, splits, M, 2 * ff, m, ff + i, a);
+            float sig = 1.0f / (1.0f + expf_c(-g));
+            f = g * sig * u;
+        }
+        v[k] = f;
+    }
+    quantize_row_block<PER>(v, ff, q + (size_t)m * q_stride, as + m,
+                            bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
+}
+
+// MTP activation: a = silu(g) * u with silu(x) = x / (1 + exp(-x))
+// (src/mtp.cpp:89-91, 157-159).
+__global__ void k_silu_mul(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ a, uint32_t n) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float s = g[i] / (1.0f + expf_c(-g[i]));
+    a[i] = s * u[i];
+}
+
+// Token embedding: x[m] = dequantized row tok[m] of the tied Q4 table.
+__global__ void k_embed(const uint8_t* __restrict__ codes, const uint16_t* __restrict__ scales,
+                        uint32_t V, uint32_t D, const PassDesc* __restrict__ pd, float* __restrict__ x) {
+    uint32_t m = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (m >= pd->m || i >= D) return;
+    int32_t tok = pd->tok[m];
+    float val = 0.0f;
+    if (tok >= 0 && (uint32_t)tok < V) {
+        uint32_t nb = D >> 5, b = i >> 5, e = i & 31u;
+        uint8_t byte = codes[((size_t)tok * nb + b) * 16u + (e >> 1)];
+        uint32_t nib = (e & 1u) ? (byte >> 4) : (byte & 15u);
+        float d = h2f(scales[(size_t)tok * nb + b]);
+        val = (float)((int)nib - 8) * d;
+    }
+    x[(size_t)m * D + i] = val;
+}
+
+// ============================================ reference plain-int8 matmul
+
+// C[i][j] = sum_k A[i][k] * B[j][k] (src/matmul_neon.cpp:80-144).  One
+// thread per output; K handled in 4-byte steps with an exact scalar tail.
+__global__ void k_matmul_int8(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
+                              int32_t* __restrict__ C, uint32_t M, uint32_t N, uint32_t K) {
+    uint32_t j = blockIdx.x * blockDim.x + threadIdx.x, i = blockIdx.y;
+    if (j >= N || i >= M) return;
+    const int8_t* a = A + (size_t)i * K;
+    const int8_t* b = B + (size_t)j * K;
+    int acc = 0;
+    uint32_t k = 0;
+    if ((((uintptr_t)a | (uintptr_t)b) & 3u) == 0) {
+        for (; k + 4 <= K; k += 4)
+            acc = __builtin_amdgcn_sdot4(*reinterpret_cast<const int*>(a + k),
+                                         *reinterpret_cast<const int*>(b + k), acc, false);
+    }
+    for (; k < K; k++) acc += (int)a[k] * (int)b[k];
+    C[(size_t)i * N + j] = acc;
+}
+
+// matmul_quantized's given-scale activation path (src/matmul_neon.cpp:158-164).
+__global__ void k_quant_div(const float* __restrict__ A, const float* __restrict__ sc,
+                            int8_t* __restrict__ q, uint32_t M, uint32_t K) {
+    uint32_t k = blockIdx.x * blockDim.x + threadIdx.x, i = blockIdx.y;
+    if (k >= K || i >= M) return;
+    q[(size_t)i * K + k] = (int8_t)(int)__builtin_roundf(A[(size_t)i * K + k] / sc[i]);
+}
+
+// C = (float)C_int * a_scale[i] * w_scale[j] (src/matmul_neon.cpp:176-180).
+__global__ void k_mm_epilogue(const int32_t* __restrict__ Ci, const float* __restrict__ as,
+                              const float* __restrict__ ws, float* __restrict__ C, uint32_t M, uint32_t N) {
+    uint32_t j = blockIdx.x * blockDim.x + threadIdx.x, i = blockIdx.y;
+    if (j >= N || i >= M) return;
+    C[(size_t)i * N + j] = (float)Ci[(size_t)i * N + j] * as[i] * ws[j];
+}
+
+}  // namespace pf

@@ -1,0 +1,94 @@
+// Data layouts in HBM shared by the host runtime and the gfx950 kernels.
+#pragma once
+#include <stdint.h>
+
+namespace pf {
+
+// ---------------------------------------------------------- weight formats
+enum Fmt : int32_t { FMT_Q4 = 0, FMT_Q2 = 1, FMT_Q15 = 2 };
+
+// Int8-activation GEMV matrices are stored in tiles of 64 output rows x 8
+// blocks (256 input columns).  Inside a tile, for block t the 64 rows' code
+// bytes are contiguous (one coalesced 1 KiB wave load per block for Q4, per
+// block pair for Q2/Q1.5), followed by the 64 rows' eight fp16 scales
+// (16 B per row).  Tiles are ordered row-group major: tile (g, c) is at
+// (g * chunks + c) * tile_bytes.
+//
+// Element order inside a block (device order, not the interchange order):
+//   Q4   : byte j, low nibble = element j, high nibble = element j + 16.
+//   Q2/Q15: dword w (0,1), bit plane t (bits 2t..2t+1 of each byte), byte jj
+//          holds element 8t + 4w + jj.
+// Code values: Q4 = nibble - 8, Q2 = code - 2, Q1.5 = code - 1 (code 3 is
+// rejected at upload).
+constexpr int TILE_ROWS = 64;
+constexpr int TILE_BLOCKS = 8;
+__host__ __device__ constexpr uint32_t code_bytes(int fmt) { return fmt == FMT_Q4 ? 16u : 8u; }
+__host__ __device__ constexpr uint32_t tile_bytes(int fmt) {
+    return (uint32_t)TILE_ROWS * TILE_BLOCKS * code_bytes(fmt) + (uint32_t)TILE_ROWS * TILE_BLOCKS * 2u;
+}
+__host__ __device__ constexpr int code_offset(int fmt) { return fmt == FMT_Q4 ? 8 : (fmt == FMT_Q2 ? 2 : 1); }
+
+// fp32-activation GEMV matrices (tied embedding / unembedding, MTP heads)
+// are row-major: codes [rows][cols/32][code_bytes] in the interchange
+// element order (Q4: byte j = elements 2j (low nibble), 2j+1 (high);
+// Q2/Q1.5: byte j = elements 4j..4j+3 at bits 0,2,4,6), scales separate
+// [rows][cols/32] fp16.
+
+// ------------------------------------------------------------- KV cache
+// One (layer, head) plane holds KV_SINK_ROWS sink rows, then `ring` window
+// slots (window index w lives in slot w % ring), then `pool_cap` pooled
+// rows.  K and V are separate planes of int8 [rows][head_dim] with fp32 row
+// scales [rows].  ring = window + pool_block + MAX_PASS_ROWS keeps every
+// window entry alive until it has been folded into its pooled row and lets a
+// verify pass write its pending rows without touching visible entries.
+constexpr uint32_t KV_SINK_ROWS = 8;
+constexpr uint32_t MAX_PASS_ROWS = 8;
+
+struct KvGeom {
+    uint32_t n_layers, n_heads, head_dim;
+    uint32_t sink_size, window, pool_block, max_context;
+    uint32_t ring, pool_cap, rows;   // rows = KV_SINK_ROWS + ring + pool_cap
+};
+
+struct KvPlanes {
+    int8_t* k;      // [layers][heads][rows][head_dim]
+    int8_t* v;
+    float* ks;      // [layers][heads][rows]
+    float* vs;
+};
+
+// ------------------------------------------------------ pass descriptor
+// A forward pass over M <= MAX_PASS_ROWS consecutive positions, read by the
+// kernels from device memory so that the control kernels can set up the
+// next pass without a host round trip.
+struct PassDesc {
+    uint32_t pos0;                 // position of row 0
+    uint32_t m;                    // rows in this pass
+    int32_t tok[MAX_PASS_ROWS];
+};
+
+// Decode-loop state kept on the device.
+struct DecodeState {
+    uint32_t pos;          // positions stored (committed) so far
+    int32_t cur;           // current token (last pushed)
+    uint32_t n_tokens;     // tokens in the output buffer (prompt included)
+    uint32_t n_gen;        // generated tokens
+    uint64_t draw;         // stochastic draws consumed
+    uint32_t accepted;     // total accepted drafts
+    uint32_t rejected;     // total pushed correctives
+    uint32_t have_row4;    // pass B row 4 already holds F(cur) at position pos
+    uint32_t round_word;   // last round: accepted | pushed << 8
+    int32_t draft[8];      // drafts of the current round
+    int32_t row_argmax[8]; // greedy argmax of each pass-B row
+    uint32_t round_acc;    // accepted drafts in the current round
+    uint32_t pad;
+};
+
+struct SamplingCfg {
+    float temperature;
+    float top_p;
+    uint32_t top_k;
+    int32_t greedy;
+};
+
+}  // namespace pf

@@ -1,0 +1,1295 @@
+// Host runtime of libpocketforge_amd.so: implements include/pf_gpu.h on
+// top of the gfx950 kernels (single translation unit with the kernels).
+#include "pf_gemv.hip"
+#include "pf_attn.hip"
+#include "pf_ctl.hip"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/pf_gpu.h"
+
+using namespace pf;
+
+// ================================================================ context
+
+struct pf_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    size_t bytes = 0;
+    // growable scratch for the kernel-level entry points
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
+};
+
+static pf_status fail(const pf_ctx* c, pf_status s, const std::string& msg) {
+    if (c) const_cast<pf_ctx*>(c)->err = msg;
+    return s;
+}
+
+#define PF_HIP(ctx, call)                                                                        \
+    do {                                                                                         \
+        hipError_t e_ = (call);                                                                  \
+        if (e_ != hipSuccess)                                                                    \
+            return fail(ctx, PF_ERR_HIP, std::string(#call) + " failed: " + hipGetErrorString(e_)); \
+    } while (0)
+
+#define PF_LAUNCHED(ctx) PF_HIP(ctx, hipGetLastError())
+
+static pf_status dalloc(pf_ctx* c, void** p, size_t bytes) {
+    *p = nullptr;
+    if (bytes == 0) bytes = 256;
+    hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) return fail(c, PF_ERR_HIP, "hipMalloc(" + std::to_string(bytes) + ") failed: " + hipGetErrorString(e));
+    c->bytes += bytes;
+    return PF_OK;
+}
+
+static void dfree(pf_ctx* c, void* p, size_t bytes) {
+    if (!p) return;
+    (void)hipFree(p);
+    if (bytes == 0) bytes = 256;
+    c->bytes -= std::min(c->bytes, bytes);
+}
+
+template <class T>
+static pf_status dalloc_t(pf_ctx* c, T** p, size_t n) {
+    return dalloc(c, reinterpret_cast<void**>(p), n * sizeof(T));
+}
+
+static pf_status scratch(pf_ctx* c, size_t bytes, void** out) {
+    if (bytes > c->scratch_bytes) {
+        if (c->scratch) {
+            PF_HIP(c, hipStreamSynchronize(c->stream));
+            dfree(c, c->scratch, c->scratch_bytes);
+            c->scratch = nullptr;
+            c->scratch_bytes = 0;
+        }
+        pf_status s = dalloc(c, &c->scratch, bytes);
+        if (s) return s;
+        c->scratch_bytes = bytes;
+    }
+    *out = c->scratch;
+    return PF_OK;
+}
+
+static std::string g_init_error;
+
+extern "C" pf_status pf_init(int device, pf_ctx** out) {
+    if (!out) return PF_ERR_ARG;
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) { g_init_error = std::string("hipGetDeviceCount: ") + hipGetErrorString(e); return PF_ERR_HIP; }
+    if (device < 0 || device >= n) { g_init_error = "device index out of range"; return PF_ERR_ARG; }
+    e = hipSetDevice(device);
+    if (e != hipSuccess) { g_init_error = std::string("hipSetDevice: ") + hipGetErrorString(e); return PF_ERR_HIP; }
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) { g_init_error = std::string("hipGetDeviceProperties: ") + hipGetErrorString(e); return PF_ERR_HIP; }
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        g_init_error = std::string("device is ") + prop.gcnArchName + ", not gfx950";
+        return PF_ERR_UNSUPPORTED;
+    }
+    pf_ctx* c = new pf_ctx();
+    c->device = device;
+    e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        g_init_error = std::string("hipStreamCreateWithFlags: ") + hipGetErrorString(e);
+        delete c;
+        return PF_ERR_HIP;
+    }
+    *out = c;
+    return PF_OK;
+}
+
+extern "C" void pf_destroy(pf_ctx* c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    if (c->scratch) (void)hipFree(c->scratch);
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+extern "C" const char* pf_last_error(const pf_ctx* c) { return c ? c->err.c_str() : g_init_error.c_str(); }
+
+extern "C" pf_status pf_malloc(pf_ctx* c, size_t bytes, void** out) {
+    if (!c || !out) return PF_ERR_ARG;
+    return dalloc(c, out, bytes);
+}
+
+extern "C" pf_status pf_free(pf_ctx* c, void* p, size_t bytes) {
+    if (!c) return PF_ERR_ARG;
+    PF_HIP(c, hipStreamSynchronize(c->stream));
+    dfree(c, p, bytes);
+    return PF_OK;
+}
+
+extern "C" pf_status pf_memcpy(pf_ctx* c, void* dst, const void* src, size_t bytes, int32_t kind) {
+    if (!c || (!dst && bytes) || (!src && bytes)) return PF_ERR_ARG;
+    hipMemcpyKind k = kind == 0 ? hipMemcpyHostToDevice : (kind == 1 ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice);
+    PF_HIP(c, hipMemcpyAsync(dst, src, bytes, k, c->stream));
+    PF_HIP(c, hipStreamSynchronize(c->stream));
+    return PF_OK;
+}
+
+extern "C" pf_status pf_device_info(pf_ctx* c, char* name, size_t len, int* cus) {
+    if (!c) return PF_ERR_ARG;
+    hipDeviceProp_t prop;
+    PF_HIP(c, hipGetDeviceProperties(&prop, c->device));
+    if (name && len) std::snprintf(name, len, "%s (%s)", prop.name, prop.gcnArchName);
+    if (cus) *cus = prop.multiProcessorCount;
+    return PF_OK;
+}
+
+extern "C" pf_status pf_synchronize(pf_ctx* c) {
+    if (!c) return PF_ERR_ARG;
+    PF_HIP(c, hipStreamSynchronize(c->stream));
+    return PF_OK;
+}
+
+extern "C" size_t pf_device_bytes(const pf_ctx* c) { return c ? c->bytes : 0; }
+
+// ============================================================== matrices
+
+struct pf_matrix {
+    pf_ctx* ctx = nullptr;
+    int32_t fmt = 0;
+    uint32_t rows = 0, cols = 0;
+    bool rowmajor = false;
+    uint8_t* data = nullptr;    // tiled: all tiles; row-major: codes
+    uint16_t* scales = nullptr; // row-major only
+    size_t bytes = 0;
+    uint32_t bpw = 2, splits = 1;
+};
+
+static uint32_t interchange_code(int fmt, const uint8_t* blk, uint32_t e) {
+    if (fmt == FMT_Q4) return (e & 1u) ? (blk[e >> 1] >> 4) : (blk[e >> 1] & 15u);
+    return (blk[e >> 2] >> (2 * (e & 3u))) & 3u;
+}
+
+// Checks the exact-sum condition of one row: nonzero block scales within 15
+// binades of each other; Q1.5 codes in {0,1,2}.
+static pf_status check_row(const pf_ctx* c, int fmt, const uint8_t* codes, const uint16_t* sc, uint32_t nb,
+                           uint32_t row) {
+    int emax = -1, emin = 99;
+    for (uint32_t b = 0; b < nb; b++) {
+        uint16_t h = sc[b];
+        if ((h & 0x7FFF) == 0) continue;
+        int e = (h >> 10) & 31;
+        if (e == 31) return fail(c, PF_ERR_RANGE, "row " + std::to_string(row) + ": non-finite block scale");
+        if (e == 0) e = 1;
+        emax = std::max(emax, e);
+        emin = std::min(emin, e);
+    }
+    if (emax >= 0 && emax - emin > 15)
+        return fail(c, PF_ERR_RANGE, "row " + std::to_string(row) +
+                                         ": block scales span more than 15 binades (exact fp64 block sums would not hold)");
+    if (fmt == FMT_Q15) {
+        for (uint32_t b = 0; b < nb * 8; b++)
+            for (int t = 0; t < 4; t++)
+                if (((codes[b] >> (2 * t)) & 3u) == 3u)
+                    return fail(c, PF_ERR_RANGE, "row " + std::to_string(row) + ": Q1.5 code 3 is not a ternary code");
+    }
+    return PF_OK;
+}
+
+// Repacks interchange rows [r0, r0 + 64*G) into tiles (device element
+// order) in `out` (G * chunks tiles).
+static void repack_tiles(int fmt, uint32_t cols, const uint8_t* codes, const uint16_t* scales, uint32_t r0,
+                         uint32_t G, uint8_t* out) {
+    const uint32_t nb = cols / 32, chunks = cols / 256, bb = code_bytes(fmt), TB = tile_bytes(fmt);
+    const uint32_t CODES = TILE_ROWS * TILE_BLOCKS * bb;
+    for (uint32_t g = 0; g < G; g++)
+        for (uint32_t c = 0; c < chunks; c++) {
+            uint8_t* tile = out + ((size_t)g * chunks + c) * TB;
+            std::memset(tile, 0, TB);
+            for (uint32_t r = 0; r < 64; r++) {
+                const uint32_t row = r0 + g * 64 + r;
+                for (uint32_t t = 0; t < 8; t++) {
+                    const uint32_t b = c * 8 + t;
+                    const uint8_t* blk = codes + ((size_t)row * nb + b) * bb;
+                    std::memcpy(tile + CODES + r * 16 + t * 2, &scales[(size_t)row * nb + b], 2);
+                    if (fmt == FMT_Q4) {
+                        uint8_t* dst = tile + t * 1024 + r * 16;
+                        for (uint32_t j = 0; j < 16; j++)
+                            dst[j] = (uint8_t)(interchange_code(fmt, blk, j) | (interchange_code(fmt, blk, j + 16) << 4));
+                    } else {
+                        uint8_t* dst = tile + (t >> 1) * 1024 + r * 16 + (t & 1) * 8;
+                        for (uint32_t e = 0; e < 32; e++) {
+                            uint32_t pl = e >> 3, w = (e >> 2) & 1u, jj = e & 3u;
+                            dst[4 * w + jj] |= (uint8_t)(interchange_code(fmt, blk, e) << (2 * pl));
+                        }
+                    }
+                }
+            }
+        }
+}
+
+static void choose_split(pf_matrix* M) {
+    const uint32_t nb = M->cols / 32, G = M->rows / 64;
+    uint32_t best = 2;
+    for (uint32_t bpw : {2u, 4u, 8u, 16u}) {
+        uint32_t splits = (nb + 4 * bpw - 1) / (4 * bpw);
+        if ((uint64_t)G * splits * 4 >= 1024) best = bpw;
+    }
+    M->bpw = best;
+    M->splits = (nb + 4 * best - 1) / (4 * best);
+}
+
+static pf_status matrix_alloc(pf_ctx* c, int32_t fmt, uint32_t rows, uint32_t cols, bool rowmajor, pf_matrix** out) {
+    if (fmt != FMT_Q4 && fmt != FMT_Q2 && fmt != FMT_Q15) return fail(c, PF_ERR_ARG, "unknown format");
+    if (cols % 256 || rows % 64 || rows == 0 || cols == 0)
+        return fail(c, PF_ERR_UNSUPPORTED, "matrix shape must have rows % 64 == 0 and cols % 256 == 0");
+    if (rowmajor && (fmt != FMT_Q4 || cols > 2048))
+        return fail(c, PF_ERR_UNSUPPORTED, "fp32-activation matrices must be Q4 with cols <= 2048");
+    pf_matrix* M = new pf_matrix();
+    M->ctx = c; M->fmt = fmt; M->rows = rows; M->cols = cols; M->rowmajor = rowmajor;
+    const uint32_t nb = cols / 32;
+    if (rowmajor) {
+        M->bytes = (size_t)rows * nb * 16;
+        pf_status s = dalloc_t(c, &M->data, M->bytes);
+        if (!s) s = dalloc_t(c, &M->scales, (size_t)rows * nb);
+        if (s) { delete M; return s; }
+    } else {
+        M->bytes = (size_t)(rows / 64) * (cols / 256) * tile_bytes(fmt);
+        pf_status s = dalloc_t(c, &M->data, M->bytes);
+        if (s) { delete M; return s; }
+        choose_split(M);
+    }
+    *out = M;
+    return PF_OK;
+}
+
+// Uploads interchange rows [r0, r0 + n) of a matrix (n % 64 == 0 for tiled).
+static pf_status matrix_put(pf_matrix* M, uint32_t r0, uint32_t n, const uint8_t* codes, const uint16_t* scales) {
+    pf_ctx* c = M->ctx;
+    const uint32_t nb = M->cols / 32, bb = code_bytes(M->fmt);
+    for (uint32_t r = 0; r < n; r++) {
+        pf_status s = check_row(c, M->fmt, codes + (size_t)r * nb * bb, scales + (size_t)r * nb, nb, r0 + r);
+        if (s) return s;
+    }
+    if (M->rowmajor) {
+        PF_HIP(c, hipMemcpy(M->data + (size_t)r0 * nb * 16, codes, (size_t)n * nb * 16, hipMemcpyHostToDevice));
+        PF_HIP(c, hipMemcpy(M->scales + (size_t)r0 * nb, scales, (size_t)n * nb * 2, hipMemcpyHostToDevice));
+        return PF_OK;
+    }
+    const uint32_t G = n / 64, chunks = M->cols / 256;
+    std::vector<uint8_t> tiles((size_t)G * chunks * tile_bytes(M->fmt));
+    // repack takes absolute rows; shift the pointers so row r0 is row 0
+    repack_tiles(M->fmt, M->cols, codes - (size_t)r0 * nb * bb, scales - (size_t)r0 * nb, r0, G, tiles.data());
+    PF_HIP(c, hipMemcpy(M->data + (size_t)(r0 / 64) * chunks * tile_bytes(M->fmt), tiles.data(), tiles.size(),
+                        hipMemcpyHostToDevice));
+    return PF_OK;
+}
+
+extern "C" pf_status pf_matrix_upload(pf_ctx* c, int32_t fmt, uint32_t rows, uint32_t cols, const uint8_t* codes,
+                                      const uint16_t* scales, int32_t rowmajor, pf_matrix** out) {
+    if (!c || !codes || !scales || !out) return PF_ERR_ARG;
+    pf_matrix* M = nullptr;
+    pf_status s = matrix_alloc(c, fmt, rows, cols, rowmajor != 0, &M);
+    if (s) return s;
+    s = matrix_put(M, 0, rows, codes, scales);
+    if (s) { pf_matrix_free(M); return s; }
+    *out = M;
+    return PF_OK;
+}
+
+extern "C" void pf_matrix_free(pf_matrix* M) {
+    if (!M) return;
+    dfree(M->ctx, M->data, M->bytes);
+    if (M->scales) dfree(M->ctx, M->scales, (size_t)M->rows * (M->cols / 32) * 2);
+    delete M;
+}
+
+// ------------------------------------------------------- kernel launches
+
+#define PF_GEMV_CASE(F, MM)                                                                              \
+    case MM:                                                                                             \
+        hipLaunchKernelGGL((k_gemv_i8<F, MM>), grid, dim3(256), 0, st, W->data, W->cols, act, act_stride,  \
+                           bsum, bsum_stride, W->bpw, W->rows, part);                                    \
+        break;
+
+#define PF_GEMV_FMT(F)                                 \
+    switch (M) {                                       \
+        PF_GEMV_CASE(F, 1) PF_GEMV_CASE(F, 2)          \
+        PF_GEMV_CASE(F, 3) PF_GEMV_CASE(F, 4)          \
+        PF_GEMV_CASE(F, 5) PF_GEMV_CASE(F, 6)          \
+        PF_GEMV_CASE(F, 7) PF_GEMV_CASE(F, 8)          \
+    }
+
+static void launch_gemv(hipStream_t st, const pf_matrix* W, uint32_t M, const int8_t* act, uint32_t act_stride,
+                        const int32_t* bsum, uint32_t bsum_stride, double* part) {
+    dim3 grid(W->rows / 64, W->splits);
+    switch (W->fmt) {
+        case FMT_Q4: PF_GEMV_FMT(FMT_Q4) break;
+        case FMT_Q2: PF_GEMV_FMT(FMT_Q2) break;
+        default: PF_GEMV_FMT(FMT_Q15) break;
+    }
+}
+
+static void launch_gemv_f32(hipStream_t st, const pf_matrix* W, uint32_t M, const float* h, uint32_t h_stride,
+                            float* y, uint32_t y_stride, const float* y_in) {
+    uint32_t waves = std::min<uint32_t>(W->rows, 2048);
+    dim3 grid((waves + 3) / 4);
+#define PF_F32_CASE(MM)                                                                                       \
+    case MM:                                                                                                  \
+        hipLaunchKernelGGL(k_gemv_f32<MM>, grid, dim3(256), 0, st, W->data, W->scales, W->rows, W->cols, h,   \
+                           h_stride, y, y_stride, y_in);                                                      \
+        break;
+    switch (M) {
+        PF_F32_CASE(1) PF_F32_CASE(2) PF_F32_CASE(3) PF_F32_CASE(4)
+        PF_F32_CASE(5) PF_F32_CASE(6) PF_F32_CASE(7) PF_F32_CASE(8)
+    }
+#undef PF_F32_CASE
+}
+
+static int per_for(uint32_t K) {
+    uint32_t per = (K + 255) / 256;
+    for (int p : {4, 8, 12, 16, 24, 32})
+        if ((uint32_t)p >= per) return p;
+    return 0;
+}
+
+#define PF_PER_SWITCH(K, CALL)                           \
+    switch (per_for(K)) {                                \
+        case 4: { constexpr int PER = 4; CALL; } break;   \
+        case 8: { constexpr int PER = 8; CALL; } break;   \
+        case 12: { constexpr int PER = 12; CALL; } break; \
+        case 16: { constexpr int PER = 16; CALL; } break; \
+        case 24: { constexpr int PER = 24; CALL; } break; \
+        case 32: { constexpr int PER = 32; CALL; } break; \
+    }
+
+static size_t gemv_part_elems(const pf_matrix* W, uint32_t M) { return (size_t)W->splits * M * W->rows; }
+
+extern "C" pf_status pf_quantize_activation_rows(pf_ctx* c, const float* src, int8_t* dst, float* scales,
+                                                 uint32_t M, uint32_t K) {
+    if (!c || !src || !dst || !scales || M == 0) return PF_ERR_ARG;
+    if (!per_for(K)) return fail(c, PF_ERR_UNSUPPORTED, "K > 8192");
+    PF_PER_SWITCH(K, hipLaunchKernelGGL(k_quant_rows<PER>, dim3(M), dim3(256), 0, c->stream, src, K, K, dst, K,
+                                        scales, (int32_t*)nullptr, 0u));
+    PF_LAUNCHED(c);
+    return PF_OK;
+}
+
+extern "C" pf_status pf_matmul_int8(pf_ctx* c, const int8_t* A, const int8_t* B, int32_t* C, uint32_t M, uint32_t N,
+                                    uint32_t K) {
+    if (!c || !A || !B || !C) return PF_ERR_ARG;
+    if (M == 0 || N == 0) return PF_OK;
+    hipLaunchKernelGGL(k_matmul_int8, dim3((N + 255) / 256, M), dim3(256), 0, c->stream, A, B, C, M, N, K);
+    PF_LAUNCHED(c);
+    return PF_OK;
+}
+
+extern "C" pf_status pf_matmul_quantized(pf_ctx* c, const float* A, const int8_t* B, float* C, uint32_t M,
+                                         uint32_t N, uint32_t K, const float* ws, const float* as_in) {
+    if (!c || !A || !B || !C || !ws) return PF_ERR_ARG;
+    if (M == 0 || N == 0) return PF_OK;
+    size_t need = (size_t)M * K + 256 + (size_t)M * 4 + 256 + (size_t)M * N * 4 + 256;
+    void* s = nullptr;
+    pf_status st = scratch(c, need, &s);
+    if (st) return st;
+    int8_t* Aq = (int8_t*)s;
+    float* as = (float*)((char*)s + (((size_t)M * K + 255) & ~(size_t)255));
+    int32_t* Ci = (int32_t*)((char*)as + (((size_t)M * 4 + 255) & ~(size_t)255));
+    if (as_in) {
+        hipLaunchKernelGGL(k_quant_div, dim3((K + 255) / 256, M), dim3(256), 0, c->stream, A, as_in, Aq, M, K);
+        PF_HIP(c, hipMemcpyAsync(as, as_in, M * 4, hipMemcpyDeviceToDevice, c->stream));
+    } else {
+        if (!per_for(K)) return fail(c, PF_ERR_UNSUPPORTED, "K > 8192");
+        PF_PER_SWITCH(K, hipLaunchKernelGGL(k_quant_rows<PER>, dim3(M), dim3(256), 0, c->stream, A, K, K, Aq, K,
+                                            as, (int32_t*)nullptr, 0u));
+    }
+    hipLaunchKernelGGL(k_matmul_int8, dim3((N + 255) / 256, M), dim3(256), 0, c->stream, Aq, B, Ci, M, N, K);
+    hipLaunchKernelGGL(k_mm_epilogue, dim3((N + 255) / 256, M), dim3(256), 0, c->stream, Ci, as, ws, C, M, N);
+    PF_LAUNCHED(c);
+    return PF_OK;
+}
+
+extern "C" pf_status pf_gemv_q(pf_ctx* c, const pf_matrix* W, const float* x, float* y, uint32_t M) {
+    if (!c || !W || !x || !y || M == 0 || M > 8) return PF_ERR_ARG;
+    if (W->rowmajor) return fail(c, PF_ERR_ARG, "pf_gemv_q needs a tiled matrix");
+    const uint32_t K = W->cols;
+    if (!per_for(K)) return fail(c, PF_ERR_UNSUPPORTED, "K > 8192");
+    size_t a_bytes = ((size_t)M * K + 255) & ~(size_t)255;
+    size_t s_bytes = 256;
+    size_t b_bytes = (((size_t)M * (K / 32) * 4) + 255) & ~(size_t)255;
+    size_t p_bytes = gemv_part_elems(W, M) * 8;
+    void* s = nullptr;
+    pf_status st = scratch(c, a_bytes + s_bytes + b_bytes + p_bytes, &s);
+    if (st) return st;
+    int8_t* act = (int8_t*)s;
+    float* as = (float*)((char*)s + a_bytes);
+    int32_t* bsum = (int32_t*)((char*)as + s_bytes);
+    double* part = (double*)((char*)bsum + b_bytes);
+    PF_PER_SWITCH(K, hipLaunchKernelGGL(k_quant_rows<PER>, dim3(M), dim3(256), 0, c->stream, x, K, K, act, K, as,
+                                        bsum, K / 32));
+    launch_gemv(c->stream, W, M, act, K, bsum, K / 32, part);
+    hipLaunchKernelGGL(k_gemv_finish, dim3((W->rows + 255) / 256, M), dim3(256), 0, c->stream, part, W->splits, M,
+                       W->rows, as, y, W->rows);
+    PF_LAUNCHED(c);
+    return PF_OK;
+}
+
+extern "C" pf_status pf_gemv_f32(pf_ctx* c, const pf_matrix* W, const float* x, float* y, uint32_t M) {
+    if (!c || !W || !x || !y || M == 0 || M > 8) return PF_ERR_ARG;
+    if (!W->rowmajor) return fail(c, PF_ERR_ARG, "pf_gemv_f32 needs a row-major matrix");
+    launch_gemv_f32(c->stream, W, M, x, W->cols, y, W->rows, nullptr);
+    PF_LAUNCHED(c);
+    return PF_OK;
+}
+
+// ================================================================= KV cache
+
+static pf_status kv_geom(const pf_ctx* c, uint32_t L, uint32_t H, uint32_t hd, uint32_t sink, uint32_t win,
+                         uint32_t pool, uint32_t maxc, KvGeom* g) {
+    if (L == 0 || H == 0 || hd == 0 || hd % 2 || hd > 128 || maxc == 0)
+        return fail(c, PF_ERR_UNSUPPORTED, "KV cache needs even head_dim <= 128 and max_context > 0");
+    g->n_layers = L; g->n_heads = H; g->head_dim = hd;
+    g->sink_size = sink;
+    g->window = std::min(win, maxc);                 // src/kv_cache.cpp:33
+    g->pool_block = std::max(1u, pool);              // src/kv_cache.cpp:34
+    g->max_context = maxc;
+    if (g->window < MAX_PASS_ROWS) return fail(c, PF_ERR_UNSUPPORTED, "window must hold at least 8 entries");
+    g->ring = g->window + g->pool_block + MAX_PASS_ROWS;
+    uint32_t evictable = maxc > sink + g->window ? maxc - sink - g->window : 0;
+    g->pool_cap = evictable / g->pool_block + 1;
+    g->rows = KV_SINK_ROWS + g->ring + g->pool_cap;
+    return PF_OK;
+}
+
+static pf_status kv_alloc(pf_ctx* c, const KvGeom& g, KvPlanes* p, size_t* bytes) {
+    size_t planes = (size_t)g.n_layers * g.n_heads, rows = planes * g.rows;
+    pf_status s = dalloc_t(c, &p->k, rows * g.head_dim);
+    if (!s) s = dalloc_t(c, &p->v, rows * g.head_dim);
+    if (!s) s = dalloc_t(c, &p->ks, rows);
+    if (!s) s = dalloc_t(c, &p->vs, rows);
+    if (s) return s;
+    PF_HIP(c, hipMemset(p->k, 0, rows * g.head_dim));
+    PF_HIP(c, hipMemset(p->v, 0, rows * g.head_dim));
+    *bytes = 2 * rows * g.head_dim + 2 * rows * 4;
+    return PF_OK;
+}
+
+static void kv_free(pf_ctx* c, const KvGeom& g, KvPlanes* p) {
+    size_t rows = (size_t)g.n_layers * g.n_heads * g.rows;
+    dfree(c, p->k, rows * g.head_dim);
+    dfree(c, p->v, rows * g.head_dim);
+    dfree(c, p->ks, rows * 4);
+    dfree(c, p->vs, rows * 4);
+}
+
+struct pf_kv {
+    pf_ctx* ctx = nullptr;
+    KvGeom g{};
+    KvPlanes p{};
+    size_t bytes = 0;
+    std::vector<uint32_t> sink_count, nw;
+    uint32_t total_stored = 0;
+    float* io = nullptr;      // staging: key, value, query, scores
+    float* S = nullptr;       // scores for weighted sum
+    float* Wp = nullptr;      // chunk partials
+    PassDesc* pd = nullptr;
+    uint32_t cap = 0;         // max visible entries
+};
+
+extern "C" pf_status pf_kv_create(pf_ctx* c, const pf_kv_config* cfg, pf_kv** out) {
+    if (!c || !cfg || !out) return PF_ERR_ARG;
+    pf_kv* kv = new pf_kv();
+    kv->ctx = c;
+    pf_status s = kv_geom(c, cfg->n_layers, cfg->n_kv_heads, cfg->head_dim, cfg->sink_size, cfg->window_size,
+                          cfg->pool_block, cfg->max_context, &kv->g);
+    if (!s) s = kv_alloc(c, kv->g, &kv->p, &kv->bytes);
+    kv->cap = KV_SINK_ROWS + kv->g.pool_cap + kv->g.window + 1;
+    if (!s) s = dalloc_t(c, &kv->io, 4 * 128);
+    if (!s) s = dalloc_t(c, &kv->S, kv->cap + 64);
+    if (!s) s = dalloc_t(c, &kv->Wp, (size_t)((kv->cap + 63) / 64 + 1) * 128);
+    if (!s) s = dalloc_t(c, &kv->pd, 1);
+    if (s) { delete kv; return s; }
+    PassDesc pd{};
+    pd.m = 1;
+    PF_HIP(c, hipMemcpy(kv->pd, &pd, sizeof(pd), hipMemcpyHostToDevice));
+    size_t planes = (size_t)kv->g.n_layers * kv->g.n_heads;
+    kv->sink_count.assign(planes, 0);
+    kv->nw.assign(planes, 0);
+    *out = kv;
+    return PF_OK;
+}
+
+extern "C" void pf_kv_destroy(pf_kv* kv) {
+    if (!kv) return;
+    pf_ctx* c = kv->ctx;
+    (void)hipStreamSynchronize(c->stream);
+    kv_free(c, kv->g, &kv->p);
+    dfree(c, kv->io, 4 * 128 * 4);
+    dfree(c, kv->S, (kv->cap + 64) * 4);
+    dfree(c, kv->Wp, (size_t)((kv->cap + 63) / 64 + 1) * 128 * 4);
+    dfree(c, kv->pd, sizeof(PassDesc));
+    delete kv;
+}
+
+// src/kv_cache.cpp:59-127 on per-plane counters; a pooled row is folded as
+// soon as its last entry is evicted, as the reference does.
+extern "C" pf_status pf_kv_store(pf_kv* kv, uint32_t layer, uint32_t head, uint32_t pos, const float* key,
+                                 const float* value) {
+    if (!kv || !key || !value) return PF_ERR_ARG;
+    pf_ctx* c = kv->ctx;
+    const KvGeom& g = kv->g;
+    if (layer >= g.n_layers || head >= g.n_heads) return PF_OK;   // silent, src/kv_cache.cpp:61
+    if (pos >= g.max_context) return PF_OK;                        // src/kv_cache.cpp:62
+    const size_t pl = (size_t)layer * g.n_heads + head;
+    uint32_t row = 0xFFFFFFFFu;
+    if (pos < g.sink_size) {
+        if (pos < KV_SINK_ROWS) {
+            row = pos;
+            kv->sink_count[pl] = std::max(kv->sink_count[pl], pos + 1);
+        }
+    } else {
+        const uint32_t w = kv->nw[pl];
+        if (w >= g.window) {
+            const uint32_t ev = w - g.window;                      // evicted window index
+            if ((ev + 1) % g.pool_block == 0) {
+                const uint32_t r = ev / g.pool_block;
+                if (r >= g.pool_cap) return fail(c, PF_ERR_CAPACITY, "pooled rows exceed capacity");
+                hipLaunchKernelGGL(k_pool_rows, dim3(1, 1), dim3(g.head_dim <= 64 ? 64 : 128), 0, c->stream, g, kv->p,
+                                   (uint32_t)pl, r);
+            }
+        }
+        row = KV_SINK_ROWS + w % g.ring;
+        kv->nw[pl] = w + 1;
+    }
+    if (row != 0xFFFFFFFFu) {
+        PF_HIP(c, hipMemcpyAsync(kv->io, key, g.head_dim * 4, hipMemcpyHostToDevice, c->stream));
+        PF_HIP(c, hipMemcpyAsync(kv->io + 128, value, g.head_dim * 4, hipMemcpyHostToDevice, c->stream));
+        hipLaunchKernelGGL(k_kv_store_row, dim3(1), dim3(64), 0, c->stream, g, kv->p, layer, head, row, kv->io,
+                           kv->io + 128);
+        PF_LAUNCHED(c);
+        PF_HIP(c, hipStreamSynchronize(c->stream));
+    }
+    if (pos >= kv->total_stored) kv->total_stored = pos + 1;
+    return PF_OK;
+}
+
+extern "C" pf_status pf_kv_attention_scores(pf_kv* kv, uint32_t layer, uint32_t head, const float* q, float* out,
+                                            uint32_t* count) {
+    if (!kv || !q || !out || !count) return PF_ERR_ARG;
+    pf_ctx* c = kv->ctx;
+    const KvGeom& g = kv->g;
+    *count = 0;
+    if (layer >= g.n_layers || head >= g.n_heads) return PF_OK;
+    const size_t pl = (size_t)layer * g.n_heads + head;
+    const KvView v = kv_view_counts(g, kv->sink_count[pl], kv->nw[pl]);
+    const uint32_t C = v.count();
+    PF_HIP(c, hipMemcpyAsync(kv->io + 256, q, g.head_dim * 4, hipMemcpyHostToDevice, c->stream));
+    // the kernel reads a full head row of q per head index: place q at head `head`
+    KvGeom g1 = g;
+    hipLaunchKernelGGL(k_attn_scores, dim3(1, 1, (C + 1 + 255) / 256), dim3(256), 0, c->stream, kv->pd, g1, kv->p,
+                       layer, (int32_t)kv->sink_count[pl], kv->nw[pl], (int32_t)head, kv->io + 256,
+                       kv->io + 256, kv->S, 0u, 0);
+    PF_LAUNCHED(c);
+    if (C) PF_HIP(c, hipMemcpyAsync(out, kv->S, (size_t)C * 4, hipMemcpyDeviceToHost, c->stream));
+    PF_HIP(c, hipStreamSynchronize(c->stream));
+    *count = C;
+    return PF_OK;
+}
+
+extern "C" pf_status pf_kv_attention_weighted_sum(pf_kv* kv, uint32_t layer, uint32_t head, const float* scores,
+                                                  float* output, uint32_t count) {
+    if (!kv || !output) return PF_ERR_ARG;
+    pf_ctx* c = kv->ctx;
+    const KvGeom& g = kv->g;
+    std::memset(output, 0, g.head_dim * 4);
+    if (layer >= g.n_layers || head >= g.n_heads || count == 0) return PF_OK;
+    if (!scores) return PF_ERR_ARG;
+    const size_t pl = (size_t)layer * g.n_heads + head;
+    const KvView v = kv_view_counts(g, kv->sink_count[pl], kv->nw[pl]);
+    const uint32_t n = std::min(count, v.count());
+    if (n == 0) return PF_OK;
+    PF_HIP(c, hipMemcpyAsync(kv->S, scores, (size_t)n * 4, hipMemcpyHostToDevice, c->stream));
+    const uint32_t nch = (n + 63) / 64;
+    hipLaunchKernelGGL(k_attn_wsum, dim3(1, 1, nch), dim3(128), 0, c->stream, kv->pd, g, kv->p, layer,
+                       (int32_t)kv->sink_count[pl], kv->nw[pl], (int32_t)head, n, kv->S, 0u, kv->Wp, nch);
+    hipLaunchKernelGGL(k_wsum_combine_one, dim3(1), dim3(128), 0, c->stream, kv->Wp, nch, g.head_dim, kv->io + 384);
+    PF_LAUNCHED(c);
+    PF_HIP(c, hipMemcpyAsync(output, kv->io + 384, g.head_dim * 4, hipMemcpyDeviceToHost, c->stream));
+    PF_HIP(c, hipStreamSynchronize(c->stream));
+    return PF_OK;
+}
+
+extern "C" uint32_t pf_kv_size(const pf_kv* kv) { return kv ? kv->total_stored : 0; }
+
+extern "C" pf_status pf_kv_clear(pf_kv* kv) {
+    if (!kv) return PF_ERR_ARG;
+    std::fill(kv->sink_count.begin(), kv->sink_count.end(), 0u);
+    std::fill(kv->nw.begin(), kv->nw.end(), 0u);
+    kv->total_stored = 0;
+    return PF_OK;
+}
+
+extern "C" size_t pf_kv_memory_usage(const pf_kv* kv) { return kv ? kv->bytes : 0; }
+
+// ================================================================== model
+
+struct pf_model {
+    pf_ctx* ctx = nullptr;
+    pf_model_desc d{};
+    std::vector<pf_matrix*> qkv, o, gu, down, mtp;
+    pf_matrix* emb = nullptr;
+    float* attn_norm = nullptr;
+    float* ffn_norm = nullptr;
+    std::vector<uint32_t> set_mask;   // per layer: bit id for matrices 0..6
+    std::vector<uint32_t> mtp_mask;
+    bool emb_set = false;
+};
+
+extern "C" pf_status pf_model_create(pf_ctx* c, const pf_model_desc* d, pf_model** out) {
+    if (!c || !d || !out) return PF_ERR_ARG;
+    if (d->n_heads * d->head_dim != d->n_embd)
+        return fail(c, PF_ERR_UNSUPPORTED, "n_heads * head_dim must equal n_embd (multi-head attention)");
+    if (d->n_embd % 256 || d->n_ff % 256 || d->n_vocab % 64 || d->n_embd > 2048 || d->n_ff > 8192)
+        return fail(c, PF_ERR_UNSUPPORTED, "n_embd and n_ff must be multiples of 256 (n_embd <= 2048, n_ff <= 8192), "
+                                           "n_vocab a multiple of 64");
+    if (d->head_dim % 16 || d->head_dim > 128) return fail(c, PF_ERR_UNSUPPORTED, "head_dim must be 16..128, multiple of 16");
+    if (d->n_mtp + 1 > MAX_PASS_ROWS) return fail(c, PF_ERR_UNSUPPORTED, "at most 7 MTP heads");
+    if (d->n_vocab > SAMPLE_MAX_V) return fail(c, PF_ERR_UNSUPPORTED, "n_vocab > 16384");
+    pf_model* m = new pf_model();
+    m->ctx = c;
+    m->d = *d;
+    m->qkv.assign(d->n_layers, nullptr);
+    m->o.assign(d->n_layers, nullptr);
+    m->gu.assign(d->n_layers, nullptr);
+    m->down.assign(d->n_layers, nullptr);
+    m->mtp.assign((size_t)d->n_mtp * 3, nullptr);
+    m->set_mask.assign(d->n_layers, 0);
+    m->mtp_mask.assign(d->n_mtp, 0);
+    size_t nn = (size_t)std::max(1u, d->n_layers) * d->n_embd;
+    pf_status s = dalloc_t(c, &m->attn_norm, nn);
+    if (!s) s = dalloc_t(c, &m->ffn_norm, nn);
+    if (s) { delete m; return s; }
+    std::vector<float> ones(nn, 1.0f);   // src/engine.cpp:171-173 fallback
+    PF_HIP(c, hipMemcpy(m->attn_norm, ones.data(), nn * 4, hipMemcpyHostToDevice));
+    PF_HIP(c, hipMemcpy(m->ffn_norm, ones.data(), nn * 4, hipMemcpyHostToDevice));
+    *out = m;
+    return PF_OK;
+}
+
+extern "C" void pf_model_destroy(pf_model* m) {
+    if (!m) return;
+    for (auto* v : {&m->qkv, &m->o, &m->gu, &m->down, &m->mtp})
+        for (pf_matrix* x : *v) pf_matrix_free(x);
+    pf_matrix_free(m->emb);
+    size_t nn = (size_t)std::max(1u, m->d.n_layers) * m->d.n_embd;
+    dfree(m->ctx, m->attn_norm, nn * 4);
+    dfree(m->ctx, m->ffn_norm, nn * 4);
+    delete m;
+}
+
+extern "C" pf_status pf_model_set_matrix(pf_model* m, uint32_t layer, int32_t id, int32_t fmt, const uint8_t* codes,
+                                         const uint16_t* scales) {
+    if (!m || !codes || !scales || layer >= m->d.n_layers || id < 0 || id > 6) return PF_ERR_ARG;
+    pf_ctx* c = m->ctx;
+    const uint32_t D = m->d.n_embd, F = m->d.n_ff;
+    pf_matrix** slot;
+    uint32_t rows_total, cols, row0, rows;
+    if (id <= 2) { slot = &m->qkv[layer]; rows_total = 3 * D; cols = D; row0 = id * D; rows = D; }
+    else if (id == 3) { slot = &m->o[layer]; rows_total = D; cols = D; row0 = 0; rows = D; }
+    else if (id <= 5) { slot = &m->gu[layer]; rows_total = 2 * F; cols = D; row0 = (id - 4) * F; rows = F; }
+    else { slot = &m->down[layer]; rows_total = D; cols = F; row0 = 0; rows = D; }
+    if (!*slot) {
+        pf_status s = matrix_alloc(c, fmt, rows_total, cols, false, slot);
+        if (s) return s;
+    } else if ((*slot)->fmt != fmt) {
+        return fail(c, PF_ERR_ARG, "Q/K/V (and gate/up) of a layer must share one format");
+    }
+    pf_status s = matrix_put(*slot, row0, rows, codes, scales);
+    if (s) return s;
+    m->set_mask[layer] |= 1u << id;
+    return PF_OK;
+}
+
+extern "C" pf_status pf_model_set_embedding(pf_model* m, const uint8_t* codes, const uint16_t* scales) {
+    if (!m || !codes || !scales) return PF_ERR_ARG;
+    if (!m->emb) {
+        pf_status s = matrix_alloc(m->ctx, FMT_Q4, m->d.n_vocab, m->d.n_embd, true, &m->emb);
+        if (s) return s;
+    }
+    pf_status s = matrix_put(m->emb, 0, m->d.n_vocab, codes, scales);
+    if (s) return s;
+    m->emb_set = true;
+    return PF_OK;
+}
+
+extern "C" pf_status pf_model_set_mtp(pf_model* m, uint32_t head, int32_t which, const uint8_t* codes,
+                                      const uint16_t* scales) {
+    if (!m || !codes || !scales || head >= m->d.n_mtp || which < 0 || which > 2) return PF_ERR_ARG;
+    pf_matrix*& M = m->mtp[(size_t)head * 3 + which];
+    if (!M) {
+        pf_status s = matrix_alloc(m->ctx, FMT_Q4, m->d.n_embd, m->d.n_embd, true, &M);
+        if (s) return s;
+    }
+    pf_status s = matrix_put(M, 0, m->d.n_embd, codes, scales);
+    if (s) return s;
+    m->mtp_mask[head] |= 1u << which;
+    return PF_OK;
+}
+
+extern "C" pf_status pf_model_set_norm(pf_model* m, uint32_t layer, int32_t which, const float* w) {
+    if (!m || !w || layer >= m->d.n_layers || (which != 7 && which != 8)) return PF_ERR_ARG;
+    float* dst = (which == 7 ? m->attn_norm : m->ffn_norm) + (size_t)layer * m->d.n_embd;
+    PF_HIP(m->ctx, hipMemcpy(dst, w, m->d.n_embd * 4, hipMemcpyHostToDevice));
+    return PF_OK;
+}
+
+static bool model_complete(const pf_model* m) {
+    if (!m->emb_set) return false;
+    for (uint32_t l = 0; l < m->d.n_layers; l++)
+        if (m->set_mask[l] != 0x7Fu) return false;
+    for (uint32_t k = 0; k < m->d.n_mtp; k++)
+        if (m->mtp_mask[k] != 0x7u) return false;
+    return true;
+}
+
+// ================================================================= engine
+
+struct TimedPass { hipEvent_t a, b; bool verify; };
+
+struct pf_engine {
+    pf_model* m = nullptr;
+    pf_ctx* c = nullptr;
+    KvGeom g{};
+    KvPlanes kv{};
+    size_t kv_bytes = 0;
+    float* rope_c = nullptr;
+    float* rope_s = nullptr;
+    uint32_t rope_pos = 0;
+    // pass scratch
+    float* x = nullptr;
+    int8_t* act = nullptr;
+    float* as = nullptr;        // [4][8]
+    int32_t* bsum = nullptr;
+    double* part = nullptr;
+    float *q = nullptr, *k = nullptr, *v = nullptr;
+    float* S = nullptr;
+    float* Wp = nullptr;
+    uint32_t s_stride = 0, cstride = 0, kmax = 0;
+    float *logitsA = nullptr, *hiddenA = nullptr, *logitsB = nullptr, *hiddenB = nullptr;
+    float *mcur = nullptr, *mg = nullptr, *mu = nullptr, *ma = nullptr, *mlogits = nullptr;
+    PassDesc *pdA = nullptr, *pdB = nullptr, *pdP = nullptr;
+    DecodeState* st = nullptr;
+    int32_t* tokens = nullptr;
+    uint32_t tok_cap = 0;
+    uint32_t* word = nullptr;   // pinned readback
+    std::vector<std::pair<void*, size_t>> owned;
+    // host mirrors
+    uint32_t pos = 0;
+    uint32_t pool_mat = 0;
+    bool hidden_valid = false;
+    size_t max_memory = 0;
+    // timing
+    std::vector<TimedPass> timed;
+    size_t timed_used = 0;
+    // per-launch timing of the int8 GEMVs of verify passes (profiling mode)
+    bool profile = false;
+    bool in_verify = false;
+    std::vector<TimedPass> kev;
+    std::vector<double> kev_bytes;
+    size_t kev_used = 0;
+    double verify_us = 0, base_us = 0;
+    uint32_t verify_n = 0, base_n = 0;
+};
+
+template <class T>
+static pf_status ealloc(pf_engine* e, T** p, size_t n) {
+    pf_status s = dalloc_t(e->c, p, n);
+    if (!s) e->owned.push_back({(void*)*p, n * sizeof(T)});
+    return s;
+}
+
+// RoPE tables of src/engine.cpp:656-682 (theta 5e6): cos/sin of pos * freq
+// for pair t, freq = 1 / pow(theta, 2t / head_dim), computed with the host
+// C library in float as the reference does.
+static void rope_tables(uint32_t hd, uint32_t npos, std::vector<float>& cs, std::vector<float>& sn) {
+    const uint32_t half = hd / 2;
+    cs.resize((size_t)npos * half);
+    sn.resize((size_t)npos * half);
+    std::vector<float> freq(half);
+    for (uint32_t t = 0; t < half; t++) freq[t] = 1.0f / powf(5000000.0f, (float)(2 * t) / (float)hd);
+    for (uint32_t p = 0; p < npos; p++)
+        for (uint32_t t = 0; t < half; t++) {
+            float ang = (float)p * freq[t];
+            cs[(size_t)p * half + t] = cosf(ang);
+            sn[(size_t)p * half + t] = sinf(ang);
+        }
+}
+
+extern "C" pf_status pf_engine_create(pf_model* m, const pf_cache_desc* cd, pf_engine** out) {
+    if (!m || !cd || !out) return PF_ERR_ARG;
+    pf_ctx* c = m->ctx;
+    if (!model_complete(m)) return fail(c, PF_ERR_STATE, "model has unset matrices");
+    pf_engine* e = new pf_engine();
+    e->m = m;
+    e->c = c;
+    const pf_model_desc& d = m->d;
+    pf_status s = kv_geom(c, d.n_layers, d.n_heads, d.head_dim, cd->sink_size, cd->window_size, cd->pool_block,
+                          cd->max_context, &e->g);
+    if (!s) s = kv_alloc(c, e->g, &e->kv, &e->kv_bytes);
+    if (s) { delete e; return s; }
+    const uint32_t D = d.n_embd, F = d.n_ff, V = d.n_vocab, H = d.n_heads, hd = d.head_dim, MR = MAX_PASS_ROWS;
+    e->rope_pos = cd->max_context + 2 * MR;
+    {
+        std::vector<float> cs, sn;
+        rope_tables(hd, e->rope_pos, cs, sn);
+        s = ealloc(e, &e->rope_c, cs.size());
+        if (!s) s = ealloc(e, &e->rope_s, sn.size());
+        if (s) { pf_engine_destroy(e); return s; }
+        PF_HIP(c, hipMemcpy(e->rope_c, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+        PF_HIP(c, hipMemcpy(e->rope_s, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+    }
+    e->kmax = std::max(D, F);
+    size_t part_elems = 0;
+    for (uint32_t l = 0; l < d.n_layers; l++)
+        for (pf_matrix* W : {m->qkv[l], m->o[l], m->gu[l], m->down[l]})
+            part_elems = std::max(part_elems, gemv_part_elems(W, MR));
+    const uint32_t cmax = KV_SINK_ROWS + e->g.pool_cap + e->g.window;
+    e->s_stride = cmax + 8;
+    e->cstride = (cmax + 63) / 64 + 1;
+    if (!s) s = ealloc(e, &e->x, (size_t)MR * D);
+    if (!s) s = ealloc(e, &e->act, (size_t)MR * e->kmax);
+    if (!s) s = ealloc(e, &e->as, 4 * MR);
+    if (!s) s = ealloc(e, &e->bsum, (size_t)MR * (e->kmax / 32));
+    if (!s) s = ealloc(e, &e->part, std::max<size_t>(part_elems, 1));
+    if (!s) s = ealloc(e, &e->q, (size_t)MR * D);
+    if (!s) s = ealloc(e, &e->k, (size_t)MR * D);
+    if (!s) s = ealloc(e, &e->v, (size_t)MR * D);
+    if (!s) s = ealloc(e, &e->S, (size_t)MR * H * e->s_stride);
+    if (!s) s = ealloc(e, &e->Wp, (size_t)MR * H * e->cstride * hd);
+    if (!s) s = ealloc(e, &e->logitsA, (size_t)MR * V);
+    if (!s) s = ealloc(e, &e->hiddenA, (size_t)MR * D);
+    if (!s) s = ealloc(e, &e->logitsB, (size_t)MR * V);
+    if (!s) s = ealloc(e, &e->hiddenB, (size_t)MR * D);
+    if (!s) s = ealloc(e, &e->mcur, D);
+    if (!s) s = ealloc(e, &e->mg, D);
+    if (!s) s = ealloc(e, &e->mu, D);
+    if (!s) s = ealloc(e, &e->ma, D);
+    if (!s) s = ealloc(e, &e->mlogits, (size_t)std::max(1u, d.n_mtp) * V);
+    if (!s) s = ealloc(e, &e->pdA, 1);
+    if (!s) s = ealloc(e, &e->pdB, 1);
+    if (!s) s = ealloc(e, &e->pdP, 1);
+    if (!s) s = ealloc(e, &e->st, 1);
+    if (s) { pf_engine_destroy(e); return s; }
+    if (hipHostMalloc((void**)&e->word, 64, hipHostMallocDefault) != hipSuccess) {
+        pf_engine_destroy(e);
+        return fail(c, PF_ERR_HIP, "hipHostMalloc failed");
+    }
+    PassDesc pb{};
+    pb.m = d.n_mtp + 1;
+    PF_HIP(c, hipMemcpy(e->pdB, &pb, sizeof(pb), hipMemcpyHostToDevice));
+    DecodeState st0{};
+    PF_HIP(c, hipMemcpy(e->st, &st0, sizeof(st0), hipMemcpyHostToDevice));
+    *out = e;
+    return PF_OK;
+}
+
+extern "C" void pf_engine_destroy(pf_engine* e) {
+    if (!e) return;
+    (void)hipStreamSynchronize(e->c->stream);
+    for (auto& t : e->timed) { (void)hipEventDestroy(t.a); (void)hipEventDestroy(t.b); }
+    for (auto& t : e->kev) { (void)hipEventDestroy(t.a); (void)hipEventDestroy(t.b); }
+    for (auto& p : e->owned) dfree(e->c, p.first, p.second);
+    if (e->tokens) dfree(e->c, e->tokens, (size_t)e->tok_cap * 4);
+    kv_free(e->c, e->g, &e->kv);
+    if (e->word) (void)hipHostFree(e->word);
+    delete e;
+}
+
+extern "C" pf_status pf_engine_reset(pf_engine* e) {
+    if (!e) return PF_ERR_ARG;
+    e->pos = 0;
+    e->pool_mat = 0;
+    e->hidden_valid = false;
+    return PF_OK;
+}
+
+extern "C" uint32_t pf_engine_position(const pf_engine* e) { return e ? e->pos : 0; }
+
+extern "C" pf_status pf_engine_set_max_memory(pf_engine* e, size_t bytes) {
+    if (!e) return PF_ERR_ARG;
+    e->max_memory = bytes;
+    return PF_OK;
+}
+
+static pf_status timed_begin(pf_engine* e, bool verify, TimedPass** tp) {
+    *tp = nullptr;
+    if (e->timed_used == e->timed.size()) {
+        TimedPass t{};
+        PF_HIP(e->c, hipEventCreate(&t.a));
+        PF_HIP(e->c, hipEventCreate(&t.b));
+        e->timed.push_back(t);
+    }
+    TimedPass* t = &e->timed[e->timed_used++];
+    t->verify = verify;
+    PF_HIP(e->c, hipEventRecord(t->a, e->c->stream));
+    *tp = t;
+    return PF_OK;
+}
+
+// Int8 GEMV launch of a pass; in profiling mode the launches of verify
+// passes are bracketed by HIP events on the engine's stream.
+static pf_status pass_gemv(pf_engine* e, const pf_matrix* W, uint32_t M) {
+    hipStream_t st = e->c->stream;
+    const uint32_t ks = e->kmax, bs = e->kmax / 32;
+    TimedPass* t = nullptr;
+    if (e->profile && e->in_verify) {
+        if (e->kev_used == e->kev.size()) {
+            TimedPass n{};
+            PF_HIP(e->c, hipEventCreate(&n.a));
+            PF_HIP(e->c, hipEventCreate(&n.b));
+            e->kev.push_back(n);
+            e->kev_bytes.push_back(0.0);
+        }
+        e->kev_bytes[e->kev_used] = (double)W->bytes + (double)M * W->cols + (double)M * W->rows * 4.0;
+        t = &e->kev[e->kev_used++];
+        PF_HIP(e->c, hipEventRecord(t->a, st));
+    }
+    launch_gemv(st, W, M, e->act, ks, e->bsum, bs, e->part);
+    if (t) PF_HIP(e->c, hipEventRecord(t->b, st));
+    return PF_OK;
+}
+
+// One forward pass of M rows (the PassDesc at `pd` holds positions and
+// tokens; pos0 is the host's copy of the first position).  hidden/logits
+// outputs are device [M][D] / [M][V]; logits may be null.
+static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0, float* logits, float* hidden) {
+    pf_ctx* c = e->c;
+    const pf_model* m = e->m;
+    const pf_model_desc& d = m->d;
+    const KvGeom& g = e->g;
+    hipStream_t st = c->stream;
+    const uint32_t D = d.n_embd, F = d.n_ff, H = d.n_heads, hd = d.head_dim;
+    if (pos0 + M > e->rope_pos) return fail(c, PF_ERR_CAPACITY, "position beyond the engine's max_context");
+    // pooled rows any row of this pass can see
+    const KvView vlast = kv_view(g, pos0 + M - 1);
+    if (vlast.pool > e->pool_mat) {
+        if (vlast.pool > g.pool_cap) return fail(c, PF_ERR_CAPACITY, "pooled rows exceed capacity");
+        hipLaunchKernelGGL(k_pool_rows, dim3(g.n_layers * g.n_heads, vlast.pool - e->pool_mat),
+                           dim3(hd <= 64 ? 64 : 128), 0, st, g, e->kv, 0u, e->pool_mat);
+        e->pool_mat = vlast.pool;
+    }
+    const uint32_t cmax = vlast.count();
+    const uint32_t zb = (cmax + 1 + 255) / 256, nch = (cmax + 63) / 64;
+    const uint32_t ks = e->kmax, bs = e->kmax / 32;
+    float* as0 = e->as;           // attention-norm act
+    float* as1 = e->as + 8;       // attention output act
+    float* as2 = e->as + 16;      // ffn-norm act
+    float* as3 = e->as + 24;      // swiglu act
+
+    hipLaunchKernelGGL(k_embed, dim3((D + 255) / 256, M), dim3(256), 0, st, m->emb->data, m->emb->scales, d.n_vocab, D,
+                       pd, e->x);
+    for (uint32_t l = 0; l < d.n_layers; l++) {
+        const float* an = m->attn_norm + (size_t)l * D;
+        const float* fn = m->ffn_norm + (size_t)l * D;
+        if (l == 0) {
+            PF_PER_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(M), dim3(256), 0, st, e->x, D,
+                                                (const double*)nullptr, 0u, M, (const float*)nullptr, an, e->act, ks,
+                                                as0, e->bsum, bs));
+        } else {
+            PF_PER_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(M), dim3(256), 0, st, e->x, D, e->part,
+                                                m->down[l - 1]->splits, M, as3, an, e->act, ks, as0, e->bsum, bs));
+        }
+        if (pf_status s = pass_gemv(e, m->qkv[l], M)) return s;
+        hipLaunchKernelGGL(k_qkv_post, dim3(M, H), dim3(64), 0, st, e->part, m->qkv[l]->splits, M, as0, pd, e->rope_c,
+                           e->rope_s, g, e->kv, l, e->q, e->k, e->v);
+        hipLaunchKernelGGL(k_attn_scores, dim3(M, H, zb), dim3(256), 0, st, pd, g, e->kv, l, -1, 0u, -1, e->q, e->k,
+                           e->S, e->s_stride, 1);
+        hipLaunchKernelGGL(k_attn_softmax, dim3(M, H), dim3(256), 0, st, pd, g, -1, 0u, e->S, e->s_stride);
+        if (nch)
+            hipLaunchKernelGGL(k_attn_wsum, dim3(M, H, nch), dim3(128), 0, st, pd, g, e->kv, l, -1, 0u, -1,
+                               0xFFFFFFFFu, e->S, e->s_stride, e->Wp, e->cstride);
+        PF_PER_SWITCH(D, hipLaunchKernelGGL(k_attn_combine<PER>, dim3(M), dim3(256), 0, st, pd, g, -1, 0u, e->S,
+                                            e->s_stride, e->Wp, e->cstride, e->v, (float*)nullptr, e->act, ks, as1,
+                                            e->bsum, bs));
+        if (pf_status s = pass_gemv(e, m->o[l], M)) return s;
+        PF_PER_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(M), dim3(256), 0, st, e->x, D, e->part,
+                                            m->o[l]->splits, M, as1, fn, e->act, ks, as2, e->bsum, bs));
+        if (pf_status s = pass_gemv(e, m->gu[l], M)) return s;
+        PF_PER_SWITCH(F, hipLaunchKernelGGL(k_swiglu_quant<PER>, dim3(M), dim3(256), 0, st, e->part, m->gu[l]->splits,
+                                            M, F, as2, e->act, ks, as3, e->bsum, bs));
+        if (pf_status s = pass_gemv(e, m->down[l], M)) return s;
+    }
+    if (d.n_layers)
+        hipLaunchKernelGGL(k_resid_add, dim3((D + 255) / 256, M), dim3(256), 0, st, e->x, D, e->part,
+                           m->down[d.n_layers - 1]->splits, M, as3);
+    if (hidden) PF_HIP(c, hipMemcpyAsync(hidden, e->x, (size_t)M * D * 4, hipMemcpyDeviceToDevice, st));
+    if (logits) launch_gemv_f32(st, m->emb, M, e->x, D, logits, d.n_vocab, nullptr);
+    PF_LAUNCHED(c);
+    e->hidden_valid = true;
+    return PF_OK;
+}
+
+extern "C" pf_status pf_forward(pf_engine* e, const int32_t* tokens, uint32_t n, float* logits, float* hidden) {
+    if (!e || !tokens || n == 0 || n > MAX_PASS_ROWS) return PF_ERR_ARG;
+    pf_ctx* c = e->c;
+    const pf_model_desc& d = e->m->d;
+    PassDesc pd{};
+    pd.pos0 = e->pos;
+    pd.m = n;
+    for (uint32_t i = 0; i < n; i++) {
+        if (tokens[i] < 0 || (uint32_t)tokens[i] >= d.n_vocab) return fail(c, PF_ERR_ARG, "token id out of range");
+        pd.tok[i] = tokens[i];
+    }
+    PF_HIP(c, hipMemcpyAsync(e->pdP, &pd, sizeof(pd), hipMemcpyHostToDevice, c->stream));
+    pf_status s = run_pass(e, e->pdP, n, e->pos, logits ? e->logitsA : nullptr, e->hiddenA);
+    if (s) return s;
+    e->pos += n;
+    if (logits)
+        PF_HIP(c, hipMemcpyAsync(logits, e->logitsA, (size_t)n * d.n_vocab * 4, hipMemcpyDeviceToHost, c->stream));
+    if (hidden) PF_HIP(c, hipMemcpyAsync(hidden, e->hiddenA, (size_t)n * d.n_embd * 4, hipMemcpyDeviceToHost, c->stream));
+    PF_HIP(c, hipStreamSynchronize(c->stream));
+    return PF_OK;
+}
+
+// MTPHeads::forward chain on the device hidden state h0 (src/mtp.cpp:63-127):
+// gate, up, silu(gate) * up, down + residual, tied unembed, per head; with
+// `sample` the draft of head k is sampled right after its logits.
+static pf_status mtp_chain(pf_engine* e, const float* h0, bool sample, const SamplingCfg* cfg, uint64_t seed) {
+    pf_ctx* c = e->c;
+    const pf_model* m = e->m;
+    const pf_model_desc& d = m->d;
+    hipStream_t st = c->stream;
+    const uint32_t D = d.n_embd, V = d.n_vocab;
+    PF_HIP(c, hipMemcpyAsync(e->mcur, h0, D * 4, hipMemcpyDeviceToDevice, st));
+    for (uint32_t k = 0; k < d.n_mtp; k++) {
+        launch_gemv_f32(st, m->mtp[k * 3 + 0], 1, e->mcur, D, e->mg, D, nullptr);
+        launch_gemv_f32(st, m->mtp[k * 3 + 1], 1, e->mcur, D, e->mu, D, nullptr);
+        hipLaunchKernelGGL(k_silu_mul, dim3((D + 255) / 256), dim3(256), 0, st, e->mg, e->mu, e->ma, D);
+        launch_gemv_f32(st, m->mtp[k * 3 + 2], 1, e->ma, D, e->mcur, D, e->mcur);
+        float* lk = e->mlogits + (size_t)k * V;
+        launch_gemv_f32(st, m->emb, 1, e->mcur, D, lk, V, nullptr);
+        if (sample)
+            hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, lk, V, 0, V, *cfg, seed, e->st, e->tokens,
+                               e->tok_cap, e->pdB, (int32_t)ROLE_DRAFT, (int32_t)k, (int32_t*)nullptr);
+    }
+    PF_LAUNCHED(c);
+    return PF_OK;
+}
+
+extern "C" pf_status pf_mtp_forward(pf_engine* e, const float* hidden, float* logits) {
+    if (!e || !hidden || !logits) return PF_ERR_ARG;
+    pf_ctx* c = e->c;
+    const pf_model_desc& d = e->m->d;
+    PF_HIP(c, hipMemcpyAsync(e->hiddenA, hidden, d.n_embd * 4, hipMemcpyHostToDevice, c->stream));
+    pf_status s = mtp_chain(e, e->hiddenA, false, nullptr, 0);
+    if (s) return s;
+    PF_HIP(c, hipMemcpyAsync(logits, e->mlogits, (size_t)d.n_mtp * d.n_vocab * 4, hipMemcpyDeviceToHost, c->stream));
+    PF_HIP(c, hipStreamSynchronize(c->stream));
+    return PF_OK;
+}
+
+static SamplingCfg to_cfg(const pf_sampling* s) {
+    SamplingCfg c{0.8f, 0.95f, 40u, 0};   // SamplingConfig defaults, include/forge/types.hpp:36-41
+    if (s) { c.temperature = s->temperature; c.top_p = s->top_p; c.top_k = s->top_k; c.greedy = s->greedy; }
+    return c;
+}
+
+extern "C" pf_status pf_sample(pf_engine* e, const float* logits, const pf_sampling* cfg, uint64_t seed,
+                               uint64_t* draw_index, int32_t* token) {
+    if (!e || !logits || !token) return PF_ERR_ARG;
+    pf_ctx* c = e->c;
+    const uint32_t V = e->m->d.n_vocab;
+    DecodeState st{};
+    st.draw = draw_index ? *draw_index : 0;
+    PF_HIP(c, hipMemcpyAsync(e->st, &st, sizeof(st), hipMemcpyHostToDevice, c->stream));
+    PF_HIP(c, hipMemcpyAsync(e->logitsA, logits, (size_t)V * 4, hipMemcpyHostToDevice, c->stream));
+    hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, c->stream, e->logitsA, V, 0, V, to_cfg(cfg), seed, e->st,
+                       (int32_t*)nullptr, 0u, (PassDesc*)nullptr, (int32_t)ROLE_PLAIN, 0,
+                       (int32_t*)&e->st->round_word);
+    PF_LAUNCHED(c);
+    PF_HIP(c, hipMemcpyAsync(&st, e->st, sizeof(st), hipMemcpyDeviceToHost, c->stream));
+    PF_HIP(c, hipStreamSynchronize(c->stream));
+    *token = (int32_t)st.round_word;
+    if (draw_index) *draw_index = st.draw;
+    return PF_OK;
+}
+
+// Engine::generate, src/engine.cpp:276-396.  Prompt prefilled in passes
+// of up to 8 tokens; then MTP rounds (src/engine.cpp:304-373) as one base
+// pass (skipped when the previous round accepted every draft: its last
+// verify row already is F(cur)), the draft chain, one verify pass over
+// [T1, drafts], acceptance and the corrective on the device; the host reads
+// one word per round.
+extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n_prompt, uint32_t max_new,
+                                 const pf_sampling* scfg, uint64_t seed, int32_t* tokens_out, uint32_t tokens_cap,
+                                 pf_gen_result* res) {
+    if (!e || (!prompt && n_prompt) || !tokens_out || !res) return PF_ERR_ARG;
+    pf_ctx* c = e->c;
+    const pf_model_desc& d = e->m->d;
+    hipStream_t st = c->stream;
+    const uint32_t V = d.n_vocab, D = d.n_embd, NM = d.n_mtp;
+    std::memset(res, 0, sizeof(*res));
+    if ((uint64_t)n_prompt + max_new + 1 > tokens_cap) return fail(c, PF_ERR_CAPACITY, "tokens_cap < prompt + max_new + 1");
+    if ((uint64_t)e->pos + n_prompt + max_new + MAX_PASS_ROWS > e->rope_pos)
+        return fail(c, PF_ERR_CAPACITY, "prompt + max_new_tokens exceed the engine's max_context");
+    for (uint32_t i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || (uint32_t)prompt[i] >= V) return fail(c, PF_ERR_ARG, "prompt token id out of range");
+    const SamplingCfg cfg = to_cfg(scfg);
+    if (e->tok_cap < tokens_cap) {
+        if (e->tokens) dfree(c, e->tokens, (size_t)e->tok_cap * 4);
+        e->tokens = nullptr;
+        e->tok_cap = 0;
+        pf_status s = dalloc_t(c, &e->tokens, tokens_cap);
+        if (s) return s;
+        e->tok_cap = tokens_cap;
+    }
+    if (n_prompt) PF_HIP(c, hipMemcpyAsync(e->tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, st));
+    auto t0 = std::chrono::steady_clock::now();
+    // prefill (src/engine.cpp:286-290): every prompt token forwarded in order
+    std::vector<PassDesc> pds((n_prompt + MAX_PASS_ROWS - 1) / MAX_PASS_ROWS);
+    for (uint32_t i = 0, j = 0; i < n_prompt; i += MAX_PASS_ROWS, j++) {
+        uint32_t n = std::min(MAX_PASS_ROWS, n_prompt - i);
+        PassDesc& pd = pds[j];
+        pd = PassDesc{};
+        pd.pos0 = e->pos;
+        pd.m = n;
+        for (uint32_t r = 0; r < n; r++) pd.tok[r] = prompt[i + r];
+        PF_HIP(c, hipMemcpyAsync(e->pdP, &pd, sizeof(pd), hipMemcpyHostToDevice, st));
+        pf_status s = run_pass(e, e->pdP, n, e->pos, nullptr, e->hiddenA);
+        if (s) return s;
+        e->pos += n;
+    }
+    DecodeState s0{};
+    s0.pos = e->pos;
+    s0.cur = n_prompt ? prompt[n_prompt - 1] : 0;
+    s0.n_tokens = n_prompt;
+    PF_HIP(c, hipMemcpyAsync(e->st, &s0, sizeof(s0), hipMemcpyHostToDevice, st));
+    PF_HIP(c, hipStreamSynchronize(st));
+    auto t1 = std::chrono::steady_clock::now();
+
+    e->timed_used = 0;
+    e->kev_used = 0;
+    uint32_t n_gen = 0;
+    bool have_row = false;
+    pf_status s = PF_OK;
+    while (n_gen < max_new) {
+        if (e->max_memory && c->bytes > e->max_memory) {   // src/engine.cpp:297-301
+            res->oom_protected = 1;
+            break;
+        }
+        const bool mtp_round = NM > 0 && e->hidden_valid && n_gen + 4 <= max_new;   // src/engine.cpp:304-305
+        TimedPass* tp = nullptr;
+        const float* base_logits;
+        const float* base_hidden;
+        if (have_row) {
+            hipLaunchKernelGGL(k_ctl_reuse_row, dim3(1), dim3(1), 0, st, e->st);
+            base_logits = e->logitsB + (size_t)NM * V;
+            base_hidden = e->hiddenB + (size_t)NM * D;
+            e->pos += 1;
+            have_row = false;
+        } else {
+            hipLaunchKernelGGL(k_ctl_pass_a, dim3(1), dim3(1), 0, st, e->st, e->pdA);
+            if ((s = timed_begin(e, false, &tp))) return s;
+            if ((s = run_pass(e, e->pdA, 1, e->pos, e->logitsA, e->hiddenA))) return s;
+            PF_HIP(c, hipEventRecord(tp->b, st));
+            res->passes++;
+            base_logits = e->logitsA;
+            base_hidden = e->hiddenA;
+            e->pos += 1;
+        }
+        if (mtp_round) {
+            hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, base_logits, V, 0, V, cfg, seed, e->st, e->tokens,
+                               e->tok_cap, e->pdB, (int32_t)ROLE_T1, 0, (int32_t*)nullptr);
+            if ((s = mtp_chain(e, base_hidden, true, &cfg, seed))) return s;
+            if ((s = timed_begin(e, true, &tp))) return s;
+            e->in_verify = true;
+            s = run_pass(e, e->pdB, NM + 1, e->pos, e->logitsB, e->hiddenB);
+            e->in_verify = false;
+            if (s) return s;
+            PF_HIP(c, hipEventRecord(tp->b, st));
+            res->passes++;
+            hipLaunchKernelGGL(k_argmax_rows, dim3(NM + 1), dim3(1024), 0, st, e->logitsB, V, V, e->pdB,
+                               e->st->row_argmax);
+            hipLaunchKernelGGL(k_ctl_accept, dim3(1), dim3(1), 0, st, e->st, e->pdB, e->tokens, e->tok_cap);
+            hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, e->logitsB, V, -1, V, cfg, seed, e->st, e->tokens,
+                               e->tok_cap, e->pdB, (int32_t)ROLE_CORRECTIVE, 0, (int32_t*)nullptr);
+            PF_LAUNCHED(c);
+            PF_HIP(c, hipMemcpyAsync(e->word, &e->st->round_word, 4, hipMemcpyDeviceToHost, st));
+            PF_HIP(c, hipStreamSynchronize(st));
+            const uint32_t w = e->word[0], a = w & 0xFFu, pushed = (w >> 8) & 1u;
+            n_gen += 1 + a + pushed;
+            res->rounds++;
+            if (a < NM) {
+                e->pos += a + 1;
+            } else {
+                e->pos += NM;
+                have_row = true;
+            }
+        } else {
+            // single-token path (src/engine.cpp:377-386)
+            hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, base_logits, V, 0, V, cfg, seed, e->st, e->tokens,
+                               e->tok_cap, e->pdB, (int32_t)ROLE_FALLBACK, 0, (int32_t*)nullptr);
+            PF_LAUNCHED(c);
+            n_gen += 1;
+        }
+    }
+    DecodeState sf{};
+    PF_HIP(c, hipMemcpyAsync(&sf, e->st, sizeof(sf), hipMemcpyDeviceToHost, st));
+    PF_HIP(c, hipStreamSynchronize(st));
+    auto t2 = std::chrono::steady_clock::now();
+    if (sf.pos != e->pos) return fail(c, PF_ERR_STATE, "device and host positions diverged");
+    const uint32_t nt = std::min(sf.n_tokens, tokens_cap);
+    PF_HIP(c, hipMemcpy(tokens_out, e->tokens, (size_t)nt * 4, hipMemcpyDeviceToHost));
+    res->n_tokens = nt;
+    res->mtp_accepted = (int32_t)sf.accepted;
+    res->mtp_rejected = (int32_t)sf.rejected;
+    res->prefill_seconds = std::chrono::duration<double>(t1 - t0).count();
+    res->decode_seconds = std::chrono::duration<double>(t2 - t1).count();
+    e->verify_us = e->base_us = 0;
+    e->verify_n = e->base_n = 0;
+    for (size_t i = 0; i < e->timed_used; i++) {
+        float ms = 0;
+        PF_HIP(c, hipEventElapsedTime(&ms, e->timed[i].a, e->timed[i].b));
+        if (e->timed[i].verify) { e->verify_us += ms * 1000.0; e->verify_n++; }
+        else { e->base_us += ms * 1000.0; e->base_n++; }
+    }
+    return PF_OK;
+}
+
+extern "C" pf_status pf_engine_profile(pf_engine* e, int32_t enable) {
+    if (!e) return PF_ERR_ARG;
+    e->profile = enable != 0;
+    return PF_OK;
+}
+
+extern "C" pf_status pf_engine_gemv_stats(pf_engine* e, uint32_t* launches, double* avg_us, double* avg_bytes) {
+    if (!e) return PF_ERR_ARG;
+    PF_HIP(e->c, hipStreamSynchronize(e->c->stream));
+    double us = 0, by = 0;
+    for (size_t i = 0; i < e->kev_used; i++) {
+        float ms = 0;
+        PF_HIP(e->c, hipEventElapsedTime(&ms, e->kev[i].a, e->kev[i].b));
+        us += ms * 1000.0;
+        by += e->kev_bytes[i];
+    }
+    const double n = (double)e->kev_used;
+    if (launches) *launches = (uint32_t)e->kev_used;
+    if (avg_us) *avg_us = n ? us / n : 0.0;
+    if (avg_bytes) *avg_bytes = n ? by / n : 0.0;
+    return PF_OK;
+}
+
+extern "C" pf_status pf_engine_pass_times(const pf_engine* e, double* verify_us, double* base_us, uint32_t* vn,
+                                          uint32_t* bn) {
+    if (!e) return PF_ERR_ARG;
+    if (verify_us) *verify_us = e->verify_n ? e->verify_us / e->verify_n : 0.0;
+    if (base_us) *base_us = e->base_n ? e->base_us / e->base_n : 0.0;
+    if (vn) *vn = e->verify_n;
+    if (bn) *bn = e->base_n;
+    return PF_OK;
+}

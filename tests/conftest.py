@@ -13,11 +13,8 @@ def pytest_configure(config):
 
 
 def _has_gpu():
-    try:
-        import torch
-        return torch.cuda.is_available()
-    except Exception:
-        return False
+    # no torch here: the library brings its own HIP runtime and device memory
+    return os.path.exists("/dev/kfd")
 
 
 @pytest.fixture(scope="session")
@@ -26,3 +23,24 @@ def gpu():
         pytest.skip("no GPU")
     import pocketforge_amd as pf
     return pf.Context(0)
+
+
+@pytest.fixture(scope="session")
+def tiny_weights():
+    from pocketforge_amd import weights as W
+    return W.TINY, W.make_weights(W.TINY, seed=1234)
+
+
+@pytest.fixture(scope="session")
+def tiny_model(gpu, tiny_weights):
+    import pocketforge_amd as pf
+    cfg, w = tiny_weights
+    return pf.Model(gpu, cfg, w)
+
+
+@pytest.fixture()
+def tiny_engine(tiny_model):
+    import pocketforge_amd as pf
+    e = pf.Engine(tiny_model, sink_size=4, window_size=64, pool_block=6, max_context=512)
+    yield e
+    e.close()

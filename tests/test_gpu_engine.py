@@ -1,0 +1,163 @@
+"""Engine-level parity of the gfx950 path against the oracle: forward
+passes (token by token and batched, across window eviction and pooling),
+MTP heads, and whole generate() token streams, bit-exact."""
+import numpy as np
+import pytest
+
+import oracle as O
+import pocketforge_amd as pf
+from pocketforge_amd import weights as W
+
+pytestmark = pytest.mark.gpu
+
+KV = dict(sink_size=4, window_size=64, pool_block=6, max_context=512)
+
+
+def _oracle(cfg, w, kv=KV):
+    c = dict(cfg)
+    c.update(kv)
+    return O.Model(c, w)
+
+
+def test_forward_token_by_token(tiny_weights, tiny_engine):
+    cfg, w = tiny_weights
+    om = _oracle(cfg, w)
+    toks = W.prompt_ids(12, cfg["n_vocab"], seed=3)
+    for t in toks:
+        lg, hg = tiny_engine.forward([t])
+        lo, ho = om.forward(t)
+        np.testing.assert_array_equal(hg[0], ho)
+        np.testing.assert_array_equal(lg[0], lo)
+    om.close()
+
+
+@pytest.mark.parametrize("chunks", [[8, 8, 8, 8, 8, 8, 8, 8, 8, 8, 8, 8, 8],
+                                    [5, 1, 5, 1, 5, 1, 7, 3, 8, 2, 5, 5, 5, 5, 5, 5, 5, 5, 5, 5, 5, 5]])
+def test_batched_passes_across_eviction_and_pooling(tiny_weights, tiny_engine, chunks):
+    """Rows of a pass equal sequential forwards, past the window (64) with
+    pooled blocks of 6 and 4 sink rows."""
+    cfg, w = tiny_weights
+    om = _oracle(cfg, w)
+    n = sum(chunks)
+    toks = W.prompt_ids(n, cfg["n_vocab"], seed=11)
+    i = 0
+    for c in chunks:
+        lg, hg = tiny_engine.forward(toks[i:i + c])
+        for j in range(c):
+            lo, ho = om.forward(toks[i + j])
+            np.testing.assert_array_equal(hg[j], ho, err_msg=f"row {i + j}")
+            np.testing.assert_array_equal(lg[j], lo, err_msg=f"row {i + j}")
+        i += c
+    assert tiny_engine.pos == n
+    om.close()
+
+
+def test_mtp_forward(tiny_weights, tiny_engine):
+    cfg, w = tiny_weights
+    om = _oracle(cfg, w)
+    rng = np.random.default_rng(4)
+    h = rng.standard_normal(cfg["n_embd"]).astype(np.float32)
+    np.testing.assert_array_equal(tiny_engine.mtp_forward(h), om.mtp_forward(h))
+    om.close()
+
+
+def _zero_mats(w, layers=True, mtp=True, scale=0.0, seed=0):
+    """Copy of a weight set with zeroed (or tiny random) matrices."""
+    import copy
+    w2 = copy.deepcopy(w)
+    rng = np.random.default_rng(seed)
+    if layers:
+        for lw in w2["layers"]:
+            for n in W.NAMES:
+                fmt, codes, scales = lw[n]
+                if scale == 0.0:
+                    codes = np.full_like(codes, 0x88 if fmt == pf.FMT_Q4 else (0xAA if fmt == pf.FMT_Q2 else 0x55))
+                    scales = np.zeros_like(scales)
+                else:
+                    r, nb, _ = codes.shape
+                    x = (rng.standard_normal((r, nb * 32)) * scale).astype(np.float32)
+                    codes, scales = pf.quantize_matrix(x, fmt)
+                lw[n] = (fmt, codes, scales)
+    if mtp:
+        for hw in w2["mtp"]:
+            for n in ("gate", "up", "down"):
+                fmt, codes, scales = hw[n]
+                hw[n] = (fmt, np.full_like(codes, 0x88), np.zeros_like(scales))
+    return w2
+
+
+GREEDY = pf.Sampling(0.8, 0.95, 40, 1)
+TOP_P = pf.Sampling(0.8, 0.95, 40, 0)
+TEMP = pf.Sampling(1.1, 1.0, 0, 0)
+TOP_K = pf.Sampling(0.9, 1.0, 12, 0)
+
+
+def _gen_both(gpu, cfg, w, prompt, max_new, samp, kv=KV, seed=7):
+    m = pf.Model(gpu, cfg, w)
+    e = pf.Engine(m, **kv)
+    toks, res = e.generate(prompt, max_new, samp, seed)
+    om = _oracle(cfg, w, kv)
+    ot, oa, orj = om.generate(prompt, max_new, O.Sampling(samp.temperature, samp.top_p, samp.top_k, samp.greedy),
+                              seed)
+    om.close()
+    e.close()
+    m.close()
+    return toks, res, ot, oa, orj
+
+
+@pytest.mark.parametrize("case", ["random", "full_accept", "mixed"])
+def test_generate_greedy_matches_oracle(gpu, tiny_weights, case):
+    cfg, w = tiny_weights
+    if case == "full_accept":
+        w = _zero_mats(w)                         # the model repeats its input: every draft is accepted
+    elif case == "mixed":
+        w = _zero_mats(w, scale=0.004, seed=5)    # mostly repeats: accept/reject mix
+    prompt = W.prompt_ids(20, cfg["n_vocab"], seed=9)
+    toks, res, ot, oa, orj = _gen_both(gpu, cfg, w, prompt, 70, GREEDY)
+    np.testing.assert_array_equal(toks, ot)
+    assert (res.mtp_accepted, res.mtp_rejected) == (oa, orj)
+    if case == "full_accept":
+        assert oa > 40
+    if case == "mixed":
+        print("mixed: accepted", oa, "rejected", orj)
+
+
+@pytest.mark.parametrize("samp", [TOP_P, TEMP, TOP_K], ids=["top_p", "temperature", "top_k"])
+def test_generate_stochastic_matches_oracle(gpu, tiny_weights, samp):
+    cfg, w = tiny_weights
+    w = _zero_mats(w, scale=0.004, seed=6)
+    prompt = W.prompt_ids(10, cfg["n_vocab"], seed=2)
+    toks, res, ot, oa, orj = _gen_both(gpu, cfg, w, prompt, 50, samp, seed=123)
+    np.testing.assert_array_equal(toks, ot)
+    assert (res.mtp_accepted, res.mtp_rejected) == (oa, orj)
+
+
+@pytest.mark.parametrize("n_prompt,max_new", [(0, 9), (1, 3), (5, 4), (3, 5), (17, 1)])
+def test_generate_edges(gpu, tiny_weights, n_prompt, max_new):
+    """Empty prompt (fallback first token), max_new < 4 (fallback only), the
+    n+4 <= N gate with its one-token overshoot."""
+    cfg, w = tiny_weights
+    w = _zero_mats(w, scale=0.004, seed=8)
+    prompt = W.prompt_ids(n_prompt, cfg["n_vocab"], seed=1)
+    toks, res, ot, oa, orj = _gen_both(gpu, cfg, w, prompt, max_new, GREEDY)
+    np.testing.assert_array_equal(toks, ot)
+    assert (res.mtp_accepted, res.mtp_rejected) == (oa, orj)
+
+
+def test_generate_long_context_pooling(gpu, tiny_weights):
+    """Window 16 / pool 3 / sink 2 with a 60-token prompt: decode rounds see
+    eviction and pooled rows created inside verify passes."""
+    cfg, w = tiny_weights
+    w = _zero_mats(w, scale=0.004, seed=10)
+    kv = dict(sink_size=2, window_size=16, pool_block=3, max_context=256)
+    prompt = W.prompt_ids(60, cfg["n_vocab"], seed=5)
+    toks, res, ot, oa, orj = _gen_both(gpu, cfg, w, prompt, 60, GREEDY, kv=kv)
+    np.testing.assert_array_equal(toks, ot)
+    assert (res.mtp_accepted, res.mtp_rejected) == (oa, orj)
+
+
+def test_oom_guard_stops_generation(gpu, tiny_weights, tiny_engine):
+    cfg, _ = tiny_weights
+    tiny_engine.set_max_memory(1)
+    toks, res = tiny_engine.generate(W.prompt_ids(4, cfg["n_vocab"]), 10, GREEDY)
+    assert res.oom_protected == 1 and len(toks) == 4
