@@ -201,14 +201,19 @@ pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n_prompt, ui
  * oom_protected when the context's device bytes exceed this (0 = off). */
 pf_status pf_engine_set_max_memory(pf_engine* e, size_t bytes);
 
-/* Timing hook for benchmarks: average device time in microseconds of the
- * verify passes (M = n_mtp + 1) and base passes (M = 1) issued by the last
- * pf_generate, measured with HIP events on the engine's stream. */
+/* Average device time (us, HIP events on the engine's stream) of the MTP
+ * rounds of the last pf_generate: base pass + draft + verify + accept. */
+pf_status pf_engine_round_time(const pf_engine* e, double* round_us, uint32_t* rounds);
+/* Average device time in microseconds of the verify passes (M = n_mtp + 1)
+ * and base passes (M = 1) of the last pf_generate run without captured
+ * graphs (profiling mode), measured with HIP events on the engine's
+ * stream. */
 pf_status pf_engine_pass_times(const pf_engine* e, double* verify_us, double* base_us,
                                uint32_t* verify_n, uint32_t* base_n);
 
-/* Profiling mode: brackets every int8 GEMV launch of the verify passes of
- * pf_generate with HIP events on the engine's stream. */
+/* Profiling mode: pf_generate issues its kernels one by one (no captured
+ * graphs) and every int8 GEMV dispatch of the verify passes carries HIP
+ * start/stop events. */
 pf_status pf_engine_profile(pf_engine* e, int32_t enable);
 /* Launch count, average duration (us) and average algorithmic bytes
  * (packed weights + int8 activations + fp32 outputs) of the GEMV launches

@@ -101,6 +101,7 @@ SYMBOLS = {
     "pf_engine_set_max_memory": (C.c_int32, [vp, C.c_size_t]),
     "pf_engine_pass_times": (C.c_int32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double), u32p, u32p]),
     "pf_engine_profile": (C.c_int32, [vp, C.c_int32]),
+    "pf_engine_round_time": (C.c_int32, [vp, C.POINTER(C.c_double), u32p]),
     "pf_engine_gemv_stats": (C.c_int32, [vp, u32p, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
 }
 
@@ -457,6 +458,11 @@ class Engine:
 
     def profile(self, enable=True):
         self.ctx.check(lib().pf_engine_profile(self.h, int(enable)), "pf_engine_profile")
+
+    def round_time(self):
+        us, n = C.c_double(0), C.c_uint32(0)
+        self.ctx.check(lib().pf_engine_round_time(self.h, C.byref(us), C.byref(n)), "pf_engine_round_time")
+        return us.value, n.value
 
     def gemv_stats(self):
         n, us, by = C.c_uint32(0), C.c_double(0), C.c_double(0)

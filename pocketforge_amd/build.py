@@ -15,10 +15,12 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
 # -ffp-contract=off: fused multiply-adds only where written (bit parity with
-# the CPU restatement).  Denormals are kept and fp32 divide/sqrt are
+# the CPU restatement).  -munsafe-fp-atomics: hardware fp64 atomic add (the
+# GEMV's split sums are exact, so their order never changes a bit; device
+# memory from hipMalloc only).  Denormals are kept and fp32 divide/sqrt are
 # correctly rounded.  Packed fp32 instructions are disabled.
 HIP_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off",
+    "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off", "-munsafe-fp-atomics",
     "-fno-gpu-flush-denormals-to-zero", "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result", "-I" + os.path.join(ROOT, "include"),

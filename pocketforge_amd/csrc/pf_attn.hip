@@ -9,8 +9,8 @@
 //                  dot over head_dim, and the fp32 self score
 //   k_attn_softmax per (row, head): max, exp, CANON(4) sum, normalise
 //   k_attn_wsum    per (row, head, 64-entry chunk): fmaf chain over entries
-//   k_attn_combine per row: chunk partials left to right + self term, then
-//                  quantize_activation_row for the O projection
+//   k_attn_merge   per (row, head): chunk partials left to right + self
+//                  term; the O projection's quantize_activation_row follows
 // k_pool_rows folds evicted window entries into pooled rows
 // (src/kv_cache.cpp:77-109) before a pass needs them.
 #include "pf_device.h"
@@ -57,27 +57,29 @@ __device__ __forceinline__ void store_pair(const KvGeom& g, KvPlanes kv, size_t 
     }
 }
 
-// Grid (M, heads), 64 threads.  part = fused QKV GEMV partials ([s][M][3D]).
+// Grid (M, heads), 64 threads.  acc = fused QKV GEMV accumulators
+// ([M][3D], cleared here), as = their activation scales.
 // RoPE of src/engine.cpp:732-749 with the host-computed angle tables
 // (cos/sin [position][head_dim/2]).
-__global__ __launch_bounds__(64) void k_qkv_post(const double* __restrict__ part, uint32_t splits, uint32_t M,
-                                                 const float* __restrict__ as, const PassDesc* __restrict__ pd,
+__global__ __launch_bounds__(64) void k_qkv_post(double* __restrict__ acc, const float* __restrict__ as,
+                                                 const PassDesc* __restrict__ pd,
                                                  const float* __restrict__ rc, const float* __restrict__ rs,
                                                  KvGeom g, KvPlanes kv, uint32_t layer,
                                                  float* __restrict__ q_out, float* __restrict__ k_out,
                                                  float* __restrict__ v_out) {
     const uint32_t m = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
     if (m >= pd->m) return;
-    const uint32_t hd = g.head_dim, D = g.n_heads * hd, N = 3 * D, half = hd >> 1;
+    const uint32_t hd = g.head_dim, D = g.n_heads * hd, half = hd >> 1;
     const uint32_t pos = pd->pos0 + m;
     const bool act = t < half;
     float k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
     if (act) {
+        const size_t r = (size_t)m * 3 * D;
         const float a = as[m];
         const uint32_t i0 = h * hd + 2 * t;
-        float q0 = gemv_out(part, splits, M, N, m, i0, a), q1 = gemv_out(part, splits, M, N, m, i0 + 1, a);
-        k0 = gemv_out(part, splits, M, N, m, D + i0, a); k1 = gemv_out(part, splits, M, N, m, D + i0 + 1, a);
-        v0 = gemv_out(part, splits, M, N, m, 2 * D + i0, a); v1 = gemv_out(part, splits, M, N, m, 2 * D + i0 + 1, a);
+        float q0 = take_acc(acc, r + i0, a), q1 = take_acc(acc, r + i0 + 1, a);
+        k0 = take_acc(acc, r + D + i0, a); k1 = take_acc(acc, r + D + i0 + 1, a);
+        v0 = take_acc(acc, r + 2 * D + i0, a); v1 = take_acc(acc, r + 2 * D + i0 + 1, a);
         const float c = rc[(size_t)pos * half + t], s = rs[(size_t)pos * half + t];
         float qr0 = __builtin_fmaf(q0, c, -(q1 * s));
         float qr1 = __builtin_fmaf(q0, s, q1 * c);
@@ -104,14 +106,13 @@ __global__ __launch_bounds__(64) void k_kv_store_row(KvGeom g, KvPlanes kv, uint
     store_pair(g, kv, plane_index(g, layer, head), row, t, act, k0, k1, v0, v1);
 }
 
-// Pooled rows [r_lo, r_lo + gridDim.y) of every plane in [plane_lo,
-// plane_lo + gridDim.x): the mean of pool_block consecutive window entries
-// accumulated in double in eviction order, scaled by (double)(1.0f/P), then
-// requantized (src/kv_cache.cpp:83-104).  head_dim threads (<= 128).
-__global__ __launch_bounds__(128) void k_pool_rows(KvGeom g, KvPlanes kv, uint32_t plane_lo, uint32_t r_lo) {
+// Pooled row r of one plane: the mean of pool_block consecutive window
+// entries accumulated in double in eviction order, scaled by
+// (double)(1.0f/P), then requantized (src/kv_cache.cpp:83-104).
+// 64 or 128 threads (head_dim <= 128).
+__device__ void pool_row(const KvGeom& g, KvPlanes kv, size_t plane, uint32_t r) {
     __shared__ float red[4];
-    const size_t plane = plane_lo + blockIdx.x;
-    const uint32_t r = r_lo + blockIdx.y, i = threadIdx.x, hd = g.head_dim, P = g.pool_block;
+    const uint32_t i = threadIdx.x, hd = g.head_dim, P = g.pool_block;
     const bool act = i < hd;
     const float inv = 1.0f / (float)P;
     const size_t prow = plane * g.rows;
@@ -127,12 +128,10 @@ __global__ __launch_bounds__(128) void k_pool_rows(KvGeom g, KvPlanes kv, uint32
             }
         }
         float avg = act ? (float)(acc * (double)inv) : 0.0f;
-        float amax = fabsf(avg);
-        // head_dim <= 128: at most two waves
-        float w = wave_max(amax);
+        float w = wave_max(fabsf(avg));
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = w;
         __syncthreads();
-        amax = (blockDim.x > 64) ? fmaxf(red[0], red[1]) : red[0];
+        const float amax = (blockDim.x > 64) ? fmaxf(red[0], red[1]) : red[0];
         __syncthreads();
         const float qi = (amax == 0.0f) ? 1.0f : 127.0f / amax;
         int8_t* d8 = which ? kv.v : kv.k;
@@ -140,6 +139,25 @@ __global__ __launch_bounds__(128) void k_pool_rows(KvGeom g, KvPlanes kv, uint32
         if (act) d8[(prow + dst) * hd + i] = quant_code(avg, qi);
         if (i == 0) ds[prow + dst] = (amax == 0.0f) ? 1.0f : amax / 127.0f;
     }
+}
+
+// One pooled row of plane `plane` (the KVCache API, which folds a block as
+// soon as its last entry is evicted).
+__global__ __launch_bounds__(128) void k_pool_row_one(KvGeom g, KvPlanes kv, uint32_t plane, uint32_t r) {
+    pool_row(g, kv, plane, r);
+}
+
+// Pooled rows a pass can see and earlier passes may not have folded: rows
+// [pool(p0 - 1), pool(p0 + M - 1)) of every plane, from the pass
+// descriptor.  Grid (planes, rows_max); refolding a row rewrites the same
+// values.
+__global__ __launch_bounds__(128) void k_pool_rows(KvGeom g, KvPlanes kv, const PassDesc* __restrict__ pd) {
+    const uint32_t p0 = pd->pos0, m = pd->m;
+    const uint32_t r_lo = kv_view(g, p0 > 0 ? p0 - 1 : 0).pool;
+    const uint32_t r_hi = kv_view(g, p0 + m - 1).pool;
+    const uint32_t r = r_lo + blockIdx.y;
+    if (r >= r_hi || r >= g.pool_cap) return;
+    pool_row(g, kv, blockIdx.x, r);
 }
 
 // ------------------------------------------------------------ attention
@@ -222,29 +240,48 @@ __global__ __launch_bounds__(256) void k_attn_softmax(const PassDesc* __restrict
 
 // Wp[((m*H + y)*cstride + c)*hd + i] = fmaf chain over the visible entries
 // [64c, min(64c+64, C, limit)) of p_j * ((float)v_j[i] * vs_j)
-// (src/kv_cache.cpp:173-197, contracted as the reference build does).
+// (src/kv_cache.cpp:173-197, contracted as the reference build does).  The
+// chunk's V rows, row scales and probabilities are staged in LDS first.
 // Grid (M, H, chunks), 128 threads (head_dim <= 128).
 __global__ __launch_bounds__(128) void k_attn_wsum(const PassDesc* __restrict__ pd, KvGeom g, KvPlanes kv,
                                                    uint32_t layer, int32_t view_sink, uint32_t view_nw,
                                                    int32_t head_override, uint32_t limit,
                                                    const float* __restrict__ S, uint32_t s_stride,
                                                    float* __restrict__ Wp, uint32_t cstride) {
+    __shared__ __align__(16) int8_t vt[64][128];
+    __shared__ float vsc[64], pp[64];
     const uint32_t m = blockIdx.x, y = blockIdx.y, c = blockIdx.z, i = threadIdx.x;
     const uint32_t h = head_override >= 0 ? (uint32_t)head_override : y;
     if (m >= pd->m) return;
     const uint32_t hd = g.head_dim;
     const KvView v = pass_view(g, pd, m, view_sink, view_nw);
     const uint32_t C = min(v.count(), limit);
-    if (c * 64u >= C || i >= hd) return;
+    if (c * 64u >= C) return;
     const size_t plane = plane_index(g, layer, h);
     const float* p = S + ((size_t)m * g.n_heads + y) * s_stride;
-    const uint32_t j1 = min(C, c * 64u + 64u);
-    float acc = 0.0f;
-    for (uint32_t j = c * 64u; j < j1; j++) {
-        uint32_t row = kv_row(g, v, j);
-        float vv = (float)kv.v[(plane * g.rows + row) * hd + i] * kv.vs[plane * g.rows + row];
-        acc = __builtin_fmaf(p[j], vv, acc);
+    const uint32_t j0 = c * 64u, n = min(64u, C - j0);
+    if ((hd & 15u) == 0) {
+        const uint32_t parts = hd >> 4;
+        for (uint32_t idx = i; idx < n * parts; idx += blockDim.x) {
+            const uint32_t e = idx / parts, q = idx % parts;
+            const uint32_t row = kv_row(g, v, j0 + e);
+            *reinterpret_cast<int4*>(&vt[e][q * 16]) =
+                *reinterpret_cast<const int4*>(kv.v + (plane * g.rows + row) * hd + q * 16);
+        }
+    } else {
+        for (uint32_t idx = i; idx < n * hd; idx += blockDim.x) {
+            const uint32_t e = idx / hd, q = idx % hd;
+            vt[e][q] = kv.v[(plane * g.rows + kv_row(g, v, j0 + e)) * hd + q];
+        }
     }
+    for (uint32_t e = i; e < n; e += blockDim.x) {
+        vsc[e] = kv.vs[plane * g.rows + kv_row(g, v, j0 + e)];
+        pp[e] = p[j0 + e];
+    }
+    __syncthreads();
+    if (i >= hd) return;
+    float acc = 0.0f;
+    for (uint32_t e = 0; e < n; e++) acc = __builtin_fmaf(pp[e], (float)vt[e][i] * vsc[e], acc);
     Wp[(((size_t)m * g.n_heads + y) * cstride + c) * hd + i] = acc;
 }
 
@@ -257,42 +294,25 @@ __global__ void k_wsum_combine_one(const float* __restrict__ Wp, uint32_t nch, u
     out[i] = o;
 }
 
-// Per row m: attention output element e = h*hd + i as chunk partials added
-// left to right, then fmaf(p_self, v_self, .).  Writes the fp32 output
-// (when out != null) and its quantize_activation_row codes for the O
-// projection.  Grid M, 256 threads, D <= 256 * PER.
-template <int PER>
-__global__ __launch_bounds__(256) void k_attn_combine(const PassDesc* __restrict__ pd, KvGeom g,
-                                                      int32_t view_sink, uint32_t view_nw,
-                                                      const float* __restrict__ S, uint32_t s_stride,
-                                                      const float* __restrict__ Wp, uint32_t cstride,
-                                                      const float* __restrict__ vself, float* __restrict__ out,
-                                                      int8_t* __restrict__ q, uint32_t q_stride,
-                                                      float* __restrict__ as, int32_t* __restrict__ bsum,
-                                                      uint32_t bsum_stride) {
-    __shared__ float red[4];
-    const uint32_t m = blockIdx.x;
+// Attention output of (row m, head h): chunk partials added left to right,
+// then fmaf(p_self, v_self, .) (src/engine.cpp:771-778, each head writing
+// its own slice).  Grid (M, H), 128 threads.
+__global__ __launch_bounds__(128) void k_attn_merge(const PassDesc* __restrict__ pd, KvGeom g,
+                                                    const float* __restrict__ S, uint32_t s_stride,
+                                                    const float* __restrict__ Wp, uint32_t cstride,
+                                                    const float* __restrict__ vself, float* __restrict__ out) {
+    const uint32_t m = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
     if (m >= pd->m) return;
     const uint32_t hd = g.head_dim, D = g.n_heads * hd;
-    const uint32_t C = pass_view(g, pd, m, view_sink, view_nw).count();
+    if (i >= hd) return;
+    const uint32_t C = kv_view(g, pd->pos0 + m).count();
     const uint32_t nch = (C + 63u) / 64u;
-    float x[PER];
-#pragma unroll
-    for (int k = 0; k < PER; k++) {
-        uint32_t e = threadIdx.x + 256u * k;
-        float o = 0.0f;
-        if (e < D) {
-            uint32_t h = e / hd, i = e % hd;
-            const float* wp = Wp + ((size_t)m * g.n_heads + h) * cstride * hd + i;
-            for (uint32_t c = 0; c < nch; c++) o = o + wp[(size_t)c * hd];
-            float ps = S[((size_t)m * g.n_heads + h) * s_stride + C];
-            o = __builtin_fmaf(ps, vself[(size_t)m * D + e], o);
-            if (out) out[(size_t)m * D + e] = o;
-        }
-        x[k] = o;
-    }
-    if (q) quantize_row_block<PER>(x, D, q + (size_t)m * q_stride, as + m,
-                                   bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
+    const float* wp = Wp + ((size_t)m * g.n_heads + h) * cstride * hd + i;
+    float o = 0.0f;
+    for (uint32_t c = 0; c < nch; c++) o = o + wp[(size_t)c * hd];
+    const float ps = S[((size_t)m * g.n_heads + h) * s_stride + C];
+    o = __builtin_fmaf(ps, vself[(size_t)m * D + h * hd + i], o);
+    out[(size_t)m * D + h * hd + i] = o;
 }
 
 }  // namespace pf

@@ -181,16 +181,6 @@ __device__ __forceinline__ uint32_t kv_row(const KvGeom& g, const KvView& v, uin
     return KV_SINK_ROWS + (v.win_lo + j) % g.ring;
 }
 
-// ------------------------------------------------- GEMV partial sums
-
-// y = (float)(sum_s part[s][m][n] * (double)a_scale[m]).
-__device__ __forceinline__ float gemv_out(const double* __restrict__ part, uint32_t splits,
-                                          uint32_t M, uint32_t N, uint32_t m, uint32_t n, float as) {
-    double S = 0.0;
-    for (uint32_t s = 0; s < splits; s++) S += part[((size_t)s * M + m) * N + n];
-    return (float)(S * (double)as);
-}
-
 // ------------------------------------------------------ quantized rows
 
 // Block sums of int8 codes over 32-element blocks for a 256-thread block
@@ -202,22 +192,24 @@ __device__ __forceinline__ int half_wave_isum(int v) {
     return v;
 }
 
-// Quantize rows (src/matmul_neon.cpp:16-29).  Grid M, 256 threads, K <=
-// 256 * PER.  Writes codes, scale and block sums (when bsum != null).
-template <int PER>
+// Quantize one row held by a block of NT threads (thread t has elements
+// t, t+NT, ...) with the arithmetic of src/matmul_neon.cpp:16-29.  Writes
+// the codes, the row scale and (when bsum != null) the sums of the codes
+// of each 32-element block: a block's elements sit in 32 consecutive lanes.
+template <int PER, int NT>
 __device__ __forceinline__ void quantize_row_block(const float (&x)[PER], uint32_t K, int8_t* q,
                                                    float* scale_out, int32_t* bsum, float* red) {
     float amax = 0.0f;
 #pragma unroll
     for (int k = 0; k < PER; k++) {
-        uint32_t i = threadIdx.x + 256u * k;
+        uint32_t i = threadIdx.x + (uint32_t)NT * k;
         if (i < K) amax = fmaxf(amax, fabsf(x[k]));
     }
-    amax = block_max<4>(amax, red);
+    amax = block_max<NT / 64>(amax, red);
     const float inv = (amax == 0.0f) ? 1.0f : 127.0f / amax;
 #pragma unroll
     for (int k = 0; k < PER; k++) {
-        uint32_t i = threadIdx.x + 256u * k;
+        uint32_t i = threadIdx.x + (uint32_t)NT * k;
         int code = 0;
         if (i < K) {
             int8_t c = quant_code(x[k], inv);

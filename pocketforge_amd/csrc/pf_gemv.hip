@@ -4,7 +4,8 @@
 //                  blocks, fp16 scale) tiled matrix, M <= 8 activation rows.
 //                  One lane per output row, wave-uniform activations in
 //                  SGPRs, v_dot4 int32 block dots, exact fp64 accumulation of
-//                  d_b * p_b.  HBM bound: every weight byte is read once.
+//                  d_b * p_b, fp32 output.  HBM bound: every weight byte is
+//                  read once.
 //  * k_gemv_f32    fp32 activations x dequantized Q4 row-major matrix (tied
 //                  unembedding, MTP heads) in the canonical 64-lane order.
 //  * row prologues quantize_activation_row, residual + RMSNorm + quantize,
@@ -36,43 +37,61 @@ __device__ __forceinline__ void unpack_codes(const uint8_t* tile, uint32_t t, ui
     }
 }
 
-// part[s][m][n] = sum over the blocks of split s of d_b * p_b (exact), where
-// p_b = sum_i a[m][32b+i] * code[n][32b+i].  Grid (N/64, splits), 256
-// threads; wave w of split s covers blocks [(4s+w)*bpw, (4s+w+1)*bpw).
+// acc[m][n] += S_split with S = sum_b d_b * p_b over the blocks of one
+// K split, p_b = sum_i a[m][32b+i] * code[n][32b+i] (int32).  Every term
+// d_b * p_b is an integer multiple of the smallest block-scale ulp of the
+// row and the row's scales span at most 15 binades (checked at upload), so
+// all partial sums are exact in fp64: the splits meet through fp64 atomic
+// adds in any order with a bit-identical result.  The consumer converts
+// (float)(acc * (double)a_scale) and clears acc.
+// Grid (N/64, splits), 256 threads; wave w of split s covers blocks
+// [(4s+w)*bpw, (4s+w+1)*bpw), lane = output row; loads are issued four
+// blocks at a time.
 template <int FMT, int M>
 __global__ __launch_bounds__(256) void k_gemv_i8(const uint8_t* __restrict__ W, uint32_t K,
                                                  const int8_t* __restrict__ act, uint32_t act_stride,
                                                  const int32_t* __restrict__ bsum, uint32_t bsum_stride,
-                                                 uint32_t bpw, uint32_t N, double* __restrict__ part) {
+                                                 uint32_t bpw, double* __restrict__ acc, uint32_t acc_stride) {
     constexpr uint32_t TB = tile_bytes(FMT);
     constexpr uint32_t CODES = TILE_ROWS * TILE_BLOCKS * code_bytes(FMT);
     constexpr int OFF = code_offset(FMT);
+    constexpr uint32_t U = 4;
     const uint32_t g = blockIdx.x, s = blockIdx.y;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t nb = K >> 5, chunks = K >> 8;
-    const uint32_t b0 = (s * 4u + wid) * bpw;
-    const uint32_t b1 = min(b0 + bpw, nb);
+    const uint32_t b_begin = (s * 4u + wid) * bpw;
+    const uint32_t b_end = min(b_begin + bpw, nb);
     const uint8_t* tiles = W + (size_t)g * chunks * TB;
 
     double S[M];
 #pragma unroll
     for (int m = 0; m < M; m++) S[m] = 0.0;
 
-    for (uint32_t b = b0; b < b1; b++) {
-        const uint32_t c = b >> 3, t = b & 7u;
-        const uint8_t* tile = tiles + (size_t)c * TB;
-        uint32_t u[8];
-        unpack_codes<FMT>(tile, t, lane, u);
-        const uint16_t sc = *reinterpret_cast<const uint16_t*>(tile + CODES + lane * 16u + t * 2u);
-        const double d = (double)h2f(sc);
+    for (uint32_t b0 = b_begin; b0 < b_end; b0 += U) {
+        uint32_t u[U][8];
+        double d[U];
 #pragma unroll
-        for (int m = 0; m < M; m++) {
-            const int32_t* a = reinterpret_cast<const int32_t*>(act + (size_t)m * act_stride + (size_t)b * 32u);
-            int acc = -OFF * bsum[(size_t)m * bsum_stride + b];
+        for (uint32_t k = 0; k < U; k++) {
+            const uint32_t b = b0 + k;
+            if (b < b_end) {
+                const uint8_t* tile = tiles + (size_t)(b >> 3) * TB;
+                unpack_codes<FMT>(tile, b & 7u, lane, u[k]);
+                d[k] = (double)h2f(*reinterpret_cast<const uint16_t*>(tile + CODES + lane * 16u + (b & 7u) * 2u));
+            }
+        }
 #pragma unroll
-            for (int k = 0; k < 8; k++) acc = __builtin_amdgcn_sdot4((int)u[k], a[k], acc, false);
-            S[m] = __builtin_fma(d, (double)acc, S[m]);
+        for (uint32_t k = 0; k < U; k++) {
+            const uint32_t b = b0 + k;
+            if (b >= b_end) break;
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                const int32_t* a = reinterpret_cast<const int32_t*>(act + (size_t)m * act_stride + (size_t)b * 32u);
+                int p = -OFF * bsum[(size_t)m * bsum_stride + b];
+#pragma unroll
+                for (int q = 0; q < 8; q++) p = __builtin_amdgcn_sdot4((int)u[k][q], a[q], p, false);
+                S[m] = __builtin_fma(d[k], (double)p, S[m]);
+            }
         }
     }
 
@@ -80,20 +99,32 @@ __global__ __launch_bounds__(256) void k_gemv_i8(const uint8_t* __restrict__ W, 
 #pragma unroll
     for (int m = 0; m < M; m++) red[wid][m][lane] = S[m];
     __syncthreads();
-    if (threadIdx.x < 64) {
-#pragma unroll
-        for (int m = 0; m < M; m++) {
-            double v = red[0][m][lane] + red[1][m][lane] + red[2][m][lane] + red[3][m][lane];
-            part[((size_t)s * M + m) * N + (size_t)g * 64u + lane] = v;
-        }
+    for (uint32_t t = threadIdx.x; t < (uint32_t)M * 64u; t += 256u) {
+        const uint32_t m = t >> 6, r = t & 63u;
+        const double v = red[0][m][r] + red[1][m][r] + red[2][m][r] + red[3][m][r];
+        atomicAdd(acc + (size_t)m * acc_stride + (size_t)g * 64u + r, v);
     }
 }
 
-__global__ void k_gemv_finish(const double* __restrict__ part, uint32_t splits, uint32_t M, uint32_t N,
-                              const float* __restrict__ as, float* __restrict__ y, uint32_t y_stride) {
-    uint32_t n = blockIdx.x * blockDim.x + threadIdx.x, m = blockIdx.y;
+// y = (float)(acc * (double)as[m]); acc cleared for its next use.
+__device__ __forceinline__ float take_acc(double* acc, size_t i, float as) {
+    const double v = acc[i];
+    acc[i] = 0.0;
+    return (float)(v * (double)as);
+}
+
+// Finishes a GEMV for the kernel-level entry point.
+__global__ void k_gemv_finish(double* __restrict__ acc, uint32_t N, const float* __restrict__ as,
+                              float* __restrict__ y) {
+    const uint32_t n = blockIdx.x * blockDim.x + threadIdx.x, m = blockIdx.y;
     if (n >= N) return;
-    y[(size_t)m * y_stride + n] = gemv_out(part, splits, M, N, m, n, as[m]);
+    y[(size_t)m * N + n] = take_acc(acc, (size_t)m * N + n, as[m]);
+}
+
+// acc[0..n) = 0 (one-time set-up of accumulators; a kernel, not a memset).
+__global__ void k_zero_f64(double* __restrict__ p, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0.0;
 }
 
 // ============================================ fp32 x dequantized Q4 GEMV
@@ -171,17 +202,18 @@ __global__ __launch_bounds__(256) void k_quant_rows(const float* __restrict__ x,
         uint32_t i = threadIdx.x + 256u * k;
         v[k] = i < K ? x[(size_t)m * x_stride + i] : 0.0f;
     }
-    quantize_row_block<PER>(v, K, q + (size_t)m * q_stride, as + m,
-                            bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
+    quantize_row_block<PER, 256>(v, K, q + (size_t)m * q_stride, as + m,
+                                 bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
 }
 
-// x[m] += (float)(GEMV partial sum * as_prev[m])   (when part != null),
+// x[m] += (float)(acc[m] * as_prev[m]) (when acc != null; acc cleared),
 // then RMSNorm (src/matmul_neon.cpp:231-239, CANON(4) sum of squares) with
-// weight w, then quantize_activation_row of the normed row.
+// weight w, then quantize_activation_row of the normed row.  Grid M, 256
+// threads.
 template <int PER>
 __global__ __launch_bounds__(256) void k_resid_norm_quant(float* __restrict__ x, uint32_t K,
-                                                          const double* __restrict__ part, uint32_t splits,
-                                                          uint32_t M, const float* __restrict__ as_prev,
+                                                          double* __restrict__ acc,
+                                                          const float* __restrict__ as_prev,
                                                           const float* __restrict__ w,
                                                           int8_t* __restrict__ q, uint32_t q_stride,
                                                           float* __restrict__ as, int32_t* __restrict__ bsum,
@@ -196,8 +228,8 @@ __global__ __launch_bounds__(256) void k_resid_norm_quant(float* __restrict__ x,
         float xi = 0.0f;
         if (i < K) {
             xi = x[(size_t)m * K + i];
-            if (part) {
-                xi = xi + gemv_out(part, splits, M, K, m, i, as_prev[m]);
+            if (acc) {
+                xi = xi + take_acc(acc, (size_t)m * K + i, as_prev[m]);
                 x[(size_t)m * K + i] = xi;
             }
             ss = __builtin_fmaf(xi, xi, ss);
@@ -212,45 +244,50 @@ __global__ __launch_bounds__(256) void k_resid_norm_quant(float* __restrict__ x,
         uint32_t i = threadIdx.x + 256u * k;
         if (i < K) v[k] = v[k] * inv * w[i];
     }
-    quantize_row_block<PER>(v, K, q + (size_t)m * q_stride, as + m,
-                            bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
+    quantize_row_block<PER, 256>(v, K, q + (size_t)m * q_stride, as + m,
+                                 bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
 }
 
-// x[m] += (float)(GEMV partial sum * as_prev[m]) only (the last layer's
-// down projection residual).
-__global__ void k_resid_add(float* __restrict__ x, uint32_t K, const double* __restrict__ part,
-                            uint32_t splits, uint32_t M, const float* __restrict__ as_prev) {
+// x[m] += (float)(acc[m] * as_prev[m]) (the last layer's down residual).
+__global__ void k_resid_add(float* __restrict__ x, uint32_t K, double* __restrict__ acc,
+                            const float* __restrict__ as_prev) {
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, m = blockIdx.y;
     if (i >= K) return;
-    x[(size_t)m * K + i] = x[(size_t)m * K + i] + gemv_out(part, splits, M, K, m, i, as_prev[m]);
+    x[(size_t)m * K + i] = x[(size_t)m * K + i] + take_acc(acc, (size_t)m * K + i, as_prev[m]);
 }
 
-// SwiGLU of src/engine.cpp:832-838 on the fused gate|up GEMV (rows [0,ff) =
-// gate, [ff, 2ff) = up), then quantize_activation_row of the result.
+// SwiGLU of src/engine.cpp:832-838 on the fused gate|up GEMV accumulators
+// (row m: [0,ff) = gate, [ff, 2ff) = up; cleared), then
+// quantize_activation_row of the result.  Grid M, 1024 threads.
 template <int PER>
-__global__ __launch_bounds__(256) void k_swiglu_quant(const double* __restrict__ part, uint32_t splits,
-                                                      uint32_t M, uint32_t ff, const float* __restrict__ as_in,
-                                                      int8_t* __restrict__ q, uint32_t q_stride,
-                                                      float* __restrict__ as, int32_t* __restrict__ bsum,
-                                                      uint32_t bsum_stride) {
-    __shared__ float red[4];
+__global__ __launch_bounds__(1024) void k_swiglu_quant(double* __restrict__ acc, const float* __restrict__ as_in,
+                                                       uint32_t ff,
+                                                       int8_t* __restrict__ q, uint32_t q_stride,
+                                                       float* __restrict__ as, int32_t* __restrict__ bsum,
+                                                       uint32_t bsum_stride) {
+    __shared__ float red[16];
     const uint32_t m = blockIdx.x;
-    const float a = as_in[m];
     float v[PER];
 #pragma unroll
     for (int k = 0; k < PER; k++) {
-        uint32_t i = threadIdx.x + 256u * k;
+        uint32_t i = threadIdx.x + 1024u * k;
         float f = 0.0f;
         if (i < ff) {
-            float g = gemv_out(part, splits, M, 2 * ff, m, i, a);
-            float u = gemv_out(part, splits, M, 2 * ff, m, ff + i, a);
-            float sig = 1.0f / (1.0f + expf_c(-g));
-            f = g * sig * u;
+            float gt = take_acc(acc, (size_t)m * 2 * ff + i, as_in[m]);
+            float u = take_acc(acc, (size_t)m * 2 * ff + ff + i, as_in[m]);
+            float sig = 1.0f / (1.0f + expf_c(-gt));
+            f = gt * sig * u;
         }
         v[k] = f;
     }
-    quantize_row_block<PER>(v, ff, q + (size_t)m * q_stride, as + m,
-                            bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
+    quantize_row_block<PER, 1024>(v, ff, q + (size_t)m * q_stride, as + m,
+                                  bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
+}
+
+// dst = src (float), used instead of a copy node inside captured passes.
+__global__ void k_copy_f32(const float* __restrict__ src, float* __restrict__ dst, uint32_t n) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = src[i];
 }
 
 // MTP activation: a = silu(g) * u with silu(x) = x / (1 + exp(-x))

@@ -4,10 +4,13 @@
 #include "pf_attn.hip"
 #include "pf_ctl.hip"
 
+#include <hip/hip_ext.h>
+
 #include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -167,7 +170,7 @@ struct pf_matrix {
     uint8_t* data = nullptr;    // tiled: all tiles; row-major: codes
     uint16_t* scales = nullptr; // row-major only
     size_t bytes = 0;
-    uint32_t bpw = 2, splits = 1;
+    uint32_t bpw = 2, splits = 1;   // blocks per wave, K splits (grid y)
 };
 
 static uint32_t interchange_code(int fmt, const uint8_t* blk, uint32_t e) {
@@ -233,12 +236,14 @@ static void repack_tiles(int fmt, uint32_t cols, const uint8_t* codes, const uin
         }
 }
 
+// K split of a tiled matrix: the largest blocks-per-wave (2..16) that still
+// gives at least 2048 waves, so every launch covers the 256 CUs.
 static void choose_split(pf_matrix* M) {
     const uint32_t nb = M->cols / 32, G = M->rows / 64;
     uint32_t best = 2;
     for (uint32_t bpw : {2u, 4u, 8u, 16u}) {
         uint32_t splits = (nb + 4 * bpw - 1) / (4 * bpw);
-        if ((uint64_t)G * splits * 4 >= 1024) best = bpw;
+        if ((uint64_t)G * splits * 4 >= 2048) best = bpw;
     }
     M->bpw = best;
     M->splits = (nb + 4 * best - 1) / (4 * best);
@@ -311,10 +316,14 @@ extern "C" void pf_matrix_free(pf_matrix* M) {
 
 // ------------------------------------------------------- kernel launches
 
-#define PF_GEMV_CASE(F, MM)                                                                              \
-    case MM:                                                                                             \
-        hipLaunchKernelGGL((k_gemv_i8<F, MM>), grid, dim3(256), 0, st, W->data, W->cols, act, act_stride,  \
-                           bsum, bsum_stride, W->bpw, W->rows, part);                                    \
+#define PF_GEMV_CASE(F, MM)                                                                                   \
+    case MM:                                                                                                  \
+        if (ev0)                                                                                              \
+            hipExtLaunchKernelGGL((k_gemv_i8<F, MM>), dim3(W->rows / 64, W->splits), dim3(256), 0, st, ev0, ev1, 0, \
+                                  W->data, W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc, acc_stride); \
+        else                                                                                                  \
+            hipLaunchKernelGGL((k_gemv_i8<F, MM>), dim3(W->rows / 64, W->splits), dim3(256), 0, st, W->data,     \
+                               W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc, acc_stride);          \
         break;
 
 #define PF_GEMV_FMT(F)                                 \
@@ -325,9 +334,11 @@ extern "C" void pf_matrix_free(pf_matrix* M) {
         PF_GEMV_CASE(F, 7) PF_GEMV_CASE(F, 8)          \
     }
 
+// acc[M][rows] += int8 activations x tiled block matrix (exact fp64).  With
+// ev0/ev1 the dispatch carries its own start/stop events.
 static void launch_gemv(hipStream_t st, const pf_matrix* W, uint32_t M, const int8_t* act, uint32_t act_stride,
-                        const int32_t* bsum, uint32_t bsum_stride, double* part) {
-    dim3 grid(W->rows / 64, W->splits);
+                        const int32_t* bsum, uint32_t bsum_stride, double* acc, uint32_t acc_stride,
+                        hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr) {
     switch (W->fmt) {
         case FMT_Q4: PF_GEMV_FMT(FMT_Q4) break;
         case FMT_Q2: PF_GEMV_FMT(FMT_Q2) break;
@@ -368,7 +379,12 @@ static int per_for(uint32_t K) {
         case 32: { constexpr int PER = 32; CALL; } break; \
     }
 
-static size_t gemv_part_elems(const pf_matrix* W, uint32_t M) { return (size_t)W->splits * M * W->rows; }
+#define PF_PER1024_SWITCH(K, CALL)                     \
+    switch (((K) + 1023) / 1024 <= 2 ? 2 : (((K) + 1023) / 1024 <= 4 ? 4 : 8)) { \
+        case 2: { constexpr int PER = 2; CALL; } break;   \
+        case 4: { constexpr int PER = 4; CALL; } break;   \
+        case 8: { constexpr int PER = 8; CALL; } break;   \
+    }
 
 extern "C" pf_status pf_quantize_activation_rows(pf_ctx* c, const float* src, int8_t* dst, float* scales,
                                                  uint32_t M, uint32_t K) {
@@ -417,24 +433,24 @@ extern "C" pf_status pf_matmul_quantized(pf_ctx* c, const float* A, const int8_t
 extern "C" pf_status pf_gemv_q(pf_ctx* c, const pf_matrix* W, const float* x, float* y, uint32_t M) {
     if (!c || !W || !x || !y || M == 0 || M > 8) return PF_ERR_ARG;
     if (W->rowmajor) return fail(c, PF_ERR_ARG, "pf_gemv_q needs a tiled matrix");
-    const uint32_t K = W->cols;
+    const uint32_t K = W->cols, N = W->rows;
     if (!per_for(K)) return fail(c, PF_ERR_UNSUPPORTED, "K > 8192");
     size_t a_bytes = ((size_t)M * K + 255) & ~(size_t)255;
     size_t s_bytes = 256;
     size_t b_bytes = (((size_t)M * (K / 32) * 4) + 255) & ~(size_t)255;
-    size_t p_bytes = gemv_part_elems(W, M) * 8;
+    size_t c_bytes = (size_t)M * N * 8;
     void* s = nullptr;
-    pf_status st = scratch(c, a_bytes + s_bytes + b_bytes + p_bytes, &s);
+    pf_status st = scratch(c, a_bytes + s_bytes + b_bytes + c_bytes, &s);
     if (st) return st;
     int8_t* act = (int8_t*)s;
     float* as = (float*)((char*)s + a_bytes);
     int32_t* bsum = (int32_t*)((char*)as + s_bytes);
-    double* part = (double*)((char*)bsum + b_bytes);
+    double* acc = (double*)((char*)bsum + b_bytes);
+    hipLaunchKernelGGL(k_zero_f64, dim3((M * N + 255) / 256), dim3(256), 0, c->stream, acc, (size_t)M * N);
     PF_PER_SWITCH(K, hipLaunchKernelGGL(k_quant_rows<PER>, dim3(M), dim3(256), 0, c->stream, x, K, K, act, K, as,
                                         bsum, K / 32));
-    launch_gemv(c->stream, W, M, act, K, bsum, K / 32, part);
-    hipLaunchKernelGGL(k_gemv_finish, dim3((W->rows + 255) / 256, M), dim3(256), 0, c->stream, part, W->splits, M,
-                       W->rows, as, y, W->rows);
+    launch_gemv(c->stream, W, M, act, K, bsum, K / 32, acc, N);
+    hipLaunchKernelGGL(k_gemv_finish, dim3((N + 255) / 256, M), dim3(256), 0, c->stream, acc, N, as, y);
     PF_LAUNCHED(c);
     return PF_OK;
 }
@@ -559,8 +575,8 @@ extern "C" pf_status pf_kv_store(pf_kv* kv, uint32_t layer, uint32_t head, uint3
             if ((ev + 1) % g.pool_block == 0) {
                 const uint32_t r = ev / g.pool_block;
                 if (r >= g.pool_cap) return fail(c, PF_ERR_CAPACITY, "pooled rows exceed capacity");
-                hipLaunchKernelGGL(k_pool_rows, dim3(1, 1), dim3(g.head_dim <= 64 ? 64 : 128), 0, c->stream, g, kv->p,
-                                   (uint32_t)pl, r);
+                hipLaunchKernelGGL(k_pool_row_one, dim3(1), dim3(g.head_dim <= 64 ? 64 : 128), 0, c->stream, g,
+                                   kv->p, (uint32_t)pl, r);
             }
         }
         row = KV_SINK_ROWS + w % g.ring;
@@ -775,7 +791,8 @@ struct pf_engine {
     int8_t* act = nullptr;
     float* as = nullptr;        // [4][8]
     int32_t* bsum = nullptr;
-    double* part = nullptr;
+    double* acc = nullptr;      // GEMV accumulators [8][max(3D, 2F)], zero between uses
+    float* attn = nullptr;      // attention output [8][D]
     float *q = nullptr, *k = nullptr, *v = nullptr;
     float* S = nullptr;
     float* Wp = nullptr;
@@ -790,18 +807,34 @@ struct pf_engine {
     std::vector<std::pair<void*, size_t>> owned;
     // host mirrors
     uint32_t pos = 0;
-    uint32_t pool_mat = 0;
+    uint32_t pool_rows_max = 1;
     bool hidden_valid = false;
     size_t max_memory = 0;
     // timing
     std::vector<TimedPass> timed;
     size_t timed_used = 0;
+    // captured decode rounds: [reuse][mtp] -> graph exec, for one sampling
+    // configuration / seed / profiling mode
+    hipGraphExec_t round_exec[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
+    uint32_t round_ev[2][2][4] = {};   // pass-event and GEMV-event slot ranges of each variant
+    hipEvent_t rev0 = nullptr, rev1 = nullptr;
+    double round_us = 0;
+    uint32_t round_n = 0;
+    hipGraphExec_t prefill_exec = nullptr;
+    SamplingCfg graph_cfg{};
+    uint64_t graph_seed = 0;
+    bool graph_profile = false;
+    bool graphs_valid = false;
+    bool capturing = false;
+    bool use_graphs = true;
     // per-launch timing of the int8 GEMVs of verify passes (profiling mode)
     bool profile = false;
     bool in_verify = false;
     std::vector<TimedPass> kev;
     std::vector<double> kev_bytes;
     size_t kev_used = 0;
+    double kev_us = 0, kev_bytes_sum = 0;
+    uint32_t kev_n = 0;
     double verify_us = 0, base_us = 0;
     uint32_t verify_n = 0, base_n = 0;
 };
@@ -854,10 +887,7 @@ extern "C" pf_status pf_engine_create(pf_model* m, const pf_cache_desc* cd, pf_e
         PF_HIP(c, hipMemcpy(e->rope_s, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
     }
     e->kmax = std::max(D, F);
-    size_t part_elems = 0;
-    for (uint32_t l = 0; l < d.n_layers; l++)
-        for (pf_matrix* W : {m->qkv[l], m->o[l], m->gu[l], m->down[l]})
-            part_elems = std::max(part_elems, gemv_part_elems(W, MR));
+    e->pool_rows_max = (MR + e->g.pool_block - 1) / e->g.pool_block + 1;
     const uint32_t cmax = KV_SINK_ROWS + e->g.pool_cap + e->g.window;
     e->s_stride = cmax + 8;
     e->cstride = (cmax + 63) / 64 + 1;
@@ -865,7 +895,9 @@ extern "C" pf_status pf_engine_create(pf_model* m, const pf_cache_desc* cd, pf_e
     if (!s) s = ealloc(e, &e->act, (size_t)MR * e->kmax);
     if (!s) s = ealloc(e, &e->as, 4 * MR);
     if (!s) s = ealloc(e, &e->bsum, (size_t)MR * (e->kmax / 32));
-    if (!s) s = ealloc(e, &e->part, std::max<size_t>(part_elems, 1));
+    const size_t acc_n = (size_t)MR * std::max(3 * D, 2 * F);
+    if (!s) s = ealloc(e, &e->acc, acc_n);
+    if (!s) s = ealloc(e, &e->attn, (size_t)MR * D);
     if (!s) s = ealloc(e, &e->q, (size_t)MR * D);
     if (!s) s = ealloc(e, &e->k, (size_t)MR * D);
     if (!s) s = ealloc(e, &e->v, (size_t)MR * D);
@@ -889,6 +921,12 @@ extern "C" pf_status pf_engine_create(pf_model* m, const pf_cache_desc* cd, pf_e
         pf_engine_destroy(e);
         return fail(c, PF_ERR_HIP, "hipHostMalloc failed");
     }
+    hipLaunchKernelGGL(k_zero_f64, dim3((acc_n + 255) / 256), dim3(256), 0, c->stream, e->acc, acc_n);
+    PF_LAUNCHED(c);
+    PF_HIP(c, hipStreamSynchronize(c->stream));
+    if (const char* ng = std::getenv("PF_NO_GRAPHS")) e->use_graphs = !(ng[0] == '1');
+    PF_HIP(c, hipEventCreate(&e->rev0));
+    PF_HIP(c, hipEventCreate(&e->rev1));
     PassDesc pb{};
     pb.m = d.n_mtp + 1;
     PF_HIP(c, hipMemcpy(e->pdB, &pb, sizeof(pb), hipMemcpyHostToDevice));
@@ -903,6 +941,12 @@ extern "C" void pf_engine_destroy(pf_engine* e) {
     (void)hipStreamSynchronize(e->c->stream);
     for (auto& t : e->timed) { (void)hipEventDestroy(t.a); (void)hipEventDestroy(t.b); }
     for (auto& t : e->kev) { (void)hipEventDestroy(t.a); (void)hipEventDestroy(t.b); }
+    for (auto& row : e->round_exec)
+        for (auto& g : row)
+            if (g) (void)hipGraphExecDestroy(g);
+    if (e->prefill_exec) (void)hipGraphExecDestroy(e->prefill_exec);
+    if (e->rev0) (void)hipEventDestroy(e->rev0);
+    if (e->rev1) (void)hipEventDestroy(e->rev1);
     for (auto& p : e->owned) dfree(e->c, p.first, p.second);
     if (e->tokens) dfree(e->c, e->tokens, (size_t)e->tok_cap * 4);
     kv_free(e->c, e->g, &e->kv);
@@ -913,7 +957,6 @@ extern "C" void pf_engine_destroy(pf_engine* e) {
 extern "C" pf_status pf_engine_reset(pf_engine* e) {
     if (!e) return PF_ERR_ARG;
     e->pos = 0;
-    e->pool_mat = 0;
     e->hidden_valid = false;
     return PF_OK;
 }
@@ -928,6 +971,7 @@ extern "C" pf_status pf_engine_set_max_memory(pf_engine* e, size_t bytes) {
 
 static pf_status timed_begin(pf_engine* e, bool verify, TimedPass** tp) {
     *tp = nullptr;
+    if (e->capturing) return PF_OK;   // events inside captured graphs cannot be timed
     if (e->timed_used == e->timed.size()) {
         TimedPass t{};
         PF_HIP(e->c, hipEventCreate(&t.a));
@@ -941,13 +985,32 @@ static pf_status timed_begin(pf_engine* e, bool verify, TimedPass** tp) {
     return PF_OK;
 }
 
-// Int8 GEMV launch of a pass; in profiling mode the launches of verify
-// passes are bracketed by HIP events on the engine's stream.
+// Accumulates the pass event pairs [t_lo, t_hi) and GEMV event pairs
+// [k_lo, k_hi) (a replayed graph's events hold that replay's times).
+static pf_status harvest_events(pf_engine* e, size_t t_lo, size_t t_hi, size_t k_lo, size_t k_hi) {
+    for (size_t i = t_lo; i < t_hi; i++) {
+        float ms = 0;
+        PF_HIP(e->c, hipEventElapsedTime(&ms, e->timed[i].a, e->timed[i].b));
+        if (e->timed[i].verify) { e->verify_us += ms * 1000.0; e->verify_n++; }
+        else { e->base_us += ms * 1000.0; e->base_n++; }
+    }
+    for (size_t i = k_lo; i < k_hi; i++) {
+        float ms = 0;
+        PF_HIP(e->c, hipEventElapsedTime(&ms, e->kev[i].a, e->kev[i].b));
+        e->kev_us += ms * 1000.0;
+        e->kev_bytes_sum += e->kev_bytes[i];
+        e->kev_n++;
+    }
+    return PF_OK;
+}
+
+// Int8 GEMV launch of a pass; in profiling mode the dispatches of verify
+// passes carry HIP start/stop events (kernel execution time, as rocprofv3
+// reports it).
 static pf_status pass_gemv(pf_engine* e, const pf_matrix* W, uint32_t M) {
     hipStream_t st = e->c->stream;
     const uint32_t ks = e->kmax, bs = e->kmax / 32;
-    TimedPass* t = nullptr;
-    if (e->profile && e->in_verify) {
+    if (e->profile && e->in_verify && !e->capturing) {
         if (e->kev_used == e->kev.size()) {
             TimedPass n{};
             PF_HIP(e->c, hipEventCreate(&n.a));
@@ -956,11 +1019,11 @@ static pf_status pass_gemv(pf_engine* e, const pf_matrix* W, uint32_t M) {
             e->kev_bytes.push_back(0.0);
         }
         e->kev_bytes[e->kev_used] = (double)W->bytes + (double)M * W->cols + (double)M * W->rows * 4.0;
-        t = &e->kev[e->kev_used++];
-        PF_HIP(e->c, hipEventRecord(t->a, st));
+        TimedPass* t = &e->kev[e->kev_used++];
+        launch_gemv(st, W, M, e->act, ks, e->bsum, bs, e->acc, W->rows, t->a, t->b);
+    } else {
+        launch_gemv(st, W, M, e->act, ks, e->bsum, bs, e->acc, W->rows);
     }
-    launch_gemv(st, W, M, e->act, ks, e->bsum, bs, e->part);
-    if (t) PF_HIP(e->c, hipEventRecord(t->b, st));
     return PF_OK;
 }
 
@@ -974,63 +1037,56 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
     const KvGeom& g = e->g;
     hipStream_t st = c->stream;
     const uint32_t D = d.n_embd, F = d.n_ff, H = d.n_heads, hd = d.head_dim;
-    if (pos0 + M > e->rope_pos) return fail(c, PF_ERR_CAPACITY, "position beyond the engine's max_context");
-    // pooled rows any row of this pass can see
-    const KvView vlast = kv_view(g, pos0 + M - 1);
-    if (vlast.pool > e->pool_mat) {
-        if (vlast.pool > g.pool_cap) return fail(c, PF_ERR_CAPACITY, "pooled rows exceed capacity");
-        hipLaunchKernelGGL(k_pool_rows, dim3(g.n_layers * g.n_heads, vlast.pool - e->pool_mat),
-                           dim3(hd <= 64 ? 64 : 128), 0, st, g, e->kv, 0u, e->pool_mat);
-        e->pool_mat = vlast.pool;
-    }
-    const uint32_t cmax = vlast.count();
+    if (!e->capturing && pos0 + M > e->rope_pos)
+        return fail(c, PF_ERR_CAPACITY, "position beyond the engine's max_context");
+    // captured passes replay at any position: grids sized for the largest view
+    const uint32_t cmax = e->capturing ? e->s_stride - 8 : kv_view(g, pos0 + M - 1).count();
     const uint32_t zb = (cmax + 1 + 255) / 256, nch = (cmax + 63) / 64;
     const uint32_t ks = e->kmax, bs = e->kmax / 32;
     float* as0 = e->as;           // attention-norm act
     float* as1 = e->as + 8;       // attention output act
     float* as2 = e->as + 16;      // ffn-norm act
     float* as3 = e->as + 24;      // swiglu act
+    const dim3 tb(hd <= 64 ? 64 : 128);
 
+    // pooled rows the pass can see (folded from window entries still in the ring)
+    hipLaunchKernelGGL(k_pool_rows, dim3(g.n_layers * g.n_heads, e->pool_rows_max), tb, 0, st, g, e->kv, pd);
     hipLaunchKernelGGL(k_embed, dim3((D + 255) / 256, M), dim3(256), 0, st, m->emb->data, m->emb->scales, d.n_vocab, D,
                        pd, e->x);
     for (uint32_t l = 0; l < d.n_layers; l++) {
         const float* an = m->attn_norm + (size_t)l * D;
         const float* fn = m->ffn_norm + (size_t)l * D;
-        if (l == 0) {
-            PF_PER_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(M), dim3(256), 0, st, e->x, D,
-                                                (const double*)nullptr, 0u, M, (const float*)nullptr, an, e->act, ks,
-                                                as0, e->bsum, bs));
-        } else {
-            PF_PER_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(M), dim3(256), 0, st, e->x, D, e->part,
-                                                m->down[l - 1]->splits, M, as3, an, e->act, ks, as0, e->bsum, bs));
-        }
+        PF_PER_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(M), dim3(256), 0, st, e->x, D,
+                                            l == 0 ? (double*)nullptr : e->acc, as3, an, e->act, ks, as0, e->bsum, bs));
         if (pf_status s = pass_gemv(e, m->qkv[l], M)) return s;
-        hipLaunchKernelGGL(k_qkv_post, dim3(M, H), dim3(64), 0, st, e->part, m->qkv[l]->splits, M, as0, pd, e->rope_c,
-                           e->rope_s, g, e->kv, l, e->q, e->k, e->v);
+        hipLaunchKernelGGL(k_qkv_post, dim3(M, H), dim3(64), 0, st, e->acc, as0, pd, e->rope_c, e->rope_s, g, e->kv, l,
+                           e->q, e->k, e->v);
         hipLaunchKernelGGL(k_attn_scores, dim3(M, H, zb), dim3(256), 0, st, pd, g, e->kv, l, -1, 0u, -1, e->q, e->k,
                            e->S, e->s_stride, 1);
         hipLaunchKernelGGL(k_attn_softmax, dim3(M, H), dim3(256), 0, st, pd, g, -1, 0u, e->S, e->s_stride);
         if (nch)
             hipLaunchKernelGGL(k_attn_wsum, dim3(M, H, nch), dim3(128), 0, st, pd, g, e->kv, l, -1, 0u, -1,
                                0xFFFFFFFFu, e->S, e->s_stride, e->Wp, e->cstride);
-        PF_PER_SWITCH(D, hipLaunchKernelGGL(k_attn_combine<PER>, dim3(M), dim3(256), 0, st, pd, g, -1, 0u, e->S,
-                                            e->s_stride, e->Wp, e->cstride, e->v, (float*)nullptr, e->act, ks, as1,
-                                            e->bsum, bs));
+        hipLaunchKernelGGL(k_attn_merge, dim3(M, H), dim3(128), 0, st, pd, g, e->S, e->s_stride, e->Wp, e->cstride,
+                           e->v, e->attn);
+        PF_PER_SWITCH(D, hipLaunchKernelGGL(k_quant_rows<PER>, dim3(M), dim3(256), 0, st, e->attn, D, D, e->act, ks,
+                                            as1, e->bsum, bs));
         if (pf_status s = pass_gemv(e, m->o[l], M)) return s;
-        PF_PER_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(M), dim3(256), 0, st, e->x, D, e->part,
-                                            m->o[l]->splits, M, as1, fn, e->act, ks, as2, e->bsum, bs));
+        PF_PER_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(M), dim3(256), 0, st, e->x, D, e->acc, as1,
+                                            fn, e->act, ks, as2, e->bsum, bs));
         if (pf_status s = pass_gemv(e, m->gu[l], M)) return s;
-        PF_PER_SWITCH(F, hipLaunchKernelGGL(k_swiglu_quant<PER>, dim3(M), dim3(256), 0, st, e->part, m->gu[l]->splits,
-                                            M, F, as2, e->act, ks, as3, e->bsum, bs));
+        PF_PER1024_SWITCH(F, hipLaunchKernelGGL(k_swiglu_quant<PER>, dim3(M), dim3(1024), 0, st, e->acc,
+                                                (const float*)as2, F, e->act, ks, as3, e->bsum, bs));
         if (pf_status s = pass_gemv(e, m->down[l], M)) return s;
     }
     if (d.n_layers)
-        hipLaunchKernelGGL(k_resid_add, dim3((D + 255) / 256, M), dim3(256), 0, st, e->x, D, e->part,
-                           m->down[d.n_layers - 1]->splits, M, as3);
-    if (hidden) PF_HIP(c, hipMemcpyAsync(hidden, e->x, (size_t)M * D * 4, hipMemcpyDeviceToDevice, st));
+        hipLaunchKernelGGL(k_resid_add, dim3((D + 255) / 256, M), dim3(256), 0, st, e->x, D, e->acc,
+                           (const float*)as3);
+    if (hidden)
+        hipLaunchKernelGGL(k_copy_f32, dim3((M * D + 255) / 256), dim3(256), 0, st, (const float*)e->x, hidden, M * D);
     if (logits) launch_gemv_f32(st, m->emb, M, e->x, D, logits, d.n_vocab, nullptr);
     PF_LAUNCHED(c);
-    e->hidden_valid = true;
+    if (!e->capturing) e->hidden_valid = true;   // capture must not change host state
     return PF_OK;
 }
 
@@ -1065,7 +1121,7 @@ static pf_status mtp_chain(pf_engine* e, const float* h0, bool sample, const Sam
     const pf_model_desc& d = m->d;
     hipStream_t st = c->stream;
     const uint32_t D = d.n_embd, V = d.n_vocab;
-    PF_HIP(c, hipMemcpyAsync(e->mcur, h0, D * 4, hipMemcpyDeviceToDevice, st));
+    hipLaunchKernelGGL(k_copy_f32, dim3((D + 255) / 256), dim3(256), 0, st, h0, e->mcur, D);
     for (uint32_t k = 0; k < d.n_mtp; k++) {
         launch_gemv_f32(st, m->mtp[k * 3 + 0], 1, e->mcur, D, e->mg, D, nullptr);
         launch_gemv_f32(st, m->mtp[k * 3 + 1], 1, e->mcur, D, e->mu, D, nullptr);
@@ -1119,6 +1175,91 @@ extern "C" pf_status pf_sample(pf_engine* e, const float* logits, const pf_sampl
     return PF_OK;
 }
 
+// One decode round, all on the engine's stream (capturable): the base pass
+// (or reuse of the last verify row), then either the MTP round
+// (src/engine.cpp:308-365: T1, drafts, verify pass, acceptance,
+// corrective) or the single-token step (src/engine.cpp:377-386).
+static pf_status round_body(pf_engine* e, bool reuse, bool mtp, const SamplingCfg& cfg, uint64_t seed) {
+    pf_ctx* c = e->c;
+    hipStream_t st = c->stream;
+    const pf_model_desc& d = e->m->d;
+    const uint32_t V = d.n_vocab, D = d.n_embd, NM = d.n_mtp;
+    pf_status s;
+    TimedPass* tp = nullptr;
+    const float* base_logits;
+    const float* base_hidden;
+    if (reuse) {
+        hipLaunchKernelGGL(k_ctl_reuse_row, dim3(1), dim3(1), 0, st, e->st);
+        base_logits = e->logitsB + (size_t)NM * V;
+        base_hidden = e->hiddenB + (size_t)NM * D;
+    } else {
+        hipLaunchKernelGGL(k_ctl_pass_a, dim3(1), dim3(1), 0, st, e->st, e->pdA);
+        if ((s = timed_begin(e, false, &tp))) return s;
+        if ((s = run_pass(e, e->pdA, 1, e->pos, e->logitsA, e->hiddenA))) return s;
+        if (tp) PF_HIP(c, hipEventRecord(tp->b, st));
+        base_logits = e->logitsA;
+        base_hidden = e->hiddenA;
+    }
+    if (mtp) {
+        hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, base_logits, V, 0, V, cfg, seed, e->st, e->tokens,
+                           e->tok_cap, e->pdB, (int32_t)ROLE_T1, 0, (int32_t*)nullptr);
+        if ((s = mtp_chain(e, base_hidden, true, &cfg, seed))) return s;
+        if ((s = timed_begin(e, true, &tp))) return s;
+        e->in_verify = true;
+        s = run_pass(e, e->pdB, NM + 1, e->pos + 1, e->logitsB, e->hiddenB);
+        e->in_verify = false;
+        if (s) return s;
+        if (tp) PF_HIP(c, hipEventRecord(tp->b, st));
+        hipLaunchKernelGGL(k_argmax_rows, dim3(NM + 1), dim3(1024), 0, st, e->logitsB, V, V, e->pdB,
+                           e->st->row_argmax);
+        hipLaunchKernelGGL(k_ctl_accept, dim3(1), dim3(1), 0, st, e->st, e->pdB, e->tokens, e->tok_cap);
+        hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, e->logitsB, V, -1, V, cfg, seed, e->st, e->tokens,
+                           e->tok_cap, e->pdB, (int32_t)ROLE_CORRECTIVE, 0, (int32_t*)nullptr);
+    } else {
+        hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, base_logits, V, 0, V, cfg, seed, e->st, e->tokens,
+                           e->tok_cap, e->pdB, (int32_t)ROLE_FALLBACK, 0, (int32_t*)nullptr);
+    }
+    PF_LAUNCHED(c);
+    return PF_OK;
+}
+
+// Captures the four round variants as graphs for this sampling
+// configuration and seed (kernel arguments are baked into the graphs; the
+// positions and tokens live in device memory).
+static pf_status ensure_round_graphs(pf_engine* e, const SamplingCfg& cfg, uint64_t seed) {
+    pf_ctx* c = e->c;
+    if (e->graphs_valid && e->graph_seed == seed && e->graph_profile == e->profile &&
+        std::memcmp(&e->graph_cfg, &cfg, sizeof(cfg)) == 0)
+        return PF_OK;
+    for (auto& row : e->round_exec)
+        for (auto& g : row)
+            if (g) { (void)hipGraphExecDestroy(g); g = nullptr; }
+    e->graphs_valid = false;
+    e->timed_used = 0;
+    e->kev_used = 0;
+    for (int reuse = 0; reuse < 2; reuse++)
+        for (int mtp = 0; mtp < 2; mtp++) {
+            hipGraph_t graph = nullptr;
+
+            PF_HIP(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+            e->capturing = true;
+            pf_status s = round_body(e, reuse != 0, mtp != 0, cfg, seed);
+            e->capturing = false;
+
+            hipError_t ee = hipStreamEndCapture(c->stream, &graph);
+            if (s) { if (graph) (void)hipGraphDestroy(graph); return s; }
+            if (ee != hipSuccess) return fail(c, PF_ERR_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(ee));
+            ee = hipGraphInstantiate(&e->round_exec[reuse][mtp], graph, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(graph);
+            if (ee != hipSuccess) return fail(c, PF_ERR_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(ee));
+        }
+    e->graph_cfg = cfg;
+    e->graph_seed = seed;
+    e->graph_profile = e->profile;
+    e->graphs_valid = true;
+    return PF_OK;
+}
+
 // Engine::generate, src/engine.cpp:276-396.  Prompt prefilled in passes
 // of up to 8 tokens; then MTP rounds (src/engine.cpp:304-373) as one base
 // pass (skipped when the previous round accepted every draft: its last
@@ -1147,10 +1288,25 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
         pf_status s = dalloc_t(c, &e->tokens, tokens_cap);
         if (s) return s;
         e->tok_cap = tokens_cap;
+        e->graphs_valid = false;   // the captured rounds hold the old buffer
     }
     if (n_prompt) PF_HIP(c, hipMemcpyAsync(e->tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, st));
     auto t0 = std::chrono::steady_clock::now();
-    // prefill (src/engine.cpp:286-290): every prompt token forwarded in order
+    // prefill (src/engine.cpp:286-290): every prompt token forwarded in order,
+    // full 8-row passes replayed from a captured graph
+    if (e->use_graphs && n_prompt >= MAX_PASS_ROWS && !e->prefill_exec) {
+        hipGraph_t graph = nullptr;
+        PF_HIP(c, hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        e->capturing = true;
+        pf_status s = run_pass(e, e->pdP, MAX_PASS_ROWS, 0, nullptr, e->hiddenA);
+        e->capturing = false;
+        hipError_t ee = hipStreamEndCapture(st, &graph);
+        if (s) { if (graph) (void)hipGraphDestroy(graph); return s; }
+        if (ee != hipSuccess) return fail(c, PF_ERR_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(ee));
+        ee = hipGraphInstantiate(&e->prefill_exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (ee != hipSuccess) return fail(c, PF_ERR_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(ee));
+    }
     std::vector<PassDesc> pds((n_prompt + MAX_PASS_ROWS - 1) / MAX_PASS_ROWS);
     for (uint32_t i = 0, j = 0; i < n_prompt; i += MAX_PASS_ROWS, j++) {
         uint32_t n = std::min(MAX_PASS_ROWS, n_prompt - i);
@@ -1160,8 +1316,13 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
         pd.m = n;
         for (uint32_t r = 0; r < n; r++) pd.tok[r] = prompt[i + r];
         PF_HIP(c, hipMemcpyAsync(e->pdP, &pd, sizeof(pd), hipMemcpyHostToDevice, st));
-        pf_status s = run_pass(e, e->pdP, n, e->pos, nullptr, e->hiddenA);
-        if (s) return s;
+        if (n == MAX_PASS_ROWS && e->prefill_exec) {
+            PF_HIP(c, hipGraphLaunch(e->prefill_exec, st));
+            e->hidden_valid = true;
+        } else {
+            pf_status s = run_pass(e, e->pdP, n, e->pos, nullptr, e->hiddenA);
+            if (s) return s;
+        }
         e->pos += n;
     }
     DecodeState s0{};
@@ -1172,70 +1333,66 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
     PF_HIP(c, hipStreamSynchronize(st));
     auto t1 = std::chrono::steady_clock::now();
 
-    e->timed_used = 0;
-    e->kev_used = 0;
+    e->verify_us = e->base_us = 0;
+    e->verify_n = e->base_n = 0;
+    e->kev_us = e->kev_bytes_sum = 0;
+    e->kev_n = 0;
+    e->round_us = 0;
+    e->round_n = 0;
+    const bool graphs = e->use_graphs && !e->profile;   // profiling times dispatches one by one
+    if (graphs) {
+        pf_status s = ensure_round_graphs(e, cfg, seed);
+        if (s) return s;
+    }
     uint32_t n_gen = 0;
     bool have_row = false;
-    pf_status s = PF_OK;
     while (n_gen < max_new) {
         if (e->max_memory && c->bytes > e->max_memory) {   // src/engine.cpp:297-301
             res->oom_protected = 1;
             break;
         }
         const bool mtp_round = NM > 0 && e->hidden_valid && n_gen + 4 <= max_new;   // src/engine.cpp:304-305
-        TimedPass* tp = nullptr;
-        const float* base_logits;
-        const float* base_hidden;
-        if (have_row) {
-            hipLaunchKernelGGL(k_ctl_reuse_row, dim3(1), dim3(1), 0, st, e->st);
-            base_logits = e->logitsB + (size_t)NM * V;
-            base_hidden = e->hiddenB + (size_t)NM * D;
-            e->pos += 1;
-            have_row = false;
+        if (e->pos + NM + 2 > e->rope_pos)
+            return fail(c, PF_ERR_CAPACITY, "position beyond the engine's max_context");
+        pf_status s;
+        size_t ev[4];
+        PF_HIP(c, hipEventRecord(e->rev0, st));
+        if (graphs) {
+            PF_HIP(c, hipGraphLaunch(e->round_exec[have_row][mtp_round], st));
+            for (int i = 0; i < 4; i++) ev[i] = 0;
+            e->hidden_valid = true;
         } else {
-            hipLaunchKernelGGL(k_ctl_pass_a, dim3(1), dim3(1), 0, st, e->st, e->pdA);
-            if ((s = timed_begin(e, false, &tp))) return s;
-            if ((s = run_pass(e, e->pdA, 1, e->pos, e->logitsA, e->hiddenA))) return s;
-            PF_HIP(c, hipEventRecord(tp->b, st));
-            res->passes++;
-            base_logits = e->logitsA;
-            base_hidden = e->hiddenA;
-            e->pos += 1;
+            e->timed_used = 0;
+            e->kev_used = 0;
+            if ((s = round_body(e, have_row, mtp_round, cfg, seed))) return s;
+            ev[0] = 0; ev[1] = e->timed_used; ev[2] = 0; ev[3] = e->kev_used;
         }
+        PF_HIP(c, hipEventRecord(e->rev1, st));
+        res->passes += (have_row ? 0 : 1) + (mtp_round ? 1 : 0);
+        e->pos += 1;   // the base position (pass A, or the reused verify row)
         if (mtp_round) {
-            hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, base_logits, V, 0, V, cfg, seed, e->st, e->tokens,
-                               e->tok_cap, e->pdB, (int32_t)ROLE_T1, 0, (int32_t*)nullptr);
-            if ((s = mtp_chain(e, base_hidden, true, &cfg, seed))) return s;
-            if ((s = timed_begin(e, true, &tp))) return s;
-            e->in_verify = true;
-            s = run_pass(e, e->pdB, NM + 1, e->pos, e->logitsB, e->hiddenB);
-            e->in_verify = false;
-            if (s) return s;
-            PF_HIP(c, hipEventRecord(tp->b, st));
-            res->passes++;
-            hipLaunchKernelGGL(k_argmax_rows, dim3(NM + 1), dim3(1024), 0, st, e->logitsB, V, V, e->pdB,
-                               e->st->row_argmax);
-            hipLaunchKernelGGL(k_ctl_accept, dim3(1), dim3(1), 0, st, e->st, e->pdB, e->tokens, e->tok_cap);
-            hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, e->logitsB, V, -1, V, cfg, seed, e->st, e->tokens,
-                               e->tok_cap, e->pdB, (int32_t)ROLE_CORRECTIVE, 0, (int32_t*)nullptr);
-            PF_LAUNCHED(c);
             PF_HIP(c, hipMemcpyAsync(e->word, &e->st->round_word, 4, hipMemcpyDeviceToHost, st));
             PF_HIP(c, hipStreamSynchronize(st));
+            if ((s = harvest_events(e, ev[0], ev[1], ev[2], ev[3]))) return s;
+            float rms = 0;
+            PF_HIP(c, hipEventElapsedTime(&rms, e->rev0, e->rev1));
+            e->round_us += rms * 1000.0;
+            e->round_n++;
             const uint32_t w = e->word[0], a = w & 0xFFu, pushed = (w >> 8) & 1u;
             n_gen += 1 + a + pushed;
             res->rounds++;
             if (a < NM) {
                 e->pos += a + 1;
+                have_row = false;
             } else {
                 e->pos += NM;
                 have_row = true;
             }
         } else {
-            // single-token path (src/engine.cpp:377-386)
-            hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, base_logits, V, 0, V, cfg, seed, e->st, e->tokens,
-                               e->tok_cap, e->pdB, (int32_t)ROLE_FALLBACK, 0, (int32_t*)nullptr);
-            PF_LAUNCHED(c);
+            PF_HIP(c, hipStreamSynchronize(st));
+            if ((s = harvest_events(e, ev[0], ev[1], ev[2], ev[3]))) return s;
             n_gen += 1;
+            have_row = false;
         }
     }
     DecodeState sf{};
@@ -1250,14 +1407,6 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
     res->mtp_rejected = (int32_t)sf.rejected;
     res->prefill_seconds = std::chrono::duration<double>(t1 - t0).count();
     res->decode_seconds = std::chrono::duration<double>(t2 - t1).count();
-    e->verify_us = e->base_us = 0;
-    e->verify_n = e->base_n = 0;
-    for (size_t i = 0; i < e->timed_used; i++) {
-        float ms = 0;
-        PF_HIP(c, hipEventElapsedTime(&ms, e->timed[i].a, e->timed[i].b));
-        if (e->timed[i].verify) { e->verify_us += ms * 1000.0; e->verify_n++; }
-        else { e->base_us += ms * 1000.0; e->base_n++; }
-    }
     return PF_OK;
 }
 
@@ -1269,18 +1418,17 @@ extern "C" pf_status pf_engine_profile(pf_engine* e, int32_t enable) {
 
 extern "C" pf_status pf_engine_gemv_stats(pf_engine* e, uint32_t* launches, double* avg_us, double* avg_bytes) {
     if (!e) return PF_ERR_ARG;
-    PF_HIP(e->c, hipStreamSynchronize(e->c->stream));
-    double us = 0, by = 0;
-    for (size_t i = 0; i < e->kev_used; i++) {
-        float ms = 0;
-        PF_HIP(e->c, hipEventElapsedTime(&ms, e->kev[i].a, e->kev[i].b));
-        us += ms * 1000.0;
-        by += e->kev_bytes[i];
-    }
-    const double n = (double)e->kev_used;
-    if (launches) *launches = (uint32_t)e->kev_used;
-    if (avg_us) *avg_us = n ? us / n : 0.0;
-    if (avg_bytes) *avg_bytes = n ? by / n : 0.0;
+    const double n = (double)e->kev_n;
+    if (launches) *launches = e->kev_n;
+    if (avg_us) *avg_us = n ? e->kev_us / n : 0.0;
+    if (avg_bytes) *avg_bytes = n ? e->kev_bytes_sum / n : 0.0;
+    return PF_OK;
+}
+
+extern "C" pf_status pf_engine_round_time(const pf_engine* e, double* round_us, uint32_t* rounds) {
+    if (!e) return PF_ERR_ARG;
+    if (round_us) *round_us = e->round_n ? e->round_us / e->round_n : 0.0;
+    if (rounds) *rounds = e->round_n;
     return PF_OK;
 }
 

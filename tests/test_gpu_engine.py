@@ -161,3 +161,31 @@ def test_oom_guard_stops_generation(gpu, tiny_weights, tiny_engine):
     tiny_engine.set_max_memory(1)
     toks, res = tiny_engine.generate(W.prompt_ids(4, cfg["n_vocab"]), 10, GREEDY)
     assert res.oom_protected == 1 and len(toks) == 4
+
+
+def test_generate_without_graphs_matches(gpu, tiny_weights, monkeypatch):
+    """The kernels issued one by one (profiling path) give the same stream
+    as the captured round graphs."""
+    cfg, w = tiny_weights
+    w = _zero_mats(w, scale=0.004, seed=12)
+    prompt = W.prompt_ids(9, cfg["n_vocab"], seed=4)
+    monkeypatch.setenv("PF_NO_GRAPHS", "1")
+    toks, res, ot, oa, orj = _gen_both(gpu, cfg, w, prompt, 33, GREEDY)
+    np.testing.assert_array_equal(toks, ot)
+    assert (res.mtp_accepted, res.mtp_rejected) == (oa, orj)
+
+
+def test_profiled_generate_matches(gpu, tiny_weights):
+    cfg, w = tiny_weights
+    m = pf.Model(gpu, cfg, w)
+    e = pf.Engine(m, **KV)
+    prompt = W.prompt_ids(12, cfg["n_vocab"], seed=8)
+    t1, _ = e.generate(prompt, 20, GREEDY)
+    e.reset()
+    e.profile(True)
+    t2, _ = e.generate(prompt, 20, GREEDY)
+    n, us, by = e.gemv_stats()
+    np.testing.assert_array_equal(t1, t2)
+    assert n > 0 and us > 0 and by > 0
+    e.close()
+    m.close()
