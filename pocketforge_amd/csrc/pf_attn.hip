@@ -309,7 +309,15 @@ __global__ __launch_bounds__(128) void k_attn_merge(const PassDesc* __restrict__
     const uint32_t nch = (C + 63u) / 64u;
     const float* wp = Wp + ((size_t)m * g.n_heads + h) * cstride * hd + i;
     float o = 0.0f;
-    for (uint32_t c = 0; c < nch; c++) o = o + wp[(size_t)c * hd];
+    uint32_t c = 0;
+    for (; c + 8 <= nch; c += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = wp[(size_t)(c + u) * hd];
+#pragma unroll
+        for (int u = 0; u < 8; u++) o = o + v[u];
+    }
+    for (; c < nch; c++) o = o + wp[(size_t)c * hd];
     const float ps = S[((size_t)m * g.n_heads + h) * s_stride + C];
     o = __builtin_fmaf(ps, vself[(size_t)m * D + h * hd + i], o);
     out[(size_t)m * D + h * hd + i] = o;

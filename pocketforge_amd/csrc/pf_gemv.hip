@@ -208,44 +208,74 @@ __global__ __launch_bounds__(256) void k_quant_rows(const float* __restrict__ x,
 
 // x[m] += (float)(acc[m] * as_prev[m]) (when acc != null; acc cleared),
 // then RMSNorm (src/matmul_neon.cpp:231-239, CANON(4) sum of squares) with
-// weight w, then quantize_activation_row of the normed row.  Grid M, 256
-// threads.
+// weight w, then quantize_activation_row of the normed row.  Grid M, 1024
+// threads: all loads are issued first; the 256 canonical lanes read the
+// row back from LDS (K <= 4096).
 template <int PER>
-__global__ __launch_bounds__(256) void k_resid_norm_quant(float* __restrict__ x, uint32_t K,
-                                                          double* __restrict__ acc,
-                                                          const float* __restrict__ as_prev,
-                                                          const float* __restrict__ w,
-                                                          int8_t* __restrict__ q, uint32_t q_stride,
-                                                          float* __restrict__ as, int32_t* __restrict__ bsum,
-                                                          uint32_t bsum_stride) {
-    __shared__ float red[4];
-    const uint32_t m = blockIdx.x;
-    float v[PER];
-    float ss = 0.0f;
+__global__ __launch_bounds__(1024) void k_resid_norm_quant(float* __restrict__ x, uint32_t K,
+                                                           double* __restrict__ acc,
+                                                           const float* __restrict__ as_prev,
+                                                           const float* __restrict__ w,
+                                                           int8_t* __restrict__ q, uint32_t q_stride,
+                                                           float* __restrict__ as, int32_t* __restrict__ bsum,
+                                                           uint32_t bsum_stride) {
+    __shared__ float row[4096];
+    __shared__ float red[16];
+    const uint32_t m = blockIdx.x, t = threadIdx.x;
+    float xv[PER], wv[PER];
+    double av[PER];
 #pragma unroll
     for (int k = 0; k < PER; k++) {
-        uint32_t i = threadIdx.x + 256u * k;
-        float xi = 0.0f;
-        if (i < K) {
-            xi = x[(size_t)m * K + i];
-            if (acc) {
-                xi = xi + take_acc(acc, (size_t)m * K + i, as_prev[m]);
-                x[(size_t)m * K + i] = xi;
-            }
-            ss = __builtin_fmaf(xi, xi, ss);
-        }
-        v[k] = xi;
+        const uint32_t i = t + 1024u * k;
+        xv[k] = i < K ? x[(size_t)m * K + i] : 0.0f;
+        wv[k] = i < K ? w[i] : 0.0f;
+        av[k] = (acc && i < K) ? acc[(size_t)m * K + i] : 0.0;
     }
-    ss = block_canon_sum<4>(ss, red);
+    const float ap = acc ? as_prev[m] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const uint32_t i = t + 1024u * k;
+        if (acc && i < K) {
+            xv[k] = xv[k] + (float)(av[k] * (double)ap);
+            x[(size_t)m * K + i] = xv[k];
+            acc[(size_t)m * K + i] = 0.0;
+        }
+        if (i < K) row[i] = xv[k];
+    }
+    __syncthreads();
+    // CANON(4): lane l < 256 sums x[l]^2, x[l+256]^2, ... in order
+    float part = 0.0f;
+    if (t < 256)
+        for (uint32_t i = t; i < K; i += 256) part = __builtin_fmaf(row[i], row[i], part);
+    float wsum = wave_tree_sum(part);
+    if ((t & 63) == 0 && t < 256) red[t >> 6] = wsum;
+    __syncthreads();
+    const float ss = (red[0] + red[2]) + (red[1] + red[3]);
     const float rms = __builtin_sqrtf(ss / (float)K + 1e-6f);
     const float inv = 1.0f / rms;
 #pragma unroll
+    for (int k = 0; k < PER; k++) xv[k] = xv[k] * inv * wv[k];
+    __syncthreads();
+    quantize_row_block<PER, 1024>(xv, K, q + (size_t)m * q_stride, as + m,
+                                  bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
+}
+
+// quantize_activation_row of rows of length K <= 1024 * PER, 1024 threads.
+template <int PER>
+__global__ __launch_bounds__(1024) void k_quant_rows_wide(const float* __restrict__ x, uint32_t K,
+                                                          int8_t* __restrict__ q, uint32_t q_stride,
+                                                          float* __restrict__ as, int32_t* __restrict__ bsum,
+                                                          uint32_t bsum_stride) {
+    __shared__ float red[16];
+    const uint32_t m = blockIdx.x;
+    float v[PER];
+#pragma unroll
     for (int k = 0; k < PER; k++) {
-        uint32_t i = threadIdx.x + 256u * k;
-        if (i < K) v[k] = v[k] * inv * w[i];
+        const uint32_t i = threadIdx.x + 1024u * k;
+        v[k] = i < K ? x[(size_t)m * K + i] : 0.0f;
     }
-    quantize_row_block<PER, 256>(v, K, q + (size_t)m * q_stride, as + m,
-                                 bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
+    quantize_row_block<PER, 1024>(v, K, q + (size_t)m * q_stride, as + m,
+                                  bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
 }
 
 // x[m] += (float)(acc[m] * as_prev[m]) (the last layer's down residual).
@@ -267,15 +297,25 @@ __global__ __launch_bounds__(1024) void k_swiglu_quant(double* __restrict__ acc,
                                                        uint32_t bsum_stride) {
     __shared__ float red[16];
     const uint32_t m = blockIdx.x;
+    double ga[PER], ua[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const uint32_t i = threadIdx.x + 1024u * k;
+        ga[k] = i < ff ? acc[(size_t)m * 2 * ff + i] : 0.0;
+        ua[k] = i < ff ? acc[(size_t)m * 2 * ff + ff + i] : 0.0;
+    }
+    const double a = (double)as_in[m];
     float v[PER];
 #pragma unroll
     for (int k = 0; k < PER; k++) {
-        uint32_t i = threadIdx.x + 1024u * k;
+        const uint32_t i = threadIdx.x + 1024u * k;
         float f = 0.0f;
         if (i < ff) {
-            float gt = take_acc(acc, (size_t)m * 2 * ff + i, as_in[m]);
-            float u = take_acc(acc, (size_t)m * 2 * ff + ff + i, as_in[m]);
-            float sig = 1.0f / (1.0f + expf_c(-gt));
+            acc[(size_t)m * 2 * ff + i] = 0.0;
+            acc[(size_t)m * 2 * ff + ff + i] = 0.0;
+            const float gt = (float)(ga[k] * a);
+            const float u = (float)(ua[k] * a);
+            const float sig = 1.0f / (1.0f + expf_c(-gt));
             f = gt * sig * u;
         }
         v[k] = f;

@@ -236,14 +236,17 @@ static void repack_tiles(int fmt, uint32_t cols, const uint8_t* codes, const uin
         }
 }
 
-// K split of a tiled matrix: the largest blocks-per-wave (2..16) that still
-// gives at least 2048 waves, so every launch covers the 256 CUs.
+// K split of a tiled matrix: the largest blocks-per-wave (1..16) that still
+// gives at least `min_waves` waves (default 2048: every launch covers the
+// 256 CUs; PF_GEMV_MIN_WAVES overrides it).
 static void choose_split(pf_matrix* M) {
     const uint32_t nb = M->cols / 32, G = M->rows / 64;
-    uint32_t best = 2;
-    for (uint32_t bpw : {2u, 4u, 8u, 16u}) {
+    uint64_t min_waves = 2048;
+    if (const char* s = std::getenv("PF_GEMV_MIN_WAVES")) min_waves = std::strtoull(s, nullptr, 10);
+    uint32_t best = 1;
+    for (uint32_t bpw : {1u, 2u, 4u, 8u, 16u}) {
         uint32_t splits = (nb + 4 * bpw - 1) / (4 * bpw);
-        if ((uint64_t)G * splits * 4 >= 2048) best = bpw;
+        if ((uint64_t)G * splits * 4 >= min_waves) best = bpw;
     }
     M->bpw = best;
     M->splits = (nb + 4 * best - 1) / (4 * best);
@@ -1056,8 +1059,9 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
     for (uint32_t l = 0; l < d.n_layers; l++) {
         const float* an = m->attn_norm + (size_t)l * D;
         const float* fn = m->ffn_norm + (size_t)l * D;
-        PF_PER_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(M), dim3(256), 0, st, e->x, D,
-                                            l == 0 ? (double*)nullptr : e->acc, as3, an, e->act, ks, as0, e->bsum, bs));
+        PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(M), dim3(1024), 0, st, e->x, D,
+                                                l == 0 ? (double*)nullptr : e->acc, as3, an, e->act, ks, as0, e->bsum,
+                                                bs));
         if (pf_status s = pass_gemv(e, m->qkv[l], M)) return s;
         hipLaunchKernelGGL(k_qkv_post, dim3(M, H), dim3(64), 0, st, e->acc, as0, pd, e->rope_c, e->rope_s, g, e->kv, l,
                            e->q, e->k, e->v);
@@ -1069,11 +1073,11 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
                                0xFFFFFFFFu, e->S, e->s_stride, e->Wp, e->cstride);
         hipLaunchKernelGGL(k_attn_merge, dim3(M, H), dim3(128), 0, st, pd, g, e->S, e->s_stride, e->Wp, e->cstride,
                            e->v, e->attn);
-        PF_PER_SWITCH(D, hipLaunchKernelGGL(k_quant_rows<PER>, dim3(M), dim3(256), 0, st, e->attn, D, D, e->act, ks,
-                                            as1, e->bsum, bs));
+        PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_quant_rows_wide<PER>, dim3(M), dim3(1024), 0, st, e->attn, D,
+                                                e->act, ks, as1, e->bsum, bs));
         if (pf_status s = pass_gemv(e, m->o[l], M)) return s;
-        PF_PER_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(M), dim3(256), 0, st, e->x, D, e->acc, as1,
-                                            fn, e->act, ks, as2, e->bsum, bs));
+        PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(M), dim3(1024), 0, st, e->x, D,
+                                                e->acc, as1, fn, e->act, ks, as2, e->bsum, bs));
         if (pf_status s = pass_gemv(e, m->gu[l], M)) return s;
         PF_PER1024_SWITCH(F, hipLaunchKernelGGL(k_swiglu_quant<PER>, dim3(M), dim3(1024), 0, st, e->acc,
                                                 (const float*)as2, F, e->act, ks, as3, e->bsum, bs));
