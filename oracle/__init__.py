@@ -92,6 +92,8 @@ def lib():
         L.orc_kv_attention_scores.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, f32p, f32p]
         for n in ("orc_kv_attention_weighted_sum", "orc_kv_attention_weighted_sum_ref"):
             getattr(L, n).argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, f32p, f32p, C.c_uint32]
+        for n in ("orc_attn_head", "orc_attn_head_ref"):
+            getattr(L, n).argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, f32p, f32p, f32p, f32p]
         L.orc_kv_size.restype = C.c_uint32
         L.orc_kv_size.argtypes = [C.c_void_p]
         L.orc_kv_clear.argtypes = [C.c_void_p]

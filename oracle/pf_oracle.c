@@ -26,8 +26,12 @@
  *   fp32 x block GEMV (tied unembed, MTP heads): lane l = b mod 64 of the
  *             64 lanes accumulates blocks b ascending, elements ascending,
  *             with fmaf(h, w, acc); then the halving tree over 64 lanes.
- *   attention weighted sum: chunks of 64 visible entries; fmaf chain inside
- *             a chunk from 0.0f; chunk partials added left to right.
+ *   attention (engine): chunks of 256 list entries with a chunk max, exp,
+ *             CANON(4) chunk sum and sub-chunk fmaf chains, merged left to
+ *             right with exp(m_c - max) factors (attn_head).
+ *   KVCache::attention_weighted_sum: chunks of 64 visible entries; fmaf
+ *             chain inside a chunk from 0.0f; chunk partials added left to
+ *             right.
  *   sampling sums / prefix sums: 64 contiguous chunks, sequential inside
  *             a chunk, chunk totals added left to right.
  */
@@ -746,6 +750,107 @@ void orc_rope_table(uint32_t hd, uint32_t pos, float* cos_out, float* sin_out) {
     }
 }
 
+/* Softmax-weighted sum of one head (src/engine.cpp:767-778 with
+ * src/matmul_neon.cpp:212-226 and src/kv_cache.cpp:160-198) in the
+ * canonical chunked order.  The list is the `cnt` visible entries followed
+ * by the fp32 self entry (scores in e->scores[0..cnt]).  Chunks of 256
+ * entries: m_c = chunk max, e_j = exp(s_j - m_c), T_c = CANON(4) sum with
+ * one entry per lane, U_c = ((W0 + W1) + W2) + W3 where W_s is the fmaf
+ * chain over the 64 entries of sub-chunk s of e_j * (float)v_j[i] * vs_j
+ * (the self entry uses v_self).  Chunks merge left to right:
+ * f_c = exp(m_c - max_c m_c), T = fmaf(T_c, f_c, T), U = fmaf(U_c, f_c, U),
+ * out = U * (1 / (T + 1e-10)). */
+static void attn_head(orc_kv* kv, const float* scores, uint32_t l, uint32_t hh, uint32_t cnt,
+                      const float* vself, float* out) {
+    const uint32_t hd = kv->hd, n = cnt + 1, nc = (n + 255) / 256;
+    const orc_head* c = &kv->h[(size_t)l * kv->n_heads + hh];
+    float* U = (float*)calloc(hd, sizeof(float));
+    float* Uc = (float*)malloc(sizeof(float) * hd);
+    float* Wv = (float*)malloc(sizeof(float) * hd);
+    float* mc = (float*)malloc(sizeof(float) * nc);
+    float* Tc = (float*)malloc(sizeof(float) * nc);
+    float* Ucs = (float*)malloc(sizeof(float) * hd * nc);
+    for (uint32_t ci = 0; ci < nc; ci++) {
+        const uint32_t j0 = ci * 256, j1 = j0 + 256 < n ? j0 + 256 : n;
+        float mx = scores[j0];
+        for (uint32_t j = j0 + 1; j < j1; j++) if (scores[j] > mx) mx = scores[j];
+        float P[256];
+        float ev[256];
+        for (uint32_t t = 0; t < 256; t++) {
+            uint32_t j = j0 + t;
+            ev[t] = j < n ? orc_expf(scores[j] - mx) : 0.0f;
+            P[t] = ev[t];
+        }
+        Tc[ci] = canon_tree(P, 4);
+        for (uint32_t i = 0; i < hd; i++) Uc[i] = 0.0f;
+        for (uint32_t s = 0; s < 4; s++) {
+            for (uint32_t i = 0; i < hd; i++) Wv[i] = 0.0f;
+            for (uint32_t t = 64 * s; t < 64 * s + 64 && j0 + t < n; t++) {
+                uint32_t j = j0 + t;
+                if (j < cnt) {
+                    const int8_t *k, *v; float ks, vs;
+                    kv_entry(kv, c, j, &k, &ks, &v, &vs);
+                    for (uint32_t i = 0; i < hd; i++) Wv[i] = fmaf(ev[t], (float)v[i] * vs, Wv[i]);
+                } else {
+                    for (uint32_t i = 0; i < hd; i++) Wv[i] = fmaf(ev[t], vself[i], Wv[i]);
+                }
+            }
+            for (uint32_t i = 0; i < hd; i++) Uc[i] = Uc[i] + Wv[i];
+        }
+        mc[ci] = mx;
+        memcpy(Ucs + (size_t)ci * hd, Uc, sizeof(float) * hd);
+    }
+    float M = mc[0];
+    for (uint32_t ci = 1; ci < nc; ci++) if (mc[ci] > M) M = mc[ci];
+    float T = 0.0f;
+    for (uint32_t ci = 0; ci < nc; ci++) {
+        float f = orc_expf(mc[ci] - M);
+        T = fmaf(Tc[ci], f, T);
+        for (uint32_t i = 0; i < hd; i++) U[i] = fmaf(Ucs[(size_t)ci * hd + i], f, U[i]);
+    }
+    float inv = 1.0f / (T + 1e-10f);
+    for (uint32_t i = 0; i < hd; i++) out[i] = U[i] * inv;
+    free(U); free(Uc); free(Wv); free(mc); free(Tc); free(Ucs);
+}
+
+/* Scores of one head's attention in the engine (src/engine.cpp:757-768):
+ * the cached entries' dots, then the self entry's sequential dot with the
+ * fp32 key, all times 1/sqrt(head_dim).  Returns the list length cnt + 1. */
+static uint32_t attn_scores(orc_kv* kv, uint32_t l, uint32_t hh, const float* q, const float* kself, float* scores) {
+    const uint32_t hd = kv->hd;
+    const float scale = 1.0f / sqrtf((float)hd);
+    uint32_t cnt = orc_kv_attention_scores(kv, l, hh, q, scores);
+    float self = 0.0f;
+    for (uint32_t i = 0; i < hd; i++) self = self + q[i] * kself[i];
+    scores[cnt] = self;
+    for (uint32_t i = 0; i <= cnt; i++) scores[i] *= scale;
+    return cnt + 1;
+}
+
+/* One head of the engine's attention in the canonical chunked order. */
+void orc_attn_head(orc_kv* kv, uint32_t layer, uint32_t head, const float* q, const float* kself,
+                   const float* vself, float* out) {
+    const orc_head* c = &kv->h[(size_t)layer * kv->n_heads + head];
+    float* sc = (float*)malloc(sizeof(float) * (kv_count(c) + 1));
+    uint32_t n = attn_scores(kv, layer, head, q, kself, sc);
+    attn_head(kv, sc, layer, head, n - 1, vself, out);
+    free(sc);
+}
+
+/* The same in the reference's own order (src/engine.cpp:767-778): softmax
+ * with libm exp and a sequential sum, the sequential weighted sum of the
+ * cached entries, then fmaf(p_self, v_self, out). */
+void orc_attn_head_ref(orc_kv* kv, uint32_t layer, uint32_t head, const float* q, const float* kself,
+                       const float* vself, float* out) {
+    const orc_head* c = &kv->h[(size_t)layer * kv->n_heads + head];
+    float* sc = (float*)malloc(sizeof(float) * (kv_count(c) + 1));
+    uint32_t n = attn_scores(kv, layer, head, q, kself, sc);
+    orc_softmax_ref(sc, n);
+    orc_kv_attention_weighted_sum_ref(kv, layer, head, sc, out, n - 1);
+    for (uint32_t i = 0; i < kv->hd; i++) out[i] = fmaf(sc[n - 1], vself[i], out[i]);
+    free(sc);
+}
+
 /* Engine::forward_with_hidden, src/engine.cpp:459-589, with the weights
  * wired (src/engine.cpp:693-715, 789-796, 815-843), position = number of
  * tokens forwarded so far, and each head writing its own output slice. */
@@ -761,7 +866,6 @@ void orc_forward(orc_engine* e, int32_t token, float* logits, float* hidden) {
     float* rc = (float*)malloc(sizeof(float) * hd / 2);
     float* rs = (float*)malloc(sizeof(float) * hd / 2);
     orc_rope_table(hd, pos, rc, rs);
-    float scale = 1.0f / sqrtf((float)hd);
 
     for (uint32_t l = 0; l < d->n_layers; l++) {
         const orc_qmat* W = d->layers + (size_t)l * 7;
@@ -783,20 +887,8 @@ void orc_forward(orc_engine* e, int32_t token, float* logits, float* hidden) {
                 kh[i + 1] = fmaf(k0, s, k1 * c);
             }
         }
-        for (uint32_t hh = 0; hh < H; hh++) {              /* src/engine.cpp:753-779 */
-            const float* qh = e->q + hh * hd; const float* kh = e->k + hh * hd;
-            const float* vh = e->v + hh * hd;
-            uint32_t cnt = orc_kv_attention_scores(e->kv, l, hh, qh, e->scores);
-            float self = 0.0f;
-            for (uint32_t i = 0; i < hd; i++) self = self + qh[i] * kh[i];
-            e->scores[cnt] = self;
-            for (uint32_t i = 0; i <= cnt; i++) e->scores[i] *= scale;
-            orc_softmax(e->scores, cnt + 1);
-            float* out = e->attn + hh * hd;
-            orc_kv_attention_weighted_sum(e->kv, l, hh, e->scores, out, cnt);
-            float ps = e->scores[cnt];
-            for (uint32_t i = 0; i < hd; i++) out[i] = fmaf(ps, vh[i], out[i]);
-        }
+        for (uint32_t hh = 0; hh < H; hh++)                /* src/engine.cpp:753-779 */
+            orc_attn_head(e->kv, l, hh, e->q + hh * hd, e->k + hh * hd, e->v + hh * hd, e->attn + hh * hd);
         for (uint32_t hh = 0; hh < H; hh++)                /* src/engine.cpp:782-786 */
             orc_kv_store(e->kv, l, hh, pos, e->k + hh * hd, e->v + hh * hd);
         orc_quantize_activation_row(e->attn, e->a8, &as, D); /* src/engine.cpp:789-796 */

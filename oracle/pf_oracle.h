@@ -82,6 +82,13 @@ void     orc_kv_attention_weighted_sum_ref(orc_kv* kv, uint32_t layer, uint32_t 
 void     orc_kv_attention_weighted_sum(orc_kv* kv, uint32_t layer, uint32_t head,
                                        const float* scores, float* out, uint32_t count);
 uint32_t orc_kv_size(const orc_kv* kv);
+/* One head of the engine's attention over the cache's visible entries plus
+ * the fp32 self entry (k_self, v_self): canonical chunked order, and the
+ * reference's own order. */
+void     orc_attn_head(orc_kv* kv, uint32_t layer, uint32_t head, const float* q, const float* k_self,
+                       const float* v_self, float* out);
+void     orc_attn_head_ref(orc_kv* kv, uint32_t layer, uint32_t head, const float* q, const float* k_self,
+                           const float* v_self, float* out);
 void     orc_kv_clear(orc_kv* kv);
 uint32_t orc_kv_pool_count(const orc_kv* kv, uint32_t layer, uint32_t head);
 /* Copies the visible rows of (layer, head) in attention order:

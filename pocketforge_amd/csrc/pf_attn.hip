@@ -5,12 +5,13 @@
 //                  written to the plane row of each position (sink slot or
 //                  ring slot; the ring has slack, so pending rows of a
 //                  verify pass never overwrite a visible entry)
-//   k_attn_scores  one thread per visible entry: the reference's sequential
-//                  dot over head_dim, and the fp32 self score
-//   k_attn_softmax per (row, head): max, exp, CANON(4) sum, normalise
-//   k_attn_wsum    per (row, head, 64-entry chunk): fmaf chain over entries
-//   k_attn_merge   per (row, head): chunk partials left to right + self
-//                  term; the O projection's quantize_activation_row follows
+//   k_attn_chunk   per (row, head, 256-entry chunk of the row's list):
+//                  scores, chunk max, exp, chunk sum and chunk-weighted V
+//   k_attn_merge_chunks  per (row, head): chunks rescaled to the row max
+//                  and merged; the O projection's quantize_activation_row
+//                  follows
+// The KVCache API (raw scores; weighted sum of caller probabilities) runs
+// k_attn_scores and k_attn_wsum.
 // k_pool_rows folds evicted window entries into pooled rows
 // (src/kv_cache.cpp:77-109) before a pass needs them.
 #include "pf_device.h"
@@ -214,30 +215,6 @@ __global__ __launch_bounds__(256) void k_attn_scores(const PassDesc* __restrict_
     }
 }
 
-// In place: S <- softmax(S[0..C]) (src/matmul_neon.cpp:212-226 with the
-// CANON(4) sum).  Grid (M, H), 256 threads.
-__global__ __launch_bounds__(256) void k_attn_softmax(const PassDesc* __restrict__ pd, KvGeom g,
-                                                      int32_t view_sink, uint32_t view_nw,
-                                                      float* __restrict__ S, uint32_t s_stride) {
-    __shared__ float red[4];
-    const uint32_t m = blockIdx.x, h = blockIdx.y;
-    if (m >= pd->m) return;
-    const uint32_t n = pass_view(g, pd, m, view_sink, view_nw).count() + 1;
-    float* s = S + ((size_t)m * g.n_heads + h) * s_stride;
-    float mx = -__builtin_inff();
-    for (uint32_t j = threadIdx.x; j < n; j += 256) mx = fmaxf(mx, s[j]);
-    mx = block_max<4>(mx, red);
-    float part = 0.0f;
-    for (uint32_t j = threadIdx.x; j < n; j += 256) {
-        float e = expf_c(s[j] - mx);
-        s[j] = e;
-        part = part + e;
-    }
-    const float sum = block_canon_sum<4>(part, red);
-    const float inv = 1.0f / (sum + 1e-10f);
-    for (uint32_t j = threadIdx.x; j < n; j += 256) s[j] = s[j] * inv;
-}
-
 // Wp[((m*H + y)*cstride + c)*hd + i] = fmaf chain over the visible entries
 // [64c, min(64c+64, C, limit)) of p_j * ((float)v_j[i] * vs_j)
 // (src/kv_cache.cpp:173-197, contracted as the reference build does).  The
@@ -294,33 +271,182 @@ __global__ void k_wsum_combine_one(const float* __restrict__ Wp, uint32_t nch, u
     out[i] = o;
 }
 
-// Attention output of (row m, head h): chunk partials added left to right,
-// then fmaf(p_self, v_self, .) (src/engine.cpp:771-778, each head writing
-// its own slice).  Grid (M, H), 128 threads.
-__global__ __launch_bounds__(128) void k_attn_merge(const PassDesc* __restrict__ pd, KvGeom g,
-                                                    const float* __restrict__ S, uint32_t s_stride,
-                                                    const float* __restrict__ Wp, uint32_t cstride,
-                                                    const float* __restrict__ vself, float* __restrict__ out) {
+// Engine attention, first stage.  Block task (row m, head h, chunk c) covers
+// list entries [256c, 256c + 256) of row m; the list is the C visible
+// entries followed by the fp32 self entry (index C).  Scores as in
+// src/engine.cpp:757-768 (cached entries: sequential fmaf dot of q with
+// (float)k * k_scale; self entry: sequential mul+add dot with the fp32 key;
+// both times 1/sqrt(head_dim)), then the chunk max m_c, e_j = exp(s_j - m_c),
+// the CANON(4) chunk sum T_c (one entry per thread) and the chunk's weighted
+// sum U_c = (((0 + W0) + W1) + W2) + W3, where W_s is the fmaf chain from
+// 0.0f over the entries of sub-chunk s (64 entries) of e_j * ((float)v_j *
+// v_scale_j), or of e_j * v_self for the self entry.  Writes
+// S[(m*H + h)*s_stride + 2c] = m_c, [.. + 2c + 1] = T_c and
+// Up[((m*H + h)*cstride + c)*hd + i] = U_c[i].
+//
+// 1-D grid of 8 * M * ceil(G / 8) blocks, G = H * chunks, task group
+// grp = c * H + h.  Blocks are dealt to the 8 XCDs round-robin, so block b
+// runs on XCD b mod 8: group grp's M rows get blocks with b mod 8 = grp mod
+// 8, and after the first row a chunk's K/V rows come from that XCD's L2.
+// 256 threads; head_dim = 16 * PARTS (up to 128).
+template <int PARTS>
+__global__ __launch_bounds__(256) void k_attn_chunk(const PassDesc* __restrict__ pd, KvGeom g, KvPlanes kv,
+                                                    uint32_t layer, uint32_t M, uint32_t n_groups,
+                                                    const float* __restrict__ q, const float* __restrict__ kself,
+                                                    const float* __restrict__ vself, float* __restrict__ S,
+                                                    uint32_t s_stride, float* __restrict__ Up, uint32_t cstride) {
+    __shared__ float qs[128], kss[128];
+    __shared__ __align__(16) int8_t vt[256][144];     // 16 bytes of padding per row
+    __shared__ float vsc[256], pe[256];
+    __shared__ float wp[4][128];
+    __shared__ float red[4];
+    const uint32_t t = threadIdx.x;
+    const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
+    const uint32_t grp = (slot / M) * 8u + xcd, m = slot % M;
+    if (grp >= n_groups || m >= pd->m) return;
+    constexpr uint32_t hd = 16 * PARTS;
+    const uint32_t D = g.n_heads * hd;
+    const uint32_t c = grp / g.n_heads, h = grp % g.n_heads;
+    const KvView v = kv_view(g, pd->pos0 + m);
+    const uint32_t C = v.count(), n = C + 1, j0 = c * 256u;
+    if (j0 >= n) return;
+    const uint32_t j = j0 + t;
+    const size_t plane = plane_index(g, layer, h);
+    const size_t qrow = (size_t)m * D + h * hd;
+    const uint32_t nvis = j0 < C ? min(256u, C - j0) : 0u;
+    // every load first: the query, the fp32 self key, this thread's K and V rows
+    if (t < hd) {
+        qs[t] = q[qrow + t];
+        kss[t] = kself[qrow + t];
+    }
+    int4 kw[PARTS];
+    float ks = 0.0f, vs = 0.0f;
+    if (t < nvis) {
+        const size_t row = plane * g.rows + kv_row(g, v, j);
+        const int4* kr = reinterpret_cast<const int4*>(kv.k + row * hd);
+        const int4* vr = reinterpret_cast<const int4*>(kv.v + row * hd);
+        int4 vw[PARTS];
+#pragma unroll
+        for (int p = 0; p < PARTS; p++) {
+            kw[p] = kr[p];
+            vw[p] = vr[p];
+        }
+        ks = kv.ks[row];
+        vs = kv.vs[row];
+#pragma unroll
+        for (int p = 0; p < PARTS; p++) *reinterpret_cast<int4*>(&vt[t][p * 16]) = vw[p];
+    }
+    vsc[t] = vs;                 // 0 past the visible entries: their terms below add exactly 0
+    __syncthreads();
+    const float scale = 1.0f / __builtin_sqrtf((float)hd);
+    float s = -__builtin_inff();
+    if (t < nvis) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int p = 0; p < PARTS; p++) {
+            const int wv[4] = {kw[p].x, kw[p].y, kw[p].z, kw[p].w};
+#pragma unroll
+            for (int b = 0; b < 16; b++) {
+                const int8_t cb = (int8_t)((wv[b >> 2] >> (8 * (b & 3))) & 0xFF);
+                acc = __builtin_fmaf(qs[p * 16 + b], (float)cb * ks, acc);
+            }
+        }
+        s = acc * scale;
+    } else if (j == C) {
+        float self = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < hd; i++) self = self + qs[i] * kss[i];
+        s = self * scale;
+    }
+    const float mx = block_max<4>(s, red);
+    const float ex = j < n ? expf_c(s - mx) : 0.0f;
+    pe[t] = ex;
+    const float T = block_canon_sum<4>(ex, red);       // its barriers publish pe
+    const uint32_t sc = t >> 6, i0 = 2u * (t & 63u);
+    if (i0 < hd) {
+        float w0 = 0.0f, w1 = 0.0f;
+        // entries [64sc, min(64sc + 64, nvis)) in groups of 8; the padding
+        // entries up to the next multiple of 8 have v_scale 0 and finite
+        // codes and weights, so fmaf(e, code * 0, w) == w
+        const uint32_t e_end = min(64u * sc + 64u, (nvis + 7u) & ~7u);
+        for (uint32_t e = 64u * sc; e < e_end; e += 8) {
+            float pp[8], vv[8];
+            uint32_t cc[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                pp[u] = pe[e + u];
+                vv[u] = vsc[e + u];
+                cc[u] = *reinterpret_cast<const uint16_t*>(&vt[e + u][i0]);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                w0 = __builtin_fmaf(pp[u], (float)(int8_t)(cc[u] & 0xFFu) * vv[u], w0);
+                w1 = __builtin_fmaf(pp[u], (float)(int8_t)(cc[u] >> 8) * vv[u], w1);
+            }
+        }
+        const uint32_t js = C - j0;                     // list index of the self entry in the chunk
+        if (js < 256u && (js >> 6) == sc) {
+            const float p = pe[js];
+            w0 = __builtin_fmaf(p, vself[qrow + i0], w0);
+            w1 = __builtin_fmaf(p, vself[qrow + i0 + 1], w1);
+        }
+        wp[sc][i0] = w0;
+        wp[sc][i0 + 1] = w1;
+    }
+    __syncthreads();
+    const size_t mh = (size_t)m * g.n_heads + h;
+    if (t < hd) {
+        float u = 0.0f;
+        u = u + wp[0][t];
+        u = u + wp[1][t];
+        u = u + wp[2][t];
+        u = u + wp[3][t];
+        Up[(mh * cstride + c) * hd + t] = u;
+    }
+    if (t == 0) {
+        S[mh * s_stride + 2 * c] = mx;
+        S[mh * s_stride + 2 * c + 1] = T;
+    }
+}
+
+// Engine attention, second stage: the chunks of (row m, head h) merged left
+// to right with f_c = exp(m_c - max_c m_c): T = fmaf(T_c, f_c, T),
+// U = fmaf(U_c, f_c, U), out = U * (1 / (T + 1e-10)) (the softmax
+// normalisation of src/matmul_neon.cpp:212-226 applied after the weighted
+// sum; each head writes its own slice, src/engine.cpp:771-778).
+// Grid (M, H), 128 threads.
+__global__ __launch_bounds__(128) void k_attn_merge_chunks(const PassDesc* __restrict__ pd, KvGeom g,
+                                                           const float* __restrict__ S, uint32_t s_stride,
+                                                           const float* __restrict__ Up, uint32_t cstride,
+                                                           float* __restrict__ out) {
+    __shared__ float fs[128], ts[128];
     const uint32_t m = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
     if (m >= pd->m) return;
     const uint32_t hd = g.head_dim, D = g.n_heads * hd;
-    if (i >= hd) return;
-    const uint32_t C = kv_view(g, pd->pos0 + m).count();
-    const uint32_t nch = (C + 63u) / 64u;
-    const float* wp = Wp + ((size_t)m * g.n_heads + h) * cstride * hd + i;
-    float o = 0.0f;
-    uint32_t c = 0;
-    for (; c + 8 <= nch; c += 8) {
-        float v[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = wp[(size_t)(c + u) * hd];
-#pragma unroll
-        for (int u = 0; u < 8; u++) o = o + v[u];
+    const uint32_t nc = (kv_view(g, pd->pos0 + m).count() + 1 + 255) / 256;
+    const size_t mh = (size_t)m * g.n_heads + h;
+    const float* st = S + mh * s_stride;
+    float mx = st[0];
+#pragma unroll 8
+    for (uint32_t c = 1; c < nc; c++) mx = fmaxf(mx, st[2 * c]);
+    const float* up = Up + mh * cstride * hd + (i < hd ? i : 0u);
+    float T = 0.0f, U = 0.0f;
+    for (uint32_t cb = 0; cb < nc; cb += 128) {
+        const uint32_t nb = min(128u, nc - cb);
+        __syncthreads();
+        if (i < nb) {
+            fs[i] = expf_c(st[2 * (cb + i)] - mx);
+            ts[i] = st[2 * (cb + i) + 1];
+        }
+        __syncthreads();
+#pragma unroll 8
+        for (uint32_t k = 0; k < nb; k++) {
+            const float f = fs[k];
+            T = __builtin_fmaf(ts[k], f, T);
+            U = __builtin_fmaf(up[(size_t)(cb + k) * hd], f, U);
+        }
     }
-    for (; c < nch; c++) o = o + wp[(size_t)c * hd];
-    const float ps = S[((size_t)m * g.n_heads + h) * s_stride + C];
-    o = __builtin_fmaf(ps, vself[(size_t)m * D + h * hd + i], o);
-    out[(size_t)m * D + h * hd + i] = o;
+    if (i < hd) out[(size_t)m * D + h * hd + i] = U * (1.0f / (T + 1e-10f));
 }
 
 }  // namespace pf

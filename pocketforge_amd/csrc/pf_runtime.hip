@@ -389,6 +389,19 @@ static int per_for(uint32_t K) {
         case 8: { constexpr int PER = 8; CALL; } break;   \
     }
 
+// head_dim / 16 (1..8; checked at model creation) as a compile-time constant
+#define PF_PARTS_SWITCH(P, CALL)                          \
+    switch (P) {                                          \
+        case 1: { constexpr int PARTS = 1; CALL; } break; \
+        case 2: { constexpr int PARTS = 2; CALL; } break; \
+        case 3: { constexpr int PARTS = 3; CALL; } break; \
+        case 4: { constexpr int PARTS = 4; CALL; } break; \
+        case 5: { constexpr int PARTS = 5; CALL; } break; \
+        case 6: { constexpr int PARTS = 6; CALL; } break; \
+        case 7: { constexpr int PARTS = 7; CALL; } break; \
+        default: { constexpr int PARTS = 8; CALL; } break; \
+    }
+
 extern "C" pf_status pf_quantize_activation_rows(pf_ctx* c, const float* src, int8_t* dst, float* scales,
                                                  uint32_t M, uint32_t K) {
     if (!c || !src || !dst || !scales || M == 0) return PF_ERR_ARG;
@@ -1044,7 +1057,9 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         return fail(c, PF_ERR_CAPACITY, "position beyond the engine's max_context");
     // captured passes replay at any position: grids sized for the largest view
     const uint32_t cmax = e->capturing ? e->s_stride - 8 : kv_view(g, pos0 + M - 1).count();
-    const uint32_t zb = (cmax + 1 + 255) / 256, nch = (cmax + 63) / 64;
+    // attention tasks: (head, 256-entry chunk) groups of M rows, 8-aligned per XCD
+    const uint32_t attn_groups = H * ((cmax + 1 + 255) / 256);
+    const uint32_t attn_blocks = 8 * M * ((attn_groups + 7) / 8);
     const uint32_t ks = e->kmax, bs = e->kmax / 32;
     float* as0 = e->as;           // attention-norm act
     float* as1 = e->as + 8;       // attention output act
@@ -1065,14 +1080,11 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         if (pf_status s = pass_gemv(e, m->qkv[l], M)) return s;
         hipLaunchKernelGGL(k_qkv_post, dim3(M, H), dim3(64), 0, st, e->acc, as0, pd, e->rope_c, e->rope_s, g, e->kv, l,
                            e->q, e->k, e->v);
-        hipLaunchKernelGGL(k_attn_scores, dim3(M, H, zb), dim3(256), 0, st, pd, g, e->kv, l, -1, 0u, -1, e->q, e->k,
-                           e->S, e->s_stride, 1);
-        hipLaunchKernelGGL(k_attn_softmax, dim3(M, H), dim3(256), 0, st, pd, g, -1, 0u, e->S, e->s_stride);
-        if (nch)
-            hipLaunchKernelGGL(k_attn_wsum, dim3(M, H, nch), dim3(128), 0, st, pd, g, e->kv, l, -1, 0u, -1,
-                               0xFFFFFFFFu, e->S, e->s_stride, e->Wp, e->cstride);
-        hipLaunchKernelGGL(k_attn_merge, dim3(M, H), dim3(128), 0, st, pd, g, e->S, e->s_stride, e->Wp, e->cstride,
-                           e->v, e->attn);
+        PF_PARTS_SWITCH(hd / 16, hipLaunchKernelGGL(k_attn_chunk<PARTS>, dim3(attn_blocks), dim3(256), 0, st, pd, g,
+                                                    e->kv, l, M, attn_groups, (const float*)e->q, (const float*)e->k,
+                                                    (const float*)e->v, e->S, e->s_stride, e->Wp, e->cstride));
+        hipLaunchKernelGGL(k_attn_merge_chunks, dim3(M, H), dim3(128), 0, st, pd, g, (const float*)e->S, e->s_stride,
+                           (const float*)e->Wp, e->cstride, e->attn);
         PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_quant_rows_wide<PER>, dim3(M), dim3(1024), 0, st, e->attn, D,
                                                 e->act, ks, as1, e->bsum, bs));
         if (pf_status s = pass_gemv(e, m->o[l], M)) return s;

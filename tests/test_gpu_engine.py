@@ -189,3 +189,39 @@ def test_profiled_generate_matches(gpu, tiny_weights):
     assert n > 0 and us > 0 and by > 0
     e.close()
     m.close()
+
+
+def test_multi_chunk_attention_with_pooling(gpu, tiny_weights):
+    """Lists longer than one 256-entry attention chunk (window 600, pool 8,
+    sink 4): prefill of 900 tokens in passes of 8, then single-row and
+    5-row passes whose lists hold 3 chunks with pooled rows; every row's
+    logits and hidden state bit-exact."""
+    cfg, w = tiny_weights
+    kv = dict(sink_size=4, window_size=600, pool_block=8, max_context=2048)
+    m = pf.Model(gpu, cfg, w)
+    e = pf.Engine(m, **kv)
+    om = _oracle(cfg, w, kv)
+    toks = W.prompt_ids(920, cfg["n_vocab"], seed=21)
+    i = 0
+    for c in [8] * 112 + [1, 5, 3, 1]:
+        lg, hg = e.forward(toks[i:i + c])
+        for j in range(c):
+            lo, ho = om.forward(toks[i + j])
+            if i + j >= 250 and (i + j) % 37 == 0 or i + c > 890:
+                np.testing.assert_array_equal(hg[j], ho, err_msg=f"row {i + j}")
+                np.testing.assert_array_equal(lg[j], lo, err_msg=f"row {i + j}")
+        i += c
+    om.close()
+    e.close()
+    m.close()
+
+
+def test_generate_multi_chunk_matches_oracle(gpu, tiny_weights):
+    """generate() with a 700-token prompt under window 600 / pool 8: MTP
+    rounds over 3-chunk attention lists, token streams identical."""
+    cfg, w = tiny_weights
+    kv = dict(sink_size=4, window_size=600, pool_block=8, max_context=2048)
+    prompt = W.prompt_ids(700, cfg["n_vocab"], seed=13)
+    toks, res, ot, oa, orj = _gen_both(gpu, cfg, w, prompt, 40, GREEDY, kv=kv)
+    np.testing.assert_array_equal(toks, ot)
+    assert (res.mtp_accepted, res.mtp_rejected) == (oa, orj)

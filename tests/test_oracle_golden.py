@@ -279,3 +279,81 @@ def test_mtp_forward_golden_fixture(MT):
     L = O.lib()
     assert L.orc_argmax(P(MT["argmax_x"], O.f32p), 5) == 1
     assert L.orc_argmax(P(MT["argmax_ties_x"], O.f32p), 5) == 1
+
+
+def _attn_f64(L, k, l, h, hd, q, kself, vself, cap):
+    """Softmax-weighted sum over the exported (dequantized) entries plus the
+    self entry, in float64."""
+    K8 = np.zeros((cap, hd), np.int8)
+    Ks = np.zeros(cap, np.float32)
+    V8 = np.zeros((cap, hd), np.int8)
+    Vs = np.zeros(cap, np.float32)
+    n = L.orc_kv_export(k, l, h, P(K8, O.i8p), P(Ks, O.f32p), P(V8, O.i8p), P(Vs, O.f32p))
+    Kd = np.vstack([K8[:n].astype(np.float64) * Ks[:n, None], kself[None].astype(np.float64)])
+    Vd = np.vstack([V8[:n].astype(np.float64) * Vs[:n, None], vself[None].astype(np.float64)])
+    s = Kd @ q.astype(np.float64) / np.sqrt(hd)
+    p = np.exp(s - s.max())
+    return (p / p.sum()) @ Vd, n
+
+
+@pytest.mark.parametrize("n_store,seed", [(40, 1), (450, 2), (1500, 3)])
+def test_engine_attention_chunked_order(n_store, seed):
+    """The engine's per-head attention in the canonical chunked order (chunks
+    of 256 list entries merged with max rescaling) against the reference's
+    order (softmax, sequential weighted sum, self term) and against the
+    float64 closed form, over a cache with sink, pooled and window entries
+    (1, 2 and 3 chunks)."""
+    L = O.lib()
+    hd, sink, win, pool, maxc = 16, 4, 600, 8, 4000
+    k = L.orc_kv_create(1, 2, hd, sink, win, pool, maxc)
+    rng = np.random.default_rng(seed)
+    for pos in range(n_store):
+        for h in range(2):
+            kk = (rng.standard_normal(hd) * 2.0).astype(np.float32)
+            vv = rng.standard_normal(hd).astype(np.float32)
+            L.orc_kv_store(k, 0, h, pos, P(kk, O.f32p), P(vv, O.f32p))
+    for h in range(2):
+        for trial in range(4):
+            q = (rng.standard_normal(hd) * (0.5 + trial)).astype(np.float32)
+            ks = (rng.standard_normal(hd) * 2.0).astype(np.float32)
+            vs = rng.standard_normal(hd).astype(np.float32)
+            out = np.zeros(hd, np.float32)
+            ref = np.zeros(hd, np.float32)
+            L.orc_attn_head(k, 0, h, P(q, O.f32p), P(ks, O.f32p), P(vs, O.f32p), P(out, O.f32p))
+            L.orc_attn_head_ref(k, 0, h, P(q, O.f32p), P(ks, O.f32p), P(vs, O.f32p), P(ref, O.f32p))
+            f64, n = _attn_f64(L, k, 0, h, hd, q, ks, vs, win + maxc // pool + 16)
+            if n_store > 1000:
+                assert n + 1 > 512 and L.orc_kv_pool_count(k, 0, h) > 0
+            tol = 2e-5 * max(1.0, np.abs(f64).max())
+            assert np.abs(out - ref).max() <= tol, (h, trial)
+            assert np.abs(out - f64).max() <= tol, (h, trial)
+    L.orc_kv_destroy(k)
+
+
+def test_engine_attention_special_cases():
+    """Equal scores give the plain mean of the values; a dominant self score
+    gives the self value."""
+    L = O.lib()
+    hd = 16
+    k = L.orc_kv_create(1, 1, hd, 4, 600, 8, 4000)
+    rng = np.random.default_rng(9)
+    vals = []
+    for pos in range(300):
+        vv = rng.standard_normal(hd).astype(np.float32)
+        L.orc_kv_store(k, 0, 0, pos, P(np.zeros(hd, np.float32), O.f32p), P(vv, O.f32p))
+        vals.append(vv)
+    K8 = np.zeros((400, hd), np.int8)
+    Ks = np.zeros(400, np.float32)
+    V8 = np.zeros((400, hd), np.int8)
+    Vs = np.zeros(400, np.float32)
+    n = L.orc_kv_export(k, 0, 0, P(K8, O.i8p), P(Ks, O.f32p), P(V8, O.i8p), P(Vs, O.f32p))
+    vself = rng.standard_normal(hd).astype(np.float32)
+    q = rng.standard_normal(hd).astype(np.float32)
+    out = np.zeros(hd, np.float32)
+    L.orc_attn_head(k, 0, 0, P(q, O.f32p), P(np.zeros(hd, np.float32), O.f32p), P(vself, O.f32p), P(out, O.f32p))
+    mean = (np.vstack([V8[:n].astype(np.float64) * Vs[:n, None], vself[None]])).mean(axis=0)
+    np.testing.assert_allclose(out, mean, rtol=0, atol=1e-5)
+    kself = (q * 200.0).astype(np.float32)
+    L.orc_attn_head(k, 0, 0, P(q, O.f32p), P(kself, O.f32p), P(vself, O.f32p), P(out, O.f32p))
+    np.testing.assert_allclose(out, vself, rtol=1e-6, atol=1e-7)
+    L.orc_kv_destroy(k)
