@@ -271,9 +271,9 @@ __global__ void k_wsum_combine_one(const float* __restrict__ Wp, uint32_t nch, u
     out[i] = o;
 }
 
-// Engine attention, first stage.  Block task (row m, head h, chunk c) covers
-// list entries [256c, 256c + 256) of row m; the list is the C visible
-// entries followed by the fp32 self entry (index C).  Scores as in
+// Engine attention, first stage.  Task (row m, head h, chunk c) covers list
+// entries [256c, 256c + 256) of row m; the list is the C visible entries
+// followed by the fp32 self entry (index C).  Scores as in
 // src/engine.cpp:757-768 (cached entries: sequential fmaf dot of q with
 // (float)k * k_scale; self entry: sequential mul+add dot with the fp32 key;
 // both times 1/sqrt(head_dim)), then the chunk max m_c, e_j = exp(s_j - m_c),
@@ -283,30 +283,28 @@ __global__ void k_wsum_combine_one(const float* __restrict__ Wp, uint32_t nch, u
 // v_scale_j), or of e_j * v_self for the self entry.  Writes
 // S[(m*H + h)*s_stride + 2c] = m_c, [.. + 2c + 1] = T_c and
 // Up[((m*H + h)*cstride + c)*hd + i] = U_c[i].
-//
-// 1-D grid of 8 * M * ceil(G / 8) blocks, G = H * chunks, task group
-// grp = c * H + h.  Blocks are dealt to the 8 XCDs round-robin, so block b
-// runs on XCD b mod 8: group grp's M rows get blocks with b mod 8 = grp mod
-// 8, and after the first row a chunk's K/V rows come from that XCD's L2.
-// 256 threads; head_dim = 16 * PARTS (up to 128).
+
+// Shared memory of one attention block (bytes): V rows of the chunk first.
+constexpr uint32_t ATT_VT = 256 * 144;             // 256 rows, 16 bytes of padding each
+constexpr uint32_t ATT_SMEM = ATT_VT + (128 + 128 + 256 + 256 + 512 + 4) * 4;
+
 template <int PARTS>
-__global__ __launch_bounds__(256) void k_attn_chunk(const PassDesc* __restrict__ pd, KvGeom g, KvPlanes kv,
-                                                    uint32_t layer, uint32_t M, uint32_t n_groups,
-                                                    const float* __restrict__ q, const float* __restrict__ kself,
-                                                    const float* __restrict__ vself, float* __restrict__ S,
-                                                    uint32_t s_stride, float* __restrict__ Up, uint32_t cstride) {
-    __shared__ float qs[128], kss[128];
-    __shared__ __align__(16) int8_t vt[256][144];     // 16 bytes of padding per row
-    __shared__ float vsc[256], pe[256];
-    __shared__ float wp[4][128];
-    __shared__ float red[4];
-    const uint32_t t = threadIdx.x;
-    const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
-    const uint32_t grp = (slot / M) * 8u + xcd, m = slot % M;
-    if (grp >= n_groups || m >= pd->m) return;
+__device__ __forceinline__ void attn_one_row(const PassDesc* __restrict__ pd, const KvGeom& g, const KvPlanes& kv,
+                                             uint32_t layer, uint32_t m, uint32_t h, uint32_t c,
+                                             const float* __restrict__ q, const float* __restrict__ kself,
+                                             const float* __restrict__ vself, float* __restrict__ S,
+                                             uint32_t s_stride, float* __restrict__ Up, uint32_t cstride,
+                                             uint8_t* smem) {
     constexpr uint32_t hd = 16 * PARTS;
+    int8_t (*vt)[144] = reinterpret_cast<int8_t (*)[144]>(smem);
+    float* qs = reinterpret_cast<float*>(smem + ATT_VT);
+    float* kss = qs + 128;
+    float* vsc = kss + 128;
+    float* pe = vsc + 256;
+    float* wp = pe + 256;                           // [4][128]
+    float* red = wp + 512;
+    const uint32_t t = threadIdx.x;
     const uint32_t D = g.n_heads * hd;
-    const uint32_t c = grp / g.n_heads, h = grp % g.n_heads;
     const KvView v = kv_view(g, pd->pos0 + m);
     const uint32_t C = v.count(), n = C + 1, j0 = c * 256u;
     if (j0 >= n) return;
@@ -390,23 +388,42 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const PassDesc* __restrict__
             w0 = __builtin_fmaf(p, vself[qrow + i0], w0);
             w1 = __builtin_fmaf(p, vself[qrow + i0 + 1], w1);
         }
-        wp[sc][i0] = w0;
-        wp[sc][i0 + 1] = w1;
+        wp[sc * 128 + i0] = w0;
+        wp[sc * 128 + i0 + 1] = w1;
     }
     __syncthreads();
     const size_t mh = (size_t)m * g.n_heads + h;
     if (t < hd) {
         float u = 0.0f;
-        u = u + wp[0][t];
-        u = u + wp[1][t];
-        u = u + wp[2][t];
-        u = u + wp[3][t];
+        u = u + wp[t];
+        u = u + wp[128 + t];
+        u = u + wp[256 + t];
+        u = u + wp[384 + t];
         Up[(mh * cstride + c) * hd + t] = u;
     }
     if (t == 0) {
         S[mh * s_stride + 2 * c] = mx;
         S[mh * s_stride + 2 * c + 1] = T;
     }
+}
+
+// 1-D grid of 8 * M * ceil(G / 8) blocks, G = H * chunks, task group
+// grp = c * H + h.  Blocks are dealt to the 8 XCDs round-robin, so block b
+// runs on XCD b mod 8: group grp's M rows get blocks with b mod 8 = grp mod
+// 8, and after the first row a chunk's K/V rows come from that XCD's L2.
+// 256 threads; head_dim = 16 * PARTS.
+template <int PARTS>
+__global__ __launch_bounds__(256) void k_attn_chunk(const PassDesc* __restrict__ pd, KvGeom g, KvPlanes kv,
+                                                    uint32_t layer, uint32_t M, uint32_t n_groups,
+                                                    const float* __restrict__ q, const float* __restrict__ kself,
+                                                    const float* __restrict__ vself, float* __restrict__ S,
+                                                    uint32_t s_stride, float* __restrict__ Up, uint32_t cstride) {
+    __shared__ __align__(16) uint8_t smem[ATT_SMEM];
+    const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
+    const uint32_t grp = (slot / M) * 8u + xcd, m = slot % M;
+    if (grp >= n_groups || m >= pd->m) return;
+    attn_one_row<PARTS>(pd, g, kv, layer, m, grp % g.n_heads, grp / g.n_heads, q, kself, vself, S, s_stride, Up,
+                        cstride, smem);
 }
 
 // Engine attention, second stage: the chunks of (row m, head h) merged left

@@ -389,18 +389,17 @@ static int per_for(uint32_t K) {
         case 8: { constexpr int PER = 8; CALL; } break;   \
     }
 
-// head_dim / 16 (1..8; checked at model creation) as a compile-time constant
-#define PF_PARTS_SWITCH(P, CALL)                          \
-    switch (P) {                                          \
-        case 1: { constexpr int PARTS = 1; CALL; } break; \
-        case 2: { constexpr int PARTS = 2; CALL; } break; \
-        case 3: { constexpr int PARTS = 3; CALL; } break; \
-        case 4: { constexpr int PARTS = 4; CALL; } break; \
-        case 5: { constexpr int PARTS = 5; CALL; } break; \
-        case 6: { constexpr int PARTS = 6; CALL; } break; \
-        case 7: { constexpr int PARTS = 7; CALL; } break; \
-        default: { constexpr int PARTS = 8; CALL; } break; \
-    }
+// Engine attention launch (head_dim 64 or 128, checked at model creation).
+static void launch_attn(hipStream_t st, uint32_t hd, uint32_t M, uint32_t blocks, const PassDesc* pd,
+                        const KvGeom& g, const KvPlanes& kv, uint32_t l, uint32_t groups, const float* q,
+                        const float* k, const float* v, float* S, uint32_t s_stride, float* Wp, uint32_t cstride) {
+    if (hd == 64)
+        hipLaunchKernelGGL(k_attn_chunk<4>, dim3(blocks), dim3(256), 0, st, pd, g, kv, l, M, groups, q, k, v, S,
+                           s_stride, Wp, cstride);
+    else
+        hipLaunchKernelGGL(k_attn_chunk<8>, dim3(blocks), dim3(256), 0, st, pd, g, kv, l, M, groups, q, k, v, S,
+                           s_stride, Wp, cstride);
+}
 
 extern "C" pf_status pf_quantize_activation_rows(pf_ctx* c, const float* src, int8_t* dst, float* scales,
                                                  uint32_t M, uint32_t K) {
@@ -689,7 +688,7 @@ extern "C" pf_status pf_model_create(pf_ctx* c, const pf_model_desc* d, pf_model
     if (d->n_embd % 256 || d->n_ff % 256 || d->n_vocab % 64 || d->n_embd > 2048 || d->n_ff > 8192)
         return fail(c, PF_ERR_UNSUPPORTED, "n_embd and n_ff must be multiples of 256 (n_embd <= 2048, n_ff <= 8192), "
                                            "n_vocab a multiple of 64");
-    if (d->head_dim % 16 || d->head_dim > 128) return fail(c, PF_ERR_UNSUPPORTED, "head_dim must be 16..128, multiple of 16");
+    if (d->head_dim != 64 && d->head_dim != 128) return fail(c, PF_ERR_UNSUPPORTED, "head_dim must be 64 or 128");
     if (d->n_mtp + 1 > MAX_PASS_ROWS) return fail(c, PF_ERR_UNSUPPORTED, "at most 7 MTP heads");
     if (d->n_vocab > SAMPLE_MAX_V) return fail(c, PF_ERR_UNSUPPORTED, "n_vocab > 16384");
     pf_model* m = new pf_model();
@@ -1080,9 +1079,8 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         if (pf_status s = pass_gemv(e, m->qkv[l], M)) return s;
         hipLaunchKernelGGL(k_qkv_post, dim3(M, H), dim3(64), 0, st, e->acc, as0, pd, e->rope_c, e->rope_s, g, e->kv, l,
                            e->q, e->k, e->v);
-        PF_PARTS_SWITCH(hd / 16, hipLaunchKernelGGL(k_attn_chunk<PARTS>, dim3(attn_blocks), dim3(256), 0, st, pd, g,
-                                                    e->kv, l, M, attn_groups, (const float*)e->q, (const float*)e->k,
-                                                    (const float*)e->v, e->S, e->s_stride, e->Wp, e->cstride));
+        launch_attn(st, hd, M, attn_blocks, pd, g, e->kv, l, attn_groups, e->q, e->k, e->v, e->S, e->s_stride,
+                    e->Wp, e->cstride);
         hipLaunchKernelGGL(k_attn_merge_chunks, dim3(M, H), dim3(128), 0, st, pd, g, (const float*)e->S, e->s_stride,
                            (const float*)e->Wp, e->cstride, e->attn);
         PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_quant_rows_wide<PER>, dim3(M), dim3(1024), 0, st, e->attn, D,
