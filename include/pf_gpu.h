@@ -112,6 +112,30 @@ pf_status pf_gemv_q(pf_ctx* ctx, const pf_matrix* W, const float* x_dev, float* 
 /* y[M][rows] = fp32 x[m] . dequantized W rows (row-major Q4 matrices). */
 pf_status pf_gemv_f32(pf_ctx* ctx, const pf_matrix* W, const float* x_dev, float* y_dev, uint32_t M);
 
+/* dot_product, softmax, rmsnorm (include/forge/matmul_neon.hpp:79-92) on
+ * device buffers, in the canonical orders (CANON(4) sums); *out_dev is one
+ * float.  MTPHeads::argmax (include/forge/mtp.hpp:49): first index of the
+ * maximum of n floats, written to *out_dev. */
+pf_status pf_dot_product(pf_ctx* ctx, const float* a_dev, const float* b_dev, uint32_t n, float* out_dev);
+pf_status pf_softmax(pf_ctx* ctx, float* vals_dev, uint32_t n);
+pf_status pf_rmsnorm(pf_ctx* ctx, float* out_dev, const float* x_dev, const float* w_dev, uint32_t n);
+pf_status pf_argmax(pf_ctx* ctx, const float* x_dev, uint32_t n, int32_t* out_dev);
+
+/* --------------------------------------------- mtp.hpp (standalone heads) */
+/* MTPHeads (include/forge/mtp.hpp:31-53) outside an engine: n_heads chained
+ * heads of n_embd x n_embd Q4 gate/up/down (n_embd a multiple of 256, up to
+ * 2048), unembedded with an fp32 tied table [n_vocab][n_embd] given by the
+ * caller (pf_mtp_set_table, host pointer, copied to HBM; NULL removes it).
+ * Without a table, forward writes the reference's placeholder logits
+ * (src/mtp.cpp:117-121).  hidden/logits are host pointers. */
+typedef struct pf_mtp pf_mtp;
+pf_status pf_mtp_create(pf_ctx* ctx, uint32_t n_heads, uint32_t n_embd, uint32_t n_vocab, pf_mtp** out);
+void pf_mtp_destroy(pf_mtp* m);
+pf_status pf_mtp_set_head(pf_mtp* m, uint32_t head, int32_t which, const uint8_t* codes, const uint16_t* scales);
+pf_status pf_mtp_set_table(pf_mtp* m, const float* table);
+pf_status pf_mtp_heads_forward(pf_mtp* m, const float* hidden, float* logits);
+size_t pf_mtp_memory(const pf_mtp* m);
+
 /* ----------------------------------------------- kv_cache.hpp (3-tier) */
 typedef struct {
     uint32_t n_layers, n_kv_heads, head_dim;
@@ -197,6 +221,9 @@ pf_status pf_sample(pf_engine* e, const float* logits, const pf_sampling* cfg, u
 pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n_prompt, uint32_t max_new_tokens,
                       const pf_sampling* cfg, uint64_t seed, int32_t* tokens_out, uint32_t tokens_cap,
                       pf_gen_result* result);
+/* Engine::set_mtp_enabled (engine.hpp:23): with 0, generate runs the
+ * single-token loop only (src/engine.cpp:304, 367-386). */
+pf_status pf_engine_set_mtp_enabled(pf_engine* e, int32_t enabled);
 /* Engine::set_max_memory (engine.hpp:25): generate stops with
  * oom_protected when the context's device bytes exceed this (0 = off). */
 pf_status pf_engine_set_max_memory(pf_engine* e, size_t bytes);

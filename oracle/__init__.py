@@ -77,6 +77,13 @@ def lib():
         L.orc_f32_to_f16.restype = C.c_uint16
         L.orc_f32_to_f16.argtypes = [C.c_float]
         L.orc_dot_product.restype = C.c_float
+        L.orc_dot_product.argtypes = [f32p, f32p, C.c_uint32]
+        L.orc_dot_canon.restype = C.c_float
+        L.orc_dot_canon.argtypes = [f32p, f32p, C.c_uint32]
+        L.orc_softmax.argtypes = [f32p, C.c_uint32]
+        L.orc_rmsnorm.argtypes = [f32p, f32p, f32p, C.c_uint32]
+        L.orc_gemv_f32_dense.argtypes = [f32p, C.c_uint32, C.c_uint32, f32p, f32p]
+        L.orc_mtp_heads_forward.argtypes = [C.POINTER(QMat), C.c_uint32, C.c_uint32, C.c_uint32, f32p, f32p, f32p]
         L.orc_canon_sum.restype = C.c_float
         L.orc_canon_sumsq.restype = C.c_float
         L.orc_canon_sum.argtypes = [f32p, C.c_uint32, C.c_uint32]
@@ -191,6 +198,25 @@ def gemv_f32(fmt, codes, scales, h):
     h = np.ascontiguousarray(h, np.float32)
     lib().orc_gemv_f32(C.byref(q), ptr(h, f32p), ptr(y, f32p))
     return y
+
+
+def mtp_heads_forward(heads, d, V, table, hidden):
+    """heads: list of n (gate, up, down) triples of (fmt, codes, scales);
+    table: fp32 [V][d] or None.  Returns logits [n][V]."""
+    n = len(heads)
+    arr = (QMat * (3 * n))()
+    keep = []
+    for k, trip in enumerate(heads):
+        for w, (fmt, codes, scales) in enumerate(trip):
+            q = qmat(fmt, codes, scales)
+            keep.append(q)
+            arr[3 * k + w] = q
+    out = np.zeros((n, V), np.float32)
+    t = None if table is None else np.ascontiguousarray(table, np.float32)
+    h = np.ascontiguousarray(hidden, np.float32)
+    lib().orc_mtp_heads_forward(arr, n, d, V, ptr(t, f32p) if t is not None else None, ptr(h, f32p),
+                                ptr(out, f32p))
+    return out
 
 
 def quantize_activation_row(x):

@@ -455,6 +455,36 @@ void orc_gemv_f32(const orc_qmat* W, const float* h, float* y) {
     }
 }
 
+/* y[n] = canonical fp32 dot of h with row n of a dense fp32 matrix
+ * E [rows][cols]: the order of orc_gemv_f32 with the weight itself. */
+void orc_gemv_f32_dense(const float* E, uint32_t rows, uint32_t cols, const float* h, float* y) {
+    uint32_t nb = cols / 32;
+#pragma omp parallel for schedule(static)
+    for (int64_t n = 0; n < (int64_t)rows; n++) {
+        float P[64];
+        for (int l = 0; l < 64; l++) P[l] = 0.0f;
+        for (uint32_t b = 0; b < nb; b++) {
+            const float* w = E + (size_t)n * cols + 32 * b;
+            float acc = P[b % 64];
+            for (uint32_t i = 0; i < 32; i++) acc = fmaf(h[32 * b + i], w[i], acc);
+            P[b % 64] = acc;
+        }
+        y[n] = canon_tree(P, 1);
+    }
+}
+
+/* dot_product (src/matmul_neon.cpp:186-207) in the CANON(4) order: lane l
+ * of 256 sums a[j] * b[j] (product, then add) for j = l, l + 256, ... */
+float orc_dot_canon(const float* a, const float* b, uint32_t n) {
+    float P[256];
+    for (uint32_t l = 0; l < 256; l++) {
+        float p = 0.0f;
+        for (uint32_t j = l; j < n; j += 256) p = p + a[j] * b[j];
+        P[l] = p;
+    }
+    return canon_tree(P, 4);
+}
+
 /* ================================================ src/kv_cache.cpp */
 
 typedef struct {
@@ -937,6 +967,37 @@ void orc_mtp_forward(orc_engine* e, const float* hidden, float* logits) {
         orc_gemv_f32(&M[2], a, dn);
         for (uint32_t i = 0; i < D; i++) cur[i] += dn[i];  /* src/mtp.cpp:105-107 */
         orc_gemv_f32(d->emb, cur, logits + (size_t)k * d->n_vocab);
+    }
+    free(cur); free(g); free(u); free(a); free(dn);
+}
+
+/* MTPHeads::forward (src/mtp.cpp:47-129) of n_heads chained heads (each
+ * gate, up, down: d x d block-quantized, fp32 activations in the canonical
+ * order) with an fp32 tied table [V][d], or the placeholder logits
+ * ((v * 2654435761 + head) mod V) / V when table is NULL (src/mtp.cpp:117-121). */
+void orc_mtp_heads_forward(const orc_qmat* heads, uint32_t n_heads, uint32_t d, uint32_t V,
+                           const float* table, const float* hidden, float* logits) {
+    float* cur = (float*)malloc(sizeof(float) * d);
+    float* g = (float*)malloc(sizeof(float) * d);
+    float* u = (float*)malloc(sizeof(float) * d);
+    float* a = (float*)malloc(sizeof(float) * d);
+    float* dn = (float*)malloc(sizeof(float) * d);
+    memcpy(cur, hidden, sizeof(float) * d);
+    for (uint32_t k = 0; k < n_heads; k++) {
+        const orc_qmat* M = heads + (size_t)k * 3;
+        orc_gemv_f32(&M[0], cur, g);
+        orc_gemv_f32(&M[1], cur, u);
+        for (uint32_t j = 0; j < d; j++) {
+            float sg = g[j] / (1.0f + orc_expf(-g[j]));
+            a[j] = sg * u[j];
+        }
+        orc_gemv_f32(&M[2], a, dn);
+        for (uint32_t i = 0; i < d; i++) cur[i] += dn[i];
+        float* lk = logits + (size_t)k * V;
+        if (table) orc_gemv_f32_dense(table, V, d, cur, lk);
+        else
+            for (uint32_t v = 0; v < V; v++)
+                lk[v] = (float)(((uint64_t)v * 2654435761ULL + (uint64_t)k) % V) / (float)V;
     }
     free(cur); free(g); free(u); free(a); free(dn);
 }

@@ -46,6 +46,7 @@ void  orc_rmsnorm_ref(float* out, const float* x, const float* w, uint32_t n);
 float orc_canon_sum(const float* x, uint32_t n, uint32_t waves);
 float orc_canon_sumsq(const float* x, uint32_t n, uint32_t waves);
 void  orc_softmax(float* v, uint32_t n);                     /* canonical, own exp */
+float orc_dot_canon(const float* a, const float* b, uint32_t n);  /* CANON(4) of products */
 void  orc_rmsnorm(float* out, const float* x, const float* w, uint32_t n);
 
 /* ------------------------------------------------- block-quant matrices */
@@ -66,6 +67,11 @@ int   orc_block_code(const orc_qmat* W, uint32_t row, uint32_t col);
 void  orc_gemv_i8(const orc_qmat* W, const int8_t* a, float a_scale, float* y);
 void  orc_gemv_f32(const orc_qmat* W, const float* h, float* y);
 void  orc_dequant_row(const orc_qmat* W, uint32_t row, float* out);
+void  orc_gemv_f32_dense(const float* E, uint32_t rows, uint32_t cols, const float* h, float* y);
+/* MTPHeads::forward with n_heads chained heads ([n_heads][3] gate/up/down)
+ * and an fp32 tied table [V][d] (NULL: placeholder logits). */
+void  orc_mtp_heads_forward(const orc_qmat* heads, uint32_t n_heads, uint32_t d, uint32_t V,
+                            const float* table, const float* hidden, float* logits);
 
 /* --------------------------------------------- src/kv_cache.cpp (3-tier) */
 typedef struct orc_kv orc_kv;

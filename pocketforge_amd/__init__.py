@@ -75,6 +75,16 @@ SYMBOLS = {
     "pf_matrix_free": (None, [vp]),
     "pf_gemv_q": (C.c_int32, [vp, vp, vp, vp, C.c_uint32]),
     "pf_gemv_f32": (C.c_int32, [vp, vp, vp, vp, C.c_uint32]),
+    "pf_dot_product": (C.c_int32, [vp, vp, vp, C.c_uint32, vp]),
+    "pf_softmax": (C.c_int32, [vp, vp, C.c_uint32]),
+    "pf_rmsnorm": (C.c_int32, [vp, vp, vp, vp, C.c_uint32]),
+    "pf_argmax": (C.c_int32, [vp, vp, C.c_uint32, vp]),
+    "pf_mtp_create": (C.c_int32, [vp, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(vp)]),
+    "pf_mtp_destroy": (None, [vp]),
+    "pf_mtp_set_head": (C.c_int32, [vp, C.c_uint32, C.c_int32, u8p, u16p]),
+    "pf_mtp_set_table": (C.c_int32, [vp, f32p]),
+    "pf_mtp_heads_forward": (C.c_int32, [vp, f32p, f32p]),
+    "pf_mtp_memory": (C.c_size_t, [vp]),
     "pf_kv_create": (C.c_int32, [vp, C.POINTER(KvConfig), C.POINTER(vp)]),
     "pf_kv_destroy": (None, [vp]),
     "pf_kv_store": (C.c_int32, [vp, C.c_uint32, C.c_uint32, C.c_uint32, f32p, f32p]),
@@ -99,6 +109,7 @@ SYMBOLS = {
     "pf_generate": (C.c_int32, [vp, i32p, C.c_uint32, C.c_uint32, C.POINTER(Sampling), C.c_uint64, i32p,
                                 C.c_uint32, C.POINTER(GenResult)]),
     "pf_engine_set_max_memory": (C.c_int32, [vp, C.c_size_t]),
+    "pf_engine_set_mtp_enabled": (C.c_int32, [vp, C.c_int32]),
     "pf_engine_pass_times": (C.c_int32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double), u32p, u32p]),
     "pf_engine_profile": (C.c_int32, [vp, C.c_int32]),
     "pf_engine_round_time": (C.c_int32, [vp, C.POINTER(C.c_double), u32p]),
@@ -263,6 +274,27 @@ class Context:
         self.synchronize()
         return Cm
 
+    def dot_product(self, a, b):
+        out = self.empty((1,), np.float32)
+        self.check(lib().pf_dot_product(self.h, _dptr(a), _dptr(b), a.shape[0], _dptr(out)), "pf_dot_product")
+        return float(out.numpy()[0])
+
+    def softmax(self, v):
+        """In place on a DeviceArray of floats."""
+        self.check(lib().pf_softmax(self.h, _dptr(v), v.shape[0]), "pf_softmax")
+        self.synchronize()
+
+    def rmsnorm(self, x, w):
+        out = self.empty(x.shape, np.float32)
+        self.check(lib().pf_rmsnorm(self.h, _dptr(out), _dptr(x), _dptr(w), x.shape[0]), "pf_rmsnorm")
+        self.synchronize()
+        return out
+
+    def argmax(self, x):
+        out = self.empty((1,), np.int32)
+        self.check(lib().pf_argmax(self.h, _dptr(x), x.shape[0], _dptr(out)), "pf_argmax")
+        return int(out.numpy()[0])
+
     def upload_matrix(self, fmt, codes, scales, rowmajor=False):
         return Matrix(self, fmt, codes, scales, rowmajor)
 
@@ -295,6 +327,45 @@ class Matrix:
     def close(self):
         if self.h:
             lib().pf_matrix_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+
+class MTPHeads:
+    """include/forge/mtp.hpp:31-53 on the GPU: n chained heads of n_embd x
+    n_embd Q4 gate/up/down, unembedded with an fp32 tied table (or the
+    placeholder logits when none is set)."""
+
+    def __init__(self, ctx, n_heads, n_embd, n_vocab):
+        self.ctx = ctx
+        self.n_heads, self.n_embd, self.n_vocab = n_heads, n_embd, n_vocab
+        self.h = vp()
+        ctx.check(lib().pf_mtp_create(ctx.h, n_heads, n_embd, n_vocab, C.byref(self.h)), "pf_mtp_create")
+
+    def set_head(self, head, which, codes, scales):
+        codes = np.ascontiguousarray(codes, np.uint8)
+        scales = np.ascontiguousarray(scales, np.uint16)
+        self.ctx.check(lib().pf_mtp_set_head(self.h, head, which, P(codes, u8p), P(scales, u16p)),
+                       "pf_mtp_set_head")
+
+    def set_table(self, table):
+        t = None if table is None else np.ascontiguousarray(table, np.float32)
+        self.ctx.check(lib().pf_mtp_set_table(self.h, P(t, f32p) if t is not None else None), "pf_mtp_set_table")
+
+    def forward(self, hidden):
+        hidden = np.ascontiguousarray(hidden, np.float32)
+        out = np.zeros((self.n_heads, self.n_vocab), np.float32)
+        self.ctx.check(lib().pf_mtp_heads_forward(self.h, P(hidden, f32p), P(out, f32p)), "pf_mtp_heads_forward")
+        return out
+
+    def memory_usage(self):
+        return lib().pf_mtp_memory(self.h)
+
+    def close(self):
+        if self.h:
+            lib().pf_mtp_destroy(self.h)
             self.h = None
 
     def __del__(self):
@@ -448,6 +519,9 @@ class Engine:
 
     def set_max_memory(self, nbytes):
         self.ctx.check(lib().pf_engine_set_max_memory(self.h, nbytes), "pf_engine_set_max_memory")
+
+    def set_mtp_enabled(self, enabled):
+        self.ctx.check(lib().pf_engine_set_mtp_enabled(self.h, int(enabled)), "pf_engine_set_mtp_enabled")
 
     def pass_times(self):
         v, b = C.c_double(0), C.c_double(0)

@@ -46,6 +46,46 @@ def _compile(unit):
     return obj
 
 
+HOST = os.path.join(HERE, "host")
+FORGE_LIB = os.path.join(LIBDIR, "libforge_amd.so")
+CPP_TESTS = os.path.join(ROOT, "tests", "cpp")
+TEST_BIN = os.path.join(LIBDIR, "tests")
+ORACLE_BUILD = os.path.join(ROOT, "oracle", "_build")
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+
+
+def build_forge():
+    """libforge_amd.so: the forge:: C++ classes over the C ABI (g++ only)."""
+    tmp = FORGE_LIB + ".tmp"
+    _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-I" + os.path.join(ROOT, "include"),
+          os.path.join(HOST, "forge_api.cpp"), "-o", tmp, "-L" + LIBDIR, "-lpocketforge_amd",
+          "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, FORGE_LIB)
+    return FORGE_LIB
+
+
+def build_cpp_tests():
+    """The forge:: C++ tests, linked against libforge_amd.so and the oracle
+    (their checker).  Binaries go to _lib/tests/."""
+    os.makedirs(TEST_BIN, exist_ok=True)
+    out = []
+    for f in sorted(os.listdir(CPP_TESTS)):
+        if not f.endswith(".cpp"):
+            continue
+        exe = os.path.join(TEST_BIN, f[:-4])
+        _run(["g++", "-O2", "-std=c++17", "-I" + os.path.join(ROOT, "include"), "-I" + CPP_TESTS,
+              "-I" + os.path.join(ROOT, "oracle"), os.path.join(CPP_TESTS, f), "-o", exe,
+              "-L" + LIBDIR, "-lforge_amd", "-lpocketforge_amd", "-L" + ORACLE_BUILD, "-loracle",
+              "-Wl,-rpath,$ORIGIN/..", "-Wl,-rpath,$ORIGIN/../../../oracle/_build"])
+        out.append(exe)
+    return out
+
+
 def build(jobs=4, verbose=False):
     os.makedirs(BUILD, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
@@ -57,8 +97,11 @@ def build(jobs=4, verbose=False):
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    build_forge()
+    if os.path.exists(os.path.join(ORACLE_BUILD, "liboracle.so")):
+        build_cpp_tests()
     if verbose:
-        print("built", LIB)
+        print("built", LIB, FORGE_LIB)
     return LIB
 
 

@@ -46,6 +46,14 @@ __device__ ArgBest block_argmax(const float* __restrict__ x, uint32_t V) {
     return b;
 }
 
+// MTPHeads::argmax (src/mtp.cpp:145-155) of one row: first index of the
+// maximum.  One block of 1024 threads.
+__global__ __launch_bounds__(1024) void k_argmax_one(const float* __restrict__ x, uint32_t n,
+                                                     int32_t* __restrict__ out) {
+    ArgBest b = block_argmax(x, n);
+    if (threadIdx.x == 0) *out = b.i;
+}
+
 // row_argmax[m] for every row of a pass.  Grid M, 1024 threads.
 __global__ __launch_bounds__(1024) void k_argmax_rows(const float* __restrict__ logits, uint32_t stride,
                                                       uint32_t V, const PassDesc* __restrict__ pd,

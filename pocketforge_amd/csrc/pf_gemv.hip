@@ -187,6 +187,100 @@ __global__ __launch_bounds__(256) void k_gemv_f32(const uint8_t* __restrict__ co
     }
 }
 
+// y[m][n] = canonical fp32 dot of h[m] with row n of a dense fp32 matrix E
+// [N][K] (an fp32 tied table handed to MTPHeads::forward): the order of
+// k_gemv_f32 with the weight value itself (lane l = block l, K <= 2048).
+template <int M>
+__global__ __launch_bounds__(256) void k_gemv_f32_dense(const float* __restrict__ E, uint32_t N, uint32_t K,
+                                                        const float* __restrict__ h, uint32_t h_stride,
+                                                        float* __restrict__ y, uint32_t y_stride) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
+    const bool live = lane < (K >> 5);
+    float hv[M][32];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+            float4 v = live ? *reinterpret_cast<const float4*>(h + (size_t)m * h_stride + lane * 32u + i)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+            hv[m][i] = v.x; hv[m][i + 1] = v.y; hv[m][i + 2] = v.z; hv[m][i + 3] = v.w;
+        }
+    }
+    for (uint32_t n = wave; n < N; n += nwaves) {
+        float acc[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) acc[m] = 0.0f;
+        if (live) {
+            const float* row = E + (size_t)n * K + lane * 32u;
+            float w[32];
+#pragma unroll
+            for (int i = 0; i < 32; i += 4) {
+                float4 v = *reinterpret_cast<const float4*>(row + i);
+                w[i] = v.x; w[i + 1] = v.y; w[i + 2] = v.z; w[i + 3] = v.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 32; i++)
+#pragma unroll
+                for (int m = 0; m < M; m++) acc[m] = __builtin_fmaf(hv[m][i], w[i], acc[m]);
+        }
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            float t = wave_tree_sum(acc[m]);
+            if (lane == 0) y[(size_t)m * y_stride + n] = t;
+        }
+    }
+}
+
+// MTPHeads::forward without a tied table (src/mtp.cpp:117-121): logits[v] =
+// ((v * 2654435761 + head) mod V) / V.
+__global__ void k_mtp_placeholder(float* __restrict__ logits, uint32_t V, uint32_t head) {
+    const uint32_t v = blockIdx.x * blockDim.x + threadIdx.x;
+    if (v >= V) return;
+    logits[v] = (float)(((uint64_t)v * 2654435761ULL + (uint64_t)head) % V) / (float)V;
+}
+
+// dot_product (src/matmul_neon.cpp:186-207) in the CANON(4) order: lane l of
+// 256 sums a[j] * b[j] (product, then add) for j = l, l + 256, ...
+__global__ __launch_bounds__(256) void k_dot_canon(const float* __restrict__ a, const float* __restrict__ b,
+                                                   uint32_t n, float* __restrict__ out) {
+    __shared__ float red[4];
+    float p = 0.0f;
+    for (uint32_t j = threadIdx.x; j < n; j += 256) p = p + a[j] * b[j];
+    const float s = block_canon_sum<4>(p, red);
+    if (threadIdx.x == 0) *out = s;
+}
+
+// softmax in place (src/matmul_neon.cpp:212-226): max, e = exp(x - max),
+// CANON(4) sum, x = e * (1 / (sum + 1e-10)).
+__global__ __launch_bounds__(256) void k_softmax_one(float* __restrict__ v, uint32_t n) {
+    __shared__ float red[4];
+    float mx = -__builtin_inff();
+    for (uint32_t j = threadIdx.x; j < n; j += 256) mx = fmaxf(mx, v[j]);
+    mx = block_max<4>(mx, red);
+    float part = 0.0f;
+    for (uint32_t j = threadIdx.x; j < n; j += 256) {
+        const float e = expf_c(v[j] - mx);
+        v[j] = e;
+        part = part + e;
+    }
+    const float inv = 1.0f / (block_canon_sum<4>(part, red) + 1e-10f);
+    for (uint32_t j = threadIdx.x; j < n; j += 256) v[j] = v[j] * inv;
+}
+
+// rmsnorm (src/matmul_neon.cpp:231-239): CANON(4) sum of squares (fmaf),
+// rms = sqrt(ss / n + 1e-6), out = x * (1 / rms) * w.
+__global__ __launch_bounds__(256) void k_rmsnorm_one(float* __restrict__ out, const float* __restrict__ x,
+                                                     const float* __restrict__ w, uint32_t n) {
+    __shared__ float red[4];
+    float p = 0.0f;
+    for (uint32_t j = threadIdx.x; j < n; j += 256) p = __builtin_fmaf(x[j], x[j], p);
+    const float ss = block_canon_sum<4>(p, red);
+    const float inv = 1.0f / __builtin_sqrtf(ss / (float)n + 1e-6f);
+    for (uint32_t j = threadIdx.x; j < n; j += 256) out[j] = x[j] * inv * w[j];
+}
+
 // ============================================================ prologues
 
 template <int PER>

@@ -478,6 +478,138 @@ extern "C" pf_status pf_gemv_f32(pf_ctx* c, const pf_matrix* W, const float* x, 
     return PF_OK;
 }
 
+// dot_product / softmax / rmsnorm / argmax of include/forge/matmul_neon.hpp
+// and src/mtp.cpp on device buffers.
+extern "C" pf_status pf_dot_product(pf_ctx* c, const float* a, const float* b, uint32_t n, float* out) {
+    if (!c || !a || !b || !out) return PF_ERR_ARG;
+    hipLaunchKernelGGL(k_dot_canon, dim3(1), dim3(256), 0, c->stream, a, b, n, out);
+    PF_LAUNCHED(c);
+    return PF_OK;
+}
+
+extern "C" pf_status pf_softmax(pf_ctx* c, float* v, uint32_t n) {
+    if (!c || !v || n == 0) return PF_ERR_ARG;
+    hipLaunchKernelGGL(k_softmax_one, dim3(1), dim3(256), 0, c->stream, v, n);
+    PF_LAUNCHED(c);
+    return PF_OK;
+}
+
+extern "C" pf_status pf_rmsnorm(pf_ctx* c, float* out, const float* x, const float* w, uint32_t n) {
+    if (!c || !out || !x || !w || n == 0) return PF_ERR_ARG;
+    hipLaunchKernelGGL(k_rmsnorm_one, dim3(1), dim3(256), 0, c->stream, out, x, w, n);
+    PF_LAUNCHED(c);
+    return PF_OK;
+}
+
+extern "C" pf_status pf_argmax(pf_ctx* c, const float* x, uint32_t n, int32_t* out) {
+    if (!c || !x || !out || n == 0) return PF_ERR_ARG;
+    hipLaunchKernelGGL(k_argmax_one, dim3(1), dim3(1024), 0, c->stream, x, n, out);
+    PF_LAUNCHED(c);
+    return PF_OK;
+}
+
+// ============================================================ MTP heads
+// A standalone MTPHeads (include/forge/mtp.hpp:31-53): its own head
+// matrices and, optionally, an fp32 tied table handed in by the caller.
+
+struct pf_mtp {
+    pf_ctx* c = nullptr;
+    uint32_t H = 0, D = 0, V = 0;
+    std::vector<pf_matrix*> mats;     // [H][3]: gate, up, down (row-major Q4)
+    float* table = nullptr;           // [V][D] fp32, or null
+    float *cur = nullptr, *g = nullptr, *u = nullptr, *a = nullptr, *logits = nullptr;
+};
+
+extern "C" void pf_mtp_destroy(pf_mtp* m) {
+    if (!m) return;
+    pf_ctx* c = m->c;
+    (void)hipStreamSynchronize(c->stream);
+    for (pf_matrix* M : m->mats) pf_matrix_free(M);
+    dfree(c, m->table, (size_t)m->V * m->D * 4);
+    dfree(c, m->cur, (size_t)m->D * 4);
+    dfree(c, m->g, (size_t)m->D * 4);
+    dfree(c, m->u, (size_t)m->D * 4);
+    dfree(c, m->a, (size_t)m->D * 4);
+    dfree(c, m->logits, (size_t)m->H * m->V * 4);
+    delete m;
+}
+
+extern "C" pf_status pf_mtp_create(pf_ctx* c, uint32_t n_heads, uint32_t n_embd, uint32_t n_vocab, pf_mtp** out) {
+    if (!c || !out || n_heads == 0 || n_vocab == 0) return PF_ERR_ARG;
+    *out = nullptr;
+    if (n_embd % 256 || n_embd == 0 || n_embd > 2048)
+        return fail(c, PF_ERR_UNSUPPORTED, "MTP heads need n_embd a multiple of 256 up to 2048");
+    pf_mtp* m = new pf_mtp();
+    m->c = c; m->H = n_heads; m->D = n_embd; m->V = n_vocab;
+    m->mats.assign((size_t)n_heads * 3, nullptr);
+    pf_status s = PF_OK;
+    for (uint32_t i = 0; i < n_heads * 3 && !s; i++) s = matrix_alloc(c, FMT_Q4, n_embd, n_embd, true, &m->mats[i]);
+    if (!s) s = dalloc_t(c, &m->cur, n_embd);
+    if (!s) s = dalloc_t(c, &m->g, n_embd);
+    if (!s) s = dalloc_t(c, &m->u, n_embd);
+    if (!s) s = dalloc_t(c, &m->a, n_embd);
+    if (!s) s = dalloc_t(c, &m->logits, (size_t)n_heads * n_vocab);
+    if (s) { pf_mtp_destroy(m); return s; }
+    *out = m;
+    return PF_OK;
+}
+
+extern "C" pf_status pf_mtp_set_head(pf_mtp* m, uint32_t head, int32_t which, const uint8_t* codes,
+                                     const uint16_t* scales) {
+    if (!m || !codes || !scales || head >= m->H || which < 0 || which > 2) return PF_ERR_ARG;
+    return matrix_put(m->mats[(size_t)head * 3 + which], 0, m->D, codes, scales);
+}
+
+extern "C" pf_status pf_mtp_set_table(pf_mtp* m, const float* table) {
+    if (!m) return PF_ERR_ARG;
+    pf_ctx* c = m->c;
+    if (!table) {
+        PF_HIP(c, hipStreamSynchronize(c->stream));
+        dfree(c, m->table, (size_t)m->V * m->D * 4);
+        m->table = nullptr;
+        return PF_OK;
+    }
+    if (!m->table) {
+        pf_status s = dalloc_t(c, &m->table, (size_t)m->V * m->D);
+        if (s) return s;
+    }
+    PF_HIP(c, hipMemcpyAsync(m->table, table, (size_t)m->V * m->D * 4, hipMemcpyHostToDevice, c->stream));
+    PF_HIP(c, hipStreamSynchronize(c->stream));
+    return PF_OK;
+}
+
+extern "C" pf_status pf_mtp_heads_forward(pf_mtp* m, const float* hidden, float* logits) {
+    if (!m || !hidden || !logits) return PF_ERR_ARG;
+    pf_ctx* c = m->c;
+    hipStream_t st = c->stream;
+    const uint32_t D = m->D, V = m->V;
+    PF_HIP(c, hipMemcpyAsync(m->cur, hidden, (size_t)D * 4, hipMemcpyHostToDevice, st));
+    for (uint32_t k = 0; k < m->H; k++) {            // src/mtp.cpp:63-127
+        launch_gemv_f32(st, m->mats[k * 3 + 0], 1, m->cur, D, m->g, D, nullptr);
+        launch_gemv_f32(st, m->mats[k * 3 + 1], 1, m->cur, D, m->u, D, nullptr);
+        hipLaunchKernelGGL(k_silu_mul, dim3((D + 255) / 256), dim3(256), 0, st, m->g, m->u, m->a, D);
+        launch_gemv_f32(st, m->mats[k * 3 + 2], 1, m->a, D, m->cur, D, m->cur);
+        float* lk = m->logits + (size_t)k * V;
+        if (m->table)
+            hipLaunchKernelGGL(k_gemv_f32_dense<1>, dim3((std::min<uint32_t>(V, 2048) + 3) / 4), dim3(256), 0, st,
+                               (const float*)m->table, V, D, (const float*)m->cur, D, lk, V);
+        else
+            hipLaunchKernelGGL(k_mtp_placeholder, dim3((V + 255) / 256), dim3(256), 0, st, lk, V, k);
+    }
+    PF_LAUNCHED(c);
+    PF_HIP(c, hipMemcpyAsync(logits, m->logits, (size_t)m->H * V * 4, hipMemcpyDeviceToHost, st));
+    PF_HIP(c, hipStreamSynchronize(st));
+    return PF_OK;
+}
+
+extern "C" size_t pf_mtp_memory(const pf_mtp* m) {
+    if (!m) return 0;
+    size_t b = 0;
+    for (const pf_matrix* M : m->mats) b += M->bytes + (size_t)M->rows * (M->cols / 32) * 2;
+    if (m->table) b += (size_t)m->V * m->D * 4;
+    return b;
+}
+
 // ================================================================= KV cache
 
 static pf_status kv_geom(const pf_ctx* c, uint32_t L, uint32_t H, uint32_t hd, uint32_t sink, uint32_t win,
@@ -825,6 +957,7 @@ struct pf_engine {
     uint32_t pool_rows_max = 1;
     bool hidden_valid = false;
     size_t max_memory = 0;
+    bool mtp_enabled = true;      // ModelConfig::mtp_enabled, include/forge/types.hpp
     // timing
     std::vector<TimedPass> timed;
     size_t timed_used = 0;
@@ -977,6 +1110,12 @@ extern "C" pf_status pf_engine_reset(pf_engine* e) {
 }
 
 extern "C" uint32_t pf_engine_position(const pf_engine* e) { return e ? e->pos : 0; }
+
+extern "C" pf_status pf_engine_set_mtp_enabled(pf_engine* e, int32_t enabled) {
+    if (!e) return PF_ERR_ARG;
+    e->mtp_enabled = enabled != 0;
+    return PF_OK;
+}
 
 extern "C" pf_status pf_engine_set_max_memory(pf_engine* e, size_t bytes) {
     if (!e) return PF_ERR_ARG;
@@ -1365,7 +1504,7 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
             res->oom_protected = 1;
             break;
         }
-        const bool mtp_round = NM > 0 && e->hidden_valid && n_gen + 4 <= max_new;   // src/engine.cpp:304-305
+        const bool mtp_round = e->mtp_enabled && NM > 0 && e->hidden_valid && n_gen + 4 <= max_new;   // src/engine.cpp:304-305
         if (e->pos + NM + 2 > e->rope_pos)
             return fail(c, PF_ERR_CAPACITY, "position beyond the engine's max_context");
         pf_status s;

@@ -225,3 +225,27 @@ def test_generate_multi_chunk_matches_oracle(gpu, tiny_weights):
     toks, res, ot, oa, orj = _gen_both(gpu, cfg, w, prompt, 40, GREEDY, kv=kv)
     np.testing.assert_array_equal(toks, ot)
     assert (res.mtp_accepted, res.mtp_rejected) == (oa, orj)
+
+
+@pytest.mark.parametrize("samp", [GREEDY, TOP_P], ids=["greedy", "top_p"])
+def test_generate_mtp_disabled(gpu, tiny_weights, samp):
+    """Engine::set_mtp_enabled(false): the single-token loop only
+    (src/engine.cpp:304, 367-386), equal to an oracle engine without heads."""
+    cfg, w = tiny_weights
+    m = pf.Model(gpu, cfg, w)
+    e = pf.Engine(m, **KV)
+    e.set_mtp_enabled(False)
+    prompt = W.prompt_ids(11, cfg["n_vocab"], seed=6)
+    toks, res = e.generate(prompt, 30, samp, 9)
+    c = dict(cfg)
+    c["n_mtp"] = 0
+    om = _oracle(c, w)
+    ot, oa, orj = om.generate(prompt, 30, O.Sampling(samp.temperature, samp.top_p, samp.top_k, samp.greedy), 9)
+    np.testing.assert_array_equal(toks, ot)
+    assert res.rounds == 0 and res.mtp_accepted == 0 and (oa, orj) == (0, 0)
+    e.set_mtp_enabled(True)
+    toks2, res2 = e.generate(prompt, 30, samp, 9)
+    assert res2.rounds > 0
+    om.close()
+    e.close()
+    m.close()

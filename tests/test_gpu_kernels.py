@@ -179,3 +179,70 @@ def test_sampler(gpu, tiny_engine, name, V):
         t, d = tiny_engine.sample(logits, cfg, 7, draw)
         t2, d2 = O.sample(logits, ocfg, 7, draw)
         assert (t, d) == (t2, d2), (name, trial)
+
+
+def test_dot_softmax_rmsnorm_argmax(gpu):
+    """matmul_neon.hpp helpers on the device against the oracle's canonical
+    orders (bit-exact), the reference's known answers
+    (tests/test_matmul.cpp:103-153) and closed forms."""
+    L = O.lib()
+    rng = np.random.default_rng(5)
+    for n in (1, 6, 255, 256, 300, 2048, 5000):
+        a = rng.standard_normal(n).astype(np.float32)
+        b = rng.standard_normal(n).astype(np.float32)
+        assert np.float32(gpu.dot_product(_t(a), _t(b))) == np.float32(L.orc_dot_canon(O.ptr(a, O.f32p),
+                                                                                         O.ptr(b, O.f32p), n))
+        v = (a * 3).astype(np.float32)
+        dv = _t(v)
+        gpu.softmax(dv)
+        ref = v.copy()
+        L.orc_softmax(O.ptr(ref, O.f32p), n)
+        np.testing.assert_array_equal(dv.numpy(), ref)
+        w = rng.standard_normal(n).astype(np.float32)
+        got = gpu.rmsnorm(_t(a), _t(w)).numpy()
+        ref = np.zeros(n, np.float32)
+        L.orc_rmsnorm(O.ptr(ref, O.f32p), O.ptr(a, O.f32p), O.ptr(w, O.f32p), n)
+        np.testing.assert_array_equal(got, ref)
+        x = a.copy()
+        x[n // 2] = x.max() + 1.0
+        if n > 3:
+            x[n // 3] = x[n // 2]                       # tie: the first index wins
+        assert gpu.argmax(_t(x)) == int(np.argmax(x))
+    # reference known answers
+    assert gpu.dot_product(_t(np.arange(1, 7, dtype=np.float32)), _t(np.arange(6, 0, -1, dtype=np.float32))) == 56.0
+    sm = _t(np.array([2.0, 1.0, 0.1, 0.5, 3.0], np.float32))
+    gpu.softmax(sm)
+    s = sm.numpy()
+    assert abs(s.sum() - 1.0) < 1e-3 and s[4] > s[0] > s[1] > s[3] > s[2]
+    rn = gpu.rmsnorm(_t(np.array([1, 2, 3, 4], np.float32)), _t(np.array([0.5, 1, 1.5, 2], np.float32))).numpy()
+    assert abs(rn[0] - 0.5 / np.sqrt(7.5)) < 0.01 and abs(rn[3] - 8 / np.sqrt(7.5)) < 0.01
+    assert gpu.argmax(_t(np.array([-1.0, 3.0, 0.5, -0.2, 2.0], np.float32))) == 1
+
+
+@pytest.mark.parametrize("with_table", [True, False])
+def test_mtp_heads_standalone(gpu, with_table):
+    """MTPHeads::forward outside an engine: 4 chained heads, fp32 tied table
+    or the placeholder logits, bit-exact against the oracle."""
+    d, V, H = 256, 1024, 4
+    heads = []
+    m = pf.MTPHeads(gpu, H, d, V)
+    for k in range(H):
+        trip = []
+        for w in range(3):
+            codes, scales = pf.gen_matrix(77, 100 + 3 * k + w, 0.02, d, d, pf.FMT_Q4)
+            m.set_head(k, w, codes, scales)
+            trip.append((O.Q4, codes, scales))
+        heads.append(trip)
+    rng = np.random.default_rng(3)
+    table = (rng.standard_normal((V, d)) * 0.02).astype(np.float32) if with_table else None
+    m.set_table(table)
+    hidden = rng.standard_normal(d).astype(np.float32)
+    got = m.forward(hidden)
+    ref = O.mtp_heads_forward(heads, d, V, table, hidden)
+    np.testing.assert_array_equal(got, ref)
+    if not with_table:
+        v = np.arange(V, dtype=np.uint64)
+        np.testing.assert_array_equal(got[2], ((v * np.uint64(2654435761) + np.uint64(2)) % np.uint64(V))
+                                      .astype(np.float32) / np.float32(V))
+    assert m.memory_usage() > 0
+    m.close()
