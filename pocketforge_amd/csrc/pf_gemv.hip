@@ -45,8 +45,10 @@ __device__ __forceinline__ void unpack_codes(const uint8_t* tile, uint32_t t, ui
 // adds in any order with a bit-identical result.  The consumer converts
 // (float)(acc * (double)a_scale) and clears acc.
 // Grid (N/64, splits), 256 threads; wave w of split s covers blocks
-// [(4s+w)*bpw, (4s+w+1)*bpw), lane = output row; loads are issued four
-// blocks at a time.
+// [(4s+w)*bpw, (4s+w+1)*bpw), bpw in {1, 2, 4} with nb % (4 bpw) == 0, lane =
+// output row.  Each wave issues all its weight loads first; the workgroup's
+// activation rows and block sums are staged in LDS with one vector load per
+// thread (they come from another kernel, often through another XCD's L2).
 template <int FMT, int M>
 __global__ __launch_bounds__(256) void k_gemv_i8(const uint8_t* __restrict__ W, uint32_t K,
                                                  const int8_t* __restrict__ act, uint32_t act_stride,
@@ -55,47 +57,61 @@ __global__ __launch_bounds__(256) void k_gemv_i8(const uint8_t* __restrict__ W, 
     constexpr uint32_t TB = tile_bytes(FMT);
     constexpr uint32_t CODES = TILE_ROWS * TILE_BLOCKS * code_bytes(FMT);
     constexpr int OFF = code_offset(FMT);
-    constexpr uint32_t U = 4;
+    __shared__ __align__(16) int32_t sa[M][16 * 8];  // activations of the workgroup's 4 bpw <= 16 blocks
+    __shared__ int32_t sb[M][16];
+    __shared__ double red[4][M][64];
     const uint32_t g = blockIdx.x, s = blockIdx.y;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t nb = K >> 5, chunks = K >> 8;
-    const uint32_t b_begin = (s * 4u + wid) * bpw;
-    const uint32_t b_end = min(b_begin + bpw, nb);
+    const uint32_t chunks = K >> 8, wb = 4u * bpw, wb0 = s * wb, b0 = wb0 + wid * bpw;
     const uint8_t* tiles = W + (size_t)g * chunks * TB;
-
+    uint32_t u[4][8];
+    double d[4];
+#pragma unroll
+    for (uint32_t k = 0; k < 4; k++) {
+        d[k] = 0.0;
+#pragma unroll
+        for (int q = 0; q < 8; q++) u[k][q] = 0u;
+        if (k < bpw) {
+            const uint32_t b = b0 + k;
+            const uint8_t* tile = tiles + (size_t)(b >> 3) * TB;
+            unpack_codes<FMT>(tile, b & 7u, lane, u[k]);
+            d[k] = (double)h2f(*reinterpret_cast<const uint16_t*>(tile + CODES + lane * 16u + (b & 7u) * 2u));
+        }
+    }
+    for (uint32_t i = threadIdx.x; i < (uint32_t)M * wb * 8u; i += 256u) {
+        const uint32_t m = i / (wb * 8u), r = i - m * wb * 8u;
+        sa[m][r] = reinterpret_cast<const int32_t*>(act + (size_t)m * act_stride)[wb0 * 8u + r];
+    }
+    if (threadIdx.x < (uint32_t)M * wb) {
+        const uint32_t m = threadIdx.x / wb, k = threadIdx.x - m * wb;
+        sb[m][k] = bsum[(size_t)m * bsum_stride + wb0 + k];
+    }
+    __syncthreads();
     double S[M];
 #pragma unroll
     for (int m = 0; m < M; m++) S[m] = 0.0;
-
-    for (uint32_t b0 = b_begin; b0 < b_end; b0 += U) {
-        uint32_t u[U][8];
-        double d[U];
 #pragma unroll
-        for (uint32_t k = 0; k < U; k++) {
-            const uint32_t b = b0 + k;
-            if (b < b_end) {
-                const uint8_t* tile = tiles + (size_t)(b >> 3) * TB;
-                unpack_codes<FMT>(tile, b & 7u, lane, u[k]);
-                d[k] = (double)h2f(*reinterpret_cast<const uint16_t*>(tile + CODES + lane * 16u + (b & 7u) * 2u));
-            }
-        }
-#pragma unroll
-        for (uint32_t k = 0; k < U; k++) {
-            const uint32_t b = b0 + k;
-            if (b >= b_end) break;
+    for (uint32_t k = 0; k < 4; k++) {
+        if (k < bpw) {
+            const uint32_t j = wid * bpw + k;
 #pragma unroll
             for (int m = 0; m < M; m++) {
-                const int32_t* a = reinterpret_cast<const int32_t*>(act + (size_t)m * act_stride + (size_t)b * 32u);
-                int p = -OFF * bsum[(size_t)m * bsum_stride + b];
-#pragma unroll
-                for (int q = 0; q < 8; q++) p = __builtin_amdgcn_sdot4((int)u[k][q], a[q], p, false);
+                const int4 a0 = *reinterpret_cast<const int4*>(&sa[m][j * 8u]);
+                const int4 a1 = *reinterpret_cast<const int4*>(&sa[m][j * 8u + 4u]);
+                int p = -OFF * sb[m][j];
+                p = __builtin_amdgcn_sdot4((int)u[k][0], a0.x, p, false);
+                p = __builtin_amdgcn_sdot4((int)u[k][1], a0.y, p, false);
+                p = __builtin_amdgcn_sdot4((int)u[k][2], a0.z, p, false);
+                p = __builtin_amdgcn_sdot4((int)u[k][3], a0.w, p, false);
+                p = __builtin_amdgcn_sdot4((int)u[k][4], a1.x, p, false);
+                p = __builtin_amdgcn_sdot4((int)u[k][5], a1.y, p, false);
+                p = __builtin_amdgcn_sdot4((int)u[k][6], a1.z, p, false);
+                p = __builtin_amdgcn_sdot4((int)u[k][7], a1.w, p, false);
                 S[m] = __builtin_fma(d[k], (double)p, S[m]);
             }
         }
     }
-
-    __shared__ double red[4][M][64];
 #pragma unroll
     for (int m = 0; m < M; m++) red[wid][m][lane] = S[m];
     __syncthreads();

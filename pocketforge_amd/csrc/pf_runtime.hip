@@ -236,20 +236,21 @@ static void repack_tiles(int fmt, uint32_t cols, const uint8_t* codes, const uin
         }
 }
 
-// K split of a tiled matrix: the largest blocks-per-wave (1..16) that still
-// gives at least `min_waves` waves (default 2048: every launch covers the
-// 256 CUs; PF_GEMV_MIN_WAVES overrides it).
+// K split of a tiled matrix: the largest blocks-per-wave in {1, 2, 4} that
+// divides the blocks into whole workgroups (nb % (4 bpw) == 0; nb is a
+// multiple of 8) and still gives at least `min_waves` waves (default 2048:
+// every launch covers the 256 CUs; PF_GEMV_MIN_WAVES overrides it).
 static void choose_split(pf_matrix* M) {
     const uint32_t nb = M->cols / 32, G = M->rows / 64;
     uint64_t min_waves = 2048;
     if (const char* s = std::getenv("PF_GEMV_MIN_WAVES")) min_waves = std::strtoull(s, nullptr, 10);
     uint32_t best = 1;
-    for (uint32_t bpw : {1u, 2u, 4u, 8u, 16u}) {
-        uint32_t splits = (nb + 4 * bpw - 1) / (4 * bpw);
-        if ((uint64_t)G * splits * 4 >= min_waves) best = bpw;
+    for (uint32_t bpw : {1u, 2u, 4u}) {
+        if (nb % (4 * bpw)) continue;
+        if ((uint64_t)G * (nb / (4 * bpw)) * 4 >= min_waves) best = bpw;
     }
     M->bpw = best;
-    M->splits = (nb + 4 * best - 1) / (4 * best);
+    M->splits = nb / (4 * best);
 }
 
 static pf_status matrix_alloc(pf_ctx* c, int32_t fmt, uint32_t rows, uint32_t cols, bool rowmajor, pf_matrix** out) {
