@@ -466,4 +466,69 @@ __global__ __launch_bounds__(128) void k_attn_merge_chunks(const PassDesc* __res
     if (i < hd) out[(size_t)m * D + h * hd + i] = U * (1.0f / (T + 1e-10f));
 }
 
+// Second stage of the engine's attention fused with the O projection's
+// quantize_activation_row (src/engine.cpp:789-796): per row m, every head's
+// chunks merged exactly as k_attn_merge_chunks does (max over the chunk
+// maxima, f_c = exp(m_c - max), T and U fmaf chains over c in order,
+// out = U * (1 / (T + 1e-10))), then the row quantized.  Grid M, 1024
+// threads; element i = t + 1024 k; heads * chunks <= 2048 (checked when the
+// engine is created).
+template <int PER>
+__global__ __launch_bounds__(1024) void k_attn_merge_quant(const PassDesc* __restrict__ pd, KvGeom g,
+                                                           const float* __restrict__ S, uint32_t s_stride,
+                                                           const float* __restrict__ Up, uint32_t cstride,
+                                                           int8_t* __restrict__ q, uint32_t q_stride,
+                                                           float* __restrict__ as, int32_t* __restrict__ bsum,
+                                                           uint32_t bsum_stride, uint32_t rows, Prefetch pf) {
+    __shared__ float fs[2048], ts[2048];
+    __shared__ float hmax[128], hinv[128];
+    __shared__ float red[16];
+    const uint32_t m = blockIdx.x, t = threadIdx.x;
+    if (m >= rows) {
+        prefetch_bytes(pf.p, pf.n, m - rows, gridDim.x - rows, pf.sink);
+        return;
+    }
+    if (m >= pd->m) return;
+    const uint32_t H = g.n_heads, hd = g.head_dim, D = H * hd;
+    const uint32_t nc = (kv_view(g, pd->pos0 + m).count() + 1 + 255) / 256;
+    const float* st = S + (size_t)m * H * s_stride;
+    for (uint32_t i = t; i < H * nc; i += 1024) {
+        const uint32_t h = i / nc, c = i - h * nc;
+        fs[i] = st[(size_t)h * s_stride + 2 * c];
+        ts[i] = st[(size_t)h * s_stride + 2 * c + 1];
+    }
+    __syncthreads();
+    if (t < H) {
+        float mx = fs[t * nc];
+        for (uint32_t c = 1; c < nc; c++) mx = fmaxf(mx, fs[t * nc + c]);
+        hmax[t] = mx;
+    }
+    __syncthreads();
+    for (uint32_t i = t; i < H * nc; i += 1024) fs[i] = expf_c(fs[i] - hmax[i / nc]);
+    __syncthreads();
+    if (t < H) {
+        float T = 0.0f;
+        for (uint32_t c = 0; c < nc; c++) T = __builtin_fmaf(ts[t * nc + c], fs[t * nc + c], T);
+        hinv[t] = 1.0f / (T + 1e-10f);
+    }
+    __syncthreads();
+    float v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const uint32_t i = t + 1024u * k;
+        v[k] = 0.0f;
+        if (i < D) {
+            const uint32_t h = i / hd, l = i - h * hd;
+            const float* up = Up + ((size_t)m * H + h) * cstride * hd + l;
+            const float* f = fs + h * nc;
+            float U = 0.0f;
+#pragma unroll 8
+            for (uint32_t c = 0; c < nc; c++) U = __builtin_fmaf(up[(size_t)c * hd], f[c], U);
+            v[k] = U * hinv[h];
+        }
+    }
+    quantize_row_block<PER, 1024>(v, D, q + (size_t)m * q_stride, as + m,
+                                  bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
+}
+
 }  // namespace pf

@@ -181,6 +181,33 @@ __device__ __forceinline__ uint32_t kv_row(const KvGeom& g, const KvView& v, uin
     return KV_SINK_ROWS + (v.win_lo + j) % g.ring;
 }
 
+// ---------------------------------------------------------- prefetch
+
+// Streams bytes [p, p + n) (n a multiple of 16) through the cache hierarchy
+// so that the next kernel finds them in the MALL.  Block b of nb prefetching
+// blocks takes every nb-th stripe of blockDim.x * 16 bytes.  The loaded
+// words feed a value that is stored only if it equals a constant, so the
+// loads stay.
+__device__ __forceinline__ void prefetch_bytes(const uint8_t* __restrict__ p, size_t n, uint32_t b, uint32_t nb,
+                                               uint32_t* __restrict__ sink) {
+    const uint4* q = reinterpret_cast<const uint4*>(p);
+    const size_t n16 = n >> 4, stride = (size_t)nb * blockDim.x;
+    uint32_t x = 0;
+    size_t i = (size_t)b * blockDim.x + threadIdx.x;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const uint4 v0 = q[i], v1 = q[i + stride], v2 = q[i + 2 * stride], v3 = q[i + 3 * stride];
+        x ^= v0.x ^ v1.y ^ v2.z ^ v3.w;
+    }
+    for (; i < n16; i += stride) x ^= q[i].x;
+    if (x == 0x7A5C3E1Fu) sink[0] = x;
+}
+
+struct Prefetch {
+    const uint8_t* p;   // bytes the next kernel reads first (null: none)
+    size_t n;
+    uint32_t* sink;
+};
+
 // ------------------------------------------------------ quantized rows
 
 // Block sums of int8 codes over 32-element blocks for a 256-thread block

@@ -321,6 +321,8 @@ __global__ __launch_bounds__(256) void k_quant_rows(const float* __restrict__ x,
 // weight w, then quantize_activation_row of the normed row.  Grid M, 1024
 // threads: all loads are issued first; the 256 canonical lanes read the
 // row back from LDS (K <= 4096).
+// Blocks past the `rows` row blocks prefetch pf (the weights of the GEMV that
+// consumes the output).
 template <int PER>
 __global__ __launch_bounds__(1024) void k_resid_norm_quant(float* __restrict__ x, uint32_t K,
                                                            double* __restrict__ acc,
@@ -328,10 +330,14 @@ __global__ __launch_bounds__(1024) void k_resid_norm_quant(float* __restrict__ x
                                                            const float* __restrict__ w,
                                                            int8_t* __restrict__ q, uint32_t q_stride,
                                                            float* __restrict__ as, int32_t* __restrict__ bsum,
-                                                           uint32_t bsum_stride) {
+                                                           uint32_t bsum_stride, uint32_t rows, Prefetch pf) {
     __shared__ float row[4096];
     __shared__ float red[16];
     const uint32_t m = blockIdx.x, t = threadIdx.x;
+    if (m >= rows) {
+        prefetch_bytes(pf.p, pf.n, m - rows, gridDim.x - rows, pf.sink);
+        return;
+    }
     float xv[PER], wv[PER];
     double av[PER];
 #pragma unroll
@@ -404,9 +410,13 @@ __global__ __launch_bounds__(1024) void k_swiglu_quant(double* __restrict__ acc,
                                                        uint32_t ff,
                                                        int8_t* __restrict__ q, uint32_t q_stride,
                                                        float* __restrict__ as, int32_t* __restrict__ bsum,
-                                                       uint32_t bsum_stride) {
+                                                       uint32_t bsum_stride, uint32_t rows, Prefetch pf) {
     __shared__ float red[16];
     const uint32_t m = blockIdx.x;
+    if (m >= rows) {
+        prefetch_bytes(pf.p, pf.n, m - rows, gridDim.x - rows, pf.sink);
+        return;
+    }
     double ga[PER], ua[PER];
 #pragma unroll
     for (int k = 0; k < PER; k++) {

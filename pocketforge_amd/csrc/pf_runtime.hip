@@ -958,6 +958,8 @@ struct pf_engine {
     uint32_t pool_rows_max = 1;
     bool hidden_valid = false;
     size_t max_memory = 0;
+    uint32_t pf_blocks = 128;     // prefetch blocks of the row kernels (PF_PREFETCH_BLOCKS)
+    uint32_t* sink = nullptr;     // 4 bytes the prefetch loops never write in practice
     bool mtp_enabled = true;      // ModelConfig::mtp_enabled, include/forge/types.hpp
     // timing
     std::vector<TimedPass> timed;
@@ -1038,8 +1040,14 @@ extern "C" pf_status pf_engine_create(pf_model* m, const pf_cache_desc* cd, pf_e
     e->kmax = std::max(D, F);
     e->pool_rows_max = (MR + e->g.pool_block - 1) / e->g.pool_block + 1;
     const uint32_t cmax = KV_SINK_ROWS + e->g.pool_cap + e->g.window;
+    if (H > 128 || (uint64_t)H * ((cmax + 1 + 255) / 256) > 2048) {
+        pf_engine_destroy(e);
+        return fail(c, PF_ERR_UNSUPPORTED, "heads x attention chunks exceeds 2048 (context too long for the merge)");
+    }
     e->s_stride = cmax + 8;
     e->cstride = (cmax + 63) / 64 + 1;
+    if (const char* v = std::getenv("PF_PREFETCH_BLOCKS")) e->pf_blocks = (uint32_t)std::strtoul(v, nullptr, 10);
+    if (!s) s = ealloc(e, &e->sink, 1);
     if (!s) s = ealloc(e, &e->x, (size_t)MR * D);
     if (!s) s = ealloc(e, &e->act, (size_t)MR * e->kmax);
     if (!s) s = ealloc(e, &e->as, 4 * MR);
@@ -1184,6 +1192,11 @@ static pf_status pass_gemv(pf_engine* e, const pf_matrix* W, uint32_t M) {
 
 // One forward pass of M rows (the PassDesc at `pd` holds positions and
 // tokens; pos0 is the host's copy of the first position).  hidden/logits
+static Prefetch prefetch_of(const pf_engine* e, const pf_matrix* W) {
+    if (!e->pf_blocks) return Prefetch{nullptr, 0, e->sink};
+    return Prefetch{W->data, W->bytes & ~(size_t)15, e->sink};
+}
+
 // outputs are device [M][D] / [M][V]; logits may be null.
 static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0, float* logits, float* hidden) {
     pf_ctx* c = e->c;
@@ -1213,24 +1226,28 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
     for (uint32_t l = 0; l < d.n_layers; l++) {
         const float* an = m->attn_norm + (size_t)l * D;
         const float* fn = m->ffn_norm + (size_t)l * D;
-        PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(M), dim3(1024), 0, st, e->x, D,
+        // row kernels carry e->pf_blocks extra blocks that stream the next
+        // GEMV's weights into the MALL while the rows are processed
+        const uint32_t rb = M + e->pf_blocks;
+        PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(rb), dim3(1024), 0, st, e->x, D,
                                                 l == 0 ? (double*)nullptr : e->acc, as3, an, e->act, ks, as0, e->bsum,
-                                                bs));
+                                                bs, M, prefetch_of(e, m->qkv[l])));
         if (pf_status s = pass_gemv(e, m->qkv[l], M)) return s;
         hipLaunchKernelGGL(k_qkv_post, dim3(M, H), dim3(64), 0, st, e->acc, as0, pd, e->rope_c, e->rope_s, g, e->kv, l,
                            e->q, e->k, e->v);
         launch_attn(st, hd, M, attn_blocks, pd, g, e->kv, l, attn_groups, e->q, e->k, e->v, e->S, e->s_stride,
                     e->Wp, e->cstride);
-        hipLaunchKernelGGL(k_attn_merge_chunks, dim3(M, H), dim3(128), 0, st, pd, g, (const float*)e->S, e->s_stride,
-                           (const float*)e->Wp, e->cstride, e->attn);
-        PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_quant_rows_wide<PER>, dim3(M), dim3(1024), 0, st, e->attn, D,
-                                                e->act, ks, as1, e->bsum, bs));
+        PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_attn_merge_quant<PER>, dim3(rb), dim3(1024), 0, st, pd, g,
+                                                (const float*)e->S, e->s_stride, (const float*)e->Wp, e->cstride,
+                                                e->act, ks, as1, e->bsum, bs, M, prefetch_of(e, m->o[l])));
         if (pf_status s = pass_gemv(e, m->o[l], M)) return s;
-        PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(M), dim3(1024), 0, st, e->x, D,
-                                                e->acc, as1, fn, e->act, ks, as2, e->bsum, bs));
+        PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(rb), dim3(1024), 0, st, e->x, D,
+                                                e->acc, as1, fn, e->act, ks, as2, e->bsum, bs, M,
+                                                prefetch_of(e, m->gu[l])));
         if (pf_status s = pass_gemv(e, m->gu[l], M)) return s;
-        PF_PER1024_SWITCH(F, hipLaunchKernelGGL(k_swiglu_quant<PER>, dim3(M), dim3(1024), 0, st, e->acc,
-                                                (const float*)as2, F, e->act, ks, as3, e->bsum, bs));
+        PF_PER1024_SWITCH(F, hipLaunchKernelGGL(k_swiglu_quant<PER>, dim3(rb), dim3(1024), 0, st, e->acc,
+                                                (const float*)as2, F, e->act, ks, as3, e->bsum, bs, M,
+                                                prefetch_of(e, m->down[l])));
         if (pf_status s = pass_gemv(e, m->down[l], M)) return s;
     }
     if (d.n_layers)
