@@ -107,7 +107,8 @@ pf_status pf_matrix_upload(pf_ctx* ctx, int32_t fmt, uint32_t rows, uint32_t col
                            const uint16_t* scales, int32_t rowmajor, pf_matrix** out);
 void pf_matrix_free(pf_matrix* m);
 /* y[M][rows] = quantize_activation_row(x[m]) x W (tiled matrices), the
- * fused matmul_quantized path with per-block scales. */
+ * fused matmul_quantized path with per-block scales.  M <= 8 runs the GEMV,
+ * 8 < M <= 512 the int8 MFMA GEMM; both give the same exact sums. */
 pf_status pf_gemv_q(pf_ctx* ctx, const pf_matrix* W, const float* x_dev, float* y_dev, uint32_t M);
 /* y[M][rows] = fp32 x[m] . dequantized W rows (row-major Q4 matrices). */
 pf_status pf_gemv_f32(pf_ctx* ctx, const pf_matrix* W, const float* x_dev, float* y_dev, uint32_t M);

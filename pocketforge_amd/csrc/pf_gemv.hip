@@ -122,6 +122,100 @@ __global__ __launch_bounds__(256) void k_gemv_i8(const uint8_t* __restrict__ W, 
     }
 }
 
+// ===================================================== int8 x block GEMM
+
+typedef int pf_v4i __attribute__((ext_vector_type(4)));
+typedef int pf_v16i __attribute__((ext_vector_type(16)));
+
+// Signed codes of the 16 elements 16h .. 16h + 15 of weight row r, block t,
+// of a tile, packed 4 per dword in element order (MFMA B operand).  Byte
+// x - OFF is formed as (x + (0x80 - OFF)) ^ 0x80 per byte (no carries: every
+// byte sum is below 0x100).
+template <int FMT>
+__device__ __forceinline__ pf_v4i gemm_codes(const uint8_t* tile, uint32_t t, uint32_t r, uint32_t h) {
+    constexpr uint32_t OFF = (uint32_t)code_offset(FMT);
+    constexpr uint32_t ADD = (0x80u - OFF) * 0x01010101u;
+    pf_v4i v;
+    if constexpr (FMT == FMT_Q4) {
+        const uint4 c = *reinterpret_cast<const uint4*>(tile + t * 1024u + r * 16u);
+        const uint32_t sh = 4u * h, m = 0x0F0F0F0Fu;
+        v.x = (int)((((c.x >> sh) & m) + ADD) ^ 0x80808080u);
+        v.y = (int)((((c.y >> sh) & m) + ADD) ^ 0x80808080u);
+        v.z = (int)((((c.z >> sh) & m) + ADD) ^ 0x80808080u);
+        v.w = (int)((((c.w >> sh) & m) + ADD) ^ 0x80808080u);
+    } else {
+        const uint2 c = *reinterpret_cast<const uint2*>(tile + (t >> 1) * 1024u + r * 16u + (t & 1u) * 8u);
+        const uint32_t sh = 4u * h, m = 0x03030303u;
+        v.x = (int)((((c.x >> sh) & m) + ADD) ^ 0x80808080u);
+        v.y = (int)((((c.y >> sh) & m) + ADD) ^ 0x80808080u);
+        v.z = (int)((((c.x >> (sh + 2u)) & m) + ADD) ^ 0x80808080u);
+        v.w = (int)((((c.y >> (sh + 2u)) & m) + ADD) ^ 0x80808080u);
+    }
+    return v;
+}
+
+// acc[m][n] += sum over the blocks [s bps, (s + 1) bps) of d[n][b] * p[m][n][b]
+// for M activation rows (M > 8: verify passes of many sequences, batched
+// prefill), the exact fp64 sum of k_gemv_i8.  p comes from
+// v_mfma_i32_32x32x32_i8, one 32-element block per instruction: lane l
+// holds activation row l % 32 and weight row l % 32, elements 16 (l / 32)
+// .. + 15; result element i is activation row 8 (i / 4) + 4 (l / 32) + i % 4,
+// weight row l % 32, so a lane needs one block scale per block.
+// Grid (N / 32, splits), 256 threads: the block's 32 weight rows
+// [32 blockIdx.x, + 32) against activation tiles w, w + 4, ... (MTW per
+// wave) of 32 rows each; act holds ceil(M / 32) * 32 readable rows.
+template <int FMT, int MTW>
+__global__ __launch_bounds__(256) void k_gemm_i8(const uint8_t* __restrict__ W, uint32_t K, uint32_t M,
+                                                 const int8_t* __restrict__ act, uint32_t act_stride, uint32_t bps,
+                                                 double* __restrict__ acc, uint32_t acc_stride) {
+    constexpr uint32_t TB = tile_bytes(FMT);
+    constexpr uint32_t CODES = TILE_ROWS * TILE_BLOCKS * code_bytes(FMT);
+    const uint32_t lane = threadIdx.x & 63u, h = lane >> 5, l32 = lane & 31u;
+    const uint32_t wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t n0 = blockIdx.x * 32u, r = (n0 & 63u) + l32;
+    const uint32_t nb = K >> 5, chunks = K >> 8, mtiles = (M + 31u) / 32u;
+    const uint32_t b_begin = blockIdx.y * bps, b_end = min(b_begin + bps, nb);
+    const uint8_t* tiles = W + (size_t)(n0 >> 6) * chunks * TB;
+    double S[MTW][16];
+#pragma unroll
+    for (int j = 0; j < MTW; j++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) S[j][i] = 0.0;
+    const pf_v16i zero = {};
+    for (uint32_t b = b_begin; b < b_end; b++) {
+        const uint8_t* tile = tiles + (size_t)(b >> 3) * TB;
+        const uint32_t t = b & 7u;
+        const pf_v4i bw = gemm_codes<FMT>(tile, t, r, h);
+        const double d = (double)h2f(*reinterpret_cast<const uint16_t*>(tile + CODES + r * 16u + t * 2u));
+        pf_v4i a[MTW];
+#pragma unroll
+        for (int j = 0; j < MTW; j++) {
+            const uint32_t mt = wid + 4u * j;
+            a[j] = mt < mtiles ? *reinterpret_cast<const pf_v4i*>(act + (size_t)(mt * 32u + l32) * act_stride +
+                                                                   b * 32u + 16u * h)
+                               : pf_v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int j = 0; j < MTW; j++) {
+            if (wid + 4u * j < mtiles) {
+                const pf_v16i p = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], bw, zero, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 16; i++) S[j][i] = __builtin_fma(d, (double)p[i], S[j][i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < MTW; j++) {
+        const uint32_t mt = wid + 4u * j;
+        if (mt >= mtiles) continue;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t m = mt * 32u + 8u * (i / 4) + 4u * h + (i % 4);
+            if (m < M) atomicAdd(acc + (size_t)m * acc_stride + n0 + l32, S[j][i]);
+        }
+    }
+}
+
 // y = (float)(acc * (double)as[m]); acc cleared for its next use.
 __device__ __forceinline__ float take_acc(double* acc, size_t i, float as) {
     const double v = acc[i];

@@ -350,6 +350,37 @@ static void launch_gemv(hipStream_t st, const pf_matrix* W, uint32_t M, const in
     }
 }
 
+// acc[M][rows] += int8 activations x tiled block matrix for M > 8 rows
+// (MFMA GEMM, exact fp64 like the GEMV).  act must hold ceil(M / 32) * 32
+// readable rows.  K splits: enough blocks for 512 workgroups.
+constexpr uint32_t MAX_GEMM_ROWS = 512;
+
+static void launch_gemm(hipStream_t st, const pf_matrix* W, uint32_t M, const int8_t* act, uint32_t act_stride,
+                        double* acc, uint32_t acc_stride) {
+    const uint32_t nb = W->cols / 32, nblk = W->rows / 32;
+    uint32_t splits = std::max(1u, std::min(nb / 2, (512 + nblk - 1) / nblk));
+    const uint32_t bps = (nb + splits - 1) / splits;
+    splits = (nb + bps - 1) / bps;
+    const uint32_t mtw = ((M + 31) / 32 + 3) / 4;
+    const dim3 grid(nblk, splits);
+#define PF_GEMM_CASE(F, T)                                                                                    \
+    case T:                                                                                                   \
+        hipLaunchKernelGGL((k_gemm_i8<F, T>), grid, dim3(256), 0, st, W->data, W->cols, M, act, act_stride, bps, \
+                           acc, acc_stride);                                                                  \
+        break;
+#define PF_GEMM_FMT(F)                                                            \
+    switch (mtw) {                                                                \
+        PF_GEMM_CASE(F, 1) PF_GEMM_CASE(F, 2) PF_GEMM_CASE(F, 3) PF_GEMM_CASE(F, 4) \
+    }
+    switch (W->fmt) {
+        case FMT_Q4: PF_GEMM_FMT(FMT_Q4) break;
+        case FMT_Q2: PF_GEMM_FMT(FMT_Q2) break;
+        default: PF_GEMM_FMT(FMT_Q15) break;
+    }
+#undef PF_GEMM_FMT
+#undef PF_GEMM_CASE
+}
+
 static void launch_gemv_f32(hipStream_t st, const pf_matrix* W, uint32_t M, const float* h, uint32_t h_stride,
                             float* y, uint32_t y_stride, const float* y_in) {
     uint32_t waves = std::min<uint32_t>(W->rows, 2048);
@@ -447,12 +478,12 @@ extern "C" pf_status pf_matmul_quantized(pf_ctx* c, const float* A, const int8_t
 }
 
 extern "C" pf_status pf_gemv_q(pf_ctx* c, const pf_matrix* W, const float* x, float* y, uint32_t M) {
-    if (!c || !W || !x || !y || M == 0 || M > 8) return PF_ERR_ARG;
+    if (!c || !W || !x || !y || M == 0 || M > MAX_GEMM_ROWS) return PF_ERR_ARG;
     if (W->rowmajor) return fail(c, PF_ERR_ARG, "pf_gemv_q needs a tiled matrix");
     const uint32_t K = W->cols, N = W->rows;
     if (!per_for(K)) return fail(c, PF_ERR_UNSUPPORTED, "K > 8192");
-    size_t a_bytes = ((size_t)M * K + 255) & ~(size_t)255;
-    size_t s_bytes = 256;
+    size_t a_bytes = ((size_t)((M + 31) / 32 * 32) * K + 255) & ~(size_t)255;
+    size_t s_bytes = ((size_t)M * 4 + 255) & ~(size_t)255;
     size_t b_bytes = (((size_t)M * (K / 32) * 4) + 255) & ~(size_t)255;
     size_t c_bytes = (size_t)M * N * 8;
     void* s = nullptr;
@@ -465,7 +496,8 @@ extern "C" pf_status pf_gemv_q(pf_ctx* c, const pf_matrix* W, const float* x, fl
     hipLaunchKernelGGL(k_zero_f64, dim3((M * N + 255) / 256), dim3(256), 0, c->stream, acc, (size_t)M * N);
     PF_PER_SWITCH(K, hipLaunchKernelGGL(k_quant_rows<PER>, dim3(M), dim3(256), 0, c->stream, x, K, K, act, K, as,
                                         bsum, K / 32));
-    launch_gemv(c->stream, W, M, act, K, bsum, K / 32, acc, N);
+    if (M <= 8) launch_gemv(c->stream, W, M, act, K, bsum, K / 32, acc, N);
+    else launch_gemm(c->stream, W, M, act, K, acc, N);
     hipLaunchKernelGGL(k_gemv_finish, dim3((N + 255) / 256, M), dim3(256), 0, c->stream, acc, N, as, y);
     PF_LAUNCHED(c);
     return PF_OK;

@@ -246,3 +246,23 @@ def test_mtp_heads_standalone(gpu, with_table):
                                       .astype(np.float32) / np.float32(V))
     assert m.memory_usage() > 0
     m.close()
+
+
+@pytest.mark.parametrize("fmt", [pf.FMT_Q4, pf.FMT_Q2, pf.FMT_Q15])
+@pytest.mark.parametrize("shape", [(128, 512), (320, 2048), (64, 1792)])
+def test_gemm_int8_block(gpu, fmt, shape):
+    """The int8 MFMA GEMM (M > 8 rows: many-sequence verify, batched prefill)
+    equals the oracle's exact block GEMV row by row, bit for bit, including
+    M not a multiple of 32 and the 10 tiles of 320 rows."""
+    N, K = shape
+    codes, scales = pf.gen_matrix(98, fmt * 11 + N, 0.02, N, K, fmt)
+    W = gpu.upload_matrix(fmt, codes, scales)
+    rng = np.random.default_rng(N * 3 + K)
+    for M in (9, 32, 45, 320):
+        x = (rng.standard_normal((M, K)) * 0.5).astype(np.float32)
+        x[M // 2] = 0.0                                   # an all-zero row (scale 1, codes 0)
+        y = gpu.gemv_q(W, _t(x)).numpy()
+        for m in range(M):
+            a8, s = O.quantize_activation_row(x[m])
+            np.testing.assert_array_equal(y[m], O.gemv_i8(fmt, codes, scales, a8, s), err_msg=f"fmt {fmt} M {M} row {m}")
+    W.close()
