@@ -127,11 +127,15 @@ def main():
     prompt = W.prompt_ids(args.prompt, cfg["n_vocab"], seed=42)
     greedy = pf.Sampling(0.8, 0.95, 40, 1)
 
+    prefill_s = []
+
     def step(profile):
         eng.reset()
-        for i in range(0, args.prompt - 1, 8):
-            eng.prefill(prompt[i:min(i + 8, args.prompt - 1)])
+        t = time.perf_counter()
+        for i in range(0, args.prompt - 1, 256):
+            eng.prefill(prompt[i:min(i + 256, args.prompt - 1)])
         ctx.synchronize()
+        prefill_s.append(time.perf_counter() - t)
         eng.profile(profile)
         t = time.perf_counter()
         toks, res = eng.generate(prompt[-1:], args.new, greedy, 7)
@@ -192,6 +196,7 @@ def main():
             "mtp_accepted": sum(accs), "mtp_rejected": sum(rejs), "rounds": sum(rounds),
             "tokens_per_step": gens[0],
             "device_us_per_round": round(r_avg, 2),
+            "prefill_tok_s": round((args.prompt - 1) / min(prefill_s), 1),
             "device": dev,
         },
         "roofline": {

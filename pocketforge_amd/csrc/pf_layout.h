@@ -38,11 +38,13 @@ __host__ __device__ constexpr int code_offset(int fmt) { return fmt == FMT_Q4 ? 
 // One (layer, head) plane holds KV_SINK_ROWS sink rows, then `ring` window
 // slots (window index w lives in slot w % ring), then `pool_cap` pooled
 // rows.  K and V are separate planes of int8 [rows][head_dim] with fp32 row
-// scales [rows].  ring = window + pool_block + MAX_PASS_ROWS keeps every
-// window entry alive until it has been folded into its pooled row and lets a
-// verify pass write its pending rows without touching visible entries.
+// scales [rows].  ring = window + pool_block + (rows of the tallest pass)
+// keeps every window entry alive until it has been folded into its pooled
+// row and lets a pass write its pending rows without touching visible
+// entries.
 constexpr uint32_t KV_SINK_ROWS = 8;
-constexpr uint32_t MAX_PASS_ROWS = 8;
+constexpr uint32_t MAX_PASS_ROWS = 8;        // decode passes (verify: n_mtp + 1 rows)
+constexpr uint32_t MAX_PREFILL_ROWS = 256;   // prompt passes (int8 MFMA GEMMs)
 
 struct KvGeom {
     uint32_t n_layers, n_heads, head_dim;
@@ -64,7 +66,7 @@ struct KvPlanes {
 struct PassDesc {
     uint32_t pos0;                 // position of row 0
     uint32_t m;                    // rows in this pass
-    int32_t tok[MAX_PASS_ROWS];
+    int32_t tok[MAX_PREFILL_ROWS];
 };
 
 // Decode-loop state kept on the device.

@@ -646,7 +646,7 @@ extern "C" size_t pf_mtp_memory(const pf_mtp* m) {
 // ================================================================= KV cache
 
 static pf_status kv_geom(const pf_ctx* c, uint32_t L, uint32_t H, uint32_t hd, uint32_t sink, uint32_t win,
-                         uint32_t pool, uint32_t maxc, KvGeom* g) {
+                         uint32_t pool, uint32_t maxc, uint32_t slack, KvGeom* g) {
     if (L == 0 || H == 0 || hd == 0 || hd % 2 || hd > 128 || maxc == 0)
         return fail(c, PF_ERR_UNSUPPORTED, "KV cache needs even head_dim <= 128 and max_context > 0");
     g->n_layers = L; g->n_heads = H; g->head_dim = hd;
@@ -655,7 +655,7 @@ static pf_status kv_geom(const pf_ctx* c, uint32_t L, uint32_t H, uint32_t hd, u
     g->pool_block = std::max(1u, pool);              // src/kv_cache.cpp:34
     g->max_context = maxc;
     if (g->window < MAX_PASS_ROWS) return fail(c, PF_ERR_UNSUPPORTED, "window must hold at least 8 entries");
-    g->ring = g->window + g->pool_block + MAX_PASS_ROWS;
+    g->ring = g->window + g->pool_block + slack;
     uint32_t evictable = maxc > sink + g->window ? maxc - sink - g->window : 0;
     g->pool_cap = evictable / g->pool_block + 1;
     g->rows = KV_SINK_ROWS + g->ring + g->pool_cap;
@@ -702,7 +702,7 @@ extern "C" pf_status pf_kv_create(pf_ctx* c, const pf_kv_config* cfg, pf_kv** ou
     pf_kv* kv = new pf_kv();
     kv->ctx = c;
     pf_status s = kv_geom(c, cfg->n_layers, cfg->n_kv_heads, cfg->head_dim, cfg->sink_size, cfg->window_size,
-                          cfg->pool_block, cfg->max_context, &kv->g);
+                          cfg->pool_block, cfg->max_context, MAX_PASS_ROWS, &kv->g);
     if (!s) s = kv_alloc(c, kv->g, &kv->p, &kv->bytes);
     kv->cap = KV_SINK_ROWS + kv->g.pool_cap + kv->g.window + 1;
     if (!s) s = dalloc_t(c, &kv->io, 4 * 128);
@@ -972,11 +972,13 @@ struct pf_engine {
     float* as = nullptr;        // [4][8]
     int32_t* bsum = nullptr;
     double* acc = nullptr;      // GEMV accumulators [8][max(3D, 2F)], zero between uses
-    float* attn = nullptr;      // attention output [8][D]
     float *q = nullptr, *k = nullptr, *v = nullptr;
     float* S = nullptr;
     float* Wp = nullptr;
     uint32_t s_stride = 0, cstride = 0, kmax = 0;
+    uint32_t cmax = 0;            // longest attention list (sink + pool + window)
+    uint32_t prefill_rows = 8;    // rows of a prompt pass
+    PassDesc pd_host{};           // staging of the prompt passes' descriptors
     float *logitsA = nullptr, *hiddenA = nullptr, *logitsB = nullptr, *hiddenB = nullptr;
     float *mcur = nullptr, *mg = nullptr, *mu = nullptr, *ma = nullptr, *mlogits = nullptr;
     PassDesc *pdA = nullptr, *pdB = nullptr, *pdP = nullptr;
@@ -1003,7 +1005,6 @@ struct pf_engine {
     hipEvent_t rev0 = nullptr, rev1 = nullptr;
     double round_us = 0;
     uint32_t round_n = 0;
-    hipGraphExec_t prefill_exec = nullptr;
     SamplingCfg graph_cfg{};
     uint64_t graph_seed = 0;
     bool graph_profile = false;
@@ -1055,11 +1056,12 @@ extern "C" pf_status pf_engine_create(pf_model* m, const pf_cache_desc* cd, pf_e
     e->c = c;
     const pf_model_desc& d = m->d;
     pf_status s = kv_geom(c, d.n_layers, d.n_heads, d.head_dim, cd->sink_size, cd->window_size, cd->pool_block,
-                          cd->max_context, &e->g);
+                          cd->max_context, MAX_PREFILL_ROWS, &e->g);
     if (!s) s = kv_alloc(c, e->g, &e->kv, &e->kv_bytes);
     if (s) { delete e; return s; }
     const uint32_t D = d.n_embd, F = d.n_ff, V = d.n_vocab, H = d.n_heads, hd = d.head_dim, MR = MAX_PASS_ROWS;
-    e->rope_pos = cd->max_context + 2 * MR;
+    const uint32_t PR = MAX_PREFILL_ROWS;   // rows of the pass buffers (prompt passes)
+    e->rope_pos = cd->max_context + 2 * PR;
     {
         std::vector<float> cs, sn;
         rope_tables(hd, e->rope_pos, cs, sn);
@@ -1070,28 +1072,31 @@ extern "C" pf_status pf_engine_create(pf_model* m, const pf_cache_desc* cd, pf_e
         PF_HIP(c, hipMemcpy(e->rope_s, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
     }
     e->kmax = std::max(D, F);
-    e->pool_rows_max = (MR + e->g.pool_block - 1) / e->g.pool_block + 1;
+    e->pool_rows_max = (PR + e->g.pool_block - 1) / e->g.pool_block + 1;
+    // prompt passes: at most one window of rows, so that every pooled row a
+    // pass sees was folded from entries stored before the pass
+    e->prefill_rows = std::min(PR, e->g.window);
     const uint32_t cmax = KV_SINK_ROWS + e->g.pool_cap + e->g.window;
     if (H > 128 || (uint64_t)H * ((cmax + 1 + 255) / 256) > 2048) {
         pf_engine_destroy(e);
         return fail(c, PF_ERR_UNSUPPORTED, "heads x attention chunks exceeds 2048 (context too long for the merge)");
     }
-    e->s_stride = cmax + 8;
-    e->cstride = (cmax + 63) / 64 + 1;
+    e->cmax = cmax;
+    e->s_stride = 2 * ((cmax + 1 + 255) / 256) + 8;    // per (row, head): chunk max and sum
+    e->cstride = (cmax + 1 + 255) / 256 + 1;          // per (row, head): chunk partials
     if (const char* v = std::getenv("PF_PREFETCH_BLOCKS")) e->pf_blocks = (uint32_t)std::strtoul(v, nullptr, 10);
     if (!s) s = ealloc(e, &e->sink, 1);
-    if (!s) s = ealloc(e, &e->x, (size_t)MR * D);
-    if (!s) s = ealloc(e, &e->act, (size_t)MR * e->kmax);
-    if (!s) s = ealloc(e, &e->as, 4 * MR);
-    if (!s) s = ealloc(e, &e->bsum, (size_t)MR * (e->kmax / 32));
-    const size_t acc_n = (size_t)MR * std::max(3 * D, 2 * F);
+    if (!s) s = ealloc(e, &e->x, (size_t)PR * D);
+    if (!s) s = ealloc(e, &e->act, (size_t)PR * e->kmax);
+    if (!s) s = ealloc(e, &e->as, 4 * PR);
+    if (!s) s = ealloc(e, &e->bsum, (size_t)PR * (e->kmax / 32));
+    const size_t acc_n = (size_t)PR * std::max(3 * D, 2 * F);
     if (!s) s = ealloc(e, &e->acc, acc_n);
-    if (!s) s = ealloc(e, &e->attn, (size_t)MR * D);
-    if (!s) s = ealloc(e, &e->q, (size_t)MR * D);
-    if (!s) s = ealloc(e, &e->k, (size_t)MR * D);
-    if (!s) s = ealloc(e, &e->v, (size_t)MR * D);
-    if (!s) s = ealloc(e, &e->S, (size_t)MR * H * e->s_stride);
-    if (!s) s = ealloc(e, &e->Wp, (size_t)MR * H * e->cstride * hd);
+    if (!s) s = ealloc(e, &e->q, (size_t)PR * D);
+    if (!s) s = ealloc(e, &e->k, (size_t)PR * D);
+    if (!s) s = ealloc(e, &e->v, (size_t)PR * D);
+    if (!s) s = ealloc(e, &e->S, (size_t)PR * H * e->s_stride);
+    if (!s) s = ealloc(e, &e->Wp, (size_t)PR * H * e->cstride * hd);
     if (!s) s = ealloc(e, &e->logitsA, (size_t)MR * V);
     if (!s) s = ealloc(e, &e->hiddenA, (size_t)MR * D);
     if (!s) s = ealloc(e, &e->logitsB, (size_t)MR * V);
@@ -1133,7 +1138,6 @@ extern "C" void pf_engine_destroy(pf_engine* e) {
     for (auto& row : e->round_exec)
         for (auto& g : row)
             if (g) (void)hipGraphExecDestroy(g);
-    if (e->prefill_exec) (void)hipGraphExecDestroy(e->prefill_exec);
     if (e->rev0) (void)hipEventDestroy(e->rev0);
     if (e->rev1) (void)hipEventDestroy(e->rev1);
     for (auto& p : e->owned) dfree(e->c, p.first, p.second);
@@ -1216,20 +1220,22 @@ static pf_status pass_gemv(pf_engine* e, const pf_matrix* W, uint32_t M) {
         e->kev_bytes[e->kev_used] = (double)W->bytes + (double)M * W->cols + (double)M * W->rows * 4.0;
         TimedPass* t = &e->kev[e->kev_used++];
         launch_gemv(st, W, M, e->act, ks, e->bsum, bs, e->acc, W->rows, t->a, t->b);
-    } else {
+    } else if (M <= MAX_PASS_ROWS) {
         launch_gemv(st, W, M, e->act, ks, e->bsum, bs, e->acc, W->rows);
+    } else {
+        launch_gemm(st, W, M, e->act, ks, e->acc, W->rows);
     }
     return PF_OK;
 }
 
-// One forward pass of M rows (the PassDesc at `pd` holds positions and
-// tokens; pos0 is the host's copy of the first position).  hidden/logits
 static Prefetch prefetch_of(const pf_engine* e, const pf_matrix* W) {
     if (!e->pf_blocks) return Prefetch{nullptr, 0, e->sink};
     return Prefetch{W->data, W->bytes & ~(size_t)15, e->sink};
 }
 
-// outputs are device [M][D] / [M][V]; logits may be null.
+// One forward pass of M rows (the PassDesc at `pd` holds positions and
+// tokens; pos0 is the host's copy of the first position).  hidden/logits
+// outputs are device [M][D] / [M][V] (M <= 8 when set); either may be null.
 static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0, float* logits, float* hidden) {
     pf_ctx* c = e->c;
     const pf_model* m = e->m;
@@ -1240,7 +1246,7 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
     if (!e->capturing && pos0 + M > e->rope_pos)
         return fail(c, PF_ERR_CAPACITY, "position beyond the engine's max_context");
     // captured passes replay at any position: grids sized for the largest view
-    const uint32_t cmax = e->capturing ? e->s_stride - 8 : kv_view(g, pos0 + M - 1).count();
+    const uint32_t cmax = e->capturing ? e->cmax : kv_view(g, pos0 + M - 1).count();
     // attention tasks: (head, 256-entry chunk) groups of M rows, 8-aligned per XCD
     const uint32_t attn_groups = H * ((cmax + 1 + 255) / 256);
     const uint32_t attn_blocks = 8 * M * ((attn_groups + 7) / 8);
@@ -1294,7 +1300,10 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
 }
 
 extern "C" pf_status pf_forward(pf_engine* e, const int32_t* tokens, uint32_t n, float* logits, float* hidden) {
-    if (!e || !tokens || n == 0 || n > MAX_PASS_ROWS) return PF_ERR_ARG;
+    if (!e || !tokens || n == 0) return PF_ERR_ARG;
+    if (n > ((logits || hidden) ? MAX_PASS_ROWS : e->prefill_rows))
+        return fail(e->c, PF_ERR_ARG, "pass too tall: 8 rows with outputs, else one window up to 256 rows");
+    if (e->pos + n > e->rope_pos) return fail(e->c, PF_ERR_CAPACITY, "position beyond the engine's max_context");
     pf_ctx* c = e->c;
     const pf_model_desc& d = e->m->d;
     PassDesc pd{};
@@ -1305,7 +1314,7 @@ extern "C" pf_status pf_forward(pf_engine* e, const int32_t* tokens, uint32_t n,
         pd.tok[i] = tokens[i];
     }
     PF_HIP(c, hipMemcpyAsync(e->pdP, &pd, sizeof(pd), hipMemcpyHostToDevice, c->stream));
-    pf_status s = run_pass(e, e->pdP, n, e->pos, logits ? e->logitsA : nullptr, e->hiddenA);
+    pf_status s = run_pass(e, e->pdP, n, e->pos, logits ? e->logitsA : nullptr, hidden ? e->hiddenA : nullptr);
     if (s) return s;
     e->pos += n;
     if (logits)
@@ -1496,36 +1505,17 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
     if (n_prompt) PF_HIP(c, hipMemcpyAsync(e->tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, st));
     auto t0 = std::chrono::steady_clock::now();
     // prefill (src/engine.cpp:286-290): every prompt token forwarded in order,
-    // full 8-row passes replayed from a captured graph
-    if (e->use_graphs && n_prompt >= MAX_PASS_ROWS && !e->prefill_exec) {
-        hipGraph_t graph = nullptr;
-        PF_HIP(c, hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-        e->capturing = true;
-        pf_status s = run_pass(e, e->pdP, MAX_PASS_ROWS, 0, nullptr, e->hiddenA);
-        e->capturing = false;
-        hipError_t ee = hipStreamEndCapture(st, &graph);
-        if (s) { if (graph) (void)hipGraphDestroy(graph); return s; }
-        if (ee != hipSuccess) return fail(c, PF_ERR_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(ee));
-        ee = hipGraphInstantiate(&e->prefill_exec, graph, nullptr, nullptr, 0);
-        (void)hipGraphDestroy(graph);
-        if (ee != hipSuccess) return fail(c, PF_ERR_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(ee));
-    }
-    std::vector<PassDesc> pds((n_prompt + MAX_PASS_ROWS - 1) / MAX_PASS_ROWS);
-    for (uint32_t i = 0, j = 0; i < n_prompt; i += MAX_PASS_ROWS, j++) {
-        uint32_t n = std::min(MAX_PASS_ROWS, n_prompt - i);
-        PassDesc& pd = pds[j];
-        pd = PassDesc{};
-        pd.pos0 = e->pos;
-        pd.m = n;
-        for (uint32_t r = 0; r < n; r++) pd.tok[r] = prompt[i + r];
-        PF_HIP(c, hipMemcpyAsync(e->pdP, &pd, sizeof(pd), hipMemcpyHostToDevice, st));
-        if (n == MAX_PASS_ROWS && e->prefill_exec) {
-            PF_HIP(c, hipGraphLaunch(e->prefill_exec, st));
-            e->hidden_valid = true;
-        } else {
-            pf_status s = run_pass(e, e->pdP, n, e->pos, nullptr, e->hiddenA);
-            if (s) return s;
-        }
+    // in passes of up to one window (256 rows), whose GEMMs run on MFMA
+    for (uint32_t i = 0; i < n_prompt; i += e->prefill_rows) {
+        const uint32_t n = std::min(e->prefill_rows, n_prompt - i);
+        e->pd_host.pos0 = e->pos;
+        e->pd_host.m = n;
+        for (uint32_t r = 0; r < n; r++) e->pd_host.tok[r] = prompt[i + r];
+        PF_HIP(c, hipMemcpyAsync(e->pdP, &e->pd_host, sizeof(PassDesc), hipMemcpyHostToDevice, st));
+        // the copy reads e->pd_host before the host overwrites it for the next pass
+        PF_HIP(c, hipStreamSynchronize(st));
+        pf_status s = run_pass(e, e->pdP, n, e->pos, nullptr, nullptr);
+        if (s) return s;
         e->pos += n;
     }
     DecodeState s0{};

@@ -249,3 +249,29 @@ def test_generate_mtp_disabled(gpu, tiny_weights, samp):
     om.close()
     e.close()
     m.close()
+
+
+@pytest.mark.parametrize("kv,n,chunk", [(dict(sink_size=4, window_size=64, pool_block=6, max_context=512), 200, 64),
+                                        (dict(sink_size=4, window_size=600, pool_block=8, max_context=2048), 700, 256),
+                                        (dict(sink_size=4, window_size=600, pool_block=8, max_context=2048), 300, 37)])
+def test_batched_prefill_equals_token_by_token(gpu, tiny_weights, kv, n, chunk):
+    """Prompt passes of up to 256 rows (int8 MFMA GEMMs, one window at
+    most) leave the cache and state exactly as n single-token forwards: the
+    next forward's logits and hidden state are bit-identical to the oracle's."""
+    cfg, w = tiny_weights
+    m = pf.Model(gpu, cfg, w)
+    e = pf.Engine(m, **kv)
+    om = _oracle(cfg, w, kv)
+    toks = W.prompt_ids(n + 1, cfg["n_vocab"], seed=31)
+    for i in range(0, n, chunk):
+        e.prefill(toks[i:min(i + chunk, n)])
+    for t in toks[:n]:
+        om.forward(t)
+    assert e.pos == n
+    lg, hg = e.forward(toks[n:n + 1])
+    lo, ho = om.forward(toks[n])
+    np.testing.assert_array_equal(hg[0], ho)
+    np.testing.assert_array_equal(lg[0], lo)
+    om.close()
+    e.close()
+    m.close()
