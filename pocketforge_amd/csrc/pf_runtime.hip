@@ -3,6 +3,7 @@
 #include "pf_gemv.hip"
 #include "pf_attn.hip"
 #include "pf_ctl.hip"
+#include "pf_decode.hip"
 
 #include <hip/hip_ext.h>
 
@@ -1021,6 +1022,24 @@ struct pf_engine {
     uint32_t kev_n = 0;
     double verify_us = 0, base_us = 0;
     uint32_t verify_n = 0, base_n = 0;
+    // persistent decode passes (M <= 8 rows; PF_PERSISTENT=1 selects them
+    // over the kernel-per-step pass)
+    bool dec = false;
+    uint32_t dec_grid[MAX_PASS_ROWS + 1] = {};   // workgroups per pass height
+    uint32_t dec_bpw[4] = {};
+    DecodeLayer* dec_layers = nullptr;
+    double* dec_acc = nullptr;
+    size_t dec_acc_n = 0;
+    float* dec_stats = nullptr;
+    float* dec_o = nullptr;
+    float* dec_f = nullptr;
+    uint32_t* dec_ctr = nullptr;
+    uint32_t dec_ctr_words = 0;
+    uint32_t dec_ctr_layer = 0;
+    uint32_t* dec_err = nullptr;
+    uint64_t* dec_trace = nullptr;     // phase timestamps of the last profiled pass
+    std::string dec_trace_path;        // PF_DECODE_TRACE: where pf_generate writes them
+    uint32_t dec_trace_grid = 0;
 };
 
 template <class T>
@@ -1045,6 +1064,175 @@ static void rope_tables(uint32_t hd, uint32_t npos, std::vector<float>& cs, std:
             cs[(size_t)p * half + t] = cosf(ang);
             sn[(size_t)p * half + t] = sinf(ang);
         }
+}
+
+// ------------------------------------------------ persistent decode pass
+
+// Kernel of pass height M (1..8) and head_dim 16 * parts.
+static const void* decode_kernel(uint32_t M, uint32_t parts) {
+#define PF_DEC_K(MM)                                                                                  \
+    case MM:                                                                                          \
+        return parts == 4 ? (const void*)k_decode<MM, 4> : (const void*)k_decode<MM, 8>;
+    switch (M) {
+        PF_DEC_K(1) PF_DEC_K(2) PF_DEC_K(3) PF_DEC_K(4) PF_DEC_K(5) PF_DEC_K(6) PF_DEC_K(7) PF_DEC_K(8)
+    }
+#undef PF_DEC_K
+    return nullptr;
+}
+
+// Smallest blocks-per-wave whose (tile, split) items fit in `grid`
+// workgroups (nb % (4 bpw) == 0), else the largest that divides nb.
+static uint32_t decode_bpw(uint32_t rows, uint32_t cols, uint32_t grid) {
+    const uint32_t nb = cols / 32, tiles = rows / 64;
+    uint32_t best = 0;
+    for (uint32_t b : {1u, 2u, 4u, 8u}) {
+        if (nb % (4 * b)) continue;
+        best = b;
+        if (tiles * (nb / (4 * b)) <= grid) return b;
+    }
+    return best;
+}
+
+// Buffers, per-layer descriptors and grid sizes of the persistent pass.
+// The grid of each pass height is the number of workgroups the device
+// holds at once (at most 4 per CU; PF_DECODE_WGS caps it), so that every
+// workgroup is resident while others wait for it.
+static pf_status decode_setup(pf_engine* e) {
+    pf_ctx* c = e->c;
+    const pf_model* m = e->m;
+    const pf_model_desc& d = m->d;
+    const uint32_t D = d.n_embd, F = d.n_ff, H = d.n_heads, L = d.n_layers, MR = MAX_PASS_ROWS;
+    int cus = 0;
+    PF_HIP(c, hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device));
+    uint32_t cap = 4u * (uint32_t)cus;
+    if (const char* v = std::getenv("PF_DECODE_WGS")) cap = std::max(8u, (uint32_t)std::strtoul(v, nullptr, 10));
+    const uint32_t parts = d.head_dim / 16;
+    uint32_t gmin = cap;
+    for (uint32_t M = 1; M <= MR; M++) {
+        int occ = 0;
+        PF_HIP(c, hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, decode_kernel(M, parts), 256, 0));
+        uint32_t G = std::min(cap, (uint32_t)occ * (uint32_t)cus) & ~7u;
+        if (G < 8) return fail(c, PF_ERR_UNSUPPORTED, "decode kernel does not fit the device");
+        e->dec_grid[M] = G;
+        gmin = std::min(gmin, G);
+    }
+    e->dec_bpw[MAT_QKV] = decode_bpw(3 * D, D, gmin);
+    e->dec_bpw[MAT_O] = decode_bpw(D, D, gmin);
+    e->dec_bpw[MAT_GU] = decode_bpw(2 * F, D, gmin);
+    e->dec_bpw[MAT_DOWN] = decode_bpw(D, F, gmin);
+    std::vector<DecodeLayer> ly(L);
+    for (uint32_t l = 0; l < L; l++) {
+        const pf_matrix* w[4] = {m->qkv[l], m->o[l], m->gu[l], m->down[l]};
+        for (int j = 0; j < 4; j++) {
+            ly[l].w[j] = w[j]->data;
+            ly[l].fmt[j] = w[j]->fmt;
+        }
+        ly[l].an = m->attn_norm + (size_t)l * D;
+        ly[l].fn = m->ffn_norm + (size_t)l * D;
+    }
+    e->dec_acc_n = (size_t)MR * (3 * D + D + 2 * F + D);
+    e->dec_ctr_layer = 16 * decode_ctr_slots(H, D / 64, F / 64);
+    e->dec_ctr_words = std::max(1u, L) * e->dec_ctr_layer;
+    pf_status s = ealloc(e, &e->dec_layers, std::max(1u, L));
+    if (!s) s = ealloc(e, &e->dec_acc, e->dec_acc_n);
+    if (!s) s = ealloc(e, &e->dec_stats, (size_t)std::max(1u, L) * 2 * 16);
+    if (!s) s = ealloc(e, &e->dec_o, (size_t)MR * D);
+    if (!s) s = ealloc(e, &e->dec_f, (size_t)MR * F);
+    if (!s) s = ealloc(e, &e->dec_ctr, e->dec_ctr_words);
+    if (!s) s = ealloc(e, &e->dec_err, 16);
+    if (s) return s;
+    if (L) PF_HIP(c, hipMemcpy(e->dec_layers, ly.data(), L * sizeof(DecodeLayer), hipMemcpyHostToDevice));
+    if (const char* tp = std::getenv("PF_DECODE_TRACE")) {
+        e->dec_trace_path = tp;
+        uint32_t gmax = 0;
+        for (uint32_t M = 1; M <= MR; M++) gmax = std::max(gmax, e->dec_grid[M]);
+        s = ealloc(e, &e->dec_trace, (size_t)std::max(1u, L) * gmax * DEC_TRACE);
+        if (s) return s;
+    }
+    PF_HIP(c, hipMemset(e->dec_err, 0, 64));
+    PF_HIP(c, hipMemset(e->dec_ctr, 0, (size_t)e->dec_ctr_words * 4));
+    hipLaunchKernelGGL(k_zero_f64, dim3((e->dec_acc_n + 255) / 256), dim3(256), 0, c->stream, e->dec_acc,
+                       e->dec_acc_n);
+    PF_LAUNCHED(c);
+    return PF_OK;
+}
+
+// Algorithmic HBM bytes of one persistent pass of M rows whose last row
+// sees `count` entries: every layer matrix once, each visible K/V row once
+// (codes and scales), the int8 activations and fp32 outputs of the GEMVs.
+static double decode_pass_bytes(const pf_engine* e, uint32_t M, uint32_t count) {
+    const pf_model* m = e->m;
+    const pf_model_desc& d = m->d;
+    double b = 0;
+    for (uint32_t l = 0; l < d.n_layers; l++) {
+        const pf_matrix* w[4] = {m->qkv[l], m->o[l], m->gu[l], m->down[l]};
+        for (const pf_matrix* W : w) b += (double)W->bytes + (double)M * W->cols + (double)M * W->rows * 4.0;
+    }
+    b += (double)d.n_layers * d.n_heads * (double)count * (2.0 * d.head_dim + 8.0);
+    return b;
+}
+
+// Launches the persistent pass of M rows (after k_pool_rows and k_embed).
+static pf_status launch_decode(pf_engine* e, const PassDesc* pd, uint32_t M, hipEvent_t ev0, hipEvent_t ev1) {
+    pf_ctx* c = e->c;
+    const pf_model_desc& d = e->m->d;
+    hipStream_t st = c->stream;
+    DecodeArgs a{};
+    a.pd = pd;
+    a.g = e->g;
+    a.kv = e->kv;
+    a.layers = e->dec_layers;
+    a.rope_c = e->rope_c;
+    a.rope_s = e->rope_s;
+    a.L = d.n_layers;
+    a.D = d.n_embd;
+    a.F = d.n_ff;
+    a.H = d.n_heads;
+    a.hd = d.head_dim;
+    for (int j = 0; j < 4; j++) a.bpw[j] = e->dec_bpw[j];
+    a.x = e->x;
+    a.stats = e->dec_stats;
+    a.acc_qkv = e->dec_acc;
+    a.acc_o = a.acc_qkv + (size_t)MAX_PASS_ROWS * 3 * a.D;
+    a.acc_gu = a.acc_o + (size_t)MAX_PASS_ROWS * a.D;
+    a.acc_d = a.acc_gu + (size_t)MAX_PASS_ROWS * 2 * a.F;
+    a.q = e->q;
+    a.k = e->k;
+    a.v = e->v;
+    a.S = e->S;
+    a.Up = e->Wp;
+    a.s_stride = e->s_stride;
+    a.cstride = e->cstride;
+    a.o = e->dec_o;
+    a.f = e->dec_f;
+    a.ctr = e->dec_ctr;
+    a.ctr_layer = e->dec_ctr_layer;
+    a.err = e->dec_err;
+    a.spin_limit = 50000000ull;   // 0.5 s of the 100 MHz wall clock
+    a.trace = nullptr;
+    if (e->dec_trace && ev0) {     // profiled verify passes only
+        a.trace = e->dec_trace;
+        e->dec_trace_grid = e->dec_grid[M];
+        PF_HIP(c, hipMemsetAsync(e->dec_trace, 0, (size_t)d.n_layers * e->dec_grid[M] * DEC_TRACE * 8, st));
+    }
+    hipLaunchKernelGGL(k_zero_u32, dim3((e->dec_ctr_words + 255) / 256), dim3(256), 0, st, e->dec_ctr,
+                       e->dec_ctr_words);
+    const dim3 grid(e->dec_grid[M]);
+    const void* fn = decode_kernel(M, d.head_dim / 16);
+    void* args[] = {&a};
+    if (ev0) PF_HIP(c, hipEventRecord(ev0, st));
+    PF_HIP(c, hipLaunchKernel(fn, grid, dim3(256), args, 0, st));
+    if (ev1) PF_HIP(c, hipEventRecord(ev1, st));
+    return PF_OK;
+}
+
+// Error word of the persistent passes (a wait that timed out).
+static pf_status decode_check(pf_engine* e) {
+    if (!e->dec) return PF_OK;
+    uint32_t w = 0;
+    PF_HIP(e->c, hipMemcpy(&w, e->dec_err, 4, hipMemcpyDeviceToHost));
+    if (w) return fail(e->c, PF_ERR_HIP, "decode pass: a workgroup wait timed out (results invalid)");
+    return PF_OK;
 }
 
 extern "C" pf_status pf_engine_create(pf_model* m, const pf_cache_desc* cd, pf_engine** out) {
@@ -1119,6 +1307,14 @@ extern "C" pf_status pf_engine_create(pf_model* m, const pf_cache_desc* cd, pf_e
     PF_LAUNCHED(c);
     PF_HIP(c, hipStreamSynchronize(c->stream));
     if (const char* ng = std::getenv("PF_NO_GRAPHS")) e->use_graphs = !(ng[0] == '1');
+    {
+        const char* pv = std::getenv("PF_PERSISTENT");
+        e->dec = pv && pv[0] == '1';
+        if (e->dec && (s = decode_setup(e))) {
+            pf_engine_destroy(e);
+            return s;
+        }
+    }
     PF_HIP(c, hipEventCreate(&e->rev0));
     PF_HIP(c, hipEventCreate(&e->rev1));
     PassDesc pb{};
@@ -1261,6 +1457,32 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
     hipLaunchKernelGGL(k_pool_rows, dim3(g.n_layers * g.n_heads, e->pool_rows_max), tb, 0, st, g, e->kv, pd);
     hipLaunchKernelGGL(k_embed, dim3((D + 255) / 256, M), dim3(256), 0, st, m->emb->data, m->emb->scales, d.n_vocab, D,
                        pd, e->x);
+    if (e->dec && M <= MAX_PASS_ROWS && d.n_layers) {
+        // every layer in one persistent kernel; verify passes carry timing
+        // events in profiling mode
+        hipEvent_t ev0 = nullptr, ev1 = nullptr;
+        if (e->profile && e->in_verify && !e->capturing) {
+            if (e->kev_used == e->kev.size()) {
+                TimedPass n{};
+                PF_HIP(c, hipEventCreate(&n.a));
+                PF_HIP(c, hipEventCreate(&n.b));
+                e->kev.push_back(n);
+                e->kev_bytes.push_back(0.0);
+            }
+            e->kev_bytes[e->kev_used] = decode_pass_bytes(e, M, kv_view(g, pos0 + M - 1).count());
+            TimedPass* t = &e->kev[e->kev_used++];
+            ev0 = t->a;
+            ev1 = t->b;
+        }
+        if (pf_status s = launch_decode(e, pd, M, ev0, ev1)) return s;
+        if (hidden)
+            hipLaunchKernelGGL(k_copy_f32, dim3((M * D + 255) / 256), dim3(256), 0, st, (const float*)e->x, hidden,
+                               M * D);
+        if (logits) launch_gemv_f32(st, m->emb, M, e->x, D, logits, d.n_vocab, nullptr);
+        PF_LAUNCHED(c);
+        if (!e->capturing) e->hidden_valid = true;
+        return PF_OK;
+    }
     for (uint32_t l = 0; l < d.n_layers; l++) {
         const float* an = m->attn_norm + (size_t)l * D;
         const float* fn = m->ffn_norm + (size_t)l * D;
@@ -1321,7 +1543,7 @@ extern "C" pf_status pf_forward(pf_engine* e, const int32_t* tokens, uint32_t n,
         PF_HIP(c, hipMemcpyAsync(logits, e->logitsA, (size_t)n * d.n_vocab * 4, hipMemcpyDeviceToHost, c->stream));
     if (hidden) PF_HIP(c, hipMemcpyAsync(hidden, e->hiddenA, (size_t)n * d.n_embd * 4, hipMemcpyDeviceToHost, c->stream));
     PF_HIP(c, hipStreamSynchronize(c->stream));
-    return PF_OK;
+    return decode_check(e);
 }
 
 // MTPHeads::forward chain on the device hidden state h0 (src/mtp.cpp:63-127):
@@ -1592,6 +1814,20 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
     PF_HIP(c, hipMemcpyAsync(&sf, e->st, sizeof(sf), hipMemcpyDeviceToHost, st));
     PF_HIP(c, hipStreamSynchronize(st));
     auto t2 = std::chrono::steady_clock::now();
+    if (pf_status s = decode_check(e)) return s;
+    if (e->dec_trace && !e->dec_trace_path.empty() && e->dec_trace_grid) {
+        // header: layers, grid, words per workgroup; then the timestamps
+        const size_t n = (size_t)d.n_layers * e->dec_trace_grid * DEC_TRACE;
+        std::vector<uint64_t> buf(3 + n);
+        buf[0] = d.n_layers;
+        buf[1] = e->dec_trace_grid;
+        buf[2] = DEC_TRACE;
+        PF_HIP(c, hipMemcpy(buf.data() + 3, e->dec_trace, n * 8, hipMemcpyDeviceToHost));
+        if (FILE* fp = std::fopen(e->dec_trace_path.c_str(), "wb")) {
+            std::fwrite(buf.data(), 8, buf.size(), fp);
+            std::fclose(fp);
+        }
+    }
     if (sf.pos != e->pos) return fail(c, PF_ERR_STATE, "device and host positions diverged");
     const uint32_t nt = std::min(sf.n_tokens, tokens_cap);
     PF_HIP(c, hipMemcpy(tokens_out, e->tokens, (size_t)nt * 4, hipMemcpyDeviceToHost));
