@@ -1025,17 +1025,16 @@ struct pf_engine {
     // persistent decode passes (M <= 8 rows; PF_PERSISTENT=1 selects them
     // over the kernel-per-step pass)
     bool dec = false;
-    uint32_t dec_grid[MAX_PASS_ROWS + 1] = {};   // workgroups per pass height
-    uint32_t dec_bpw[4] = {};
+    uint32_t dec_grid = 0;             // workgroups: one per CU
     DecodeLayer* dec_layers = nullptr;
-    double* dec_acc = nullptr;
-    size_t dec_acc_n = 0;
-    float* dec_stats = nullptr;
-    float* dec_o = nullptr;
-    float* dec_f = nullptr;
+    uint8_t* dec_lbuf = nullptr;       // per-layer buffers of the pass
+    size_t dec_lstride = 0;
+    DecodeOffsets dec_off{};
+    uint32_t dec_s_stride = 0, dec_cstride = 0;
     uint32_t* dec_ctr = nullptr;
     uint32_t dec_ctr_words = 0;
     uint32_t dec_ctr_layer = 0;
+    uint32_t* dec_glob = nullptr;      // [0] workgroups done, [16] epoch
     uint32_t* dec_err = nullptr;
     uint64_t* dec_trace = nullptr;     // phase timestamps of the last profiled pass
     std::string dec_trace_path;        // PF_DECODE_TRACE: where pf_generate writes them
@@ -1080,46 +1079,42 @@ static const void* decode_kernel(uint32_t M, uint32_t parts) {
     return nullptr;
 }
 
-// Smallest blocks-per-wave whose (tile, split) items fit in `grid`
-// workgroups (nb % (4 bpw) == 0), else the largest that divides nb.
-static uint32_t decode_bpw(uint32_t rows, uint32_t cols, uint32_t grid) {
-    const uint32_t nb = cols / 32, tiles = rows / 64;
-    uint32_t best = 0;
-    for (uint32_t b : {1u, 2u, 4u, 8u}) {
-        if (nb % (4 * b)) continue;
-        best = b;
-        if (tiles * (nb / (4 * b)) <= grid) return b;
-    }
-    return best;
+// Counters at zero and the epoch at 1 (set-up, and after a failed pass).
+static pf_status decode_reset_sync(pf_engine* e) {
+    pf_ctx* c = e->c;
+    PF_HIP(c, hipStreamSynchronize(c->stream));
+    PF_HIP(c, hipMemset(e->dec_ctr, 0, (size_t)e->dec_ctr_words * 4));
+    std::vector<uint32_t> glob(32, 0u);
+    glob[16] = 1u;
+    PF_HIP(c, hipMemcpy(e->dec_glob, glob.data(), glob.size() * 4, hipMemcpyHostToDevice));
+    PF_HIP(c, hipMemset(e->dec_err, 0, 64));
+    return PF_OK;
 }
 
-// Buffers, per-layer descriptors and grid sizes of the persistent pass.
-// The grid of each pass height is the number of workgroups the device
-// holds at once (at most 4 per CU; PF_DECODE_WGS caps it), so that every
-// workgroup is resident while others wait for it.
+// Buffers, per-layer descriptors and the grid of the persistent pass: one
+// workgroup per CU (PF_DECODE_WGS lowers it), all resident at once, so a
+// workgroup that waits never holds back one that has not started.
 static pf_status decode_setup(pf_engine* e) {
     pf_ctx* c = e->c;
     const pf_model* m = e->m;
     const pf_model_desc& d = m->d;
     const uint32_t D = d.n_embd, F = d.n_ff, H = d.n_heads, L = d.n_layers, MR = MAX_PASS_ROWS;
+    if (D > DEC_MAXD || D % 256 || F % 256 || (d.head_dim != 64 && d.head_dim != 128))
+        return fail(c, PF_ERR_UNSUPPORTED, "persistent pass needs n_embd <= 2048, n_embd and n_ff multiples of 256, "
+                                           "head_dim 64 or 128");
+    if ((e->cmax + 1 + 255) / 256 > DEC_MAX_CHUNKS)
+        return fail(c, PF_ERR_UNSUPPORTED, "persistent pass: attention list longer than 256 chunks");
     int cus = 0;
     PF_HIP(c, hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device));
-    uint32_t cap = 4u * (uint32_t)cus;
-    if (const char* v = std::getenv("PF_DECODE_WGS")) cap = std::max(8u, (uint32_t)std::strtoul(v, nullptr, 10));
-    const uint32_t parts = d.head_dim / 16;
-    uint32_t gmin = cap;
+    uint32_t G = (uint32_t)cus;
+    if (const char* v = std::getenv("PF_DECODE_WGS")) G = std::max(8u, std::min(G, (uint32_t)std::strtoul(v, nullptr, 10)));
+    if (G < 8) return fail(c, PF_ERR_UNSUPPORTED, "persistent pass needs at least 8 CUs");
     for (uint32_t M = 1; M <= MR; M++) {
         int occ = 0;
-        PF_HIP(c, hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, decode_kernel(M, parts), 256, 0));
-        uint32_t G = std::min(cap, (uint32_t)occ * (uint32_t)cus) & ~7u;
-        if (G < 8) return fail(c, PF_ERR_UNSUPPORTED, "decode kernel does not fit the device");
-        e->dec_grid[M] = G;
-        gmin = std::min(gmin, G);
+        PF_HIP(c, hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, decode_kernel(M, d.head_dim / 16), 256, 0));
+        if (occ < 1) return fail(c, PF_ERR_UNSUPPORTED, "decode kernel does not fit a CU");
     }
-    e->dec_bpw[MAT_QKV] = decode_bpw(3 * D, D, gmin);
-    e->dec_bpw[MAT_O] = decode_bpw(D, D, gmin);
-    e->dec_bpw[MAT_GU] = decode_bpw(2 * F, D, gmin);
-    e->dec_bpw[MAT_DOWN] = decode_bpw(D, F, gmin);
+    e->dec_grid = G;
     std::vector<DecodeLayer> ly(L);
     for (uint32_t l = 0; l < L; l++) {
         const pf_matrix* w[4] = {m->qkv[l], m->o[l], m->gu[l], m->down[l]};
@@ -1130,31 +1125,53 @@ static pf_status decode_setup(pf_engine* e) {
         ly[l].an = m->attn_norm + (size_t)l * D;
         ly[l].fn = m->ffn_norm + (size_t)l * D;
     }
-    e->dec_acc_n = (size_t)MR * (3 * D + D + 2 * F + D);
+    // per-layer buffers, each on a 256-byte boundary; the chunk statistics
+    // of one (row, head) take a multiple of 64 floats, so that no cache line
+    // holds values of two heads
+    const uint32_t NCmax = (e->cmax + 1 + 255) / 256;
+    e->dec_s_stride = (2 * NCmax + 63) / 64 * 64;
+    e->dec_cstride = NCmax;
+    {
+        size_t o = 0;
+        auto take = [&](size_t bytes) {
+            const size_t r = o;
+            o += (bytes + 255) / 256 * 256;
+            return (uint32_t)r;
+        };
+        DecodeOffsets& f = e->dec_off;
+        f.xin = take((size_t)MR * D * 4);
+        f.xmid = take((size_t)MR * D * 4);
+        f.acc_qkv = take((size_t)MR * 3 * D * 8);
+        f.acc_o = take((size_t)MR * D * 8);
+        f.acc_gu = take((size_t)MR * 2 * F * 8);
+        f.acc_d = take((size_t)MR * D * 8);
+        f.rs = take(MR * 4);
+        f.amax_o = take((size_t)H * 8 * 4);
+        f.amax_f = take((size_t)(F / 64) * 8 * 4);
+        f.o = take((size_t)MR * D * 4);
+        f.f = take((size_t)MR * F * 4);
+        f.S = take((size_t)MR * H * e->dec_s_stride * 4);
+        f.Up = take((size_t)MR * H * e->dec_cstride * d.head_dim * 4);
+        f.stats_a = take(8 * 2 * 4);
+        f.stats_f = take(8 * 2 * 4);
+        e->dec_lstride = o;
+    }
     e->dec_ctr_layer = 16 * decode_ctr_slots(H, D / 64, F / 64);
     e->dec_ctr_words = std::max(1u, L) * e->dec_ctr_layer;
     pf_status s = ealloc(e, &e->dec_layers, std::max(1u, L));
-    if (!s) s = ealloc(e, &e->dec_acc, e->dec_acc_n);
-    if (!s) s = ealloc(e, &e->dec_stats, (size_t)std::max(1u, L) * 2 * 16);
-    if (!s) s = ealloc(e, &e->dec_o, (size_t)MR * D);
-    if (!s) s = ealloc(e, &e->dec_f, (size_t)MR * F);
+    if (!s) s = ealloc(e, &e->dec_lbuf, (size_t)std::max(1u, L) * e->dec_lstride);
     if (!s) s = ealloc(e, &e->dec_ctr, e->dec_ctr_words);
+    if (!s) s = ealloc(e, &e->dec_glob, 32);
     if (!s) s = ealloc(e, &e->dec_err, 16);
     if (s) return s;
     if (L) PF_HIP(c, hipMemcpy(e->dec_layers, ly.data(), L * sizeof(DecodeLayer), hipMemcpyHostToDevice));
     if (const char* tp = std::getenv("PF_DECODE_TRACE")) {
         e->dec_trace_path = tp;
-        uint32_t gmax = 0;
-        for (uint32_t M = 1; M <= MR; M++) gmax = std::max(gmax, e->dec_grid[M]);
-        s = ealloc(e, &e->dec_trace, (size_t)std::max(1u, L) * gmax * DEC_TRACE);
+        s = ealloc(e, &e->dec_trace, (size_t)std::max(1u, L) * G * DEC_TRACE);
         if (s) return s;
     }
-    PF_HIP(c, hipMemset(e->dec_err, 0, 64));
-    PF_HIP(c, hipMemset(e->dec_ctr, 0, (size_t)e->dec_ctr_words * 4));
-    hipLaunchKernelGGL(k_zero_f64, dim3((e->dec_acc_n + 255) / 256), dim3(256), 0, c->stream, e->dec_acc,
-                       e->dec_acc_n);
-    PF_LAUNCHED(c);
-    return PF_OK;
+    PF_HIP(c, hipMemset(e->dec_lbuf, 0, (size_t)std::max(1u, L) * e->dec_lstride));
+    return decode_reset_sync(e);
 }
 
 // Algorithmic HBM bytes of one persistent pass of M rows whose last row
@@ -1189,49 +1206,41 @@ static pf_status launch_decode(pf_engine* e, const PassDesc* pd, uint32_t M, hip
     a.F = d.n_ff;
     a.H = d.n_heads;
     a.hd = d.head_dim;
-    for (int j = 0; j < 4; j++) a.bpw[j] = e->dec_bpw[j];
     a.x = e->x;
-    a.stats = e->dec_stats;
-    a.acc_qkv = e->dec_acc;
-    a.acc_o = a.acc_qkv + (size_t)MAX_PASS_ROWS * 3 * a.D;
-    a.acc_gu = a.acc_o + (size_t)MAX_PASS_ROWS * a.D;
-    a.acc_d = a.acc_gu + (size_t)MAX_PASS_ROWS * 2 * a.F;
-    a.q = e->q;
-    a.k = e->k;
-    a.v = e->v;
-    a.S = e->S;
-    a.Up = e->Wp;
-    a.s_stride = e->s_stride;
-    a.cstride = e->cstride;
-    a.o = e->dec_o;
-    a.f = e->dec_f;
+    a.lbuf = e->dec_lbuf;
+    a.lstride = e->dec_lstride;
+    a.off = e->dec_off;
+    a.s_stride = e->dec_s_stride;
+    a.cstride = e->dec_cstride;
     a.ctr = e->dec_ctr;
     a.ctr_layer = e->dec_ctr_layer;
+    a.glob = e->dec_glob;
     a.err = e->dec_err;
-    a.spin_limit = 50000000ull;   // 0.5 s of the 100 MHz wall clock
+    a.spin_limit = 20000000ull;   // 0.2 s of the 100 MHz wall clock
     a.trace = nullptr;
     if (e->dec_trace && ev0) {     // profiled verify passes only
         a.trace = e->dec_trace;
-        e->dec_trace_grid = e->dec_grid[M];
-        PF_HIP(c, hipMemsetAsync(e->dec_trace, 0, (size_t)d.n_layers * e->dec_grid[M] * DEC_TRACE * 8, st));
+        e->dec_trace_grid = e->dec_grid;
+        PF_HIP(c, hipMemsetAsync(e->dec_trace, 0, (size_t)d.n_layers * e->dec_grid * DEC_TRACE * 8, st));
     }
-    hipLaunchKernelGGL(k_zero_u32, dim3((e->dec_ctr_words + 255) / 256), dim3(256), 0, st, e->dec_ctr,
-                       e->dec_ctr_words);
-    const dim3 grid(e->dec_grid[M]);
     const void* fn = decode_kernel(M, d.head_dim / 16);
     void* args[] = {&a};
     if (ev0) PF_HIP(c, hipEventRecord(ev0, st));
-    PF_HIP(c, hipLaunchKernel(fn, grid, dim3(256), args, 0, st));
+    PF_HIP(c, hipLaunchKernel(fn, dim3(e->dec_grid), dim3(256), args, 0, st));
     if (ev1) PF_HIP(c, hipEventRecord(ev1, st));
     return PF_OK;
 }
 
-// Error word of the persistent passes (a wait that timed out).
+// Error word of the persistent passes (a wait that timed out).  After a
+// failure the counters are reset so that the engine can run again.
 static pf_status decode_check(pf_engine* e) {
     if (!e->dec) return PF_OK;
     uint32_t w = 0;
     PF_HIP(e->c, hipMemcpy(&w, e->dec_err, 4, hipMemcpyDeviceToHost));
-    if (w) return fail(e->c, PF_ERR_HIP, "decode pass: a workgroup wait timed out (results invalid)");
+    if (w) {
+        decode_reset_sync(e);
+        return fail(e->c, PF_ERR_HIP, "decode pass: a workgroup wait timed out (results invalid)");
+    }
     return PF_OK;
 }
 
