@@ -129,11 +129,12 @@ struct LayerBufs {
 };
 
 // Phase timestamps of one workgroup in one layer (wall clock, 100 MHz).
-constexpr uint32_t DEC_TRACE = 24;
+constexpr uint32_t DEC_TRACE = 32;
 enum : uint32_t {
     TR_Q_WAIT = 0, TR_Q_NORM, TR_Q_DONE, TR_A_WAIT, TR_A_QKV, TR_A_DONE, TR_MERGE, TR_O_WAIT, TR_O_DONE,
     TR_O_FIN, TR_G_WAIT, TR_G_DONE, TR_G_FIN, TR_D_WAIT, TR_D_DONE, TR_D_FIN,
-    TR_A_KVQ, TR_A_SELF, TR_A_SCORE, TR_A_EXP, TR_A_WSUM, TR_G_NORM, TR_O_AMAX, TR_D_AMAX
+    TR_A_KVQ, TR_A_SELF, TR_A_SCORE, TR_A_EXP, TR_A_WSUM, TR_G_NORM, TR_O_AMAX, TR_D_AMAX,
+    TR_SA_BEG, TR_SA_END, TR_SF_BEG, TR_SF_END, TR_Q_STATS, TR_G_STATS, TR_M_T, TR_M_END
 };
 
 // Counter words of one layer, each in its own 64-byte slot (16 words).
@@ -485,21 +486,33 @@ __device__ __forceinline__ void item_dots(const WRaw& w, int32_t fmt, const int8
         unpack_raw(fmt, w, k, u);
         const double dk = (double)h2f((uint16_t)(w.s >> (16 * k)));
         const uint32_t b = b0 + (uint32_t)k;
+        int4 a0[M], a1[M];
+        int p[M];
 #pragma unroll
         for (int m = 0; m < M; m++) {
-            const int4 a0 = *reinterpret_cast<const int4*>(sa + m * DEC_MAXD + b * 32u);
-            const int4 a1 = *reinterpret_cast<const int4*>(sa + m * DEC_MAXD + b * 32u + 16u);
-            int p = -off * sb[m * 64 + b];
-            p = __builtin_amdgcn_sdot4((int)u[0], a0.x, p, false);
-            p = __builtin_amdgcn_sdot4((int)u[1], a0.y, p, false);
-            p = __builtin_amdgcn_sdot4((int)u[2], a0.z, p, false);
-            p = __builtin_amdgcn_sdot4((int)u[3], a0.w, p, false);
-            p = __builtin_amdgcn_sdot4((int)u[4], a1.x, p, false);
-            p = __builtin_amdgcn_sdot4((int)u[5], a1.y, p, false);
-            p = __builtin_amdgcn_sdot4((int)u[6], a1.z, p, false);
-            p = __builtin_amdgcn_sdot4((int)u[7], a1.w, p, false);
-            S[m] = __builtin_fma(dk, (double)p, S[m]);
+            a0[m] = *reinterpret_cast<const int4*>(sa + m * DEC_MAXD + b * 32u);
+            a1[m] = *reinterpret_cast<const int4*>(sa + m * DEC_MAXD + b * 32u + 16u);
+            p[m] = -off * sb[m * 64 + b];
         }
+        // the rows' integer chains interleaved (independent, exact)
+#pragma unroll
+        for (int m = 0; m < M; m++) p[m] = __builtin_amdgcn_sdot4((int)u[0], a0[m].x, p[m], false);
+#pragma unroll
+        for (int m = 0; m < M; m++) p[m] = __builtin_amdgcn_sdot4((int)u[1], a0[m].y, p[m], false);
+#pragma unroll
+        for (int m = 0; m < M; m++) p[m] = __builtin_amdgcn_sdot4((int)u[2], a0[m].z, p[m], false);
+#pragma unroll
+        for (int m = 0; m < M; m++) p[m] = __builtin_amdgcn_sdot4((int)u[3], a0[m].w, p[m], false);
+#pragma unroll
+        for (int m = 0; m < M; m++) p[m] = __builtin_amdgcn_sdot4((int)u[4], a1[m].x, p[m], false);
+#pragma unroll
+        for (int m = 0; m < M; m++) p[m] = __builtin_amdgcn_sdot4((int)u[5], a1[m].y, p[m], false);
+#pragma unroll
+        for (int m = 0; m < M; m++) p[m] = __builtin_amdgcn_sdot4((int)u[6], a1[m].z, p[m], false);
+#pragma unroll
+        for (int m = 0; m < M; m++) p[m] = __builtin_amdgcn_sdot4((int)u[7], a1[m].w, p[m], false);
+#pragma unroll
+        for (int m = 0; m < M; m++) S[m] = __builtin_fma(dk, (double)p[m], S[m]);
     }
 }
 
@@ -533,6 +546,78 @@ constexpr uint32_t DEC_IB = 3;
 __device__ __forceinline__ void item_range(uint32_t N, uint32_t w, uint32_t G, uint32_t& lo, uint32_t& hi) {
     lo = (uint32_t)(((uint64_t)w * N) / G);
     hi = (uint32_t)(((uint64_t)(w + 1) * N) / G);
+}
+
+// Tiles (of `per` items each) t0 .. t0 + DEC_IB - 1 overlapping [lo, hi):
+// thread 0 adds each tile's item count to its counter ctr(tile), every
+// atomic in flight together; bit j of the result is set when tile t0 + j
+// got its last arrival (its counter then reset for the next pass).  Call
+// after drain().
+template <class C>
+__device__ __forceinline__ uint32_t arrive_tiles(C ctr, uint32_t t0, uint32_t lo, uint32_t hi, uint32_t per,
+                                                 DecShared& sh) {
+    if (threadIdx.x == 0) {
+        uint32_t old[DEC_IB], n[DEC_IB];
+#pragma unroll
+        for (uint32_t j = 0; j < DEC_IB; j++) {
+            const uint32_t tl = t0 + j, a0 = max(lo, tl * per), a1 = min(hi, (tl + 1) * per);
+            n[j] = a1 > a0 ? a1 - a0 : 0u;
+            old[j] = n[j] ? arrive_n(ctr(tl), n[j]) : 0u;
+        }
+        uint32_t mask = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < DEC_IB; j++)
+            if (n[j] && old[j] + n[j] == per) {
+                mask |= 1u << j;
+                stc(ctr(t0 + j), 0u);
+            }
+        sh.flag = mask;
+    }
+    __syncthreads();
+    const uint32_t mask = sh.flag;
+    __syncthreads();
+    return mask;
+}
+
+// Tile of element group jj among the set bits of mask (bit j = tile t0 + j).
+__device__ __forceinline__ uint32_t nth_tile(uint32_t mask, uint32_t t0, uint32_t jj) {
+    uint32_t j = 0;
+#pragma unroll
+    for (uint32_t b = 0; b < DEC_IB; b++) {
+        if (mask & (1u << b)) {
+            if (jj == 0) j = b;
+            jj = jj == 0 ? 0xFFFFFFFFu : jj - 1u;
+        }
+    }
+    return t0 + j;
+}
+
+// xd[m][64 tile + r] = xs[...] + (float)(acc * as[m]) for the tiles of
+// mask, acc cleared (k_resid_norm_quant's residual); every load first.
+template <int M>
+__device__ __forceinline__ void finalize_resid(uint32_t mask, uint32_t t0, const float* xs, float* xd, double* acc,
+                                               uint32_t D, const DecShared& sh) {
+    constexpr uint32_t PER = (DEC_IB * M * 64 + 255) / 256;
+    const uint32_t n = __builtin_popcount(mask) * (uint32_t)M * 64u;
+    float xv[PER];
+    double av[PER];
+    size_t off[PER];
+    uint32_t mr[PER];
+#pragma unroll
+    for (uint32_t k = 0; k < PER; k++) {
+        const uint32_t e = min(threadIdx.x + 256u * k, n - 1u), jj = e / ((uint32_t)M * 64u), r = e - jj * M * 64u;
+        const uint32_t m = r >> 6, col = nth_tile(mask, t0, jj) * 64u + (r & 63u);
+        off[k] = (size_t)m * D + col;
+        mr[k] = m;
+        xv[k] = xs[off[k]];
+        av[k] = acc[off[k]];
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < PER; k++) {
+        if (threadIdx.x + 256u * k >= n) continue;
+        stc(xd + off[k], xv[k] + (float)(av[k] * (double)sh.as[mr[k]]));
+        stc(acc + off[k], 0.0);
+    }
 }
 
 // ------------------------------------------------------------ attention
@@ -749,24 +834,32 @@ __device__ __forceinline__ bool attn_item(const DecodeArgs& a, const LayerBufs& 
         for (int m = 0; m < M; m++) acc[m] = 0.0f;
 #pragma unroll 1
         for (int p = 0; p < PARTS; p++) {
+            // every read of the step first (one LDS round trip per step),
+            // then the dequantized key and the fmaf chains
             const int4 kc = *reinterpret_cast<const int4*>(&kt[t][p * 16]);
+            float4 qv[M][4];
+#pragma unroll
+            for (int m = 0; m < M; m++)
+#pragma unroll
+                for (int b4 = 0; b4 < 4; b4++) qv[m][b4] = *reinterpret_cast<const float4*>(qs + m * 128 + p * 16 + b4 * 4);
+            __builtin_amdgcn_sched_barrier(0);
             const int wv[4] = {kc.x, kc.y, kc.z, kc.w};
             float kd[16];
 #pragma unroll
             for (int b = 0; b < 16; b++) kd[b] = (float)(int8_t)((wv[b >> 2] >> (8 * (b & 3))) & 0xFF) * ks;
 #pragma unroll
             for (int m = 0; m < M; m++) {
-                // every row, live or not (no branches: the query reads stay
-                // batched); rows that are not live are ignored
+                // every row, live or not (no branches); rows that are not
+                // live are ignored
 #pragma unroll
                 for (int b4 = 0; b4 < 4; b4++) {
-                    const float4 q4 = *reinterpret_cast<const float4*>(qs + m * 128 + p * 16 + b4 * 4);
-                    acc[m] = __builtin_fmaf(q4.x, kd[4 * b4], acc[m]);
-                    acc[m] = __builtin_fmaf(q4.y, kd[4 * b4 + 1], acc[m]);
-                    acc[m] = __builtin_fmaf(q4.z, kd[4 * b4 + 2], acc[m]);
-                    acc[m] = __builtin_fmaf(q4.w, kd[4 * b4 + 3], acc[m]);
+                    acc[m] = __builtin_fmaf(qv[m][b4].x, kd[4 * b4], acc[m]);
+                    acc[m] = __builtin_fmaf(qv[m][b4].y, kd[4 * b4 + 1], acc[m]);
+                    acc[m] = __builtin_fmaf(qv[m][b4].z, kd[4 * b4 + 2], acc[m]);
+                    acc[m] = __builtin_fmaf(qv[m][b4].w, kd[4 * b4 + 3], acc[m]);
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
         __syncthreads();   // self scores published
         PF_TR(l, TR_A_SCORE);
@@ -808,24 +901,37 @@ __device__ __forceinline__ bool attn_item(const DecodeArgs& a, const LayerBufs& 
             for (int m = 0; m < M; m++) w0[m] = w1[m] = 0.0f;
             const uint32_t e_end = min(64u * sc + 64u, (nv_max + 7u) & ~7u);
             for (uint32_t e = 64u * sc; e < e_end; e += 8) {
+                // every read of the step first (one LDS round trip)
+                uint32_t cc2[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) cc2[u] = *reinterpret_cast<const uint16_t*>(&vt[e + u][i0]);
+                const float4 vs0 = *reinterpret_cast<const float4*>(vsc + e);
+                const float4 vs1 = *reinterpret_cast<const float4*>(vsc + e + 4);
+                float4 pp0[M], pp1[M];
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+                    pp0[m] = *reinterpret_cast<const float4*>(pe + m * 256 + e);
+                    pp1[m] = *reinterpret_cast<const float4*>(pe + m * 256 + e + 4);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                const float vsu[8] = {vs0.x, vs0.y, vs0.z, vs0.w, vs1.x, vs1.y, vs1.z, vs1.w};
                 float vv0[8], vv1[8];
 #pragma unroll
                 for (int u = 0; u < 8; u++) {
-                    const uint32_t cc2 = *reinterpret_cast<const uint16_t*>(&vt[e + u][i0]);
-                    const float vsu = vsc[e + u];
-                    vv0[u] = (float)(int8_t)(cc2 & 0xFFu) * vsu;
-                    vv1[u] = (float)(int8_t)(cc2 >> 8) * vsu;
+                    vv0[u] = (float)(int8_t)(cc2[u] & 0xFFu) * vsu[u];
+                    vv1[u] = (float)(int8_t)(cc2[u] >> 8) * vsu[u];
                 }
 #pragma unroll
                 for (int m = 0; m < M; m++) {
                     // rows that are not live have zero weights here
+                    const float pw[8] = {pp0[m].x, pp0[m].y, pp0[m].z, pp0[m].w, pp1[m].x, pp1[m].y, pp1[m].z, pp1[m].w};
 #pragma unroll
                     for (int u = 0; u < 8; u++) {
-                        const float pp = pe[m * 256 + e + u];
-                        w0[m] = __builtin_fmaf(pp, vv0[u], w0[m]);
-                        w1[m] = __builtin_fmaf(pp, vv1[u], w1[m]);
+                        w0[m] = __builtin_fmaf(pw[u], vv0[u], w0[m]);
+                        w1[m] = __builtin_fmaf(pw[u], vv1[u], w1[m]);
                     }
                 }
+                __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
             for (int m = 0; m < M; m++) {
@@ -878,79 +984,115 @@ __device__ __forceinline__ bool attn_item(const DecodeArgs& a, const LayerBufs& 
 // maxima, f_c = exp(m_c - max), T and U fmaf chains over c in order, out =
 // U * (1 / (T + 1e-10))); rows past the pass are written as 0.  Publishes
 // the head's output slice and row maxima, clears the head's QKV sums.
+// Every load that does not depend on another is issued first: the clears,
+// the thread's chunk partials of its outputs (first 16 chunks) and the
+// chunk statistics.
 template <int M>
-__device__ __forceinline__ void merge_head(const DecodeArgs& a, const LayerBufs& B, uint32_t h, uint32_t pos0,
-                                           uint32_t pm, uint8_t* smem, DecShared& sh) {
+__device__ __forceinline__ void merge_head(const DecodeArgs& a, const LayerBufs& B, uint32_t l, uint32_t h,
+                                           uint32_t pos0, uint32_t pm, uint8_t* smem, DecShared& sh) {
     const KvGeom& g = a.g;
     const uint32_t hd = a.hd, H = a.H, D = a.D, t = threadIdx.x, lane = t & 63u, wid = t >> 6;
-    float* ss = reinterpret_cast<float*>(smem + M_SS);   // [8][256][2]
-    float* fs = reinterpret_cast<float*>(smem + M_FS);   // [8][256]
+    float* ts = reinterpret_cast<float*>(smem + M_SS);   // [8][256] chunk sums
+    float* fs = reinterpret_cast<float*>(smem + M_FS);   // [8][256] exp factors
+    constexpr uint32_t KO = (M * 128 + 255) / 256;      // outputs per thread (head_dim <= 128)
     uint32_t nc[M];
-    uint32_t ncm = 1;
 #pragma unroll
-    for (int m = 0; m < M; m++) {
-        nc[m] = (uint32_t)m < pm ? (kv_view(g, pos0 + m).count() + 1 + 255) / 256 : 0u;
-        ncm = max(ncm, nc[m]);
+    for (int m = 0; m < M; m++) nc[m] = (uint32_t)m < pm ? (kv_view(g, pos0 + m).count() + 1 + 255) / 256 : 0u;
+    auto nc_of = [&](uint32_t m) {
+        uint32_t r = 0;
+#pragma unroll
+        for (int mm = 0; mm < M; mm++)
+            if ((uint32_t)mm == m) r = nc[mm];
+        return r;
+    };
+    // the head's QKV sums are consumed by every chunk of the head: clear
+    for (uint32_t e = t; e < (uint32_t)M * 3u * hd; e += 256u) {
+        const uint32_t m = e / (3u * hd), r = e - m * 3u * hd, part = r / hd, i = r - part * hd;
+        stc(B.acc_qkv + (size_t)m * 3 * D + (size_t)part * D + h * hd + i, 0.0);
     }
-    // chunk statistics of every row, loads issued together
-    for (uint32_t e0 = 0; e0 < (uint32_t)M * ncm; e0 += 1024u) {
+    // this thread's outputs e = t + 256 k: partials of the first 16 chunks
+    float uv[KO][16];
+#pragma unroll
+    for (uint32_t k = 0; k < KO; k++) {
+        const uint32_t e = min(t + 256u * k, (uint32_t)M * hd - 1u), m = e / hd, i = e - m * hd;
+        const uint32_t ncr = max(nc_of(m), 1u);
+        const float* up = B.Up + ((size_t)m * H + h) * a.cstride * hd + i;
+#pragma unroll
+        for (uint32_t c = 0; c < 16; c++) uv[k][c] = up[(size_t)min(c, ncr - 1u) * hd];
+    }
+    // chunk statistics: wave w takes rows w, w + 4, lane = chunk
+    for (uint32_t m = wid; m < (uint32_t)M; m += 4) {
+        const uint32_t ncr = nc_of(m);
+        if (ncr == 0) continue;
+        const float* st = B.S + ((size_t)m * H + h) * a.s_stride;
         float mv[4], tv[4];
-        // unconditional loads (indices clamped into the row's buffer; values
-        // of chunks a row does not have are never read)
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const uint32_t e = min(e0 + t + 256u * k, (uint32_t)M * ncm - 1u), m = e / ncm, cix = e - m * ncm;
-            const float* st = B.S + ((size_t)m * H + h) * a.s_stride + 2 * cix;
-            mv[k] = st[0];
-            tv[k] = st[1];
+        for (int gi = 0; gi < 4; gi++) {
+            const uint32_t c = min(lane + 64u * gi, ncr - 1u);
+            mv[gi] = st[2 * c];
+            tv[gi] = st[2 * c + 1];
         }
+        float mx = -__builtin_inff();
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const uint32_t e = e0 + t + 256u * k, m = e / ncm, cix = e - m * ncm;
-            if (e < (uint32_t)M * ncm) {
-                ss[(m * 256 + cix) * 2] = mv[k];
-                ss[(m * 256 + cix) * 2 + 1] = tv[k];
+        for (int gi = 0; gi < 4; gi++)
+            if (lane + 64u * gi < ncr) mx = fmaxf(mx, mv[gi]);
+        mx = wave_max(mx);
+#pragma unroll
+        for (int gi = 0; gi < 4; gi++) {
+            const uint32_t c = lane + 64u * gi;
+            if (c < ncr) {
+                fs[m * 256 + c] = expf_c(mv[gi] - mx);
+                ts[m * 256 + c] = tv[gi];
             }
         }
     }
     __syncthreads();
-    // per row (one wave): max, f_c, T chain
-    for (uint32_t m = wid; m < (uint32_t)M; m += 4) {
-        uint32_t ncr = 0;
+    // T chains in chunk order (thread m < M), 16 values per LDS round trip
+    if (t < (uint32_t)M) {
+        const uint32_t ncr = nc_of(t);
+        float T = 0.0f;
+        for (uint32_t c0 = 0; c0 < ncr; c0 += 16) {
+            float tq[16], fq[16];
 #pragma unroll
-        for (int mm = 0; mm < M; mm++)
-            if ((uint32_t)mm == m) ncr = nc[mm];
-        if (ncr == 0) continue;
-        float mx = -__builtin_inff();
-        for (uint32_t cix = lane; cix < ncr; cix += 64) mx = fmaxf(mx, ss[(m * 256 + cix) * 2]);
-        mx = wave_max(mx);
-        for (uint32_t cix = lane; cix < ncr; cix += 64) fs[m * 256 + cix] = expf_c(ss[(m * 256 + cix) * 2] - mx);
-        if (lane == 0) {
-            float T = 0.0f;
-            for (uint32_t cix = 0; cix < ncr; cix++) T = __builtin_fmaf(ss[(m * 256 + cix) * 2 + 1], fs[m * 256 + cix], T);
-            sh.hinv[m] = 1.0f / (T + 1e-10f);
+            for (int k = 0; k < 16; k++) {
+                tq[k] = ts[t * 256 + min(c0 + k, 255u)];
+                fq[k] = fs[t * 256 + min(c0 + k, 255u)];
+            }
+#pragma unroll
+            for (int k = 0; k < 16; k++)
+                if (c0 + k < ncr) T = __builtin_fmaf(tq[k], fq[k], T);
         }
+        sh.hinv[t] = 1.0f / (T + 1e-10f);
     }
     __syncthreads();
-    // U chains: output e = m * hd + i; loads in batches of 16 chunks
+    PF_TR(l, TR_M_T);
+    // U chains in chunk order
     float wmax[M];
 #pragma unroll
     for (int m = 0; m < M; m++) wmax[m] = 0.0f;
-    for (uint32_t e = t; e < (uint32_t)M * hd; e += 256u) {
-        const uint32_t m = e / hd, i = e - m * hd;
-        uint32_t ncr = 0;
 #pragma unroll
-        for (int mm = 0; mm < M; mm++)
-            if ((uint32_t)mm == m) ncr = nc[mm];
-        const float* up = B.Up + ((size_t)m * H + h) * a.cstride * hd + i;
+    for (uint32_t k = 0; k < KO; k++) {
+        const uint32_t e = t + 256u * k;
+        if (e >= (uint32_t)M * hd) continue;
+        const uint32_t m = e / hd, i = e - m * hd, ncr = nc_of(m);
+        float fq[16];
+#pragma unroll
+        for (int c = 0; c < 16; c++) fq[c] = fs[m * 256 + c];
         float U = 0.0f;
-        for (uint32_t c0 = 0; c0 < ncr; c0 += 16) {
-            float uv[16];
 #pragma unroll
-            for (int k = 0; k < 16; k++) uv[k] = up[(size_t)min(c0 + k, ncr - 1u) * hd];
+        for (uint32_t c = 0; c < 16; c++)
+            if (c < ncr) U = __builtin_fmaf(uv[k][c], fq[c], U);
+        const float* up = B.Up + ((size_t)m * H + h) * a.cstride * hd + i;
+        for (uint32_t c0 = 16; c0 < ncr; c0 += 16) {
+            float u2[16];
 #pragma unroll
-            for (int k = 0; k < 16; k++)
-                if (c0 + k < ncr) U = __builtin_fmaf(uv[k], fs[m * 256 + c0 + k], U);
+            for (int c = 0; c < 16; c++) {
+                u2[c] = up[(size_t)min(c0 + c, ncr - 1u) * hd];
+                fq[c] = fs[m * 256 + min(c0 + c, 255u)];
+            }
+#pragma unroll
+            for (uint32_t c = 0; c < 16; c++)
+                if (c0 + c < ncr) U = __builtin_fmaf(u2[c], fq[c], U);
         }
         const float val = ncr ? U * sh.hinv[m] : 0.0f;
         stc(B.o + (size_t)m * D + h * hd + i, val);
@@ -962,11 +1104,6 @@ __device__ __forceinline__ void merge_head(const DecodeArgs& a, const LayerBufs&
     for (int m = 0; m < M; m++) {
         const float w = wave_max(wmax[m]);
         if (lane == 0) sh.red[wid][m] = w;
-    }
-    // the head's QKV sums are consumed by every chunk of the head: clear
-    for (uint32_t e = t; e < (uint32_t)M * 3u * hd; e += 256u) {
-        const uint32_t m = e / (3u * hd), r = e - m * 3u * hd, part = r / hd, i = r - part * hd;
-        stc(B.acc_qkv + (size_t)m * 3 * D + (size_t)part * D + h * hd + i, 0.0);
     }
     __syncthreads();
     if (t < (uint32_t)M)
@@ -1049,7 +1186,9 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a0) {
         // ---------------------------------------------------------- norm
         if (wg < 8u) {
             if (l > 0 && !wait_ge(cc.x_ready(), TD * E, a, sh)) return;
+            PF_TR(l, TR_SA_BEG);
             stats_step<M>(B.xin, Ly.an, D, B.stats_a, cc.stats_a(), sh);
+            PF_TR(l, TR_SA_END);
         }
         // ---------------------------------------------------------- QKV
         {
@@ -1065,6 +1204,7 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a0) {
                 PF_TR(l, TR_Q_WAIT);
                 if (!wait_ge(cc.stats_a(), 8u * E, a, sh)) return;
                 load_stats<M>(B.stats_a, sh);
+                PF_TR(l, TR_Q_STATS);
                 // codes of the slices of this workgroup's items
                 for (uint32_t it = lo; it < hi; it++)
                     if (it == lo || it % NS != (it - 1) % NS) norm_slice<M>(B.xin, Ly.an, D, 256 * (it % NS), sa, sb, sh);
@@ -1120,7 +1260,7 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a0) {
             drain();
             PF_TR(l, TR_A_DONE);
             if (arrive_last(cc.att_cnt(h), 1u, NC, sh)) {
-                merge_head<M>(a, B, h, pos0, pm, smem, sh);
+                merge_head<M>(a, B, l, h, pos0, pm, smem, sh);
                 if (t == 0) stc(cc.att_cnt(h), 0u);
                 drain();
                 PF_TR(l, TR_MERGE);
@@ -1177,20 +1317,13 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a0) {
                 drain();
                 PF_TR(l, TR_O_DONE);
                 // per tile: the last split adds the tile to the residual rows
-                for (uint32_t tile = lo / NS; tile <= (hi - 1) / NS; tile++) {
-                    const uint32_t n = min(hi, (tile + 1) * NS) - max(lo, tile * NS);
-                    if (arrive_last(cc.o_tile(tile), n, NS, sh)) {
-                        for (uint32_t e = t; e < (uint32_t)M * 64u; e += 256u) {
-                            const uint32_t m = e >> 6, col = tile * 64u + (e & 63u);
-                            double* ap = B.acc_o + (size_t)m * D + col;
-                            const float xn = B.xin[(size_t)m * D + col] + (float)(*ap * (double)sh.as[m]);
-                            stc(B.xmid + (size_t)m * D + col, xn);
-                            stc(ap, 0.0);
-                        }
-                        if (t == 0) stc(cc.o_tile(tile), 0u);
+                for (uint32_t t0 = lo / NS; t0 <= (hi - 1) / NS; t0 += DEC_IB) {
+                    const uint32_t mask = arrive_tiles([&](uint32_t x) { return cc.o_tile(x); }, t0, lo, hi, NS, sh);
+                    if (mask) {
+                        finalize_resid<M>(mask, t0, B.xin, B.xmid, B.acc_o, D, sh);
                         drain();
                         PF_TR(l, TR_O_FIN);
-                        if (t == 0) arrive_n(cc.xmid(), 1u);
+                        if (t == 0) arrive_n(cc.xmid(), __builtin_popcount(mask));
                     }
                 }
             }
@@ -1198,7 +1331,9 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a0) {
         // ---------------------------------------------------------- FFN norm
         if (wg < 8u) {
             if (!wait_ge(cc.xmid(), TD * E, a, sh)) return;
+            PF_TR(l, TR_SF_BEG);
             stats_step<M>(B.xmid, Ly.fn, D, B.stats_f, cc.stats_f(), sh);
+            PF_TR(l, TR_SF_END);
         }
         // ---------------------------------------------------------- gate|up
         {
@@ -1217,6 +1352,7 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a0) {
                 PF_TR(l, TR_G_WAIT);
                 if (!wait_ge(cc.stats_f(), 8u * E, a, sh)) return;
                 load_stats<M>(B.stats_f, sh);
+                PF_TR(l, TR_G_STATS);
                 for (uint32_t it = lo; it < hi; it++)
                     if (it == lo || it % NS != (it - 1) % NS) norm_slice<M>(B.xmid, Ly.fn, D, 256 * (it % NS), sa, sb, sh);
                 PF_TR(l, TR_G_NORM);
@@ -1250,31 +1386,42 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a0) {
                 }
                 drain();
                 PF_TR(l, TR_G_DONE);
-                for (uint32_t p = lo / NS; p <= (hi - 1) / NS; p++) {
-                    const uint32_t n = min(hi, (p + 1) * NS) - max(lo, p * NS);
-                    if (arrive_last(cc.gu_pair(p), n, NS, sh)) {
-                        // SwiGLU of columns [64p, 64p + 64) (k_swiglu_quant's
-                        // arithmetic); wave w takes rows w, w + 4
-                        for (uint32_t m = wid; m < (uint32_t)M; m += 4) {
-                            const uint32_t col = p * 64u + lane;
-                            double* gp = B.acc_gu + (size_t)m * 2 * F + col;
-                            const double ga = gp[0], ua = gp[F];
-                            stc(gp, 0.0);
-                            stc(gp + F, 0.0);
-                            const double as = (double)sh.as[m];
-                            const float gt = (float)(ga * as);
-                            const float uu = (float)(ua * as);
-                            const float sig = 1.0f / (1.0f + expf_c(-gt));
-                            const float fv = gt * sig * uu;
-                            stc(B.f + (size_t)m * F + col, fv);
-                            const float wm = wave_max(fabsf(fv));
-                            if (lane == 0) stc(B.amax_f + p * 8u + m, wm);
-                        }
-                        if (t == 0) stc(cc.gu_pair(p), 0u);
-                        drain();
-                        PF_TR(l, TR_G_FIN);
-                        if (t == 0) arrive_n(cc.pairs(), 1u);
+                for (uint32_t t0 = lo / NS; t0 <= (hi - 1) / NS; t0 += DEC_IB) {
+                    const uint32_t mask = arrive_tiles([&](uint32_t x) { return cc.gu_pair(x); }, t0, lo, hi, NS, sh);
+                    if (!mask) continue;
+                    // SwiGLU of the columns [64p, 64p + 64) of every last-
+                    // arrived pair p (k_swiglu_quant's arithmetic); wave w
+                    // takes (pair, row) combinations w, w + 4, ...; loads first
+                    constexpr uint32_t KC = (DEC_IB * M + 3) / 4;
+                    const uint32_t ncb = __builtin_popcount(mask) * (uint32_t)M;
+                    double ga[KC], ua[KC];
+#pragma unroll
+                    for (uint32_t k = 0; k < KC; k++) {
+                        const uint32_t c = min(wid + 4u * k, ncb - 1u), m = c % M;
+                        const uint32_t col = nth_tile(mask, t0, c / M) * 64u + lane;
+                        ga[k] = B.acc_gu[(size_t)m * 2 * F + col];
+                        ua[k] = B.acc_gu[(size_t)m * 2 * F + F + col];
                     }
+#pragma unroll
+                    for (uint32_t k = 0; k < KC; k++) {
+                        const uint32_t c = wid + 4u * k;
+                        if (c >= ncb) continue;   // wave-uniform
+                        const uint32_t m = c % M, p = nth_tile(mask, t0, c / M), col = p * 64u + lane;
+                        double* gp = B.acc_gu + (size_t)m * 2 * F + col;
+                        stc(gp, 0.0);
+                        stc(gp + F, 0.0);
+                        const double as = (double)sh.as[m];
+                        const float gt = (float)(ga[k] * as);
+                        const float uu = (float)(ua[k] * as);
+                        const float sig = 1.0f / (1.0f + expf_c(-gt));
+                        const float fv = gt * sig * uu;
+                        stc(B.f + (size_t)m * F + col, fv);
+                        const float wm = wave_max(fabsf(fv));
+                        if (lane == 0) stc(B.amax_f + p * 8u + m, wm);
+                    }
+                    drain();
+                    PF_TR(l, TR_G_FIN);
+                    if (t == 0) arrive_n(cc.pairs(), __builtin_popcount(mask));
                 }
             }
         }
@@ -1327,20 +1474,13 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a0) {
                 }
                 drain();
                 PF_TR(l, TR_D_DONE);
-                for (uint32_t tile = lo / NSF; tile <= (hi - 1) / NSF; tile++) {
-                    const uint32_t n = min(hi, (tile + 1) * NSF) - max(lo, tile * NSF);
-                    if (arrive_last(cc.d_tile(tile), n, NSF, sh)) {
-                        for (uint32_t e = t; e < (uint32_t)M * 64u; e += 256u) {
-                            const uint32_t m = e >> 6, col = tile * 64u + (e & 63u);
-                            double* ap = B.acc_d + (size_t)m * D + col;
-                            const float xn = B.xmid[(size_t)m * D + col] + (float)(*ap * (double)sh.as[m]);
-                            stc(B.xout + (size_t)m * D + col, xn);
-                            stc(ap, 0.0);
-                        }
-                        if (t == 0) stc(cc.d_tile(tile), 0u);
+                for (uint32_t t0 = lo / NSF; t0 <= (hi - 1) / NSF; t0 += DEC_IB) {
+                    const uint32_t mask = arrive_tiles([&](uint32_t x) { return cc.d_tile(x); }, t0, lo, hi, NSF, sh);
+                    if (mask) {
+                        finalize_resid<M>(mask, t0, B.xmid, B.xout, B.acc_d, D, sh);
                         drain();
                         PF_TR(l, TR_D_FIN);
-                        if (t == 0 && l + 1 < a.L) arrive_n(a.ctr + (size_t)(l + 1) * a.ctr_layer, 1u);
+                        if (t == 0 && l + 1 < a.L) arrive_n(a.ctr + (size_t)(l + 1) * a.ctr_layer, __builtin_popcount(mask));
                     }
                 }
             }
