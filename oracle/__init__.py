@@ -82,6 +82,7 @@ def lib():
         L.orc_dot_canon.argtypes = [f32p, f32p, C.c_uint32]
         L.orc_softmax.argtypes = [f32p, C.c_uint32]
         L.orc_rmsnorm.argtypes = [f32p, f32p, f32p, C.c_uint32]
+        L.orc_engine_rmsnorm.argtypes = [f32p, f32p, f32p, C.c_uint32]
         L.orc_gemv_f32_dense.argtypes = [f32p, C.c_uint32, C.c_uint32, f32p, f32p]
         L.orc_mtp_heads_forward.argtypes = [C.POINTER(QMat), C.c_uint32, C.c_uint32, C.c_uint32, f32p, f32p, f32p]
         L.orc_canon_sum.restype = C.c_float

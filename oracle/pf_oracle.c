@@ -305,6 +305,27 @@ void orc_rmsnorm(float* out, const float* x, const float* w, uint32_t n) {
     for (uint32_t i = 0; i < n; i++) out[i] = x[i] * inv * w[i];
 }
 
+/* The engine's RMSNorm (src/engine.cpp:515-523, 526-541 calling
+ * src/matmul_neon.cpp:231-239): the same formula in the tile-canonical
+ * order of the GPU pass.  The sum of squares is the sequential sum, tile
+ * by tile, of each 64-element tile's halving tree of x * x (offsets 32, 16,
+ * ..., 1); the normed value is (x * w) * inv.  n % 64 == 0.  Because
+ * rounding is monotone, max |out| = fl(max |fl(x * w)| * inv), so the
+ * row maximum needed by quantize_activation_row also decomposes by tile. */
+void orc_engine_rmsnorm(float* out, const float* x, const float* w, uint32_t n) {
+    float ss = 0.0f;
+    for (uint32_t t = 0; t < n / 64; t++) {
+        float L[64];
+        for (uint32_t l = 0; l < 64; l++) L[l] = x[64 * t + l] * x[64 * t + l];
+        for (uint32_t off = 32; off >= 1; off >>= 1)
+            for (uint32_t l = 0; l < off; l++) L[l] = L[l] + L[l + off];
+        ss = ss + L[0];
+    }
+    float rms = sqrtf(ss / (float)n + 1e-6f);
+    float inv = 1.0f / rms;
+    for (uint32_t i = 0; i < n; i++) out[i] = (x[i] * w[i]) * inv;
+}
+
 /* ============================================== block-quantized matrices */
 
 uint32_t orc_block_bytes(int32_t fmt) { return fmt == ORC_Q4 ? 16u : 8u; }
@@ -901,7 +922,7 @@ void orc_forward(orc_engine* e, int32_t token, float* logits, float* hidden) {
         const orc_qmat* W = d->layers + (size_t)l * 7;
         float as;
         /* attention block (src/engine.cpp:515-523, 646-799) */
-        orc_rmsnorm(e->normed, h, d->attn_norm + (size_t)l * D, D);
+        orc_engine_rmsnorm(e->normed, h, d->attn_norm + (size_t)l * D, D);
         orc_quantize_activation_row(e->normed, e->a8, &as, D);
         orc_gemv_i8(&W[0], e->a8, as, e->q);
         orc_gemv_i8(&W[1], e->a8, as, e->k);
@@ -925,7 +946,7 @@ void orc_forward(orc_engine* e, int32_t token, float* logits, float* hidden) {
         orc_gemv_i8(&W[3], e->a8, as, e->o);
         for (uint32_t i = 0; i < D; i++) h[i] += e->o[i];
         /* FFN block (src/engine.cpp:526-541, 805-843) */
-        orc_rmsnorm(e->normed, h, d->ffn_norm + (size_t)l * D, D);
+        orc_engine_rmsnorm(e->normed, h, d->ffn_norm + (size_t)l * D, D);
         orc_quantize_activation_row(e->normed, e->a8, &as, D);
         orc_gemv_i8(&W[4], e->a8, as, e->g);
         orc_gemv_i8(&W[5], e->a8, as, e->u);

@@ -48,6 +48,7 @@ float orc_canon_sumsq(const float* x, uint32_t n, uint32_t waves);
 void  orc_softmax(float* v, uint32_t n);                     /* canonical, own exp */
 float orc_dot_canon(const float* a, const float* b, uint32_t n);  /* CANON(4) of products */
 void  orc_rmsnorm(float* out, const float* x, const float* w, uint32_t n);
+void  orc_engine_rmsnorm(float* out, const float* x, const float* w, uint32_t n);
 
 /* ------------------------------------------------- block-quant matrices */
 enum { ORC_Q4 = 0, ORC_Q2 = 1, ORC_Q15 = 2 };

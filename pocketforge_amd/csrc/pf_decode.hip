@@ -124,8 +124,9 @@ struct LayerBufs {
     float* f;                    // [8][F] SwiGLU output
     float* S;                    // [8][H][s_stride] chunk max / sum
     float* Up;                   // [8][H][cstride][hd] chunk partials
-    float* stats_a;              // [8][2]: 1 / rms and normed row maximum of xin
-    float* stats_f;              // [8][2]: the same for xmid (its own 256-byte slot)
+    float* stats_a;              // [D / 64][8][2] tile statistics of xin (tree of x * x, max |x * w|)
+    float* stats_f;              // the same for xmid
+    float* stats_next;           // stats_a of the next layer (null in the last layer)
 };
 
 // Phase timestamps of one workgroup in one layer (wall clock, 100 MHz).
@@ -139,7 +140,7 @@ enum : uint32_t {
 
 // Counter words of one layer, each in its own 64-byte slot (16 words).
 // Polled (grow by a fixed count per pass): x_ready, head_cnt, heads_done,
-// xmid, pairs, stats_a, stats_f.  Last-arrival only (reset by the last arrival): att_cnt,
+// xmid, pairs.  Last-arrival only (reset by the last arrival): att_cnt,
 // o_tile, gu_pair, d_tile.
 struct Ctr {
     uint32_t* base;
@@ -154,11 +155,9 @@ struct Ctr {
     __device__ uint32_t* gu_pair(uint32_t p) const { return slot(3 + 2 * H + TD + p); }
     __device__ uint32_t* pairs() const { return slot(3 + 2 * H + TD + TF); }
     __device__ uint32_t* d_tile(uint32_t t) const { return slot(4 + 2 * H + TD + TF + t); }
-    __device__ uint32_t* stats_a() const { return slot(4 + 2 * H + 2 * TD + TF); }
-    __device__ uint32_t* stats_f() const { return slot(5 + 2 * H + 2 * TD + TF); }
 };
 __host__ __device__ constexpr uint32_t decode_ctr_slots(uint32_t H, uint32_t TD, uint32_t TF) {
-    return 6 + 2 * H + 2 * TD + TF;
+    return 4 + 2 * H + 2 * TD + TF;
 }
 
 // ------------------------------------------------------------ shared memory
@@ -172,6 +171,8 @@ __host__ __device__ constexpr uint32_t decode_ctr_slots(uint32_t H, uint32_t TD,
 //         [256][144]
 //   MERGE chunk maxima and sums [8][256][2], exp factors [8][256]
 constexpr uint32_t DEC_MAXD = 2048;
+// Items per prefetch batch (weights of a batch are loaded before the wait).
+constexpr uint32_t DEC_IB = 3;
 constexpr uint32_t G_SA = 0;
 constexpr uint32_t G_SB = 8 * DEC_MAXD;                        // 16384
 constexpr uint32_t G_RED = G_SB + 8 * 64 * 4;                 // 18432
@@ -271,51 +272,52 @@ __device__ __forceinline__ void block_sums(const int8_t* sa, int32_t* sb, uint32
     }
 }
 
-// RMSNorm statistics of one row x[D] with k_resid_norm_quant's arithmetic:
-// CANON(4) sum of squares (canonical lane t < 256 takes elements t, t + 256,
-// ... with an fmaf chain; wave trees; (W0 + W2) + (W1 + W3)), inv = 1 /
-// sqrt(ss / D + 1e-6), and the maximum of |(x * inv) * w| over the row
-// (quantize_activation_row's amax, src/matmul_neon.cpp:16-29, of the normed
-// row).  Every load is issued before any use.  Returns inv and amax to
-// every thread.
-__device__ __forceinline__ void row_stats(const float* x, const float* w, uint32_t D, DecShared& sh, float& inv,
-                                          float& amax) {
-    const uint32_t t = threadIdx.x, lane = t & 63u, nk = D >> 8;   // D % 256 == 0, <= 2048
-    const uint32_t q = __builtin_amdgcn_readfirstlane(t >> 6);
-    float xv[8], wt[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const uint32_t i = t + 256u * min((uint32_t)k, nk - 1u);   // past D: re-read, ignored
-        xv[k] = x[i];
-        wt[k] = w[i];
+// The engine's RMSNorm (src/matmul_neon.cpp:231-239) in tile-canonical
+// order, as k_resid_norm_quant computes it: the sum of squares of a row is
+// the sequential sum over its 64-column tiles of each tile's halving tree
+// of x * x, normed = (x * w) * inv, and quantize_activation_row's row
+// maximum is fl(max |fl(x * w)| * inv) (rounding is monotone).  The wave
+// holding (tile, row) with lane = column publishes the tile's tree and
+// max |x * w| to st[tile][row].
+__device__ __forceinline__ void tile_stat(float xv, float wv, float* st, uint32_t tile, uint32_t m) {
+    const float s = wave_tree_sum(xv * xv);
+    const float a = wave_max(fabsf(xv * wv));
+    if ((threadIdx.x & 63u) == 0) {
+        stc(st + (tile * 8u + m) * 2u, s);
+        stc(st + (tile * 8u + m) * 2u + 1u, a);
     }
-    float part = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 8; k++)
-        if ((uint32_t)k < nk) part = __builtin_fmaf(xv[k], xv[k], part);
-    const float W = wave_tree_sum(part);
-    if (lane == 0) sh.red[q][0] = W;
-    __syncthreads();
-    const float ss = (sh.red[0][0] + sh.red[2][0]) + (sh.red[1][0] + sh.red[3][0]);
-    inv = 1.0f / __builtin_sqrtf(ss / (float)D + 1e-6f);
-    float am = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 8; k++)
-        if ((uint32_t)k < nk) am = fmaxf(am, fabsf(xv[k] * inv * wt[k]));
-    am = wave_max(am);
-    if (lane == 0) sh.red2[q][0] = am;
-    __syncthreads();
-    amax = fmaxf(fmaxf(fmaxf(sh.red2[0][0], sh.red2[1][0]), sh.red2[2][0]), sh.red2[3][0]);
-    __syncthreads();
 }
 
-// Row factors from published statistics st[m] = {inv, amax}: sh.inv,
+// Row factors from the tile statistics st[TD][8][2] (complete): sh.inv,
 // sh.invq = 127 / amax, sh.as = amax / 127 (1 when amax is 0).
 template <int M>
-__device__ __forceinline__ void load_stats(const float* st, DecShared& sh) {
+__device__ __forceinline__ void combine_stats(const float* st, uint32_t TD, uint32_t D, DecShared& sh) {
     const uint32_t t = threadIdx.x;
+    if (t < TD * 8u) {
+        const float2 v = *reinterpret_cast<const float2*>(st + 2u * t);
+        sh.am[2u * t] = v.x;
+        sh.am[2u * t + 1u] = v.y;
+    }
+    __syncthreads();
     if (t < (uint32_t)M) {
-        const float inv = st[2 * t], amax = st[2 * t + 1];
+        float ss = 0.0f, ax = 0.0f;
+        for (uint32_t t0 = 0; t0 < TD; t0 += 16) {
+            float sv[16], av[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const uint32_t tl = min(t0 + k, TD - 1u);
+                sv[k] = sh.am[(tl * 8u + t) * 2u];
+                av[k] = sh.am[(tl * 8u + t) * 2u + 1u];
+            }
+#pragma unroll
+            for (int k = 0; k < 16; k++)
+                if (t0 + k < TD) {
+                    ss = ss + sv[k];
+                    ax = fmaxf(ax, av[k]);
+                }
+        }
+        const float inv = 1.0f / __builtin_sqrtf(ss / (float)D + 1e-6f);
+        const float amax = ax * inv;
         sh.inv[t] = inv;
         sh.invq[t] = (amax == 0.0f) ? 1.0f : 127.0f / amax;
         sh.as[t] = (amax == 0.0f) ? 1.0f : amax / 127.0f;
@@ -323,42 +325,32 @@ __device__ __forceinline__ void load_stats(const float* st, DecShared& sh) {
     __syncthreads();
 }
 
-// Codes of the 256-column slice at col0 of the normed rows (x[m] * inv[m])
-// * w with the row factors in sh: thread t takes column col0 + t of every
-// row (loads first).  Codes to sa[m][DEC_MAXD] at col0, then the slice's
-// 32-block sums to sb.  Ends with a barrier.
+// Codes of the 256-column slices [col0_i, col0_i + 256) of the normed rows
+// (x[m] * w) * inv[m] with the row factors in sh: thread t takes column t
+// of every slice and row (every load first).  Codes to sa[m][DEC_MAXD],
+// then the slices' 32-block sums to sb.  Ends with a barrier.
 template <int M>
-__device__ __forceinline__ void norm_slice(const float* x, const float* w, uint32_t D, uint32_t col0, int8_t* sa,
-                                           int32_t* sb, DecShared& sh) {
+__device__ __forceinline__ void norm_slices(const float* x, const float* w, uint32_t D, const uint32_t (&col0)[DEC_IB],
+                                            uint32_t ns, int8_t* sa, int32_t* sb, DecShared& sh) {
     const uint32_t t = threadIdx.x;
-    float v[M];
+    float v[DEC_IB][M], wv[DEC_IB];
 #pragma unroll
-    for (int m = 0; m < M; m++) v[m] = x[(size_t)m * D + col0 + t];
-    const float wv = w[col0 + t];
+    for (uint32_t i = 0; i < DEC_IB; i++) {
+        const uint32_t c = col0[min(i, ns - 1u)] + t;
 #pragma unroll
-    for (int m = 0; m < M; m++) sa[m * DEC_MAXD + col0 + t] = quant_code(v[m] * sh.inv[m] * wv, sh.invq[m]);
-    __syncthreads();
-    block_sums<M>(sa, sb, col0 >> 5, 8);
-    __syncthreads();
-}
-
-// The statistics step of a norm: workgroup m < 8 computes row m's
-// statistics (rows past the pass: none) and counts on `ready` (8 arrivals
-// per pass).
-template <int M>
-__device__ __forceinline__ void stats_step(const float* x, const float* w, uint32_t D, float* st, uint32_t* ready,
-                                           DecShared& sh) {
-    const uint32_t wg = blockIdx.x;
-    if (wg < (uint32_t)M) {
-        float inv, amax;
-        row_stats(x + (size_t)wg * D, w, D, sh, inv, amax);
-        if (threadIdx.x == 0) {
-            stc(st + 2 * wg, inv);
-            stc(st + 2 * wg + 1, amax);
-        }
+        for (int m = 0; m < M; m++) v[i][m] = x[(size_t)m * D + c];
+        wv[i] = w[c];
     }
-    drain();
-    if (threadIdx.x == 0) arrive_n(ready, 1u);
+#pragma unroll
+    for (uint32_t i = 0; i < DEC_IB; i++) {
+        if (i >= ns) break;
+#pragma unroll
+        for (int m = 0; m < M; m++)
+            sa[m * DEC_MAXD + col0[i] + t] = quant_code((v[i][m] * wv[i]) * sh.inv[m], sh.invq[m]);
+    }
+    __syncthreads();
+    for (uint32_t i = 0; i < ns; i++) block_sums<M>(sa, sb, col0[i] >> 5, 8);
+    __syncthreads();
 }
 
 // Codes of one 256-column slice of rows src[m] (row stride `stride`) with
@@ -538,8 +530,6 @@ __device__ __forceinline__ void flush_tile(double (&S)[M], double* red, double* 
     __syncthreads();
 }
 
-// Items per prefetch batch (weights of a batch are loaded before the wait).
-constexpr uint32_t DEC_IB = 3;
 
 
 // Contiguous item range [lo, hi) of workgroup w out of G for N items.
@@ -593,13 +583,15 @@ __device__ __forceinline__ uint32_t nth_tile(uint32_t mask, uint32_t t0, uint32_
 }
 
 // xd[m][64 tile + r] = xs[...] + (float)(acc * as[m]) for the tiles of
-// mask, acc cleared (k_resid_norm_quant's residual); every load first.
+// mask, acc cleared (k_resid_norm_quant's residual), and with wn (the next
+// RMSNorm's weights) the tiles' statistics of xd to st; every load first.
+// A wave holds one (tile, row) with lane = column.
 template <int M>
 __device__ __forceinline__ void finalize_resid(uint32_t mask, uint32_t t0, const float* xs, float* xd, double* acc,
-                                               uint32_t D, const DecShared& sh) {
+                                               uint32_t D, const DecShared& sh, const float* wn, float* st) {
     constexpr uint32_t PER = (DEC_IB * M * 64 + 255) / 256;
     const uint32_t n = __builtin_popcount(mask) * (uint32_t)M * 64u;
-    float xv[PER];
+    float xv[PER], wq[PER];
     double av[PER];
     size_t off[PER];
     uint32_t mr[PER];
@@ -611,12 +603,15 @@ __device__ __forceinline__ void finalize_resid(uint32_t mask, uint32_t t0, const
         mr[k] = m;
         xv[k] = xs[off[k]];
         av[k] = acc[off[k]];
+        wq[k] = wn ? wn[col] : 0.0f;
     }
 #pragma unroll
     for (uint32_t k = 0; k < PER; k++) {
-        if (threadIdx.x + 256u * k >= n) continue;
-        stc(xd + off[k], xv[k] + (float)(av[k] * (double)sh.as[mr[k]]));
+        if (threadIdx.x + 256u * k >= n) continue;   // wave-uniform (n % 64 == 0)
+        const float xn = xv[k] + (float)(av[k] * (double)sh.as[mr[k]]);
+        stc(xd + off[k], xn);
         stc(acc + off[k], 0.0);
+        if (wn) tile_stat(xn, wq[k], st, (uint32_t)(off[k] % D) >> 6, mr[k]);
     }
 }
 
@@ -1167,6 +1162,7 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a0) {
             B.Up = reinterpret_cast<float*>(lb + a0.off.Up);
             B.stats_a = reinterpret_cast<float*>(lb + a0.off.stats_a);
             B.stats_f = reinterpret_cast<float*>(lb + a0.off.stats_f);
+            B.stats_next = l + 1 < a0.L ? reinterpret_cast<float*>(ln + a0.off.stats_a) : nullptr;
         }
         a.kv.k = opaque(a0.kv.k);
         a.kv.v = opaque(a0.kv.v);
@@ -1183,12 +1179,18 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a0) {
         const DecodeLayer& Ly = a.layers[l];
         const Ctr cc{a.ctr + (size_t)l * a.ctr_layer, H, TD, TF};
 
-        // ---------------------------------------------------------- norm
-        if (wg < 8u) {
-            if (l > 0 && !wait_ge(cc.x_ready(), TD * E, a, sh)) return;
-            PF_TR(l, TR_SA_BEG);
-            stats_step<M>(B.xin, Ly.an, D, B.stats_a, cc.stats_a(), sh);
-            PF_TR(l, TR_SA_END);
+        // ---------------------------------------------------------- layer 0 norm
+        if (l == 0) {
+            // tile statistics of the embedded rows (later layers get them
+            // from the down projection's last splits); wave w takes rows w,
+            // w + 4
+            for (uint32_t tl = wg; tl < TD; tl += G) {
+                for (uint32_t m = wid; m < (uint32_t)M; m += 4)
+                    tile_stat(B.xin[(size_t)m * D + 64u * tl + lane], Ly.an[64u * tl + lane], B.stats_a, tl, m);
+                drain();
+                PF_TR(l, TR_SA_END);
+                if (t == 0) arrive_n(cc.x_ready(), 1u);
+            }
         }
         // ---------------------------------------------------------- QKV
         {
@@ -1202,12 +1204,16 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a0) {
                 for (uint32_t i = 0; i < DEC_IB; i++)
                     load_w2(fmt, W, D, min(lo + i, hi - 1) / NS, min(lo + i, hi - 1) % NS, wid, lane, wr[i]);
                 PF_TR(l, TR_Q_WAIT);
-                if (!wait_ge(cc.stats_a(), 8u * E, a, sh)) return;
-                load_stats<M>(B.stats_a, sh);
+                if (!wait_ge(cc.x_ready(), TD * E, a, sh)) return;
+                combine_stats<M>(B.stats_a, TD, D, sh);
                 PF_TR(l, TR_Q_STATS);
                 // codes of the slices of this workgroup's items
-                for (uint32_t it = lo; it < hi; it++)
-                    if (it == lo || it % NS != (it - 1) % NS) norm_slice<M>(B.xin, Ly.an, D, 256 * (it % NS), sa, sb, sh);
+                for (uint32_t i0 = lo; i0 < hi; i0 += DEC_IB) {
+                    uint32_t col0[DEC_IB], ns = 0;
+                    for (uint32_t it = i0; it < min(hi, i0 + DEC_IB); it++)
+                        if (it == i0 || it % NS != (it - 1) % NS) col0[ns++] = 256u * (it % NS);
+                    norm_slices<M>(B.xin, Ly.an, D, col0, ns, sa, sb, sh);
+                }
                 PF_TR(l, TR_Q_NORM);
                 if (t < (uint32_t)M) stc(B.rs + t, sh.as[t]);
                 double S[M];
@@ -1320,20 +1326,13 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a0) {
                 for (uint32_t t0 = lo / NS; t0 <= (hi - 1) / NS; t0 += DEC_IB) {
                     const uint32_t mask = arrive_tiles([&](uint32_t x) { return cc.o_tile(x); }, t0, lo, hi, NS, sh);
                     if (mask) {
-                        finalize_resid<M>(mask, t0, B.xin, B.xmid, B.acc_o, D, sh);
+                        finalize_resid<M>(mask, t0, B.xin, B.xmid, B.acc_o, D, sh, Ly.fn, B.stats_f);
                         drain();
                         PF_TR(l, TR_O_FIN);
                         if (t == 0) arrive_n(cc.xmid(), __builtin_popcount(mask));
                     }
                 }
             }
-        }
-        // ---------------------------------------------------------- FFN norm
-        if (wg < 8u) {
-            if (!wait_ge(cc.xmid(), TD * E, a, sh)) return;
-            PF_TR(l, TR_SF_BEG);
-            stats_step<M>(B.xmid, Ly.fn, D, B.stats_f, cc.stats_f(), sh);
-            PF_TR(l, TR_SF_END);
         }
         // ---------------------------------------------------------- gate|up
         {
@@ -1350,11 +1349,15 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a0) {
                     load_w2(fmt, W, D, p + TF, s, wid, lane, wu_[i]);
                 }
                 PF_TR(l, TR_G_WAIT);
-                if (!wait_ge(cc.stats_f(), 8u * E, a, sh)) return;
-                load_stats<M>(B.stats_f, sh);
+                if (!wait_ge(cc.xmid(), TD * E, a, sh)) return;
+                combine_stats<M>(B.stats_f, TD, D, sh);
                 PF_TR(l, TR_G_STATS);
-                for (uint32_t it = lo; it < hi; it++)
-                    if (it == lo || it % NS != (it - 1) % NS) norm_slice<M>(B.xmid, Ly.fn, D, 256 * (it % NS), sa, sb, sh);
+                for (uint32_t i0 = lo; i0 < hi; i0 += DEC_IB) {
+                    uint32_t col0[DEC_IB], ns = 0;
+                    for (uint32_t it = i0; it < min(hi, i0 + DEC_IB); it++)
+                        if (it == i0 || it % NS != (it - 1) % NS) col0[ns++] = 256u * (it % NS);
+                    norm_slices<M>(B.xmid, Ly.fn, D, col0, ns, sa, sb, sh);
+                }
                 PF_TR(l, TR_G_NORM);
                 double Sg[M], Su[M];
 #pragma unroll
@@ -1477,7 +1480,8 @@ __global__ __launch_bounds__(256) void k_decode(DecodeArgs a0) {
                 for (uint32_t t0 = lo / NSF; t0 <= (hi - 1) / NSF; t0 += DEC_IB) {
                     const uint32_t mask = arrive_tiles([&](uint32_t x) { return cc.d_tile(x); }, t0, lo, hi, NSF, sh);
                     if (mask) {
-                        finalize_resid<M>(mask, t0, B.xmid, B.xout, B.acc_d, D, sh);
+                        finalize_resid<M>(mask, t0, B.xmid, B.xout, B.acc_d, D, sh,
+                                          B.stats_next ? a.layers[l + 1].an : nullptr, B.stats_next);
                         drain();
                         PF_TR(l, TR_D_FIN);
                         if (t == 0 && l + 1 < a.L) arrive_n(a.ctr + (size_t)(l + 1) * a.ctr_layer, __builtin_popcount(mask));

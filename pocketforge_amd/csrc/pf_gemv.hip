@@ -411,10 +411,12 @@ __global__ __launch_bounds__(256) void k_quant_rows(const float* __restrict__ x,
 }
 
 // x[m] += (float)(acc[m] * as_prev[m]) (when acc != null; acc cleared),
-// then RMSNorm (src/matmul_neon.cpp:231-239, CANON(4) sum of squares) with
-// weight w, then quantize_activation_row of the normed row.  Grid M, 1024
-// threads: all loads are issued first; the 256 canonical lanes read the
-// row back from LDS (K <= 4096).
+// then the engine's RMSNorm (src/matmul_neon.cpp:231-239) with weight w in
+// tile-canonical order (the sum of squares is the sequential sum over
+// 64-element tiles of each tile's halving tree of x * x; normed = (x * w) *
+// inv), then quantize_activation_row of the normed row.  Grid M, 1024
+// threads: all loads are issued first; wave w builds the trees of tiles w,
+// w + 16, ... from the row in LDS (K <= 4096, K % 64 == 0).
 // Blocks past the `rows` row blocks prefetch pf (the weights of the GEMV that
 // consumes the output).
 template <int PER>
@@ -426,6 +428,7 @@ __global__ __launch_bounds__(1024) void k_resid_norm_quant(float* __restrict__ x
                                                            float* __restrict__ as, int32_t* __restrict__ bsum,
                                                            uint32_t bsum_stride, uint32_t rows, Prefetch pf) {
     __shared__ float row[4096];
+    __shared__ float tree[64];
     __shared__ float red[16];
     const uint32_t m = blockIdx.x, t = threadIdx.x;
     if (m >= rows) {
@@ -453,18 +456,26 @@ __global__ __launch_bounds__(1024) void k_resid_norm_quant(float* __restrict__ x
         if (i < K) row[i] = xv[k];
     }
     __syncthreads();
-    // CANON(4): lane l < 256 sums x[l]^2, x[l+256]^2, ... in order
-    float part = 0.0f;
-    if (t < 256)
-        for (uint32_t i = t; i < K; i += 256) part = __builtin_fmaf(row[i], row[i], part);
-    float wsum = wave_tree_sum(part);
-    if ((t & 63) == 0 && t < 256) red[t >> 6] = wsum;
+    // tile trees of x * x, then their sequential sum
+    const uint32_t wid = t >> 6, lane = t & 63u;
+    for (uint32_t tl = wid; tl < K / 64u; tl += 16u) {
+        const float v = row[64u * tl + lane];
+        const float s = wave_tree_sum(v * v);
+        if (lane == 0) tree[tl] = s;
+    }
     __syncthreads();
-    const float ss = (red[0] + red[2]) + (red[1] + red[3]);
+    if (t == 0) {
+        float ss = 0.0f;
+        for (uint32_t tl = 0; tl < K / 64u; tl++) ss = ss + tree[tl];
+        red[0] = ss;
+    }
+    __syncthreads();
+    const float ss = red[0];
+    __syncthreads();
     const float rms = __builtin_sqrtf(ss / (float)K + 1e-6f);
     const float inv = 1.0f / rms;
 #pragma unroll
-    for (int k = 0; k < PER; k++) xv[k] = xv[k] * inv * wv[k];
+    for (int k = 0; k < PER; k++) xv[k] = (xv[k] * wv[k]) * inv;
     __syncthreads();
     quantize_row_block<PER, 1024>(xv, K, q + (size_t)m * q_stride, as + m,
                                   bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);

@@ -1152,8 +1152,8 @@ static pf_status decode_setup(pf_engine* e) {
         f.f = take((size_t)MR * F * 4);
         f.S = take((size_t)MR * H * e->dec_s_stride * 4);
         f.Up = take((size_t)MR * H * e->dec_cstride * d.head_dim * 4);
-        f.stats_a = take(8 * 2 * 4);
-        f.stats_f = take(8 * 2 * 4);
+        f.stats_a = take((size_t)(D / 64) * 8 * 2 * 4);
+        f.stats_f = take((size_t)(D / 64) * 8 * 2 * 4);
         e->dec_lstride = o;
     }
     e->dec_ctr_layer = 16 * decode_ctr_slots(H, D / 64, F / 64);

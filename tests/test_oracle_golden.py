@@ -147,6 +147,37 @@ def test_rmsnorm_softmax_closed_forms():
     assert v[4] > v[0] > v[1] > v[3] > v[2]
 
 
+@pytest.mark.parametrize("n", [256, 768, 2048])
+def test_engine_rmsnorm_tile_order(n):
+    """The engine's RMSNorm in tile-canonical order against the reference
+    restatement (src/matmul_neon.cpp:231-239, sequential sum) and the float64
+    closed form; its row maximum decomposes by tile exactly."""
+    L = O.lib()
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(n).astype(np.float32) * np.float32(3.0)
+    w = (1.0 + 0.25 * rng.standard_normal(n)).astype(np.float32)
+    o = np.zeros(n, np.float32)
+    ref = np.zeros(n, np.float32)
+    L.orc_engine_rmsnorm(P(o, O.f32p), P(x, O.f32p), P(w, O.f32p), n)
+    L.orc_rmsnorm_ref(P(ref, O.f32p), P(x, O.f32p), P(w, O.f32p), n)
+    np.testing.assert_allclose(o, ref, rtol=1e-6, atol=0)
+    xd = x.astype(np.float64)
+    closed = xd / np.sqrt(np.mean(xd * xd) + 1e-6) * w.astype(np.float64)
+    np.testing.assert_allclose(o, closed, rtol=2e-6, atol=0)
+    # tile-canonical sum of squares and the decomposed row maximum
+    ss = np.float32(0)
+    for t in range(n // 64):
+        lv = (x[64 * t:64 * t + 64] * x[64 * t:64 * t + 64]).astype(np.float32)
+        off = 32
+        while off >= 1:
+            lv[:off] = lv[:off] + lv[off:2 * off]
+            off //= 2
+        ss = np.float32(ss + lv[0])
+    inv = np.float32(1) / np.sqrt(np.float32(ss / np.float32(n) + np.float32(1e-6)))
+    np.testing.assert_array_equal(o, (x * w) * inv)
+    assert np.abs(o).max() == np.float32(np.abs(x * w).max() * inv)
+
+
 from golden_cfg import KV_CFGS  # noqa: E402
 
 
