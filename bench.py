@@ -1,9 +1,11 @@
 """Benchmark: accepted tokens/s of MTP speculative decoding on one MI355X.
 
-Workload: 1B-class decoder (24 layers, hidden 2048, 16 heads x 128, SwiGLU
-5632, tied vocab 16384), all matrices Q4 (32-wide blocks, fp16 scale,
-weights N(0, 0.02)), 4 Q4 MTP heads, int8 3-tier KV (sink 4, window 8192),
-greedy draft = 4, batch 1, 2048-token uniform random prompt, 512 generated.
+Workload (default, --config B): 1B-class decoder (24 layers, hidden 2048, 16
+heads x 128, SwiGLU 5632, tied vocab 16384), all matrices Q4 (32-wide
+blocks, fp16 scale, weights N(0, 0.02)), 4 Q4 MTP heads, int8 3-tier KV
+(sink 4, window 8192), greedy draft = 4, batch 1, 2048-token uniform random
+prompt, 512 generated.  --config S / B-mix / B-long select the other
+single-sequence workloads (see CONFIGS).
 
 A step is one decode of 512 tokens after the prompt: the engine is reset and
 the first 2047 prompt tokens are prefilled before the timer starts (their KV
@@ -30,6 +32,29 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBPS = 8000.0
 METRIC = "accepted tok/s @1B Q4 MTP draft=4, bs=1; verify-step HBM GB/s vs peak"
 
+# Single-sequence workloads: model, weight formats, KV geometry (sink,
+# window, pool), prompt and generated lengths, sampling (temperature,
+# top-p, top-k, greedy).  "B" is the headline configuration.
+CONFIGS = {
+    "B": dict(model="ONE_B", fmts="ALL_Q4", kv=(4, 8192, 64), prompt=2048, new=512, samp=(0.8, 0.95, 40, 1),
+              name="1B Q4 (24L, d2048, 16x128 heads, ff5632, vocab 16384 tied), 4 Q4 MTP heads, greedy"),
+    "S": dict(model="SMALL", fmts="ALL_Q4", kv=(4, 8192, 64), prompt=64, new=256, samp=(0.8, 0.95, 40, 1),
+              name="150M Q4 (12L, d768, 12x64 heads, ff2048, vocab 16384 tied), 4 Q4 MTP heads, greedy"),
+    "B-mix": dict(model="ONE_B", fmts="MIXED", kv=(4, 8192, 64), prompt=1024, new=512, samp=(0.8, 0.95, 40, 0),
+                  name="1B mixed (attention Q4, gate/up Q2, down Q1.5), 4 Q4 MTP heads, temperature 0.8, top-p 0.95 "
+                       "(top-k 40 not reached: the reference dispatch takes top-p first), Philox seed 7"),
+    "B-long": dict(model="ONE_B", fmts="ALL_Q4", kv=(4, 4096, 16), prompt=32768, new=256, samp=(0.8, 0.95, 40, 1),
+                   name="1B Q4, 4 Q4 MTP heads, greedy, long context"),
+}
+
+
+def view_count(pos, sink, window, pool):
+    """Visible entries of a query at position pos (sink + pooled + window)."""
+    s = min(pos, sink)
+    nw = max(0, pos - sink)
+    win = min(nw, window)
+    return s + (nw - win) // pool + win
+
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
@@ -51,13 +76,13 @@ def measured_traffic():
     return None
 
 
-def cpu_baseline(cfg, w, kv, prompt, n_prompt=16, n_new=8):
+def cpu_baseline(cfg, w, kv, prompt, samp, what, n_prompt=16, n_new=8):
     import oracle as O
     c = dict(cfg)
     c.update(kv)
     om = O.Model(c, w)
     t0 = time.perf_counter()
-    toks, acc, rej = om.generate(prompt[:n_prompt], n_new, O.Sampling(0.8, 0.95, 40, 1), 7)
+    toks, acc, rej = om.generate(prompt[:n_prompt], n_new, O.Sampling(*samp), 7)
     wall = time.perf_counter() - t0
     dec = O.lib().orc_last_decode_seconds()
     om.close()
@@ -67,9 +92,10 @@ def cpu_baseline(cfg, w, kv, prompt, n_prompt=16, n_new=8):
         "unit": "tok/s",
         "cores": int(O.lib().orc_num_threads()),
         "kind": "port",
-        "sample": (f"oracle (C restatement, OpenMP row-parallel GEMVs) greedy MTP decode of {gen} tokens after a "
-                   f"{n_prompt}-token prompt on the same 1B Q4 weights; decode time {dec:.2f}s of {wall:.2f}s wall "
-                   f"(prefill excluded); context 16-24 instead of 2048-2560"),
+        "sample": (f"oracle (C restatement, OpenMP row-parallel GEMVs) MTP decode of {gen} tokens after a "
+                   f"{n_prompt}-token prompt on the same weights and sampling ({what}); decode time {dec:.2f}s of "
+                   f"{wall:.2f}s wall (prefill excluded); context {n_prompt}-{n_prompt + n_new} instead of the "
+                   f"workload's"),
     }
 
 
@@ -93,10 +119,12 @@ def copy_probe(nbytes):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--config", default="B", choices=sorted(CONFIGS),
+                    help="workload (default B, the headline configuration)")
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--prompt", type=int, default=2048)
-    ap.add_argument("--new", type=int, default=512)
+    ap.add_argument("--prompt", type=int, default=0, help="prompt length (default: the configuration's)")
+    ap.add_argument("--new", type=int, default=0, help="generated tokens (default: the configuration's)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only run 3 device-to-device copies of this many bytes (hardware-counter calibration)")
@@ -112,9 +140,12 @@ def main():
     import pocketforge_amd as pf
     from pocketforge_amd import weights as W
 
-    cfg = W.ONE_B
+    C = CONFIGS[args.config]
+    args.prompt = args.prompt or C["prompt"]
+    args.new = args.new or C["new"]
+    cfg = getattr(W, C["model"])
     t0 = time.perf_counter()
-    w = W.make_weights(cfg, seed=1234)
+    w = W.make_weights(cfg, seed=1234, fmts=getattr(W, C["fmts"]))
     log(f"weights generated in {time.perf_counter() - t0:.1f}s")
     ctx = pf.Context(0)
     dev, cus = ctx.device_info()
@@ -122,10 +153,11 @@ def main():
     model = pf.Model(ctx, cfg, w)
     log(f"weights uploaded in {time.perf_counter() - t0:.1f}s on {dev} ({cus} CUs)")
     max_ctx = args.prompt + args.new + 64
-    kv = dict(sink_size=4, window_size=8192, pool_block=64, max_context=max_ctx)
+    sink, window, pool = C["kv"]
+    kv = dict(sink_size=sink, window_size=window, pool_block=pool, max_context=max_ctx)
     eng = pf.Engine(model, **kv)
     prompt = W.prompt_ids(args.prompt, cfg["n_vocab"], seed=42)
-    greedy = pf.Sampling(0.8, 0.95, 40, 1)
+    greedy = pf.Sampling(*C["samp"])
 
     prefill_s = []
 
@@ -170,13 +202,14 @@ def main():
     r_avg = sum(r[0] * r[1] for r in round_us) / max(1, sum(r[1] for r in round_us))
     # verify pass algorithmic bytes: every packed weight once (incl. the tied
     # unembedding) + the visible int8 KV rows with fp32 scales, at the mean
-    # context length of the decode
+    # visible list length of the decode
     wbytes = W.packed_bytes(w) + w["emb"][1].nbytes + w["emb"][2].nbytes
-    ctx_mean = args.prompt + args.new / 2
+    ctx_mean = sum(view_count(p, sink, window, pool) for p in range(args.prompt, args.prompt + args.new)) / args.new
     kv_bytes = cfg["n_layers"] * 2 * cfg["n_heads"] * (cfg["head_dim"] + 4) * ctx_mean
     pass_bytes = wbytes + kv_bytes
+    headline = args.config == "B"
     out = {
-        "metric": METRIC,
+        "metric": METRIC if headline else f"accepted tok/s, configuration {args.config}, MTP draft=4, bs=1",
         "value": round(value, 3),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -189,9 +222,8 @@ def main():
         "dtype": "int8",
         "data": "synthetic (random-init weights N(0,0.02), uniform random prompt ids)",
         "config": {
-            "workload": (f"1B Q4 (24L, d2048, 16x128 heads, ff5632, vocab 16384 tied), 4 Q4 MTP heads, greedy "
-                         f"draft=4, bs=1, {args.prompt}-token prompt, {args.new} generated, int8 3-tier KV "
-                         f"(sink 4, window 8192, pool 64)"),
+            "workload": (f"{C['name']}, draft=4, bs=1, {args.prompt}-token prompt, {args.new} generated, "
+                         f"int8 3-tier KV (sink {sink}, window {window}, pool {pool})"),
             "accepted_per_round": round(sum(accs) / max(1, sum(rounds)), 4),
             "mtp_accepted": sum(accs), "mtp_rejected": sum(rejs), "rounds": sum(rounds),
             "tokens_per_step": gens[0],
@@ -200,13 +232,13 @@ def main():
             "device": dev,
         },
         "roofline": {
-            "kernel": "k_gemv_i8<Q4,M=5> (verify-pass int8 x Q4 GEMV)",
+            "kernel": "k_gemv_i8<fmt,M=5> (verify-pass int8 x block-quantized GEMV)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": measured_traffic(),
+            "traffic": measured_traffic() if headline else None,
             "traffic_source": "profiles/gemv_i8_traffic_1b_q4.md (rocprofv3 FETCH_SIZE x 1.99985 + WRITE_SIZE x 1.0, "
                               "factors from a copy kernel of known size)",
             "avg_launch_us": round(gemv_us, 3),
@@ -224,7 +256,7 @@ def main():
     }
     if not args.no_cpu:
         log("cpu baseline ...")
-        out["cpu_baseline"] = cpu_baseline(cfg, w, kv, prompt)
+        out["cpu_baseline"] = cpu_baseline(cfg, w, kv, prompt, C["samp"], args.config)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

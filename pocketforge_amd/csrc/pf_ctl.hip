@@ -14,6 +14,8 @@
 // round (accepted count | corrective pushed << 8).
 #include "pf_device.h"
 
+#include <rocprim/block/block_radix_sort.hpp>
+
 namespace pf {
 
 struct ArgBest { float v; int32_t i; };
@@ -70,36 +72,39 @@ __device__ __forceinline__ uint32_t ord_f(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Bitonic sort of n (power of two) 64-bit keys in LDS, ascending.
-__device__ void lds_bitonic(uint64_t* a, uint32_t n) {
-    for (uint32_t k = 2; k <= n; k <<= 1) {
-        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-            for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-                uint32_t l = i ^ j;
-                if (l > i) {
-                    uint64_t x = a[i], y = a[l];
-                    bool up = (i & k) == 0;
-                    if ((x > y) == up) { a[i] = y; a[l] = x; }
-                }
-            }
-            __syncthreads();
-        }
-    }
-}
-
 // LDS arena for the sampler: 16384 64-bit slots (128 KiB).
 constexpr uint32_t SAMPLE_MAX_V = 16384;
+constexpr uint32_t SAMPLE_IPT = SAMPLE_MAX_V / 1024;   // items per thread of the 1024-thread sampler
 
-// Sorted (logit desc, index asc) order into `a` (hi = ord bits, lo = idx);
-// returns the padded power-of-two size.
+// Stable radix sort of 16384 32-bit keys with their indices (rocPRIM's
+// block radix sort with the blocked-order rank algorithm): thread t holds
+// positions 16 t .. 16 t + 15 before and after, and equal keys keep their
+// order of positions.
+typedef rocprim::block_radix_sort<uint32_t, 1024, SAMPLE_IPT, uint32_t, 1, 1, 8,
+                                  rocprim::block_radix_rank_algorithm::basic_memoize>
+    SampleSort;
+static_assert(sizeof(SampleSort::storage_type) <= SAMPLE_MAX_V * sizeof(uint64_t),
+              "sampler sort storage must fit the arena");
+
+// Sorted (logit desc, index asc) order into `a` (hi = ~ord bits, lo = idx):
+// a stable ascending sort of ~ord(x) over the indices in ascending order,
+// so equal logits keep ascending indices.  Slots past V hold ~0 keys and
+// sort last.  1024 threads; `a` doubles as the sort's scratch.
 __device__ uint32_t sort_desc(const float* __restrict__ x, uint32_t V, uint64_t* a) {
-    uint32_t n = 1;
-    while (n < V) n <<= 1;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x)
-        a[i] = i < V ? (((uint64_t)(~ord_f(x[i]))) << 32) | i : ~0ull;
+    uint32_t key[SAMPLE_IPT], idx[SAMPLE_IPT];
+#pragma unroll
+    for (uint32_t j = 0; j < SAMPLE_IPT; j++) {
+        const uint32_t i = threadIdx.x * SAMPLE_IPT + j;
+        key[j] = i < V ? ~ord_f(x[i]) : ~0u;
+        idx[j] = i;
+    }
+    SampleSort().sort(key, idx, *reinterpret_cast<SampleSort::storage_type*>(a));
     __syncthreads();
-    lds_bitonic(a, n);
-    return n;
+#pragma unroll
+    for (uint32_t j = 0; j < SAMPLE_IPT; j++)
+        a[threadIdx.x * SAMPLE_IPT + j] = ((uint64_t)key[j] << 32) | idx[j];
+    __syncthreads();
+    return SAMPLE_MAX_V;
 }
 
 __device__ __forceinline__ float key_val(uint64_t k) {
@@ -156,7 +161,7 @@ __device__ ScanHit chunk64_scan(const uint64_t* a, uint32_t n, float thr1, float
 // thread 0.  `draw` is the draw index to use for a stochastic call.
 __device__ int32_t sample_row(const float* __restrict__ x, uint32_t V, const SamplingCfg& cfg, uint64_t seed,
                               uint64_t draw, bool* used_draw) {
-    __shared__ uint64_t arena[SAMPLE_MAX_V];
+    __shared__ __align__(16) uint64_t arena[SAMPLE_MAX_V];
     __shared__ float tot[64];
     __shared__ float bcast[2];
     *used_draw = false;
@@ -168,6 +173,7 @@ __device__ int32_t sample_row(const float* __restrict__ x, uint32_t V, const Sam
     if (cfg.top_p < 1.0f && cfg.top_p > 0.0f) {            // src/engine.cpp:961-1003
         sort_desc(x, V, arena);
         const float mx = key_val(arena[0]);
+        __syncthreads();   // every thread has read slot 0 before it is rewritten
         for (uint32_t i = threadIdx.x; i < V; i += blockDim.x) {
             uint64_t k = arena[i];
             float p = expf_c((key_val(k) - mx) / temp);

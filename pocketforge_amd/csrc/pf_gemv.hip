@@ -465,8 +465,16 @@ __global__ __launch_bounds__(1024) void k_resid_norm_quant(float* __restrict__ x
     }
     __syncthreads();
     if (t == 0) {
+        // sequential sum of the tile trees, 16 LDS reads in flight at a time
         float ss = 0.0f;
-        for (uint32_t tl = 0; tl < K / 64u; tl++) ss = ss + tree[tl];
+        for (uint32_t t0 = 0; t0 < K / 64u; t0 += 16) {
+            float tv[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++) tv[k] = tree[min(t0 + k, 63u)];
+#pragma unroll
+            for (int k = 0; k < 16; k++)
+                if (t0 + k < K / 64u) ss = ss + tv[k];
+        }
         red[0] = ss;
     }
     __syncthreads();
