@@ -248,6 +248,37 @@ pf_status pf_engine_profile(pf_engine* e, int32_t enable);
  * recorded by the last pf_generate in profiling mode. */
 pf_status pf_engine_gemv_stats(pf_engine* e, uint32_t* launches, double* avg_us, double* avg_bytes);
 
+/* ------------------------------------------------- multi-sequence engine
+ * No counterpart in the reference, which decodes one sequence per Engine
+ * (include/forge/engine.hpp:20-74).  An engine of n_seq independent
+ * sequences (n_seq * (n_mtp + 1) <= 512) over one model: each sequence owns
+ * its 3-tier KV cache, position, decode state, seed and draw counter, and
+ * produces exactly the tokens of a single-sequence engine given the same
+ * prompt and seed (Engine::generate, src/engine.cpp:276-396, per
+ * sequence).  Passes are batched across sequences: a round runs one base
+ * pass of n_seq rows and one verify pass of n_seq * (n_mtp + 1) rows.
+ * pf_engine_destroy, pf_engine_reset, pf_engine_profile and the timing
+ * queries apply; pf_forward and pf_generate need n_seq == 1. */
+pf_status pf_batch_create(pf_model* m, const pf_cache_desc* cache, uint32_t n_seq, pf_engine** out);
+uint32_t pf_batch_sequences(const pf_engine* e);
+/* Next position of sequence `seq` (tokens it has forwarded). */
+uint32_t pf_batch_position(const pf_engine* e, uint32_t seq);
+/* Forwards n prompt tokens of one sequence at its next positions. */
+pf_status pf_batch_prefill(pf_engine* e, uint32_t seq, const int32_t* tokens, uint32_t n);
+/* One batched pass: sequence seqs[i] (distinct) forwards tokens
+ * [i * rows_per_seq, (i + 1) * rows_per_seq) at its next positions; row r
+ * of logits [n * rows_per_seq][n_vocab] and hidden [..][n_embd] (either
+ * may be NULL) equals the matching row of pf_forward on that sequence.
+ * With outputs, n * rows_per_seq <= max(8, n_seq * (n_mtp + 1)). */
+pf_status pf_batch_forward(pf_engine* e, const uint32_t* seqs, uint32_t n, uint32_t rows_per_seq,
+                           const int32_t* tokens, float* logits, float* hidden);
+/* Engine::generate for every sequence: prompts concatenated (prompt_lens
+ * [n_seq]), seeds [n_seq], tokens_out [n_seq][tokens_cap] (prompt
+ * included), results [n_seq]. */
+pf_status pf_batch_generate(pf_engine* e, const int32_t* prompts, const uint32_t* prompt_lens,
+                            uint32_t max_new_tokens, const pf_sampling* cfg, const uint64_t* seeds,
+                            int32_t* tokens_out, uint32_t tokens_cap, pf_gen_result* results);
+
 #ifdef __cplusplus
 }
 #endif

@@ -114,6 +114,13 @@ SYMBOLS = {
     "pf_engine_profile": (C.c_int32, [vp, C.c_int32]),
     "pf_engine_round_time": (C.c_int32, [vp, C.POINTER(C.c_double), u32p]),
     "pf_engine_gemv_stats": (C.c_int32, [vp, u32p, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    "pf_batch_create": (C.c_int32, [vp, C.POINTER(CacheDesc), C.c_uint32, C.POINTER(vp)]),
+    "pf_batch_sequences": (C.c_uint32, [vp]),
+    "pf_batch_position": (C.c_uint32, [vp, C.c_uint32]),
+    "pf_batch_prefill": (C.c_int32, [vp, C.c_uint32, i32p, C.c_uint32]),
+    "pf_batch_forward": (C.c_int32, [vp, u32p, C.c_uint32, C.c_uint32, i32p, f32p, f32p]),
+    "pf_batch_generate": (C.c_int32, [vp, i32p, u32p, C.c_uint32, C.POINTER(Sampling), C.POINTER(C.c_uint64), i32p,
+                                      C.c_uint32, C.POINTER(GenResult)]),
 }
 
 _lib = None
@@ -551,3 +558,55 @@ class Engine:
 
     def __del__(self):
         self.close()
+
+
+class BatchEngine(Engine):
+    """n_seq independent sequences over one model, decoded together: each
+    sequence's tokens equal a single-sequence Engine's for the same prompt
+    and seed, while every forward pass covers all sequences (no counterpart
+    in the reference, which decodes one sequence per Engine)."""
+
+    def __init__(self, model, n_seq, sink_size=4, window_size=8192, pool_block=64, max_context=4096):
+        self.model = model
+        self.ctx = model.ctx
+        self.cfg = model.cfg
+        self.n_seq = n_seq
+        cd = CacheDesc(sink_size, window_size, pool_block, max_context)
+        self.h = vp()
+        self.ctx.check(lib().pf_batch_create(model.h, C.byref(cd), n_seq, C.byref(self.h)), "pf_batch_create")
+
+    def position(self, seq):
+        return lib().pf_batch_position(self.h, seq)
+
+    def prefill_seq(self, seq, tokens):
+        toks = np.ascontiguousarray(np.atleast_1d(tokens), np.int32)
+        self.ctx.check(lib().pf_batch_prefill(self.h, seq, P(toks, i32p), len(toks)), "pf_batch_prefill")
+
+    def forward_batch(self, seqs, tokens, want_logits=True):
+        """tokens [len(seqs)][rows]: one pass; returns logits and hidden [len(seqs)][rows][...]."""
+        seqs = np.ascontiguousarray(seqs, np.uint32)
+        toks = np.ascontiguousarray(tokens, np.int32).reshape(len(seqs), -1)
+        n, r = toks.shape
+        V, D = self.cfg["n_vocab"], self.cfg["n_embd"]
+        logits = np.zeros((n, r, V), np.float32) if want_logits else None
+        hidden = np.zeros((n, r, D), np.float32)
+        self.ctx.check(lib().pf_batch_forward(self.h, P(seqs, u32p), n, r, P(toks, i32p),
+                                              P(logits, f32p) if want_logits else None, P(hidden, f32p)),
+                       "pf_batch_forward")
+        return logits, hidden
+
+    def generate_batch(self, prompts, max_new, sampling=None, seeds=None):
+        """prompts: list of n_seq int arrays; returns (list of token arrays, list of GenResult)."""
+        s = sampling or Sampling(0.8, 0.95, 40, 1)
+        assert len(prompts) == self.n_seq
+        lens = np.array([len(p) for p in prompts], np.uint32)
+        flat = np.ascontiguousarray(np.concatenate([np.asarray(p, np.int32) for p in prompts]) if lens.sum()
+                                    else np.zeros(1, np.int32), np.int32)
+        seeds = np.ascontiguousarray(seeds if seeds is not None else np.full(self.n_seq, 7), np.uint64)
+        cap = int(lens.max()) + max_new + 8
+        toks = np.zeros((self.n_seq, cap), np.int32)
+        res = (GenResult * self.n_seq)()
+        self.ctx.check(lib().pf_batch_generate(self.h, P(flat, i32p), P(lens, u32p), max_new, C.byref(s),
+                                               seeds.ctypes.data_as(C.POINTER(C.c_uint64)), P(toks, i32p), cap,
+                                               res), "pf_batch_generate")
+        return [toks[i, : res[i].n_tokens].copy() for i in range(self.n_seq)], list(res)

@@ -18,8 +18,8 @@
 
 namespace pf {
 
-__device__ __forceinline__ size_t plane_index(const KvGeom& g, uint32_t layer, uint32_t head) {
-    return (size_t)layer * g.n_heads + head;
+__device__ __forceinline__ size_t plane_index(const KvGeom& g, uint32_t seq, uint32_t layer, uint32_t head) {
+    return ((size_t)seq * g.n_layers + layer) * g.n_heads + head;
 }
 
 // View of row m of a pass: from its position, or from explicit counts when
@@ -27,7 +27,7 @@ __device__ __forceinline__ size_t plane_index(const KvGeom& g, uint32_t layer, u
 __device__ __forceinline__ KvView pass_view(const KvGeom& g, const PassDesc* pd, uint32_t m,
                                             int32_t view_sink, uint32_t view_nw) {
     if (view_sink >= 0) return kv_view_counts(g, (uint32_t)view_sink, view_nw);
-    return kv_view(g, pd->pos0 + m);
+    return kv_view(g, row_pos(pd, m));
 }
 
 // ------------------------------------------------------------ store side
@@ -71,7 +71,7 @@ __global__ __launch_bounds__(64) void k_qkv_post(double* __restrict__ acc, const
     const uint32_t m = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
     if (m >= pd->m) return;
     const uint32_t hd = g.head_dim, D = g.n_heads * hd, half = hd >> 1;
-    const uint32_t pos = pd->pos0 + m;
+    const uint32_t pos = row_pos(pd, m);
     const bool act = t < half;
     float k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
     if (act) {
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(64) void k_qkv_post(double* __restrict__ acc, const
         k_out[o] = kr0; k_out[o + 1] = kr1;
         v_out[o] = v0; v_out[o + 1] = v1;
     }
-    store_pair(g, kv, plane_index(g, layer, h), kv_store_row(g, pos), t, act, k0, k1, v0, v1);
+    store_pair(g, kv, plane_index(g, row_seq(pd, m), layer, h), kv_store_row(g, pos), t, act, k0, k1, v0, v1);
 }
 
 // KVCache::store of one (layer, head) row given fp32 key/value (the
@@ -104,7 +104,7 @@ __global__ __launch_bounds__(64) void k_kv_store_row(KvGeom g, KvPlanes kv, uint
     const bool act = t < half;
     float k0 = act ? key[2 * t] : 0.f, k1 = act ? key[2 * t + 1] : 0.f;
     float v0 = act ? val[2 * t] : 0.f, v1 = act ? val[2 * t + 1] : 0.f;
-    store_pair(g, kv, plane_index(g, layer, head), row, t, act, k0, k1, v0, v1);
+    store_pair(g, kv, plane_index(g, 0, layer, head), row, t, act, k0, k1, v0, v1);
 }
 
 // Pooled row r of one plane: the mean of pool_block consecutive window
@@ -148,17 +148,29 @@ __global__ __launch_bounds__(128) void k_pool_row_one(KvGeom g, KvPlanes kv, uin
     pool_row(g, kv, plane, r);
 }
 
-// Pooled rows a pass can see and earlier passes may not have folded: rows
-// [pool(p0 - 1), pool(p0 + M - 1)) of every plane, from the pass
-// descriptor.  Grid (planes, rows_max); refolding a row rewrites the same
-// values.
+// Pooled rows a pass can see and earlier passes may not have folded, from
+// the pass descriptor; refolding a row rewrites the same values.  Grid
+// (layers * heads, y), y over the rows [pool(p0 - 1), pool(p0 + M - 1)) of
+// a single-sequence pass, or over the pass rows of a batched pass: row m at
+// position p folds [pool(p - 1), pool(p)), at most one row, since the
+// pooled count grows by at most one per position.
 __global__ __launch_bounds__(128) void k_pool_rows(KvGeom g, KvPlanes kv, const PassDesc* __restrict__ pd) {
-    const uint32_t p0 = pd->pos0, m = pd->m;
-    const uint32_t r_lo = kv_view(g, p0 > 0 ? p0 - 1 : 0).pool;
-    const uint32_t r_hi = kv_view(g, p0 + m - 1).pool;
-    const uint32_t r = r_lo + blockIdx.y;
+    uint32_t p_first, p_last, seq, y = blockIdx.y;
+    if (pd->batch) {
+        if (y >= pd->m) return;
+        p_first = p_last = pd->rpos[y];
+        seq = pd->rseq[y];
+        y = 0;
+    } else {
+        p_first = pd->pos0;
+        p_last = pd->pos0 + pd->m - 1;
+        seq = pd->seq0;
+    }
+    const uint32_t r_lo = kv_view(g, p_first > 0 ? p_first - 1 : 0).pool;
+    const uint32_t r_hi = kv_view(g, p_last).pool;
+    const uint32_t r = r_lo + y;
     if (r >= r_hi || r >= g.pool_cap) return;
-    pool_row(g, kv, blockIdx.x, r);
+    pool_row(g, kv, (size_t)seq * g.n_layers * g.n_heads + blockIdx.x, r);
 }
 
 // ------------------------------------------------------------ attention
@@ -188,7 +200,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(const PassDesc* __restrict_
     const float scale = scaled ? 1.0f / __builtin_sqrtf((float)hd) : 1.0f;
     float* out = S + ((size_t)m * g.n_heads + y) * s_stride;
     if (j < C) {
-        const size_t plane = plane_index(g, layer, h);
+        const size_t plane = plane_index(g, row_seq(pd, m), layer, h);
         const uint32_t row = kv_row(g, v, j);
         const int8_t* kr = kv.k + (plane * g.rows + row) * hd;
         const float ks = kv.ks[plane * g.rows + row];
@@ -234,7 +246,7 @@ __global__ __launch_bounds__(128) void k_attn_wsum(const PassDesc* __restrict__ 
     const KvView v = pass_view(g, pd, m, view_sink, view_nw);
     const uint32_t C = min(v.count(), limit);
     if (c * 64u >= C) return;
-    const size_t plane = plane_index(g, layer, h);
+    const size_t plane = plane_index(g, row_seq(pd, m), layer, h);
     const float* p = S + ((size_t)m * g.n_heads + y) * s_stride;
     const uint32_t j0 = c * 64u, n = min(64u, C - j0);
     if ((hd & 15u) == 0) {
@@ -305,11 +317,11 @@ __device__ __forceinline__ void attn_one_row(const PassDesc* __restrict__ pd, co
     float* red = wp + 512;
     const uint32_t t = threadIdx.x;
     const uint32_t D = g.n_heads * hd;
-    const KvView v = kv_view(g, pd->pos0 + m);
+    const KvView v = kv_view(g, row_pos(pd, m));
     const uint32_t C = v.count(), n = C + 1, j0 = c * 256u;
     if (j0 >= n) return;
     const uint32_t j = j0 + t;
-    const size_t plane = plane_index(g, layer, h);
+    const size_t plane = plane_index(g, row_seq(pd, m), layer, h);
     const size_t qrow = (size_t)m * D + h * hd;
     const uint32_t nvis = j0 < C ? min(256u, C - j0) : 0u;
     // every load first: the query, the fp32 self key, this thread's K and V rows
@@ -440,7 +452,7 @@ __global__ __launch_bounds__(128) void k_attn_merge_chunks(const PassDesc* __res
     const uint32_t m = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
     if (m >= pd->m) return;
     const uint32_t hd = g.head_dim, D = g.n_heads * hd;
-    const uint32_t nc = (kv_view(g, pd->pos0 + m).count() + 1 + 255) / 256;
+    const uint32_t nc = (kv_view(g, row_pos(pd, m)).count() + 1 + 255) / 256;
     const size_t mh = (size_t)m * g.n_heads + h;
     const float* st = S + mh * s_stride;
     float mx = st[0];
@@ -490,7 +502,7 @@ __global__ __launch_bounds__(1024) void k_attn_merge_quant(const PassDesc* __res
     }
     if (m >= pd->m) return;
     const uint32_t H = g.n_heads, hd = g.head_dim, D = H * hd;
-    const uint32_t nc = (kv_view(g, pd->pos0 + m).count() + 1 + 255) / 256;
+    const uint32_t nc = (kv_view(g, row_pos(pd, m)).count() + 1 + 255) / 256;
     const float* st = S + (size_t)m * H * s_stride;
     for (uint32_t i = t; i < H * nc; i += 1024) {
         const uint32_t h = i / nc, c = i - h * nc;

@@ -287,6 +287,8 @@ __global__ __launch_bounds__(1024) void k_sample(const float* __restrict__ logit
             push_token(st, tokens, cap, t);
             pdB->tok[0] = t;
             pdB->pos0 = st->pos;
+            pdB->batch = 0;
+            pdB->seq0 = 0;
             break;
         case ROLE_DRAFT:
             st->draft[k] = t;
@@ -311,6 +313,8 @@ __global__ __launch_bounds__(1024) void k_sample(const float* __restrict__ logit
 __global__ void k_ctl_pass_a(DecodeState* st, PassDesc* pdA) {
     pdA->pos0 = st->pos;
     pdA->m = 1;
+    pdA->batch = 0;
+    pdA->seq0 = 0;
     pdA->tok[0] = st->cur;
     st->pos += 1;
     st->have_row4 = 0;
@@ -341,6 +345,123 @@ __global__ void k_ctl_accept(DecodeState* st, const PassDesc* pdB, int32_t* toke
         st->have_row4 = 1;
     }
     st->round_word = a;
+}
+
+// ------------------------------------------- multi-sequence decode rounds
+//
+// A batched round runs the round above for n independent sequences at
+// once: row i of the base pass is sequence sel[i] (state st[sel[i]], token
+// buffer tokens + sel[i] * cap, seed seeds[sel[i]]); the first nm of them
+// run the MTP round and own verify rows [R i, R i + R), R = n_mtp + 1, the
+// rest take the single-token step.  Every decision per sequence is the
+// single-sequence one; the base pass always runs (a verify row that already
+// holds F(cur) is recomputed bit for bit).
+
+// Base pass of a batched round: row i forwards sequence sel[i]'s current
+// token at its next position.  One block.
+__global__ void k_bctl_pass_a(DecodeState* st, const uint32_t* __restrict__ sel, uint32_t n, PassDesc* pdA) {
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
+        DecodeState* S = st + sel[i];
+        pdA->rpos[i] = S->pos;
+        pdA->rseq[i] = sel[i];
+        pdA->tok[i] = S->cur;
+        S->pos += 1;
+        S->have_row4 = 0;
+    }
+    if (threadIdx.x == 0) {
+        pdA->m = n;
+        pdA->batch = 1;
+        pdA->pos0 = 0;
+        pdA->seq0 = 0;
+    }
+}
+
+// Engine::sample for row i of a batched round, block i.  Roles as k_sample:
+// T1 (row i of `logits`; sets up verify rows [R i, R i + R)), DRAFT k (row
+// i), CORRECTIVE (verify row R i + round_acc), FALLBACK (row i).
+__global__ __launch_bounds__(1024) void k_bsample(const float* __restrict__ logits, uint32_t stride, uint32_t V,
+                                                  SamplingCfg cfg, const uint64_t* __restrict__ seeds,
+                                                  DecodeState* st, const uint32_t* __restrict__ sel,
+                                                  uint32_t row0, int32_t* tokens, uint32_t cap, PassDesc* pdB,
+                                                  uint32_t R, int32_t role, int32_t k) {
+    const uint32_t i = row0 + blockIdx.x, s = sel[i];
+    DecodeState* S = st + s;
+    __shared__ uint32_t skip;
+    if (threadIdx.x == 0) skip = (role == ROLE_CORRECTIVE && S->round_acc >= R - 1) ? 1u : 0u;
+    __syncthreads();
+    if (skip) return;
+    const uint32_t r = role == ROLE_CORRECTIVE ? R * i + S->round_acc : i;
+    bool used = false;
+    const int32_t t = sample_row(logits + (size_t)r * stride, V, cfg, seeds[s], S->draw, &used);
+    if (threadIdx.x != 0) return;
+    if (used) S->draw++;
+    int32_t* tk = tokens + (size_t)s * cap;
+    switch (role) {
+        case ROLE_T1:
+            push_token(S, tk, cap, t);
+            pdB->tok[R * i] = t;
+            for (uint32_t j = 0; j < R; j++) {
+                pdB->rpos[R * i + j] = S->pos + j;
+                pdB->rseq[R * i + j] = s;
+            }
+            if (blockIdx.x == 0) {
+                pdB->m = R * gridDim.x;
+                pdB->batch = 1;
+                pdB->pos0 = 0;
+                pdB->seq0 = 0;
+            }
+            break;
+        case ROLE_DRAFT:
+            S->draft[k] = t;
+            pdB->tok[R * i + k + 1] = t;
+            break;
+        case ROLE_CORRECTIVE: {
+            uint32_t a = S->round_acc;
+            uint32_t pushed = 0;
+            if (t != S->draft[a]) { push_token(S, tk, cap, t); S->rejected++; pushed = 1; }
+            S->round_word = a | (pushed << 8);
+            break;
+        }
+        case ROLE_FALLBACK:
+            push_token(S, tk, cap, t);
+            break;
+        default:
+            break;
+    }
+}
+
+// Greedy argmax of every verify row of a batched round: row r is sequence
+// sel[r / R], verify row r % R.  Grid rows, 1024 threads.
+__global__ __launch_bounds__(1024) void k_bargmax_rows(const float* __restrict__ logits, uint32_t V, uint32_t R,
+                                                       const uint32_t* __restrict__ sel, DecodeState* st) {
+    const uint32_t r = blockIdx.x;
+    ArgBest b = block_argmax(logits + (size_t)r * V, V);
+    if (threadIdx.x == 0) st[sel[r / R]].row_argmax[r % R] = b.i;
+}
+
+// Acceptance of k_ctl_accept for the nm MTP sequences of a batched round.
+__global__ void k_bctl_accept(DecodeState* st, const uint32_t* __restrict__ sel, uint32_t nm,
+                              const PassDesc* __restrict__ pdB, uint32_t R, int32_t* tokens, uint32_t cap) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nm) return;
+    const uint32_t s = sel[i], n_mtp = R - 1, pos0 = pdB->rpos[R * i];
+    DecodeState* S = st + s;
+    int32_t* tk = tokens + (size_t)s * cap;
+    uint32_t a = 0;
+    while (a < n_mtp && S->row_argmax[a] == S->draft[a]) {
+        push_token(S, tk, cap, S->draft[a]);
+        a++;
+    }
+    S->round_acc = a;
+    S->accepted += a;
+    if (a < n_mtp) {
+        S->pos = pos0 + a + 1;
+        S->have_row4 = 0;
+    } else {
+        S->pos = pos0 + n_mtp;
+        S->have_row4 = 1;
+    }
+    S->round_word = a;
 }
 
 }  // namespace pf

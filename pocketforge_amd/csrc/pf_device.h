@@ -172,6 +172,14 @@ __device__ __host__ __forceinline__ uint32_t kv_store_row(const KvGeom& g, uint3
     return KV_SINK_ROWS + (p - g.sink_size) % g.ring;
 }
 
+// Position and sequence of row m of a pass.
+__device__ __forceinline__ uint32_t row_pos(const PassDesc* pd, uint32_t m) {
+    return pd->batch ? pd->rpos[m] : pd->pos0 + m;
+}
+__device__ __forceinline__ uint32_t row_seq(const PassDesc* pd, uint32_t m) {
+    return pd->batch ? pd->rseq[m] : pd->seq0;
+}
+
 // Row index (within one (layer, head) plane) of visible entry j.
 __device__ __forceinline__ uint32_t kv_row(const KvGeom& g, const KvView& v, uint32_t j) {
     if (j < v.sink) return j;

@@ -45,28 +45,38 @@ __host__ __device__ constexpr int code_offset(int fmt) { return fmt == FMT_Q4 ? 
 constexpr uint32_t KV_SINK_ROWS = 8;
 constexpr uint32_t MAX_PASS_ROWS = 8;        // decode passes (verify: n_mtp + 1 rows)
 constexpr uint32_t MAX_PREFILL_ROWS = 256;   // prompt passes (int8 MFMA GEMMs)
+constexpr uint32_t MAX_SEQS = 128;           // sequences of a multi-sequence engine
+constexpr uint32_t MAX_ROWS = 512;           // rows of any pass (batched verify: rows x sequences)
 
 struct KvGeom {
     uint32_t n_layers, n_heads, head_dim;
     uint32_t sink_size, window, pool_block, max_context;
     uint32_t ring, pool_cap, rows;   // rows = KV_SINK_ROWS + ring + pool_cap
+    uint32_t n_seq;                  // independent sequences (planes per layer and head)
 };
 
 struct KvPlanes {
-    int8_t* k;      // [layers][heads][rows][head_dim]
+    int8_t* k;      // [sequences][layers][heads][rows][head_dim]
     int8_t* v;
-    float* ks;      // [layers][heads][rows]
+    float* ks;      // [sequences][layers][heads][rows]
     float* vs;
 };
 
 // ------------------------------------------------------ pass descriptor
-// A forward pass over M <= MAX_PASS_ROWS consecutive positions, read by the
-// kernels from device memory so that the control kernels can set up the
-// next pass without a host round trip.
+// A forward pass, read by the kernels from device memory so that the
+// control kernels can set up the next pass without a host round trip.
+// Single-sequence passes (batch == 0) forward consecutive positions
+// pos0, pos0 + 1, ... of sequence seq0.  Batched passes (batch == 1) give
+// each row its own sequence rseq[r] and position rpos[r]; the rows of one
+// sequence are consecutive positions in consecutive rows.
 struct PassDesc {
-    uint32_t pos0;                 // position of row 0
+    uint32_t pos0;                 // position of row 0 (batch == 0)
     uint32_t m;                    // rows in this pass
-    int32_t tok[MAX_PREFILL_ROWS];
+    uint32_t batch;
+    uint32_t seq0;                 // sequence of every row (batch == 0)
+    int32_t tok[MAX_ROWS];
+    uint32_t rpos[MAX_ROWS];       // batch == 1
+    uint32_t rseq[MAX_ROWS];
 };
 
 // Decode-loop state kept on the device.

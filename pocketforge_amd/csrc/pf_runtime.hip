@@ -357,7 +357,7 @@ static void launch_gemv(hipStream_t st, const pf_matrix* W, uint32_t M, const in
 constexpr uint32_t MAX_GEMM_ROWS = 512;
 
 static void launch_gemm(hipStream_t st, const pf_matrix* W, uint32_t M, const int8_t* act, uint32_t act_stride,
-                        double* acc, uint32_t acc_stride) {
+                        double* acc, uint32_t acc_stride, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr) {
     const uint32_t nb = W->cols / 32, nblk = W->rows / 32;
     uint32_t splits = std::max(1u, std::min(nb / 2, (512 + nblk - 1) / nblk));
     const uint32_t bps = (nb + splits - 1) / splits;
@@ -366,8 +366,12 @@ static void launch_gemm(hipStream_t st, const pf_matrix* W, uint32_t M, const in
     const dim3 grid(nblk, splits);
 #define PF_GEMM_CASE(F, T)                                                                                    \
     case T:                                                                                                   \
-        hipLaunchKernelGGL((k_gemm_i8<F, T>), grid, dim3(256), 0, st, W->data, W->cols, M, act, act_stride, bps, \
-                           acc, acc_stride);                                                                  \
+        if (ev0)                                                                                              \
+            hipExtLaunchKernelGGL((k_gemm_i8<F, T>), grid, dim3(256), 0, st, ev0, ev1, 0, W->data, W->cols, M, \
+                                  act, act_stride, bps, acc, acc_stride);                                     \
+        else                                                                                                  \
+            hipLaunchKernelGGL((k_gemm_i8<F, T>), grid, dim3(256), 0, st, W->data, W->cols, M, act, act_stride, \
+                               bps, acc, acc_stride);                                                         \
         break;
 #define PF_GEMM_FMT(F)                                                            \
     switch (mtw) {                                                                \
@@ -382,20 +386,28 @@ static void launch_gemm(hipStream_t st, const pf_matrix* W, uint32_t M, const in
 #undef PF_GEMM_CASE
 }
 
+// y[m] (+= y_in[m]) = h[m] x dequantized rows, any M (launches of up to 8
+// rows; each row's result does not depend on the rows beside it).
 static void launch_gemv_f32(hipStream_t st, const pf_matrix* W, uint32_t M, const float* h, uint32_t h_stride,
                             float* y, uint32_t y_stride, const float* y_in) {
     uint32_t waves = std::min<uint32_t>(W->rows, 2048);
     dim3 grid((waves + 3) / 4);
+    for (uint32_t r0 = 0; r0 < M; r0 += 8) {
+        const uint32_t mb = std::min(8u, M - r0);
+        const float* hr = h + (size_t)r0 * h_stride;
+        float* yr = y + (size_t)r0 * y_stride;
+        const float* yi = y_in ? y_in + (size_t)r0 * y_stride : nullptr;
 #define PF_F32_CASE(MM)                                                                                       \
     case MM:                                                                                                  \
-        hipLaunchKernelGGL(k_gemv_f32<MM>, grid, dim3(256), 0, st, W->data, W->scales, W->rows, W->cols, h,   \
-                           h_stride, y, y_stride, y_in);                                                      \
+        hipLaunchKernelGGL(k_gemv_f32<MM>, grid, dim3(256), 0, st, W->data, W->scales, W->rows, W->cols, hr,  \
+                           h_stride, yr, y_stride, yi);                                                       \
         break;
-    switch (M) {
-        PF_F32_CASE(1) PF_F32_CASE(2) PF_F32_CASE(3) PF_F32_CASE(4)
-        PF_F32_CASE(5) PF_F32_CASE(6) PF_F32_CASE(7) PF_F32_CASE(8)
-    }
+        switch (mb) {
+            PF_F32_CASE(1) PF_F32_CASE(2) PF_F32_CASE(3) PF_F32_CASE(4)
+            PF_F32_CASE(5) PF_F32_CASE(6) PF_F32_CASE(7) PF_F32_CASE(8)
+        }
 #undef PF_F32_CASE
+    }
 }
 
 static int per_for(uint32_t K) {
@@ -660,11 +672,12 @@ static pf_status kv_geom(const pf_ctx* c, uint32_t L, uint32_t H, uint32_t hd, u
     uint32_t evictable = maxc > sink + g->window ? maxc - sink - g->window : 0;
     g->pool_cap = evictable / g->pool_block + 1;
     g->rows = KV_SINK_ROWS + g->ring + g->pool_cap;
+    g->n_seq = 1;
     return PF_OK;
 }
 
 static pf_status kv_alloc(pf_ctx* c, const KvGeom& g, KvPlanes* p, size_t* bytes) {
-    size_t planes = (size_t)g.n_layers * g.n_heads, rows = planes * g.rows;
+    size_t planes = (size_t)g.n_seq * g.n_layers * g.n_heads, rows = planes * g.rows;
     pf_status s = dalloc_t(c, &p->k, rows * g.head_dim);
     if (!s) s = dalloc_t(c, &p->v, rows * g.head_dim);
     if (!s) s = dalloc_t(c, &p->ks, rows);
@@ -677,7 +690,7 @@ static pf_status kv_alloc(pf_ctx* c, const KvGeom& g, KvPlanes* p, size_t* bytes
 }
 
 static void kv_free(pf_ctx* c, const KvGeom& g, KvPlanes* p) {
-    size_t rows = (size_t)g.n_layers * g.n_heads * g.rows;
+    size_t rows = (size_t)g.n_seq * g.n_layers * g.n_heads * g.rows;
     dfree(c, p->k, rows * g.head_dim);
     dfree(c, p->v, rows * g.head_dim);
     dfree(c, p->ks, rows * 4);
@@ -985,8 +998,17 @@ struct pf_engine {
     PassDesc *pdA = nullptr, *pdB = nullptr, *pdP = nullptr;
     DecodeState* st = nullptr;
     int32_t* tokens = nullptr;
-    uint32_t tok_cap = 0;
+    uint32_t tok_cap = 0;         // token-buffer capacity of each sequence
+    size_t tok_alloc = 0;         // elements allocated (nseq * tok_cap)
     uint32_t* word = nullptr;   // pinned readback
+    // multi-sequence engines (pf_batch_*): nseq sequences, each with its own
+    // KV planes, decode state (st[s]) and token buffer (tokens + s * tok_cap)
+    uint32_t nseq = 1;
+    uint32_t rows = MAX_PREFILL_ROWS;   // rows of the pass buffers
+    std::vector<uint32_t> spos;         // host mirror of each sequence's position
+    uint64_t* seeds = nullptr;          // [nseq] sampling seed of each sequence
+    uint32_t* sel = nullptr;            // [nseq] row -> sequence of a batched round
+    float* mlogb = nullptr;             // [nseq][V] draft logits of one head
     std::vector<std::pair<void*, size_t>> owned;
     // host mirrors
     uint32_t pos = 0;
@@ -1244,20 +1266,31 @@ static pf_status decode_check(pf_engine* e) {
     return PF_OK;
 }
 
-extern "C" pf_status pf_engine_create(pf_model* m, const pf_cache_desc* cd, pf_engine** out) {
-    if (!m || !cd || !out) return PF_ERR_ARG;
+static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t nseq, pf_engine** out) {
+    if (!m || !cd || !out || nseq == 0) return PF_ERR_ARG;
     pf_ctx* c = m->ctx;
     if (!model_complete(m)) return fail(c, PF_ERR_STATE, "model has unset matrices");
+    const pf_model_desc& d = m->d;
+    const uint32_t R = d.n_mtp + 1;
+    if (nseq > MAX_SEQS || R * nseq > MAX_ROWS)
+        return fail(c, PF_ERR_UNSUPPORTED, "sequences x (n_mtp + 1) verify rows exceed 512, or more than 128 sequences");
     pf_engine* e = new pf_engine();
     e->m = m;
     e->c = c;
-    const pf_model_desc& d = m->d;
+    e->nseq = nseq;
     pf_status s = kv_geom(c, d.n_layers, d.n_heads, d.head_dim, cd->sink_size, cd->window_size, cd->pool_block,
                           cd->max_context, MAX_PREFILL_ROWS, &e->g);
+    e->g.n_seq = nseq;
     if (!s) s = kv_alloc(c, e->g, &e->kv, &e->kv_bytes);
     if (s) { delete e; return s; }
-    const uint32_t D = d.n_embd, F = d.n_ff, V = d.n_vocab, H = d.n_heads, hd = d.head_dim, MR = MAX_PASS_ROWS;
-    const uint32_t PR = MAX_PREFILL_ROWS;   // rows of the pass buffers (prompt passes)
+    const uint32_t D = d.n_embd, F = d.n_ff, V = d.n_vocab, H = d.n_heads, hd = d.head_dim;
+    // rows of the pass buffers: prompt passes, or a batched verify pass
+    // (the MFMA GEMM reads whole 32-row activation tiles)
+    const uint32_t PR = std::max(MAX_PREFILL_ROWS, (R * nseq + 31) / 32 * 32);
+    const uint32_t MR = std::max(MAX_PASS_ROWS, R * nseq);   // rows of pass-B outputs
+    const uint32_t MA = std::max(MAX_PASS_ROWS, nseq);       // rows of pass-A outputs
+    e->rows = PR;
+    e->spos.assign(nseq, 0);
     e->rope_pos = cd->max_context + 2 * PR;
     {
         std::vector<float> cs, sn;
@@ -1269,7 +1302,7 @@ extern "C" pf_status pf_engine_create(pf_model* m, const pf_cache_desc* cd, pf_e
         PF_HIP(c, hipMemcpy(e->rope_s, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
     }
     e->kmax = std::max(D, F);
-    e->pool_rows_max = (PR + e->g.pool_block - 1) / e->g.pool_block + 1;
+    e->pool_rows_max = (MAX_PREFILL_ROWS + e->g.pool_block - 1) / e->g.pool_block + 1;
     // prompt passes: at most one window of rows, so that every pooled row a
     // pass sees was folded from entries stored before the pass
     e->prefill_rows = std::min(PR, e->g.window);
@@ -1294,19 +1327,22 @@ extern "C" pf_status pf_engine_create(pf_model* m, const pf_cache_desc* cd, pf_e
     if (!s) s = ealloc(e, &e->v, (size_t)PR * D);
     if (!s) s = ealloc(e, &e->S, (size_t)PR * H * e->s_stride);
     if (!s) s = ealloc(e, &e->Wp, (size_t)PR * H * e->cstride * hd);
-    if (!s) s = ealloc(e, &e->logitsA, (size_t)MR * V);
-    if (!s) s = ealloc(e, &e->hiddenA, (size_t)MR * D);
+    if (!s) s = ealloc(e, &e->logitsA, (size_t)MA * V);
+    if (!s) s = ealloc(e, &e->hiddenA, (size_t)MA * D);
     if (!s) s = ealloc(e, &e->logitsB, (size_t)MR * V);
     if (!s) s = ealloc(e, &e->hiddenB, (size_t)MR * D);
-    if (!s) s = ealloc(e, &e->mcur, D);
-    if (!s) s = ealloc(e, &e->mg, D);
-    if (!s) s = ealloc(e, &e->mu, D);
-    if (!s) s = ealloc(e, &e->ma, D);
+    if (!s) s = ealloc(e, &e->mcur, (size_t)nseq * D);
+    if (!s) s = ealloc(e, &e->mg, (size_t)nseq * D);
+    if (!s) s = ealloc(e, &e->mu, (size_t)nseq * D);
+    if (!s) s = ealloc(e, &e->ma, (size_t)nseq * D);
     if (!s) s = ealloc(e, &e->mlogits, (size_t)std::max(1u, d.n_mtp) * V);
+    if (!s) s = ealloc(e, &e->mlogb, (size_t)nseq * V);
+    if (!s) s = ealloc(e, &e->seeds, nseq);
+    if (!s) s = ealloc(e, &e->sel, nseq);
     if (!s) s = ealloc(e, &e->pdA, 1);
     if (!s) s = ealloc(e, &e->pdB, 1);
     if (!s) s = ealloc(e, &e->pdP, 1);
-    if (!s) s = ealloc(e, &e->st, 1);
+    if (!s) s = ealloc(e, &e->st, nseq);
     if (s) { pf_engine_destroy(e); return s; }
     if (hipHostMalloc((void**)&e->word, 64, hipHostMallocDefault) != hipSuccess) {
         pf_engine_destroy(e);
@@ -1318,7 +1354,7 @@ extern "C" pf_status pf_engine_create(pf_model* m, const pf_cache_desc* cd, pf_e
     if (const char* ng = std::getenv("PF_NO_GRAPHS")) e->use_graphs = !(ng[0] == '1');
     {
         const char* pv = std::getenv("PF_PERSISTENT");
-        e->dec = pv && pv[0] == '1';
+        e->dec = pv && pv[0] == '1' && nseq == 1;
         if (e->dec && (s = decode_setup(e))) {
             pf_engine_destroy(e);
             return s;
@@ -1326,13 +1362,21 @@ extern "C" pf_status pf_engine_create(pf_model* m, const pf_cache_desc* cd, pf_e
     }
     PF_HIP(c, hipEventCreate(&e->rev0));
     PF_HIP(c, hipEventCreate(&e->rev1));
+    // every field of the pass descriptors defined (single-sequence passes of
+    // sequence 0) before any kernel reads them
     PassDesc pb{};
+    PF_HIP(c, hipMemcpy(e->pdA, &pb, sizeof(pb), hipMemcpyHostToDevice));
+    PF_HIP(c, hipMemcpy(e->pdP, &pb, sizeof(pb), hipMemcpyHostToDevice));
     pb.m = d.n_mtp + 1;
     PF_HIP(c, hipMemcpy(e->pdB, &pb, sizeof(pb), hipMemcpyHostToDevice));
-    DecodeState st0{};
-    PF_HIP(c, hipMemcpy(e->st, &st0, sizeof(st0), hipMemcpyHostToDevice));
+    std::vector<DecodeState> st0(nseq);
+    PF_HIP(c, hipMemcpy(e->st, st0.data(), nseq * sizeof(DecodeState), hipMemcpyHostToDevice));
     *out = e;
     return PF_OK;
+}
+
+extern "C" pf_status pf_engine_create(pf_model* m, const pf_cache_desc* cd, pf_engine** out) {
+    return engine_create(m, cd, 1, out);
 }
 
 extern "C" void pf_engine_destroy(pf_engine* e) {
@@ -1346,7 +1390,7 @@ extern "C" void pf_engine_destroy(pf_engine* e) {
     if (e->rev0) (void)hipEventDestroy(e->rev0);
     if (e->rev1) (void)hipEventDestroy(e->rev1);
     for (auto& p : e->owned) dfree(e->c, p.first, p.second);
-    if (e->tokens) dfree(e->c, e->tokens, (size_t)e->tok_cap * 4);
+    if (e->tokens) dfree(e->c, e->tokens, e->tok_alloc * 4);
     kv_free(e->c, e->g, &e->kv);
     if (e->word) (void)hipHostFree(e->word);
     delete e;
@@ -1355,6 +1399,7 @@ extern "C" void pf_engine_destroy(pf_engine* e) {
 extern "C" pf_status pf_engine_reset(pf_engine* e) {
     if (!e) return PF_ERR_ARG;
     e->pos = 0;
+    std::fill(e->spos.begin(), e->spos.end(), 0u);
     e->hidden_valid = false;
     return PF_OK;
 }
@@ -1424,7 +1469,8 @@ static pf_status pass_gemv(pf_engine* e, const pf_matrix* W, uint32_t M) {
         }
         e->kev_bytes[e->kev_used] = (double)W->bytes + (double)M * W->cols + (double)M * W->rows * 4.0;
         TimedPass* t = &e->kev[e->kev_used++];
-        launch_gemv(st, W, M, e->act, ks, e->bsum, bs, e->acc, W->rows, t->a, t->b);
+        if (M <= MAX_PASS_ROWS) launch_gemv(st, W, M, e->act, ks, e->bsum, bs, e->acc, W->rows, t->a, t->b);
+        else launch_gemm(st, W, M, e->act, ks, e->acc, W->rows, t->a, t->b);
     } else if (M <= MAX_PASS_ROWS) {
         launch_gemv(st, W, M, e->act, ks, e->bsum, bs, e->acc, W->rows);
     } else {
@@ -1440,33 +1486,41 @@ static Prefetch prefetch_of(const pf_engine* e, const pf_matrix* W) {
 
 // One forward pass of M rows (the PassDesc at `pd` holds positions and
 // tokens; pos0 is the host's copy of the first position).  hidden/logits
-// outputs are device [M][D] / [M][V] (M <= 8 when set); either may be null.
-static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0, float* logits, float* hidden) {
+// outputs are device [M][D] / [M][V]; either may be null.  A batched pass
+// (the descriptor gives every row its sequence and position) passes
+// batch = true and the highest position of its rows as pos_last.
+static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0, float* logits, float* hidden,
+                          bool batch = false, uint32_t pos_last = 0) {
     pf_ctx* c = e->c;
     const pf_model* m = e->m;
     const pf_model_desc& d = m->d;
     const KvGeom& g = e->g;
     hipStream_t st = c->stream;
     const uint32_t D = d.n_embd, F = d.n_ff, H = d.n_heads, hd = d.head_dim;
-    if (!e->capturing && pos0 + M > e->rope_pos)
+    if (!batch) pos_last = pos0 + M - 1;
+    if (M == 0 || M > e->rows) return fail(c, PF_ERR_ARG, "pass height beyond the engine's pass buffers");
+    if (!e->capturing && pos_last + 1 > e->rope_pos)
         return fail(c, PF_ERR_CAPACITY, "position beyond the engine's max_context");
     // captured passes replay at any position: grids sized for the largest view
-    const uint32_t cmax = e->capturing ? e->cmax : kv_view(g, pos0 + M - 1).count();
+    const uint32_t cmax = e->capturing ? e->cmax : kv_view(g, pos_last).count();
     // attention tasks: (head, 256-entry chunk) groups of M rows, 8-aligned per XCD
     const uint32_t attn_groups = H * ((cmax + 1 + 255) / 256);
     const uint32_t attn_blocks = 8 * M * ((attn_groups + 7) / 8);
     const uint32_t ks = e->kmax, bs = e->kmax / 32;
-    float* as0 = e->as;           // attention-norm act
-    float* as1 = e->as + 8;       // attention output act
-    float* as2 = e->as + 16;      // ffn-norm act
-    float* as3 = e->as + 24;      // swiglu act
+    // activation scales [4][rows]: each kernel reads one array and writes
+    // another, so the arrays must not overlap for any pass height
+    float* as0 = e->as;                   // attention-norm act
+    float* as1 = e->as + e->rows;         // attention output act
+    float* as2 = e->as + 2 * e->rows;     // ffn-norm act
+    float* as3 = e->as + 3 * e->rows;     // swiglu act
     const dim3 tb(hd <= 64 ? 64 : 128);
 
     // pooled rows the pass can see (folded from window entries still in the ring)
-    hipLaunchKernelGGL(k_pool_rows, dim3(g.n_layers * g.n_heads, e->pool_rows_max), tb, 0, st, g, e->kv, pd);
+    hipLaunchKernelGGL(k_pool_rows, dim3(g.n_layers * g.n_heads, batch ? M : e->pool_rows_max), tb, 0, st, g, e->kv,
+                       pd);
     hipLaunchKernelGGL(k_embed, dim3((D + 255) / 256, M), dim3(256), 0, st, m->emb->data, m->emb->scales, d.n_vocab, D,
                        pd, e->x);
-    if (e->dec && M <= MAX_PASS_ROWS && d.n_layers) {
+    if (e->dec && !batch && M <= MAX_PASS_ROWS && d.n_layers) {
         // every layer in one persistent kernel; verify passes carry timing
         // events in profiling mode
         hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -1532,6 +1586,7 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
 
 extern "C" pf_status pf_forward(pf_engine* e, const int32_t* tokens, uint32_t n, float* logits, float* hidden) {
     if (!e || !tokens || n == 0) return PF_ERR_ARG;
+    if (e->nseq != 1) return fail(e->c, PF_ERR_STATE, "multi-sequence engine: use pf_batch_forward");
     if (n > ((logits || hidden) ? MAX_PASS_ROWS : e->prefill_rows))
         return fail(e->c, PF_ERR_ARG, "pass too tall: 8 rows with outputs, else one window up to 256 rows");
     if (e->pos + n > e->rope_pos) return fail(e->c, PF_ERR_CAPACITY, "position beyond the engine's max_context");
@@ -1703,6 +1758,20 @@ static pf_status ensure_round_graphs(pf_engine* e, const SamplingCfg& cfg, uint6
     return PF_OK;
 }
 
+// Token buffers of every sequence with `cap` entries each (tokens + s * cap).
+static pf_status ensure_tokens(pf_engine* e, uint32_t cap) {
+    if (e->tokens) dfree(e->c, e->tokens, e->tok_alloc * 4);
+    e->tokens = nullptr;
+    e->tok_cap = 0;
+    e->tok_alloc = 0;
+    const size_t n = (size_t)e->nseq * cap;
+    if (pf_status s = dalloc_t(e->c, &e->tokens, n)) return s;
+    e->tok_cap = cap;
+    e->tok_alloc = n;
+    e->graphs_valid = false;   // the captured rounds hold the old buffer
+    return PF_OK;
+}
+
 // Engine::generate, src/engine.cpp:276-396.  Prompt prefilled in passes
 // of up to 8 tokens; then MTP rounds (src/engine.cpp:304-373) as one base
 // pass (skipped when the previous round accepted every draft: its last
@@ -1713,6 +1782,7 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
                                  const pf_sampling* scfg, uint64_t seed, int32_t* tokens_out, uint32_t tokens_cap,
                                  pf_gen_result* res) {
     if (!e || (!prompt && n_prompt) || !tokens_out || !res) return PF_ERR_ARG;
+    if (e->nseq != 1) return fail(e->c, PF_ERR_STATE, "multi-sequence engine: use pf_batch_generate");
     pf_ctx* c = e->c;
     const pf_model_desc& d = e->m->d;
     hipStream_t st = c->stream;
@@ -1725,13 +1795,7 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
         if (prompt[i] < 0 || (uint32_t)prompt[i] >= V) return fail(c, PF_ERR_ARG, "prompt token id out of range");
     const SamplingCfg cfg = to_cfg(scfg);
     if (e->tok_cap < tokens_cap) {
-        if (e->tokens) dfree(c, e->tokens, (size_t)e->tok_cap * 4);
-        e->tokens = nullptr;
-        e->tok_cap = 0;
-        pf_status s = dalloc_t(c, &e->tokens, tokens_cap);
-        if (s) return s;
-        e->tok_cap = tokens_cap;
-        e->graphs_valid = false;   // the captured rounds hold the old buffer
+        if (pf_status s = ensure_tokens(e, tokens_cap)) return s;
     }
     if (n_prompt) PF_HIP(c, hipMemcpyAsync(e->tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice, st));
     auto t0 = std::chrono::steady_clock::now();
@@ -1879,3 +1943,5 @@ extern "C" pf_status pf_engine_pass_times(const pf_engine* e, double* verify_us,
     if (bn) *bn = e->base_n;
     return PF_OK;
 }
+
+#include "pf_batch.hip"
