@@ -45,6 +45,10 @@ CONFIGS = {
                        "(top-k 40 not reached: the reference dispatch takes top-p first), Philox seed 7"),
     "B-long": dict(model="ONE_B", fmts="ALL_Q4", kv=(4, 4096, 16), prompt=32768, new=256, samp=(0.8, 0.95, 40, 1),
                    name="1B Q4, 4 Q4 MTP heads, greedy, long context"),
+    # many sequences decoded together: verify passes of 64 x 5 = 320 rows on
+    # the int8 MFMA GEMM; a step generates `new` tokens per sequence
+    "E": dict(model="ONE_B", fmts="ALL_Q4", kv=(4, 8192, 64), prompt=8192, new=64, samp=(0.8, 0.95, 40, 1),
+              seqs=64, name="1B Q4, 4 Q4 MTP heads, greedy, 64 sequences (distinct prompts) decoded together"),
 }
 
 
@@ -152,6 +156,9 @@ def main():
     t0 = time.perf_counter()
     model = pf.Model(ctx, cfg, w)
     log(f"weights uploaded in {time.perf_counter() - t0:.1f}s on {dev} ({cus} CUs)")
+    if "seqs" in C:
+        bench_batch(args, C, cfg, w, ctx, dev, model)
+        return
     max_ctx = args.prompt + args.new + 64
     sink, window, pool = C["kv"]
     kv = dict(sink_size=sink, window_size=window, pool_block=pool, max_context=max_ctx)
@@ -257,6 +264,136 @@ def main():
     if not args.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(cfg, w, kv, prompt, C["samp"], args.config)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+    eng.close()
+    model.close()
+    ctx.close()
+
+
+GEMM_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA
+
+
+def bench_batch(args, C, cfg, w, ctx, dev, model):
+    """Many sequences decoded together.  Every sequence's prompt (its own
+    seed) is prefilled once, outside the timer, up to its last token; step k
+    is one batched generate of `new` tokens per sequence that forwards each
+    sequence's last token and continues its decode (the contexts grow by
+    about new + 1 per step).  value = generated tokens of all sequences /
+    wall time of the timed steps."""
+    import pocketforge_amd as pf
+    from pocketforge_amd import weights as W
+    N = C["seqs"]
+    sink, window, pool = C["kv"]
+    n_steps = args.warmup + args.steps + 1
+    max_ctx = args.prompt + (args.new + 8) * n_steps + 64
+    kv = dict(sink_size=sink, window_size=window, pool_block=pool, max_context=max_ctx)
+    eng = pf.BatchEngine(model, N, **kv)
+    samp = pf.Sampling(*C["samp"])
+    seeds = np.full(N, 7, np.uint64)
+    prompts = [W.prompt_ids(args.prompt, cfg["n_vocab"], seed=42 + s) for s in range(N)]
+    t = time.perf_counter()
+    for s in range(N):
+        eng.prefill_seq(s, prompts[s][:-1])
+        if s % 8 == 7:
+            log(f"prefilled {s + 1} sequences ({time.perf_counter() - t:.1f}s)")
+    prefill_s = time.perf_counter() - t
+    last = [p[-1:] for p in prompts]
+
+    def step(profile):
+        eng.profile(profile)
+        t0 = time.perf_counter()
+        toks, res = eng.generate_batch(last, args.new, samp, seeds)
+        ctx.synchronize()
+        dt = time.perf_counter() - t0
+        for s in range(N):
+            last[s] = toks[s][-1:]
+        return dt, toks, res
+
+    for i in range(args.warmup):
+        dt, toks, res = step(False)
+        log(f"warmup {i}: {sum(len(x) - 1 for x in toks)} tokens in {dt * 1e3:.1f} ms")
+    times, gens, accs, rejs, rounds, round_us = [], [], [], [], [], []
+    for i in range(args.steps):
+        dt, toks, res = step(False)
+        r_us, r_n = eng.round_time()
+        times.append(dt)
+        gens.append(sum(len(x) - 1 for x in toks))
+        accs.append(sum(r.mtp_accepted for r in res))
+        rejs.append(sum(r.mtp_rejected for r in res))
+        rounds.append(max(r.rounds for r in res))
+        round_us.append((r_us, r_n))
+        log(f"step {i}: {gens[-1]} tokens in {dt * 1e3:.1f} ms ({gens[-1] / dt:.1f} tok/s), rounds {rounds[-1]}, "
+            f"device time per round {r_us:.1f} us")
+    value = sum(gens) / sum(times)
+    # one more step of the same workload with HIP start/stop events attached
+    # to every GEMM dispatch of the verify passes (M = 5 x sequences)
+    dt_p, toks_p, res_p = step(True)
+    n_l, gemm_us, gemm_bytes = eng.gemv_stats()
+    v_us, b_us, vn, bn = eng.pass_times()
+    eng.profile(False)
+    M = N * (cfg["n_mtp"] + 1)
+    D, F = cfg["n_embd"], cfg["n_ff"]
+    nk = [(3 * D, D), (D, D), (2 * F, D), (D, F)]    # QKV, O, gate|up, down (N x K) of every layer
+    gemm_ops = 2.0 * M * sum(n * k for n, k in nk) / len(nk)
+    log(f"profiled step: {dt_p * 1e3:.1f} ms, verify pass {v_us:.1f} us x{vn}, base pass {b_us:.1f} us x{bn}, "
+        f"gemm {gemm_us:.2f} us avg x{n_l}")
+    achieved = gemm_ops / gemm_us / 1e6
+    r_avg = sum(r[0] * r[1] for r in round_us) / max(1, sum(r[1] for r in round_us))
+    wbytes = W.packed_bytes(w) + w["emb"][1].nbytes + w["emb"][2].nbytes
+    p_mid = args.prompt + (args.warmup + args.steps // 2) * (args.new + 1)
+    kv_bytes = N * cfg["n_layers"] * 2 * cfg["n_heads"] * (cfg["head_dim"] + 4) * view_count(p_mid, sink, window, pool)
+    out = {
+        "metric": f"accepted tok/s (all sequences), configuration E, MTP draft=4, {N} sequences",
+        "value": round(value, 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * sum(times) / len(times), 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (random-init weights N(0,0.02), uniform random prompt ids, one prompt seed per sequence)",
+        "config": {
+            "workload": (f"{C['name']}, draft=4, {args.prompt}-token prompt per sequence, {args.new} generated per "
+                         f"sequence per step, int8 3-tier KV (sink {sink}, window {window}, pool {pool})"),
+            "sequences": N,
+            "verify_rows": M,
+            "accepted_per_round": round(sum(accs) / max(1, sum(rounds) * N), 4),
+            "mtp_accepted": sum(accs), "mtp_rejected": sum(rejs), "rounds": sum(rounds),
+            "tokens_per_step": gens[0],
+            "device_us_per_round": round(r_avg, 2),
+            "prefill_tok_s": round(N * (args.prompt - 1) / prefill_s, 1),
+            "device": dev,
+        },
+        "roofline": {
+            "kernel": f"k_gemm_i8<Q4> (verify-pass int8 x Q4 GEMM, M={M})",
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": GEMM_PEAK_TOPS,
+            "unit": "TOP/s",
+            "frac": round(achieved / GEMM_PEAK_TOPS, 4),
+            "traffic": None,
+            "avg_launch_us": round(gemm_us, 3),
+            "avg_ops_per_launch": round(gemm_ops),
+            "avg_bytes_per_launch": round(gemm_bytes),
+            "launches": n_l,
+            "timing": "HIP start/stop events attached to each GEMM dispatch (hipExtLaunchKernelGGL) on the engine "
+                      "stream, in one extra step of the same workload",
+        },
+        "verify_pass": {
+            "avg_us": round(v_us, 2),
+            "bytes": round(wbytes + kv_bytes),
+            "achieved_GBps": round((wbytes + kv_bytes) / v_us / 1e3, 1),
+            "frac": round((wbytes + kv_bytes) / v_us / 1e3 / HBM_PEAK_GBPS, 4),
+        },
+    }
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline(cfg, w, kv, prompts[0], C["samp"], "E, one sequence")
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

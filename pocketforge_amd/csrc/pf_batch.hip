@@ -138,7 +138,10 @@ static pf_status batch_mtp_chain(pf_engine* e, const float* h0, uint32_t n, cons
 }
 
 // Engine::generate (src/engine.cpp:276-396) for every sequence at once.
-// Prompts are prefilled sequence by sequence; then each round runs one
+// Prompts are forwarded in order: all but the last 8 tokens of each in
+// single-sequence passes, the rest in passes that batch the prompt tails of
+// many sequences (a one-token prompt per sequence is one pass); then each
+// round runs one
 // batched base pass over the unfinished sequences, T1 and the drafts of the
 // sequences that take an MTP round (n_gen + 4 <= max_new), one batched
 // verify pass over their [T1, drafts] rows, acceptance and correctives, and
@@ -181,14 +184,49 @@ extern "C" pf_status pf_batch_generate(pf_engine* e, const int32_t* prompts, con
     auto t0 = std::chrono::steady_clock::now();
     std::vector<DecodeState> hs(N);
     {
-        size_t off = 0;
+        // long prompts in single-sequence passes (their rows share one KV
+        // list), the last <= 8 tokens of every prompt in batched passes
+        std::vector<size_t> off(N + 1, 0);
+        for (uint32_t s = 0; s < N; s++) off[s + 1] = off[s] + prompt_lens[s];
+        std::vector<uint32_t> tail(N);
         for (uint32_t s = 0; s < N; s++) {
-            if (pf_status r = batch_prefill_seq(e, s, prompts + off, prompt_lens[s])) { batch_sync_out(e); return r; }
+            const uint32_t head = prompt_lens[s] > MAX_PASS_ROWS ? prompt_lens[s] - MAX_PASS_ROWS : 0;
+            tail[s] = prompt_lens[s] - head;
+            if (pf_status r = batch_prefill_seq(e, s, prompts + off[s], head)) { batch_sync_out(e); return r; }
+        }
+        PassDesc& pd = e->pd_host;
+        for (uint32_t s0 = 0; s0 < N;) {
+            uint32_t rows = 0, pos_last = 0, s1 = s0;
+            for (; s1 < N && rows + tail[s1] <= e->rows; s1++) {
+                const uint32_t head = prompt_lens[s1] - tail[s1];
+                for (uint32_t j = 0; j < tail[s1]; j++, rows++) {
+                    pd.tok[rows] = prompts[off[s1] + head + j];
+                    pd.rpos[rows] = e->spos[s1] + j;
+                    pd.rseq[rows] = s1;
+                    pos_last = std::max(pos_last, pd.rpos[rows]);
+                }
+            }
+            if (rows) {
+                pd.pos0 = 0;
+                pd.m = rows;
+                pd.batch = 1;
+                pd.seq0 = 0;
+                PF_HIP(c, hipMemcpyAsync(e->pdP, &pd, sizeof(PassDesc), hipMemcpyHostToDevice, st));
+                PF_HIP(c, hipStreamSynchronize(st));
+                pd.batch = 0;
+                if (pf_status r = run_pass(e, e->pdP, rows, 0, nullptr, nullptr, true, pos_last)) {
+                    batch_sync_out(e);
+                    return r;
+                }
+                for (uint32_t s = s0; s < s1; s++) e->spos[s] += tail[s];
+            }
+            s0 = s1;
+        }
+        for (uint32_t s = 0; s < N; s++) {
             hs[s] = DecodeState{};
             hs[s].pos = e->spos[s];
-            hs[s].cur = prompt_lens[s] ? prompts[off + prompt_lens[s] - 1] : 0;
+            hs[s].cur = prompt_lens[s] ? prompts[off[s] + prompt_lens[s] - 1] : 0;
             hs[s].n_tokens = prompt_lens[s];
-            off += prompt_lens[s];
         }
     }
     PF_HIP(c, hipMemcpyAsync(e->st, hs.data(), (size_t)N * sizeof(DecodeState), hipMemcpyHostToDevice, st));
