@@ -297,7 +297,10 @@ __global__ void k_wsum_combine_one(const float* __restrict__ Wp, uint32_t nch, u
 // Up[((m*H + h)*cstride + c)*hd + i] = U_c[i].
 
 // Shared memory of one attention block (bytes): V rows of the chunk first.
-constexpr uint32_t ATT_VT = 256 * 144;             // 256 rows, 16 bytes of padding each
+// V rows with 8 bytes of padding each: the block's LDS stays under 40 KB,
+// so four blocks fit in a CU's 160 KB
+constexpr uint32_t ATT_VROW = 136;
+constexpr uint32_t ATT_VT = 256 * ATT_VROW;
 constexpr uint32_t ATT_SMEM = ATT_VT + (128 + 128 + 256 + 256 + 512 + 4) * 4;
 
 template <int PARTS>
@@ -308,7 +311,7 @@ __device__ __forceinline__ void attn_one_row(const PassDesc* __restrict__ pd, co
                                              uint32_t s_stride, float* __restrict__ Up, uint32_t cstride,
                                              uint8_t* smem) {
     constexpr uint32_t hd = 16 * PARTS;
-    int8_t (*vt)[144] = reinterpret_cast<int8_t (*)[144]>(smem);
+    int8_t (*vt)[ATT_VROW] = reinterpret_cast<int8_t (*)[ATT_VROW]>(smem);
     float* qs = reinterpret_cast<float*>(smem + ATT_VT);
     float* kss = qs + 128;
     float* vsc = kss + 128;
@@ -344,7 +347,10 @@ __device__ __forceinline__ void attn_one_row(const PassDesc* __restrict__ pd, co
         ks = kv.ks[row];
         vs = kv.vs[row];
 #pragma unroll
-        for (int p = 0; p < PARTS; p++) *reinterpret_cast<int4*>(&vt[t][p * 16]) = vw[p];
+        for (int p = 0; p < PARTS; p++) {
+            *reinterpret_cast<int2*>(&vt[t][p * 16]) = make_int2(vw[p].x, vw[p].y);
+            *reinterpret_cast<int2*>(&vt[t][p * 16 + 8]) = make_int2(vw[p].z, vw[p].w);
+        }
     }
     vsc[t] = vs;                 // 0 past the visible entries: their terms below add exactly 0
     __syncthreads();
