@@ -40,16 +40,10 @@ __device__ __forceinline__ float expf_c(float x) {
     return p * u2f((uint32_t)(k + 127) << 23);
 }
 
-// IEEE binary16 bits -> float (exact).
+// IEEE binary16 bits -> float: v_cvt_f32_f16, exact for every finite value
+// (subnormal halves included: this code is built without denormal flushing).
 __device__ __forceinline__ float h2f(uint16_t h) {
-    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
-    uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
-    if (e == 0) {
-        float v = (float)m * 0x1p-24f;
-        return sign ? -v : v;
-    }
-    if (e == 31) return u2f(sign | 0x7F800000u | (m << 13));
-    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+    return (float)__builtin_bit_cast(_Float16, h);
 }
 
 // Philox4x32-10 (Salmon et al., SC'11).

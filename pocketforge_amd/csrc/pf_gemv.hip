@@ -131,6 +131,36 @@ typedef int pf_v16i __attribute__((ext_vector_type(16)));
 // of a tile, packed 4 per dword in element order (MFMA B operand).  Byte
 // x - OFF is formed as (x + (0x80 - OFF)) ^ 0x80 per byte (no carries: every
 // byte sum is below 0x100).
+// Raw code bytes of weight row r, block t (Q4: 16 bytes; Q2/Q1.5: 8 bytes in
+// .x, .y), loaded one block ahead of their use.
+template <int FMT>
+__device__ __forceinline__ uint4 gemm_raw(const uint8_t* tile, uint32_t t, uint32_t r) {
+    if constexpr (FMT == FMT_Q4) return *reinterpret_cast<const uint4*>(tile + t * 1024u + r * 16u);
+    const uint2 c = *reinterpret_cast<const uint2*>(tile + (t >> 1) * 1024u + r * 16u + (t & 1u) * 8u);
+    return make_uint4(c.x, c.y, 0u, 0u);
+}
+
+template <int FMT>
+__device__ __forceinline__ pf_v4i gemm_unpack(uint4 c, uint32_t h) {
+    constexpr uint32_t OFF = (uint32_t)code_offset(FMT);
+    constexpr uint32_t ADD = (0x80u - OFF) * 0x01010101u;
+    pf_v4i v;
+    if constexpr (FMT == FMT_Q4) {
+        const uint32_t sh = 4u * h, m = 0x0F0F0F0Fu;
+        v.x = (int)((((c.x >> sh) & m) + ADD) ^ 0x80808080u);
+        v.y = (int)((((c.y >> sh) & m) + ADD) ^ 0x80808080u);
+        v.z = (int)((((c.z >> sh) & m) + ADD) ^ 0x80808080u);
+        v.w = (int)((((c.w >> sh) & m) + ADD) ^ 0x80808080u);
+    } else {
+        const uint32_t sh = 4u * h, m = 0x03030303u;
+        v.x = (int)((((c.x >> sh) & m) + ADD) ^ 0x80808080u);
+        v.y = (int)((((c.y >> sh) & m) + ADD) ^ 0x80808080u);
+        v.z = (int)((((c.x >> (sh + 2u)) & m) + ADD) ^ 0x80808080u);
+        v.w = (int)((((c.y >> (sh + 2u)) & m) + ADD) ^ 0x80808080u);
+    }
+    return v;
+}
+
 template <int FMT>
 __device__ __forceinline__ pf_v4i gemm_codes(const uint8_t* tile, uint32_t t, uint32_t r, uint32_t h) {
     constexpr uint32_t OFF = (uint32_t)code_offset(FMT);
@@ -182,25 +212,41 @@ __global__ __launch_bounds__(256) void k_gemm_i8(const uint8_t* __restrict__ W, 
 #pragma unroll
         for (int i = 0; i < 16; i++) S[j][i] = 0.0;
     const pf_v16i zero = {};
-    for (uint32_t b = b_begin; b < b_end; b++) {
+    // raw operands of block b: code bytes, block scale bits, activation tiles
+    auto load = [&](uint32_t b, uint4& bw, uint16_t& d, pf_v4i (&a)[MTW]) {
         const uint8_t* tile = tiles + (size_t)(b >> 3) * TB;
         const uint32_t t = b & 7u;
-        const pf_v4i bw = gemm_codes<FMT>(tile, t, r, h);
-        const double d = (double)h2f(*reinterpret_cast<const uint16_t*>(tile + CODES + r * 16u + t * 2u));
-        pf_v4i a[MTW];
+        bw = gemm_raw<FMT>(tile, t, r);
+        d = *reinterpret_cast<const uint16_t*>(tile + CODES + r * 16u + t * 2u);
+        // every tile loads (a wave's tiles past the last one reload it, unused),
+        // so the number of loads in flight is fixed and the waits are exact
 #pragma unroll
         for (int j = 0; j < MTW; j++) {
-            const uint32_t mt = wid + 4u * j;
-            a[j] = mt < mtiles ? *reinterpret_cast<const pf_v4i*>(act + (size_t)(mt * 32u + l32) * act_stride +
-                                                                   b * 32u + 16u * h)
-                               : pf_v4i{0, 0, 0, 0};
+            const uint32_t mt = min(wid + 4u * j, mtiles - 1u);
+            a[j] = *reinterpret_cast<const pf_v4i*>(act + (size_t)(mt * 32u + l32) * act_stride + b * 32u + 16u * h);
         }
+    };
+    // the next block's operands load while this block's MFMAs and scaling run
+    uint4 bw_n{};
+    uint16_t d_n = 0;
+    pf_v4i a_n[MTW];
+    if (b_begin < b_end) load(b_begin, bw_n, d_n, a_n);
+    for (uint32_t b = b_begin; b < b_end; b++) {
+        const pf_v4i bw = gemm_unpack<FMT>(bw_n, h);
+        const double d = (double)h2f(d_n);
+        pf_v4i a[MTW];
+#pragma unroll
+        for (int j = 0; j < MTW; j++) a[j] = a_n[j];
+        load(min(b + 1, b_end - 1), bw_n, d_n, a_n);      // unconditional: exact wait counts
+        pf_v16i p[MTW];
+#pragma unroll
+        for (int j = 0; j < MTW; j++)
+            if (wid + 4u * j < mtiles) p[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], bw, zero, 0, 0, 0);
 #pragma unroll
         for (int j = 0; j < MTW; j++) {
             if (wid + 4u * j < mtiles) {
-                const pf_v16i p = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], bw, zero, 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 16; i++) S[j][i] = __builtin_fma(d, (double)p[i], S[j][i]);
+                for (int i = 0; i < 16; i++) S[j][i] = __builtin_fma(d, (double)p[j][i], S[j][i]);
             }
         }
     }

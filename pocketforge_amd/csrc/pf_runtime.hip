@@ -353,16 +353,19 @@ static void launch_gemv(hipStream_t st, const pf_matrix* W, uint32_t M, const in
 
 // acc[M][rows] += int8 activations x tiled block matrix for M > 8 rows
 // (MFMA GEMM, exact fp64 like the GEMV).  act must hold ceil(M / 32) * 32
-// readable rows.  K splits: enough blocks for 512 workgroups.
+// readable rows.  K splits: enough for about 256 workgroups when each wave
+// holds two or more M tiles, 512 with one (measured on MI355X at M = 64,
+// 256 and 320 over the 1B shapes).
 constexpr uint32_t MAX_GEMM_ROWS = 512;
 
 static void launch_gemm(hipStream_t st, const pf_matrix* W, uint32_t M, const int8_t* act, uint32_t act_stride,
                         double* acc, uint32_t acc_stride, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr) {
     const uint32_t nb = W->cols / 32, nblk = W->rows / 32;
-    uint32_t splits = std::max(1u, std::min(nb / 2, (512 + nblk - 1) / nblk));
+    const uint32_t mtw = ((M + 31) / 32 + 3) / 4;
+    const uint32_t target = mtw >= 2 ? 256 : 512;
+    uint32_t splits = std::max(1u, std::min(nb / 2, (target + nblk - 1) / nblk));
     const uint32_t bps = (nb + splits - 1) / splits;
     splits = (nb + bps - 1) / bps;
-    const uint32_t mtw = ((M + 31) / 32 + 3) / 4;
     const dim3 grid(nblk, splits);
 #define PF_GEMM_CASE(F, T)                                                                                    \
     case T:                                                                                                   \
