@@ -63,3 +63,51 @@ def test_config_blong_cache_geometry(gpu, tiny_weights):
     toks, res, ot, oa, orj = _both(gpu, cfg, w, kv, prompt, 40, pf.Sampling(0.8, 0.95, 40, 1), 7)
     np.testing.assert_array_equal(toks, ot)
     assert (res.mtp_accepted, res.mtp_rejected) == (oa, orj)
+
+
+# ------------------------------------------------ full-size token streams
+#
+# The oracle's streams at the benchmark configurations' full sizes are
+# fixtures (tests/golden/stream_*.npz, written by
+# tests/golden/make_config_streams.py on the host): B (2048-token prompt,
+# 64 greedy tokens), B-mix (1024-token prompt, 64 top-p tokens), one
+# sequence of configuration E (8192-token prompt, 32 greedy tokens) and
+# B-long (32768-token prompt through sink 4 / window 4096 / pool 16, 32
+# greedy tokens).
+
+import importlib.util  # noqa: E402
+import os  # noqa: E402
+
+_GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+_spec = importlib.util.spec_from_file_location("config_streams", os.path.join(_GOLDEN, "make_config_streams.py"))
+_streams = importlib.util.module_from_spec(_spec)
+_spec.loader.exec_module(_streams)
+_WEIGHTS = {}
+
+
+def _weights(model, fmts):
+    if (model, fmts) not in _WEIGHTS:
+        _WEIGHTS.clear()                      # one 1B weight set in host memory at a time
+        _WEIGHTS[(model, fmts)] = W.make_weights(getattr(W, model), seed=1234, fmts=getattr(W, fmts))
+    return _WEIGHTS[(model, fmts)]
+
+
+@pytest.mark.parametrize("name", ["B", "E0", "B-long", "B-mix"])
+def test_config_full_size_stream_matches_oracle_fixture(gpu, name):
+    path = os.path.join(_GOLDEN, f"stream_{name}.npz")
+    if not os.path.exists(path):
+        pytest.skip(f"fixture {path} not generated")
+    ref = np.load(path)
+    spec = _streams.STREAMS[name]
+    cfg = getattr(W, spec[0])
+    w = _weights(spec[0], spec[1])
+    prompt = W.prompt_ids(spec[3], cfg["n_vocab"], seed=spec[4])
+    print(f"{name}: prompt {spec[3]}, {spec[5]} tokens", flush=True)
+    m = pf.Model(gpu, cfg, w)
+    e = pf.Engine(m, **_streams.kv_of(spec))
+    toks, res = e.generate(prompt, spec[5], pf.Sampling(*spec[6]), _streams.SEED)
+    e.close()
+    m.close()
+    assert int(ref["n_prompt"]) == spec[3]
+    np.testing.assert_array_equal(toks, ref["tokens"])
+    assert (res.mtp_accepted, res.mtp_rejected) == (int(ref["accepted"]), int(ref["rejected"]))
