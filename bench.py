@@ -80,23 +80,30 @@ def measured_traffic():
     return None
 
 
-def cpu_baseline(cfg, w, kv, prompt, samp, what, n_prompt=16, n_new=8):
+def cpu_baseline(cfg, w, kv, prompt, samp, what, n_prompt=16, n_new=8, threads=0):
+    """The oracle's MTP decode on the host: all cores (threads=0), or a given
+    number of threads (1: the reference's single-threaded compute)."""
     import oracle as O
     c = dict(cfg)
     c.update(kv)
+    all_threads = int(O.lib().orc_num_threads())
+    O.lib().orc_set_num_threads(threads or all_threads)
     om = O.Model(c, w)
     t0 = time.perf_counter()
     toks, acc, rej = om.generate(prompt[:n_prompt], n_new, O.Sampling(*samp), 7)
     wall = time.perf_counter() - t0
     dec = O.lib().orc_last_decode_seconds()
     om.close()
+    used = int(O.lib().orc_num_threads())
+    O.lib().orc_set_num_threads(all_threads)
     gen = len(toks) - n_prompt
+    par = "single thread" if used == 1 else f"OpenMP row-parallel GEMVs, {used} threads"
     return {
         "value": round(gen / dec, 4),
         "unit": "tok/s",
-        "cores": int(O.lib().orc_num_threads()),
+        "cores": used,
         "kind": "port",
-        "sample": (f"oracle (C restatement, OpenMP row-parallel GEMVs) MTP decode of {gen} tokens after a "
+        "sample": (f"oracle (C restatement, {par}) MTP decode of {gen} tokens after a "
                    f"{n_prompt}-token prompt on the same weights and sampling ({what}); decode time {dec:.2f}s of "
                    f"{wall:.2f}s wall (prefill excluded); context {n_prompt}-{n_prompt + n_new} instead of the "
                    f"workload's"),
@@ -264,6 +271,8 @@ def main():
     if not args.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(cfg, w, kv, prompt, C["samp"], args.config)
+        log("cpu baseline, one thread ...")
+        out["cpu_baseline_1thread"] = cpu_baseline(cfg, w, kv, prompt, C["samp"], args.config, n_new=4, threads=1)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

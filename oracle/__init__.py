@@ -130,6 +130,7 @@ def lib():
         L.orc_rope_table.argtypes = [C.c_uint32, C.c_uint32, f32p, f32p]
         L.orc_quantize_matrix.argtypes = [f32p, C.c_uint32, C.c_uint32, C.c_int32, u8p, u16p]
         L.orc_num_threads.restype = C.c_int
+        L.orc_set_num_threads.argtypes = [C.c_int]
         L.orc_last_decode_seconds.restype = C.c_double
         _lib = L
     return _lib

@@ -146,6 +146,16 @@ int orc_num_threads(void) {
 #endif
 }
 
+/* Threads of the OpenMP row-parallel loops from now on (1: the reference's
+ * single-threaded compute).  Results do not depend on it. */
+void orc_set_num_threads(int n) {
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}
+
 /* ================================= src/matmul_neon.cpp, reference order */
 
 /* src/matmul_neon.cpp:16-29 */

@@ -138,6 +138,7 @@ int32_t  orc_generate(orc_engine* e, const int32_t* prompt, uint32_t n_prompt,
                       int32_t* tokens_out, uint32_t tokens_cap, uint32_t* n_tokens,
                       int32_t* mtp_accepted, int32_t* mtp_rejected);
 int      orc_num_threads(void);
+void     orc_set_num_threads(int n);
 double   orc_last_decode_seconds(void);
 
 #ifdef __cplusplus

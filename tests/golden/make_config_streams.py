@@ -2,13 +2,13 @@
 sizes, for the GPU parity tests of tests/test_gpu_configs.py: the same
 seeded weights (pocketforge_amd.weights, seed 1234), prompts (prompt_ids)
 and sampling as bench.py, run through the C restatement (oracle/) on the
-host.  The 1B runs take minutes (B, B-mix), about ten minutes (one
-sequence of configuration E, 8192-token prompt) and most of an hour
-(B-long, 32768-token prompt) on 8 host cores, so their outputs are kept
+host.  The 1B runs take minutes (B: 13 minutes on 6 host cores),
+up to an hour (one sequence of configuration E, 8192-token prompt; B-long's
+geometry with a 5000-token prompt), so their outputs are kept
 here as fixtures: stream_<name>.npz with the prompt length, the generated
 tokens (prompt included) and the acceptance counters.
 
-Run:  python tests/golden/make_config_streams.py [B B-mix E0 B-long]
+Run:  python tests/golden/make_config_streams.py [B B-mix E0 B-long-5k]
 """
 import os
 import sys
@@ -26,7 +26,10 @@ STREAMS = {
     "B": ("ONE_B", "ALL_Q4", (4, 8192, 64), 2048, 42, 64, (0.8, 0.95, 40, 1)),
     "B-mix": ("ONE_B", "MIXED", (4, 8192, 64), 1024, 42, 64, (0.8, 0.95, 40, 0)),
     "E0": ("ONE_B", "ALL_Q4", (4, 8192, 64), 8192, 42, 32, (0.8, 0.95, 40, 1)),
-    "B-long": ("ONE_B", "ALL_Q4", (4, 4096, 16), 32768, 42, 32, (0.8, 0.95, 40, 1)),
+    # B-long's cache geometry on the 1B model with a 5000-token prompt: the
+    # window is full and 56 pooled rows exist before decoding starts (the
+    # 32768-token prompt itself would take hours in the oracle)
+    "B-long-5k": ("ONE_B", "ALL_Q4", (4, 4096, 16), 5000, 42, 32, (0.8, 0.95, 40, 1)),
 }
 SEED = 7
 

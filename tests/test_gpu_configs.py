@@ -72,8 +72,8 @@ def test_config_blong_cache_geometry(gpu, tiny_weights):
 # tests/golden/make_config_streams.py on the host): B (2048-token prompt,
 # 64 greedy tokens), B-mix (1024-token prompt, 64 top-p tokens), one
 # sequence of configuration E (8192-token prompt, 32 greedy tokens) and
-# B-long (32768-token prompt through sink 4 / window 4096 / pool 16, 32
-# greedy tokens).
+# B-long's cache geometry (sink 4 / window 4096 / pool 16) on the 1B model
+# with a 5000-token prompt (full window, 56 pooled rows), 32 greedy tokens.
 
 import importlib.util  # noqa: E402
 import os  # noqa: E402
@@ -92,7 +92,7 @@ def _weights(model, fmts):
     return _WEIGHTS[(model, fmts)]
 
 
-@pytest.mark.parametrize("name", ["B", "E0", "B-long", "B-mix"])
+@pytest.mark.parametrize("name", ["B", "E0", "B-long-5k", "B-mix"])
 def test_config_full_size_stream_matches_oracle_fixture(gpu, name):
     path = os.path.join(_GOLDEN, f"stream_{name}.npz")
     if not os.path.exists(path):
