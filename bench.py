@@ -208,6 +208,7 @@ def main():
     # HIP start/stop events attached to every verify-pass GEMV dispatch
     dt_p, toks_p, res_p = step(True)
     n_l, gemv_us, gemv_bytes = eng.gemv_stats()
+    a_n, attn_us = eng.attn_stats()
     v_us, b_us, vn, bn = eng.pass_times()
     eng.profile(False)
     log(f"profiled step: {dt_p * 1e3:.1f} ms, verify pass {v_us:.1f} us x{vn}, base pass {b_us:.1f} us x{bn}, "
@@ -266,6 +267,8 @@ def main():
             "bytes": round(pass_bytes),
             "achieved_GBps": round(pass_bytes / v_us / 1e3, 1),
             "frac": round(pass_bytes / v_us / 1e3 / HBM_PEAK_GBPS, 4),
+            "attention_avg_us": round(attn_us, 2),
+            "attention_launches": a_n,
         },
     }
     if not args.no_cpu:
@@ -340,6 +343,7 @@ def bench_batch(args, C, cfg, w, ctx, dev, model):
     # to every GEMM dispatch of the verify passes (M = 5 x sequences)
     dt_p, toks_p, res_p = step(True)
     n_l, gemm_us, gemm_bytes = eng.gemv_stats()
+    a_n, attn_us = eng.attn_stats()
     v_us, b_us, vn, bn = eng.pass_times()
     eng.profile(False)
     M = N * (cfg["n_mtp"] + 1)
@@ -353,6 +357,11 @@ def bench_batch(args, C, cfg, w, ctx, dev, model):
     wbytes = W.packed_bytes(w) + w["emb"][1].nbytes + w["emb"][2].nbytes
     p_mid = args.prompt + (args.warmup + args.steps // 2) * (args.new + 1)
     kv_bytes = N * cfg["n_layers"] * 2 * cfg["n_heads"] * (cfg["head_dim"] + 4) * view_count(p_mid, sink, window, pool)
+    # verify-pass attention of one layer: every sequence's visible K/V rows
+    # (int8 codes + fp32 row scales) once, at the profiled step's mid context
+    p_prof = args.prompt + (args.warmup + args.steps) * (args.new + 1) + args.new // 2
+    attn_bytes = N * 2 * cfg["n_heads"] * (cfg["head_dim"] + 4) * view_count(p_prof, sink, window, pool)
+    attn_gbps = attn_bytes / attn_us / 1e3 if attn_us else 0.0
     out = {
         "metric": f"accepted tok/s (all sequences), configuration E, MTP draft=4, {N} sequences",
         "value": round(value, 3),
@@ -378,20 +387,33 @@ def bench_batch(args, C, cfg, w, ctx, dev, model):
             "prefill_tok_s": round(N * (args.prompt - 1) / prefill_s, 1),
             "device": dev,
         },
+        # the step's dominant kernel: verify-pass attention (78% of the decode's
+        # kernel time), bound by HBM
         "roofline": {
+            "kernel": f"k_attn_chunk<8> (verify-pass attention, {M} rows over {N} sequences' int8 K/V)",
+            "bound": "hbm",
+            "achieved": round(attn_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(attn_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "avg_launch_us": round(attn_us, 2),
+            "avg_bytes_per_launch": round(attn_bytes),
+            "launches": a_n,
+            "timing": "HIP start/stop events attached to each attention dispatch of the verify passes "
+                      "(hipExtLaunchKernelGGL) on the engine stream, in one extra step of the same workload",
+        },
+        "gemm_roofline": {
             "kernel": f"k_gemm_i8<Q4> (verify-pass int8 x Q4 GEMM, M={M})",
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": GEMM_PEAK_TOPS,
             "unit": "TOP/s",
             "frac": round(achieved / GEMM_PEAK_TOPS, 4),
-            "traffic": None,
             "avg_launch_us": round(gemm_us, 3),
             "avg_ops_per_launch": round(gemm_ops),
             "avg_bytes_per_launch": round(gemm_bytes),
             "launches": n_l,
-            "timing": "HIP start/stop events attached to each GEMM dispatch (hipExtLaunchKernelGGL) on the engine "
-                      "stream, in one extra step of the same workload",
         },
         "verify_pass": {
             "avg_us": round(v_us, 2),

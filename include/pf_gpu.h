@@ -247,6 +247,10 @@ pf_status pf_engine_profile(pf_engine* e, int32_t enable);
  * (packed weights + int8 activations + fp32 outputs) of the GEMV launches
  * recorded by the last pf_generate in profiling mode. */
 pf_status pf_engine_gemv_stats(pf_engine* e, uint32_t* launches, double* avg_us, double* avg_bytes);
+/* Launch count and average duration (us) of the attention kernel of the
+ * verify passes recorded by the last pf_generate / pf_batch_generate in
+ * profiling mode (one launch per layer and pass). */
+pf_status pf_engine_attn_stats(const pf_engine* e, uint32_t* launches, double* avg_us);
 
 /* ------------------------------------------------- multi-sequence engine
  * No counterpart in the reference, which decodes one sequence per Engine

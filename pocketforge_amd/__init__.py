@@ -114,6 +114,7 @@ SYMBOLS = {
     "pf_engine_profile": (C.c_int32, [vp, C.c_int32]),
     "pf_engine_round_time": (C.c_int32, [vp, C.POINTER(C.c_double), u32p]),
     "pf_engine_gemv_stats": (C.c_int32, [vp, u32p, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    "pf_engine_attn_stats": (C.c_int32, [vp, u32p, C.POINTER(C.c_double)]),
     "pf_batch_create": (C.c_int32, [vp, C.POINTER(CacheDesc), C.c_uint32, C.POINTER(vp)]),
     "pf_batch_sequences": (C.c_uint32, [vp]),
     "pf_batch_position": (C.c_uint32, [vp, C.c_uint32]),
@@ -550,6 +551,11 @@ class Engine:
         self.ctx.check(lib().pf_engine_gemv_stats(self.h, C.byref(n), C.byref(us), C.byref(by)),
                        "pf_engine_gemv_stats")
         return n.value, us.value, by.value
+
+    def attn_stats(self):
+        n, us = C.c_uint32(0), C.c_double(0)
+        self.ctx.check(lib().pf_engine_attn_stats(self.h, C.byref(n), C.byref(us)), "pf_engine_attn_stats")
+        return n.value, us.value
 
     def close(self):
         if self.h:

@@ -296,14 +296,15 @@ __global__ void k_wsum_combine_one(const float* __restrict__ Wp, uint32_t nch, u
 // S[(m*H + h)*s_stride + 2c] = m_c, [.. + 2c + 1] = T_c and
 // Up[((m*H + h)*cstride + c)*hd + i] = U_c[i].
 
-// Shared memory of one attention block (bytes): V rows of the chunk first.
-// V rows with 8 bytes of padding each: the block's LDS stays under 40 KB,
-// so four blocks fit in a CU's 160 KB
-constexpr uint32_t ATT_VROW = 136;
-constexpr uint32_t ATT_VT = 256 * ATT_VROW;
-constexpr uint32_t ATT_SMEM = ATT_VT + (128 + 128 + 256 + 256 + 512 + 4) * 4;
+// Shared memory of one attention block (bytes): V rows of the chunk first,
+// VROW bytes each.  VROW = 136 (8 bytes of padding) keeps the block under
+// 40 KB, so four blocks fit in a CU's 160 KB: passes of many rows.  VROW =
+// 144 (16-byte rows, one 16-byte store per part) for passes of a few rows,
+// whose grids do not fill the CUs anyway.
+constexpr uint32_t att_vt(uint32_t vrow) { return 256 * vrow; }
+constexpr uint32_t att_smem(uint32_t vrow) { return att_vt(vrow) + (128 + 128 + 256 + 256 + 512 + 4) * 4; }
 
-template <int PARTS>
+template <int PARTS, uint32_t VROW = 144>
 __device__ __forceinline__ void attn_one_row(const PassDesc* __restrict__ pd, const KvGeom& g, const KvPlanes& kv,
                                              uint32_t layer, uint32_t m, uint32_t h, uint32_t c,
                                              const float* __restrict__ q, const float* __restrict__ kself,
@@ -311,8 +312,8 @@ __device__ __forceinline__ void attn_one_row(const PassDesc* __restrict__ pd, co
                                              uint32_t s_stride, float* __restrict__ Up, uint32_t cstride,
                                              uint8_t* smem) {
     constexpr uint32_t hd = 16 * PARTS;
-    int8_t (*vt)[ATT_VROW] = reinterpret_cast<int8_t (*)[ATT_VROW]>(smem);
-    float* qs = reinterpret_cast<float*>(smem + ATT_VT);
+    int8_t (*vt)[VROW] = reinterpret_cast<int8_t (*)[VROW]>(smem);
+    float* qs = reinterpret_cast<float*>(smem + att_vt(VROW));
     float* kss = qs + 128;
     float* vsc = kss + 128;
     float* pe = vsc + 256;
@@ -348,6 +349,10 @@ __device__ __forceinline__ void attn_one_row(const PassDesc* __restrict__ pd, co
         vs = kv.vs[row];
 #pragma unroll
         for (int p = 0; p < PARTS; p++) {
+            if constexpr (VROW % 16 == 0) {
+                *reinterpret_cast<int4*>(&vt[t][p * 16]) = vw[p];
+                continue;
+            }
             *reinterpret_cast<int2*>(&vt[t][p * 16]) = make_int2(vw[p].x, vw[p].y);
             *reinterpret_cast<int2*>(&vt[t][p * 16 + 8]) = make_int2(vw[p].z, vw[p].w);
         }
@@ -429,19 +434,19 @@ __device__ __forceinline__ void attn_one_row(const PassDesc* __restrict__ pd, co
 // grp = c * H + h.  Blocks are dealt to the 8 XCDs round-robin, so block b
 // runs on XCD b mod 8: group grp's M rows get blocks with b mod 8 = grp mod
 // 8, and after the first row a chunk's K/V rows come from that XCD's L2.
-// 256 threads; head_dim = 16 * PARTS.
-template <int PARTS>
+// 256 threads; head_dim = 16 * PARTS; V rows of VROW bytes in LDS.
+template <int PARTS, uint32_t VROW>
 __global__ __launch_bounds__(256) void k_attn_chunk(const PassDesc* __restrict__ pd, KvGeom g, KvPlanes kv,
                                                     uint32_t layer, uint32_t M, uint32_t n_groups,
                                                     const float* __restrict__ q, const float* __restrict__ kself,
                                                     const float* __restrict__ vself, float* __restrict__ S,
                                                     uint32_t s_stride, float* __restrict__ Up, uint32_t cstride) {
-    __shared__ __align__(16) uint8_t smem[ATT_SMEM];
+    __shared__ __align__(16) uint8_t smem[att_smem(VROW)];
     const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
     const uint32_t grp = (slot / M) * 8u + xcd, m = slot % M;
     if (grp >= n_groups || m >= pd->m) return;
-    attn_one_row<PARTS>(pd, g, kv, layer, m, grp % g.n_heads, grp / g.n_heads, q, kself, vself, S, s_stride, Up,
-                        cstride, smem);
+    attn_one_row<PARTS, VROW>(pd, g, kv, layer, m, grp % g.n_heads, grp / g.n_heads, q, kself, vself, S, s_stride,
+                              Up, cstride, smem);
 }
 
 // Engine attention, second stage: the chunks of (row m, head h) merged left

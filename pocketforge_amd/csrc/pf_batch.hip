@@ -237,6 +237,9 @@ extern "C" pf_status pf_batch_generate(pf_engine* e, const int32_t* prompts, con
     e->verify_n = e->base_n = 0;
     e->kev_us = e->kev_bytes_sum = 0;
     e->kev_n = 0;
+    e->aev_us = 0;
+    e->aev_n = 0;
+    e->aev_used = 0;
     e->round_us = 0;
     e->round_n = 0;
     std::vector<uint32_t> n_gen(N, 0), sel(N);

@@ -66,17 +66,18 @@ __global__ __launch_bounds__(256) void k_gemv_i8(const uint8_t* __restrict__ W, 
     const uint32_t chunks = K >> 8, wb = 4u * bpw, wb0 = s * wb, b0 = wb0 + wid * bpw;
     const uint8_t* tiles = W + (size_t)g * chunks * TB;
     uint32_t u[4][8];
-    double d[4];
+    uint16_t dh[4];        // scale bits: converted after the staging below, so that no
+                           // conversion waits on a load before every load is issued
 #pragma unroll
     for (uint32_t k = 0; k < 4; k++) {
-        d[k] = 0.0;
+        dh[k] = 0;
 #pragma unroll
         for (int q = 0; q < 8; q++) u[k][q] = 0u;
         if (k < bpw) {
             const uint32_t b = b0 + k;
             const uint8_t* tile = tiles + (size_t)(b >> 3) * TB;
             unpack_codes<FMT>(tile, b & 7u, lane, u[k]);
-            d[k] = (double)h2f(*reinterpret_cast<const uint16_t*>(tile + CODES + lane * 16u + (b & 7u) * 2u));
+            dh[k] = *reinterpret_cast<const uint16_t*>(tile + CODES + lane * 16u + (b & 7u) * 2u);
         }
     }
     for (uint32_t i = threadIdx.x; i < (uint32_t)M * wb * 8u; i += 256u) {
@@ -88,6 +89,9 @@ __global__ __launch_bounds__(256) void k_gemv_i8(const uint8_t* __restrict__ W, 
         sb[m][k] = bsum[(size_t)m * bsum_stride + wb0 + k];
     }
     __syncthreads();
+    double d[4];
+#pragma unroll
+    for (uint32_t k = 0; k < 4; k++) d[k] = (double)h2f(dh[k]);
     double S[M];
 #pragma unroll
     for (int m = 0; m < M; m++) S[m] = 0.0;

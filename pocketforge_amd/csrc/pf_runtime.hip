@@ -437,16 +437,32 @@ static int per_for(uint32_t K) {
         case 8: { constexpr int PER = 8; CALL; } break;   \
     }
 
-// Engine attention launch (head_dim 64 or 128, checked at model creation).
+// Engine attention of a pass (head_dim 64 or 128, checked at model
+// creation): one block per (row, head, 256-entry chunk).
+// Passes of 16 or more rows stage V rows in 136-byte LDS rows (four blocks
+// per CU); smaller passes use 144-byte rows (one 16-byte store per part).
 static void launch_attn(hipStream_t st, uint32_t hd, uint32_t M, uint32_t blocks, const PassDesc* pd,
                         const KvGeom& g, const KvPlanes& kv, uint32_t l, uint32_t groups, const float* q,
-                        const float* k, const float* v, float* S, uint32_t s_stride, float* Wp, uint32_t cstride) {
-    if (hd == 64)
-        hipLaunchKernelGGL(k_attn_chunk<4>, dim3(blocks), dim3(256), 0, st, pd, g, kv, l, M, groups, q, k, v, S,
-                           s_stride, Wp, cstride);
-    else
-        hipLaunchKernelGGL(k_attn_chunk<8>, dim3(blocks), dim3(256), 0, st, pd, g, kv, l, M, groups, q, k, v, S,
-                           s_stride, Wp, cstride);
+                        const float* k, const float* v, float* S, uint32_t s_stride, float* Wp, uint32_t cstride,
+                        hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr) {
+#define PF_ATTN_LAUNCH(P, VR)                                                                                 \
+    do {                                                                                                      \
+        if (ev0)                                                                                              \
+            hipExtLaunchKernelGGL((k_attn_chunk<P, VR>), dim3(blocks), dim3(256), 0, st, ev0, ev1, 0, pd, g, kv, \
+                                  l, M, groups, q, k, v, S, s_stride, Wp, cstride);                           \
+        else                                                                                                  \
+            hipLaunchKernelGGL((k_attn_chunk<P, VR>), dim3(blocks), dim3(256), 0, st, pd, g, kv, l, M, groups, q, \
+                               k, v, S, s_stride, Wp, cstride);                                               \
+    } while (0)
+    const bool many = M >= 16;
+    if (hd == 64) {
+        if (many) PF_ATTN_LAUNCH(4, 136u);
+        else PF_ATTN_LAUNCH(4, 144u);
+    } else {
+        if (many) PF_ATTN_LAUNCH(8, 136u);
+        else PF_ATTN_LAUNCH(8, 144u);
+    }
+#undef PF_ATTN_LAUNCH
 }
 
 extern "C" pf_status pf_quantize_activation_rows(pf_ctx* c, const float* src, int8_t* dst, float* scales,
@@ -1043,6 +1059,10 @@ struct pf_engine {
     std::vector<TimedPass> kev;
     std::vector<double> kev_bytes;
     size_t kev_used = 0;
+    std::vector<TimedPass> aev;        // attention launches of verify passes (profiling mode)
+    size_t aev_used = 0;
+    double aev_us = 0;
+    uint32_t aev_n = 0;
     double kev_us = 0, kev_bytes_sum = 0;
     uint32_t kev_n = 0;
     double verify_us = 0, base_us = 0;
@@ -1387,6 +1407,7 @@ extern "C" void pf_engine_destroy(pf_engine* e) {
     (void)hipStreamSynchronize(e->c->stream);
     for (auto& t : e->timed) { (void)hipEventDestroy(t.a); (void)hipEventDestroy(t.b); }
     for (auto& t : e->kev) { (void)hipEventDestroy(t.a); (void)hipEventDestroy(t.b); }
+    for (auto& t : e->aev) { (void)hipEventDestroy(t.a); (void)hipEventDestroy(t.b); }
     for (auto& row : e->round_exec)
         for (auto& g : row)
             if (g) (void)hipGraphExecDestroy(g);
@@ -1440,6 +1461,13 @@ static pf_status timed_begin(pf_engine* e, bool verify, TimedPass** tp) {
 // Accumulates the pass event pairs [t_lo, t_hi) and GEMV event pairs
 // [k_lo, k_hi) (a replayed graph's events hold that replay's times).
 static pf_status harvest_events(pf_engine* e, size_t t_lo, size_t t_hi, size_t k_lo, size_t k_hi) {
+    for (size_t i = 0; i < e->aev_used; i++) {
+        float ms = 0;
+        PF_HIP(e->c, hipEventElapsedTime(&ms, e->aev[i].a, e->aev[i].b));
+        e->aev_us += ms * 1000.0;
+        e->aev_n++;
+    }
+    e->aev_used = 0;
     for (size_t i = t_lo; i < t_hi; i++) {
         float ms = 0;
         PF_HIP(e->c, hipEventElapsedTime(&ms, e->timed[i].a, e->timed[i].b));
@@ -1561,8 +1589,20 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         if (pf_status s = pass_gemv(e, m->qkv[l], M)) return s;
         hipLaunchKernelGGL(k_qkv_post, dim3(M, H), dim3(64), 0, st, e->acc, as0, pd, e->rope_c, e->rope_s, g, e->kv, l,
                            e->q, e->k, e->v);
+        hipEvent_t aev0 = nullptr, aev1 = nullptr;
+        if (e->profile && e->in_verify && !e->capturing) {
+            if (e->aev_used == e->aev.size()) {
+                TimedPass n{};
+                PF_HIP(c, hipEventCreate(&n.a));
+                PF_HIP(c, hipEventCreate(&n.b));
+                e->aev.push_back(n);
+            }
+            aev0 = e->aev[e->aev_used].a;
+            aev1 = e->aev[e->aev_used].b;
+            e->aev_used++;
+        }
         launch_attn(st, hd, M, attn_blocks, pd, g, e->kv, l, attn_groups, e->q, e->k, e->v, e->S, e->s_stride,
-                    e->Wp, e->cstride);
+                    e->Wp, e->cstride, aev0, aev1);
         PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_attn_merge_quant<PER>, dim3(rb), dim3(1024), 0, st, pd, g,
                                                 (const float*)e->S, e->s_stride, (const float*)e->Wp, e->cstride,
                                                 e->act, ks, as1, e->bsum, bs, M, prefetch_of(e, m->o[l])));
@@ -1828,6 +1868,9 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
     e->verify_n = e->base_n = 0;
     e->kev_us = e->kev_bytes_sum = 0;
     e->kev_n = 0;
+    e->aev_us = 0;
+    e->aev_n = 0;
+    e->aev_used = 0;
     e->round_us = 0;
     e->round_n = 0;
     const bool graphs = e->use_graphs && !e->profile;   // profiling times dispatches one by one
@@ -1927,6 +1970,13 @@ extern "C" pf_status pf_engine_gemv_stats(pf_engine* e, uint32_t* launches, doub
     if (launches) *launches = e->kev_n;
     if (avg_us) *avg_us = n ? e->kev_us / n : 0.0;
     if (avg_bytes) *avg_bytes = n ? e->kev_bytes_sum / n : 0.0;
+    return PF_OK;
+}
+
+extern "C" pf_status pf_engine_attn_stats(const pf_engine* e, uint32_t* launches, double* avg_us) {
+    if (!e) return PF_ERR_ARG;
+    if (launches) *launches = e->aev_n;
+    if (avg_us) *avg_us = e->aev_n ? e->aev_us / e->aev_n : 0.0;
     return PF_OK;
 }
 
