@@ -128,6 +128,13 @@ def lib():
         L.orc_generate.argtypes = [C.c_void_p, i32p, C.c_uint32, C.c_uint32, C.POINTER(Sampling),
                                    C.c_uint64, i32p, C.c_uint32, u32p, i32p, i32p]
         L.orc_rope_table.argtypes = [C.c_uint32, C.c_uint32, f32p, f32p]
+        L.orc_engine_set_layer_skip.argtypes = [C.c_void_p, C.c_float, C.c_uint32]
+        L.orc_engine_skip_count.restype = C.c_uint32
+        L.orc_engine_skip_count.argtypes = [C.c_void_p]
+        L.orc_skip_delta.restype = C.c_float
+        L.orc_skip_delta.argtypes = [f32p, f32p, C.c_uint32]
+        L.orc_skip_decide.restype = C.c_int
+        L.orc_skip_decide.argtypes = [f32p, C.c_uint32, C.c_uint32, C.c_float, C.c_uint32, C.c_uint32, f32p]
         L.orc_quantize_matrix.argtypes = [f32p, C.c_uint32, C.c_uint32, C.c_int32, u8p, u16p]
         L.orc_num_threads.restype = C.c_int
         L.orc_set_num_threads.argtypes = [C.c_int]
@@ -272,6 +279,13 @@ class Model:
 
     def reset(self):
         lib().orc_engine_reset(self.h)
+
+    def set_layer_skip(self, threshold, interval=4):
+        lib().orc_engine_set_layer_skip(self.h, float(threshold), int(interval))
+
+    @property
+    def skip_count(self):
+        return lib().orc_engine_skip_count(self.h)
 
     @property
     def pos(self):

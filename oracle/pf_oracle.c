@@ -768,6 +768,12 @@ struct orc_engine {
     float *h, *normed, *q, *k, *v, *attn, *o, *g, *u, *f, *last_hidden, *scores;
     int8_t* a8;
     uint32_t scores_cap;
+    /* LayerSkipController state (src/layer_skip.cpp:8-20): threshold,
+     * anchor interval, the normed FFN input last computed per layer */
+    float skip_threshold;
+    uint32_t skip_interval;
+    float* skip_cache;             /* [n_layers][n_embd] */
+    uint32_t skips;                /* FFN blocks skipped so far */
 };
 
 orc_engine* orc_engine_create(const orc_model_desc* d) {
@@ -785,7 +791,67 @@ orc_engine* orc_engine_create(const orc_model_desc* d) {
     e->a8 = (int8_t*)calloc(F > D ? F : D, 1);
     e->scores_cap = d->max_context + 64;
     e->scores = (float*)calloc(e->scores_cap, 4);
+    e->skip_threshold = 0.0f;      /* off: delta < 0 never holds */
+    e->skip_interval = 4;          /* ModelConfig::skip_interval, include/forge/types.hpp:237 */
+    e->skip_cache = (float*)calloc((size_t)d->n_layers * D, 4);
     return e;
+}
+
+/* Engine::set_layer_skip_threshold (src/engine.cpp:266-269) and the
+ * controller's anchor interval (ModelConfig::skip_interval). */
+void orc_engine_set_layer_skip(orc_engine* e, float threshold, uint32_t interval) {
+    e->skip_threshold = threshold;
+    e->skip_interval = interval;
+}
+
+uint32_t orc_engine_skip_count(const orc_engine* e) { return e->skips; }
+
+/* LayerSkipController::hidden_delta (src/layer_skip.cpp:105-111), sqrt of
+ * the mean squared difference, with the sum in the tile order of the
+ * engine's RMSNorm (per 64-element tile a halving tree, tiles added in
+ * order) instead of one sequential sum.  n % 64 == 0. */
+float orc_skip_delta(const float* a, const float* b, uint32_t n) {
+    float sum = 0.0f;
+    for (uint32_t t = 0; t < n / 64; t++) {
+        float L[64];
+        for (uint32_t l = 0; l < 64; l++) {
+            float d = a[64 * t + l] - b[64 * t + l];
+            L[l] = d * d;
+        }
+        for (uint32_t off = 32; off >= 1; off >>= 1)
+            for (uint32_t l = 0; l < off; l++) L[l] = L[l] + L[l + off];
+        sum = sum + L[0];
+    }
+    return sqrtf(sum / (float)n);
+}
+
+/* LayerSkipController::should_skip_ffn (src/layer_skip.cpp:22-67) on the
+ * FFN's normed input.  The anchor test compares tokens_since_anchor_ with
+ * the interval; Engine never calls new_token() (src/layer_skip.cpp:83-87
+ * has no caller), so the count stays 0 and only an interval of 0 anchors.
+ * The threshold doubles for mid/2 < layer < mid + mid/2 (mid = layers / 2)
+ * and the first and last two layers never skip. */
+int orc_skip_decide(float* caches, uint32_t L, uint32_t D, float threshold, uint32_t interval, uint32_t l,
+                    const float* normed) {
+    if (l >= L) return 0;
+    float* cache = caches + (size_t)l * D;
+    if (interval == 0) {                                /* 0 >= interval: anchor */
+        memcpy(cache, normed, sizeof(float) * D);
+        return 0;
+    }
+    float delta = orc_skip_delta(normed, cache, D);
+    uint32_t mid = L / 2;
+    float thr = threshold;
+    if (l > mid / 2 && l < mid + mid / 2) thr *= 2.0f;
+    if (l < 2 || l >= L - 2) thr = -1.0f;
+    int skip = delta < thr;
+    if (!skip) memcpy(cache, normed, sizeof(float) * D);
+    return skip;
+}
+
+static int skip_ffn(orc_engine* e, uint32_t l, const float* normed) {
+    return orc_skip_decide(e->skip_cache, e->d.n_layers, e->d.n_embd, e->skip_threshold, e->skip_interval, l,
+                           normed);
 }
 
 void orc_engine_destroy(orc_engine* e) {
@@ -793,10 +859,16 @@ void orc_engine_destroy(orc_engine* e) {
     orc_kv_destroy(e->kv);
     free(e->h); free(e->normed); free(e->q); free(e->k); free(e->v); free(e->attn);
     free(e->o); free(e->g); free(e->u); free(e->f); free(e->last_hidden); free(e->a8);
-    free(e->scores); free(e);
+    free(e->scores); free(e->skip_cache); free(e);
 }
 
-void orc_engine_reset(orc_engine* e) { orc_kv_clear(e->kv); e->pos = 0; e->hidden_valid = 0; }
+void orc_engine_reset(orc_engine* e) {
+    orc_kv_clear(e->kv);
+    e->pos = 0;
+    e->hidden_valid = 0;
+    memset(e->skip_cache, 0, sizeof(float) * e->d.n_layers * e->d.n_embd);   /* LayerSkipController::reset */
+    e->skips = 0;
+}
 uint32_t orc_engine_pos(const orc_engine* e) { return e->pos; }
 orc_kv* orc_engine_kv(orc_engine* e) { return e->kv; }
 
@@ -957,6 +1029,10 @@ void orc_forward(orc_engine* e, int32_t token, float* logits, float* hidden) {
         for (uint32_t i = 0; i < D; i++) h[i] += e->o[i];
         /* FFN block (src/engine.cpp:526-541, 805-843) */
         orc_engine_rmsnorm(e->normed, h, d->ffn_norm + (size_t)l * D, D);
+        if (skip_ffn(e, l, e->normed)) {                 /* src/engine.cpp:529-534 */
+            e->skips++;
+            continue;
+        }
         orc_quantize_activation_row(e->normed, e->a8, &as, D);
         orc_gemv_i8(&W[4], e->a8, as, e->g);
         orc_gemv_i8(&W[5], e->a8, as, e->u);

@@ -129,6 +129,16 @@ uint32_t orc_engine_pos(const orc_engine* e);
 orc_kv*  orc_engine_kv(orc_engine* e);
 void     orc_rope_table(uint32_t head_dim, uint32_t pos, float* cos_out, float* sin_out);
 void     orc_forward(orc_engine* e, int32_t token, float* logits, float* hidden);
+/* LayerSkipController (src/layer_skip.cpp) in the forward pass: threshold
+ * (0 = off, the default here; the reference's ModelConfig default is 0.01)
+ * and anchor interval (default 4). */
+void     orc_engine_set_layer_skip(orc_engine* e, float threshold, uint32_t interval);
+uint32_t orc_engine_skip_count(const orc_engine* e);
+float    orc_skip_delta(const float* a, const float* b, uint32_t n);
+/* One should_skip_ffn decision on caller-held caches [L][D]: returns 1 to
+ * skip layer l's FFN; updates cache l when the FFN runs. */
+int      orc_skip_decide(float* caches, uint32_t L, uint32_t D, float threshold, uint32_t interval, uint32_t l,
+                         const float* normed);
 void     orc_mtp_forward(orc_engine* e, const float* hidden, float* logits);
 int32_t  orc_argmax(const float* x, uint32_t n);
 int32_t  orc_sample(const float* logits, uint32_t n_vocab, const orc_sampling* cfg,

@@ -10,6 +10,7 @@
 #include <functional>
 #include "forge/matmul_neon.hpp"
 #include "forge/kv_cache.hpp"
+#include "forge/layer_skip.hpp"
 // MTPHeads keeps its weights private; the harness reads and writes them to
 // run the reference forward on chosen weights.
 #define private public
@@ -80,6 +81,18 @@ int32_t ref_mtp_speculative_accept(void* m, int32_t tok, const float* logits, ui
     std::vector<std::vector<float>> l(heads);
     for (uint32_t h = 0; h < heads; h++) l[h].assign(logits + (size_t)h * vocab, logits + (size_t)(h + 1) * vocab);
     return ((forge::MTPHeads*)m)->speculative_accept(tok, l);
+}
+
+// LayerSkipController (src/layer_skip.cpp) with a ModelConfig holding the
+// given layer count, width, threshold and anchor interval.
+void* ref_skip_create(uint32_t n_layers, uint32_t n_embd, float threshold, uint32_t interval) {
+    forge::ModelConfig c;
+    c.n_layers = n_layers; c.n_embd = n_embd; c.skip_threshold = threshold; c.skip_interval = interval;
+    return new forge::LayerSkipController(c);
+}
+void ref_skip_destroy(void* s) { delete (forge::LayerSkipController*)s; }
+int ref_skip_should_skip_ffn(void* s, uint32_t layer, const float* normed, uint32_t n) {
+    return ((forge::LayerSkipController*)s)->should_skip_ffn(layer, normed, n) ? 1 : 0;
 }
 
 }  // extern "C"

@@ -168,8 +168,69 @@ def mtp(R, tag, out):
     R.ref_mtp_destroy(m)
 
 
-def main():
+# LayerSkipController decisions (src/layer_skip.cpp:22-67): configurations
+# (layers, threshold, anchor interval) over one stream of FFN inputs
+# [token][layer][width]; each token's input is base + eps * noise with eps
+# cycling through values below, near and above the thresholds.  A stream is
+# kept only if every delta sits at least 5% away from its threshold, so the
+# decisions do not depend on the order of the sum of squares.
+SKIP_CONFIGS = [(8, 0.02, 4), (8, 0.02, 0), (8, 0.0, 4), (3, 0.02, 4), (16, 0.02, 4), (16, 0.05, 1)]
+
+
+def skip(R, out):
+    R.ref_skip_create.restype = C.c_void_p
+    R.ref_skip_create.argtypes = [C.c_uint32, C.c_uint32, C.c_float, C.c_uint32]
+    R.ref_skip_destroy.argtypes = [C.c_void_p]
+    R.ref_skip_should_skip_ffn.restype = C.c_int
+    R.ref_skip_should_skip_ffn.argtypes = [C.c_void_p, C.c_uint32, f32p, C.c_uint32]
+    T, Lmax, D = 10, 16, 128
+    epss = np.array([0.0, 0.002, 0.008, 0.03, 0.2, 0.005], np.float64)
+    for seed in range(100):
+        rng = np.random.default_rng(1000 + seed)
+        base = rng.standard_normal((Lmax, D))
+        eps = epss[rng.integers(0, len(epss), (T, Lmax))]
+        x = (base[None] + eps[..., None] * rng.standard_normal((T, Lmax, D))).astype(np.float32)
+        ok = True
+        decisions = {}
+        for (L, thr, interval) in SKIP_CONFIGS:
+            h = R.ref_skip_create(L, D, thr, interval)
+            dec = np.zeros((T, L), np.int32)
+            cache = np.zeros((L, D), np.float64)
+            mid = L // 2
+            for t in range(T):
+                for l in range(L):
+                    v = np.ascontiguousarray(x[t, l])
+                    dec[t, l] = R.ref_skip_should_skip_ffn(h, l, P(v, f32p), D)
+                    a = thr * (2.0 if (l > mid // 2 and l < mid + mid // 2) else 1.0)
+                    never = l < 2 or l >= L - 2 or interval == 0
+                    delta = np.sqrt(np.mean((v.astype(np.float64) - cache[l]) ** 2))
+                    if not never and a > 0 and abs(delta - a) < 0.05 * a:
+                        ok = False
+                    if not dec[t, l]:
+                        cache[l] = v
+            R.ref_skip_destroy(h)
+            decisions[(L, thr, interval)] = dec
+        if ok:
+            break
+    else:
+        raise SystemExit("no skip stream with clear margins")
+    out["skip_x"] = x
+    for i, (cfg, dec) in enumerate(decisions.items()):
+        out[f"skip_cfg{i}"] = np.array(cfg, np.float64)
+        out[f"skip_dec{i}"] = dec
+    print("skip stream seed", 1000 + seed, {k: int(v.sum()) for k, v in decisions.items()})
+
+
+def main(groups):
     O.build(ref=True)
+    if groups == ["skip"]:
+        R = O.ref_lib()
+        if R is None:
+            raise SystemExit("reference TUs not built (needs /root/reference)")
+        d = {}
+        skip(R, d)
+        np.savez_compressed(os.path.join(HERE, "ref_skip.npz"), **d)
+        return
     outs = {"kernels": {}, "kv": {}, "mtp": {}}
     for tag, nofma in (("fma", False), ("nofma", True)):
         R = O.ref_lib(nofma=nofma)
@@ -184,4 +245,4 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    main(sys.argv[1:])

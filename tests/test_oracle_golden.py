@@ -388,3 +388,101 @@ def test_engine_attention_special_cases():
     L.orc_attn_head(k, 0, 0, P(q, O.f32p), P(kself, O.f32p), P(vself, O.f32p), P(out, O.f32p))
     np.testing.assert_allclose(out, vself, rtol=1e-6, atol=1e-7)
     L.orc_kv_destroy(k)
+
+
+# ----------------------------------------------- layer-skip controller
+
+def test_skip_decisions_match_reference_controller():
+    """orc_skip_decide replays the stream that tests/golden/make_golden.py fed
+    to the reference LayerSkipController (src/layer_skip.cpp:22-67) and must
+    take the same decisions: threshold doubling in the middle band, the first
+    and last two layers never skipping, interval 0 anchoring every call, the
+    strict `delta < threshold` and the cache kept on skipped calls."""
+    S = dict(np.load(os.path.join(G, "ref_skip.npz")))
+    x = S["skip_x"]
+    T, _, D = x.shape
+    i = 0
+    while f"skip_cfg{i}" in S:
+        L, thr, interval = S[f"skip_cfg{i}"]
+        L, interval = int(L), int(interval)
+        dec = S[f"skip_dec{i}"]
+        caches = np.zeros((L, D), np.float32)
+        got = np.zeros_like(dec)
+        for t in range(T):
+            for l in range(L):
+                v = np.ascontiguousarray(x[t, l])
+                got[t, l] = O.lib().orc_skip_decide(P(caches, O.f32p), L, D, float(thr), interval, l,
+                                                     P(v, O.f32p))
+        np.testing.assert_array_equal(got, dec, err_msg=f"config {L, thr, interval}")
+        i += 1
+    assert i >= 6
+    # the fixture exercises both outcomes in the middle band
+    assert S["skip_dec4"].sum() > 0 and (S["skip_dec4"][:, 2:14] == 0).sum() > 0
+
+
+def test_skip_delta_is_rms_of_difference():
+    rng = np.random.default_rng(5)
+    for n in (64, 128, 2048):
+        a = rng.standard_normal(n).astype(np.float32)
+        b = rng.standard_normal(n).astype(np.float32)
+        d = O.lib().orc_skip_delta(P(a, O.f32p), P(b, O.f32p), n)
+        ref = np.sqrt(np.mean((a.astype(np.float64) - b) ** 2))
+        assert abs(d - ref) <= 1e-6 * ref
+        assert O.lib().orc_skip_delta(P(a, O.f32p), P(a, O.f32p), n) == 0.0
+
+
+def test_skip_controller_live_against_reference_build():
+    """Random streams through both controllers when the reference TUs are
+    built here."""
+    R = O.ref_lib()
+    if R is None or not hasattr(R, "ref_skip_create"):
+        pytest.skip("reference TUs not built here")
+    R.ref_skip_create.restype = C.c_void_p
+    R.ref_skip_create.argtypes = [C.c_uint32, C.c_uint32, C.c_float, C.c_uint32]
+    R.ref_skip_destroy.argtypes = [C.c_void_p]
+    R.ref_skip_should_skip_ffn.restype = C.c_int
+    R.ref_skip_should_skip_ffn.argtypes = [C.c_void_p, C.c_uint32, O.f32p, C.c_uint32]
+    rng = np.random.default_rng(11)
+    D = 64
+    for L, thr, interval in ((6, 0.5, 4), (12, 0.3, 2), (5, 1.0, 0)):
+        h = R.ref_skip_create(L, D, thr, interval)
+        caches = np.zeros((L, D), np.float32)
+        base = rng.standard_normal((L, D)).astype(np.float32)
+        for t in range(8):
+            for l in range(L):
+                v = (base[l] + rng.choice([0.0, 0.05, 2.0]) * rng.standard_normal(D)).astype(np.float32)
+                a = R.ref_skip_should_skip_ffn(h, l, P(v, O.f32p), D)
+                b = O.lib().orc_skip_decide(P(caches, O.f32p), L, D, thr, interval, l, P(v, O.f32p))
+                assert a == b, (L, thr, interval, t, l)
+        R.ref_skip_destroy(h)
+
+
+def test_engine_skip_omits_ffn_and_its_residual():
+    """With a threshold no delta reaches, every layer in [2, L-2) skips its FFN
+    from the first token on (the caches start at zero), so the forward pass
+    equals one over a model whose middle down projections are zero (their
+    FFN output is exactly 0)."""
+    from pocketforge_amd import weights as W
+    cfg = dict(n_layers=6, n_embd=128, n_heads=2, head_dim=64, n_ff=256, n_vocab=96, n_mtp=0,
+               sink_size=4, window_size=16, pool_block=4, max_context=64)
+    w = W.make_weights(cfg, seed=3)
+    a = O.Model(cfg, w)
+    a.set_layer_skip(1e30, 4)
+    z = W.make_weights(cfg, seed=3)
+    for l in range(2, 4):
+        fmt, codes, scales = z["layers"][l]["wdown"]
+        z["layers"][l]["wdown"] = (fmt, codes, np.zeros_like(scales))
+    b = O.Model(cfg, z)
+    for tok in (5, 17, 3, 90):
+        la, ha = a.forward(tok)
+        lb, hb = b.forward(tok)
+        np.testing.assert_array_equal(la, lb)
+        np.testing.assert_array_equal(ha, hb)
+    assert a.skip_count == 4 * 2
+    # off (threshold 0): nothing skips, outputs differ from the zeroed model
+    a.reset()
+    a.set_layer_skip(0.0, 4)
+    b.reset()
+    la, _ = a.forward(5)
+    lb, _ = b.forward(5)
+    assert a.skip_count == 0 and not np.array_equal(la, lb)
