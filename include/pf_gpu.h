@@ -228,6 +228,17 @@ pf_status pf_engine_set_mtp_enabled(pf_engine* e, int32_t enabled);
 /* Engine::set_max_memory (engine.hpp:25): generate stops with
  * oom_protected when the context's device bytes exceed this (0 = off). */
 pf_status pf_engine_set_max_memory(pf_engine* e, size_t bytes);
+/* Engine::set_layer_skip_threshold (engine.hpp:24, src/engine.cpp:266-269)
+ * plus the controller's anchor interval (ModelConfig::skip_interval,
+ * types.hpp): LayerSkipController (src/layer_skip.cpp:22-67) on the FFN
+ * input of every layer of every pass.  On while threshold > 0 (default off;
+ * the reference's ModelConfig default is 0.01); switching it on starts from
+ * zeroed caches.  Passes run kernel-per-step while it is on. */
+pf_status pf_engine_set_layer_skip(pf_engine* e, float threshold, uint32_t interval);
+/* FFN blocks skipped since creation or pf_engine_reset (the reference's
+ * GenerationResult::layers_skipped reads a counter that is never
+ * incremented, src/engine.cpp:393). */
+pf_status pf_engine_layer_skip_count(pf_engine* e, uint64_t* count);
 
 /* Average device time (us, HIP events on the engine's stream) of the MTP
  * rounds of the last pf_generate: base pass + draft + verify + accept. */

@@ -110,6 +110,8 @@ SYMBOLS = {
                                 C.c_uint32, C.POINTER(GenResult)]),
     "pf_engine_set_max_memory": (C.c_int32, [vp, C.c_size_t]),
     "pf_engine_set_mtp_enabled": (C.c_int32, [vp, C.c_int32]),
+    "pf_engine_set_layer_skip": (C.c_int32, [vp, C.c_float, C.c_uint32]),
+    "pf_engine_layer_skip_count": (C.c_int32, [vp, C.POINTER(C.c_uint64)]),
     "pf_engine_pass_times": (C.c_int32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double), u32p, u32p]),
     "pf_engine_profile": (C.c_int32, [vp, C.c_int32]),
     "pf_engine_round_time": (C.c_int32, [vp, C.POINTER(C.c_double), u32p]),
@@ -530,6 +532,15 @@ class Engine:
 
     def set_mtp_enabled(self, enabled):
         self.ctx.check(lib().pf_engine_set_mtp_enabled(self.h, int(enabled)), "pf_engine_set_mtp_enabled")
+
+    def set_layer_skip(self, threshold, interval=4):
+        self.ctx.check(lib().pf_engine_set_layer_skip(self.h, float(threshold), int(interval)),
+                       "pf_engine_set_layer_skip")
+
+    def layer_skip_count(self):
+        n = C.c_uint64(0)
+        self.ctx.check(lib().pf_engine_layer_skip_count(self.h, C.byref(n)), "pf_engine_layer_skip_count")
+        return n.value
 
     def pass_times(self):
         v, b = C.c_double(0), C.c_double(0)

@@ -288,6 +288,7 @@ extern "C" pf_status pf_batch_generate(pf_engine* e, const int32_t* prompts, con
                                (const uint32_t*)e->sel, e->st);
             hipLaunchKernelGGL(k_bctl_accept, dim3((nm + 63) / 64), dim3(64), 0, st, e->st, (const uint32_t*)e->sel,
                                nm, (const PassDesc*)e->pdB, R, e->tokens, e->tok_cap);
+            if (e->skip_on) launch_skip_commit(e, e->pdB, nm * R, 0, 0, true);
             hipLaunchKernelGGL(k_bsample, dim3(nm), dim3(1024), 0, st, (const float*)e->logitsB, V, V, cfg,
                                (const uint64_t*)e->seeds, e->st, (const uint32_t*)e->sel, 0u, e->tokens, e->tok_cap,
                                e->pdB, R, (int32_t)ROLE_CORRECTIVE, 0);

@@ -468,7 +468,9 @@ __global__ __launch_bounds__(256) void k_quant_rows(const float* __restrict__ x,
 // threads: all loads are issued first; wave w builds the trees of tiles w,
 // w + 16, ... from the row in LDS (K <= 4096, K % 64 == 0).
 // Blocks past the `rows` row blocks prefetch pf (the weights of the GEMV that
-// consumes the output).
+// consumes the output).  With skipm, rows whose flag is set take no residual
+// (their FFN was skipped; acc is still cleared); with nout, the normed rows
+// are also written there in fp32.
 template <int PER>
 __global__ __launch_bounds__(1024) void k_resid_norm_quant(float* __restrict__ x, uint32_t K,
                                                            double* __restrict__ acc,
@@ -476,7 +478,9 @@ __global__ __launch_bounds__(1024) void k_resid_norm_quant(float* __restrict__ x
                                                            const float* __restrict__ w,
                                                            int8_t* __restrict__ q, uint32_t q_stride,
                                                            float* __restrict__ as, int32_t* __restrict__ bsum,
-                                                           uint32_t bsum_stride, uint32_t rows, Prefetch pf) {
+                                                           uint32_t bsum_stride, uint32_t rows, Prefetch pf,
+                                                           const uint32_t* __restrict__ skipm = nullptr,
+                                                           float* __restrict__ nout = nullptr) {
     __shared__ float row[4096];
     __shared__ float tree[64];
     __shared__ float red[16];
@@ -495,12 +499,15 @@ __global__ __launch_bounds__(1024) void k_resid_norm_quant(float* __restrict__ x
         av[k] = (acc && i < K) ? acc[(size_t)m * K + i] : 0.0;
     }
     const float ap = acc ? as_prev[m] : 0.0f;
+    const bool add = acc && !(skipm && skipm[m]);
 #pragma unroll
     for (int k = 0; k < PER; k++) {
         const uint32_t i = t + 1024u * k;
         if (acc && i < K) {
-            xv[k] = xv[k] + (float)(av[k] * (double)ap);
-            x[(size_t)m * K + i] = xv[k];
+            if (add) {
+                xv[k] = xv[k] + (float)(av[k] * (double)ap);
+                x[(size_t)m * K + i] = xv[k];
+            }
             acc[(size_t)m * K + i] = 0.0;
         }
         if (i < K) row[i] = xv[k];
@@ -534,6 +541,13 @@ __global__ __launch_bounds__(1024) void k_resid_norm_quant(float* __restrict__ x
     const float inv = 1.0f / rms;
 #pragma unroll
     for (int k = 0; k < PER; k++) xv[k] = (xv[k] * wv[k]) * inv;
+    if (nout) {
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const uint32_t i = t + 1024u * k;
+            if (i < K) nout[(size_t)m * K + i] = xv[k];
+        }
+    }
     __syncthreads();
     quantize_row_block<PER, 1024>(xv, K, q + (size_t)m * q_stride, as + m,
                                   bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
@@ -557,12 +571,91 @@ __global__ __launch_bounds__(1024) void k_quant_rows_wide(const float* __restric
                                   bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
 }
 
-// x[m] += (float)(acc[m] * as_prev[m]) (the last layer's down residual).
+// x[m] += (float)(acc[m] * as_prev[m]) (the last layer's down residual;
+// none for rows flagged in skipm, whose acc is still cleared).
 __global__ void k_resid_add(float* __restrict__ x, uint32_t K, double* __restrict__ acc,
-                            const float* __restrict__ as_prev) {
+                            const float* __restrict__ as_prev, const uint32_t* __restrict__ skipm = nullptr) {
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, m = blockIdx.y;
     if (i >= K) return;
-    x[(size_t)m * K + i] = x[(size_t)m * K + i] + take_acc(acc, (size_t)m * K + i, as_prev[m]);
+    const float r = take_acc(acc, (size_t)m * K + i, as_prev[m]);
+    if (!(skipm && skipm[m])) x[(size_t)m * K + i] = x[(size_t)m * K + i] + r;
+}
+
+// LayerSkipController::should_skip_ffn (src/layer_skip.cpp:22-67) at one
+// layer for the rows of sequence blockIdx.x in pass order.  normed holds the
+// FFN inputs of the pass's rows [M][K]; each row's delta (hidden_delta,
+// src/layer_skip.cpp:105-111: sqrt of the mean squared difference, the sum in
+// the tile order of the engine's RMSNorm) is taken against the input of the
+// sequence's last row in this pass that ran its FFN, else against the
+// sequence's cache (cache + blockIdx.x * cache_seq_stride).  flag[r] = 1:
+// row r skips its FFN.  thr is the layer's adjusted threshold (< 0: the layer
+// never skips).  The cache is written by k_skip_commit once it is known which
+// rows count.  K % 64 == 0, K <= 4096; 1024 threads.
+__global__ __launch_bounds__(1024) void k_layer_skip(const PassDesc* __restrict__ pd, uint32_t M,
+                                                     const float* __restrict__ normed,
+                                                     const float* __restrict__ cache, size_t cache_seq_stride,
+                                                     uint32_t K, float thr, uint32_t* __restrict__ flag) {
+    __shared__ float tree[64];
+    __shared__ uint32_t skipped;
+    const uint32_t s = blockIdx.x, t = threadIdx.x, wid = t >> 6, lane = t & 63u;
+    const float* ref = cache + (size_t)s * cache_seq_stride;
+    for (uint32_t r = 0; r < M; r++) {
+        if (row_seq(pd, r) != s) continue;
+        const float* a = normed + (size_t)r * K;
+        if (!(thr >= 0.0f)) {
+            if (t == 0) flag[r] = 0;
+            ref = a;
+            continue;
+        }
+        for (uint32_t tl = wid; tl < K / 64u; tl += 16u) {
+            const float d = a[64u * tl + lane] - ref[64u * tl + lane];
+            const float sq = wave_tree_sum(d * d);
+            if (lane == 0) tree[tl] = sq;
+        }
+        __syncthreads();
+        if (t == 0) {
+            float sum = 0.0f;
+            for (uint32_t tl = 0; tl < K / 64u; tl++) sum = sum + tree[tl];
+            const uint32_t sk = __builtin_sqrtf(sum / (float)K) < thr ? 1u : 0u;
+            flag[r] = sk;
+            skipped = sk;
+        }
+        __syncthreads();
+        if (!skipped) ref = a;
+    }
+}
+
+// The cache update of should_skip_ffn (src/layer_skip.cpp:57-62) for the rows
+// of a pass that count: per (layer blockIdx.x, sequence blockIdx.y), the
+// sequence's rows j0 <= j < j1 (j numbering the sequence's rows in pass
+// order), where for a verify pass (st non-null) j1 = min(accepted + 1, n_mtp)
+// with the round's accepted drafts from st[sequence] -- the rows that
+// src/engine.cpp:336-365 forwards.  The cache takes the FFN input of the last
+// such row that ran its FFN; skips counts the rows that skipped.
+// stage [L][rows][K], flags [L][rows], cache [nseq][L][K]; 256 threads.
+__global__ __launch_bounds__(256) void k_skip_commit(const PassDesc* __restrict__ pd, uint32_t M,
+                                                     const float* __restrict__ stage,
+                                                     const uint32_t* __restrict__ flags, uint32_t rows,
+                                                     float* __restrict__ cache, uint32_t L, uint32_t K, uint32_t j0,
+                                                     uint32_t j1, const DecodeState* __restrict__ st,
+                                                     uint32_t n_mtp, uint32_t* __restrict__ skips) {
+    const uint32_t l = blockIdx.x, s = blockIdx.y;
+    const uint32_t hi = st ? min(st[s].round_acc + 1u, n_mtp) : j1;
+    int32_t src = -1;
+    uint32_t j = 0, nskip = 0;
+    for (uint32_t r = 0; r < M; r++) {
+        if (row_seq(pd, r) != s) continue;
+        if (j >= j0 && j < hi) {
+            if (flags[(size_t)l * rows + r]) nskip++;
+            else src = (int32_t)r;
+        }
+        j++;
+    }
+    if (threadIdx.x == 0 && nskip) atomicAdd(skips, nskip);
+    if (src < 0) return;
+    const float* a = stage + ((size_t)l * rows + (uint32_t)src) * K;
+    float* c = cache + ((size_t)s * L + l) * K;
+    for (uint32_t i = threadIdx.x; i < K; i += 256) c[i] = a[i];
 }
 
 // SwiGLU of src/engine.cpp:832-838 on the fused gate|up GEMV accumulators

@@ -1037,6 +1037,16 @@ struct pf_engine {
     uint32_t pf_blocks = 128;     // prefetch blocks of the row kernels (PF_PREFETCH_BLOCKS)
     uint32_t* sink = nullptr;     // 4 bytes the prefetch loops never write in practice
     bool mtp_enabled = true;      // ModelConfig::mtp_enabled, include/forge/types.hpp
+    // layer skip (LayerSkipController, src/layer_skip.cpp): on while the
+    // threshold is > 0; caches [nseq][L][D], FFN inputs of the last pass
+    // [L][rows][D], skip flags [L][rows], skipped-row counter
+    bool skip_on = false;
+    float skip_thr = 0.0f;
+    uint32_t skip_interval = 4;
+    float* skip_cache = nullptr;
+    float* skip_stage = nullptr;
+    uint32_t* skip_flags = nullptr;
+    uint32_t* skip_ctr = nullptr;
     // timing
     std::vector<TimedPass> timed;
     size_t timed_used = 0;
@@ -1425,6 +1435,57 @@ extern "C" pf_status pf_engine_reset(pf_engine* e) {
     e->pos = 0;
     std::fill(e->spos.begin(), e->spos.end(), 0u);
     e->hidden_valid = false;
+    if (e->skip_cache) {
+        // LayerSkipController::reset (src/layer_skip.cpp:89-99)
+        const pf_model_desc& d = e->m->d;
+        PF_HIP(e->c, hipMemset(e->skip_cache, 0, (size_t)e->nseq * d.n_layers * d.n_embd * 4));
+        PF_HIP(e->c, hipMemset(e->skip_ctr, 0, 4));
+    }
+    return PF_OK;
+}
+
+// Engine::set_layer_skip_threshold (src/engine.cpp:266-269) with the
+// controller's anchor interval (ModelConfig::skip_interval).  The controller
+// runs while threshold > 0; switching it on starts from zeroed caches (a new
+// controller's state).  Kernel-per-step passes only: the persistent pass is
+// not used while it runs.
+extern "C" pf_status pf_engine_set_layer_skip(pf_engine* e, float threshold, uint32_t interval) {
+    if (!e) return PF_ERR_ARG;
+    pf_ctx* c = e->c;
+    if (!(threshold == threshold)) return fail(c, PF_ERR_ARG, "layer-skip threshold is NaN");
+    const pf_model_desc& d = e->m->d;
+    const bool on = threshold > 0.0f && d.n_layers > 0;
+    if (on && (d.n_embd % 64 || d.n_embd > 4096))
+        return fail(c, PF_ERR_ARG, "layer skip needs n_embd % 64 == 0 and n_embd <= 4096");
+    if (on && !e->skip_cache) {
+        const size_t LD = (size_t)d.n_layers * d.n_embd;
+        if (pf_status s = ealloc(e, &e->skip_cache, e->nseq * LD)) return s;
+        if (pf_status s = ealloc(e, &e->skip_stage, (size_t)e->rows * LD)) return s;
+        if (pf_status s = ealloc(e, &e->skip_flags, (size_t)e->rows * d.n_layers)) return s;
+        if (pf_status s = ealloc(e, &e->skip_ctr, 1)) return s;
+        PF_HIP(c, hipMemset(e->skip_flags, 0, (size_t)e->rows * d.n_layers * 4));
+        PF_HIP(c, hipMemset(e->skip_ctr, 0, 4));
+    }
+    if (on && !e->skip_on) {
+        PF_HIP(c, hipStreamSynchronize(c->stream));
+        PF_HIP(c, hipMemset(e->skip_cache, 0, (size_t)e->nseq * d.n_layers * d.n_embd * 4));
+    }
+    e->skip_on = on;
+    e->skip_thr = threshold;
+    e->skip_interval = interval;
+    e->graphs_valid = false;   // thresholds and launches are baked into captured rounds
+    return PF_OK;
+}
+
+// FFN blocks skipped (rows that count) since the engine was created or reset.
+extern "C" pf_status pf_engine_layer_skip_count(pf_engine* e, uint64_t* count) {
+    if (!e || !count) return PF_ERR_ARG;
+    uint32_t v = 0;
+    if (e->skip_ctr) {
+        PF_HIP(e->c, hipStreamSynchronize(e->c->stream));
+        PF_HIP(e->c, hipMemcpy(&v, e->skip_ctr, 4, hipMemcpyDeviceToHost));
+    }
+    *count = v;
     return PF_OK;
 }
 
@@ -1520,6 +1581,31 @@ static Prefetch prefetch_of(const pf_engine* e, const pf_matrix* W) {
 // outputs are device [M][D] / [M][V]; either may be null.  A batched pass
 // (the descriptor gives every row its sequence and position) passes
 // batch = true and the highest position of its rows as pos_last.
+// LayerSkipController's threshold for layer l (src/layer_skip.cpp:43-55):
+// doubled for mid/2 < l < mid + mid/2 (mid = layers / 2), never skipping
+// (-1) for the first and last two layers.  An anchor interval of 0 anchors
+// every token (tokens_since_anchor_ stays 0, src/layer_skip.cpp:29-35: no
+// skip, cache updated), which the threshold -1 reproduces.
+static float skip_threshold(const pf_engine* e, uint32_t l) {
+    const uint32_t L = e->m->d.n_layers, mid = L / 2;
+    float thr = e->skip_thr;
+    if (l > mid / 2 && l < mid + mid / 2) thr *= 2.0f;
+    if (l < 2 || l >= L - 2 || e->skip_interval == 0) thr = -1.0f;
+    return thr;
+}
+
+// Cache update for the rows j0 <= j < j1 of each sequence of a pass, or,
+// with verify, for the rows the round's acceptance keeps.
+static void launch_skip_commit(pf_engine* e, const PassDesc* pd, uint32_t M, uint32_t j0, uint32_t j1,
+                               bool verify) {
+    const pf_model_desc& d = e->m->d;
+    if (!d.n_layers) return;
+    hipLaunchKernelGGL(k_skip_commit, dim3(d.n_layers, e->nseq), dim3(256), 0, e->c->stream, pd, M,
+                       (const float*)e->skip_stage, (const uint32_t*)e->skip_flags, e->rows, e->skip_cache,
+                       d.n_layers, d.n_embd, j0, j1, verify ? (const DecodeState*)e->st : nullptr, d.n_mtp,
+                       e->skip_ctr);
+}
+
 static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0, float* logits, float* hidden,
                           bool batch = false, uint32_t pos_last = 0) {
     pf_ctx* c = e->c;
@@ -1551,7 +1637,7 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
                        pd);
     hipLaunchKernelGGL(k_embed, dim3((D + 255) / 256, M), dim3(256), 0, st, m->emb->data, m->emb->scales, d.n_vocab, D,
                        pd, e->x);
-    if (e->dec && !batch && M <= MAX_PASS_ROWS && d.n_layers) {
+    if (e->dec && !batch && !e->skip_on && M <= MAX_PASS_ROWS && d.n_layers) {
         // every layer in one persistent kernel; verify passes carry timing
         // events in profiling mode
         hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -1583,9 +1669,10 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         // row kernels carry e->pf_blocks extra blocks that stream the next
         // GEMV's weights into the MALL while the rows are processed
         const uint32_t rb = M + e->pf_blocks;
+        const uint32_t* skip_prev = (e->skip_on && l > 0) ? e->skip_flags + (size_t)(l - 1) * e->rows : nullptr;
         PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(rb), dim3(1024), 0, st, e->x, D,
                                                 l == 0 ? (double*)nullptr : e->acc, as3, an, e->act, ks, as0, e->bsum,
-                                                bs, M, prefetch_of(e, m->qkv[l])));
+                                                bs, M, prefetch_of(e, m->qkv[l]), skip_prev, (float*)nullptr));
         if (pf_status s = pass_gemv(e, m->qkv[l], M)) return s;
         hipLaunchKernelGGL(k_qkv_post, dim3(M, H), dim3(64), 0, st, e->acc, as0, pd, e->rope_c, e->rope_s, g, e->kv, l,
                            e->q, e->k, e->v);
@@ -1607,9 +1694,14 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
                                                 (const float*)e->S, e->s_stride, (const float*)e->Wp, e->cstride,
                                                 e->act, ks, as1, e->bsum, bs, M, prefetch_of(e, m->o[l])));
         if (pf_status s = pass_gemv(e, m->o[l], M)) return s;
+        float* nout = e->skip_on ? e->skip_stage + (size_t)l * e->rows * D : nullptr;
         PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(rb), dim3(1024), 0, st, e->x, D,
                                                 e->acc, as1, fn, e->act, ks, as2, e->bsum, bs, M,
-                                                prefetch_of(e, m->gu[l])));
+                                                prefetch_of(e, m->gu[l]), (const uint32_t*)nullptr, nout));
+        if (e->skip_on)
+            hipLaunchKernelGGL(k_layer_skip, dim3(e->nseq), dim3(1024), 0, st, (const PassDesc*)pd, M,
+                               (const float*)nout, (const float*)e->skip_cache + (size_t)l * D,
+                               (size_t)d.n_layers * D, D, skip_threshold(e, l), e->skip_flags + (size_t)l * e->rows);
         if (pf_status s = pass_gemv(e, m->gu[l], M)) return s;
         PF_PER1024_SWITCH(F, hipLaunchKernelGGL(k_swiglu_quant<PER>, dim3(rb), dim3(1024), 0, st, e->acc,
                                                 (const float*)as2, F, e->act, ks, as3, e->bsum, bs, M,
@@ -1618,7 +1710,12 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
     }
     if (d.n_layers)
         hipLaunchKernelGGL(k_resid_add, dim3((D + 255) / 256, M), dim3(256), 0, st, e->x, D, e->acc,
-                           (const float*)as3);
+                           (const float*)as3,
+                           e->skip_on ? (const uint32_t*)e->skip_flags + (size_t)(d.n_layers - 1) * e->rows
+                                      : (const uint32_t*)nullptr);
+    // every row of a pass counts for the skip caches except in verify passes,
+    // whose caller commits the rows the acceptance keeps
+    if (e->skip_on && !e->in_verify) launch_skip_commit(e, pd, M, 0, 0xFFFFFFFFu, false);
     if (hidden)
         hipLaunchKernelGGL(k_copy_f32, dim3((M * D + 255) / 256), dim3(256), 0, st, (const float*)e->x, hidden, M * D);
     if (logits) launch_gemv_f32(st, m->emb, M, e->x, D, logits, d.n_vocab, nullptr);
@@ -1731,6 +1828,8 @@ static pf_status round_body(pf_engine* e, bool reuse, bool mtp, const SamplingCf
     const float* base_hidden;
     if (reuse) {
         hipLaunchKernelGGL(k_ctl_reuse_row, dim3(1), dim3(1), 0, st, e->st);
+        // the reused row (F(cur), the last verify row) is this round's base pass
+        if (e->skip_on) launch_skip_commit(e, e->pdB, NM + 1, NM, NM + 1, false);
         base_logits = e->logitsB + (size_t)NM * V;
         base_hidden = e->hiddenB + (size_t)NM * D;
     } else {
@@ -1754,6 +1853,7 @@ static pf_status round_body(pf_engine* e, bool reuse, bool mtp, const SamplingCf
         hipLaunchKernelGGL(k_argmax_rows, dim3(NM + 1), dim3(1024), 0, st, e->logitsB, V, V, e->pdB,
                            e->st->row_argmax);
         hipLaunchKernelGGL(k_ctl_accept, dim3(1), dim3(1), 0, st, e->st, e->pdB, e->tokens, e->tok_cap);
+        if (e->skip_on) launch_skip_commit(e, e->pdB, NM + 1, 0, 0, true);
         hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, e->logitsB, V, -1, V, cfg, seed, e->st, e->tokens,
                            e->tok_cap, e->pdB, (int32_t)ROLE_CORRECTIVE, 0, (int32_t*)nullptr);
     } else {

@@ -308,6 +308,7 @@ struct Engine::Device {
     pf_engine* eng = nullptr;
     bool mtp_enabled = true;
     size_t max_memory = 0;           // 0: no device-memory guard
+    float skip_threshold = 0.0f;     // layer skip off until set_layer_skip_threshold
     uint64_t draw = 0;               // stochastic draws of sample()
     size_t weight_bytes = 0, mtp_bytes = 0;
     ~Device() {
@@ -335,6 +336,7 @@ bool Engine::rebuild_engine() {
     if (pf_engine_create(dev_->model, &kc, &dev_->eng) != PF_OK) return false;
     pf_engine_set_mtp_enabled(dev_->eng, dev_->mtp_enabled ? 1 : 0);
     pf_engine_set_max_memory(dev_->eng, dev_->max_memory);
+    pf_engine_set_layer_skip(dev_->eng, dev_->skip_threshold, config_.skip_interval);
     return true;
 }
 
@@ -389,8 +391,17 @@ void Engine::set_mtp_enabled(bool enabled) {
     if (dev_->eng) pf_engine_set_mtp_enabled(dev_->eng, enabled ? 1 : 0);
 }
 
-// The layer-skip controller is not part of this build; the threshold is kept.
-void Engine::set_layer_skip_threshold(float threshold) { config_.skip_threshold = threshold; }
+// src/engine.cpp:266-269.  The reference creates its controller at load time
+// with ModelConfig::skip_threshold (0.01); here the controller stays off
+// until this call, since skipping changes the outputs.
+// GenerationResult::layers_skipped stays 0 as in the reference, whose
+// controller never increments its counter; pf_engine_layer_skip_count has
+// the real count.
+void Engine::set_layer_skip_threshold(float threshold) {
+    config_.skip_threshold = threshold;
+    dev_->skip_threshold = threshold;
+    if (dev_->eng) pf_engine_set_layer_skip(dev_->eng, threshold, config_.skip_interval);
+}
 
 void Engine::set_max_memory(size_t bytes) {
     config_.max_memory = bytes;
