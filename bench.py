@@ -137,6 +137,8 @@ def main():
     ap.add_argument("--prompt", type=int, default=0, help="prompt length (default: the configuration's)")
     ap.add_argument("--new", type=int, default=0, help="generated tokens (default: the configuration's)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--layer-skip", type=float, default=0.0,
+                    help="layer-skip threshold (0: off, the default; single-sequence configurations)")
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only run 3 device-to-device copies of this many bytes (hardware-counter calibration)")
     args = ap.parse_args()
@@ -170,6 +172,8 @@ def main():
     sink, window, pool = C["kv"]
     kv = dict(sink_size=sink, window_size=window, pool_block=pool, max_context=max_ctx)
     eng = pf.Engine(model, **kv)
+    if args.layer_skip:
+        eng.set_layer_skip(args.layer_skip, 4)
     prompt = W.prompt_ids(args.prompt, cfg["n_vocab"], seed=42)
     greedy = pf.Sampling(*C["samp"])
 
@@ -245,6 +249,8 @@ def main():
             "device_us_per_round": round(r_avg, 2),
             "prefill_tok_s": round((args.prompt - 1) / min(prefill_s), 1),
             "device": dev,
+            **({"layer_skip_threshold": args.layer_skip,
+                "ffn_blocks_skipped_last_step": eng.layer_skip_count()} if args.layer_skip else {}),
         },
         "roofline": {
             "kernel": "k_gemv_i8<fmt,M=5> (verify-pass int8 x block-quantized GEMV)",

@@ -53,10 +53,12 @@ template <int FMT, int M>
 __global__ __launch_bounds__(256) void k_gemv_i8(const uint8_t* __restrict__ W, uint32_t K,
                                                  const int8_t* __restrict__ act, uint32_t act_stride,
                                                  const int32_t* __restrict__ bsum, uint32_t bsum_stride,
-                                                 uint32_t bpw, double* __restrict__ acc, uint32_t acc_stride) {
+                                                 uint32_t bpw, double* __restrict__ acc, uint32_t acc_stride,
+                                                 const uint32_t* __restrict__ gate) {
     constexpr uint32_t TB = tile_bytes(FMT);
     constexpr uint32_t CODES = TILE_ROWS * TILE_BLOCKS * code_bytes(FMT);
     constexpr int OFF = code_offset(FMT);
+    if (gate && *gate == 0u) return;   // no row of the pass needs this product
     __shared__ __align__(16) int32_t sa[M][16 * 8];  // activations of the workgroup's 4 bpw <= 16 blocks
     __shared__ int32_t sb[M][16];
     __shared__ double red[4][M][64];
@@ -201,9 +203,11 @@ __device__ __forceinline__ pf_v4i gemm_codes(const uint8_t* tile, uint32_t t, ui
 template <int FMT, int MTW>
 __global__ __launch_bounds__(256) void k_gemm_i8(const uint8_t* __restrict__ W, uint32_t K, uint32_t M,
                                                  const int8_t* __restrict__ act, uint32_t act_stride, uint32_t bps,
-                                                 double* __restrict__ acc, uint32_t acc_stride) {
+                                                 double* __restrict__ acc, uint32_t acc_stride,
+                                                 const uint32_t* __restrict__ gate) {
     constexpr uint32_t TB = tile_bytes(FMT);
     constexpr uint32_t CODES = TILE_ROWS * TILE_BLOCKS * code_bytes(FMT);
+    if (gate && *gate == 0u) return;   // no row of the pass needs this product
     const uint32_t lane = threadIdx.x & 63u, h = lane >> 5, l32 = lane & 31u;
     const uint32_t wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t n0 = blockIdx.x * 32u, r = (n0 & 63u) + l32;
@@ -470,7 +474,8 @@ __global__ __launch_bounds__(256) void k_quant_rows(const float* __restrict__ x,
 // Blocks past the `rows` row blocks prefetch pf (the weights of the GEMV that
 // consumes the output).  With skipm, rows whose flag is set take no residual
 // (their FFN was skipped; acc is still cleared); with nout, the normed rows
-// are also written there in fp32.
+// are also written there in fp32; with nclear, block 0 zeroes that word
+// (the count of rows that run the layer's FFN, built by k_layer_skip).
 template <int PER>
 __global__ __launch_bounds__(1024) void k_resid_norm_quant(float* __restrict__ x, uint32_t K,
                                                            double* __restrict__ acc,
@@ -479,12 +484,13 @@ __global__ __launch_bounds__(1024) void k_resid_norm_quant(float* __restrict__ x
                                                            int8_t* __restrict__ q, uint32_t q_stride,
                                                            float* __restrict__ as, int32_t* __restrict__ bsum,
                                                            uint32_t bsum_stride, uint32_t rows, Prefetch pf,
-                                                           const uint32_t* __restrict__ skipm = nullptr,
-                                                           float* __restrict__ nout = nullptr) {
+                                                           const uint32_t* __restrict__ skipm,
+                                                           float* __restrict__ nout, uint32_t* __restrict__ nclear) {
     __shared__ float row[4096];
     __shared__ float tree[64];
     __shared__ float red[16];
     const uint32_t m = blockIdx.x, t = threadIdx.x;
+    if (nclear && m == 0 && t == 0) *nclear = 0u;
     if (m >= rows) {
         prefetch_bytes(pf.p, pf.n, m - rows, gridDim.x - rows, pf.sink);
         return;
@@ -574,7 +580,7 @@ __global__ __launch_bounds__(1024) void k_quant_rows_wide(const float* __restric
 // x[m] += (float)(acc[m] * as_prev[m]) (the last layer's down residual;
 // none for rows flagged in skipm, whose acc is still cleared).
 __global__ void k_resid_add(float* __restrict__ x, uint32_t K, double* __restrict__ acc,
-                            const float* __restrict__ as_prev, const uint32_t* __restrict__ skipm = nullptr) {
+                            const float* __restrict__ as_prev, const uint32_t* __restrict__ skipm) {
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, m = blockIdx.y;
     if (i >= K) return;
     const float r = take_acc(acc, (size_t)m * K + i, as_prev[m]);
@@ -589,22 +595,28 @@ __global__ void k_resid_add(float* __restrict__ x, uint32_t K, double* __restric
 // sequence's last row in this pass that ran its FFN, else against the
 // sequence's cache (cache + blockIdx.x * cache_seq_stride).  flag[r] = 1:
 // row r skips its FFN.  thr is the layer's adjusted threshold (< 0: the layer
-// never skips).  The cache is written by k_skip_commit once it is known which
-// rows count.  K % 64 == 0, K <= 4096; 1024 threads.
+// never skips).  nrun (zeroed earlier in the pass) gains the number of rows
+// that run their FFN: the FFN products of a pass in which no row runs it are
+// not computed.  The cache is written by k_skip_commit once it is known which
+// rows count.  Rows go one after another, the 16 waves sharing each row's
+// tiles.  K % 64 == 0, K <= 4096; 1024 threads.
 __global__ __launch_bounds__(1024) void k_layer_skip(const PassDesc* __restrict__ pd, uint32_t M,
                                                      const float* __restrict__ normed,
                                                      const float* __restrict__ cache, size_t cache_seq_stride,
-                                                     uint32_t K, float thr, uint32_t* __restrict__ flag) {
+                                                     uint32_t K, float thr, uint32_t* __restrict__ flag,
+                                                     uint32_t* __restrict__ nrun) {
     __shared__ float tree[64];
     __shared__ uint32_t skipped;
     const uint32_t s = blockIdx.x, t = threadIdx.x, wid = t >> 6, lane = t & 63u;
     const float* ref = cache + (size_t)s * cache_seq_stride;
+    uint32_t runs = 0;
     for (uint32_t r = 0; r < M; r++) {
         if (row_seq(pd, r) != s) continue;
         const float* a = normed + (size_t)r * K;
         if (!(thr >= 0.0f)) {
             if (t == 0) flag[r] = 0;
             ref = a;
+            runs++;
             continue;
         }
         for (uint32_t tl = wid; tl < K / 64u; tl += 16u) {
@@ -621,8 +633,12 @@ __global__ __launch_bounds__(1024) void k_layer_skip(const PassDesc* __restrict_
             skipped = sk;
         }
         __syncthreads();
-        if (!skipped) ref = a;
+        if (!skipped) {
+            ref = a;
+            runs++;
+        }
     }
+    if (t == 0 && runs) atomicAdd(nrun, runs);
 }
 
 // The cache update of should_skip_ffn (src/layer_skip.cpp:57-62) for the rows

@@ -325,10 +325,10 @@ extern "C" void pf_matrix_free(pf_matrix* M) {
     case MM:                                                                                                  \
         if (ev0)                                                                                              \
             hipExtLaunchKernelGGL((k_gemv_i8<F, MM>), dim3(W->rows / 64, W->splits), dim3(256), 0, st, ev0, ev1, 0, \
-                                  W->data, W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc, acc_stride); \
+                                  W->data, W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc, acc_stride, gate); \
         else                                                                                                  \
             hipLaunchKernelGGL((k_gemv_i8<F, MM>), dim3(W->rows / 64, W->splits), dim3(256), 0, st, W->data,     \
-                               W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc, acc_stride);          \
+                               W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc, acc_stride, gate);    \
         break;
 
 #define PF_GEMV_FMT(F)                                 \
@@ -343,7 +343,7 @@ extern "C" void pf_matrix_free(pf_matrix* M) {
 // ev0/ev1 the dispatch carries its own start/stop events.
 static void launch_gemv(hipStream_t st, const pf_matrix* W, uint32_t M, const int8_t* act, uint32_t act_stride,
                         const int32_t* bsum, uint32_t bsum_stride, double* acc, uint32_t acc_stride,
-                        hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr) {
+                        hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr, const uint32_t* gate = nullptr) {
     switch (W->fmt) {
         case FMT_Q4: PF_GEMV_FMT(FMT_Q4) break;
         case FMT_Q2: PF_GEMV_FMT(FMT_Q2) break;
@@ -359,7 +359,8 @@ static void launch_gemv(hipStream_t st, const pf_matrix* W, uint32_t M, const in
 constexpr uint32_t MAX_GEMM_ROWS = 512;
 
 static void launch_gemm(hipStream_t st, const pf_matrix* W, uint32_t M, const int8_t* act, uint32_t act_stride,
-                        double* acc, uint32_t acc_stride, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr) {
+                        double* acc, uint32_t acc_stride, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr,
+                        const uint32_t* gate = nullptr) {
     const uint32_t nb = W->cols / 32, nblk = W->rows / 32;
     const uint32_t mtw = ((M + 31) / 32 + 3) / 4;
     const uint32_t target = mtw >= 2 ? 256 : 512;
@@ -371,10 +372,10 @@ static void launch_gemm(hipStream_t st, const pf_matrix* W, uint32_t M, const in
     case T:                                                                                                   \
         if (ev0)                                                                                              \
             hipExtLaunchKernelGGL((k_gemm_i8<F, T>), grid, dim3(256), 0, st, ev0, ev1, 0, W->data, W->cols, M, \
-                                  act, act_stride, bps, acc, acc_stride);                                     \
+                                  act, act_stride, bps, acc, acc_stride, gate);                                     \
         else                                                                                                  \
             hipLaunchKernelGGL((k_gemm_i8<F, T>), grid, dim3(256), 0, st, W->data, W->cols, M, act, act_stride, \
-                               bps, acc, acc_stride);                                                         \
+                               bps, acc, acc_stride, gate);                                                         \
         break;
 #define PF_GEMM_FMT(F)                                                            \
     switch (mtw) {                                                                \
@@ -1047,6 +1048,7 @@ struct pf_engine {
     float* skip_stage = nullptr;
     uint32_t* skip_flags = nullptr;
     uint32_t* skip_ctr = nullptr;
+    uint32_t* skip_nrun = nullptr;     // [L] rows of the current pass that run the layer's FFN
     // timing
     std::vector<TimedPass> timed;
     size_t timed_used = 0;
@@ -1463,6 +1465,7 @@ extern "C" pf_status pf_engine_set_layer_skip(pf_engine* e, float threshold, uin
         if (pf_status s = ealloc(e, &e->skip_stage, (size_t)e->rows * LD)) return s;
         if (pf_status s = ealloc(e, &e->skip_flags, (size_t)e->rows * d.n_layers)) return s;
         if (pf_status s = ealloc(e, &e->skip_ctr, 1)) return s;
+        if (pf_status s = ealloc(e, &e->skip_nrun, d.n_layers)) return s;
         PF_HIP(c, hipMemset(e->skip_flags, 0, (size_t)e->rows * d.n_layers * 4));
         PF_HIP(c, hipMemset(e->skip_ctr, 0, 4));
     }
@@ -1548,7 +1551,7 @@ static pf_status harvest_events(pf_engine* e, size_t t_lo, size_t t_hi, size_t k
 // Int8 GEMV launch of a pass; in profiling mode the dispatches of verify
 // passes carry HIP start/stop events (kernel execution time, as rocprofv3
 // reports it).
-static pf_status pass_gemv(pf_engine* e, const pf_matrix* W, uint32_t M) {
+static pf_status pass_gemv(pf_engine* e, const pf_matrix* W, uint32_t M, const uint32_t* gate = nullptr) {
     hipStream_t st = e->c->stream;
     const uint32_t ks = e->kmax, bs = e->kmax / 32;
     if (e->profile && e->in_verify && !e->capturing) {
@@ -1561,12 +1564,12 @@ static pf_status pass_gemv(pf_engine* e, const pf_matrix* W, uint32_t M) {
         }
         e->kev_bytes[e->kev_used] = (double)W->bytes + (double)M * W->cols + (double)M * W->rows * 4.0;
         TimedPass* t = &e->kev[e->kev_used++];
-        if (M <= MAX_PASS_ROWS) launch_gemv(st, W, M, e->act, ks, e->bsum, bs, e->acc, W->rows, t->a, t->b);
-        else launch_gemm(st, W, M, e->act, ks, e->acc, W->rows, t->a, t->b);
+        if (M <= MAX_PASS_ROWS) launch_gemv(st, W, M, e->act, ks, e->bsum, bs, e->acc, W->rows, t->a, t->b, gate);
+        else launch_gemm(st, W, M, e->act, ks, e->acc, W->rows, t->a, t->b, gate);
     } else if (M <= MAX_PASS_ROWS) {
-        launch_gemv(st, W, M, e->act, ks, e->bsum, bs, e->acc, W->rows);
+        launch_gemv(st, W, M, e->act, ks, e->bsum, bs, e->acc, W->rows, nullptr, nullptr, gate);
     } else {
-        launch_gemm(st, W, M, e->act, ks, e->acc, W->rows);
+        launch_gemm(st, W, M, e->act, ks, e->acc, W->rows, nullptr, nullptr, gate);
     }
     return PF_OK;
 }
@@ -1576,11 +1579,6 @@ static Prefetch prefetch_of(const pf_engine* e, const pf_matrix* W) {
     return Prefetch{W->data, W->bytes & ~(size_t)15, e->sink};
 }
 
-// One forward pass of M rows (the PassDesc at `pd` holds positions and
-// tokens; pos0 is the host's copy of the first position).  hidden/logits
-// outputs are device [M][D] / [M][V]; either may be null.  A batched pass
-// (the descriptor gives every row its sequence and position) passes
-// batch = true and the highest position of its rows as pos_last.
 // LayerSkipController's threshold for layer l (src/layer_skip.cpp:43-55):
 // doubled for mid/2 < l < mid + mid/2 (mid = layers / 2), never skipping
 // (-1) for the first and last two layers.  An anchor interval of 0 anchors
@@ -1606,6 +1604,11 @@ static void launch_skip_commit(pf_engine* e, const PassDesc* pd, uint32_t M, uin
                        e->skip_ctr);
 }
 
+// One forward pass of M rows (the PassDesc at `pd` holds positions and
+// tokens; pos0 is the host's copy of the first position).  hidden/logits
+// outputs are device [M][D] / [M][V]; either may be null.  A batched pass
+// (the descriptor gives every row its sequence and position) passes
+// batch = true and the highest position of its rows as pos_last.
 static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0, float* logits, float* hidden,
                           bool batch = false, uint32_t pos_last = 0) {
     pf_ctx* c = e->c;
@@ -1672,7 +1675,8 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         const uint32_t* skip_prev = (e->skip_on && l > 0) ? e->skip_flags + (size_t)(l - 1) * e->rows : nullptr;
         PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(rb), dim3(1024), 0, st, e->x, D,
                                                 l == 0 ? (double*)nullptr : e->acc, as3, an, e->act, ks, as0, e->bsum,
-                                                bs, M, prefetch_of(e, m->qkv[l]), skip_prev, (float*)nullptr));
+                                                bs, M, prefetch_of(e, m->qkv[l]), skip_prev, (float*)nullptr,
+                                                e->skip_on ? e->skip_nrun + l : (uint32_t*)nullptr));
         if (pf_status s = pass_gemv(e, m->qkv[l], M)) return s;
         hipLaunchKernelGGL(k_qkv_post, dim3(M, H), dim3(64), 0, st, e->acc, as0, pd, e->rope_c, e->rope_s, g, e->kv, l,
                            e->q, e->k, e->v);
@@ -1694,19 +1698,24 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
                                                 (const float*)e->S, e->s_stride, (const float*)e->Wp, e->cstride,
                                                 e->act, ks, as1, e->bsum, bs, M, prefetch_of(e, m->o[l])));
         if (pf_status s = pass_gemv(e, m->o[l], M)) return s;
+        // with layer skip on, the FFN products run only if some row needs
+        // them (gate word)
         float* nout = e->skip_on ? e->skip_stage + (size_t)l * e->rows * D : nullptr;
+        const uint32_t* gate = e->skip_on ? e->skip_nrun + l : nullptr;
         PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(rb), dim3(1024), 0, st, e->x, D,
                                                 e->acc, as1, fn, e->act, ks, as2, e->bsum, bs, M,
-                                                prefetch_of(e, m->gu[l]), (const uint32_t*)nullptr, nout));
+                                                prefetch_of(e, m->gu[l]), (const uint32_t*)nullptr, nout,
+                                                (uint32_t*)nullptr));
         if (e->skip_on)
             hipLaunchKernelGGL(k_layer_skip, dim3(e->nseq), dim3(1024), 0, st, (const PassDesc*)pd, M,
                                (const float*)nout, (const float*)e->skip_cache + (size_t)l * D,
-                               (size_t)d.n_layers * D, D, skip_threshold(e, l), e->skip_flags + (size_t)l * e->rows);
-        if (pf_status s = pass_gemv(e, m->gu[l], M)) return s;
+                               (size_t)d.n_layers * D, D, skip_threshold(e, l), e->skip_flags + (size_t)l * e->rows,
+                               e->skip_nrun + l);
+        if (pf_status s = pass_gemv(e, m->gu[l], M, gate)) return s;
         PF_PER1024_SWITCH(F, hipLaunchKernelGGL(k_swiglu_quant<PER>, dim3(rb), dim3(1024), 0, st, e->acc,
                                                 (const float*)as2, F, e->act, ks, as3, e->bsum, bs, M,
                                                 prefetch_of(e, m->down[l])));
-        if (pf_status s = pass_gemv(e, m->down[l], M)) return s;
+        if (pf_status s = pass_gemv(e, m->down[l], M, gate)) return s;
     }
     if (d.n_layers)
         hipLaunchKernelGGL(k_resid_add, dim3((D + 255) / 256, M), dim3(256), 0, st, e->x, D, e->acc,
