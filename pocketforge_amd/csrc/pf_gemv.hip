@@ -49,7 +49,7 @@ __device__ __forceinline__ void unpack_codes(const uint8_t* tile, uint32_t t, ui
 // output row.  Each wave issues all its weight loads first; the workgroup's
 // activation rows and block sums are staged in LDS with one vector load per
 // thread (they come from another kernel, often through another XCD's L2).
-template <int FMT, int M>
+template <int FMT, int M, bool GATED = false>
 __global__ __launch_bounds__(256) void k_gemv_i8(const uint8_t* __restrict__ W, uint32_t K,
                                                  const int8_t* __restrict__ act, uint32_t act_stride,
                                                  const int32_t* __restrict__ bsum, uint32_t bsum_stride,
@@ -58,7 +58,8 @@ __global__ __launch_bounds__(256) void k_gemv_i8(const uint8_t* __restrict__ W, 
     constexpr uint32_t TB = tile_bytes(FMT);
     constexpr uint32_t CODES = TILE_ROWS * TILE_BLOCKS * code_bytes(FMT);
     constexpr int OFF = code_offset(FMT);
-    if (gate && *gate == 0u) return;   // no row of the pass needs this product
+    if constexpr (GATED)
+        if (*gate == 0u) return;   // no row of the pass needs this product
     __shared__ __align__(16) int32_t sa[M][16 * 8];  // activations of the workgroup's 4 bpw <= 16 blocks
     __shared__ int32_t sb[M][16];
     __shared__ double red[4][M][64];
@@ -200,14 +201,15 @@ __device__ __forceinline__ pf_v4i gemm_codes(const uint8_t* tile, uint32_t t, ui
 // Grid (N / 32, splits), 256 threads: the block's 32 weight rows
 // [32 blockIdx.x, + 32) against activation tiles w, w + 4, ... (MTW per
 // wave) of 32 rows each; act holds ceil(M / 32) * 32 readable rows.
-template <int FMT, int MTW>
+template <int FMT, int MTW, bool GATED = false>
 __global__ __launch_bounds__(256) void k_gemm_i8(const uint8_t* __restrict__ W, uint32_t K, uint32_t M,
                                                  const int8_t* __restrict__ act, uint32_t act_stride, uint32_t bps,
                                                  double* __restrict__ acc, uint32_t acc_stride,
                                                  const uint32_t* __restrict__ gate) {
     constexpr uint32_t TB = tile_bytes(FMT);
     constexpr uint32_t CODES = TILE_ROWS * TILE_BLOCKS * code_bytes(FMT);
-    if (gate && *gate == 0u) return;   // no row of the pass needs this product
+    if constexpr (GATED)
+        if (*gate == 0u) return;   // no row of the pass needs this product
     const uint32_t lane = threadIdx.x & 63u, h = lane >> 5, l32 = lane & 31u;
     const uint32_t wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t n0 = blockIdx.x * 32u, r = (n0 & 63u) + l32;
@@ -472,11 +474,12 @@ __global__ __launch_bounds__(256) void k_quant_rows(const float* __restrict__ x,
 // threads: all loads are issued first; wave w builds the trees of tiles w,
 // w + 16, ... from the row in LDS (K <= 4096, K % 64 == 0).
 // Blocks past the `rows` row blocks prefetch pf (the weights of the GEMV that
-// consumes the output).  With skipm, rows whose flag is set take no residual
+// consumes the output).  SKIP instances (layer skip on): with skipm, rows
+// whose flag is set take no residual
 // (their FFN was skipped; acc is still cleared); with nout, the normed rows
 // are also written there in fp32; with nclear, block 0 zeroes that word
 // (the count of rows that run the layer's FFN, built by k_layer_skip).
-template <int PER>
+template <int PER, bool SKIP = false>
 __global__ __launch_bounds__(1024) void k_resid_norm_quant(float* __restrict__ x, uint32_t K,
                                                            double* __restrict__ acc,
                                                            const float* __restrict__ as_prev,
@@ -490,7 +493,8 @@ __global__ __launch_bounds__(1024) void k_resid_norm_quant(float* __restrict__ x
     __shared__ float tree[64];
     __shared__ float red[16];
     const uint32_t m = blockIdx.x, t = threadIdx.x;
-    if (nclear && m == 0 && t == 0) *nclear = 0u;
+    if constexpr (SKIP)
+        if (nclear && m == 0 && t == 0) *nclear = 0u;
     if (m >= rows) {
         prefetch_bytes(pf.p, pf.n, m - rows, gridDim.x - rows, pf.sink);
         return;
@@ -505,7 +509,8 @@ __global__ __launch_bounds__(1024) void k_resid_norm_quant(float* __restrict__ x
         av[k] = (acc && i < K) ? acc[(size_t)m * K + i] : 0.0;
     }
     const float ap = acc ? as_prev[m] : 0.0f;
-    const bool add = acc && !(skipm && skipm[m]);
+    bool add = acc != nullptr;
+    if constexpr (SKIP) add = add && !(skipm && skipm[m]);
 #pragma unroll
     for (int k = 0; k < PER; k++) {
         const uint32_t i = t + 1024u * k;
@@ -547,7 +552,7 @@ __global__ __launch_bounds__(1024) void k_resid_norm_quant(float* __restrict__ x
     const float inv = 1.0f / rms;
 #pragma unroll
     for (int k = 0; k < PER; k++) xv[k] = (xv[k] * wv[k]) * inv;
-    if (nout) {
+    if (SKIP && nout) {
 #pragma unroll
         for (int k = 0; k < PER; k++) {
             const uint32_t i = t + 1024u * k;

@@ -323,7 +323,14 @@ extern "C" void pf_matrix_free(pf_matrix* M) {
 
 #define PF_GEMV_CASE(F, MM)                                                                                   \
     case MM:                                                                                                  \
-        if (ev0)                                                                                              \
+        if (gate && ev0)                                                                                      \
+            hipExtLaunchKernelGGL((k_gemv_i8<F, MM, true>), dim3(W->rows / 64, W->splits), dim3(256), 0, st, ev0, \
+                                  ev1, 0, W->data, W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc,   \
+                                  acc_stride, gate);                                                          \
+        else if (gate)                                                                                        \
+            hipLaunchKernelGGL((k_gemv_i8<F, MM, true>), dim3(W->rows / 64, W->splits), dim3(256), 0, st, W->data, \
+                               W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc, acc_stride, gate);    \
+        else if (ev0)                                                                                         \
             hipExtLaunchKernelGGL((k_gemv_i8<F, MM>), dim3(W->rows / 64, W->splits), dim3(256), 0, st, ev0, ev1, 0, \
                                   W->data, W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc, acc_stride, gate); \
         else                                                                                                  \
@@ -370,7 +377,13 @@ static void launch_gemm(hipStream_t st, const pf_matrix* W, uint32_t M, const in
     const dim3 grid(nblk, splits);
 #define PF_GEMM_CASE(F, T)                                                                                    \
     case T:                                                                                                   \
-        if (ev0)                                                                                              \
+        if (gate && ev0)                                                                                      \
+            hipExtLaunchKernelGGL((k_gemm_i8<F, T, true>), grid, dim3(256), 0, st, ev0, ev1, 0, W->data, W->cols, \
+                                  M, act, act_stride, bps, acc, acc_stride, gate);                            \
+        else if (gate)                                                                                        \
+            hipLaunchKernelGGL((k_gemm_i8<F, T, true>), grid, dim3(256), 0, st, W->data, W->cols, M, act,       \
+                               act_stride, bps, acc, acc_stride, gate);                                       \
+        else if (ev0)                                                                                         \
             hipExtLaunchKernelGGL((k_gemm_i8<F, T>), grid, dim3(256), 0, st, ev0, ev1, 0, W->data, W->cols, M, \
                                   act, act_stride, bps, acc, acc_stride, gate);                                     \
         else                                                                                                  \
@@ -1673,10 +1686,17 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         // GEMV's weights into the MALL while the rows are processed
         const uint32_t rb = M + e->pf_blocks;
         const uint32_t* skip_prev = (e->skip_on && l > 0) ? e->skip_flags + (size_t)(l - 1) * e->rows : nullptr;
-        PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(rb), dim3(1024), 0, st, e->x, D,
-                                                l == 0 ? (double*)nullptr : e->acc, as3, an, e->act, ks, as0, e->bsum,
-                                                bs, M, prefetch_of(e, m->qkv[l]), skip_prev, (float*)nullptr,
-                                                e->skip_on ? e->skip_nrun + l : (uint32_t*)nullptr));
+        if (e->skip_on) {
+            PF_PER1024_SWITCH(D, hipLaunchKernelGGL((k_resid_norm_quant<PER, true>), dim3(rb), dim3(1024), 0, st,
+                                                    e->x, D, l == 0 ? (double*)nullptr : e->acc, as3, an, e->act, ks,
+                                                    as0, e->bsum, bs, M, prefetch_of(e, m->qkv[l]), skip_prev,
+                                                    (float*)nullptr, e->skip_nrun + l));
+        } else {
+            PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(rb), dim3(1024), 0, st, e->x, D,
+                                                    l == 0 ? (double*)nullptr : e->acc, as3, an, e->act, ks, as0,
+                                                    e->bsum, bs, M, prefetch_of(e, m->qkv[l]),
+                                                    (const uint32_t*)nullptr, (float*)nullptr, (uint32_t*)nullptr));
+        }
         if (pf_status s = pass_gemv(e, m->qkv[l], M)) return s;
         hipLaunchKernelGGL(k_qkv_post, dim3(M, H), dim3(64), 0, st, e->acc, as0, pd, e->rope_c, e->rope_s, g, e->kv, l,
                            e->q, e->k, e->v);
@@ -1702,10 +1722,17 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         // them (gate word)
         float* nout = e->skip_on ? e->skip_stage + (size_t)l * e->rows * D : nullptr;
         const uint32_t* gate = e->skip_on ? e->skip_nrun + l : nullptr;
-        PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(rb), dim3(1024), 0, st, e->x, D,
-                                                e->acc, as1, fn, e->act, ks, as2, e->bsum, bs, M,
-                                                prefetch_of(e, m->gu[l]), (const uint32_t*)nullptr, nout,
-                                                (uint32_t*)nullptr));
+        if (e->skip_on) {
+            PF_PER1024_SWITCH(D, hipLaunchKernelGGL((k_resid_norm_quant<PER, true>), dim3(rb), dim3(1024), 0, st,
+                                                    e->x, D, e->acc, as1, fn, e->act, ks, as2, e->bsum, bs, M,
+                                                    prefetch_of(e, m->gu[l]), (const uint32_t*)nullptr, nout,
+                                                    (uint32_t*)nullptr));
+        } else {
+            PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(rb), dim3(1024), 0, st, e->x, D,
+                                                    e->acc, as1, fn, e->act, ks, as2, e->bsum, bs, M,
+                                                    prefetch_of(e, m->gu[l]), (const uint32_t*)nullptr,
+                                                    (float*)nullptr, (uint32_t*)nullptr));
+        }
         if (e->skip_on)
             hipLaunchKernelGGL(k_layer_skip, dim3(e->nseq), dim3(1024), 0, st, (const PassDesc*)pd, M,
                                (const float*)nout, (const float*)e->skip_cache + (size_t)l * D,

@@ -111,6 +111,26 @@ def test_skip_off_leaves_persistent_pass_and_outputs(gpu, w8, monkeypatch):
     m.close()
 
 
+def test_skip_profiled_generate_matches(gpu, w8):
+    """Profiling mode times every verify-pass dispatch with its own events,
+    the gated FFN products included."""
+    prompt = W.prompt_ids(16, CFG["n_vocab"], seed=31)
+    m = pf.Model(gpu, CFG, w8)
+    e = pf.Engine(m, **KV)
+    e.set_layer_skip(0.1, 4)
+    e.profile(True)
+    toks, res = e.generate(prompt, 40, GREEDY, 7)
+    n, avg_us, _ = e.gemv_stats()
+    assert n > 0 and avg_us > 0
+    om = _oracle(w8, 0.1, 4)
+    ot, oa, orj = om.generate(prompt, 40, O.Sampling(0.8, 0.95, 40, 1), 7)
+    np.testing.assert_array_equal(toks, ot)
+    assert e.layer_skip_count() == om.skip_count
+    e.close()
+    om.close()
+    m.close()
+
+
 def test_skip_reset_and_rejections(gpu, w8):
     m = pf.Model(gpu, CFG, w8)
     e = pf.Engine(m, **KV)
