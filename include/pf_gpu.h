@@ -36,6 +36,7 @@ typedef int32_t pf_status;
 #define PF_ERR_UNSUPPORTED -4  /* shape outside what the kernels support */
 #define PF_ERR_STATE -5        /* call out of order (e.g. model incomplete) */
 #define PF_ERR_CAPACITY -6     /* position/token capacity exceeded */
+#define PF_ERR_FORMAT -7       /* malformed or unsupported file contents */
 
 typedef struct pf_ctx pf_ctx;
 typedef struct pf_model pf_model;
@@ -177,6 +178,41 @@ pf_status pf_model_set_mtp(pf_model* m, uint32_t head, int32_t which, const uint
                            const uint16_t* scales);
 /* RMSNorm weights: which 7 = attention, 8 = FFN (default 1.0). */
 pf_status pf_model_set_norm(pf_model* m, uint32_t layer, int32_t which, const float* w);
+
+/* ------------------------------------------------------ .squeeze files */
+/* WeightLoader (include/forge/quant_format.hpp:92-140, src/quant_format.cpp:
+ * 227-444) on the host: the file is mapped, matrices are zstd-decompressed
+ * (the system's libzstd.so.1) with their block scales parsed, and
+ * pf_squeeze_load_model uploads a whole model in the device layout. */
+typedef struct pf_squeeze pf_squeeze;
+typedef struct {
+    uint32_t version, n_blocks;
+    uint32_t n_layers, n_embd, n_heads, n_kv_heads, n_ff, n_vocab, max_seq_len, mtp_heads;
+} pf_squeeze_info;   /* SqueezeHeader, include/forge/quant_format.hpp:30-46 */
+
+/* WeightLoader::open: mapped, magic and index checked. */
+pf_status pf_squeeze_open(const char* path, pf_squeeze** out);
+void pf_squeeze_close(pf_squeeze* s);
+/* Message of the last failed call on s (or of the last failed open). */
+const char* pf_squeeze_last_error(const pf_squeeze* s);
+/* WeightLoader::config. */
+pf_status pf_squeeze_get_info(const pf_squeeze* s, pf_squeeze_info* out);
+/* Shape and quant type (0 Q8, 1 Q4, 2 Q2, 3 Q1.5) of matrix `matrix` of
+ * layer `layer` (WeightBlock, include/forge/types.hpp:205-214). */
+pf_status pf_squeeze_block_shape(const pf_squeeze* s, uint32_t layer, uint32_t matrix, uint32_t* rows,
+                                 uint32_t* cols, uint32_t* quant_type);
+/* WeightLoader::load_block_with_scales with the block scales parsed:
+ * codes [rows * cols] (signed), block_scales [ceil(rows * cols / 32)], the
+ * multiplier of each 32-element block of the flattened matrix (1 / the
+ * stored inverse scale; 1 for Q1.5). */
+pf_status pf_squeeze_load_block(pf_squeeze* s, uint32_t layer, uint32_t matrix, int8_t* codes,
+                                float* block_scales);
+/* Engine::load_model + load_layer_weights (src/engine.cpp:48-201, 606-640):
+ * layer matrices 0-6 (Q4 / Q2 / Q1.5, repacked with the fp16 scale
+ * 1 / inverse scale), norms 7-8, the Q4 tied embedding (layer 0, matrix 10),
+ * all resident.  MTP heads are not stored in the format: set them with
+ * pf_model_set_mtp. */
+pf_status pf_squeeze_load_model(pf_ctx* ctx, pf_squeeze* s, pf_model** out);
 
 /* -------------------------------------------------------------- engine */
 typedef struct {

@@ -50,6 +50,11 @@ class GenResult(C.Structure):
                 ("prefill_seconds", C.c_double), ("decode_seconds", C.c_double)]
 
 
+class SqueezeInfo(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("version", "n_blocks", "n_layers", "n_embd", "n_heads", "n_kv_heads",
+                                          "n_ff", "n_vocab", "max_seq_len", "mtp_heads")]
+
+
 class CacheDesc(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in ("sink_size", "window_size", "pool_block", "max_context")]
 
@@ -111,6 +116,13 @@ SYMBOLS = {
     "pf_engine_set_max_memory": (C.c_int32, [vp, C.c_size_t]),
     "pf_engine_set_mtp_enabled": (C.c_int32, [vp, C.c_int32]),
     "pf_engine_set_layer_skip": (C.c_int32, [vp, C.c_float, C.c_uint32]),
+    "pf_squeeze_open": (C.c_int32, [C.c_char_p, C.POINTER(vp)]),
+    "pf_squeeze_close": (None, [vp]),
+    "pf_squeeze_last_error": (C.c_char_p, [vp]),
+    "pf_squeeze_get_info": (C.c_int32, [vp, C.POINTER(SqueezeInfo)]),
+    "pf_squeeze_block_shape": (C.c_int32, [vp, C.c_uint32, C.c_uint32, u32p, u32p, u32p]),
+    "pf_squeeze_load_block": (C.c_int32, [vp, C.c_uint32, C.c_uint32, vp, f32p]),
+    "pf_squeeze_load_model": (C.c_int32, [vp, vp, C.POINTER(vp)]),
     "pf_engine_layer_skip_count": (C.c_int32, [vp, C.POINTER(C.c_uint64)]),
     "pf_engine_pass_times": (C.c_int32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double), u32p, u32p]),
     "pf_engine_profile": (C.c_int32, [vp, C.c_int32]),
@@ -433,8 +445,76 @@ class KVCache:
         self.close()
 
 
+class Squeeze:
+    """A .squeeze file (WeightLoader, include/forge/quant_format.hpp:92-140) read
+    on the host; no GPU use."""
+
+    def __init__(self, path):
+        self.h = vp()
+        rc = lib().pf_squeeze_open(str(path).encode(), C.byref(self.h))
+        if rc:
+            self.h = None
+            raise PFError(f"pf_squeeze_open failed ({rc}): {lib().pf_squeeze_last_error(None).decode()}")
+        self._info = SqueezeInfo()
+        lib().pf_squeeze_get_info(self.h, C.byref(self._info))
+
+    def _check(self, rc, what):
+        if rc:
+            raise PFError(f"{what} failed ({rc}): {lib().pf_squeeze_last_error(self.h).decode()}")
+
+    def info(self):
+        return {n: getattr(self._info, n) for n, _ in SqueezeInfo._fields_}
+
+    def block_shape(self, layer, matrix):
+        r, c, q = C.c_uint32(0), C.c_uint32(0), C.c_uint32(0)
+        self._check(lib().pf_squeeze_block_shape(self.h, layer, matrix, C.byref(r), C.byref(c), C.byref(q)),
+                    "pf_squeeze_block_shape")
+        return r.value, c.value, q.value
+
+    def load_block(self, layer, matrix):
+        """(codes int8 [rows, cols], block multipliers float32 [ceil(rows*cols/32)], quant type)."""
+        rows, cols, q = self.block_shape(layer, matrix)
+        codes = np.zeros((rows, cols), np.int8)
+        scales = np.zeros((rows * cols + 31) // 32, np.float32)
+        self._check(lib().pf_squeeze_load_block(self.h, layer, matrix, codes.ctypes.data_as(vp), P(scales, f32p)),
+                    "pf_squeeze_load_block")
+        return codes, scales, q
+
+    def close(self):
+        if self.h:
+            lib().pf_squeeze_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+
 class Model:
     """Weights resident in HBM (pf_model_*)."""
+
+    @classmethod
+    def from_squeeze(cls, ctx, path, mtp=None):
+        """Engine::load_model over a .squeeze file: every layer uploaded in the
+        device layout.  mtp: optional [n_mtp] list of {gate, up, down} Q4
+        (fmt, codes, scales) heads, which the file format does not hold."""
+        sq = Squeeze(path)
+        try:
+            self = cls.__new__(cls)
+            self.ctx = ctx
+            i = sq.info()
+            self.cfg = dict(n_layers=i["n_layers"], n_embd=i["n_embd"], n_heads=i["n_heads"],
+                            head_dim=i["n_embd"] // max(1, i["n_heads"]), n_ff=i["n_ff"], n_vocab=i["n_vocab"],
+                            n_mtp=i["mtp_heads"])
+            self.h = vp()
+            sq._check(lib().pf_squeeze_load_model(ctx.h, sq.h, C.byref(self.h)), "pf_squeeze_load_model")
+            for k, hw in enumerate(mtp or []):
+                for j, n in enumerate(["gate", "up", "down"]):
+                    fmt, codes, scales = hw[n]
+                    ctx.check(lib().pf_model_set_mtp(self.h, k, j, P(codes, u8p), P(scales, u16p)),
+                              "pf_model_set_mtp")
+            return self
+        finally:
+            sq.close()
 
     def __init__(self, ctx, cfg, weights):
         self.ctx = ctx

@@ -30,6 +30,7 @@ CXX_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-ffp-contract=off", "-I" + os.path.j
 UNITS = [
     ("pf_runtime.hip", "hip"),
     ("pf_host.cpp", "cxx"),
+    ("pf_squeeze.cpp", "cxx"),
 ]
 
 

@@ -134,6 +134,10 @@ bool valid_fmt(int fmt) { return fmt == PF_FMT_Q4 || fmt == PF_FMT_Q2 || fmt == 
 
 }  // namespace
 
+namespace pf_host {
+uint16_t half_rne(float f) { return to_half(f); }
+}  // namespace pf_host
+
 extern "C" pf_status pf_quantize_matrix(const float* w, uint32_t rows, uint32_t cols, int32_t fmt,
                                         uint8_t* codes, uint16_t* scales) {
     if (!w || !codes || !scales || cols % 32 || !valid_fmt(fmt)) return PF_ERR_ARG;

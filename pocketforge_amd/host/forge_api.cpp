@@ -324,7 +324,45 @@ size_t Engine::MemoryStats::total() const {
     return weights_mmap + weights_decompressed + kv_cache + activations + prefetch_buffer + mtp_heads + other;
 }
 
-bool Engine::load_model(const std::string&) { return false; }
+// src/engine.cpp:48-201: the .squeeze file's configuration and weights
+// (every layer resident in HBM).  The format holds no MTP heads; the
+// reference draws them at load time (MTPHeads::init_weights), here they are
+// the seeded N(0, 0.02) Q4 heads of load_random_model (seed 0).
+bool Engine::load_model(const std::string& path) {
+    if (!dev_->ctx) dev_->ctx = shared_ctx();
+    pf_squeeze* sq = nullptr;
+    if (pf_squeeze_open(path.c_str(), &sq) != PF_OK) return false;
+    pf_squeeze_info info{};
+    pf_squeeze_get_info(sq, &info);
+    pf_engine_destroy(dev_->eng);
+    dev_->eng = nullptr;
+    pf_model_destroy(dev_->model);
+    dev_->model = nullptr;
+    const pf_status st = pf_squeeze_load_model(dev_->ctx.get(), sq, &dev_->model);
+    dev_->weight_bytes = 0;   // not tracked for loaded files
+    pf_squeeze_close(sq);
+    if (st != PF_OK) return false;
+    ModelConfig cfg = config_;
+    cfg.n_layers = info.n_layers;
+    cfg.n_embd = info.n_embd;
+    cfg.n_heads = info.n_heads;
+    cfg.n_kv_heads = info.n_kv_heads ? info.n_kv_heads : info.n_heads;
+    cfg.n_ff = info.n_ff;
+    cfg.n_vocab = info.n_vocab;
+    cfg.max_seq_len = info.max_seq_len;
+    cfg.mtp_heads = info.mtp_heads;
+    config_ = cfg;
+    const uint32_t D = cfg.n_embd;
+    dev_->mtp_bytes = 0;
+    for (uint32_t k = 0; k < cfg.mtp_heads; k++)
+        for (int32_t j = 0; j < 3; j++) {
+            HostMatrix m = gen_matrix(0, 0x20000u + 3u * k + (uint32_t)j, D, D, PF_FMT_Q4);
+            if (pf_model_set_mtp(dev_->model, k, j, m.codes.data(), m.scales.data()) != PF_OK) return false;
+            dev_->mtp_bytes += m.codes.size() + m.scales.size() * 2;
+        }
+    dev_->mtp_enabled = cfg.mtp_enabled;
+    return rebuild_engine();
+}
 bool Engine::load_norm_weights_from_gguf(const std::string&) { return false; }
 
 bool Engine::rebuild_engine() {

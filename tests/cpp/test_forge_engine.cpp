@@ -3,6 +3,7 @@
 // parity with the oracle engine on the same weights: forward logits bit for
 // bit, greedy and top-p token streams, MTP counters, step_mtp and the
 // MTP-disabled loop.
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -60,7 +61,17 @@ int run() {
     cfg.kv_cache_size = 64;
     cfg.mtp_heads = 4;
     forge::Engine engine;
-    CHECK(".squeeze loading is not part of this build", !engine.load_model("/nonexistent.squeeze"));
+    CHECK("a missing .squeeze file does not load", !engine.load_model("/nonexistent.squeeze"));
+    if (const char* sq = std::getenv("PF_TEST_SQUEEZE")) {
+        // a file in the reference's .squeeze format (written by the test driver)
+        forge::Engine fe;
+        CHECK(".squeeze model loads", fe.load_model(sq));
+        CHECK(".squeeze config layers", fe.config().n_layers == 2 && fe.config().n_embd == 256);
+        CHECK(".squeeze config vocab and heads", fe.config().n_vocab == 1024 && fe.config().mtp_heads == 4);
+        std::vector<int32_t> prompt = {5, 6, 7};
+        auto r = fe.generate(prompt, 12, nullptr, nullptr);
+        CHECK(".squeeze model generates", r.tokens.size() == prompt.size() + 12);
+    }
     CHECK("engine loads a synthetic model", engine.load_random_model(cfg, 1234));
     CHECK("config matches layers", engine.config().n_layers == cfg.n_layers);
     CHECK("config matches embd", engine.config().n_embd == cfg.n_embd);

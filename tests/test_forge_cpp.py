@@ -39,10 +39,29 @@ def test_forge_fails_loudly_without_a_gpu():
     assert r.returncode == 2 and "pf_init" in r.stderr
 
 
+def _squeeze_file(path):
+    """A 2-layer model (n_embd 256, n_ff 512, vocab 1024, 4 MTP heads) in the
+    reference's .squeeze format."""
+    import numpy as np
+    import squeeze_writer as SW
+    rng = np.random.default_rng(1)
+    D, F, V = 256, 512, 1024
+    shapes = [(D, D)] * 4 + [(F, D), (F, D), (D, F)]
+    blocks = [(l, m, (0.02 * rng.standard_normal(s)).astype(np.float32), SW.Q4)
+              for l in range(2) for m, s in enumerate(shapes)]
+    blocks.append((0, 10, (0.02 * rng.standard_normal((V, D))).astype(np.float32), SW.Q4))
+    SW.write_squeeze(str(path), dict(n_layers=2, n_embd=D, n_heads=4, n_kv_heads=4, n_ff=F, n_vocab=V,
+                                     max_seq_len=512, mtp_heads=4), blocks)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("name", TESTS)
-def test_forge_cpp(gpu, name):
-    r = subprocess.run([_built(name)], capture_output=True, text=True, timeout=300)
+def test_forge_cpp(gpu, name, tmp_path):
+    env = dict(os.environ)
+    if name == "test_forge_engine":
+        _squeeze_file(tmp_path / "m.squeeze")
+        env["PF_TEST_SQUEEZE"] = str(tmp_path / "m.squeeze")
+    r = subprocess.run([_built(name)], capture_output=True, text=True, timeout=300, env=env)
     print(r.stdout[-3000:])
     print(r.stderr[-3000:])
     assert r.returncode == 0, f"{name} failed:\n{r.stderr[-2000:]}"
