@@ -212,6 +212,7 @@ def main():
     # HIP start/stop events attached to every verify-pass GEMV dispatch
     dt_p, toks_p, res_p = step(True)
     n_l, gemv_us, gemv_bytes = eng.gemv_stats()
+    gemv_groups = eng.gemv_by_size()
     a_n, attn_us = eng.attn_stats()
     v_us, b_us, vn, bn = eng.pass_times()
     eng.profile(False)
@@ -267,6 +268,8 @@ def main():
             "launches": n_l,
             "timing": "HIP start/stop events attached to each GEMV dispatch (hipExtLaunchKernelGGL) on the engine "
                       "stream, in one extra decode step of the same workload issued without graphs",
+            "by_matrix": [{"bytes": round(b), "launches": n, "avg_us": round(u, 3),
+                           "GBps": round(b / u / 1e3, 1)} for b, n, u in gemv_groups],
         },
         "verify_pass": {
             "avg_us": round(v_us, 2),

@@ -294,6 +294,11 @@ pf_status pf_engine_profile(pf_engine* e, int32_t enable);
  * (packed weights + int8 activations + fp32 outputs) of the GEMV launches
  * recorded by the last pf_generate in profiling mode. */
 pf_status pf_engine_gemv_stats(pf_engine* e, uint32_t* launches, double* avg_us, double* avg_bytes);
+/* The same launches grouped by algorithmic bytes, one group per matrix shape
+ * (ascending bytes): up to `cap` groups are written, *n receives the number
+ * of groups.  Profiling aid; no reference counterpart. */
+pf_status pf_engine_gemv_by_size(const pf_engine* e, uint32_t cap, double* bytes, uint32_t* launches,
+                                 double* avg_us, uint32_t* n);
 /* Launch count and average duration (us) of the attention kernel of the
  * verify passes recorded by the last pf_generate / pf_batch_generate in
  * profiling mode (one launch per layer and pass). */

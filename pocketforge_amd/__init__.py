@@ -129,6 +129,8 @@ SYMBOLS = {
     "pf_engine_round_time": (C.c_int32, [vp, C.POINTER(C.c_double), u32p]),
     "pf_engine_gemv_stats": (C.c_int32, [vp, u32p, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "pf_engine_attn_stats": (C.c_int32, [vp, u32p, C.POINTER(C.c_double)]),
+    "pf_engine_gemv_by_size": (C.c_int32, [vp, C.c_uint32, C.POINTER(C.c_double), u32p, C.POINTER(C.c_double),
+                                           u32p]),
     "pf_batch_create": (C.c_int32, [vp, C.POINTER(CacheDesc), C.c_uint32, C.POINTER(vp)]),
     "pf_batch_sequences": (C.c_uint32, [vp]),
     "pf_batch_position": (C.c_uint32, [vp, C.c_uint32]),
@@ -642,6 +644,17 @@ class Engine:
         self.ctx.check(lib().pf_engine_gemv_stats(self.h, C.byref(n), C.byref(us), C.byref(by)),
                        "pf_engine_gemv_stats")
         return n.value, us.value, by.value
+
+    def gemv_by_size(self):
+        """[(algorithmic bytes, launches, average us)] of the profiled GEMV
+        launches, one entry per matrix shape."""
+        n = C.c_uint32(0)
+        self.ctx.check(lib().pf_engine_gemv_by_size(self.h, 0, None, None, None, C.byref(n)),
+                       "pf_engine_gemv_by_size")
+        k = n.value
+        by, ln, us = (C.c_double * k)(), (C.c_uint32 * k)(), (C.c_double * k)()
+        self.ctx.check(lib().pf_engine_gemv_by_size(self.h, k, by, ln, us, C.byref(n)), "pf_engine_gemv_by_size")
+        return [(by[i], ln[i], us[i]) for i in range(min(k, n.value))]
 
     def attn_stats(self):
         n, us = C.c_uint32(0), C.c_double(0)

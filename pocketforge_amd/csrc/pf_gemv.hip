@@ -44,13 +44,16 @@ __device__ __forceinline__ void unpack_codes(const uint8_t* tile, uint32_t t, ui
 // all partial sums are exact in fp64: the splits meet through fp64 atomic
 // adds in any order with a bit-identical result.  The consumer converts
 // (float)(acc * (double)a_scale) and clears acc.
-// Grid (N/64, splits), 256 threads; wave w of split s covers blocks
-// [(4s+w)*bpw, (4s+w+1)*bpw), bpw in {1, 2, 4} with nb % (4 bpw) == 0, lane =
-// output row.  Each wave issues all its weight loads first; the workgroup's
-// activation rows and block sums are staged in LDS with one vector load per
-// thread (they come from another kernel, often through another XCD's L2).
-template <int FMT, int M, bool GATED = false>
-__global__ __launch_bounds__(256) void k_gemv_i8(const uint8_t* __restrict__ W, uint32_t K,
+// Grid (N/64, splits), 64 WAVES threads; wave w of split s covers blocks
+// [(WAVES s+w)*bpw, (WAVES s+w+1)*bpw), bpw in {1, 2, 4} with
+// nb % (WAVES bpw) == 0, lane = output row.  The waves of a workgroup meet in
+// LDS, so larger workgroups mean fewer K splits and fewer fp64 atomics for
+// the same number of waves.  Each wave issues all its weight loads first; the
+// workgroup's activation rows and block sums are staged in LDS with one
+// vector load per thread (they come from another kernel, often through
+// another XCD's L2).
+template <int FMT, int M, bool GATED = false, int WAVES = 4>
+__global__ __launch_bounds__(64 * WAVES) void k_gemv_i8(const uint8_t* __restrict__ W, uint32_t K,
                                                  const int8_t* __restrict__ act, uint32_t act_stride,
                                                  const int32_t* __restrict__ bsum, uint32_t bsum_stride,
                                                  uint32_t bpw, double* __restrict__ acc, uint32_t acc_stride,
@@ -60,13 +63,14 @@ __global__ __launch_bounds__(256) void k_gemv_i8(const uint8_t* __restrict__ W, 
     constexpr int OFF = code_offset(FMT);
     if constexpr (GATED)
         if (*gate == 0u) return;   // no row of the pass needs this product
-    __shared__ __align__(16) int32_t sa[M][16 * 8];  // activations of the workgroup's 4 bpw <= 16 blocks
-    __shared__ int32_t sb[M][16];
-    __shared__ double red[4][M][64];
+    constexpr uint32_t NT = 64u * WAVES;
+    __shared__ __align__(16) int32_t sa[M][WAVES * 4 * 8];  // activations of the workgroup's WAVES bpw blocks
+    __shared__ int32_t sb[M][WAVES * 4];
+    __shared__ double red[WAVES][M][64];
     const uint32_t g = blockIdx.x, s = blockIdx.y;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t chunks = K >> 8, wb = 4u * bpw, wb0 = s * wb, b0 = wb0 + wid * bpw;
+    const uint32_t chunks = K >> 8, wb = WAVES * bpw, wb0 = s * wb, b0 = wb0 + wid * bpw;
     const uint8_t* tiles = W + (size_t)g * chunks * TB;
     uint32_t u[4][8];
     uint16_t dh[4];        // scale bits: converted after the staging below, so that no
@@ -83,7 +87,7 @@ __global__ __launch_bounds__(256) void k_gemv_i8(const uint8_t* __restrict__ W, 
             dh[k] = *reinterpret_cast<const uint16_t*>(tile + CODES + lane * 16u + (b & 7u) * 2u);
         }
     }
-    for (uint32_t i = threadIdx.x; i < (uint32_t)M * wb * 8u; i += 256u) {
+    for (uint32_t i = threadIdx.x; i < (uint32_t)M * wb * 8u; i += NT) {
         const uint32_t m = i / (wb * 8u), r = i - m * wb * 8u;
         sa[m][r] = reinterpret_cast<const int32_t*>(act + (size_t)m * act_stride)[wb0 * 8u + r];
     }
@@ -122,9 +126,11 @@ __global__ __launch_bounds__(256) void k_gemv_i8(const uint8_t* __restrict__ W, 
 #pragma unroll
     for (int m = 0; m < M; m++) red[wid][m][lane] = S[m];
     __syncthreads();
-    for (uint32_t t = threadIdx.x; t < (uint32_t)M * 64u; t += 256u) {
+    for (uint32_t t = threadIdx.x; t < (uint32_t)M * 64u; t += NT) {
         const uint32_t m = t >> 6, r = t & 63u;
-        const double v = red[0][m][r] + red[1][m][r] + red[2][m][r] + red[3][m][r];
+        double v = red[0][m][r];
+#pragma unroll
+        for (int w = 1; w < WAVES; w++) v += red[w][m][r];
         atomicAdd(acc + (size_t)m * acc_stride + (size_t)g * 64u + r, v);
     }
 }

@@ -12,6 +12,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <map>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -172,6 +173,7 @@ struct pf_matrix {
     uint16_t* scales = nullptr; // row-major only
     size_t bytes = 0;
     uint32_t bpw = 2, splits = 1;   // blocks per wave, K splits (grid y)
+    uint32_t waves = 4;             // waves per GEMV workgroup
 };
 
 static uint32_t interchange_code(int fmt, const uint8_t* blk, uint32_t e) {
@@ -238,20 +240,31 @@ static void repack_tiles(int fmt, uint32_t cols, const uint8_t* codes, const uin
 }
 
 // K split of a tiled matrix: the largest blocks-per-wave in {1, 2, 4} that
-// divides the blocks into whole workgroups (nb % (4 bpw) == 0; nb is a
-// multiple of 8) and still gives at least `min_waves` waves (default 2048:
-// every launch covers the 256 CUs; PF_GEMV_MIN_WAVES overrides it).
+// still gives at least `min_waves` waves in all (default 4096, four waves
+// per SIMD; PF_GEMV_MIN_WAVES overrides it), then the largest workgroup of
+// at most `max_wg` waves (default 8; PF_GEMV_WAVES overrides it) that
+// divides the blocks into whole workgroups (nb % (waves bpw) == 0; nb is a
+// multiple of 8).  The wave count depends on bpw only: larger workgroups
+// just meet in LDS instead of through fp64 atomics.  Defaults from a sweep
+// of min_waves {1024, 2048, 4096} x waves {4, 8} over the 1B verify pass
+// (M = 5): 6.09 us per launch on average against 6.58 us at 2048 x 4.
 static void choose_split(pf_matrix* M) {
     const uint32_t nb = M->cols / 32, G = M->rows / 64;
-    uint64_t min_waves = 2048;
+    uint64_t min_waves = 4096;
+    uint32_t max_wg = 8;
     if (const char* s = std::getenv("PF_GEMV_MIN_WAVES")) min_waves = std::strtoull(s, nullptr, 10);
+    if (const char* s = std::getenv("PF_GEMV_WAVES")) max_wg = (uint32_t)std::strtoul(s, nullptr, 10);
     uint32_t best = 1;
     for (uint32_t bpw : {1u, 2u, 4u}) {
         if (nb % (4 * bpw)) continue;
-        if ((uint64_t)G * (nb / (4 * bpw)) * 4 >= min_waves) best = bpw;
+        if ((uint64_t)G * (nb / bpw) >= min_waves) best = bpw;
     }
+    uint32_t waves = 4;
+    for (uint32_t w : {8u, 16u})
+        if (w <= max_wg && nb % (w * best) == 0) waves = w;
     M->bpw = best;
-    M->splits = nb / (4 * best);
+    M->waves = waves;
+    M->splits = nb / (waves * best);
 }
 
 static pf_status matrix_alloc(pf_ctx* c, int32_t fmt, uint32_t rows, uint32_t cols, bool rowmajor, pf_matrix** out) {
@@ -321,21 +334,27 @@ extern "C" void pf_matrix_free(pf_matrix* M) {
 
 // ------------------------------------------------------- kernel launches
 
-#define PF_GEMV_CASE(F, MM)                                                                                   \
-    case MM:                                                                                                  \
-        if (gate && ev0)                                                                                      \
-            hipExtLaunchKernelGGL((k_gemv_i8<F, MM, true>), dim3(W->rows / 64, W->splits), dim3(256), 0, st, ev0, \
-                                  ev1, 0, W->data, W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc,   \
-                                  acc_stride, gate);                                                          \
-        else if (gate)                                                                                        \
-            hipLaunchKernelGGL((k_gemv_i8<F, MM, true>), dim3(W->rows / 64, W->splits), dim3(256), 0, st, W->data, \
-                               W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc, acc_stride, gate);    \
-        else if (ev0)                                                                                         \
-            hipExtLaunchKernelGGL((k_gemv_i8<F, MM>), dim3(W->rows / 64, W->splits), dim3(256), 0, st, ev0, ev1, 0, \
-                                  W->data, W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc, acc_stride, gate); \
-        else                                                                                                  \
-            hipLaunchKernelGGL((k_gemv_i8<F, MM>), dim3(W->rows / 64, W->splits), dim3(256), 0, st, W->data,     \
-                               W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc, acc_stride, gate);    \
+#define PF_GEMV_LAUNCH(F, MM, WV)                                                                             \
+    if (gate && ev0)                                                                                          \
+        hipExtLaunchKernelGGL((k_gemv_i8<F, MM, true, WV>), dim3(W->rows / 64, W->splits), dim3(64 * WV), 0, st, \
+                              ev0, ev1, 0, W->data, W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc,  \
+                              acc_stride, gate);                                                              \
+    else if (gate)                                                                                            \
+        hipLaunchKernelGGL((k_gemv_i8<F, MM, true, WV>), dim3(W->rows / 64, W->splits), dim3(64 * WV), 0, st,  \
+                           W->data, W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc, acc_stride, gate); \
+    else if (ev0)                                                                                             \
+        hipExtLaunchKernelGGL((k_gemv_i8<F, MM, false, WV>), dim3(W->rows / 64, W->splits), dim3(64 * WV), 0, \
+                              st, ev0, ev1, 0, W->data, W->cols, act, act_stride, bsum, bsum_stride, W->bpw,   \
+                              acc, acc_stride, gate);                                                         \
+    else                                                                                                      \
+        hipLaunchKernelGGL((k_gemv_i8<F, MM, false, WV>), dim3(W->rows / 64, W->splits), dim3(64 * WV), 0, st, \
+                           W->data, W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc, acc_stride, gate);
+
+#define PF_GEMV_CASE(F, MM)                                      \
+    case MM:                                                     \
+        if (W->waves == 16) { PF_GEMV_LAUNCH(F, MM, 16) }        \
+        else if (W->waves == 8) { PF_GEMV_LAUNCH(F, MM, 8) }     \
+        else { PF_GEMV_LAUNCH(F, MM, 4) }                        \
         break;
 
 #define PF_GEMV_FMT(F)                                 \
@@ -1090,6 +1109,7 @@ struct pf_engine {
     uint32_t aev_n = 0;
     double kev_us = 0, kev_bytes_sum = 0;
     uint32_t kev_n = 0;
+    std::map<double, std::pair<double, uint32_t>> kev_by_size;   // bytes -> (us sum, launches)
     double verify_us = 0, base_us = 0;
     uint32_t verify_n = 0, base_n = 0;
     // persistent decode passes (M <= 8 rows; PF_PERSISTENT=1 selects them
@@ -1557,6 +1577,9 @@ static pf_status harvest_events(pf_engine* e, size_t t_lo, size_t t_hi, size_t k
         e->kev_us += ms * 1000.0;
         e->kev_bytes_sum += e->kev_bytes[i];
         e->kev_n++;
+        auto& bucket = e->kev_by_size[e->kev_bytes[i]];
+        bucket.first += ms * 1000.0;
+        bucket.second++;
     }
     return PF_OK;
 }
@@ -2004,6 +2027,7 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
     e->verify_n = e->base_n = 0;
     e->kev_us = e->kev_bytes_sum = 0;
     e->kev_n = 0;
+    e->kev_by_size.clear();
     e->aev_us = 0;
     e->aev_n = 0;
     e->aev_used = 0;
@@ -2106,6 +2130,22 @@ extern "C" pf_status pf_engine_gemv_stats(pf_engine* e, uint32_t* launches, doub
     if (launches) *launches = e->kev_n;
     if (avg_us) *avg_us = n ? e->kev_us / n : 0.0;
     if (avg_bytes) *avg_bytes = n ? e->kev_bytes_sum / n : 0.0;
+    return PF_OK;
+}
+
+extern "C" pf_status pf_engine_gemv_by_size(const pf_engine* e, uint32_t cap, double* bytes, uint32_t* launches,
+                                             double* avg_us, uint32_t* n) {
+    if (!e || !n || (cap && (!bytes || !launches || !avg_us))) return PF_ERR_ARG;
+    uint32_t i = 0;
+    for (const auto& kv : e->kev_by_size) {
+        if (i < cap) {
+            bytes[i] = kv.first;
+            launches[i] = kv.second.second;
+            avg_us[i] = kv.second.first / kv.second.second;
+        }
+        i++;
+    }
+    *n = i;
     return PF_OK;
 }
 
