@@ -261,7 +261,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": measured_traffic() if headline else None,
-            "traffic_source": "profiles/gemv_i8_traffic_1b_q4.md (rocprofv3 FETCH_SIZE x 1.99985 + WRITE_SIZE x 1.0, "
+            "traffic_source": "profiles/gemv_i8_traffic_1b_q4.md (rocprofv3 FETCH_SIZE x 1.99978 + WRITE_SIZE x 1.0, "
                               "factors from a copy kernel of known size)",
             "avg_launch_us": round(gemv_us, 3),
             "avg_bytes_per_launch": round(gemv_bytes),
