@@ -304,7 +304,7 @@ __global__ void k_wsum_combine_one(const float* __restrict__ Wp, uint32_t nch, u
 constexpr uint32_t att_vt(uint32_t vrow) { return 256 * vrow; }
 constexpr uint32_t att_smem(uint32_t vrow) { return att_vt(vrow) + (128 + 128 + 256 + 256 + 512 + 4) * 4; }
 
-template <int PARTS, uint32_t VROW = 144>
+template <int PARTS, uint32_t VROW = 144, bool COH = false>
 __device__ __forceinline__ void attn_one_row(const PassDesc* __restrict__ pd, const KvGeom& g, const KvPlanes& kv,
                                              uint32_t layer, uint32_t m, uint32_t h, uint32_t c,
                                              const float* __restrict__ q, const float* __restrict__ kself,
@@ -422,11 +422,17 @@ __device__ __forceinline__ void attn_one_row(const PassDesc* __restrict__ pd, co
         u = u + wp[128 + t];
         u = u + wp[256 + t];
         u = u + wp[384 + t];
-        Up[(mh * cstride + c) * hd + t] = u;
+        if constexpr (COH) stc(&Up[(mh * cstride + c) * hd + t], u);
+        else Up[(mh * cstride + c) * hd + t] = u;
     }
     if (t == 0) {
-        S[mh * s_stride + 2 * c] = mx;
-        S[mh * s_stride + 2 * c + 1] = T;
+        if constexpr (COH) {
+            stc(&S[mh * s_stride + 2 * c], mx);
+            stc(&S[mh * s_stride + 2 * c + 1], T);
+        } else {
+            S[mh * s_stride + 2 * c] = mx;
+            S[mh * s_stride + 2 * c + 1] = T;
+        }
     }
 }
 
@@ -493,9 +499,89 @@ __global__ __launch_bounds__(128) void k_attn_merge_chunks(const PassDesc* __res
 // quantize_activation_row (src/engine.cpp:789-796): per row m, every head's
 // chunks merged exactly as k_attn_merge_chunks does (max over the chunk
 // maxima, f_c = exp(m_c - max), T and U fmaf chains over c in order,
-// out = U * (1 / (T + 1e-10))), then the row quantized.  Grid M, 1024
-// threads; element i = t + 1024 k; heads * chunks <= 2048 (checked when the
-// engine is created).
+// out = U * (1 / (T + 1e-10))), then the row quantized.  NT threads;
+// element i = t + NT k; heads * chunks <= 2048 (checked when the engine is
+// created).  COH: S and Up are read with device-coherent loads (written by
+// other workgroups of the same kernel).  fs and ts hold 2048 floats each,
+// hmax and hinv 128, red 16.
+template <int PER, int NT, bool COH>
+__device__ __forceinline__ void merge_quant_row(const PassDesc* __restrict__ pd, const KvGeom& g, uint32_t m,
+                                                const float* __restrict__ S, uint32_t s_stride,
+                                                const float* __restrict__ Up, uint32_t cstride,
+                                                int8_t* __restrict__ q, uint32_t q_stride, float* __restrict__ as,
+                                                int32_t* __restrict__ bsum, uint32_t bsum_stride, float* fs,
+                                                float* ts, float* hmax, float* hinv, float* red) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t H = g.n_heads, hd = g.head_dim, D = H * hd;
+    const uint32_t nc = (kv_view(g, row_pos(pd, m)).count() + 1 + 255) / 256;
+    const float* st = S + (size_t)m * H * s_stride;
+    for (uint32_t i = t; i < H * nc; i += NT) {
+        const uint32_t h = i / nc, c = i - h * nc;
+        if constexpr (COH) {
+            fs[i] = ldc(&st[(size_t)h * s_stride + 2 * c]);
+            ts[i] = ldc(&st[(size_t)h * s_stride + 2 * c + 1]);
+        } else {
+            fs[i] = st[(size_t)h * s_stride + 2 * c];
+            ts[i] = st[(size_t)h * s_stride + 2 * c + 1];
+        }
+    }
+    __syncthreads();
+    if (t < H) {
+        float mx = fs[t * nc];
+        for (uint32_t c = 1; c < nc; c++) mx = fmaxf(mx, fs[t * nc + c]);
+        hmax[t] = mx;
+    }
+    __syncthreads();
+    for (uint32_t i = t; i < H * nc; i += NT) fs[i] = expf_c(fs[i] - hmax[i / nc]);
+    __syncthreads();
+    if (t < H) {
+        float T = 0.0f;
+        for (uint32_t c = 0; c < nc; c++) T = __builtin_fmaf(ts[t * nc + c], fs[t * nc + c], T);
+        hinv[t] = 1.0f / (T + 1e-10f);
+    }
+    __syncthreads();
+    // U chains over c in order per element; the loads of 8 chunks of all
+    // PER elements are issued before their FMAs
+    float v[PER];
+    const float* up[PER];
+    const float* f[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const uint32_t i = t + (uint32_t)NT * k;
+        const uint32_t h = i < D ? i / hd : 0u, l = i < D ? i - h * hd : 0u;
+        up[k] = Up + ((size_t)m * H + h) * cstride * hd + l;
+        f[k] = fs + h * nc;
+        v[k] = 0.0f;
+    }
+    for (uint32_t c0 = 0; c0 < nc; c0 += 8) {
+        const uint32_t nb = min(8u, nc - c0);
+        float uc[PER][8];
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const bool in = t + (uint32_t)NT * k < D;
+#pragma unroll
+            for (uint32_t u = 0; u < 8; u++) {
+                const float* a = up[k] + (size_t)(c0 + u) * hd;
+                uc[k][u] = (in && u < nb) ? (COH ? ldc(a) : *a) : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+#pragma unroll
+            for (uint32_t u = 0; u < 8; u++)
+                if (u < nb) v[k] = __builtin_fmaf(uc[k][u], f[k][c0 + u], v[k]);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const uint32_t i = t + (uint32_t)NT * k;
+        v[k] = i < D ? v[k] * hinv[i / hd] : 0.0f;
+    }
+    quantize_row_block<PER, NT>(v, D, q + (size_t)m * q_stride, as + m,
+                                bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
+}
+
+// Grid M + prefetch blocks, 1024 threads: merge_quant_row per row.
 template <int PER>
 __global__ __launch_bounds__(1024) void k_attn_merge_quant(const PassDesc* __restrict__ pd, KvGeom g,
                                                            const float* __restrict__ S, uint32_t s_stride,
@@ -506,52 +592,59 @@ __global__ __launch_bounds__(1024) void k_attn_merge_quant(const PassDesc* __res
     __shared__ float fs[2048], ts[2048];
     __shared__ float hmax[128], hinv[128];
     __shared__ float red[16];
-    const uint32_t m = blockIdx.x, t = threadIdx.x;
+    const uint32_t m = blockIdx.x;
     if (m >= rows) {
         prefetch_bytes(pf.p, pf.n, m - rows, gridDim.x - rows, pf.sink);
         return;
     }
     if (m >= pd->m) return;
-    const uint32_t H = g.n_heads, hd = g.head_dim, D = H * hd;
+    merge_quant_row<PER, 1024, false>(pd, g, m, S, s_stride, Up, cstride, q, q_stride, as, bsum, bsum_stride, fs, ts,
+                                      hmax, hinv, red);
+}
+
+// k_attn_chunk and k_attn_merge_quant in one kernel (passes of a few rows):
+// each (row, head, chunk) block stores its chunk results with coherent
+// stores, drains them and arrives on the row's counter; the block that
+// arrives last (heads x chunks arrivals) resets the counter and runs
+// merge_quant_row for that row.  No block waits for another.  Blocks past
+// `ablocks` prefetch pf (the O projection's weights).  cnt[m] is zero
+// between launches.
+template <int PARTS, uint32_t VROW, int PER>
+__global__ __launch_bounds__(256) void k_attn_chunk_mq(const PassDesc* __restrict__ pd, KvGeom g, KvPlanes kv,
+                                                       uint32_t layer, uint32_t M, uint32_t n_groups,
+                                                       uint32_t ablocks, const float* __restrict__ q,
+                                                       const float* __restrict__ kself,
+                                                       const float* __restrict__ vself, float* __restrict__ S,
+                                                       uint32_t s_stride, float* __restrict__ Up, uint32_t cstride,
+                                                       uint32_t* __restrict__ cnt, int8_t* __restrict__ qo,
+                                                       uint32_t q_stride, float* __restrict__ as,
+                                                       int32_t* __restrict__ bsum, uint32_t bsum_stride,
+                                                       Prefetch pf) {
+    static_assert(att_smem(VROW) >= (2048 + 2048 + 128 + 128 + 16) * 4, "merge scratch must fit the block's LDS");
+    __shared__ __align__(16) uint8_t smem[att_smem(VROW)];
+    __shared__ uint32_t last;
+    if (blockIdx.x >= ablocks) {
+        prefetch_bytes(pf.p, pf.n, blockIdx.x - ablocks, gridDim.x - ablocks, pf.sink);
+        return;
+    }
+    const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
+    const uint32_t grp = (slot / M) * 8u + xcd, m = slot % M;
+    if (grp >= n_groups || m >= pd->m) return;
+    const uint32_t H = g.n_heads, h = grp % H, c = grp / H;
     const uint32_t nc = (kv_view(g, row_pos(pd, m)).count() + 1 + 255) / 256;
-    const float* st = S + (size_t)m * H * s_stride;
-    for (uint32_t i = t; i < H * nc; i += 1024) {
-        const uint32_t h = i / nc, c = i - h * nc;
-        fs[i] = st[(size_t)h * s_stride + 2 * c];
-        ts[i] = st[(size_t)h * s_stride + 2 * c + 1];
+    if (c >= nc) return;   // attn_one_row writes nothing for such a chunk
+    attn_one_row<PARTS, VROW, true>(pd, g, kv, layer, m, h, c, q, kself, vself, S, s_stride, Up, cstride, smem);
+    drain();
+    if (threadIdx.x == 0) {
+        const uint32_t before = arrive_n(&cnt[m], 1u);
+        last = before + 1u == H * nc ? 1u : 0u;
+        if (last) stc(&cnt[m], 0u);
     }
     __syncthreads();
-    if (t < H) {
-        float mx = fs[t * nc];
-        for (uint32_t c = 1; c < nc; c++) mx = fmaxf(mx, fs[t * nc + c]);
-        hmax[t] = mx;
-    }
-    __syncthreads();
-    for (uint32_t i = t; i < H * nc; i += 1024) fs[i] = expf_c(fs[i] - hmax[i / nc]);
-    __syncthreads();
-    if (t < H) {
-        float T = 0.0f;
-        for (uint32_t c = 0; c < nc; c++) T = __builtin_fmaf(ts[t * nc + c], fs[t * nc + c], T);
-        hinv[t] = 1.0f / (T + 1e-10f);
-    }
-    __syncthreads();
-    float v[PER];
-#pragma unroll
-    for (int k = 0; k < PER; k++) {
-        const uint32_t i = t + 1024u * k;
-        v[k] = 0.0f;
-        if (i < D) {
-            const uint32_t h = i / hd, l = i - h * hd;
-            const float* up = Up + ((size_t)m * H + h) * cstride * hd + l;
-            const float* f = fs + h * nc;
-            float U = 0.0f;
-#pragma unroll 8
-            for (uint32_t c = 0; c < nc; c++) U = __builtin_fmaf(up[(size_t)c * hd], f[c], U);
-            v[k] = U * hinv[h];
-        }
-    }
-    quantize_row_block<PER, 1024>(v, D, q + (size_t)m * q_stride, as + m,
-                                  bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
+    if (!last) return;
+    float* fs = reinterpret_cast<float*>(smem);
+    merge_quant_row<PER, 256, true>(pd, g, m, S, s_stride, Up, cstride, qo, q_stride, as, bsum, bsum_stride, fs,
+                                    fs + 2048, fs + 4096, fs + 4224, fs + 4352);
 }
 
 }  // namespace pf

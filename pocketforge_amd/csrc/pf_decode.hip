@@ -48,25 +48,6 @@
 
 namespace pf {
 
-// ------------------------------------------------------------ coherence
-
-template <class T>
-__device__ __forceinline__ T ldc(const T* p) {
-    return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <class T>
-__device__ __forceinline__ void stc(T* p, T v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t arrive_n(uint32_t* c, uint32_t n) {
-    return __hip_atomic_fetch_add(c, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Every wave's memory operations complete, then the workgroup barrier.
-__device__ __forceinline__ void drain() {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-}
-
 // ------------------------------------------------------------ arguments
 
 struct DecodeOffsets {

@@ -204,6 +204,29 @@ __device__ __forceinline__ void prefetch_bytes(const uint8_t* __restrict__ p, si
     if (x == 0x7A5C3E1Fu) sink[0] = x;
 }
 
+// ------------------------------------------------------------ coherence
+
+// Hand-offs between workgroups of one kernel: agent-scope relaxed atomic
+// loads and stores reach the device-coherent level (the L2s of the XCDs are
+// not coherent with each other), drain() completes them before an arrival.
+
+template <class T>
+__device__ __forceinline__ T ldc(const T* p) {
+    return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ void stc(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t arrive_n(uint32_t* c, uint32_t n) {
+    return __hip_atomic_fetch_add(c, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Every wave's memory operations complete, then the workgroup barrier.
+__device__ __forceinline__ void drain() {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+}
+
 struct Prefetch {
     const uint8_t* p;   // bytes the next kernel reads first (null: none)
     size_t n;

@@ -498,6 +498,39 @@ static void launch_attn(hipStream_t st, uint32_t hd, uint32_t M, uint32_t blocks
 #undef PF_ATTN_LAUNCH
 }
 
+// Attention of a pass of fewer than 16 rows with the chunk merge and the O
+// input's quantization in the same kernel (k_attn_chunk_mq): `ablocks`
+// attention blocks, then blocks up to `blocks` that prefetch pf.
+// Model width D <= 4096.
+static void launch_attn_mq(hipStream_t st, uint32_t hd, uint32_t D, uint32_t M, uint32_t ablocks, uint32_t blocks,
+                           const PassDesc* pd, const KvGeom& g, const KvPlanes& kv, uint32_t l, uint32_t groups,
+                           const float* q, const float* k, const float* v, float* S, uint32_t s_stride, float* Wp,
+                           uint32_t cstride, uint32_t* cnt, int8_t* qo, uint32_t q_stride, float* as,
+                           int32_t* bsum, uint32_t bsum_stride, Prefetch pf, hipEvent_t ev0 = nullptr,
+                           hipEvent_t ev1 = nullptr) {
+#define PF_ATTN_MQ(P, PER)                                                                                        \
+    do {                                                                                                          \
+        if (ev0)                                                                                                  \
+            hipExtLaunchKernelGGL((k_attn_chunk_mq<P, 144u, PER>), dim3(blocks), dim3(256), 0, st, ev0, ev1, 0, pd, \
+                                  g, kv, l, M, groups, ablocks, q, k, v, S, s_stride, Wp, cstride, cnt, qo,      \
+                                  q_stride, as, bsum, bsum_stride, pf);                                         \
+        else                                                                                                      \
+            hipLaunchKernelGGL((k_attn_chunk_mq<P, 144u, PER>), dim3(blocks), dim3(256), 0, st, pd, g, kv, l, M,   \
+                               groups, ablocks, q, k, v, S, s_stride, Wp, cstride, cnt, qo, q_stride, as, bsum,   \
+                               bsum_stride, pf);                                                                 \
+    } while (0)
+#define PF_ATTN_MQ_PER(P)                          \
+    do {                                           \
+        if (D <= 1024) PF_ATTN_MQ(P, 4);           \
+        else if (D <= 2048) PF_ATTN_MQ(P, 8);      \
+        else PF_ATTN_MQ(P, 16);                    \
+    } while (0)
+    if (hd == 64) PF_ATTN_MQ_PER(4);
+    else PF_ATTN_MQ_PER(8);
+#undef PF_ATTN_MQ_PER
+#undef PF_ATTN_MQ
+}
+
 extern "C" pf_status pf_quantize_activation_rows(pf_ctx* c, const float* src, int8_t* dst, float* scales,
                                                  uint32_t M, uint32_t K) {
     if (!c || !src || !dst || !scales || M == 0) return PF_ERR_ARG;
@@ -1041,6 +1074,9 @@ struct pf_engine {
     float *q = nullptr, *k = nullptr, *v = nullptr;
     float* S = nullptr;
     float* Wp = nullptr;
+    uint32_t* attn_cnt = nullptr;   // per row: chunk arrivals of the fused attention, zero between launches
+    bool attn_fused = false;        // passes of < 16 rows: attention and merge in one kernel (PF_ATTN_FUSED=1;
+                                    // bit-exact, slower: 34 us against 17 + 6 us per layer at M = 5)
     uint32_t s_stride = 0, cstride = 0, kmax = 0;
     uint32_t cmax = 0;            // longest attention list (sink + pool + window)
     uint32_t prefill_rows = 8;    // rows of a prompt pass
@@ -1395,6 +1431,10 @@ static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t ns
     if (!s) s = ealloc(e, &e->v, (size_t)PR * D);
     if (!s) s = ealloc(e, &e->S, (size_t)PR * H * e->s_stride);
     if (!s) s = ealloc(e, &e->Wp, (size_t)PR * H * e->cstride * hd);
+    if (!s) s = ealloc(e, &e->attn_cnt, (size_t)PR);
+    if (!s && hipMemset(e->attn_cnt, 0, (size_t)PR * sizeof(uint32_t)) != hipSuccess)
+        s = fail(c, PF_ERR_HIP, "hipMemset of the attention counters failed");
+    if (const char* v = std::getenv("PF_ATTN_FUSED")) e->attn_fused = v[0] == '1';
     if (!s) s = ealloc(e, &e->logitsA, (size_t)MA * V);
     if (!s) s = ealloc(e, &e->hiddenA, (size_t)MA * D);
     if (!s) s = ealloc(e, &e->logitsB, (size_t)MR * V);
@@ -1735,11 +1775,17 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
             aev1 = e->aev[e->aev_used].b;
             e->aev_used++;
         }
-        launch_attn(st, hd, M, attn_blocks, pd, g, e->kv, l, attn_groups, e->q, e->k, e->v, e->S, e->s_stride,
-                    e->Wp, e->cstride, aev0, aev1);
-        PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_attn_merge_quant<PER>, dim3(rb), dim3(1024), 0, st, pd, g,
-                                                (const float*)e->S, e->s_stride, (const float*)e->Wp, e->cstride,
-                                                e->act, ks, as1, e->bsum, bs, M, prefetch_of(e, m->o[l])));
+        if (e->attn_fused && M < 16 && D <= 4096) {
+            launch_attn_mq(st, hd, D, M, attn_blocks, attn_blocks + 4 * e->pf_blocks, pd, g, e->kv, l, attn_groups,
+                           e->q, e->k, e->v, e->S, e->s_stride, e->Wp, e->cstride, e->attn_cnt, e->act, ks, as1,
+                           e->bsum, bs, prefetch_of(e, m->o[l]), aev0, aev1);
+        } else {
+            launch_attn(st, hd, M, attn_blocks, pd, g, e->kv, l, attn_groups, e->q, e->k, e->v, e->S, e->s_stride,
+                        e->Wp, e->cstride, aev0, aev1);
+            PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_attn_merge_quant<PER>, dim3(rb), dim3(1024), 0, st, pd, g,
+                                                    (const float*)e->S, e->s_stride, (const float*)e->Wp, e->cstride,
+                                                    e->act, ks, as1, e->bsum, bs, M, prefetch_of(e, m->o[l])));
+        }
         if (pf_status s = pass_gemv(e, m->o[l], M)) return s;
         // with layer skip on, the FFN products run only if some row needs
         // them (gate word)
