@@ -244,7 +244,7 @@ static void repack_tiles(int fmt, uint32_t cols, const uint8_t* codes, const uin
 // per SIMD; PF_GEMV_MIN_WAVES overrides it), then the largest workgroup of
 // at most `max_wg` waves (default 8; PF_GEMV_WAVES overrides it) that
 // divides the blocks into whole workgroups (nb % (waves bpw) == 0; nb is a
-// multiple of 8).  The wave count depends on bpw only: larger workgroups
+// multiple of 8) and still leaves a workgroup per CU (256 or more).  The wave count depends on bpw only: larger workgroups
 // just meet in LDS instead of through fp64 atomics.  Defaults from a sweep
 // of min_waves {1024, 2048, 4096} x waves {4, 8} over the 1B verify pass
 // (M = 5): 6.09 us per launch on average against 6.58 us at 2048 x 4.
@@ -261,7 +261,7 @@ static void choose_split(pf_matrix* M) {
     }
     uint32_t waves = 4;
     for (uint32_t w : {8u, 16u})
-        if (w <= max_wg && nb % (w * best) == 0) waves = w;
+        if (w <= max_wg && nb % (w * best) == 0 && (uint64_t)G * (nb / (w * best)) >= 256) waves = w;
     M->bpw = best;
     M->waves = waves;
     M->splits = nb / (waves * best);
