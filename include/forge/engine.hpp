@@ -24,8 +24,11 @@ public:
     Engine(const Engine&) = delete;
     Engine& operator=(const Engine&) = delete;
 
-    // The .squeeze reader is not part of this build: returns false and
-    // leaves the engine unloaded.
+    // Reads a .squeeze file (src/quant_format.cpp:231-425 format): Q4, Q2 and
+    // Q1.5 layer matrices, norms and the Q4 tied embedding go to the device;
+    // the MTP heads (absent from the format) are the seeded synthetic ones.
+    // Returns false when the file is missing, malformed or holds a matrix type
+    // without a device format (Q8 layer matrices).
     bool load_model(const std::string& squeezef_path);
     // This build's loader: seeded N(0, 0.02) weights (Philox4x32-10 +
     // Box-Muller, stream = matrix id), block-quantized, RMSNorm weights 1,
@@ -51,7 +54,12 @@ public:
 
     // src/engine.cpp:402-448: drafts from the MTP heads on hidden_state,
     // verified one token at a time with greedy argmax.  Returns (accepted,
-    // logits of the rejecting forward, or empty when all were accepted).
+    // logits of the rejecting forward, or empty when all were accepted).  As
+    // in the reference, mtp_accepted_out stays 0 on a rejection and
+    // mtp_rejected_out = heads - accepted.  The heads use the engine's tied
+    // table (embedding_table is only tested for emptiness: empty means one
+    // plain forward, like a model without heads); a hidden_state shorter than
+    // n_embd throws std::invalid_argument.
     std::pair<int, std::vector<float>> step_mtp(int32_t current_token, const std::vector<float>& hidden_state,
                                                 const std::vector<float>& embedding_table, int& mtp_accepted_out,
                                                 int& mtp_rejected_out);

@@ -54,6 +54,16 @@ class Sampling(C.Structure):
                 ("greedy", C.c_int32)]
 
 
+FWD_FN = C.CFUNCTYPE(None, C.c_void_p, C.c_int32, f32p)
+VALID_FN = C.CFUNCTYPE(C.c_int32, C.c_void_p)
+MTP_FN = C.CFUNCTYPE(None, C.c_void_p, f32p, f32p)
+
+
+class GenOps(C.Structure):
+    _fields_ = [("ctx", C.c_void_p), ("n_vocab", C.c_uint32), ("n_mtp", C.c_uint32),
+                ("forward", FWD_FN), ("hidden_valid", VALID_FN), ("mtp", MTP_FN)]
+
+
 def _load(path):
     lib = C.CDLL(path)
     return lib
@@ -128,6 +138,16 @@ def lib():
         L.orc_generate.argtypes = [C.c_void_p, i32p, C.c_uint32, C.c_uint32, C.POINTER(Sampling),
                                    C.c_uint64, i32p, C.c_uint32, u32p, i32p, i32p]
         L.orc_rope_table.argtypes = [C.c_uint32, C.c_uint32, f32p, f32p]
+        L.orc_philox4x32_10.argtypes = [u32p, u32p, u32p]
+        L.orc_rope_rotate.argtypes = [f32p, C.c_uint32, f32p, f32p]
+        L.orc_generate_ops.restype = C.c_int32
+        L.orc_generate_ops.argtypes = [C.POINTER(GenOps), i32p, C.c_uint32, C.c_uint32, C.POINTER(Sampling),
+                                       C.c_uint64, i32p, C.c_uint32, u32p, i32p, i32p]
+        step_args = [C.POINTER(Sampling), C.c_uint64, C.POINTER(C.c_uint64), f32p, u32p, i32p, i32p]
+        L.orc_step_mtp_ops.restype = C.c_int32
+        L.orc_step_mtp_ops.argtypes = [C.POINTER(GenOps), C.c_int32, f32p, C.c_int32] + step_args
+        L.orc_step_mtp.restype = C.c_int32
+        L.orc_step_mtp.argtypes = [C.c_void_p, C.c_int32, f32p, C.c_int32] + step_args
         L.orc_engine_set_layer_skip.argtypes = [C.c_void_p, C.c_float, C.c_uint32]
         L.orc_engine_skip_count.restype = C.c_uint32
         L.orc_engine_skip_count.argtypes = [C.c_void_p]
@@ -318,6 +338,68 @@ class Model:
                                 ptr(toks, i32p), cap, C.byref(n), C.byref(acc), C.byref(rej))
         assert rc == 0
         return toks[: n.value].copy(), acc.value, rej.value
+
+
+def philox4x32_10(ctr, key):
+    c = np.ascontiguousarray(ctr, np.uint32)
+    k = np.ascontiguousarray(key, np.uint32)
+    out = np.zeros(4, np.uint32)
+    lib().orc_philox4x32_10(ptr(c, u32p), ptr(k, u32p), ptr(out, u32p))
+    return out
+
+
+class ScriptedModel:
+    """A model for the decode control flow whose logits come from Python
+    callables: forward(token) -> logits [V] (records every call) and
+    heads(hidden or None) -> [n_mtp][V].  hidden_valid follows the
+    reference: false until the first forward (src/engine.cpp:551)."""
+
+    def __init__(self, n_vocab, n_mtp, forward, heads):
+        self.V, self.NH = n_vocab, n_mtp
+        self.calls = []
+        self.mtp_calls = 0
+        self._valid = 0
+
+        def fwd(_ctx, tok, out):
+            lg = np.asarray(forward(int(tok)), np.float32)
+            self.calls.append(int(tok))
+            self._valid = 1
+            if out:
+                C.memmove(out, lg.ctypes.data, 4 * self.V)
+
+        def valid(_ctx):
+            return self._valid
+
+        def mtp(_ctx, hidden, out):
+            h = None if not hidden else np.ctypeslib.as_array(hidden, (1,)).copy()
+            lg = np.ascontiguousarray(heads(h), np.float32).reshape(self.NH, self.V)
+            self.mtp_calls += 1
+            C.memmove(out, lg.ctypes.data, 4 * self.V * self.NH)
+
+        self._cb = (FWD_FN(fwd), VALID_FN(valid), MTP_FN(mtp))
+        self.ops = GenOps(None, n_vocab, n_mtp, *self._cb)
+
+    def generate(self, prompt, max_new, sampling, seed=7, cap=None):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        cap = cap or len(prompt) + max_new + 8
+        toks = np.zeros(max(cap, 1), np.int32)
+        n = C.c_uint32(0)
+        acc = C.c_int32(0)
+        rej = C.c_int32(0)
+        rc = lib().orc_generate_ops(C.byref(self.ops), ptr(prompt, i32p), len(prompt), max_new, C.byref(sampling),
+                                    seed, ptr(toks, i32p), cap, C.byref(n), C.byref(acc), C.byref(rej))
+        return rc, toks[: n.value].copy(), acc.value, rej.value
+
+    def step_mtp(self, token, hidden, has_table, sampling, seed=42, draw=0):
+        h = np.ascontiguousarray(hidden if hidden is not None else np.zeros(1), np.float32)
+        lg = np.zeros(self.V, np.float32)
+        d = C.c_uint64(draw)
+        nl = C.c_uint32(0)
+        a = C.c_int32(0)
+        r = C.c_int32(0)
+        k = lib().orc_step_mtp_ops(C.byref(self.ops), int(token), ptr(h, f32p), int(has_table), C.byref(sampling),
+                                   seed, C.byref(d), ptr(lg, f32p), C.byref(nl), C.byref(a), C.byref(r))
+        return k, (lg if nl.value else None), a.value, r.value, d.value
 
 
 def sample(logits, cfg, seed, draw_idx):

@@ -883,6 +883,19 @@ void orc_rope_table(uint32_t hd, uint32_t pos, float* cos_out, float* sin_out) {
     }
 }
 
+/* RoPE rotation of one head vector, src/engine.cpp:739-748: pair
+ * (x[2t], x[2t+1]) -> (x0 c - x1 s, x0 s + x1 c) with cos/sin of pair t, in
+ * the contracted form the reference's x86 build (-march=native) emits:
+ * fmaf(x0, c, -(x1 s)) and fmaf(x0, s, x1 c). */
+void orc_rope_rotate(float* x, uint32_t hd, const float* cos_t, const float* sin_t) {
+    for (uint32_t i = 0; i < hd; i += 2) {
+        float c = cos_t[i / 2], s = sin_t[i / 2];
+        float x0 = x[i], x1 = x[i + 1];
+        x[i] = fmaf(x0, c, -(x1 * s));
+        x[i + 1] = fmaf(x0, s, x1 * c);
+    }
+}
+
 /* Softmax-weighted sum of one head (src/engine.cpp:767-778 with
  * src/matmul_neon.cpp:212-226 and src/kv_cache.cpp:160-198) in the
  * canonical chunked order.  The list is the `cnt` visible entries followed
@@ -1010,15 +1023,8 @@ void orc_forward(orc_engine* e, int32_t token, float* logits, float* hidden) {
         orc_gemv_i8(&W[1], e->a8, as, e->k);
         orc_gemv_i8(&W[2], e->a8, as, e->v);
         for (uint32_t hh = 0; hh < H; hh++) {              /* src/engine.cpp:732-749 */
-            float* qh = e->q + hh * hd; float* kh = e->k + hh * hd;
-            for (uint32_t i = 0; i < hd; i += 2) {
-                float c = rc[i / 2], s = rs[i / 2];
-                float q0 = qh[i], q1 = qh[i + 1], k0 = kh[i], k1 = kh[i + 1];
-                qh[i] = fmaf(q0, c, -(q1 * s));
-                qh[i + 1] = fmaf(q0, s, q1 * c);
-                kh[i] = fmaf(k0, c, -(k1 * s));
-                kh[i + 1] = fmaf(k0, s, k1 * c);
-            }
+            orc_rope_rotate(e->q + hh * hd, hd, rc, rs);
+            orc_rope_rotate(e->k + hh * hd, hd, rc, rs);
         }
         for (uint32_t hh = 0; hh < H; hh++)                /* src/engine.cpp:753-779 */
             orc_attn_head(e->kv, l, hh, e->q + hh * hd, e->k + hh * hd, e->v + hh * hd, e->attn + hh * hd);
@@ -1219,61 +1225,135 @@ static double now_s(void) {
 /* Wall time of the decode loop (after the prompt) of the last orc_generate. */
 double orc_last_decode_seconds(void) { return g_last_decode_seconds; }
 
-/* Engine::generate, src/engine.cpp:276-396, MTP branch :304-373 and the
- * fallback :377-386, with the sampling configuration passed explicitly.
- * Returns 0, or -1 when tokens_cap is too small. */
-int32_t orc_generate(orc_engine* e, const int32_t* prompt, uint32_t n_prompt,
-                     uint32_t max_new, const orc_sampling* cfg, uint64_t seed,
-                     int32_t* tokens, uint32_t cap, uint32_t* n_tokens,
-                     int32_t* mtp_accepted, int32_t* mtp_rejected) {
-    const orc_model_desc* d = &e->d;
-    uint32_t V = d->n_vocab, D = d->n_embd, NH = d->n_mtp;
+/* Engine::generate, src/engine.cpp:276-396 (MTP branch :304-373, fallback
+ * :377-386) over an abstract model (orc_gen_ops), so that the same control
+ * flow runs on the oracle engine and on scripted logits.  The sampling
+ * configuration is passed explicitly (the reference can only use its
+ * defaults, :311, 324, 355, 383).  Returns 0, or -1 when tokens_cap is too
+ * small. */
+int32_t orc_generate_ops(const orc_gen_ops* ops, const int32_t* prompt, uint32_t n_prompt,
+                         uint32_t max_new, const orc_sampling* cfg, uint64_t seed,
+                         int32_t* tokens, uint32_t cap, uint32_t* n_tokens,
+                         int32_t* mtp_accepted, int32_t* mtp_rejected) {
+    uint32_t V = ops->n_vocab, NH = ops->n_mtp;
     uint64_t draw = 0;
     uint32_t nt = 0;
     int32_t acc_total = 0, rej_total = 0;
     float* logits = (float*)malloc(sizeof(float) * V);
     float* mtp_logits = (float*)malloc(sizeof(float) * V * (NH ? NH : 1));
-    float* hid = (float*)malloc(sizeof(float) * D);
     int32_t* preds = (int32_t*)malloc(sizeof(int32_t) * (NH ? NH : 1));
 #define PUSH(t) do { if (nt >= cap) { nt = cap + 1; goto done; } tokens[nt++] = (t); } while (0)
-    for (uint32_t i = 0; i < n_prompt; i++) orc_forward(e, prompt[i], NULL, NULL);
+    for (uint32_t i = 0; i < n_prompt; i++) ops->forward(ops->ctx, prompt[i], NULL);   /* :286-290 */
     for (uint32_t i = 0; i < n_prompt; i++) PUSH(prompt[i]);
     double t_dec = now_s();
     uint32_t n_gen = 0;
-    int32_t cur = n_prompt ? prompt[n_prompt - 1] : 0;
+    int32_t cur = n_prompt ? prompt[n_prompt - 1] : 0;                     /* :294 */
     while (n_gen < max_new) {
-        if (NH > 0 && e->hidden_valid && n_gen + 4 <= max_new) {
-            orc_forward(e, cur, logits, NULL);
-            int32_t T1 = orc_sample(logits, V, cfg, seed, &draw);
+        /* :304-305: MTP heads present, a hidden state, and n + 4 <= N */
+        if (NH > 0 && ops->hidden_valid(ops->ctx) && n_gen + 4 <= max_new) {
+            ops->forward(ops->ctx, cur, logits);                          /* :308 */
+            int32_t T1 = orc_sample(logits, V, cfg, seed, &draw);         /* :311 */
             PUSH(T1); n_gen++;
-            orc_mtp_forward(e, e->last_hidden, mtp_logits);
+            ops->mtp(ops->ctx, NULL, mtp_logits);                         /* :318-319 */
             for (uint32_t k = 0; k < NH; k++) preds[k] = orc_sample(mtp_logits + (size_t)k * V, V, cfg, seed, &draw);
             int accepted = 0, rejected = 0;
-            for (uint32_t k = 0; k < NH; k++) {
+            for (uint32_t k = 0; k < NH; k++) {                           /* :332-366 */
                 int32_t in = (k == 0) ? T1 : preds[k - 1];
-                orc_forward(e, in, logits, hid);
+                ops->forward(ops->ctx, in, logits);
                 int32_t main_pred = orc_argmax(logits, V);
                 if (main_pred == preds[k]) {
                     PUSH(preds[k]); n_gen++; accepted++;
                 } else {
                     int32_t corr = orc_sample(logits, V, cfg, seed, &draw);
-                    if (corr != preds[k]) { PUSH(corr); n_gen++; rejected++; }
+                    if (corr != preds[k]) { PUSH(corr); n_gen++; rejected++; }   /* :357-363 */
                     break;
                 }
             }
             acc_total += accepted; rej_total += rejected;
-            cur = tokens[nt - 1];
+            cur = tokens[nt - 1];                                         /* :372 */
             continue;
         }
-        orc_forward(e, cur, logits, NULL);
+        ops->forward(ops->ctx, cur, logits);                              /* :378 */
         cur = orc_sample(logits, V, cfg, seed, &draw);
         PUSH(cur); n_gen++;
     }
 done:
 #undef PUSH
     g_last_decode_seconds = now_s() - t_dec;
-    free(logits); free(mtp_logits); free(hid); free(preds);
+    free(logits); free(mtp_logits); free(preds);
     *n_tokens = nt > cap ? cap : nt;
     *mtp_accepted = acc_total; *mtp_rejected = rej_total;
     return nt > cap ? -1 : 0;
+}
+
+/* Engine::step_mtp, src/engine.cpp:402-448, over an abstract model: drafts
+ * sampled from the heads on `hidden`, each verified by one greedy forward.
+ * Without heads (or with no table, has_table == 0) it is one plain forward
+ * of current_token (:413-416).  On a rejection the reference returns the
+ * rejecting forward's logits and leaves mtp_accepted_out at 0 (:437-440);
+ * when every draft is accepted the logits are empty (:443-447).  Returns the
+ * accepted count; *n_logits is V when logits_out was written, else 0.  The
+ * draw counter advances once per stochastic sample. */
+int32_t orc_step_mtp_ops(const orc_gen_ops* ops, int32_t current_token, const float* hidden, int32_t has_table,
+                         const orc_sampling* cfg, uint64_t seed, uint64_t* draw, float* logits_out,
+                         uint32_t* n_logits, int32_t* acc_out, int32_t* rej_out) {
+    uint32_t V = ops->n_vocab, NH = ops->n_mtp;
+    *acc_out = 0; *rej_out = 0; *n_logits = 0;
+    if (NH == 0 || !has_table) {
+        ops->forward(ops->ctx, current_token, logits_out);
+        *n_logits = V;
+        return 0;
+    }
+    float* mtp_logits = (float*)malloc(sizeof(float) * V * NH);
+    int32_t* preds = (int32_t*)malloc(sizeof(int32_t) * NH);
+    ops->mtp(ops->ctx, hidden, mtp_logits);
+    for (uint32_t k = 0; k < NH; k++) preds[k] = orc_sample(mtp_logits + (size_t)k * V, V, cfg, seed, draw);
+    int32_t accepted = 0;
+    for (uint32_t k = 0; k < NH; k++) {
+        int32_t in = (k == 0) ? current_token : preds[k - 1];
+        ops->forward(ops->ctx, in, logits_out);
+        if (orc_argmax(logits_out, V) == preds[k]) {
+            accepted++;
+        } else {
+            *rej_out = (int32_t)NH - accepted;
+            *n_logits = V;
+            free(mtp_logits); free(preds);
+            return accepted;
+        }
+    }
+    *acc_out = accepted;
+    free(mtp_logits); free(preds);
+    return accepted;
+}
+
+/* The oracle engine as an orc_gen_ops model: forward = orc_forward,
+ * hidden_valid = Engine::hidden_valid_ (set by every forward,
+ * src/engine.cpp:551), heads = MTPHeads::forward on the given hidden state
+ * or on the last forward's (last_hidden_, :550) with the tied table. */
+static void eng_forward(void* ctx, int32_t token, float* logits) { orc_forward((orc_engine*)ctx, token, logits, NULL); }
+static int32_t eng_hidden_valid(void* ctx) { return ((orc_engine*)ctx)->hidden_valid; }
+static void eng_mtp(void* ctx, const float* hidden, float* logits) {
+    orc_engine* e = (orc_engine*)ctx;
+    orc_mtp_forward(e, hidden ? hidden : e->last_hidden, logits);
+}
+static orc_gen_ops engine_ops(orc_engine* e) {
+    orc_gen_ops o = {e, e->d.n_vocab, e->d.n_mtp, eng_forward, eng_hidden_valid, eng_mtp};
+    return o;
+}
+
+int32_t orc_generate(orc_engine* e, const int32_t* prompt, uint32_t n_prompt,
+                     uint32_t max_new, const orc_sampling* cfg, uint64_t seed,
+                     int32_t* tokens, uint32_t cap, uint32_t* n_tokens,
+                     int32_t* mtp_accepted, int32_t* mtp_rejected) {
+    orc_gen_ops o = engine_ops(e);
+    return orc_generate_ops(&o, prompt, n_prompt, max_new, cfg, seed, tokens, cap, n_tokens, mtp_accepted,
+                            mtp_rejected);
+}
+
+int32_t orc_step_mtp(orc_engine* e, int32_t current_token, const float* hidden, int32_t has_table,
+                     const orc_sampling* cfg, uint64_t seed, uint64_t* draw, float* logits_out,
+                     uint32_t* n_logits, int32_t* acc_out, int32_t* rej_out) {
+    orc_gen_ops o = engine_ops(e);
+    return orc_step_mtp_ops(&o, current_token, hidden, has_table, cfg, seed, draw, logits_out, n_logits, acc_out,
+                            rej_out);
 }

@@ -128,6 +128,7 @@ void     orc_engine_reset(orc_engine* e);
 uint32_t orc_engine_pos(const orc_engine* e);
 orc_kv*  orc_engine_kv(orc_engine* e);
 void     orc_rope_table(uint32_t head_dim, uint32_t pos, float* cos_out, float* sin_out);
+void     orc_rope_rotate(float* x, uint32_t head_dim, const float* cos_t, const float* sin_t);
 void     orc_forward(orc_engine* e, int32_t token, float* logits, float* hidden);
 /* LayerSkipController (src/layer_skip.cpp) in the forward pass: threshold
  * (0 = off, the default here; the reference's ModelConfig default is 0.01)
@@ -143,6 +144,26 @@ void     orc_mtp_forward(orc_engine* e, const float* hidden, float* logits);
 int32_t  orc_argmax(const float* x, uint32_t n);
 int32_t  orc_sample(const float* logits, uint32_t n_vocab, const orc_sampling* cfg,
                     uint64_t seed, uint64_t* draw_idx);
+/* An abstract model for the decode control flow: forward one token
+ * (logits may be NULL), whether a hidden state exists, and the MTP heads on
+ * `hidden` (NULL: the last forward's hidden state) writing [n_mtp][V]. */
+typedef struct {
+    void*    ctx;
+    uint32_t n_vocab, n_mtp;
+    void     (*forward)(void* ctx, int32_t token, float* logits);
+    int32_t  (*hidden_valid)(void* ctx);
+    void     (*mtp)(void* ctx, const float* hidden, float* logits);
+} orc_gen_ops;
+int32_t  orc_generate_ops(const orc_gen_ops* ops, const int32_t* prompt, uint32_t n_prompt,
+                          uint32_t max_new, const orc_sampling* cfg, uint64_t seed,
+                          int32_t* tokens_out, uint32_t tokens_cap, uint32_t* n_tokens,
+                          int32_t* mtp_accepted, int32_t* mtp_rejected);
+int32_t  orc_step_mtp_ops(const orc_gen_ops* ops, int32_t current_token, const float* hidden, int32_t has_table,
+                          const orc_sampling* cfg, uint64_t seed, uint64_t* draw, float* logits_out,
+                          uint32_t* n_logits, int32_t* acc_out, int32_t* rej_out);
+int32_t  orc_step_mtp(orc_engine* e, int32_t current_token, const float* hidden, int32_t has_table,
+                      const orc_sampling* cfg, uint64_t seed, uint64_t* draw, float* logits_out,
+                      uint32_t* n_logits, int32_t* acc_out, int32_t* rej_out);
 int32_t  orc_generate(orc_engine* e, const int32_t* prompt, uint32_t n_prompt,
                       uint32_t max_new, const orc_sampling* cfg, uint64_t seed,
                       int32_t* tokens_out, uint32_t tokens_cap, uint32_t* n_tokens,

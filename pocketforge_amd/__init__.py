@@ -3,9 +3,8 @@
 The binding mirrors the reference's C++ API surface for the MTP hot path
 (include/forge/{matmul_neon,kv_cache,mtp,engine}.hpp): every call goes to
 the gfx950 kernels; there is no CPU fallback.  If the library is missing the
-import raises.  Device buffers for the kernel-level entry points are torch
-buffers come from the library's own pf_malloc (DeviceArray); torch tensors
-are accepted too but not needed.
+import raises.  Device buffers for the kernel-level entry points come from
+the library's own pf_malloc (DeviceArray).
 """
 import ctypes as C
 import os
@@ -265,7 +264,7 @@ class Context:
     def device_bytes(self):
         return lib().pf_device_bytes(self.h)
 
-    # matmul_neon.hpp mirrors (device buffers: DeviceArray or torch tensors)
+    # matmul_neon.hpp mirrors (device buffers: DeviceArray)
     def to_device(self, a):
         return DeviceArray.from_numpy(self, a)
 

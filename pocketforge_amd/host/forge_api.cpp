@@ -509,11 +509,15 @@ std::pair<int, std::vector<float>> Engine::step_mtp(int32_t current_token, const
                                                     int& rej_out) {
     acc_out = 0;
     rej_out = 0;
-    if (!dev_->eng || config_.mtp_heads == 0 || !dev_->mtp_enabled || embedding_table.empty() ||
-        hidden_state.size() < config_.n_embd)
-        return {0, forward({current_token})};
-    // The engine's heads and its device-resident tied table (the reference
-    // passes its own dequantized table here, src/engine.cpp:308-365).
+    // src/engine.cpp:413-416: no heads, or no table, is one plain forward.  As
+    // in the reference, ModelConfig::mtp_enabled is not consulted here.
+    if (!dev_->eng || config_.mtp_heads == 0 || embedding_table.empty()) return {0, forward({current_token})};
+    if (hidden_state.size() < config_.n_embd)
+        throw std::invalid_argument("Engine::step_mtp: hidden_state shorter than n_embd");
+    // The heads run on the engine's device-resident tied table; the caller's
+    // fp32 table is only checked for emptiness.  Engine::generate passes the
+    // dequantized tied table itself (src/engine.cpp:318-319), so the two agree
+    // for the reference's own caller.
     const uint32_t V = config_.n_vocab, NH = config_.mtp_heads;
     std::vector<float> mtp_logits((size_t)NH * V);
     check(dev_->ctx.get(), pf_mtp_forward(dev_->eng, hidden_state.data(), mtp_logits.data()), "pf_mtp_forward");

@@ -114,16 +114,36 @@ int run() {
             same = same && lg == lo && hid == ho;
         }
         CHECK("forward logits and hidden equal the oracle (12 tokens)", same);
-        // step_mtp (src/engine.cpp:402-448) on the last hidden state
-        int acc = -1, rej = -1;
-        std::vector<float> table(1, 0.0f);
-        auto st = e.step_mtp(7, hid, table, acc, rej);
-        CHECK("step_mtp counts", st.first >= 0 && st.first <= 4 &&
-                                     ((st.second.empty() && acc == st.first && rej == 0) ||
-                                      (st.second.size() == cfg.n_vocab && acc == 0 && rej == 4 - st.first)));
+        // step_mtp (src/engine.cpp:402-448) on the last hidden state, against
+        // the oracle's restatement on the same state: default sampling
+        // (top-p), seed 42, the engine's draw counter (0: only forwards ran)
+        const forge::SamplingConfig dflt;
+        const orc_sampling os{dflt.temperature, dflt.top_p, dflt.top_k, 0};
+        uint64_t draw = 0;
+        for (int round = 0; round < 3; round++) {
+            int acc = -1, rej = -1;
+            std::vector<float> table(1, 0.0f);
+            const int32_t tok = 7 + 100 * round;
+            auto st = e.step_mtp(tok, hid, table, acc, rej);
+            std::vector<float> ol(cfg.n_vocab);
+            uint32_t nl = 0;
+            int32_t oacc = -1, orej = -1;
+            const int32_t ok = orc_step_mtp(o, tok, hid.data(), 1, &os, 42, &draw, ol.data(), &nl, &oacc, &orej);
+            ol.resize(nl);
+            CHECK("step_mtp (accepted, counters, logits) equal the oracle",
+                  st.first == ok && acc == oacc && rej == orej && st.second == ol);
+            e.forward_with_hidden({tok}, hid);
+            orc_forward(o, tok, lo.data(), ho.data());
+            CHECK("forward after step_mtp equals the oracle", hid == ho);
+        }
         int acc2 = -1, rej2 = -1;
         auto st2 = e.step_mtp(7, hid, {}, acc2, rej2);
-        CHECK("step_mtp without a table forwards the token", st2.first == 0 && st2.second.size() == cfg.n_vocab);
+        uint32_t nl = 0;
+        int32_t oacc = -1, orej = -1;
+        std::vector<float> ol(cfg.n_vocab);
+        orc_step_mtp(o, 7, hid.data(), 0, &os, 42, &draw, ol.data(), &nl, &oacc, &orej);
+        CHECK("step_mtp without a table forwards the token",
+              st2.first == 0 && acc2 == 0 && rej2 == 0 && nl == cfg.n_vocab && st2.second == ol);
         orc_engine_destroy(o);
     }
     for (int greedy = 1; greedy >= 0; greedy--) {
