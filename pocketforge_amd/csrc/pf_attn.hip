@@ -1,15 +1,15 @@
 // 3-tier int8 KV cache and verify attention for gfx950.
 //
-// A pass of M rows at consecutive positions p0..p0+M-1 runs, per layer:
-//   k_qkv_post     Q/K/V from the fused GEMV partials, RoPE, int8 K/V rows
-//                  written to the plane row of each position (sink slot or
-//                  ring slot; the ring has slack, so pending rows of a
-//                  verify pass never overwrite a visible entry)
+// A pass of M rows at consecutive positions p0..p0+M-1 runs, per layer
+// (after the Q/K/V product, whose epilogue applies RoPE, pf_mm.hip):
+//   k_kv_store_pass  int8 K/V rows of each pass row written to the plane row
+//                  of its position (sink slot or ring slot; the ring has
+//                  slack, so pending rows of a verify pass never overwrite a
+//                  visible entry)
 //   k_attn_chunk   per (row, head, 256-entry chunk of the row's list):
 //                  scores, chunk max, exp, chunk sum and chunk-weighted V
-//   k_attn_merge_chunks  per (row, head): chunks rescaled to the row max
-//                  and merged; the O projection's quantize_activation_row
-//                  follows
+//   k_attn_merge_quant  per row: chunks rescaled to the row max and merged,
+//                  then the O projection's quantize_activation_row
 // The KVCache API (raw scores; weighted sum of caller probabilities) runs
 // k_attn_scores and k_attn_wsum.
 // k_pool_rows folds evicted window entries into pooled rows
@@ -58,16 +58,12 @@ __device__ __forceinline__ void store_pair(const KvGeom& g, KvPlanes kv, size_t 
     }
 }
 
-// Grid (M, heads), 64 threads.  acc = fused QKV GEMV accumulators
-// ([M][3D], cleared here), as = their activation scales.
-// RoPE of src/engine.cpp:732-749 with the host-computed angle tables
-// (cos/sin [position][head_dim/2]).
-__global__ __launch_bounds__(64) void k_qkv_post(double* __restrict__ acc, const float* __restrict__ as,
-                                                 const PassDesc* __restrict__ pd,
-                                                 const float* __restrict__ rc, const float* __restrict__ rs,
-                                                 KvGeom g, KvPlanes kv, uint32_t layer,
-                                                 float* __restrict__ q_out, float* __restrict__ k_out,
-                                                 float* __restrict__ v_out) {
+// KVCache::store (src/kv_cache.cpp:59-127) of every row of a pass: grid
+// (M, heads), 64 threads; k and v [M][D] hold the rows' keys (after RoPE) and
+// values in fp32.
+__global__ __launch_bounds__(64) void k_kv_store_pass(const PassDesc* __restrict__ pd, KvGeom g, KvPlanes kv,
+                                                      uint32_t layer, const float* __restrict__ k,
+                                                      const float* __restrict__ v) {
     const uint32_t m = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
     if (m >= pd->m) return;
     const uint32_t hd = g.head_dim, D = g.n_heads * hd, half = hd >> 1;
@@ -75,22 +71,9 @@ __global__ __launch_bounds__(64) void k_qkv_post(double* __restrict__ acc, const
     const bool act = t < half;
     float k0 = 0.f, k1 = 0.f, v0 = 0.f, v1 = 0.f;
     if (act) {
-        const size_t r = (size_t)m * 3 * D;
-        const float a = as[m];
-        const uint32_t i0 = h * hd + 2 * t;
-        float q0 = take_acc(acc, r + i0, a), q1 = take_acc(acc, r + i0 + 1, a);
-        k0 = take_acc(acc, r + D + i0, a); k1 = take_acc(acc, r + D + i0 + 1, a);
-        v0 = take_acc(acc, r + 2 * D + i0, a); v1 = take_acc(acc, r + 2 * D + i0 + 1, a);
-        const float c = rc[(size_t)pos * half + t], s = rs[(size_t)pos * half + t];
-        float qr0 = __builtin_fmaf(q0, c, -(q1 * s));
-        float qr1 = __builtin_fmaf(q0, s, q1 * c);
-        float kr0 = __builtin_fmaf(k0, c, -(k1 * s));
-        float kr1 = __builtin_fmaf(k0, s, k1 * c);
-        k0 = kr0; k1 = kr1;
-        size_t o = (size_t)m * D + i0;
-        q_out[o] = qr0; q_out[o + 1] = qr1;
-        k_out[o] = kr0; k_out[o + 1] = kr1;
-        v_out[o] = v0; v_out[o + 1] = v1;
+        const size_t o = (size_t)m * D + h * hd + 2 * t;
+        k0 = k[o]; k1 = k[o + 1];
+        v0 = v[o]; v1 = v[o + 1];
     }
     store_pair(g, kv, plane_index(g, row_seq(pd, m), layer, h), kv_store_row(g, pos), t, act, k0, k1, v0, v1);
 }
@@ -304,7 +287,7 @@ __global__ void k_wsum_combine_one(const float* __restrict__ Wp, uint32_t nch, u
 constexpr uint32_t att_vt(uint32_t vrow) { return 256 * vrow; }
 constexpr uint32_t att_smem(uint32_t vrow) { return att_vt(vrow) + (128 + 128 + 256 + 256 + 512 + 4) * 4; }
 
-template <int PARTS, uint32_t VROW = 144, bool COH = false>
+template <int PARTS, uint32_t VROW = 144>
 __device__ __forceinline__ void attn_one_row(const PassDesc* __restrict__ pd, const KvGeom& g, const KvPlanes& kv,
                                              uint32_t layer, uint32_t m, uint32_t h, uint32_t c,
                                              const float* __restrict__ q, const float* __restrict__ kself,
@@ -422,17 +405,11 @@ __device__ __forceinline__ void attn_one_row(const PassDesc* __restrict__ pd, co
         u = u + wp[128 + t];
         u = u + wp[256 + t];
         u = u + wp[384 + t];
-        if constexpr (COH) stc(&Up[(mh * cstride + c) * hd + t], u);
-        else Up[(mh * cstride + c) * hd + t] = u;
+        Up[(mh * cstride + c) * hd + t] = u;
     }
     if (t == 0) {
-        if constexpr (COH) {
-            stc(&S[mh * s_stride + 2 * c], mx);
-            stc(&S[mh * s_stride + 2 * c + 1], T);
-        } else {
-            S[mh * s_stride + 2 * c] = mx;
-            S[mh * s_stride + 2 * c + 1] = T;
-        }
+        S[mh * s_stride + 2 * c] = mx;
+        S[mh * s_stride + 2 * c + 1] = T;
     }
 }
 
@@ -501,10 +478,8 @@ __global__ __launch_bounds__(128) void k_attn_merge_chunks(const PassDesc* __res
 // maxima, f_c = exp(m_c - max), T and U fmaf chains over c in order,
 // out = U * (1 / (T + 1e-10))), then the row quantized.  NT threads;
 // element i = t + NT k; heads * chunks <= 2048 (checked when the engine is
-// created).  COH: S and Up are read with device-coherent loads (written by
-// other workgroups of the same kernel).  fs and ts hold 2048 floats each,
-// hmax and hinv 128, red 16.
-template <int PER, int NT, bool COH>
+// created).  fs and ts hold 2048 floats each, hmax and hinv 128, red 16.
+template <int PER, int NT>
 __device__ __forceinline__ void merge_quant_row(const PassDesc* __restrict__ pd, const KvGeom& g, uint32_t m,
                                                 const float* __restrict__ S, uint32_t s_stride,
                                                 const float* __restrict__ Up, uint32_t cstride,
@@ -517,13 +492,8 @@ __device__ __forceinline__ void merge_quant_row(const PassDesc* __restrict__ pd,
     const float* st = S + (size_t)m * H * s_stride;
     for (uint32_t i = t; i < H * nc; i += NT) {
         const uint32_t h = i / nc, c = i - h * nc;
-        if constexpr (COH) {
-            fs[i] = ldc(&st[(size_t)h * s_stride + 2 * c]);
-            ts[i] = ldc(&st[(size_t)h * s_stride + 2 * c + 1]);
-        } else {
-            fs[i] = st[(size_t)h * s_stride + 2 * c];
-            ts[i] = st[(size_t)h * s_stride + 2 * c + 1];
-        }
+        fs[i] = st[(size_t)h * s_stride + 2 * c];
+        ts[i] = st[(size_t)h * s_stride + 2 * c + 1];
     }
     __syncthreads();
     if (t < H) {
@@ -562,7 +532,7 @@ __device__ __forceinline__ void merge_quant_row(const PassDesc* __restrict__ pd,
 #pragma unroll
             for (uint32_t u = 0; u < 8; u++) {
                 const float* a = up[k] + (size_t)(c0 + u) * hd;
-                uc[k][u] = (in && u < nb) ? (COH ? ldc(a) : *a) : 0.0f;
+                uc[k][u] = (in && u < nb) ? *a : 0.0f;
             }
         }
 #pragma unroll
@@ -598,53 +568,8 @@ __global__ __launch_bounds__(1024) void k_attn_merge_quant(const PassDesc* __res
         return;
     }
     if (m >= pd->m) return;
-    merge_quant_row<PER, 1024, false>(pd, g, m, S, s_stride, Up, cstride, q, q_stride, as, bsum, bsum_stride, fs, ts,
+    merge_quant_row<PER, 1024>(pd, g, m, S, s_stride, Up, cstride, q, q_stride, as, bsum, bsum_stride, fs, ts,
                                       hmax, hinv, red);
-}
-
-// k_attn_chunk and k_attn_merge_quant in one kernel (passes of a few rows):
-// each (row, head, chunk) block stores its chunk results with coherent
-// stores, drains them and arrives on the row's counter; the block that
-// arrives last (heads x chunks arrivals) resets the counter and runs
-// merge_quant_row for that row.  No block waits for another.  Blocks past
-// `ablocks` prefetch pf (the O projection's weights).  cnt[m] is zero
-// between launches.
-template <int PARTS, uint32_t VROW, int PER>
-__global__ __launch_bounds__(256) void k_attn_chunk_mq(const PassDesc* __restrict__ pd, KvGeom g, KvPlanes kv,
-                                                       uint32_t layer, uint32_t M, uint32_t n_groups,
-                                                       uint32_t ablocks, const float* __restrict__ q,
-                                                       const float* __restrict__ kself,
-                                                       const float* __restrict__ vself, float* __restrict__ S,
-                                                       uint32_t s_stride, float* __restrict__ Up, uint32_t cstride,
-                                                       uint32_t* __restrict__ cnt, int8_t* __restrict__ qo,
-                                                       uint32_t q_stride, float* __restrict__ as,
-                                                       int32_t* __restrict__ bsum, uint32_t bsum_stride,
-                                                       Prefetch pf) {
-    static_assert(att_smem(VROW) >= (2048 + 2048 + 128 + 128 + 16) * 4, "merge scratch must fit the block's LDS");
-    __shared__ __align__(16) uint8_t smem[att_smem(VROW)];
-    __shared__ uint32_t last;
-    if (blockIdx.x >= ablocks) {
-        prefetch_bytes(pf.p, pf.n, blockIdx.x - ablocks, gridDim.x - ablocks, pf.sink);
-        return;
-    }
-    const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
-    const uint32_t grp = (slot / M) * 8u + xcd, m = slot % M;
-    if (grp >= n_groups || m >= pd->m) return;
-    const uint32_t H = g.n_heads, h = grp % H, c = grp / H;
-    const uint32_t nc = (kv_view(g, row_pos(pd, m)).count() + 1 + 255) / 256;
-    if (c >= nc) return;   // attn_one_row writes nothing for such a chunk
-    attn_one_row<PARTS, VROW, true>(pd, g, kv, layer, m, h, c, q, kself, vself, S, s_stride, Up, cstride, smem);
-    drain();
-    if (threadIdx.x == 0) {
-        const uint32_t before = arrive_n(&cnt[m], 1u);
-        last = before + 1u == H * nc ? 1u : 0u;
-        if (last) stc(&cnt[m], 0u);
-    }
-    __syncthreads();
-    if (!last) return;
-    float* fs = reinterpret_cast<float*>(smem);
-    merge_quant_row<PER, 256, true>(pd, g, m, S, s_stride, Up, cstride, qo, q_stride, as, bsum, bsum_stride, fs,
-                                    fs + 2048, fs + 4096, fs + 4224, fs + 4352);
 }
 
 }  // namespace pf

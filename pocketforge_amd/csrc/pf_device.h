@@ -69,18 +69,47 @@ __device__ __forceinline__ float uniform(uint64_t seed, uint64_t idx) {
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, PF_WAVE); }
 __device__ __forceinline__ double shfl_xor(double v, int m) { return __shfl_xor(v, m, PF_WAVE); }
 
-// Halving tree over the 64 lanes of a wave: after the butterfly every lane
-// holds ((P0+P32)+(P16+P48)) ... in the order offsets 32,16,8,4,2,1.
-__device__ __forceinline__ float wave_tree_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = v + shfl_xor(v, off);
+// Value of lane (lane & ~15) | ((lane & 15) - n) mod 16 (DPP row_ror:n), or a
+// quad permutation (DPP quad_perm), without the LDS path.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+constexpr int DPP_ROR4 = 0x124, DPP_ROR8 = 0x128, DPP_ROR12 = 0x12C, DPP_XOR2 = 0x4E, DPP_XOR1 = 0xB1;
+
+// The butterfly steps of offsets 8, 4, 2, 1 inside each row of 16 lanes:
+// lane i adds the value of lane i ^ off (row_ror:8 is xor 8; xor 4 takes
+// row_ror:4 or row_ror:12 by bit 2 of the lane).
+__device__ __forceinline__ float row16_tree_sum(float v) {
+    v = v + dpp_mov<DPP_ROR8>(v);
+    const float a = v + dpp_mov<DPP_ROR4>(v), b = v + dpp_mov<DPP_ROR12>(v);
+    v = (threadIdx.x & 4u) ? a : b;
+    v = v + dpp_mov<DPP_XOR2>(v);
+    v = v + dpp_mov<DPP_XOR1>(v);
+    return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_mov<DPP_ROR8>(v));
+    v = fmaxf(v, dpp_mov<DPP_ROR4>(v));
+    v = fmaxf(v, dpp_mov<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_mov<DPP_XOR1>(v));
     return v;
 }
 
+// Halving tree over the 64 lanes of a wave: after the butterfly every lane
+// holds ((P0+P32)+(P16+P48)) ... in the order offsets 32,16,8,4,2,1 (the
+// offsets below 16 stay inside a row of 16 lanes and use DPP; additions are
+// commutative, so every lane's sum has the same bits).
+__device__ __forceinline__ float wave_tree_sum(float v) {
+    v = v + shfl_xor(v, 32);
+    v = v + shfl_xor(v, 16);
+    return row16_tree_sum(v);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, shfl_xor(v, off));
-    return v;
+    v = fmaxf(v, shfl_xor(v, 32));
+    v = fmaxf(v, shfl_xor(v, 16));
+    return row16_max(v);
 }
 
 // Canonical sum over a block of W waves where each thread has already
@@ -202,29 +231,6 @@ __device__ __forceinline__ void prefetch_bytes(const uint8_t* __restrict__ p, si
     }
     for (; i < n16; i += stride) x ^= q[i].x;
     if (x == 0x7A5C3E1Fu) sink[0] = x;
-}
-
-// ------------------------------------------------------------ coherence
-
-// Hand-offs between workgroups of one kernel: agent-scope relaxed atomic
-// loads and stores reach the device-coherent level (the L2s of the XCDs are
-// not coherent with each other), drain() completes them before an arrival.
-
-template <class T>
-__device__ __forceinline__ T ldc(const T* p) {
-    return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <class T>
-__device__ __forceinline__ void stc(T* p, T v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t arrive_n(uint32_t* c, uint32_t n) {
-    return __hip_atomic_fetch_add(c, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Every wave's memory operations complete, then the workgroup barrier.
-__device__ __forceinline__ void drain() {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
 }
 
 struct Prefetch {

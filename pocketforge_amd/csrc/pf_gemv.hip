@@ -1,303 +1,14 @@
-// GEMV / GEMM kernels for gfx950.
+// fp32-activation GEMV and the row kernels of the gfx950 path.
 //
-//  * k_gemv_i8     int8 activations x block-quantized (Q4/Q2/Q1.5, 32-wide
-//                  blocks, fp16 scale) tiled matrix, M <= 8 activation rows.
-//                  One lane per output row, wave-uniform activations in
-//                  SGPRs, v_dot4 int32 block dots, exact fp64 accumulation of
-//                  d_b * p_b, fp32 output.  HBM bound: every weight byte is
-//                  read once.
 //  * k_gemv_f32    fp32 activations x dequantized Q4 row-major matrix (tied
 //                  unembedding, MTP heads) in the canonical 64-lane order.
-//  * row prologues quantize_activation_row, residual + RMSNorm + quantize,
-//                  SwiGLU + quantize, all producing int8 rows, the row scale
-//                  and per-32-block sums of the codes.
+//  * row kernels   quantize_activation_row of whole rows, layer-skip
+//                  decisions and cache commits, embedding, small copies.
 //  * k_matmul_int8 / k_mm_epilogue: the reference's plain int8 matmul API.
+// The int8-activation x block-quantized products are in pf_mm.hip.
 #include "pf_device.h"
 
 namespace pf {
-
-// ===================================================== int8 x block GEMV
-
-template <int FMT>
-__device__ __forceinline__ void unpack_codes(const uint8_t* tile, uint32_t t, uint32_t lane,
-                                             uint32_t u[8]) {
-    if constexpr (FMT == FMT_Q4) {
-        uint4 c = *reinterpret_cast<const uint4*>(tile + t * 1024u + lane * 16u);
-        const uint32_t m = 0x0F0F0F0Fu;
-        u[0] = c.x & m; u[1] = c.y & m; u[2] = c.z & m; u[3] = c.w & m;
-        u[4] = (c.x >> 4) & m; u[5] = (c.y >> 4) & m; u[6] = (c.z >> 4) & m; u[7] = (c.w >> 4) & m;
-    } else {
-        uint2 c = *reinterpret_cast<const uint2*>(tile + (t >> 1) * 1024u + lane * 16u + (t & 1u) * 8u);
-        const uint32_t m = 0x03030303u;
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-            u[2 * p] = (c.x >> (2 * p)) & m;
-            u[2 * p + 1] = (c.y >> (2 * p)) & m;
-        }
-    }
-}
-
-// acc[m][n] += S_split with S = sum_b d_b * p_b over the blocks of one
-// K split, p_b = sum_i a[m][32b+i] * code[n][32b+i] (int32).  Every term
-// d_b * p_b is an integer multiple of the smallest block-scale ulp of the
-// row and the row's scales span at most 15 binades (checked at upload), so
-// all partial sums are exact in fp64: the splits meet through fp64 atomic
-// adds in any order with a bit-identical result.  The consumer converts
-// (float)(acc * (double)a_scale) and clears acc.
-// Grid (N/64, splits), 64 WAVES threads; wave w of split s covers blocks
-// [(WAVES s+w)*bpw, (WAVES s+w+1)*bpw), bpw in {1, 2, 4} with
-// nb % (WAVES bpw) == 0, lane = output row.  The waves of a workgroup meet in
-// LDS, so larger workgroups mean fewer K splits and fewer fp64 atomics for
-// the same number of waves.  Each wave issues all its weight loads first; the
-// workgroup's activation rows and block sums are staged in LDS with one
-// vector load per thread (they come from another kernel, often through
-// another XCD's L2).
-template <int FMT, int M, bool GATED = false, int WAVES = 4>
-__global__ __launch_bounds__(64 * WAVES) void k_gemv_i8(const uint8_t* __restrict__ W, uint32_t K,
-                                                 const int8_t* __restrict__ act, uint32_t act_stride,
-                                                 const int32_t* __restrict__ bsum, uint32_t bsum_stride,
-                                                 uint32_t bpw, double* __restrict__ acc, uint32_t acc_stride,
-                                                 const uint32_t* __restrict__ gate) {
-    constexpr uint32_t TB = tile_bytes(FMT);
-    constexpr uint32_t CODES = TILE_ROWS * TILE_BLOCKS * code_bytes(FMT);
-    constexpr int OFF = code_offset(FMT);
-    if constexpr (GATED)
-        if (*gate == 0u) return;   // no row of the pass needs this product
-    constexpr uint32_t NT = 64u * WAVES;
-    __shared__ __align__(16) int32_t sa[M][WAVES * 4 * 8];  // activations of the workgroup's WAVES bpw blocks
-    __shared__ int32_t sb[M][WAVES * 4];
-    __shared__ double red[WAVES][M][64];
-    const uint32_t g = blockIdx.x, s = blockIdx.y;
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t chunks = K >> 8, wb = WAVES * bpw, wb0 = s * wb, b0 = wb0 + wid * bpw;
-    const uint8_t* tiles = W + (size_t)g * chunks * TB;
-    uint32_t u[4][8];
-    uint16_t dh[4];        // scale bits: converted after the staging below, so that no
-                           // conversion waits on a load before every load is issued
-#pragma unroll
-    for (uint32_t k = 0; k < 4; k++) {
-        dh[k] = 0;
-#pragma unroll
-        for (int q = 0; q < 8; q++) u[k][q] = 0u;
-        if (k < bpw) {
-            const uint32_t b = b0 + k;
-            const uint8_t* tile = tiles + (size_t)(b >> 3) * TB;
-            unpack_codes<FMT>(tile, b & 7u, lane, u[k]);
-            dh[k] = *reinterpret_cast<const uint16_t*>(tile + CODES + lane * 16u + (b & 7u) * 2u);
-        }
-    }
-    for (uint32_t i = threadIdx.x; i < (uint32_t)M * wb * 8u; i += NT) {
-        const uint32_t m = i / (wb * 8u), r = i - m * wb * 8u;
-        sa[m][r] = reinterpret_cast<const int32_t*>(act + (size_t)m * act_stride)[wb0 * 8u + r];
-    }
-    if (threadIdx.x < (uint32_t)M * wb) {
-        const uint32_t m = threadIdx.x / wb, k = threadIdx.x - m * wb;
-        sb[m][k] = bsum[(size_t)m * bsum_stride + wb0 + k];
-    }
-    __syncthreads();
-    double d[4];
-#pragma unroll
-    for (uint32_t k = 0; k < 4; k++) d[k] = (double)h2f(dh[k]);
-    double S[M];
-#pragma unroll
-    for (int m = 0; m < M; m++) S[m] = 0.0;
-#pragma unroll
-    for (uint32_t k = 0; k < 4; k++) {
-        if (k < bpw) {
-            const uint32_t j = wid * bpw + k;
-#pragma unroll
-            for (int m = 0; m < M; m++) {
-                const int4 a0 = *reinterpret_cast<const int4*>(&sa[m][j * 8u]);
-                const int4 a1 = *reinterpret_cast<const int4*>(&sa[m][j * 8u + 4u]);
-                int p = -OFF * sb[m][j];
-                p = __builtin_amdgcn_sdot4((int)u[k][0], a0.x, p, false);
-                p = __builtin_amdgcn_sdot4((int)u[k][1], a0.y, p, false);
-                p = __builtin_amdgcn_sdot4((int)u[k][2], a0.z, p, false);
-                p = __builtin_amdgcn_sdot4((int)u[k][3], a0.w, p, false);
-                p = __builtin_amdgcn_sdot4((int)u[k][4], a1.x, p, false);
-                p = __builtin_amdgcn_sdot4((int)u[k][5], a1.y, p, false);
-                p = __builtin_amdgcn_sdot4((int)u[k][6], a1.z, p, false);
-                p = __builtin_amdgcn_sdot4((int)u[k][7], a1.w, p, false);
-                S[m] = __builtin_fma(d[k], (double)p, S[m]);
-            }
-        }
-    }
-#pragma unroll
-    for (int m = 0; m < M; m++) red[wid][m][lane] = S[m];
-    __syncthreads();
-    for (uint32_t t = threadIdx.x; t < (uint32_t)M * 64u; t += NT) {
-        const uint32_t m = t >> 6, r = t & 63u;
-        double v = red[0][m][r];
-#pragma unroll
-        for (int w = 1; w < WAVES; w++) v += red[w][m][r];
-        atomicAdd(acc + (size_t)m * acc_stride + (size_t)g * 64u + r, v);
-    }
-}
-
-// ===================================================== int8 x block GEMM
-
-typedef int pf_v4i __attribute__((ext_vector_type(4)));
-typedef int pf_v16i __attribute__((ext_vector_type(16)));
-
-// Signed codes of the 16 elements 16h .. 16h + 15 of weight row r, block t,
-// of a tile, packed 4 per dword in element order (MFMA B operand).  Byte
-// x - OFF is formed as (x + (0x80 - OFF)) ^ 0x80 per byte (no carries: every
-// byte sum is below 0x100).
-// Raw code bytes of weight row r, block t (Q4: 16 bytes; Q2/Q1.5: 8 bytes in
-// .x, .y), loaded one block ahead of their use.
-template <int FMT>
-__device__ __forceinline__ uint4 gemm_raw(const uint8_t* tile, uint32_t t, uint32_t r) {
-    if constexpr (FMT == FMT_Q4) return *reinterpret_cast<const uint4*>(tile + t * 1024u + r * 16u);
-    const uint2 c = *reinterpret_cast<const uint2*>(tile + (t >> 1) * 1024u + r * 16u + (t & 1u) * 8u);
-    return make_uint4(c.x, c.y, 0u, 0u);
-}
-
-template <int FMT>
-__device__ __forceinline__ pf_v4i gemm_unpack(uint4 c, uint32_t h) {
-    constexpr uint32_t OFF = (uint32_t)code_offset(FMT);
-    constexpr uint32_t ADD = (0x80u - OFF) * 0x01010101u;
-    pf_v4i v;
-    if constexpr (FMT == FMT_Q4) {
-        const uint32_t sh = 4u * h, m = 0x0F0F0F0Fu;
-        v.x = (int)((((c.x >> sh) & m) + ADD) ^ 0x80808080u);
-        v.y = (int)((((c.y >> sh) & m) + ADD) ^ 0x80808080u);
-        v.z = (int)((((c.z >> sh) & m) + ADD) ^ 0x80808080u);
-        v.w = (int)((((c.w >> sh) & m) + ADD) ^ 0x80808080u);
-    } else {
-        const uint32_t sh = 4u * h, m = 0x03030303u;
-        v.x = (int)((((c.x >> sh) & m) + ADD) ^ 0x80808080u);
-        v.y = (int)((((c.y >> sh) & m) + ADD) ^ 0x80808080u);
-        v.z = (int)((((c.x >> (sh + 2u)) & m) + ADD) ^ 0x80808080u);
-        v.w = (int)((((c.y >> (sh + 2u)) & m) + ADD) ^ 0x80808080u);
-    }
-    return v;
-}
-
-template <int FMT>
-__device__ __forceinline__ pf_v4i gemm_codes(const uint8_t* tile, uint32_t t, uint32_t r, uint32_t h) {
-    constexpr uint32_t OFF = (uint32_t)code_offset(FMT);
-    constexpr uint32_t ADD = (0x80u - OFF) * 0x01010101u;
-    pf_v4i v;
-    if constexpr (FMT == FMT_Q4) {
-        const uint4 c = *reinterpret_cast<const uint4*>(tile + t * 1024u + r * 16u);
-        const uint32_t sh = 4u * h, m = 0x0F0F0F0Fu;
-        v.x = (int)((((c.x >> sh) & m) + ADD) ^ 0x80808080u);
-        v.y = (int)((((c.y >> sh) & m) + ADD) ^ 0x80808080u);
-        v.z = (int)((((c.z >> sh) & m) + ADD) ^ 0x80808080u);
-        v.w = (int)((((c.w >> sh) & m) + ADD) ^ 0x80808080u);
-    } else {
-        const uint2 c = *reinterpret_cast<const uint2*>(tile + (t >> 1) * 1024u + r * 16u + (t & 1u) * 8u);
-        const uint32_t sh = 4u * h, m = 0x03030303u;
-        v.x = (int)((((c.x >> sh) & m) + ADD) ^ 0x80808080u);
-        v.y = (int)((((c.y >> sh) & m) + ADD) ^ 0x80808080u);
-        v.z = (int)((((c.x >> (sh + 2u)) & m) + ADD) ^ 0x80808080u);
-        v.w = (int)((((c.y >> (sh + 2u)) & m) + ADD) ^ 0x80808080u);
-    }
-    return v;
-}
-
-// acc[m][n] += sum over the blocks [s bps, (s + 1) bps) of d[n][b] * p[m][n][b]
-// for M activation rows (M > 8: verify passes of many sequences, batched
-// prefill), the exact fp64 sum of k_gemv_i8.  p comes from
-// v_mfma_i32_32x32x32_i8, one 32-element block per instruction: lane l
-// holds activation row l % 32 and weight row l % 32, elements 16 (l / 32)
-// .. + 15; result element i is activation row 8 (i / 4) + 4 (l / 32) + i % 4,
-// weight row l % 32, so a lane needs one block scale per block.
-// Grid (N / 32, splits), 256 threads: the block's 32 weight rows
-// [32 blockIdx.x, + 32) against activation tiles w, w + 4, ... (MTW per
-// wave) of 32 rows each; act holds ceil(M / 32) * 32 readable rows.
-template <int FMT, int MTW, bool GATED = false>
-__global__ __launch_bounds__(256) void k_gemm_i8(const uint8_t* __restrict__ W, uint32_t K, uint32_t M,
-                                                 const int8_t* __restrict__ act, uint32_t act_stride, uint32_t bps,
-                                                 double* __restrict__ acc, uint32_t acc_stride,
-                                                 const uint32_t* __restrict__ gate) {
-    constexpr uint32_t TB = tile_bytes(FMT);
-    constexpr uint32_t CODES = TILE_ROWS * TILE_BLOCKS * code_bytes(FMT);
-    if constexpr (GATED)
-        if (*gate == 0u) return;   // no row of the pass needs this product
-    const uint32_t lane = threadIdx.x & 63u, h = lane >> 5, l32 = lane & 31u;
-    const uint32_t wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t n0 = blockIdx.x * 32u, r = (n0 & 63u) + l32;
-    const uint32_t nb = K >> 5, chunks = K >> 8, mtiles = (M + 31u) / 32u;
-    const uint32_t b_begin = blockIdx.y * bps, b_end = min(b_begin + bps, nb);
-    const uint8_t* tiles = W + (size_t)(n0 >> 6) * chunks * TB;
-    double S[MTW][16];
-#pragma unroll
-    for (int j = 0; j < MTW; j++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) S[j][i] = 0.0;
-    const pf_v16i zero = {};
-    // raw operands of block b: code bytes, block scale bits, activation tiles
-    auto load = [&](uint32_t b, uint4& bw, uint16_t& d, pf_v4i (&a)[MTW]) {
-        const uint8_t* tile = tiles + (size_t)(b >> 3) * TB;
-        const uint32_t t = b & 7u;
-        bw = gemm_raw<FMT>(tile, t, r);
-        d = *reinterpret_cast<const uint16_t*>(tile + CODES + r * 16u + t * 2u);
-        // every tile loads (a wave's tiles past the last one reload it, unused),
-        // so the number of loads in flight is fixed and the waits are exact
-#pragma unroll
-        for (int j = 0; j < MTW; j++) {
-            const uint32_t mt = min(wid + 4u * j, mtiles - 1u);
-            a[j] = *reinterpret_cast<const pf_v4i*>(act + (size_t)(mt * 32u + l32) * act_stride + b * 32u + 16u * h);
-        }
-    };
-    // the next block's operands load while this block's MFMAs and scaling run
-    uint4 bw_n{};
-    uint16_t d_n = 0;
-    pf_v4i a_n[MTW];
-    if (b_begin < b_end) load(b_begin, bw_n, d_n, a_n);
-    for (uint32_t b = b_begin; b < b_end; b++) {
-        const pf_v4i bw = gemm_unpack<FMT>(bw_n, h);
-        const double d = (double)h2f(d_n);
-        pf_v4i a[MTW];
-#pragma unroll
-        for (int j = 0; j < MTW; j++) a[j] = a_n[j];
-        load(min(b + 1, b_end - 1), bw_n, d_n, a_n);      // unconditional: exact wait counts
-        pf_v16i p[MTW];
-#pragma unroll
-        for (int j = 0; j < MTW; j++)
-            if (wid + 4u * j < mtiles) p[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], bw, zero, 0, 0, 0);
-#pragma unroll
-        for (int j = 0; j < MTW; j++) {
-            if (wid + 4u * j < mtiles) {
-#pragma unroll
-                for (int i = 0; i < 16; i++) S[j][i] = __builtin_fma(d, (double)p[j][i], S[j][i]);
-            }
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < MTW; j++) {
-        const uint32_t mt = wid + 4u * j;
-        if (mt >= mtiles) continue;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const uint32_t m = mt * 32u + 8u * (i / 4) + 4u * h + (i % 4);
-            if (m < M) atomicAdd(acc + (size_t)m * acc_stride + n0 + l32, S[j][i]);
-        }
-    }
-}
-
-// y = (float)(acc * (double)as[m]); acc cleared for its next use.
-__device__ __forceinline__ float take_acc(double* acc, size_t i, float as) {
-    const double v = acc[i];
-    acc[i] = 0.0;
-    return (float)(v * (double)as);
-}
-
-// Finishes a GEMV for the kernel-level entry point.
-__global__ void k_gemv_finish(double* __restrict__ acc, uint32_t N, const float* __restrict__ as,
-                              float* __restrict__ y) {
-    const uint32_t n = blockIdx.x * blockDim.x + threadIdx.x, m = blockIdx.y;
-    if (n >= N) return;
-    y[(size_t)m * N + n] = take_acc(acc, (size_t)m * N + n, as[m]);
-}
-
-// acc[0..n) = 0 (one-time set-up of accumulators; a kernel, not a memset).
-__global__ void k_zero_f64(double* __restrict__ p, size_t n) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0.0;
-}
 
 // ============================================ fp32 x dequantized Q4 GEMV
 
@@ -472,104 +183,6 @@ __global__ __launch_bounds__(256) void k_quant_rows(const float* __restrict__ x,
                                  bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
 }
 
-// x[m] += (float)(acc[m] * as_prev[m]) (when acc != null; acc cleared),
-// then the engine's RMSNorm (src/matmul_neon.cpp:231-239) with weight w in
-// tile-canonical order (the sum of squares is the sequential sum over
-// 64-element tiles of each tile's halving tree of x * x; normed = (x * w) *
-// inv), then quantize_activation_row of the normed row.  Grid M, 1024
-// threads: all loads are issued first; wave w builds the trees of tiles w,
-// w + 16, ... from the row in LDS (K <= 4096, K % 64 == 0).
-// Blocks past the `rows` row blocks prefetch pf (the weights of the GEMV that
-// consumes the output).  SKIP instances (layer skip on): with skipm, rows
-// whose flag is set take no residual
-// (their FFN was skipped; acc is still cleared); with nout, the normed rows
-// are also written there in fp32; with nclear, block 0 zeroes that word
-// (the count of rows that run the layer's FFN, built by k_layer_skip).
-template <int PER, bool SKIP = false>
-__global__ __launch_bounds__(1024) void k_resid_norm_quant(float* __restrict__ x, uint32_t K,
-                                                           double* __restrict__ acc,
-                                                           const float* __restrict__ as_prev,
-                                                           const float* __restrict__ w,
-                                                           int8_t* __restrict__ q, uint32_t q_stride,
-                                                           float* __restrict__ as, int32_t* __restrict__ bsum,
-                                                           uint32_t bsum_stride, uint32_t rows, Prefetch pf,
-                                                           const uint32_t* __restrict__ skipm,
-                                                           float* __restrict__ nout, uint32_t* __restrict__ nclear) {
-    __shared__ float row[4096];
-    __shared__ float tree[64];
-    __shared__ float red[16];
-    const uint32_t m = blockIdx.x, t = threadIdx.x;
-    if constexpr (SKIP)
-        if (nclear && m == 0 && t == 0) *nclear = 0u;
-    if (m >= rows) {
-        prefetch_bytes(pf.p, pf.n, m - rows, gridDim.x - rows, pf.sink);
-        return;
-    }
-    float xv[PER], wv[PER];
-    double av[PER];
-#pragma unroll
-    for (int k = 0; k < PER; k++) {
-        const uint32_t i = t + 1024u * k;
-        xv[k] = i < K ? x[(size_t)m * K + i] : 0.0f;
-        wv[k] = i < K ? w[i] : 0.0f;
-        av[k] = (acc && i < K) ? acc[(size_t)m * K + i] : 0.0;
-    }
-    const float ap = acc ? as_prev[m] : 0.0f;
-    bool add = acc != nullptr;
-    if constexpr (SKIP) add = add && !(skipm && skipm[m]);
-#pragma unroll
-    for (int k = 0; k < PER; k++) {
-        const uint32_t i = t + 1024u * k;
-        if (acc && i < K) {
-            if (add) {
-                xv[k] = xv[k] + (float)(av[k] * (double)ap);
-                x[(size_t)m * K + i] = xv[k];
-            }
-            acc[(size_t)m * K + i] = 0.0;
-        }
-        if (i < K) row[i] = xv[k];
-    }
-    __syncthreads();
-    // tile trees of x * x, then their sequential sum
-    const uint32_t wid = t >> 6, lane = t & 63u;
-    for (uint32_t tl = wid; tl < K / 64u; tl += 16u) {
-        const float v = row[64u * tl + lane];
-        const float s = wave_tree_sum(v * v);
-        if (lane == 0) tree[tl] = s;
-    }
-    __syncthreads();
-    if (t == 0) {
-        // sequential sum of the tile trees, 16 LDS reads in flight at a time
-        float ss = 0.0f;
-        for (uint32_t t0 = 0; t0 < K / 64u; t0 += 16) {
-            float tv[16];
-#pragma unroll
-            for (int k = 0; k < 16; k++) tv[k] = tree[min(t0 + k, 63u)];
-#pragma unroll
-            for (int k = 0; k < 16; k++)
-                if (t0 + k < K / 64u) ss = ss + tv[k];
-        }
-        red[0] = ss;
-    }
-    __syncthreads();
-    const float ss = red[0];
-    __syncthreads();
-    const float rms = __builtin_sqrtf(ss / (float)K + 1e-6f);
-    const float inv = 1.0f / rms;
-#pragma unroll
-    for (int k = 0; k < PER; k++) xv[k] = (xv[k] * wv[k]) * inv;
-    if (SKIP && nout) {
-#pragma unroll
-        for (int k = 0; k < PER; k++) {
-            const uint32_t i = t + 1024u * k;
-            if (i < K) nout[(size_t)m * K + i] = xv[k];
-        }
-    }
-    __syncthreads();
-    quantize_row_block<PER, 1024>(xv, K, q + (size_t)m * q_stride, as + m,
-                                  bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
-}
-
 // quantize_activation_row of rows of length K <= 1024 * PER, 1024 threads.
 template <int PER>
 __global__ __launch_bounds__(1024) void k_quant_rows_wide(const float* __restrict__ x, uint32_t K,
@@ -586,16 +199,6 @@ __global__ __launch_bounds__(1024) void k_quant_rows_wide(const float* __restric
     }
     quantize_row_block<PER, 1024>(v, K, q + (size_t)m * q_stride, as + m,
                                   bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
-}
-
-// x[m] += (float)(acc[m] * as_prev[m]) (the last layer's down residual;
-// none for rows flagged in skipm, whose acc is still cleared).
-__global__ void k_resid_add(float* __restrict__ x, uint32_t K, double* __restrict__ acc,
-                            const float* __restrict__ as_prev, const uint32_t* __restrict__ skipm) {
-    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x, m = blockIdx.y;
-    if (i >= K) return;
-    const float r = take_acc(acc, (size_t)m * K + i, as_prev[m]);
-    if (!(skipm && skipm[m])) x[(size_t)m * K + i] = x[(size_t)m * K + i] + r;
 }
 
 // LayerSkipController::should_skip_ffn (src/layer_skip.cpp:22-67) at one
@@ -683,48 +286,6 @@ __global__ __launch_bounds__(256) void k_skip_commit(const PassDesc* __restrict_
     const float* a = stage + ((size_t)l * rows + (uint32_t)src) * K;
     float* c = cache + ((size_t)s * L + l) * K;
     for (uint32_t i = threadIdx.x; i < K; i += 256) c[i] = a[i];
-}
-
-// SwiGLU of src/engine.cpp:832-838 on the fused gate|up GEMV accumulators
-// (row m: [0,ff) = gate, [ff, 2ff) = up; cleared), then
-// quantize_activation_row of the result.  Grid M, 1024 threads.
-template <int PER>
-__global__ __launch_bounds__(1024) void k_swiglu_quant(double* __restrict__ acc, const float* __restrict__ as_in,
-                                                       uint32_t ff,
-                                                       int8_t* __restrict__ q, uint32_t q_stride,
-                                                       float* __restrict__ as, int32_t* __restrict__ bsum,
-                                                       uint32_t bsum_stride, uint32_t rows, Prefetch pf) {
-    __shared__ float red[16];
-    const uint32_t m = blockIdx.x;
-    if (m >= rows) {
-        prefetch_bytes(pf.p, pf.n, m - rows, gridDim.x - rows, pf.sink);
-        return;
-    }
-    double ga[PER], ua[PER];
-#pragma unroll
-    for (int k = 0; k < PER; k++) {
-        const uint32_t i = threadIdx.x + 1024u * k;
-        ga[k] = i < ff ? acc[(size_t)m * 2 * ff + i] : 0.0;
-        ua[k] = i < ff ? acc[(size_t)m * 2 * ff + ff + i] : 0.0;
-    }
-    const double a = (double)as_in[m];
-    float v[PER];
-#pragma unroll
-    for (int k = 0; k < PER; k++) {
-        const uint32_t i = threadIdx.x + 1024u * k;
-        float f = 0.0f;
-        if (i < ff) {
-            acc[(size_t)m * 2 * ff + i] = 0.0;
-            acc[(size_t)m * 2 * ff + ff + i] = 0.0;
-            const float gt = (float)(ga[k] * a);
-            const float u = (float)(ua[k] * a);
-            const float sig = 1.0f / (1.0f + expf_c(-gt));
-            f = gt * sig * u;
-        }
-        v[k] = f;
-    }
-    quantize_row_block<PER, 1024>(v, ff, q + (size_t)m * q_stride, as + m,
-                                  bsum ? bsum + (size_t)m * bsum_stride : nullptr, red);
 }
 
 // dst = src (float), used instead of a copy node inside captured passes.

@@ -7,25 +7,25 @@ namespace pf {
 // ---------------------------------------------------------- weight formats
 enum Fmt : int32_t { FMT_Q4 = 0, FMT_Q2 = 1, FMT_Q15 = 2 };
 
-// Int8-activation GEMV matrices are stored in tiles of 64 output rows x 8
-// blocks (256 input columns).  Inside a tile, for block t the 64 rows' code
-// bytes are contiguous (one coalesced 1 KiB wave load per block for Q4, per
-// block pair for Q2/Q1.5), followed by the 64 rows' eight fp16 scales
-// (16 B per row).  Tiles are ordered row-group major: tile (g, c) is at
-// (g * chunks + c) * tile_bytes.
-//
-// Element order inside a block (device order, not the interchange order):
-//   Q4   : byte j, low nibble = element j, high nibble = element j + 16.
-//   Q2/Q15: dword w (0,1), bit plane t (bits 2t..2t+1 of each byte), byte jj
-//          holds element 8t + 4w + jj.
+// Int8-activation matrices (fused QKV, O, fused gate|up, down) are stored
+// in tiles of 32 output rows x 256 input columns (8 blocks of 32), the
+// operand layout of v_mfma_i32_32x32x32_i8: lane l = r + 32 h of a wave
+// feeds weight row r, elements 16 h .. 16 h + 15 of a block.  Tile (g, c)
+// (row group g, column chunk c) is at (g * K / 256 + c) * tile_bytes and
+// holds the codes as 1 KiB sets (lane l's 16 bytes at l * 16) followed by
+// the 32 rows' fp16 block scales (row r's eight at codes + 16 r).
+//   Q4    : 4 sets; set s covers blocks 2s and 2s + 1, 8 bytes each, where
+//           byte j holds element 16h + j (low nibble) and 16h + j + 8 (high).
+//   Q2/Q15: 2 sets; set s covers blocks 4s .. 4s + 3, one dword each, where
+//           bits 2u, 2u + 1 of byte j hold element 16h + 4u + j.
 // Code values: Q4 = nibble - 8, Q2 = code - 2, Q1.5 = code - 1 (code 3 is
-// rejected at upload).
-constexpr int TILE_ROWS = 64;
-constexpr int TILE_BLOCKS = 8;
+// rejected at upload).  The fused gate|up matrix interleaves its halves by
+// 16 rows: group g holds gate rows 16g .. 16g + 15, then up rows 16g ..
+// 16g + 15, so the SwiGLU pairs meet in one group.
+constexpr int GROUP_ROWS = 32;
 __host__ __device__ constexpr uint32_t code_bytes(int fmt) { return fmt == FMT_Q4 ? 16u : 8u; }
-__host__ __device__ constexpr uint32_t tile_bytes(int fmt) {
-    return (uint32_t)TILE_ROWS * TILE_BLOCKS * code_bytes(fmt) + (uint32_t)TILE_ROWS * TILE_BLOCKS * 2u;
-}
+__host__ __device__ constexpr uint32_t g32_code_bytes(int fmt) { return fmt == FMT_Q4 ? 4096u : 2048u; }
+__host__ __device__ constexpr uint32_t g32_tile_bytes(int fmt) { return g32_code_bytes(fmt) + 512u; }
 __host__ __device__ constexpr int code_offset(int fmt) { return fmt == FMT_Q4 ? 8 : (fmt == FMT_Q2 ? 2 : 1); }
 
 // fp32-activation GEMV matrices (tied embedding / unembedding, MTP heads)

@@ -1,0 +1,585 @@
+// Int8-activation x block-quantized matrix products for gfx950, on the
+// 32-row group layout of pf_layout.h.
+//
+//  * k_gemv  M <= 8 activation rows (decode passes).  One workgroup owns a
+//            32-row group and all of K: its waves split the 256-column chunks
+//            and meet in LDS, so every output is final inside the workgroup
+//            and no partial sum leaves it.  The workgroup quantizes its own
+//            copy of the activation rows first (prologue: RMSNorm + quantize,
+//            or quantize, or a copy of rows quantized elsewhere) while its
+//            weight loads are in flight, and applies the consumer's step to
+//            the outputs (epilogue: store, residual add, RoPE + Q/K/V split,
+//            SwiGLU of interleaved gate/up rows).
+//  * k_gemm  M > 8 rows (prompt passes, many-sequence verify): the same
+//            exact arithmetic over 32-row activation tiles quantized by the
+//            row kernels, with the same epilogues.
+//
+// Arithmetic: v_mfma_i32_32x32x32_i8 gives the exact int32 dot p of one
+// 32-element block of an activation row and a weight row; the output is
+// y = (float)(a_s * sum_b d_b * p_b) with the sum exact in fp64 (every term is
+// a multiple of the smallest block-scale ulp of the row and the row's scales
+// span at most 15 binades, checked at upload), so any association order
+// gives the same bits.  The activation quantization and RMSNorm follow
+// src/matmul_neon.cpp:16-29 and :231-239 in the canonical orders of
+// pf_gemv.hip.
+#include "pf_device.h"
+
+namespace pf {
+
+typedef int pf_v4i __attribute__((ext_vector_type(4)));
+typedef int pf_v16i __attribute__((ext_vector_type(16)));
+
+enum Pro : int { PRO_NORM = 0, PRO_QUANT = 1, PRO_INT8 = 2, PRO_QPART = 3 };
+enum Epi : int { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_SWIGLU = 3 };
+
+// Consumer step applied to the outputs.  Row n is a device row (pf_layout.h).
+struct MmEpi {
+    float* y;                  // STORE: y[m][logical n]; RESID: y[m][n] += ; SWIGLU: y[m][j]
+    uint32_t y_stride;
+    uint32_t ilv;              // STORE: the matrix holds two halves interleaved by 16 rows
+    const uint32_t* skipm;     // RESID: rows m with skipm[m] != 0 take no residual (layer skip)
+    float *q, *k, *v;          // QKV: [rows][D] each
+    const float *rc, *rs;      // QKV: RoPE cos/sin [position][head_dim / 2]
+    const PassDesc* pd;        // QKV: positions of the pass rows
+    uint32_t D, hd;
+    float* pmax;               // SWIGLU (GEMV): per-workgroup row maxima of |output| [M][N / 32], or null
+};
+
+// Logical row of device row n of a matrix whose halves [0, N/2) and
+// [N/2, N) are interleaved by 16 rows.
+__device__ __forceinline__ uint32_t ilv_logical(uint32_t n, uint32_t N) {
+    const uint32_t g = n >> 5, r = n & 31u;
+    return r < 16u ? 16u * g + r : N / 2u + 16u * g + (r - 16u);
+}
+
+// Operands of the epilogue that come from memory, loaded before the
+// product so that their latency overlaps it: RESID the old value (a) and
+// the skip flag (b != 0: no residual); QKV the RoPE cos (a) and sin (b).
+struct EpiPre { float a, b; };
+
+template <int EPI>
+__device__ __forceinline__ EpiPre epi_prefetch(const MmEpi& e, uint32_t m, uint32_t n) {
+    EpiPre p{0.0f, 0.0f};
+    if constexpr (EPI == EPI_RESID) {
+        p.a = e.y[(size_t)m * e.y_stride + n];
+        p.b = (e.skipm && e.skipm[m]) ? 1.0f : 0.0f;
+    } else if constexpr (EPI == EPI_QKV) {
+        const uint32_t sec = n / e.D, i = n - sec * e.D;
+        if (sec < 2u) {
+            const uint32_t half = e.hd >> 1, t = (i % e.hd) >> 1;
+            const uint32_t pos = row_pos(e.pd, m);
+            p.a = e.rc[(size_t)pos * half + t];
+            p.b = e.rs[(size_t)pos * half + t];
+        }
+    }
+    return p;
+}
+
+// y is this lane's output for (row m, device row n); y1 and y16 are the
+// outputs of rows n ^ 1 and n ^ 16 of the same m (lane partners).  Returns
+// the value a SWIGLU lane stores (0 for the others).
+template <int EPI>
+__device__ __forceinline__ float epi_apply(const MmEpi& e, const EpiPre& p, uint32_t N, uint32_t m, uint32_t n,
+                                           float y, float y1, float y16) {
+    if constexpr (EPI == EPI_STORE) {
+        e.y[(size_t)m * e.y_stride + (e.ilv ? ilv_logical(n, N) : n)] = y;
+    } else if constexpr (EPI == EPI_RESID) {
+        if (p.b == 0.0f) e.y[(size_t)m * e.y_stride + n] = p.a + y;
+    } else if constexpr (EPI == EPI_QKV) {
+        // src/engine.cpp:693-715 (Q, K, V rows of the fused matrix) and the
+        // RoPE of :732-749 for Q and K: pair (2t, 2t+1) of a head
+        const uint32_t sec = n / e.D, i = n - sec * e.D;
+        float out = y;
+        if (sec < 2u) out = (n & 1u) ? __builtin_fmaf(y1, p.b, y * p.a) : __builtin_fmaf(y, p.a, -(y1 * p.b));
+        float* dst = sec == 0u ? e.q : (sec == 1u ? e.k : e.v);
+        dst[(size_t)m * e.D + i] = out;
+    } else {
+        // SwiGLU of src/engine.cpp:832-838 on gate row j (group rows 0-15)
+        // and up row j (rows 16-31): g * (1 / (1 + exp(-g))) * u
+        if ((n & 31u) < 16u) {
+            const uint32_t j = 16u * (n >> 5) + (n & 31u);
+            const float sig = 1.0f / (1.0f + expf_c(-y));
+            const float f = y * sig * y16;
+            e.y[(size_t)m * e.y_stride + j] = f;
+            return f;
+        }
+    }
+    return 0.0f;
+}
+
+// ------------------------------------------------------------ operands
+
+// B operand (16 signed codes, element order) of block t of a 256-column
+// chunk for this lane (row lane % 32, elements 16 (lane / 32) ..): cw holds
+// the lane's 16-byte words of the chunk's sets.
+template <int FMT>
+__device__ __forceinline__ pf_v4i b_operand(const uint4* cw, uint32_t t) {
+    constexpr uint32_t ADD = (0x80u - (uint32_t)code_offset(FMT)) * 0x01010101u;
+    pf_v4i v;
+    if constexpr (FMT == FMT_Q4) {
+        const uint4 c = cw[t >> 1];
+        const uint32_t x0 = (t & 1u) ? c.z : c.x, x1 = (t & 1u) ? c.w : c.y, mk = 0x0F0F0F0Fu;
+        v.x = (int)(((x0 & mk) + ADD) ^ 0x80808080u);
+        v.y = (int)(((x1 & mk) + ADD) ^ 0x80808080u);
+        v.z = (int)((((x0 >> 4) & mk) + ADD) ^ 0x80808080u);
+        v.w = (int)((((x1 >> 4) & mk) + ADD) ^ 0x80808080u);
+    } else {
+        const uint4 c = cw[t >> 2];
+        const uint32_t s = t & 3u;
+        const uint32_t x = s == 0u ? c.x : (s == 1u ? c.y : (s == 2u ? c.z : c.w)), mk = 0x03030303u;
+        v.x = (int)(((x & mk) + ADD) ^ 0x80808080u);
+        v.y = (int)((((x >> 2) & mk) + ADD) ^ 0x80808080u);
+        v.z = (int)((((x >> 4) & mk) + ADD) ^ 0x80808080u);
+        v.w = (int)((((x >> 6) & mk) + ADD) ^ 0x80808080u);
+    }
+    return v;
+}
+
+template <int FMT>
+constexpr int sets_of() { return FMT == FMT_Q4 ? 4 : 2; }
+
+// =============================================================== GEMV
+
+constexpr int GEMV_WAVES = 8;
+constexpr uint32_t GEMV_MAX_M = 8;
+
+struct GemvArgs {
+    const uint8_t* W;
+    uint32_t N, K, M;
+    const float* x;            // NORM / QUANT / QPART input rows [M][xs]
+    uint32_t xs;
+    const float* nw;           // NORM weight [K]
+    const int8_t* a8;          // INT8 input: codes [M][xs] and row scales [M]
+    const float* a8s;
+    const float* pin;          // QPART: row maxima partials of the input [M][np]
+    uint32_t np;
+    const uint32_t* gate;      // gated instances: 0 -> nothing to compute
+    MmEpi e;
+};
+
+// Dynamic LDS of k_gemv (bytes), laid out as: fp64 partials [waves][64][4],
+// int8 rows [M][K + 16], tile sums [M][K / 64], maxima [M][4 waves], row
+// statistics [3][8].
+__host__ __device__ constexpr uint32_t gemv_kp(uint32_t K) { return K + 16u; }
+__host__ __device__ constexpr uint32_t gemv_smem(uint32_t M, uint32_t K) {
+    return (uint32_t)GEMV_WAVES * 64u * 4u * 8u + M * gemv_kp(K) + M * (K / 64u) * 4u +
+           M * 4u * (uint32_t)GEMV_WAVES * 4u + 3u * 8u * 4u;
+}
+
+// Codes of four values with the row's 127 / amax.
+__device__ __forceinline__ uint32_t pack_codes(float4 v, float q) {
+    const uint32_t b0 = (uint8_t)quant_code(v.x, q), b1 = (uint8_t)quant_code(v.y, q);
+    const uint32_t b2 = (uint8_t)quant_code(v.z, q), b3 = (uint8_t)quant_code(v.w, q);
+    return b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+}
+
+__device__ __forceinline__ float max4abs(float4 v) {
+    return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+
+// Grid N / 32 (one 32-row group per workgroup), 64 * GEMV_WAVES threads,
+// gemv_smem(M, K) bytes of dynamic LDS.  K % 256 == 0, K <= 1024 CPW
+// (CPW chunks of 256 columns per wave, held in registers), M <= MR <= 8.
+//
+// The workgroup first loads everything its prologue needs, then its weight
+// words (wave w takes chunks [nch w / W, nch (w + 1) / W)), then the
+// epilogue's operands, so that the prologue's arithmetic waits only for the
+// first loads while the weights are in flight.  Every load is issued
+// unconditionally from a clamped address (rows past M reload row M - 1 and
+// are not used), so no load sits behind a branch:
+//   NORM : K = D <= 2048.  Wave w, row q of 16 lanes takes tile T = w + 8q;
+//          lane i holds elements i, i + 16, i + 32, i + 48 of the tile in
+//          every row m, so the tile's halving tree (offsets 32 and 16 first)
+//          starts inside the lane and ends with DPP steps.  Tile sums in
+//          column order give 1 / rms; amax = max|x * w| * inv (rounding is
+//          monotone); codes of (x * w) * inv.
+//   QUANT: the row held (CPW float4 per thread and row), amax, codes.
+//   QPART: the same, amax from the producer's per-workgroup maxima.
+//   INT8 : rows quantized by another kernel, copied.
+template <int FMT, int PRO, int EPI, bool GATED, int CPW, int MR>
+__global__ __launch_bounds__(64 * GEMV_WAVES) void k_gemv(GemvArgs a) {
+    constexpr uint32_t TB = g32_tile_bytes(FMT), CODES = g32_code_bytes(FMT);
+    constexpr int SETS = sets_of<FMT>();
+    constexpr uint32_t NT = 64u * GEMV_WAVES;
+    if constexpr (GATED)
+        if (*a.gate == 0u) return;   // no row of the pass needs this product
+    extern __shared__ __align__(16) uint8_t smem[];
+    double* red = reinterpret_cast<double*>(smem);
+    int8_t* act = reinterpret_cast<int8_t*>(smem + GEMV_WAVES * 64 * 4 * 8);
+    const uint32_t K = a.K, M = a.M, kp = gemv_kp(K), nt = K / 64u, xs = a.xs, mlast = M - 1u;
+    float* tss = reinterpret_cast<float*>(act + M * kp);
+    float* wmx = tss + M * nt;                 // [M][4 GEMV_WAVES]
+    float* st = wmx + M * 4u * GEMV_WAVES;
+    float* st_q = st + 8;                      // 127 / amax
+    float* st_as = st + 16;                    // amax / 127
+    const uint32_t t = threadIdx.x, lane = t & 63u, r = lane & 31u, h = lane >> 5;
+    const uint32_t wid = __builtin_amdgcn_readfirstlane(t >> 6);
+    const float* __restrict__ xg = a.x;
+
+    // ---- prologue loads
+    const uint32_t li = lane & 15u, q = lane >> 4, T = wid + GEMV_WAVES * q;   // NORM tile of this lane
+    float xv[MR][4], wv[4];
+    float4 hv[MR][CPW];
+    float pv[MR];
+    uint4 iv[2];
+    const uint32_t per4 = K / 4u, per16 = K / 16u;
+    if constexpr (PRO == PRO_NORM) {
+        const uint32_t col = 64u * min(T, nt - 1u) + li;
+#pragma unroll
+        for (int k = 0; k < 4; k++) wv[k] = a.nw[col + 16u * k];
+#pragma unroll
+        for (uint32_t m = 0; m < MR; m++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) xv[m][k] = xg[(size_t)min(m, mlast) * xs + col + 16u * k];
+    } else if constexpr (PRO == PRO_INT8) {
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const uint32_t i = t + NT * k, m = min(i / per16, mlast), c = i % per16;
+            iv[k] = *reinterpret_cast<const uint4*>(a.a8 + (size_t)m * xs + 16u * c);
+        }
+    } else {
+#pragma unroll
+        for (uint32_t m = 0; m < MR; m++)
+#pragma unroll
+            for (int k = 0; k < CPW; k++) {
+                const uint32_t c = min(t + NT * k, per4 - 1u);
+                hv[m][k] = *reinterpret_cast<const float4*>(xg + (size_t)min(m, mlast) * xs + 4u * c);
+            }
+        if constexpr (PRO == PRO_QPART) {
+            const uint32_t ti = min(t, a.np - 1u);
+#pragma unroll
+            for (uint32_t m = 0; m < MR; m++) pv[m] = a.pin[(size_t)min(m, mlast) * a.np + ti];
+        }
+    }
+
+    // ---- weight loads
+    const uint32_t nch = K >> 8, c0 = nch * wid / GEMV_WAVES, c1 = nch * (wid + 1) / GEMV_WAVES;
+    const uint8_t* tiles = a.W + (size_t)blockIdx.x * nch * TB;
+    uint4 cw[CPW][SETS], sw[CPW];
+#pragma unroll
+    for (int j = 0; j < CPW; j++) {
+        const uint8_t* tile = tiles + (size_t)min(c0 + j, nch - 1u) * TB;
+#pragma unroll
+        for (int s = 0; s < SETS; s++) cw[j][s] = *reinterpret_cast<const uint4*>(tile + s * 1024 + lane * 16);
+        sw[j] = *reinterpret_cast<const uint4*>(tile + CODES + r * 16);
+    }
+    // ---- epilogue operands: thread t outputs row om of device row on
+    const uint32_t om = t >> 5, on = 32u * blockIdx.x + (t & 31u);
+    const EpiPre pre = epi_prefetch<EPI>(a.e, min(om, mlast), on);
+
+    // ---- prologue arithmetic
+    if constexpr (PRO == PRO_INT8) {
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const uint32_t i = t + NT * k, m = i / per16, c = i % per16;
+            if (m < M) *reinterpret_cast<uint4*>(act + m * kp + 16u * c) = iv[k];
+        }
+        if (t < M) st_as[t] = a.a8s[t];
+    } else if constexpr (PRO == PRO_NORM) {
+#pragma unroll
+        for (uint32_t m = 0; m < MR; m++) {
+            if (m >= M) break;
+            float s = (xv[m][0] * xv[m][0] + xv[m][2] * xv[m][2]) + (xv[m][1] * xv[m][1] + xv[m][3] * xv[m][3]);
+            s = row16_tree_sum(s);
+            const float mx = row16_max(fmaxf(fmaxf(fabsf(xv[m][0] * wv[0]), fabsf(xv[m][1] * wv[1])),
+                                             fmaxf(fabsf(xv[m][2] * wv[2]), fabsf(xv[m][3] * wv[3]))));
+            if (li == 0) {
+                if (T < nt) tss[m * nt + T] = s;
+                wmx[m * 4u * GEMV_WAVES + 4u * wid + q] = T < nt ? mx : 0.0f;
+            }
+        }
+        __syncthreads();
+        if (t < M) {
+            // tile sums in column order from +0 (all loaded first); rms of
+            // src/matmul_neon.cpp:231-239
+            float tv[32], wm[4 * GEMV_WAVES];
+#pragma unroll
+            for (uint32_t i = 0; i < 32; i += 4) {
+                const float4 v4 = *reinterpret_cast<const float4*>(tss + t * nt + min(i, nt - 4u));
+                tv[i] = v4.x; tv[i + 1] = v4.y; tv[i + 2] = v4.z; tv[i + 3] = v4.w;
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < 4 * GEMV_WAVES; i += 4) {
+                const float4 v4 = *reinterpret_cast<const float4*>(wmx + t * 4u * GEMV_WAVES + i);
+                wm[i] = v4.x; wm[i + 1] = v4.y; wm[i + 2] = v4.z; wm[i + 3] = v4.w;
+            }
+            float ss = 0.0f;
+#pragma unroll
+            for (uint32_t i = 0; i < 32; i++)
+                if (i < nt) ss = ss + tv[i];
+            const float inv = 1.0f / __builtin_sqrtf(ss / (float)K + 1e-6f);
+            float mw = 0.0f;
+#pragma unroll
+            for (uint32_t i = 0; i < 4 * GEMV_WAVES; i++) mw = fmaxf(mw, wm[i]);
+            const float amax = mw * inv;
+            st[t] = inv;
+            st_q[t] = amax == 0.0f ? 1.0f : 127.0f / amax;
+            st_as[t] = amax == 0.0f ? 1.0f : amax / 127.0f;
+        }
+        __syncthreads();
+        if (T < nt) {
+#pragma unroll
+            for (uint32_t m = 0; m < MR; m++) {
+                if (m >= M) break;
+                const float inv = st[m], qq = st_q[m];
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    act[m * kp + 64u * T + li + 16u * k] = quant_code((xv[m][k] * wv[k]) * inv, qq);
+            }
+        }
+    } else {
+#pragma unroll
+        for (uint32_t m = 0; m < MR; m++) {
+            if (m >= M) break;
+            float mx;
+            if constexpr (PRO == PRO_QPART) {
+                mx = t < a.np ? pv[m] : 0.0f;
+            } else {
+                mx = 0.0f;
+#pragma unroll
+                for (int k = 0; k < CPW; k++) mx = fmaxf(mx, max4abs(hv[m][k]));
+            }
+            mx = row16_max(mx);
+            if (li == 0) wmx[m * 4u * GEMV_WAVES + 4u * wid + q] = mx;
+        }
+        __syncthreads();
+        if (t < M) {
+            float wm[4 * GEMV_WAVES];
+#pragma unroll
+            for (uint32_t i = 0; i < 4 * GEMV_WAVES; i += 4) {
+                const float4 v4 = *reinterpret_cast<const float4*>(wmx + t * 4u * GEMV_WAVES + i);
+                wm[i] = v4.x; wm[i + 1] = v4.y; wm[i + 2] = v4.z; wm[i + 3] = v4.w;
+            }
+            float amax = 0.0f;
+#pragma unroll
+            for (uint32_t i = 0; i < 4 * GEMV_WAVES; i++) amax = fmaxf(amax, wm[i]);
+            st_q[t] = amax == 0.0f ? 1.0f : 127.0f / amax;
+            st_as[t] = amax == 0.0f ? 1.0f : amax / 127.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t m = 0; m < MR; m++) {
+            if (m >= M) break;
+            const float qq = st_q[m];
+#pragma unroll
+            for (int k = 0; k < CPW; k++) {
+                const uint32_t c = t + NT * k;
+                if (c < per4) *reinterpret_cast<uint32_t*>(act + m * kp + 4u * c) = pack_codes(hv[m][k], qq);
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- product
+    double S[4] = {0.0, 0.0, 0.0, 0.0};
+    const pf_v16i zero = {};
+    const pf_v4i za = {0, 0, 0, 0};
+    const int8_t* arow = act + min(r, mlast) * kp + 16u * h;
+#pragma unroll
+    for (int j = 0; j < CPW; j++) {
+        if (c0 + j >= c1) break;
+        const uint32_t c = c0 + j;
+        const uint16_t* sc = reinterpret_cast<const uint16_t*>(&sw[j]);
+        pf_v4i A[8];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; u++) {
+            const pf_v4i v = *reinterpret_cast<const pf_v4i*>(arow + 32u * (8u * c + u));
+            A[u] = r < M ? v : za;
+        }
+        // two blocks' MFMAs in flight before their results are scaled
+#pragma unroll
+        for (uint32_t u = 0; u < 8; u += 2) {
+            const pf_v16i D0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[u], b_operand<FMT>(cw[j], u), zero, 0, 0, 0);
+            const pf_v16i D1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[u + 1], b_operand<FMT>(cw[j], u + 1), zero, 0, 0, 0);
+            const double d0 = (double)h2f(sc[u]), d1 = (double)h2f(sc[u + 1]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) S[i] = __builtin_fma(d0, (double)D0[i], S[i]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) S[i] = __builtin_fma(d1, (double)D1[i], S[i]);
+        }
+    }
+    // lane (r, h) holds rows m = 4h + i of device row r; the waves meet in LDS
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[(wid * 64 + lane) * 4 + i] = S[i];
+    __syncthreads();
+    float y = 0.0f;
+    if (om < M) {
+        const uint32_t L = (t & 31u) + 32u * (om >> 2), i = om & 3u;
+        double v = red[L * 4 + i];
+#pragma unroll
+        for (uint32_t w = 1; w < GEMV_WAVES; w++) v += red[(w * 64 + L) * 4 + i];
+        y = (float)(v * (double)st_as[om]);
+    }
+    const float y1 = __shfl_xor(y, 1, 64), y16 = __shfl_xor(y, 16, 64);
+    float f = 0.0f;
+    if (om < M) f = epi_apply<EPI>(a.e, pre, a.N, om, on, y, y1, y16);
+    if constexpr (EPI == EPI_SWIGLU) {
+        // row maximum of |f| over the group's 16 outputs (lanes of one m
+        // are a half wave), for the consumer's quantization
+        float mx = fabsf(f);
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        if (a.e.pmax && om < M && (t & 31u) == 0) a.e.pmax[(size_t)om * (a.N / 32u) + blockIdx.x] = mx;
+    }
+}
+
+// =============================================================== GEMM
+
+struct GemmArgs {
+    const uint8_t* W;
+    uint32_t N, K, M;
+    const int8_t* act;         // [ceil(M / 32) * 32][act_stride] readable rows
+    uint32_t act_stride;
+    const float* as;           // [M]
+    const uint32_t* gate;
+    MmEpi e;
+};
+
+// Grid (N / 32, ceil(M / 128)), 256 threads: wave w of workgroup (g, y)
+// computes M tile 4y + w (32 activation rows) against row group g over all
+// of K.  Each lane keeps the 16 outputs of its MFMA tile in fp64.  The next
+// chunk's weight words and activation tiles load while the current chunk
+// runs (every load is issued unconditionally, so the waits are exact).
+template <int FMT, int EPI, bool GATED = false>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
+    constexpr uint32_t TB = g32_tile_bytes(FMT), CODES = g32_code_bytes(FMT);
+    constexpr int SETS = sets_of<FMT>();
+    if constexpr (GATED)
+        if (*a.gate == 0u) return;
+    const uint32_t lane = threadIdx.x & 63u, r = lane & 31u, h = lane >> 5;
+    const uint32_t mt = blockIdx.y * 4u + (threadIdx.x >> 6);
+    if (mt * 32u >= a.M) return;
+    const uint32_t nch = a.K >> 8;
+    const uint8_t* tiles = a.W + (size_t)blockIdx.x * nch * TB;
+    const int8_t* arow = a.act + (size_t)(mt * 32u + r) * a.act_stride + 16u * h;
+    double S[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) S[i] = 0.0;
+    const pf_v16i zero = {};
+    uint4 cwn[SETS], swn;
+    pf_v4i an[8];
+    auto load = [&](uint32_t c) {
+        const uint8_t* tile = tiles + (size_t)c * TB;
+#pragma unroll
+        for (int s = 0; s < SETS; s++) cwn[s] = *reinterpret_cast<const uint4*>(tile + s * 1024 + lane * 16);
+        swn = *reinterpret_cast<const uint4*>(tile + CODES + r * 16);
+#pragma unroll
+        for (int t = 0; t < 8; t++) an[t] = *reinterpret_cast<const pf_v4i*>(arow + 256u * c + 32u * t);
+    };
+    load(0);
+    for (uint32_t c = 0; c < nch; c++) {
+        uint4 cw[SETS], sw = swn;
+        pf_v4i A[8];
+#pragma unroll
+        for (int s = 0; s < SETS; s++) cw[s] = cwn[s];
+#pragma unroll
+        for (int t = 0; t < 8; t++) A[t] = an[t];
+        load(c + 1 < nch ? c + 1 : c);
+        const uint16_t* sc = reinterpret_cast<const uint16_t*>(&sw);
+#pragma unroll
+        for (uint32_t t = 0; t < 8; t++) {
+            const pf_v16i D = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[t], b_operand<FMT>(cw, t), zero, 0, 0, 0);
+            const double d = (double)h2f(sc[t]);
+#pragma unroll
+            for (int i = 0; i < 16; i++) S[i] = __builtin_fma(d, (double)D[i], S[i]);
+        }
+    }
+    // output i of lane (r, h): activation row 8 (i / 4) + 4 h + i % 4 of the
+    // tile, device row r of the group
+    const uint32_t n = 32u * blockIdx.x + r;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const uint32_t m = mt * 32u + 8u * (i / 4) + 4u * h + (i % 4);
+        const float y = m < a.M ? (float)(S[i] * (double)a.as[m]) : 0.0f;
+        const float y1 = __shfl_xor(y, 1, 64), y16 = __shfl_xor(y, 16, 64);
+        if (m < a.M) {
+            const EpiPre pre = epi_prefetch<EPI>(a.e, m, n);
+            epi_apply<EPI>(a.e, pre, a.N, m, n, y, y1, y16);
+        }
+    }
+}
+
+// ===================================================== row kernels (M > 8)
+
+// The engine's RMSNorm of one row (1024 threads, element i = t + 1024 k) in
+// the canonical tile order of the GEMV prologue: per 64-column tile a
+// halving tree of x * x, tile sums added in column order from +0, then
+// normed = (x * w) * inv.  K % 64 == 0, K <= 4096.
+template <int PER>
+__device__ __forceinline__ void norm_row_1024(float (&xv)[PER], const float (&wv)[PER], uint32_t K, float* row,
+                                              float* tree, float* red) {
+    const uint32_t t = threadIdx.x, wid = t >> 6, lane = t & 63u;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const uint32_t i = t + 1024u * k;
+        if (i < K) row[i] = xv[k];
+    }
+    __syncthreads();
+    for (uint32_t tl = wid; tl < K / 64u; tl += 16u) {
+        const float v = row[64u * tl + lane];
+        const float s = wave_tree_sum(v * v);
+        if (lane == 0) tree[tl] = s;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float ss = 0.0f;
+        for (uint32_t tl = 0; tl < K / 64u; tl++) ss = ss + tree[tl];
+        red[0] = ss;
+    }
+    __syncthreads();
+    const float ss = red[0];
+    __syncthreads();
+    const float inv = 1.0f / __builtin_sqrtf(ss / (float)K + 1e-6f);
+#pragma unroll
+    for (int k = 0; k < PER; k++) xv[k] = (xv[k] * wv[k]) * inv;
+}
+
+// Grid M, 1024 threads: normed rows (fp32) of x into out; with nclear,
+// block 0 zeroes that word (the layer-skip row counter of the layer).
+template <int PER>
+__global__ __launch_bounds__(1024) void k_norm_rows(const float* __restrict__ x, uint32_t K,
+                                                    const float* __restrict__ w, float* __restrict__ out,
+                                                    uint32_t* __restrict__ nclear) {
+    __shared__ float row[4096];
+    __shared__ float tree[64];
+    __shared__ float red[16];
+    const uint32_t m = blockIdx.x, t = threadIdx.x;
+    if (nclear && m == 0 && t == 0) *nclear = 0u;
+    float xv[PER], wv[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const uint32_t i = t + 1024u * k;
+        xv[k] = i < K ? x[(size_t)m * K + i] : 0.0f;
+        wv[k] = i < K ? w[i] : 0.0f;
+    }
+    norm_row_1024<PER>(xv, wv, K, row, tree, red);
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const uint32_t i = t + 1024u * k;
+        if (i < K) out[(size_t)m * K + i] = xv[k];
+    }
+}
+
+// Grid M, 1024 threads: normed rows quantized (quantize_activation_row)
+// into q [M][q_stride] with row scales as[M].
+template <int PER>
+__global__ __launch_bounds__(1024) void k_norm_quant(const float* __restrict__ x, uint32_t K,
+                                                     const float* __restrict__ w, int8_t* __restrict__ q,
+                                                     uint32_t q_stride, float* __restrict__ as) {
+    __shared__ float row[4096];
+    __shared__ float tree[64];
+    __shared__ float red[16];
+    const uint32_t m = blockIdx.x, t = threadIdx.x;
+    float xv[PER], wv[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const uint32_t i = t + 1024u * k;
+        xv[k] = i < K ? x[(size_t)m * K + i] : 0.0f;
+        wv[k] = i < K ? w[i] : 0.0f;
+    }
+    norm_row_1024<PER>(xv, wv, K, row, tree, red);
+    __syncthreads();
+    quantize_row_block<PER, 1024>(xv, K, q + (size_t)m * q_stride, as + m, nullptr, red);
+}
+
+}  // namespace pf

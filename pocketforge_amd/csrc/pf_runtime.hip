@@ -1,9 +1,9 @@
 // Host runtime of libpocketforge_amd.so: implements include/pf_gpu.h on
 // top of the gfx950 kernels (single translation unit with the kernels).
 #include "pf_gemv.hip"
+#include "pf_mm.hip"
 #include "pf_attn.hip"
 #include "pf_ctl.hip"
-#include "pf_decode.hip"
 
 #include <hip/hip_ext.h>
 
@@ -169,11 +169,10 @@ struct pf_matrix {
     int32_t fmt = 0;
     uint32_t rows = 0, cols = 0;
     bool rowmajor = false;
-    uint8_t* data = nullptr;    // tiled: all tiles; row-major: codes
+    bool ilv = false;           // halves [0, rows/2) and [rows/2, rows) interleaved by 16 rows
+    uint8_t* data = nullptr;    // 32-row group tiles; row-major: codes
     uint16_t* scales = nullptr; // row-major only
     size_t bytes = 0;
-    uint32_t bpw = 2, splits = 1;   // blocks per wave, K splits (grid y)
-    uint32_t waves = 4;             // waves per GEMV workgroup
 };
 
 static uint32_t interchange_code(int fmt, const uint8_t* blk, uint32_t e) {
@@ -207,74 +206,53 @@ static pf_status check_row(const pf_ctx* c, int fmt, const uint8_t* codes, const
     return PF_OK;
 }
 
-// Repacks interchange rows [r0, r0 + 64*G) into tiles (device element
-// order) in `out` (G * chunks tiles).
-static void repack_tiles(int fmt, uint32_t cols, const uint8_t* codes, const uint16_t* scales, uint32_t r0,
-                         uint32_t G, uint8_t* out) {
-    const uint32_t nb = cols / 32, chunks = cols / 256, bb = code_bytes(fmt), TB = tile_bytes(fmt);
-    const uint32_t CODES = TILE_ROWS * TILE_BLOCKS * bb;
-    for (uint32_t g = 0; g < G; g++)
-        for (uint32_t c = 0; c < chunks; c++) {
-            uint8_t* tile = out + ((size_t)g * chunks + c) * TB;
-            std::memset(tile, 0, TB);
-            for (uint32_t r = 0; r < 64; r++) {
-                const uint32_t row = r0 + g * 64 + r;
-                for (uint32_t t = 0; t < 8; t++) {
-                    const uint32_t b = c * 8 + t;
-                    const uint8_t* blk = codes + ((size_t)row * nb + b) * bb;
-                    std::memcpy(tile + CODES + r * 16 + t * 2, &scales[(size_t)row * nb + b], 2);
-                    if (fmt == FMT_Q4) {
-                        uint8_t* dst = tile + t * 1024 + r * 16;
-                        for (uint32_t j = 0; j < 16; j++)
-                            dst[j] = (uint8_t)(interchange_code(fmt, blk, j) | (interchange_code(fmt, blk, j + 16) << 4));
-                    } else {
-                        uint8_t* dst = tile + (t >> 1) * 1024 + r * 16 + (t & 1) * 8;
-                        for (uint32_t e = 0; e < 32; e++) {
-                            uint32_t pl = e >> 3, w = (e >> 2) & 1u, jj = e & 3u;
-                            dst[4 * w + jj] |= (uint8_t)(interchange_code(fmt, blk, e) << (2 * pl));
-                        }
-                    }
+// Device row of logical row r (pf_layout.h: the fused gate|up matrix
+// interleaves its halves by 16 rows).
+static uint32_t device_row(const pf_matrix* M, uint32_t r) {
+    if (!M->ilv) return r;
+    const uint32_t half = M->rows / 2, hi = r >= half ? 1u : 0u, j = r - hi * half;
+    return 32u * (j / 16u) + 16u * hi + (j % 16u);
+}
+
+// Writes one interchange row (codes [cols/32][code_bytes], fp16 scales
+// [cols/32]) as row r of a 32-row group whose tiles start at gtiles.
+static void pack_row(int fmt, uint32_t cols, const uint8_t* codes, const uint16_t* scales, uint32_t r,
+                     uint8_t* gtiles) {
+    const uint32_t nb = cols / 32, bb = code_bytes(fmt), TB = g32_tile_bytes(fmt), CODES = g32_code_bytes(fmt);
+    for (uint32_t b = 0; b < nb; b++) {
+        uint8_t* tile = gtiles + (size_t)(b / 8) * TB;
+        const uint32_t t = b % 8;
+        const uint8_t* blk = codes + (size_t)b * bb;
+        std::memcpy(tile + CODES + r * 16 + t * 2, &scales[b], 2);
+        for (uint32_t h = 0; h < 2; h++) {
+            const uint32_t lane = r + 32 * h;
+            if (fmt == FMT_Q4) {
+                uint8_t* dst = tile + (t >> 1) * 1024 + lane * 16 + (t & 1) * 8;
+                for (uint32_t j = 0; j < 8; j++)
+                    dst[j] = (uint8_t)(interchange_code(fmt, blk, 16 * h + j) |
+                                       (interchange_code(fmt, blk, 16 * h + j + 8) << 4));
+            } else {
+                uint8_t* dst = tile + (t >> 2) * 1024 + lane * 16 + (t & 3) * 4;
+                for (uint32_t j = 0; j < 4; j++) {
+                    uint32_t v = 0;
+                    for (uint32_t u = 0; u < 4; u++) v |= interchange_code(fmt, blk, 16 * h + 4 * u + j) << (2 * u);
+                    dst[j] = (uint8_t)v;
                 }
             }
         }
-}
-
-// K split of a tiled matrix: the largest blocks-per-wave in {1, 2, 4} that
-// still gives at least `min_waves` waves in all (default 4096, four waves
-// per SIMD; PF_GEMV_MIN_WAVES overrides it), then the largest workgroup of
-// at most `max_wg` waves (default 8; PF_GEMV_WAVES overrides it) that
-// divides the blocks into whole workgroups (nb % (waves bpw) == 0; nb is a
-// multiple of 8) and still leaves a workgroup per CU (256 or more).  The wave count depends on bpw only: larger workgroups
-// just meet in LDS instead of through fp64 atomics.  Defaults from a sweep
-// of min_waves {1024, 2048, 4096} x waves {4, 8} over the 1B verify pass
-// (M = 5): 6.09 us per launch on average against 6.58 us at 2048 x 4.
-static void choose_split(pf_matrix* M) {
-    const uint32_t nb = M->cols / 32, G = M->rows / 64;
-    uint64_t min_waves = 4096;
-    uint32_t max_wg = 8;
-    if (const char* s = std::getenv("PF_GEMV_MIN_WAVES")) min_waves = std::strtoull(s, nullptr, 10);
-    if (const char* s = std::getenv("PF_GEMV_WAVES")) max_wg = (uint32_t)std::strtoul(s, nullptr, 10);
-    uint32_t best = 1;
-    for (uint32_t bpw : {1u, 2u, 4u}) {
-        if (nb % (4 * bpw)) continue;
-        if ((uint64_t)G * (nb / bpw) >= min_waves) best = bpw;
     }
-    uint32_t waves = 4;
-    for (uint32_t w : {8u, 16u})
-        if (w <= max_wg && nb % (w * best) == 0 && (uint64_t)G * (nb / (w * best)) >= 256) waves = w;
-    M->bpw = best;
-    M->waves = waves;
-    M->splits = nb / (waves * best);
 }
 
-static pf_status matrix_alloc(pf_ctx* c, int32_t fmt, uint32_t rows, uint32_t cols, bool rowmajor, pf_matrix** out) {
+static pf_status matrix_alloc(pf_ctx* c, int32_t fmt, uint32_t rows, uint32_t cols, bool rowmajor, pf_matrix** out,
+                              bool ilv = false) {
     if (fmt != FMT_Q4 && fmt != FMT_Q2 && fmt != FMT_Q15) return fail(c, PF_ERR_ARG, "unknown format");
     if (cols % 256 || rows % 64 || rows == 0 || cols == 0)
         return fail(c, PF_ERR_UNSUPPORTED, "matrix shape must have rows % 64 == 0 and cols % 256 == 0");
     if (rowmajor && (fmt != FMT_Q4 || cols > 2048))
         return fail(c, PF_ERR_UNSUPPORTED, "fp32-activation matrices must be Q4 with cols <= 2048");
+    if (!rowmajor && cols > 8192) return fail(c, PF_ERR_UNSUPPORTED, "int8-activation matrices need cols <= 8192");
     pf_matrix* M = new pf_matrix();
-    M->ctx = c; M->fmt = fmt; M->rows = rows; M->cols = cols; M->rowmajor = rowmajor;
+    M->ctx = c; M->fmt = fmt; M->rows = rows; M->cols = cols; M->rowmajor = rowmajor; M->ilv = ilv;
     const uint32_t nb = cols / 32;
     if (rowmajor) {
         M->bytes = (size_t)rows * nb * 16;
@@ -282,19 +260,22 @@ static pf_status matrix_alloc(pf_ctx* c, int32_t fmt, uint32_t rows, uint32_t co
         if (!s) s = dalloc_t(c, &M->scales, (size_t)rows * nb);
         if (s) { delete M; return s; }
     } else {
-        M->bytes = (size_t)(rows / 64) * (cols / 256) * tile_bytes(fmt);
+        M->bytes = (size_t)(rows / 32) * (cols / 256) * g32_tile_bytes(fmt);
         pf_status s = dalloc_t(c, &M->data, M->bytes);
         if (s) { delete M; return s; }
-        choose_split(M);
     }
     *out = M;
     return PF_OK;
 }
 
-// Uploads interchange rows [r0, r0 + n) of a matrix (n % 64 == 0 for tiled).
+// Uploads interchange rows [r0, r0 + n) of a matrix.  A 32-row group that
+// the upload covers only in part keeps its other rows (its tiles are read
+// back, patched and written).
 static pf_status matrix_put(pf_matrix* M, uint32_t r0, uint32_t n, const uint8_t* codes, const uint16_t* scales) {
     pf_ctx* c = M->ctx;
     const uint32_t nb = M->cols / 32, bb = code_bytes(M->fmt);
+    if (n == 0) return PF_OK;
+    if ((uint64_t)r0 + n > M->rows) return fail(c, PF_ERR_ARG, "rows beyond the matrix");
     for (uint32_t r = 0; r < n; r++) {
         pf_status s = check_row(c, M->fmt, codes + (size_t)r * nb * bb, scales + (size_t)r * nb, nb, r0 + r);
         if (s) return s;
@@ -304,12 +285,22 @@ static pf_status matrix_put(pf_matrix* M, uint32_t r0, uint32_t n, const uint8_t
         PF_HIP(c, hipMemcpy(M->scales + (size_t)r0 * nb, scales, (size_t)n * nb * 2, hipMemcpyHostToDevice));
         return PF_OK;
     }
-    const uint32_t G = n / 64, chunks = M->cols / 256;
-    std::vector<uint8_t> tiles((size_t)G * chunks * tile_bytes(M->fmt));
-    // repack takes absolute rows; shift the pointers so row r0 is row 0
-    repack_tiles(M->fmt, M->cols, codes - (size_t)r0 * nb * bb, scales - (size_t)r0 * nb, r0, G, tiles.data());
-    PF_HIP(c, hipMemcpy(M->data + (size_t)(r0 / 64) * chunks * tile_bytes(M->fmt), tiles.data(), tiles.size(),
-                        hipMemcpyHostToDevice));
+    const size_t gbytes = (size_t)(M->cols / 256) * g32_tile_bytes(M->fmt);
+    uint32_t g_lo = UINT32_MAX, g_hi = 0;
+    for (uint32_t r = r0; r < r0 + n; r++) {
+        const uint32_t g = device_row(M, r) / 32;
+        g_lo = std::min(g_lo, g);
+        g_hi = std::max(g_hi, g);
+    }
+    std::vector<uint8_t> buf((size_t)(g_hi - g_lo + 1) * gbytes);
+    const bool whole = !M->ilv && r0 % 32 == 0 && n % 32 == 0;
+    if (!whole) PF_HIP(c, hipMemcpy(buf.data(), M->data + g_lo * gbytes, buf.size(), hipMemcpyDeviceToHost));
+    for (uint32_t r = r0; r < r0 + n; r++) {
+        const uint32_t dr = device_row(M, r);
+        pack_row(M->fmt, M->cols, codes + (size_t)(r - r0) * nb * bb, scales + (size_t)(r - r0) * nb, dr % 32,
+                 buf.data() + (size_t)(dr / 32 - g_lo) * gbytes);
+    }
+    PF_HIP(c, hipMemcpy(M->data + g_lo * gbytes, buf.data(), buf.size(), hipMemcpyHostToDevice));
     return PF_OK;
 }
 
@@ -334,93 +325,105 @@ extern "C" void pf_matrix_free(pf_matrix* M) {
 
 // ------------------------------------------------------- kernel launches
 
-#define PF_GEMV_LAUNCH(F, MM, WV)                                                                             \
-    if (gate && ev0)                                                                                          \
-        hipExtLaunchKernelGGL((k_gemv_i8<F, MM, true, WV>), dim3(W->rows / 64, W->splits), dim3(64 * WV), 0, st, \
-                              ev0, ev1, 0, W->data, W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc,  \
-                              acc_stride, gate);                                                              \
-    else if (gate)                                                                                            \
-        hipLaunchKernelGGL((k_gemv_i8<F, MM, true, WV>), dim3(W->rows / 64, W->splits), dim3(64 * WV), 0, st,  \
-                           W->data, W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc, acc_stride, gate); \
-    else if (ev0)                                                                                             \
-        hipExtLaunchKernelGGL((k_gemv_i8<F, MM, false, WV>), dim3(W->rows / 64, W->splits), dim3(64 * WV), 0, \
-                              st, ev0, ev1, 0, W->data, W->cols, act, act_stride, bsum, bsum_stride, W->bpw,   \
-                              acc, acc_stride, gate);                                                         \
-    else                                                                                                      \
-        hipLaunchKernelGGL((k_gemv_i8<F, MM, false, WV>), dim3(W->rows / 64, W->splits), dim3(64 * WV), 0, st, \
-                           W->data, W->cols, act, act_stride, bsum, bsum_stride, W->bpw, acc, acc_stride, gate);
+// Instances of k_gemv / k_gemm in use: (prologue, epilogue, gated).
+enum MmKind : int {
+    MM_QKV = 0,       // NORM -> QKV                 (attention input)
+    MM_O = 1,         // INT8 -> RESID               (O projection)
+    MM_GU = 2,        // NORM -> SWIGLU              (gate|up)
+    MM_GU_SKIP = 3,   // QUANT -> SWIGLU, gated      (gate|up on staged normed rows, layer skip)
+    MM_DOWN = 4,      // QPART -> RESID              (down)
+    MM_DOWN_SKIP = 5, // QPART -> RESID, gated       (down, layer skip)
+    MM_STORE = 6,     // QUANT -> STORE              (kernel-level entry point)
+};
 
-#define PF_GEMV_CASE(F, MM)                                      \
-    case MM:                                                     \
-        if (W->waves == 16) { PF_GEMV_LAUNCH(F, MM, 16) }        \
-        else if (W->waves == 8) { PF_GEMV_LAUNCH(F, MM, 8) }     \
-        else { PF_GEMV_LAUNCH(F, MM, 4) }                        \
-        break;
+template <int F, int PRO, int EPI, bool G, int CPW, int MR>
+static void gemv_one(hipStream_t st, const GemvArgs& a, hipEvent_t ev0, hipEvent_t ev1) {
+    const uint32_t smem = gemv_smem(a.M, a.K);
+    static bool attr = false;   // LDS beyond 64 KiB is granted per kernel
+    if (!attr) {
+        (void)hipFuncSetAttribute((const void*)k_gemv<F, PRO, EPI, G, CPW, MR>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, gemv_smem(GEMV_MAX_M, 8192));
+        attr = true;
+    }
+    if (ev0)
+        hipExtLaunchKernelGGL((k_gemv<F, PRO, EPI, G, CPW, MR>), dim3(a.N / 32), dim3(64 * GEMV_WAVES), smem, st, ev0,
+                              ev1, 0, a);
+    else
+        hipLaunchKernelGGL((k_gemv<F, PRO, EPI, G, CPW, MR>), dim3(a.N / 32), dim3(64 * GEMV_WAVES), smem, st, a);
+}
 
-#define PF_GEMV_FMT(F)                                 \
-    switch (M) {                                       \
-        PF_GEMV_CASE(F, 1) PF_GEMV_CASE(F, 2)          \
-        PF_GEMV_CASE(F, 3) PF_GEMV_CASE(F, 4)          \
-        PF_GEMV_CASE(F, 5) PF_GEMV_CASE(F, 6)          \
-        PF_GEMV_CASE(F, 7) PF_GEMV_CASE(F, 8)          \
+// Rows held in registers: 1 (base passes), 5 (verify passes of four
+// heads), else 8.
+template <int F, int PRO, int EPI, bool G, int CPW>
+static void gemv_mr(hipStream_t st, const GemvArgs& a, hipEvent_t ev0, hipEvent_t ev1) {
+    if (a.M == 1) gemv_one<F, PRO, EPI, G, CPW, 1>(st, a, ev0, ev1);
+    else if (a.M <= 5) gemv_one<F, PRO, EPI, G, CPW, 5>(st, a, ev0, ev1);
+    else gemv_one<F, PRO, EPI, G, CPW, 8>(st, a, ev0, ev1);
+}
+
+// Chunks per wave of a K-column product: products over n_embd (<= 2048)
+// take one, those over n_ff up to four.
+template <int F, int PRO, int EPI, bool G>
+static void gemv_cpw(hipStream_t st, const GemvArgs& a, hipEvent_t ev0, hipEvent_t ev1) {
+    const uint32_t cpw = (a.K / 256 + GEMV_WAVES - 1) / GEMV_WAVES;
+    if (cpw <= 1) gemv_mr<F, PRO, EPI, G, 1>(st, a, ev0, ev1);
+    else if (cpw == 2) gemv_mr<F, PRO, EPI, G, 2>(st, a, ev0, ev1);
+    else if (cpw == 3) gemv_mr<F, PRO, EPI, G, 3>(st, a, ev0, ev1);
+    else gemv_mr<F, PRO, EPI, G, 4>(st, a, ev0, ev1);
+}
+
+template <int F, int EPI, bool G>
+static void gemm_one(hipStream_t st, const GemmArgs& a, hipEvent_t ev0, hipEvent_t ev1) {
+    const dim3 grid(a.N / 32, (a.M + 127) / 128);
+    if (ev0) hipExtLaunchKernelGGL((k_gemm<F, EPI, G>), grid, dim3(256), 0, st, ev0, ev1, 0, a);
+    else hipLaunchKernelGGL((k_gemm<F, EPI, G>), grid, dim3(256), 0, st, a);
+}
+
+#define PF_MM_FMT(fmt, CALL)                                  \
+    switch (fmt) {                                            \
+        case FMT_Q4: { constexpr int F = FMT_Q4; CALL; } break; \
+        case FMT_Q2: { constexpr int F = FMT_Q2; CALL; } break; \
+        default: { constexpr int F = FMT_Q15; CALL; } break;    \
     }
 
-// acc[M][rows] += int8 activations x tiled block matrix (exact fp64).  With
-// ev0/ev1 the dispatch carries its own start/stop events.
-static void launch_gemv(hipStream_t st, const pf_matrix* W, uint32_t M, const int8_t* act, uint32_t act_stride,
-                        const int32_t* bsum, uint32_t bsum_stride, double* acc, uint32_t acc_stride,
-                        hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr, const uint32_t* gate = nullptr) {
-    switch (W->fmt) {
-        case FMT_Q4: PF_GEMV_FMT(FMT_Q4) break;
-        case FMT_Q2: PF_GEMV_FMT(FMT_Q2) break;
-        default: PF_GEMV_FMT(FMT_Q15) break;
+// M <= 8 rows: one workgroup per 32-row group over all of K (products over
+// n_embd hold one chunk per wave).
+static void launch_gemv(hipStream_t st, const pf_matrix* W, MmKind kind, const GemvArgs& a, hipEvent_t ev0 = nullptr,
+                        hipEvent_t ev1 = nullptr) {
+    switch (kind) {
+        case MM_QKV: PF_MM_FMT(W->fmt, (gemv_mr<F, PRO_NORM, EPI_QKV, false, 1>(st, a, ev0, ev1))) break;
+        case MM_O: PF_MM_FMT(W->fmt, (gemv_mr<F, PRO_INT8, EPI_RESID, false, 1>(st, a, ev0, ev1))) break;
+        case MM_GU: PF_MM_FMT(W->fmt, (gemv_mr<F, PRO_NORM, EPI_SWIGLU, false, 1>(st, a, ev0, ev1))) break;
+        case MM_GU_SKIP: PF_MM_FMT(W->fmt, (gemv_mr<F, PRO_QUANT, EPI_SWIGLU, true, 1>(st, a, ev0, ev1))) break;
+        case MM_DOWN: PF_MM_FMT(W->fmt, (gemv_cpw<F, PRO_QPART, EPI_RESID, false>(st, a, ev0, ev1))) break;
+        case MM_DOWN_SKIP: PF_MM_FMT(W->fmt, (gemv_cpw<F, PRO_QPART, EPI_RESID, true>(st, a, ev0, ev1))) break;
+        default:
+            PF_MM_FMT(W->fmt, ({
+                          const uint32_t cpw = (a.K / 256 + GEMV_WAVES - 1) / GEMV_WAVES;
+                          if (cpw <= 1) gemv_one<F, PRO_QUANT, EPI_STORE, false, 1, 8>(st, a, ev0, ev1);
+                          else if (cpw == 2) gemv_one<F, PRO_QUANT, EPI_STORE, false, 2, 8>(st, a, ev0, ev1);
+                          else if (cpw == 3) gemv_one<F, PRO_QUANT, EPI_STORE, false, 3, 8>(st, a, ev0, ev1);
+                          else gemv_one<F, PRO_QUANT, EPI_STORE, false, 4, 8>(st, a, ev0, ev1);
+                      }))
+            break;
     }
 }
 
-// acc[M][rows] += int8 activations x tiled block matrix for M > 8 rows
-// (MFMA GEMM, exact fp64 like the GEMV).  act must hold ceil(M / 32) * 32
-// readable rows.  K splits: enough for about 256 workgroups when each wave
-// holds two or more M tiles, 512 with one (measured on MI355X at M = 64,
-// 256 and 320 over the 1B shapes).
+// M > 8 rows: activation rows quantized beforehand (int8 + scales).
+static void launch_gemm(hipStream_t st, const pf_matrix* W, MmKind kind, const GemmArgs& a, hipEvent_t ev0 = nullptr,
+                        hipEvent_t ev1 = nullptr) {
+    switch (kind) {
+        case MM_QKV: PF_MM_FMT(W->fmt, (gemm_one<F, EPI_QKV, false>(st, a, ev0, ev1))) break;
+        case MM_O:
+        case MM_DOWN: PF_MM_FMT(W->fmt, (gemm_one<F, EPI_RESID, false>(st, a, ev0, ev1))) break;
+        case MM_GU: PF_MM_FMT(W->fmt, (gemm_one<F, EPI_SWIGLU, false>(st, a, ev0, ev1))) break;
+        case MM_GU_SKIP: PF_MM_FMT(W->fmt, (gemm_one<F, EPI_SWIGLU, true>(st, a, ev0, ev1))) break;
+        case MM_DOWN_SKIP: PF_MM_FMT(W->fmt, (gemm_one<F, EPI_RESID, true>(st, a, ev0, ev1))) break;
+        default: PF_MM_FMT(W->fmt, (gemm_one<F, EPI_STORE, false>(st, a, ev0, ev1))) break;
+    }
+}
+
 constexpr uint32_t MAX_GEMM_ROWS = 512;
-
-static void launch_gemm(hipStream_t st, const pf_matrix* W, uint32_t M, const int8_t* act, uint32_t act_stride,
-                        double* acc, uint32_t acc_stride, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr,
-                        const uint32_t* gate = nullptr) {
-    const uint32_t nb = W->cols / 32, nblk = W->rows / 32;
-    const uint32_t mtw = ((M + 31) / 32 + 3) / 4;
-    const uint32_t target = mtw >= 2 ? 256 : 512;
-    uint32_t splits = std::max(1u, std::min(nb / 2, (target + nblk - 1) / nblk));
-    const uint32_t bps = (nb + splits - 1) / splits;
-    splits = (nb + bps - 1) / bps;
-    const dim3 grid(nblk, splits);
-#define PF_GEMM_CASE(F, T)                                                                                    \
-    case T:                                                                                                   \
-        if (gate && ev0)                                                                                      \
-            hipExtLaunchKernelGGL((k_gemm_i8<F, T, true>), grid, dim3(256), 0, st, ev0, ev1, 0, W->data, W->cols, \
-                                  M, act, act_stride, bps, acc, acc_stride, gate);                            \
-        else if (gate)                                                                                        \
-            hipLaunchKernelGGL((k_gemm_i8<F, T, true>), grid, dim3(256), 0, st, W->data, W->cols, M, act,       \
-                               act_stride, bps, acc, acc_stride, gate);                                       \
-        else if (ev0)                                                                                         \
-            hipExtLaunchKernelGGL((k_gemm_i8<F, T>), grid, dim3(256), 0, st, ev0, ev1, 0, W->data, W->cols, M, \
-                                  act, act_stride, bps, acc, acc_stride, gate);                                     \
-        else                                                                                                  \
-            hipLaunchKernelGGL((k_gemm_i8<F, T>), grid, dim3(256), 0, st, W->data, W->cols, M, act, act_stride, \
-                               bps, acc, acc_stride, gate);                                                         \
-        break;
-#define PF_GEMM_FMT(F)                                                            \
-    switch (mtw) {                                                                \
-        PF_GEMM_CASE(F, 1) PF_GEMM_CASE(F, 2) PF_GEMM_CASE(F, 3) PF_GEMM_CASE(F, 4) \
-    }
-    switch (W->fmt) {
-        case FMT_Q4: PF_GEMM_FMT(FMT_Q4) break;
-        case FMT_Q2: PF_GEMM_FMT(FMT_Q2) break;
-        default: PF_GEMM_FMT(FMT_Q15) break;
-    }
-#undef PF_GEMM_FMT
-#undef PF_GEMM_CASE
-}
 
 // y[m] (+= y_in[m]) = h[m] x dequantized rows, any M (launches of up to 8
 // rows; each row's result does not depend on the rows beside it).
@@ -498,39 +501,6 @@ static void launch_attn(hipStream_t st, uint32_t hd, uint32_t M, uint32_t blocks
 #undef PF_ATTN_LAUNCH
 }
 
-// Attention of a pass of fewer than 16 rows with the chunk merge and the O
-// input's quantization in the same kernel (k_attn_chunk_mq): `ablocks`
-// attention blocks, then blocks up to `blocks` that prefetch pf.
-// Model width D <= 4096.
-static void launch_attn_mq(hipStream_t st, uint32_t hd, uint32_t D, uint32_t M, uint32_t ablocks, uint32_t blocks,
-                           const PassDesc* pd, const KvGeom& g, const KvPlanes& kv, uint32_t l, uint32_t groups,
-                           const float* q, const float* k, const float* v, float* S, uint32_t s_stride, float* Wp,
-                           uint32_t cstride, uint32_t* cnt, int8_t* qo, uint32_t q_stride, float* as,
-                           int32_t* bsum, uint32_t bsum_stride, Prefetch pf, hipEvent_t ev0 = nullptr,
-                           hipEvent_t ev1 = nullptr) {
-#define PF_ATTN_MQ(P, PER)                                                                                        \
-    do {                                                                                                          \
-        if (ev0)                                                                                                  \
-            hipExtLaunchKernelGGL((k_attn_chunk_mq<P, 144u, PER>), dim3(blocks), dim3(256), 0, st, ev0, ev1, 0, pd, \
-                                  g, kv, l, M, groups, ablocks, q, k, v, S, s_stride, Wp, cstride, cnt, qo,      \
-                                  q_stride, as, bsum, bsum_stride, pf);                                         \
-        else                                                                                                      \
-            hipLaunchKernelGGL((k_attn_chunk_mq<P, 144u, PER>), dim3(blocks), dim3(256), 0, st, pd, g, kv, l, M,   \
-                               groups, ablocks, q, k, v, S, s_stride, Wp, cstride, cnt, qo, q_stride, as, bsum,   \
-                               bsum_stride, pf);                                                                 \
-    } while (0)
-#define PF_ATTN_MQ_PER(P)                          \
-    do {                                           \
-        if (D <= 1024) PF_ATTN_MQ(P, 4);           \
-        else if (D <= 2048) PF_ATTN_MQ(P, 8);      \
-        else PF_ATTN_MQ(P, 16);                    \
-    } while (0)
-    if (hd == 64) PF_ATTN_MQ_PER(4);
-    else PF_ATTN_MQ_PER(8);
-#undef PF_ATTN_MQ_PER
-#undef PF_ATTN_MQ
-}
-
 extern "C" pf_status pf_quantize_activation_rows(pf_ctx* c, const float* src, int8_t* dst, float* scales,
                                                  uint32_t M, uint32_t K) {
     if (!c || !src || !dst || !scales || M == 0) return PF_ERR_ARG;
@@ -577,30 +547,35 @@ extern "C" pf_status pf_matmul_quantized(pf_ctx* c, const float* A, const int8_t
 
 extern "C" pf_status pf_gemv_q(pf_ctx* c, const pf_matrix* W, const float* x, float* y, uint32_t M) {
     if (!c || !W || !x || !y || M == 0 || M > MAX_GEMM_ROWS) return PF_ERR_ARG;
-    if (W->rowmajor) return fail(c, PF_ERR_ARG, "pf_gemv_q needs a tiled matrix");
+    if (W->rowmajor) return fail(c, PF_ERR_ARG, "pf_gemv_q needs an int8-activation (tiled) matrix");
     const uint32_t K = W->cols, N = W->rows;
+    MmEpi e{};
+    e.y = y;
+    e.y_stride = N;
+    e.ilv = W->ilv ? 1u : 0u;
+    if (M <= GEMV_MAX_M) {
+        // the workgroups quantize x themselves: no scratch
+        GemvArgs a{};
+        a.W = W->data; a.N = N; a.K = K; a.M = M; a.x = x; a.xs = K; a.e = e;
+        launch_gemv(c->stream, W, MM_STORE, a);
+        PF_LAUNCHED(c);
+        return PF_OK;
+    }
     if (!per_for(K)) return fail(c, PF_ERR_UNSUPPORTED, "K > 8192");
-    size_t a_bytes = ((size_t)((M + 31) / 32 * 32) * K + 255) & ~(size_t)255;
-    size_t s_bytes = ((size_t)M * 4 + 255) & ~(size_t)255;
-    size_t b_bytes = (((size_t)M * (K / 32) * 4) + 255) & ~(size_t)255;
-    size_t c_bytes = (size_t)M * N * 8;
+    const size_t a_bytes = ((size_t)((M + 31) / 32 * 32) * K + 255) & ~(size_t)255;
     void* s = nullptr;
-    pf_status st = scratch(c, a_bytes + s_bytes + b_bytes + c_bytes, &s);
+    pf_status st = scratch(c, a_bytes + (size_t)M * 4, &s);
     if (st) return st;
     int8_t* act = (int8_t*)s;
     float* as = (float*)((char*)s + a_bytes);
-    int32_t* bsum = (int32_t*)((char*)as + s_bytes);
-    double* acc = (double*)((char*)bsum + b_bytes);
-    hipLaunchKernelGGL(k_zero_f64, dim3((M * N + 255) / 256), dim3(256), 0, c->stream, acc, (size_t)M * N);
     PF_PER_SWITCH(K, hipLaunchKernelGGL(k_quant_rows<PER>, dim3(M), dim3(256), 0, c->stream, x, K, K, act, K, as,
-                                        bsum, K / 32));
-    if (M <= 8) launch_gemv(c->stream, W, M, act, K, bsum, K / 32, acc, N);
-    else launch_gemm(c->stream, W, M, act, K, acc, N);
-    hipLaunchKernelGGL(k_gemv_finish, dim3((N + 255) / 256, M), dim3(256), 0, c->stream, acc, N, as, y);
+                                        (int32_t*)nullptr, 0u));
+    GemmArgs g{};
+    g.W = W->data; g.N = N; g.K = K; g.M = M; g.act = act; g.act_stride = K; g.as = as; g.e = e;
+    launch_gemm(c->stream, W, MM_STORE, g);
     PF_LAUNCHED(c);
     return PF_OK;
 }
-
 extern "C" pf_status pf_gemv_f32(pf_ctx* c, const pf_matrix* W, const float* x, float* y, uint32_t M) {
     if (!c || !W || !x || !y || M == 0 || M > 8) return PF_ERR_ARG;
     if (!W->rowmajor) return fail(c, PF_ERR_ARG, "pf_gemv_f32 needs a row-major matrix");
@@ -999,7 +974,7 @@ extern "C" pf_status pf_model_set_matrix(pf_model* m, uint32_t layer, int32_t id
     else if (id <= 5) { slot = &m->gu[layer]; rows_total = 2 * F; cols = D; row0 = (id - 4) * F; rows = F; }
     else { slot = &m->down[layer]; rows_total = D; cols = F; row0 = 0; rows = D; }
     if (!*slot) {
-        pf_status s = matrix_alloc(c, fmt, rows_total, cols, false, slot);
+        pf_status s = matrix_alloc(c, fmt, rows_total, cols, false, slot, id == 4 || id == 5);
         if (s) return s;
     } else if ((*slot)->fmt != fmt) {
         return fail(c, PF_ERR_ARG, "Q/K/V (and gate/up) of a layer must share one format");
@@ -1066,17 +1041,14 @@ struct pf_engine {
     float* rope_s = nullptr;
     uint32_t rope_pos = 0;
     // pass scratch
-    float* x = nullptr;
-    int8_t* act = nullptr;
-    float* as = nullptr;        // [4][8]
-    int32_t* bsum = nullptr;
-    double* acc = nullptr;      // GEMV accumulators [8][max(3D, 2F)], zero between uses
-    float *q = nullptr, *k = nullptr, *v = nullptr;
+    float* x = nullptr;         // residual stream [rows][D]
+    int8_t* act = nullptr;      // quantized activation rows [rows][kmax]
+    float* as = nullptr;        // their row scales [4][rows]
+    float *q = nullptr, *k = nullptr, *v = nullptr;   // [rows][D] after RoPE
+    float* sg = nullptr;        // SwiGLU output [rows][F]
+    float* pmax = nullptr;      // its per-workgroup row maxima [8][2F / 32] (decode passes)
     float* S = nullptr;
     float* Wp = nullptr;
-    uint32_t* attn_cnt = nullptr;   // per row: chunk arrivals of the fused attention, zero between launches
-    bool attn_fused = false;        // passes of < 16 rows: attention and merge in one kernel (PF_ATTN_FUSED=1;
-                                    // bit-exact, slower: 34 us against 17 + 6 us per layer at M = 5)
     uint32_t s_stride = 0, cstride = 0, kmax = 0;
     uint32_t cmax = 0;            // longest attention list (sink + pool + window)
     uint32_t prefill_rows = 8;    // rows of a prompt pass
@@ -1103,7 +1075,7 @@ struct pf_engine {
     uint32_t pool_rows_max = 1;
     bool hidden_valid = false;
     size_t max_memory = 0;
-    uint32_t pf_blocks = 128;     // prefetch blocks of the row kernels (PF_PREFETCH_BLOCKS)
+    uint32_t pf_blocks = 128;     // blocks of the attention merge that stream the O weights (PF_PREFETCH_BLOCKS)
     uint32_t* sink = nullptr;     // 4 bytes the prefetch loops never write in practice
     bool mtp_enabled = true;      // ModelConfig::mtp_enabled, include/forge/types.hpp
     // layer skip (LayerSkipController, src/layer_skip.cpp): on while the
@@ -1148,23 +1120,6 @@ struct pf_engine {
     std::map<double, std::pair<double, uint32_t>> kev_by_size;   // bytes -> (us sum, launches)
     double verify_us = 0, base_us = 0;
     uint32_t verify_n = 0, base_n = 0;
-    // persistent decode passes (M <= 8 rows; PF_PERSISTENT=1 selects them
-    // over the kernel-per-step pass)
-    bool dec = false;
-    uint32_t dec_grid = 0;             // workgroups: one per CU
-    DecodeLayer* dec_layers = nullptr;
-    uint8_t* dec_lbuf = nullptr;       // per-layer buffers of the pass
-    size_t dec_lstride = 0;
-    DecodeOffsets dec_off{};
-    uint32_t dec_s_stride = 0, dec_cstride = 0;
-    uint32_t* dec_ctr = nullptr;
-    uint32_t dec_ctr_words = 0;
-    uint32_t dec_ctr_layer = 0;
-    uint32_t* dec_glob = nullptr;      // [0] workgroups done, [16] epoch
-    uint32_t* dec_err = nullptr;
-    uint64_t* dec_trace = nullptr;     // phase timestamps of the last profiled pass
-    std::string dec_trace_path;        // PF_DECODE_TRACE: where pf_generate writes them
-    uint32_t dec_trace_grid = 0;
 };
 
 template <class T>
@@ -1189,185 +1144,6 @@ static void rope_tables(uint32_t hd, uint32_t npos, std::vector<float>& cs, std:
             cs[(size_t)p * half + t] = cosf(ang);
             sn[(size_t)p * half + t] = sinf(ang);
         }
-}
-
-// ------------------------------------------------ persistent decode pass
-
-// Kernel of pass height M (1..8) and head_dim 16 * parts.
-static const void* decode_kernel(uint32_t M, uint32_t parts) {
-#define PF_DEC_K(MM)                                                                                  \
-    case MM:                                                                                          \
-        return parts == 4 ? (const void*)k_decode<MM, 4> : (const void*)k_decode<MM, 8>;
-    switch (M) {
-        PF_DEC_K(1) PF_DEC_K(2) PF_DEC_K(3) PF_DEC_K(4) PF_DEC_K(5) PF_DEC_K(6) PF_DEC_K(7) PF_DEC_K(8)
-    }
-#undef PF_DEC_K
-    return nullptr;
-}
-
-// Counters at zero and the epoch at 1 (set-up, and after a failed pass).
-static pf_status decode_reset_sync(pf_engine* e) {
-    pf_ctx* c = e->c;
-    PF_HIP(c, hipStreamSynchronize(c->stream));
-    PF_HIP(c, hipMemset(e->dec_ctr, 0, (size_t)e->dec_ctr_words * 4));
-    std::vector<uint32_t> glob(32, 0u);
-    glob[16] = 1u;
-    PF_HIP(c, hipMemcpy(e->dec_glob, glob.data(), glob.size() * 4, hipMemcpyHostToDevice));
-    PF_HIP(c, hipMemset(e->dec_err, 0, 64));
-    return PF_OK;
-}
-
-// Buffers, per-layer descriptors and the grid of the persistent pass: one
-// workgroup per CU (PF_DECODE_WGS lowers it), all resident at once, so a
-// workgroup that waits never holds back one that has not started.
-static pf_status decode_setup(pf_engine* e) {
-    pf_ctx* c = e->c;
-    const pf_model* m = e->m;
-    const pf_model_desc& d = m->d;
-    const uint32_t D = d.n_embd, F = d.n_ff, H = d.n_heads, L = d.n_layers, MR = MAX_PASS_ROWS;
-    if (D > DEC_MAXD || D % 256 || F % 256 || (d.head_dim != 64 && d.head_dim != 128))
-        return fail(c, PF_ERR_UNSUPPORTED, "persistent pass needs n_embd <= 2048, n_embd and n_ff multiples of 256, "
-                                           "head_dim 64 or 128");
-    if ((e->cmax + 1 + 255) / 256 > DEC_MAX_CHUNKS)
-        return fail(c, PF_ERR_UNSUPPORTED, "persistent pass: attention list longer than 256 chunks");
-    int cus = 0;
-    PF_HIP(c, hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device));
-    uint32_t G = (uint32_t)cus;
-    if (const char* v = std::getenv("PF_DECODE_WGS")) G = std::max(8u, std::min(G, (uint32_t)std::strtoul(v, nullptr, 10)));
-    if (G < 8) return fail(c, PF_ERR_UNSUPPORTED, "persistent pass needs at least 8 CUs");
-    for (uint32_t M = 1; M <= MR; M++) {
-        int occ = 0;
-        PF_HIP(c, hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, decode_kernel(M, d.head_dim / 16), 256, 0));
-        if (occ < 1) return fail(c, PF_ERR_UNSUPPORTED, "decode kernel does not fit a CU");
-    }
-    e->dec_grid = G;
-    std::vector<DecodeLayer> ly(L);
-    for (uint32_t l = 0; l < L; l++) {
-        const pf_matrix* w[4] = {m->qkv[l], m->o[l], m->gu[l], m->down[l]};
-        for (int j = 0; j < 4; j++) {
-            ly[l].w[j] = w[j]->data;
-            ly[l].fmt[j] = w[j]->fmt;
-        }
-        ly[l].an = m->attn_norm + (size_t)l * D;
-        ly[l].fn = m->ffn_norm + (size_t)l * D;
-    }
-    // per-layer buffers, each on a 256-byte boundary; the chunk statistics
-    // of one (row, head) take a multiple of 64 floats, so that no cache line
-    // holds values of two heads
-    const uint32_t NCmax = (e->cmax + 1 + 255) / 256;
-    e->dec_s_stride = (2 * NCmax + 63) / 64 * 64;
-    e->dec_cstride = NCmax;
-    {
-        size_t o = 0;
-        auto take = [&](size_t bytes) {
-            const size_t r = o;
-            o += (bytes + 255) / 256 * 256;
-            return (uint32_t)r;
-        };
-        DecodeOffsets& f = e->dec_off;
-        f.xin = take((size_t)MR * D * 4);
-        f.xmid = take((size_t)MR * D * 4);
-        f.acc_qkv = take((size_t)MR * 3 * D * 8);
-        f.acc_o = take((size_t)MR * D * 8);
-        f.acc_gu = take((size_t)MR * 2 * F * 8);
-        f.acc_d = take((size_t)MR * D * 8);
-        f.rs = take(MR * 4);
-        f.amax_o = take((size_t)H * 8 * 4);
-        f.amax_f = take((size_t)(F / 64) * 8 * 4);
-        f.o = take((size_t)MR * D * 4);
-        f.f = take((size_t)MR * F * 4);
-        f.S = take((size_t)MR * H * e->dec_s_stride * 4);
-        f.Up = take((size_t)MR * H * e->dec_cstride * d.head_dim * 4);
-        f.stats_a = take((size_t)(D / 64) * 8 * 2 * 4);
-        f.stats_f = take((size_t)(D / 64) * 8 * 2 * 4);
-        e->dec_lstride = o;
-    }
-    e->dec_ctr_layer = 16 * decode_ctr_slots(H, D / 64, F / 64);
-    e->dec_ctr_words = std::max(1u, L) * e->dec_ctr_layer;
-    pf_status s = ealloc(e, &e->dec_layers, std::max(1u, L));
-    if (!s) s = ealloc(e, &e->dec_lbuf, (size_t)std::max(1u, L) * e->dec_lstride);
-    if (!s) s = ealloc(e, &e->dec_ctr, e->dec_ctr_words);
-    if (!s) s = ealloc(e, &e->dec_glob, 32);
-    if (!s) s = ealloc(e, &e->dec_err, 16);
-    if (s) return s;
-    if (L) PF_HIP(c, hipMemcpy(e->dec_layers, ly.data(), L * sizeof(DecodeLayer), hipMemcpyHostToDevice));
-    if (const char* tp = std::getenv("PF_DECODE_TRACE")) {
-        e->dec_trace_path = tp;
-        s = ealloc(e, &e->dec_trace, (size_t)std::max(1u, L) * G * DEC_TRACE);
-        if (s) return s;
-    }
-    PF_HIP(c, hipMemset(e->dec_lbuf, 0, (size_t)std::max(1u, L) * e->dec_lstride));
-    return decode_reset_sync(e);
-}
-
-// Algorithmic HBM bytes of one persistent pass of M rows whose last row
-// sees `count` entries: every layer matrix once, each visible K/V row once
-// (codes and scales), the int8 activations and fp32 outputs of the GEMVs.
-static double decode_pass_bytes(const pf_engine* e, uint32_t M, uint32_t count) {
-    const pf_model* m = e->m;
-    const pf_model_desc& d = m->d;
-    double b = 0;
-    for (uint32_t l = 0; l < d.n_layers; l++) {
-        const pf_matrix* w[4] = {m->qkv[l], m->o[l], m->gu[l], m->down[l]};
-        for (const pf_matrix* W : w) b += (double)W->bytes + (double)M * W->cols + (double)M * W->rows * 4.0;
-    }
-    b += (double)d.n_layers * d.n_heads * (double)count * (2.0 * d.head_dim + 8.0);
-    return b;
-}
-
-// Launches the persistent pass of M rows (after k_pool_rows and k_embed).
-static pf_status launch_decode(pf_engine* e, const PassDesc* pd, uint32_t M, hipEvent_t ev0, hipEvent_t ev1) {
-    pf_ctx* c = e->c;
-    const pf_model_desc& d = e->m->d;
-    hipStream_t st = c->stream;
-    DecodeArgs a{};
-    a.pd = pd;
-    a.g = e->g;
-    a.kv = e->kv;
-    a.layers = e->dec_layers;
-    a.rope_c = e->rope_c;
-    a.rope_s = e->rope_s;
-    a.L = d.n_layers;
-    a.D = d.n_embd;
-    a.F = d.n_ff;
-    a.H = d.n_heads;
-    a.hd = d.head_dim;
-    a.x = e->x;
-    a.lbuf = e->dec_lbuf;
-    a.lstride = e->dec_lstride;
-    a.off = e->dec_off;
-    a.s_stride = e->dec_s_stride;
-    a.cstride = e->dec_cstride;
-    a.ctr = e->dec_ctr;
-    a.ctr_layer = e->dec_ctr_layer;
-    a.glob = e->dec_glob;
-    a.err = e->dec_err;
-    a.spin_limit = 20000000ull;   // 0.2 s of the 100 MHz wall clock
-    a.trace = nullptr;
-    if (e->dec_trace && ev0) {     // profiled verify passes only
-        a.trace = e->dec_trace;
-        e->dec_trace_grid = e->dec_grid;
-        PF_HIP(c, hipMemsetAsync(e->dec_trace, 0, (size_t)d.n_layers * e->dec_grid * DEC_TRACE * 8, st));
-    }
-    const void* fn = decode_kernel(M, d.head_dim / 16);
-    void* args[] = {&a};
-    if (ev0) PF_HIP(c, hipEventRecord(ev0, st));
-    PF_HIP(c, hipLaunchKernel(fn, dim3(e->dec_grid), dim3(256), args, 0, st));
-    if (ev1) PF_HIP(c, hipEventRecord(ev1, st));
-    return PF_OK;
-}
-
-// Error word of the persistent passes (a wait that timed out).  After a
-// failure the counters are reset so that the engine can run again.
-static pf_status decode_check(pf_engine* e) {
-    if (!e->dec) return PF_OK;
-    uint32_t w = 0;
-    PF_HIP(e->c, hipMemcpy(&w, e->dec_err, 4, hipMemcpyDeviceToHost));
-    if (w) {
-        decode_reset_sync(e);
-        return fail(e->c, PF_ERR_HIP, "decode pass: a workgroup wait timed out (results invalid)");
-    }
-    return PF_OK;
 }
 
 static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t nseq, pf_engine** out) {
@@ -1423,18 +1199,13 @@ static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t ns
     if (!s) s = ealloc(e, &e->x, (size_t)PR * D);
     if (!s) s = ealloc(e, &e->act, (size_t)PR * e->kmax);
     if (!s) s = ealloc(e, &e->as, 4 * PR);
-    if (!s) s = ealloc(e, &e->bsum, (size_t)PR * (e->kmax / 32));
-    const size_t acc_n = (size_t)PR * std::max(3 * D, 2 * F);
-    if (!s) s = ealloc(e, &e->acc, acc_n);
     if (!s) s = ealloc(e, &e->q, (size_t)PR * D);
     if (!s) s = ealloc(e, &e->k, (size_t)PR * D);
     if (!s) s = ealloc(e, &e->v, (size_t)PR * D);
     if (!s) s = ealloc(e, &e->S, (size_t)PR * H * e->s_stride);
     if (!s) s = ealloc(e, &e->Wp, (size_t)PR * H * e->cstride * hd);
-    if (!s) s = ealloc(e, &e->attn_cnt, (size_t)PR);
-    if (!s && hipMemset(e->attn_cnt, 0, (size_t)PR * sizeof(uint32_t)) != hipSuccess)
-        s = fail(c, PF_ERR_HIP, "hipMemset of the attention counters failed");
-    if (const char* v = std::getenv("PF_ATTN_FUSED")) e->attn_fused = v[0] == '1';
+    if (!s) s = ealloc(e, &e->sg, (size_t)PR * F);
+    if (!s) s = ealloc(e, &e->pmax, (size_t)GEMV_MAX_M * (2 * F / 32));
     if (!s) s = ealloc(e, &e->logitsA, (size_t)MA * V);
     if (!s) s = ealloc(e, &e->hiddenA, (size_t)MA * D);
     if (!s) s = ealloc(e, &e->logitsB, (size_t)MR * V);
@@ -1456,18 +1227,7 @@ static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t ns
         pf_engine_destroy(e);
         return fail(c, PF_ERR_HIP, "hipHostMalloc failed");
     }
-    hipLaunchKernelGGL(k_zero_f64, dim3((acc_n + 255) / 256), dim3(256), 0, c->stream, e->acc, acc_n);
-    PF_LAUNCHED(c);
-    PF_HIP(c, hipStreamSynchronize(c->stream));
     if (const char* ng = std::getenv("PF_NO_GRAPHS")) e->use_graphs = !(ng[0] == '1');
-    {
-        const char* pv = std::getenv("PF_PERSISTENT");
-        e->dec = pv && pv[0] == '1' && nseq == 1;
-        if (e->dec && (s = decode_setup(e))) {
-            pf_engine_destroy(e);
-            return s;
-        }
-    }
     PF_HIP(c, hipEventCreate(&e->rev0));
     PF_HIP(c, hipEventCreate(&e->rev1));
     // every field of the pass descriptors defined (single-sequence passes of
@@ -1522,8 +1282,7 @@ extern "C" pf_status pf_engine_reset(pf_engine* e) {
 // Engine::set_layer_skip_threshold (src/engine.cpp:266-269) with the
 // controller's anchor interval (ModelConfig::skip_interval).  The controller
 // runs while threshold > 0; switching it on starts from zeroed caches (a new
-// controller's state).  Kernel-per-step passes only: the persistent pass is
-// not used while it runs.
+// controller's state).
 extern "C" pf_status pf_engine_set_layer_skip(pf_engine* e, float threshold, uint32_t interval) {
     if (!e) return PF_ERR_ARG;
     pf_ctx* c = e->c;
@@ -1624,12 +1383,17 @@ static pf_status harvest_events(pf_engine* e, size_t t_lo, size_t t_hi, size_t k
     return PF_OK;
 }
 
-// Int8 GEMV launch of a pass; in profiling mode the dispatches of verify
-// passes carry HIP start/stop events (kernel execution time, as rocprofv3
-// reports it).
-static pf_status pass_gemv(pf_engine* e, const pf_matrix* W, uint32_t M, const uint32_t* gate = nullptr) {
+// One int8-activation product of a pass: the GEMV (M <= 8; it quantizes
+// its own input, x / xs / nw / a8 of `a`) or, for taller passes, the GEMM
+// over act / as.  In profiling mode the dispatches of verify passes carry
+// HIP start/stop events (kernel execution time, as rocprofv3 reports it).
+static pf_status pass_mm(pf_engine* e, const pf_matrix* W, MmKind kind, uint32_t M, GemvArgs a, const float* as_in) {
     hipStream_t st = e->c->stream;
-    const uint32_t ks = e->kmax, bs = e->kmax / 32;
+    a.W = W->data;
+    a.N = W->rows;
+    a.K = W->cols;
+    a.M = M;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
     if (e->profile && e->in_verify && !e->capturing) {
         if (e->kev_used == e->kev.size()) {
             TimedPass n{};
@@ -1638,14 +1402,20 @@ static pf_status pass_gemv(pf_engine* e, const pf_matrix* W, uint32_t M, const u
             e->kev.push_back(n);
             e->kev_bytes.push_back(0.0);
         }
-        e->kev_bytes[e->kev_used] = (double)W->bytes + (double)M * W->cols + (double)M * W->rows * 4.0;
+        // weights, fp32 (or int8) input rows and fp32 outputs
+        const double in_b = kind == MM_O ? 1.0 : 4.0;
+        e->kev_bytes[e->kev_used] = (double)W->bytes + in_b * M * W->cols + 4.0 * M * W->rows;
         TimedPass* t = &e->kev[e->kev_used++];
-        if (M <= MAX_PASS_ROWS) launch_gemv(st, W, M, e->act, ks, e->bsum, bs, e->acc, W->rows, t->a, t->b, gate);
-        else launch_gemm(st, W, M, e->act, ks, e->acc, W->rows, t->a, t->b, gate);
-    } else if (M <= MAX_PASS_ROWS) {
-        launch_gemv(st, W, M, e->act, ks, e->bsum, bs, e->acc, W->rows, nullptr, nullptr, gate);
+        ev0 = t->a;
+        ev1 = t->b;
+    }
+    if (M <= GEMV_MAX_M) {
+        launch_gemv(st, W, kind, a, ev0, ev1);
     } else {
-        launch_gemm(st, W, M, e->act, ks, e->acc, W->rows, nullptr, nullptr, gate);
+        GemmArgs g{};
+        g.W = a.W; g.N = a.N; g.K = a.K; g.M = M;
+        g.act = e->act; g.act_stride = e->kmax; g.as = as_in; g.gate = a.gate; g.e = a.e;
+        launch_gemm(st, W, kind, g, ev0, ev1);
     }
     return PF_OK;
 }
@@ -1685,6 +1455,13 @@ static void launch_skip_commit(pf_engine* e, const PassDesc* pd, uint32_t M, uin
 // outputs are device [M][D] / [M][V]; either may be null.  A batched pass
 // (the descriptor gives every row its sequence and position) passes
 // batch = true and the highest position of its rows as pos_last.
+//
+// Per layer, for M <= 8 rows: QKV product (RMSNorm + quantize prologue,
+// RoPE epilogue), KV store, attention chunks, chunk merge + quantize, O
+// product (residual epilogue), gate|up product (RMSNorm + quantize
+// prologue, SwiGLU epilogue), down product (quantize prologue, residual
+// epilogue): seven kernels.  Taller passes quantize their rows in row
+// kernels and run the GEMM with the same epilogues.
 static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0, float* logits, float* hidden,
                           bool batch = false, uint32_t pos_last = 0) {
     pf_ctx* c = e->c;
@@ -1702,9 +1479,9 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
     // attention tasks: (head, 256-entry chunk) groups of M rows, 8-aligned per XCD
     const uint32_t attn_groups = H * ((cmax + 1 + 255) / 256);
     const uint32_t attn_blocks = 8 * M * ((attn_groups + 7) / 8);
-    const uint32_t ks = e->kmax, bs = e->kmax / 32;
-    // activation scales [4][rows]: each kernel reads one array and writes
-    // another, so the arrays must not overlap for any pass height
+    const uint32_t ks = e->kmax;
+    const bool tall = M > GEMV_MAX_M;
+    // activation scales [4][rows] of the tall passes' row kernels
     float* as0 = e->as;                   // attention-norm act
     float* as1 = e->as + e->rows;         // attention output act
     float* as2 = e->as + 2 * e->rows;     // ffn-norm act
@@ -1716,53 +1493,20 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
                        pd);
     hipLaunchKernelGGL(k_embed, dim3((D + 255) / 256, M), dim3(256), 0, st, m->emb->data, m->emb->scales, d.n_vocab, D,
                        pd, e->x);
-    if (e->dec && !batch && !e->skip_on && M <= MAX_PASS_ROWS && d.n_layers) {
-        // every layer in one persistent kernel; verify passes carry timing
-        // events in profiling mode
-        hipEvent_t ev0 = nullptr, ev1 = nullptr;
-        if (e->profile && e->in_verify && !e->capturing) {
-            if (e->kev_used == e->kev.size()) {
-                TimedPass n{};
-                PF_HIP(c, hipEventCreate(&n.a));
-                PF_HIP(c, hipEventCreate(&n.b));
-                e->kev.push_back(n);
-                e->kev_bytes.push_back(0.0);
-            }
-            e->kev_bytes[e->kev_used] = decode_pass_bytes(e, M, kv_view(g, pos0 + M - 1).count());
-            TimedPass* t = &e->kev[e->kev_used++];
-            ev0 = t->a;
-            ev1 = t->b;
-        }
-        if (pf_status s = launch_decode(e, pd, M, ev0, ev1)) return s;
-        if (hidden)
-            hipLaunchKernelGGL(k_copy_f32, dim3((M * D + 255) / 256), dim3(256), 0, st, (const float*)e->x, hidden,
-                               M * D);
-        if (logits) launch_gemv_f32(st, m->emb, M, e->x, D, logits, d.n_vocab, nullptr);
-        PF_LAUNCHED(c);
-        if (!e->capturing) e->hidden_valid = true;
-        return PF_OK;
-    }
     for (uint32_t l = 0; l < d.n_layers; l++) {
         const float* an = m->attn_norm + (size_t)l * D;
         const float* fn = m->ffn_norm + (size_t)l * D;
-        // row kernels carry e->pf_blocks extra blocks that stream the next
-        // GEMV's weights into the MALL while the rows are processed
-        const uint32_t rb = M + e->pf_blocks;
-        const uint32_t* skip_prev = (e->skip_on && l > 0) ? e->skip_flags + (size_t)(l - 1) * e->rows : nullptr;
-        if (e->skip_on) {
-            PF_PER1024_SWITCH(D, hipLaunchKernelGGL((k_resid_norm_quant<PER, true>), dim3(rb), dim3(1024), 0, st,
-                                                    e->x, D, l == 0 ? (double*)nullptr : e->acc, as3, an, e->act, ks,
-                                                    as0, e->bsum, bs, M, prefetch_of(e, m->qkv[l]), skip_prev,
-                                                    (float*)nullptr, e->skip_nrun + l));
-        } else {
-            PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(rb), dim3(1024), 0, st, e->x, D,
-                                                    l == 0 ? (double*)nullptr : e->acc, as3, an, e->act, ks, as0,
-                                                    e->bsum, bs, M, prefetch_of(e, m->qkv[l]),
-                                                    (const uint32_t*)nullptr, (float*)nullptr, (uint32_t*)nullptr));
-        }
-        if (pf_status s = pass_gemv(e, m->qkv[l], M)) return s;
-        hipLaunchKernelGGL(k_qkv_post, dim3(M, H), dim3(64), 0, st, e->acc, as0, pd, e->rope_c, e->rope_s, g, e->kv, l,
-                           e->q, e->k, e->v);
+        // Q/K/V with RoPE (src/engine.cpp:515-523, 693-749)
+        GemvArgs a{};
+        a.e.q = e->q; a.e.k = e->k; a.e.v = e->v;
+        a.e.rc = e->rope_c; a.e.rs = e->rope_s; a.e.pd = pd; a.e.D = D; a.e.hd = hd;
+        a.x = e->x; a.xs = D; a.nw = an;
+        if (tall)
+            PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_norm_quant<PER>, dim3(M), dim3(1024), 0, st, (const float*)e->x,
+                                                    D, an, e->act, ks, as0));
+        if (pf_status s = pass_mm(e, m->qkv[l], MM_QKV, M, a, as0)) return s;
+        hipLaunchKernelGGL(k_kv_store_pass, dim3(M, H), dim3(64), 0, st, (const PassDesc*)pd, g, e->kv, l,
+                           (const float*)e->k, (const float*)e->v);
         hipEvent_t aev0 = nullptr, aev1 = nullptr;
         if (e->profile && e->in_verify && !e->capturing) {
             if (e->aev_used == e->aev.size()) {
@@ -1775,49 +1519,57 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
             aev1 = e->aev[e->aev_used].b;
             e->aev_used++;
         }
-        if (e->attn_fused && M < 16 && D <= 4096) {
-            launch_attn_mq(st, hd, D, M, attn_blocks, attn_blocks + 4 * e->pf_blocks, pd, g, e->kv, l, attn_groups,
-                           e->q, e->k, e->v, e->S, e->s_stride, e->Wp, e->cstride, e->attn_cnt, e->act, ks, as1,
-                           e->bsum, bs, prefetch_of(e, m->o[l]), aev0, aev1);
-        } else {
-            launch_attn(st, hd, M, attn_blocks, pd, g, e->kv, l, attn_groups, e->q, e->k, e->v, e->S, e->s_stride,
-                        e->Wp, e->cstride, aev0, aev1);
-            PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_attn_merge_quant<PER>, dim3(rb), dim3(1024), 0, st, pd, g,
-                                                    (const float*)e->S, e->s_stride, (const float*)e->Wp, e->cstride,
-                                                    e->act, ks, as1, e->bsum, bs, M, prefetch_of(e, m->o[l])));
-        }
-        if (pf_status s = pass_gemv(e, m->o[l], M)) return s;
-        // with layer skip on, the FFN products run only if some row needs
-        // them (gate word)
-        float* nout = e->skip_on ? e->skip_stage + (size_t)l * e->rows * D : nullptr;
-        const uint32_t* gate = e->skip_on ? e->skip_nrun + l : nullptr;
+        launch_attn(st, hd, M, attn_blocks, pd, g, e->kv, l, attn_groups, e->q, e->k, e->v, e->S, e->s_stride, e->Wp,
+                    e->cstride, aev0, aev1);
+        // chunk merge and the O input's quantization; the extra blocks stream
+        // the O weights through the cache hierarchy
+        PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_attn_merge_quant<PER>, dim3(M + e->pf_blocks), dim3(1024), 0, st, pd,
+                                                g, (const float*)e->S, e->s_stride, (const float*)e->Wp, e->cstride,
+                                                e->act, ks, as1, (int32_t*)nullptr, 0u, M, prefetch_of(e, m->o[l])));
+        // O projection + residual (src/engine.cpp:789-800)
+        a = GemvArgs{};
+        a.a8 = e->act; a.a8s = as1; a.xs = ks;
+        a.e.y = e->x; a.e.y_stride = D;
+        if (pf_status s = pass_mm(e, m->o[l], MM_O, M, a, as1)) return s;
+        // FFN (src/engine.cpp:526-541, 805-854); with layer skip on, the
+        // normed rows are staged for the skip decisions and the products run
+        // only if some row needs them (gate word)
+        a = GemvArgs{};
+        a.e.y = e->sg; a.e.y_stride = F;
+        a.e.pmax = tall ? nullptr : e->pmax;
         if (e->skip_on) {
-            PF_PER1024_SWITCH(D, hipLaunchKernelGGL((k_resid_norm_quant<PER, true>), dim3(rb), dim3(1024), 0, st,
-                                                    e->x, D, e->acc, as1, fn, e->act, ks, as2, e->bsum, bs, M,
-                                                    prefetch_of(e, m->gu[l]), (const uint32_t*)nullptr, nout,
-                                                    (uint32_t*)nullptr));
-        } else {
-            PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_resid_norm_quant<PER>, dim3(rb), dim3(1024), 0, st, e->x, D,
-                                                    e->acc, as1, fn, e->act, ks, as2, e->bsum, bs, M,
-                                                    prefetch_of(e, m->gu[l]), (const uint32_t*)nullptr,
-                                                    (float*)nullptr, (uint32_t*)nullptr));
-        }
-        if (e->skip_on)
+            float* nout = e->skip_stage + (size_t)l * e->rows * D;
+            PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_norm_rows<PER>, dim3(M), dim3(1024), 0, st, (const float*)e->x, D,
+                                                    fn, nout, e->skip_nrun + l));
             hipLaunchKernelGGL(k_layer_skip, dim3(e->nseq), dim3(1024), 0, st, (const PassDesc*)pd, M,
                                (const float*)nout, (const float*)e->skip_cache + (size_t)l * D,
                                (size_t)d.n_layers * D, D, skip_threshold(e, l), e->skip_flags + (size_t)l * e->rows,
                                e->skip_nrun + l);
-        if (pf_status s = pass_gemv(e, m->gu[l], M, gate)) return s;
-        PF_PER1024_SWITCH(F, hipLaunchKernelGGL(k_swiglu_quant<PER>, dim3(rb), dim3(1024), 0, st, e->acc,
-                                                (const float*)as2, F, e->act, ks, as3, e->bsum, bs, M,
-                                                prefetch_of(e, m->down[l])));
-        if (pf_status s = pass_gemv(e, m->down[l], M, gate)) return s;
+            a.x = nout; a.xs = D; a.gate = e->skip_nrun + l;
+            if (tall)
+                PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_quant_rows_wide<PER>, dim3(M), dim3(1024), 0, st,
+                                                        (const float*)nout, D, e->act, ks, as2, (int32_t*)nullptr, 0u));
+            if (pf_status s = pass_mm(e, m->gu[l], MM_GU_SKIP, M, a, as2)) return s;
+        } else {
+            a.x = e->x; a.xs = D; a.nw = fn;
+            if (tall)
+                PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_norm_quant<PER>, dim3(M), dim3(1024), 0, st,
+                                                        (const float*)e->x, D, fn, e->act, ks, as2));
+            if (pf_status s = pass_mm(e, m->gu[l], MM_GU, M, a, as2)) return s;
+        }
+        // down + residual; rows whose FFN was skipped take no residual
+        a = GemvArgs{};
+        a.x = e->sg; a.xs = F; a.pin = e->pmax; a.np = 2 * F / 32;
+        a.e.y = e->x; a.e.y_stride = D;
+        if (e->skip_on) {
+            a.gate = e->skip_nrun + l;
+            a.e.skipm = e->skip_flags + (size_t)l * e->rows;
+        }
+        if (tall)
+            PF_PER1024_SWITCH(F, hipLaunchKernelGGL(k_quant_rows_wide<PER>, dim3(M), dim3(1024), 0, st,
+                                                    (const float*)e->sg, F, e->act, ks, as3, (int32_t*)nullptr, 0u));
+        if (pf_status s = pass_mm(e, m->down[l], e->skip_on ? MM_DOWN_SKIP : MM_DOWN, M, a, as3)) return s;
     }
-    if (d.n_layers)
-        hipLaunchKernelGGL(k_resid_add, dim3((D + 255) / 256, M), dim3(256), 0, st, e->x, D, e->acc,
-                           (const float*)as3,
-                           e->skip_on ? (const uint32_t*)e->skip_flags + (size_t)(d.n_layers - 1) * e->rows
-                                      : (const uint32_t*)nullptr);
     // every row of a pass counts for the skip caches except in verify passes,
     // whose caller commits the rows the acceptance keeps
     if (e->skip_on && !e->in_verify) launch_skip_commit(e, pd, M, 0, 0xFFFFFFFFu, false);
@@ -1852,7 +1604,7 @@ extern "C" pf_status pf_forward(pf_engine* e, const int32_t* tokens, uint32_t n,
         PF_HIP(c, hipMemcpyAsync(logits, e->logitsA, (size_t)n * d.n_vocab * 4, hipMemcpyDeviceToHost, c->stream));
     if (hidden) PF_HIP(c, hipMemcpyAsync(hidden, e->hiddenA, (size_t)n * d.n_embd * 4, hipMemcpyDeviceToHost, c->stream));
     PF_HIP(c, hipStreamSynchronize(c->stream));
-    return decode_check(e);
+    return PF_OK;
 }
 
 // MTPHeads::forward chain on the device hidden state h0 (src/mtp.cpp:63-127):
@@ -2139,20 +1891,6 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
     PF_HIP(c, hipMemcpyAsync(&sf, e->st, sizeof(sf), hipMemcpyDeviceToHost, st));
     PF_HIP(c, hipStreamSynchronize(st));
     auto t2 = std::chrono::steady_clock::now();
-    if (pf_status s = decode_check(e)) return s;
-    if (e->dec_trace && !e->dec_trace_path.empty() && e->dec_trace_grid) {
-        // header: layers, grid, words per workgroup; then the timestamps
-        const size_t n = (size_t)d.n_layers * e->dec_trace_grid * DEC_TRACE;
-        std::vector<uint64_t> buf(3 + n);
-        buf[0] = d.n_layers;
-        buf[1] = e->dec_trace_grid;
-        buf[2] = DEC_TRACE;
-        PF_HIP(c, hipMemcpy(buf.data() + 3, e->dec_trace, n * 8, hipMemcpyDeviceToHost));
-        if (FILE* fp = std::fopen(e->dec_trace_path.c_str(), "wb")) {
-            std::fwrite(buf.data(), 8, buf.size(), fp);
-            std::fclose(fp);
-        }
-    }
     if (sf.pos != e->pos) return fail(c, PF_ERR_STATE, "device and host positions diverged");
     const uint32_t nt = std::min(sf.n_tokens, tokens_cap);
     PF_HIP(c, hipMemcpy(tokens_out, e->tokens, (size_t)nt * 4, hipMemcpyDeviceToHost));

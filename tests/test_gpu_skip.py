@@ -91,11 +91,9 @@ def test_skip_generate_matches_oracle(gpu, w8, case, thr, interval, samp, graphs
     m.close()
 
 
-def test_skip_off_leaves_persistent_pass_and_outputs(gpu, w8, monkeypatch):
-    """Threshold 0 is off: the stream equals the oracle's without skipping,
-    also with the persistent pass selected; switching on falls back to the
-    kernel-per-step pass and still matches."""
-    monkeypatch.setenv("PF_PERSISTENT", "1")
+def test_skip_off_leaves_outputs(gpu, w8):
+    """Threshold 0 is off: the stream equals the oracle's without skipping;
+    switched on it still matches the oracle's controller."""
     prompt = W.prompt_ids(12, CFG["n_vocab"], seed=21)
     m = pf.Model(gpu, CFG, w8)
     for thr in (0.0, 0.1):
