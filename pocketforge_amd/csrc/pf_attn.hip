@@ -2,12 +2,14 @@
 //
 // A pass of M rows at consecutive positions p0..p0+M-1 runs, per layer
 // (after the Q/K/V product, whose epilogue applies RoPE, pf_mm.hip):
-//   k_kv_store_pass  int8 K/V rows of each pass row written to the plane row
-//                  of its position (sink slot or ring slot; the ring has
-//                  slack, so pending rows of a verify pass never overwrite a
-//                  visible entry)
-//   k_attn_chunk   per (row, head, 256-entry chunk of the row's list):
-//                  scores, chunk max, exp, chunk sum and chunk-weighted V
+//   k_kv_store_pass  (passes of more than 8 rows) int8 K/V rows of each pass
+//                  row written to the plane row of its position (sink slot
+//                  or ring slot; the ring has slack, so pending rows of a
+//                  verify pass never overwrite a visible entry)
+//   k_attn_group   per (head, 256-entry chunk, group of rows whose lists
+//                  extend each other): scores, chunk max, exp, chunk sum and
+//                  chunk-weighted V of each row; passes of at most 8 rows
+//                  also quantize and store their own K/V rows here
 //   k_attn_merge_quant  per row: chunks rescaled to the row max and merged,
 //                  then the O projection's quantize_activation_row
 // The KVCache API (raw scores; weighted sum of caller probabilities) runs
@@ -279,157 +281,393 @@ __global__ void k_wsum_combine_one(const float* __restrict__ Wp, uint32_t nch, u
 // S[(m*H + h)*s_stride + 2c] = m_c, [.. + 2c + 1] = T_c and
 // Up[((m*H + h)*cstride + c)*hd + i] = U_c[i].
 
-// Shared memory of one attention block (bytes): V rows of the chunk first,
-// VROW bytes each.  VROW = 136 (8 bytes of padding) keeps the block under
-// 40 KB, so four blocks fit in a CU's 160 KB: passes of many rows.  VROW =
-// 144 (16-byte rows, one 16-byte store per part) for passes of a few rows,
-// whose grids do not fill the CUs anyway.
-constexpr uint32_t att_vt(uint32_t vrow) { return 256 * vrow; }
-constexpr uint32_t att_smem(uint32_t vrow) { return att_vt(vrow) + (128 + 128 + 256 + 256 + 512 + 4) * 4; }
+// ------------------------------------------------- grouped attention
 
-template <int PARTS, uint32_t VROW = 144>
-__device__ __forceinline__ void attn_one_row(const PassDesc* __restrict__ pd, const KvGeom& g, const KvPlanes& kv,
-                                             uint32_t layer, uint32_t m, uint32_t h, uint32_t c,
-                                             const float* __restrict__ q, const float* __restrict__ kself,
-                                             const float* __restrict__ vself, float* __restrict__ S,
-                                             uint32_t s_stride, float* __restrict__ Up, uint32_t cstride,
-                                             uint8_t* smem) {
-    constexpr uint32_t hd = 16 * PARTS;
-    int8_t (*vt)[VROW] = reinterpret_cast<int8_t (*)[VROW]>(smem);
-    float* qs = reinterpret_cast<float*>(smem + att_vt(VROW));
-    float* kss = qs + 128;
-    float* vsc = kss + 128;
-    float* pe = vsc + 256;
-    float* wp = pe + 256;                           // [4][128]
-    float* red = wp + 512;
-    const uint32_t t = threadIdx.x;
-    const uint32_t D = g.n_heads * hd;
-    const KvView v = kv_view(g, row_pos(pd, m));
-    const uint32_t C = v.count(), n = C + 1, j0 = c * 256u;
-    if (j0 >= n) return;
-    const uint32_t j = j0 + t;
-    const size_t plane = plane_index(g, row_seq(pd, m), layer, h);
-    const size_t qrow = (size_t)m * D + h * hd;
-    const uint32_t nvis = j0 < C ? min(256u, C - j0) : 0u;
-    // every load first: the query, the fp32 self key, this thread's K and V rows
-    if (t < hd) {
-        qs[t] = q[qrow + t];
-        kss[t] = kself[qrow + t];
-    }
-    int4 kw[PARTS];
-    float ks = 0.0f, vs = 0.0f;
-    if (t < nvis) {
-        const size_t row = plane * g.rows + kv_row(g, v, j);
-        const int4* kr = reinterpret_cast<const int4*>(kv.k + row * hd);
-        const int4* vr = reinterpret_cast<const int4*>(kv.v + row * hd);
-        int4 vw[PARTS];
-#pragma unroll
-        for (int p = 0; p < PARTS; p++) {
-            kw[p] = kr[p];
-            vw[p] = vr[p];
-        }
-        ks = kv.ks[row];
-        vs = kv.vs[row];
-#pragma unroll
-        for (int p = 0; p < PARTS; p++) {
-            if constexpr (VROW % 16 == 0) {
-                *reinterpret_cast<int4*>(&vt[t][p * 16]) = vw[p];
-                continue;
-            }
-            *reinterpret_cast<int2*>(&vt[t][p * 16]) = make_int2(vw[p].x, vw[p].y);
-            *reinterpret_cast<int2*>(&vt[t][p * 16 + 8]) = make_int2(vw[p].z, vw[p].w);
-        }
-    }
-    vsc[t] = vs;                 // 0 past the visible entries: their terms below add exactly 0
-    __syncthreads();
-    const float scale = 1.0f / __builtin_sqrtf((float)hd);
-    float s = -__builtin_inff();
-    if (t < nvis) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int p = 0; p < PARTS; p++) {
-            const int wv[4] = {kw[p].x, kw[p].y, kw[p].z, kw[p].w};
-#pragma unroll
-            for (int b = 0; b < 16; b++) {
-                const int8_t cb = (int8_t)((wv[b >> 2] >> (8 * (b & 3))) & 0xFF);
-                acc = __builtin_fmaf(qs[p * 16 + b], (float)cb * ks, acc);
-            }
-        }
-        s = acc * scale;
-    } else if (j == C) {
-        float self = 0.0f;
-#pragma unroll
-        for (uint32_t i = 0; i < hd; i++) self = self + qs[i] * kss[i];
-        s = self * scale;
-    }
-    const float mx = block_max<4>(s, red);
-    const float ex = j < n ? expf_c(s - mx) : 0.0f;
-    pe[t] = ex;
-    const float T = block_canon_sum<4>(ex, red);       // its barriers publish pe
-    const uint32_t sc = t >> 6, i0 = 2u * (t & 63u);
-    if (i0 < hd) {
-        float w0 = 0.0f, w1 = 0.0f;
-        // entries [64sc, min(64sc + 64, nvis)) in groups of 8; the padding
-        // entries up to the next multiple of 8 have v_scale 0 and finite
-        // codes and weights, so fmaf(e, code * 0, w) == w
-        const uint32_t e_end = min(64u * sc + 64u, (nvis + 7u) & ~7u);
-        for (uint32_t e = 64u * sc; e < e_end; e += 8) {
-            float pp[8], vv[8];
-            uint32_t cc[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                pp[u] = pe[e + u];
-                vv[u] = vsc[e + u];
-                cc[u] = *reinterpret_cast<const uint16_t*>(&vt[e + u][i0]);
-            }
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                w0 = __builtin_fmaf(pp[u], (float)(int8_t)(cc[u] & 0xFFu) * vv[u], w0);
-                w1 = __builtin_fmaf(pp[u], (float)(int8_t)(cc[u] >> 8) * vv[u], w1);
-            }
-        }
-        const uint32_t js = C - j0;                     // list index of the self entry in the chunk
-        if (js < 256u && (js >> 6) == sc) {
-            const float p = pe[js];
-            w0 = __builtin_fmaf(p, vself[qrow + i0], w0);
-            w1 = __builtin_fmaf(p, vself[qrow + i0 + 1], w1);
-        }
-        wp[sc * 128 + i0] = w0;
-        wp[sc * 128 + i0 + 1] = w1;
-    }
-    __syncthreads();
-    const size_t mh = (size_t)m * g.n_heads + h;
-    if (t < hd) {
-        float u = 0.0f;
-        u = u + wp[t];
-        u = u + wp[128 + t];
-        u = u + wp[256 + t];
-        u = u + wp[384 + t];
-        Up[(mh * cstride + c) * hd + t] = u;
-    }
-    if (t == 0) {
-        S[mh * s_stride + 2 * c] = mx;
-        S[mh * s_stride + 2 * c + 1] = T;
-    }
+// Rows b = a + 1 of one sequence whose lists extend each other: b sees a's
+// entries plus one more, the store of a's position (same sink and pooled
+// counts, same oldest window entry).  Chunk c then holds the same entries
+// for both, so one block serves both rows.
+__device__ __forceinline__ bool rows_aligned(const KvGeom& g, const PassDesc* pd, uint32_t a, uint32_t b) {
+    if (row_seq(pd, a) != row_seq(pd, b)) return false;
+    const uint32_t pa = row_pos(pd, a), pb = row_pos(pd, b);
+    if (pb != pa + 1u) return false;
+    // kv_view without the pooled count (equal win_lo gives equal counts)
+    const uint32_t s_eff = min(g.sink_size, KV_SINK_ROWS);
+    const uint32_t na = min(pa, g.max_context), nb = min(pb, g.max_context);
+    const uint32_t wa = na > g.sink_size ? na - g.sink_size : 0u, wb = nb > g.sink_size ? nb - g.sink_size : 0u;
+    const uint32_t la = wa > g.window ? wa - g.window : 0u, lb = wb > g.window ? wb - g.window : 0u;
+    return min(na, s_eff) == min(nb, s_eff) && la == lb && wb == wa + 1u;
 }
 
-// 1-D grid of 8 * M * ceil(G / 8) blocks, G = H * chunks, task group
-// grp = c * H + h.  Blocks are dealt to the 8 XCDs round-robin, so block b
-// runs on XCD b mod 8: group grp's M rows get blocks with b mod 8 = grp mod
-// 8, and after the first row a chunk's K/V rows come from that XCD's L2.
-// 256 threads; head_dim = 16 * PARTS; V rows of VROW bytes in LDS.
-template <int PARTS, uint32_t VROW>
-__global__ __launch_bounds__(256) void k_attn_chunk(const PassDesc* __restrict__ pd, KvGeom g, KvPlanes kv,
-                                                    uint32_t layer, uint32_t M, uint32_t n_groups,
-                                                    const float* __restrict__ q, const float* __restrict__ kself,
-                                                    const float* __restrict__ vself, float* __restrict__ S,
-                                                    uint32_t s_stride, float* __restrict__ Up, uint32_t cstride) {
-    __shared__ __align__(16) uint8_t smem[att_smem(VROW)];
-    const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
-    const uint32_t grp = (slot / M) * 8u + xcd, m = slot % M;
-    if (grp >= n_groups || m >= pd->m) return;
-    attn_one_row<PARTS, VROW>(pd, g, kv, layer, m, grp % g.n_heads, grp / g.n_heads, q, kself, vself, S, s_stride,
-                              Up, cstride, smem);
+// Position of visible entry j of a view (sink slot j holds position j,
+// window entry w position sink_size + w); pooled rows have none (UINT32_MAX).
+__device__ __forceinline__ uint32_t entry_pos(const KvGeom& g, const KvView& v, uint32_t j) {
+    if (j < v.sink) return j;
+    j -= v.sink;
+    if (j < v.pool) return 0xFFFFFFFFu;
+    return g.sink_size + v.win_lo + (j - v.pool);
+}
+
+// List index of position P in view v, or UINT32_MAX when v does not show it.
+__device__ __forceinline__ uint32_t list_index(const KvGeom& g, const KvView& v, uint32_t P) {
+    if (P < g.sink_size) return P < v.sink ? P : 0xFFFFFFFFu;
+    const uint32_t w = P - g.sink_size;
+    if (w < v.win_lo || w >= v.win_hi) return 0xFFFFFFFFu;
+    return v.sink + v.pool + (w - v.win_lo);
+}
+
+// kv_row for the entries j >= wstart of one chunk, wstart = max(j0,
+// sink + pool) and wb = kv_row's ring index of entry wstart (one division
+// per block instead of one per entry).
+__device__ __forceinline__ uint32_t chunk_row(const KvGeom& g, const KvView& v, uint32_t j, uint32_t wstart,
+                                              uint32_t wb) {
+    if (j < v.sink) return j;
+    if (j < wstart) return KV_SINK_ROWS + g.ring + (j - v.sink);
+    uint32_t x = wb + (j - wstart);
+    x = g.ring >= 256u ? (x >= g.ring ? x - g.ring : x) : x % g.ring;
+    return KV_SINK_ROWS + x;
+}
+
+constexpr uint32_t AG_MAX_ROWS = 8;   // rows of one attention group
+
+// LDS of k_attn_group (bytes): K and V rows of the chunk, 32 KB each, their
+// scales [2][256], the group's queries and self keys [NR][128] fp32 each,
+// probabilities [NR][256], wave maxima and sums [2][NR][4], self weights
+// [NR].  The V partials [NR][4][128] reuse the K rows.  K is stored by
+// 16-byte part: part p of entry e at slot p * 256 + (e ^ p), so that the
+// 8 lanes writing one row and the lanes reading part p of consecutive rows
+// both fall on distinct banks.  V rows are plain [256][128].
+constexpr uint32_t ag_smem(uint32_t nr) { return 2u * 256u * 128u + (512u + nr * (256u + 256u + 8u + 1u)) * 4u; }
+
+// Engine attention of every row of a pass (the first stage above), one
+// block per (head h, 256-entry chunk c, share of a group of rows), with the
+// chunk's K and V rows loaded once, coalesced, into LDS for all the rows
+// the block serves.
+//
+// Groups are the runs of aligned rows inside each 8-row slice of the pass
+// (rows 8s .. 8s + 7); the lists of a group's rows are prefixes of its last
+// row's list: row r of the group sees C + r entries (C the count of its
+// first row), then its fp32 self entry at list index C + r.  A group of n
+// rows is served by ceil(n / NR) blocks of at most NR rows each.
+// Grid (heads * chunks, M), 256 threads: block (x, m) serves share
+// m - m0 of the group led by row m0 (if that share exists).
+//
+// FUSED (passes of at most 8 rows): the pass's own K/V rows are not yet in
+// the cache.  Entries at positions of this pass are quantized here from the
+// fp32 k / v rows (KVCache::quantize_row arithmetic, as store_pair), and the
+// block whose chunk holds row r's self entry writes row r's K/V to the
+// cache (src/kv_cache.cpp:59-127).  The ring's slack keeps those rows out
+// of every list of the pass, so blocks still reading other chunks never see
+// them change.  Otherwise k_kv_store_pass has stored the pass's rows.
+template <int PARTS, bool FUSED, int NR>
+__global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__ pd, KvGeom g, KvPlanes kv,
+                                                    uint32_t layer, uint32_t M, const float* __restrict__ q,
+                                                    const float* __restrict__ kself, const float* __restrict__ vself,
+                                                    float* __restrict__ S, uint32_t s_stride,
+                                                    float* __restrict__ Up, uint32_t cstride) {
+    constexpr uint32_t hd = 16 * PARTS;
+    __shared__ __align__(16) uint8_t smem[ag_smem(NR)];
+    int4* kt = reinterpret_cast<int4*>(smem);                       // [PARTS][256], swizzled
+    int8_t (*vt)[128] = reinterpret_cast<int8_t (*)[128]>(smem + 256u * 128u);
+    float* ksc = reinterpret_cast<float*>(smem + 512u * 128u);      // [256]
+    float* vsc = ksc + 256;                                         // [256]
+    float* qs = vsc + 256;                                          // [NR][128]
+    float* kss = qs + NR * 128;                                     // [NR][128]
+    float* pe = kss + NR * 128;                                     // [NR][256]
+    float* rmx = pe + NR * 256;                                     // [NR][4] wave maxima
+    float* rsm = rmx + NR * 4;                                      // [NR][4] wave sums
+    float* pself = rsm + NR * 4;                                    // [NR]
+    float* wp = reinterpret_cast<float*>(smem);                     // [NR][4][128], after the scores
+
+    const uint32_t H = g.n_heads, h = blockIdx.x % H, c = blockIdx.x / H, m0 = blockIdx.y;
+    const uint32_t t = threadIdx.x, lane = t & 63u, wid = t >> 6;
+    const uint32_t Mp = min(M, pd->m);
+    if (m0 >= Mp) return;
+    // lane l < 8: row base + l starts a group (not aligned with row base + l - 1)
+    const uint32_t base = m0 & ~7u;
+    bool st = true;
+    if (lane >= 1u && lane < 8u && base + lane < Mp) st = !rows_aligned(g, pd, base + lane - 1u, base + lane);
+    const uint32_t starts = (uint32_t)__ballot(st) & 0xFFu;
+    const uint32_t k = m0 - base;                                   // this block's row in the slice
+    const uint32_t lead = 31u - (uint32_t)__builtin_clz(starts & ((2u << k) - 1u));
+    const uint32_t after = starts & ~((2u << lead) - 1u);           // starts of the later groups
+    const uint32_t glen = min(after ? (uint32_t)__builtin_ctz(after) : 8u, Mp - base) - lead;
+    const uint32_t nsh = (glen + NR - 1u) / NR, share = k - lead;
+    if (share >= nsh) return;                                       // no share for this block
+    const uint32_t per = (glen + nsh - 1u) / nsh;
+    const uint32_t mb = base + lead + share * per;                  // first row of this block
+    const uint32_t G = min(per, glen - share * per);
+    const KvView vL = kv_view(g, row_pos(pd, mb + G - 1u));         // the longest list
+    const uint32_t CL = vL.count(), C0 = CL - (G - 1u), j0 = 256u * c;
+    if (j0 > CL) return;                                            // past the last row's self entry
+    const uint32_t D = H * hd, seq = row_seq(pd, mb);
+    const size_t plane = plane_index(g, seq, layer, h);
+    const uint32_t nvis = j0 < CL ? min(256u, CL - j0) : 0u;
+    const uint32_t wstart = max(j0, vL.sink + vL.pool), wb = (vL.win_lo + (wstart - vL.sink - vL.pool)) % g.ring;
+    // FUSED: the sequence's first row in the pass; entries at its position
+    // or later are the pass's own rows
+    uint32_t first = mb, p_first = 0xFFFFFFFFu;
+    if constexpr (FUSED) {
+        while (first > 0 && row_seq(pd, first - 1u) == seq) first--;
+        p_first = row_pos(pd, first);
+    }
+
+    // ---- loads, all issued before any is used
+    // the group's queries and self keys: element i = t + 256 k of [NR][hd]
+    constexpr uint32_t QPT = (NR * hd + 255u) / 256u;
+    float qv[QPT], kvv[QPT];
+#pragma unroll
+    for (uint32_t k = 0; k < QPT; k++) {
+        const uint32_t i = t + 256u * k, r = i / hd, d = i - r * hd;
+        qv[k] = 0.0f;
+        kvv[k] = 0.0f;
+        if (r < G) {
+            const size_t o = (size_t)(mb + r) * D + h * hd + d;
+            qv[k] = q[o];
+            kvv[k] = kself[o];
+        }
+    }
+    // FUSED: wave w quantizes pass rows first + w and first + w + 4 (at most
+    // 8 rows in the pass), two elements per lane
+    const uint32_t nq = FUSED ? mb + G - first : 0u;
+    float fk[2][2], fv[2][2];
+#pragma unroll
+    for (uint32_t u = 0; u < 2; u++) {
+        const uint32_t i = wid + 4u * u;
+        fk[u][0] = fk[u][1] = fv[u][0] = fv[u][1] = 0.0f;
+        if (i < nq && 2u * lane < hd) {
+            const size_t o = (size_t)(first + i) * D + h * hd + 2u * lane;
+            fk[u][0] = kself[o];
+            fk[u][1] = kself[o + 1];
+            fv[u][0] = vself[o];
+            fv[u][1] = vself[o + 1];
+        }
+    }
+    // K and V rows: 16-byte piece pi = t + 256 i is part pi % PARTS of
+    // entry pi / PARTS, so a wave reads 64 / PARTS whole rows per load
+    int4 kw[PARTS], vw[PARTS];
+#pragma unroll
+    for (uint32_t i = 0; i < (uint32_t)PARTS; i++) {
+        const uint32_t pi = t + 256u * i, e = pi / PARTS, part = pi % PARTS;
+        kw[i] = make_int4(0, 0, 0, 0);
+        vw[i] = make_int4(0, 0, 0, 0);
+        if (e < nvis) {
+            const uint32_t pos = FUSED ? entry_pos(g, vL, j0 + e) : 0xFFFFFFFFu;
+            if (pos == 0xFFFFFFFFu || pos < p_first) {
+                const size_t row = plane * g.rows + chunk_row(g, vL, j0 + e, wstart, wb);
+                kw[i] = reinterpret_cast<const int4*>(kv.k + row * hd)[part];
+                vw[i] = reinterpret_cast<const int4*>(kv.v + row * hd)[part];
+            }
+        }
+    }
+    float ks = 0.0f, vs = 0.0f;
+    bool pend = false;
+    if (t < nvis) {
+        const uint32_t pos = FUSED ? entry_pos(g, vL, j0 + t) : 0xFFFFFFFFu;
+        pend = pos != 0xFFFFFFFFu && pos >= p_first;
+        if (!pend) {
+            const size_t row = plane * g.rows + chunk_row(g, vL, j0 + t, wstart, wb);
+            ks = kv.ks[row];
+            vs = kv.vs[row];
+        }
+    }
+
+    // ---- LDS: queries, self keys, pass rows quantized here, cached rows
+#pragma unroll
+    for (uint32_t k = 0; k < QPT; k++) {
+        const uint32_t i = t + 256u * k, r = i / hd, d = i - r * hd;
+        if (r < (uint32_t)NR) {
+            qs[r * 128 + d] = qv[k];
+            kss[r * 128 + d] = kvv[k];
+        }
+    }
+    if constexpr (FUSED) {
+#pragma unroll
+        for (uint32_t u = 0; u < 2; u++) {
+            const uint32_t i = wid + 4u * u;
+            if (i >= nq) continue;
+            const float ak = wave_max(fmaxf(fabsf(fk[u][0]), fabsf(fk[u][1])));
+            const float av = wave_max(fmaxf(fabsf(fv[u][0]), fabsf(fv[u][1])));
+            const float ik = ak == 0.0f ? 1.0f : 127.0f / ak, iv = av == 0.0f ? 1.0f : 127.0f / av;
+            const float sk = ak == 0.0f ? 1.0f : ak / 127.0f, sv = av == 0.0f ? 1.0f : av / 127.0f;
+            const uint16_t ck = (uint16_t)(uint8_t)quant_code(fk[u][0], ik) |
+                                (uint16_t)((uint16_t)(uint8_t)quant_code(fk[u][1], ik) << 8);
+            const uint16_t cv = (uint16_t)(uint8_t)quant_code(fv[u][0], iv) |
+                                (uint16_t)((uint16_t)(uint8_t)quant_code(fv[u][1], iv) << 8);
+            const uint32_t P = p_first + i;
+            // an entry of this chunk for the group's later rows
+            const uint32_t jl = list_index(g, vL, P) - j0;
+            if (jl < nvis) {
+                if (2u * lane < hd) {
+                    const uint32_t pp = lane >> 3;
+                    *reinterpret_cast<uint16_t*>(reinterpret_cast<int8_t*>(&kt[pp * 256u + (jl ^ pp)]) +
+                                                 2u * (lane & 7u)) = ck;
+                    *reinterpret_cast<uint16_t*>(&vt[jl][2 * lane]) = cv;
+                }
+                if (lane == 0) {
+                    ksc[jl] = sk;
+                    vsc[jl] = sv;
+                }
+            }
+            // the store of a group row whose self entry is in this chunk
+            const uint32_t r = first + i - mb;
+            if (r < G && C0 + r - j0 < 256u) {
+                const uint32_t dst = kv_store_row(g, P);
+                if (dst != 0xFFFFFFFFu) {
+                    const size_t base = (plane * g.rows + dst) * hd;
+                    if (2u * lane < hd) {
+                        *reinterpret_cast<uint16_t*>(kv.k + base + 2u * lane) = ck;
+                        *reinterpret_cast<uint16_t*>(kv.v + base + 2u * lane) = cv;
+                    }
+                    if (lane == 0) {
+                        kv.ks[plane * g.rows + dst] = sk;
+                        kv.vs[plane * g.rows + dst] = sv;
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < (uint32_t)PARTS; i++) {
+        const uint32_t pi = t + 256u * i, e = pi / PARTS, part = pi % PARTS;
+        if (e < nvis) {
+            const uint32_t pos = FUSED ? entry_pos(g, vL, j0 + e) : 0xFFFFFFFFu;
+            if (pos == 0xFFFFFFFFu || pos < p_first) {
+                kt[part * 256u + (e ^ part)] = kw[i];
+                *reinterpret_cast<int4*>(&vt[e][16 * part]) = vw[i];
+            }
+        }
+    }
+    if (!pend) {                      // 0 past the visible entries: their terms below add exactly 0
+        ksc[t] = ks;
+        vsc[t] = vs;
+    }
+    __syncthreads();
+
+    // ---- scores: per row an fmaf chain over the converted key
+    const uint32_t j = j0 + t;
+    const float scale = 1.0f / __builtin_sqrtf((float)hd);
+    float acc[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) acc[r] = 0.0f;
+    if (t < nvis) {
+        const float ksv = ksc[t];
+#pragma unroll
+        for (int p = 0; p < PARTS; p++) {
+            const int4 w4 = kt[p * 256u + (t ^ (uint32_t)p)];
+            const int wv4[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+            for (int b = 0; b < 16; b++) {
+                const float kf = (float)(int8_t)((wv4[b >> 2] >> (8 * (b & 3))) & 0xFF) * ksv;
+#pragma unroll
+                for (int r = 0; r < NR; r++) acc[r] = __builtin_fmaf(qs[r * 128 + p * 16 + b], kf, acc[r]);
+            }
+        }
+    }
+    // the self score of row j - C0, when this thread holds that row's self entry
+    float selfd = 0.0f;
+    const uint32_t rs = j - C0;
+    if (rs < G) {
+#pragma unroll 16
+        for (uint32_t i = 0; i < hd; i++) selfd = selfd + qs[rs * 128 + i] * kss[rs * 128 + i];
+    }
+    float sc[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        const uint32_t Cr = C0 + r;
+        sc[r] = -__builtin_inff();
+        if ((uint32_t)r < G) sc[r] = j < Cr ? acc[r] * scale : (j == Cr ? selfd * scale : -__builtin_inff());
+    }
+    // ---- chunk max, exp and CANON(4) chunk sum per row
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        const float w = wave_max(sc[r]);
+        if (lane == 0) rmx[r * 4 + wid] = w;
+    }
+    __syncthreads();
+    float ex[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        const float* rr = rmx + r * 4;
+        const float mx = fmaxf(fmaxf(rr[0], rr[1]), fmaxf(rr[2], rr[3]));
+        const bool in = (uint32_t)r < G && j <= C0 + r;
+        ex[r] = in ? expf_c(sc[r] - mx) : 0.0f;
+        // the V chains take cached and pending entries; the self term is added apart
+        pe[r * 256 + t] = j < C0 + r ? ex[r] : 0.0f;
+        if (in && j == C0 + r) pself[r] = ex[r];
+        const float w = wave_tree_sum(ex[r]);
+        if (lane == 0) rsm[r * 4 + wid] = w;
+    }
+    __syncthreads();
+    // ---- V: per row and 64-entry sub-chunk an fmaf chain, conversions shared
+    const uint32_t sub = wid, i0 = 2u * lane;
+    if (i0 < hd) {
+        float w0[NR], w1[NR];
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            w0[r] = 0.0f;
+            w1[r] = 0.0f;
+        }
+        // entries [64 sub, min(64 sub + 64, nvis)) in groups of 4; entries
+        // past nvis up to the next multiple of 8 have v_scale 0 and finite
+        // codes, and entries past a row's list have weight 0
+        const uint32_t e_end = min(64u * sub + 64u, (nvis + 7u) & ~7u);
+        for (uint32_t e = 64u * sub; e < e_end; e += 4) {
+            float a0[4], a1[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t cc = *reinterpret_cast<const uint16_t*>(&vt[e + u][i0]);
+                const float vv = vsc[e + u];
+                a0[u] = (float)(int8_t)(cc & 0xFFu) * vv;
+                a1[u] = (float)(int8_t)(cc >> 8) * vv;
+            }
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                const float4 pp = *reinterpret_cast<const float4*>(&pe[r * 256 + e]);
+                w0[r] = __builtin_fmaf(pp.x, a0[0], w0[r]);
+                w1[r] = __builtin_fmaf(pp.x, a1[0], w1[r]);
+                w0[r] = __builtin_fmaf(pp.y, a0[1], w0[r]);
+                w1[r] = __builtin_fmaf(pp.y, a1[1], w1[r]);
+                w0[r] = __builtin_fmaf(pp.z, a0[2], w0[r]);
+                w1[r] = __builtin_fmaf(pp.z, a1[2], w1[r]);
+                w0[r] = __builtin_fmaf(pp.w, a0[3], w0[r]);
+                w1[r] = __builtin_fmaf(pp.w, a1[3], w1[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            if ((uint32_t)r >= G) continue;
+            const uint32_t js = C0 + r - j0;          // row r's self entry in the chunk
+            if (js < 256u && (js >> 6) == sub) {
+                const float ps = pself[r];
+                const size_t o = (size_t)(mb + r) * D + h * hd + i0;
+                w0[r] = __builtin_fmaf(ps, vself[o], w0[r]);
+                w1[r] = __builtin_fmaf(ps, vself[o + 1], w1[r]);
+            }
+            wp[(r * 4 + sub) * 128 + i0] = w0[r];
+            wp[(r * 4 + sub) * 128 + i0 + 1] = w1[r];
+        }
+    }
+    __syncthreads();
+    // ---- outputs of the rows whose list reaches this chunk
+    for (uint32_t i = t; i < G * hd; i += 256u) {
+        const uint32_t r = i / hd, d = i - r * hd;
+        if (j0 > C0 + r) continue;
+        const size_t mh = (size_t)(mb + r) * H + h;
+        float u = 0.0f;
+        u = u + wp[(r * 4 + 0) * 128 + d];
+        u = u + wp[(r * 4 + 1) * 128 + d];
+        u = u + wp[(r * 4 + 2) * 128 + d];
+        u = u + wp[(r * 4 + 3) * 128 + d];
+        Up[(mh * cstride + c) * hd + d] = u;
+    }
+    if (t < G && j0 <= C0 + t) {
+        const float* mm = rmx + t * 4;
+        const float* ss = rsm + t * 4;
+        const size_t mh = (size_t)(mb + t) * H + h;
+        S[mh * s_stride + 2 * c] = fmaxf(fmaxf(mm[0], mm[1]), fmaxf(mm[2], mm[3]));
+        S[mh * s_stride + 2 * c + 1] = (ss[0] + ss[2]) + (ss[1] + ss[3]);   // CANON(4) over the wave totals
+    }
 }
 
 // Engine attention, second stage: the chunks of (row m, head h) merged left

@@ -474,30 +474,44 @@ static int per_for(uint32_t K) {
     }
 
 // Engine attention of a pass (head_dim 64 or 128, checked at model
-// creation): one block per (row, head, 256-entry chunk).
-// Passes of 16 or more rows stage V rows in 136-byte LDS rows (four blocks
-// per CU); smaller passes use 144-byte rows (one 16-byte store per part).
-static void launch_attn(hipStream_t st, uint32_t hd, uint32_t M, uint32_t blocks, const PassDesc* pd,
-                        const KvGeom& g, const KvPlanes& kv, uint32_t l, uint32_t groups, const float* q,
-                        const float* k, const float* v, float* S, uint32_t s_stride, float* Wp, uint32_t cstride,
+// creation): one block per (head, 256-entry chunk, share of a group of
+// aligned rows), grid (heads * chunks, M); groups of more than 3 rows are
+// split over two or three blocks (two blocks fit on a CU), so that the
+// chip's CUs share the work.  Passes of at most 8 rows quantize and store
+// their own K/V rows inside the attention kernel (FUSED); taller passes have
+// them stored by k_kv_store_pass first.
+static bool attn_fused(uint32_t M) { return M <= AG_MAX_ROWS; }
+static void launch_attn(hipStream_t st, uint32_t hd, uint32_t M, uint32_t tasks, const PassDesc* pd,
+                        const KvGeom& g, const KvPlanes& kv, uint32_t l, const float* q, const float* k,
+                        const float* v, float* S, uint32_t s_stride, float* Wp, uint32_t cstride,
                         hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr) {
-#define PF_ATTN_LAUNCH(P, VR)                                                                                 \
+#define PF_ATTN_LAUNCH(P, F, NR)                                                                              \
     do {                                                                                                      \
         if (ev0)                                                                                              \
-            hipExtLaunchKernelGGL((k_attn_chunk<P, VR>), dim3(blocks), dim3(256), 0, st, ev0, ev1, 0, pd, g, kv, \
-                                  l, M, groups, q, k, v, S, s_stride, Wp, cstride);                           \
+            hipExtLaunchKernelGGL((k_attn_group<P, F, NR>), dim3(tasks, M), dim3(256), 0, st, ev0, ev1, 0, pd, g, \
+                                  kv, l, M, q, k, v, S, s_stride, Wp, cstride);                              \
         else                                                                                                  \
-            hipLaunchKernelGGL((k_attn_chunk<P, VR>), dim3(blocks), dim3(256), 0, st, pd, g, kv, l, M, groups, q, \
-                               k, v, S, s_stride, Wp, cstride);                                               \
+            hipLaunchKernelGGL((k_attn_group<P, F, NR>), dim3(tasks, M), dim3(256), 0, st, pd, g, kv, l, M, q, k, \
+                               v, S, s_stride, Wp, cstride);                                                  \
     } while (0)
-    const bool many = M >= 16;
-    if (hd == 64) {
-        if (many) PF_ATTN_LAUNCH(4, 136u);
-        else PF_ATTN_LAUNCH(4, 144u);
-    } else {
-        if (many) PF_ATTN_LAUNCH(8, 136u);
-        else PF_ATTN_LAUNCH(8, 144u);
+#define PF_ATTN_ROWS(P)                              \
+    switch (M) {                                     \
+        case 1: PF_ATTN_LAUNCH(P, true, 1); break;   \
+        case 2: PF_ATTN_LAUNCH(P, true, 2); break;   \
+        case 3: PF_ATTN_LAUNCH(P, true, 3); break;   \
+        case 4: PF_ATTN_LAUNCH(P, true, 2); break;   \
+        case 5: PF_ATTN_LAUNCH(P, true, 2); break;   \
+        case 6: PF_ATTN_LAUNCH(P, true, 3); break;   \
+        case 7: PF_ATTN_LAUNCH(P, true, 4); break;   \
+        case 8: PF_ATTN_LAUNCH(P, true, 4); break;   \
+        default: PF_ATTN_LAUNCH(P, false, 4); break; \
     }
+    if (hd == 64) {
+        PF_ATTN_ROWS(4);
+    } else {
+        PF_ATTN_ROWS(8);
+    }
+#undef PF_ATTN_ROWS
 #undef PF_ATTN_LAUNCH
 }
 
@@ -1476,9 +1490,8 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         return fail(c, PF_ERR_CAPACITY, "position beyond the engine's max_context");
     // captured passes replay at any position: grids sized for the largest view
     const uint32_t cmax = e->capturing ? e->cmax : kv_view(g, pos_last).count();
-    // attention tasks: (head, 256-entry chunk) groups of M rows, 8-aligned per XCD
-    const uint32_t attn_groups = H * ((cmax + 1 + 255) / 256);
-    const uint32_t attn_blocks = 8 * M * ((attn_groups + 7) / 8);
+    // attention tasks: (head, 256-entry chunk)
+    const uint32_t attn_tasks = H * ((cmax + 1 + 255) / 256);
     const uint32_t ks = e->kmax;
     const bool tall = M > GEMV_MAX_M;
     // activation scales [4][rows] of the tall passes' row kernels
@@ -1505,8 +1518,9 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
             PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_norm_quant<PER>, dim3(M), dim3(1024), 0, st, (const float*)e->x,
                                                     D, an, e->act, ks, as0));
         if (pf_status s = pass_mm(e, m->qkv[l], MM_QKV, M, a, as0)) return s;
-        hipLaunchKernelGGL(k_kv_store_pass, dim3(M, H), dim3(64), 0, st, (const PassDesc*)pd, g, e->kv, l,
-                           (const float*)e->k, (const float*)e->v);
+        if (!attn_fused(M))
+            hipLaunchKernelGGL(k_kv_store_pass, dim3(M, H), dim3(64), 0, st, (const PassDesc*)pd, g, e->kv, l,
+                               (const float*)e->k, (const float*)e->v);
         hipEvent_t aev0 = nullptr, aev1 = nullptr;
         if (e->profile && e->in_verify && !e->capturing) {
             if (e->aev_used == e->aev.size()) {
@@ -1519,7 +1533,7 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
             aev1 = e->aev[e->aev_used].b;
             e->aev_used++;
         }
-        launch_attn(st, hd, M, attn_blocks, pd, g, e->kv, l, attn_groups, e->q, e->k, e->v, e->S, e->s_stride, e->Wp,
+        launch_attn(st, hd, M, attn_tasks, pd, g, e->kv, l, e->q, e->k, e->v, e->S, e->s_stride, e->Wp,
                     e->cstride, aev0, aev1);
         // chunk merge and the O input's quantization; the extra blocks stream
         // the O weights through the cache hierarchy
