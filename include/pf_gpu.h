@@ -111,6 +111,16 @@ void pf_matrix_free(pf_matrix* m);
  * fused matmul_quantized path with per-block scales.  M <= 8 runs the GEMV,
  * 8 < M <= 512 the int8 MFMA GEMM; both give the same exact sums. */
 pf_status pf_gemv_q(pf_ctx* ctx, const pf_matrix* W, const float* x_dev, float* y_dev, uint32_t M);
+/* pf_gemv_q without allocating: the same kernels and results, with the
+ * M > 8 path's int8 activation rows and scales in a fixed device array of
+ * the library (1 MiB of activation codes plus 2 KB of scales per GPU, held
+ * until the process ends) instead of memory the context allocates.  It has
+ * no counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops).
+ * Requires ceil(M / 32) * 32 * W's cols <= 1 MiB, else PF_ERR_CAPACITY.
+ * All calls on one GPU share the array: calls that overlap on one GPU
+ * (other streams or contexts) race. */
+pf_status pf_gemv_q_noalloc(pf_ctx* ctx, const pf_matrix* W, const float* x_dev, float* y_dev, uint32_t M);
 /* y[M][rows] = fp32 x[m] . dequantized W rows (row-major Q4 matrices). */
 pf_status pf_gemv_f32(pf_ctx* ctx, const pf_matrix* W, const float* x_dev, float* y_dev, uint32_t M);
 

@@ -78,6 +78,7 @@ SYMBOLS = {
     "pf_matrix_upload": (C.c_int32, [vp, C.c_int32, C.c_uint32, C.c_uint32, u8p, u16p, C.c_int32, C.POINTER(vp)]),
     "pf_matrix_free": (None, [vp]),
     "pf_gemv_q": (C.c_int32, [vp, vp, vp, vp, C.c_uint32]),
+    "pf_gemv_q_noalloc": (C.c_int32, [vp, vp, vp, vp, C.c_uint32]),
     "pf_gemv_f32": (C.c_int32, [vp, vp, vp, vp, C.c_uint32]),
     "pf_dot_product": (C.c_int32, [vp, vp, vp, C.c_uint32, vp]),
     "pf_softmax": (C.c_int32, [vp, vp, C.c_uint32]),
@@ -325,6 +326,15 @@ class Context:
         M = x.shape[0]
         y = self.empty((M, W.rows), np.float32)
         self.check(lib().pf_gemv_q(self.h, W.h, _dptr(x), _dptr(y), M), "pf_gemv_q")
+        self.synchronize()
+        return y
+
+    def gemv_q_noalloc(self, W, x):
+        """gemv_q through the entry point that allocates nothing (its M > 8
+        path uses the library's fixed per-GPU scratch)."""
+        M = x.shape[0]
+        y = self.empty((M, W.rows), np.float32)
+        self.check(lib().pf_gemv_q_noalloc(self.h, W.h, _dptr(x), _dptr(y), M), "pf_gemv_q_noalloc")
         self.synchronize()
         return y
 

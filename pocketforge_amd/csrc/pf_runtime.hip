@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <map>
+#include <mutex>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -68,7 +69,7 @@ static pf_status dalloc_t(pf_ctx* c, T** p, size_t n) {
     return dalloc(c, reinterpret_cast<void**>(p), n * sizeof(T));
 }
 
-static pf_status scratch(pf_ctx* c, size_t bytes, void** out) {
+static pf_status ctx_scratch(pf_ctx* c, size_t bytes, void** out) {
     if (bytes > c->scratch_bytes) {
         if (c->scratch) {
             PF_HIP(c, hipStreamSynchronize(c->stream));
@@ -86,6 +87,29 @@ static pf_status scratch(pf_ctx* c, size_t bytes, void** out) {
 
 static std::string g_init_error;
 
+// Fixed scratch of pf_gemv_q_noalloc: the int8 activation rows of its
+// M > 8 path (ceil(M / 32) * 32 rows of K codes) followed by their M fp32
+// scales.  Each GPU holds its own copy until the process ends; host code
+// reaches a GPU's copy only through the address that hipGetSymbolAddress
+// gave for that GPU (g_scratch_dev), resolved once per device by pf_init.
+constexpr size_t NOALLOC_ACT_BYTES = (size_t)1 << 20;
+constexpr size_t NOALLOC_SCALE_BYTES = 512 * 4;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_ACT_BYTES + NOALLOC_SCALE_BYTES];
+constexpr int MAX_DEVICES = 64;
+static void* g_scratch_dev[MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+// With `device` current: the device address of its scratch copy.
+static hipError_t resolve_scratch(int device) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_dev[device]) return hipSuccess;
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_dev[device] = p;
+    return hipSuccess;
+}
+
 extern "C" pf_status pf_init(int device, pf_ctx** out) {
     if (!out) return PF_ERR_ARG;
     *out = nullptr;
@@ -102,6 +126,9 @@ extern "C" pf_status pf_init(int device, pf_ctx** out) {
         g_init_error = std::string("device is ") + prop.gcnArchName + ", not gfx950";
         return PF_ERR_UNSUPPORTED;
     }
+    if (device >= MAX_DEVICES) { g_init_error = "device index beyond the library's table"; return PF_ERR_ARG; }
+    e = resolve_scratch(device);
+    if (e != hipSuccess) { g_init_error = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e); return PF_ERR_HIP; }
     pf_ctx* c = new pf_ctx();
     c->device = device;
     e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
@@ -424,6 +451,7 @@ static void launch_gemm(hipStream_t st, const pf_matrix* W, MmKind kind, const G
 }
 
 constexpr uint32_t MAX_GEMM_ROWS = 512;
+static_assert(NOALLOC_SCALE_BYTES >= MAX_GEMM_ROWS * 4, "one scale per GEMM row");
 
 // y[m] (+= y_in[m]) = h[m] x dequantized rows, any M (launches of up to 8
 // rows; each row's result does not depend on the rows beside it).
@@ -540,7 +568,7 @@ extern "C" pf_status pf_matmul_quantized(pf_ctx* c, const float* A, const int8_t
     if (M == 0 || N == 0) return PF_OK;
     size_t need = (size_t)M * K + 256 + (size_t)M * 4 + 256 + (size_t)M * N * 4 + 256;
     void* s = nullptr;
-    pf_status st = scratch(c, need, &s);
+    pf_status st = ctx_scratch(c, need, &s);
     if (st) return st;
     int8_t* Aq = (int8_t*)s;
     float* as = (float*)((char*)s + (((size_t)M * K + 255) & ~(size_t)255));
@@ -559,29 +587,32 @@ extern "C" pf_status pf_matmul_quantized(pf_ctx* c, const float* A, const int8_t
     return PF_OK;
 }
 
-extern "C" pf_status pf_gemv_q(pf_ctx* c, const pf_matrix* W, const float* x, float* y, uint32_t M) {
+// pf_gemv_q and pf_gemv_q_noalloc: M <= 8 runs the GEMV, which quantizes
+// x itself; larger M quantizes x into act / as (ceil(M / 32) * 32 rows of
+// K codes, M scales) and runs the int8 MFMA GEMM.
+static pf_status gemv_q_check(pf_ctx* c, const pf_matrix* W, const float* x, float* y, uint32_t M) {
     if (!c || !W || !x || !y || M == 0 || M > MAX_GEMM_ROWS) return PF_ERR_ARG;
     if (W->rowmajor) return fail(c, PF_ERR_ARG, "pf_gemv_q needs an int8-activation (tiled) matrix");
+    if (M > GEMV_MAX_M && !per_for(W->cols)) return fail(c, PF_ERR_UNSUPPORTED, "K > 8192");
+    return PF_OK;
+}
+static size_t gemv_q_act_bytes(uint32_t M, uint32_t K) {
+    return ((size_t)((M + 31) / 32 * 32) * K + 255) & ~(size_t)255;
+}
+static pf_status gemv_q_run(pf_ctx* c, const pf_matrix* W, const float* x, float* y, uint32_t M, int8_t* act,
+                            float* as) {
     const uint32_t K = W->cols, N = W->rows;
     MmEpi e{};
     e.y = y;
     e.y_stride = N;
     e.ilv = W->ilv ? 1u : 0u;
     if (M <= GEMV_MAX_M) {
-        // the workgroups quantize x themselves: no scratch
         GemvArgs a{};
         a.W = W->data; a.N = N; a.K = K; a.M = M; a.x = x; a.xs = K; a.e = e;
         launch_gemv(c->stream, W, MM_STORE, a);
         PF_LAUNCHED(c);
         return PF_OK;
     }
-    if (!per_for(K)) return fail(c, PF_ERR_UNSUPPORTED, "K > 8192");
-    const size_t a_bytes = ((size_t)((M + 31) / 32 * 32) * K + 255) & ~(size_t)255;
-    void* s = nullptr;
-    pf_status st = scratch(c, a_bytes + (size_t)M * 4, &s);
-    if (st) return st;
-    int8_t* act = (int8_t*)s;
-    float* as = (float*)((char*)s + a_bytes);
     PF_PER_SWITCH(K, hipLaunchKernelGGL(k_quant_rows<PER>, dim3(M), dim3(256), 0, c->stream, x, K, K, act, K, as,
                                         (int32_t*)nullptr, 0u));
     GemmArgs g{};
@@ -589,6 +620,35 @@ extern "C" pf_status pf_gemv_q(pf_ctx* c, const pf_matrix* W, const float* x, fl
     launch_gemm(c->stream, W, MM_STORE, g);
     PF_LAUNCHED(c);
     return PF_OK;
+}
+
+extern "C" pf_status pf_gemv_q(pf_ctx* c, const pf_matrix* W, const float* x, float* y, uint32_t M) {
+    if (pf_status st = gemv_q_check(c, W, x, y, M)) return st;
+    if (M <= GEMV_MAX_M) return gemv_q_run(c, W, x, y, M, nullptr, nullptr);
+    const size_t a_bytes = gemv_q_act_bytes(M, W->cols);
+    void* s = nullptr;
+    pf_status st = ctx_scratch(c, a_bytes + (size_t)M * 4, &s);
+    if (st) return st;
+    return gemv_q_run(c, W, x, y, M, (int8_t*)s, (float*)((char*)s + a_bytes));
+}
+
+// The same without allocating: the M > 8 path's activation rows and scales
+// live in the GPU's copy of `scratch`.  Every buffer byte the GEMM reads is
+// written first by the quantize kernel, except the padding rows up to a
+// multiple of 32, which feed only outputs the GEMM discards; nothing needs
+// clearing.  Calls that overlap on one GPU (other streams or contexts)
+// share the array and race.
+extern "C" pf_status pf_gemv_q_noalloc(pf_ctx* c, const pf_matrix* W, const float* x, float* y, uint32_t M) {
+    if (pf_status st = gemv_q_check(c, W, x, y, M)) return st;
+    if (M <= GEMV_MAX_M) return gemv_q_run(c, W, x, y, M, nullptr, nullptr);
+    if (gemv_q_act_bytes(M, W->cols) > NOALLOC_ACT_BYTES)
+        return fail(c, PF_ERR_CAPACITY,
+                    "pf_gemv_q_noalloc: ceil(M / 32) * 32 * cols = " +
+                        std::to_string((size_t)((M + 31) / 32 * 32) * W->cols) +
+                        " activation bytes, beyond its fixed scratch of 1 MiB");
+    uint8_t* p = (uint8_t*)g_scratch_dev[c->device];
+    if (!p) return fail(c, PF_ERR_STATE, "scratch address not resolved for this device");
+    return gemv_q_run(c, W, x, y, M, (int8_t*)p, (float*)(p + NOALLOC_ACT_BYTES));
 }
 extern "C" pf_status pf_gemv_f32(pf_ctx* c, const pf_matrix* W, const float* x, float* y, uint32_t M) {
     if (!c || !W || !x || !y || M == 0 || M > 8) return PF_ERR_ARG;
