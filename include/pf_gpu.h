@@ -252,6 +252,17 @@ void pf_engine_destroy(pf_engine* e);
 /* Clears the cache and the position counter. */
 pf_status pf_engine_reset(pf_engine* e);
 uint32_t pf_engine_position(const pf_engine* e);
+/* (new) State snapshot of one KV plane, for parity checks from a state and
+ * checkpoints; the reference keeps this state inside KVCache
+ * (src/kv_cache.cpp:59-127) with no export.  Writes the plane of (sequence
+ * seq, layer, head) at the sequence's position: counts[0] sink rows,
+ * counts[1] pooled rows, counts[2] window rows oldest first (KVCache's
+ * attention order, src/kv_cache.cpp:137-155), then counts[3] evicted window
+ * rows, in eviction order, that the next pooled row will fold (the
+ * reference's running double sum, src/kv_cache.cpp:77-109).  k, v
+ * [cap][head_dim] int8 codes, ks, vs [cap] row scales. */
+pf_status pf_engine_kv_export(pf_engine* e, uint32_t seq, uint32_t layer, uint32_t head, int8_t* k, float* ks,
+                              int8_t* v, float* vs, uint32_t cap, uint32_t* counts);
 /* Engine::forward_with_hidden (engine.hpp:38-41) for n <= 8 consecutive
  * tokens in one pass; row j equals the j-th of n sequential forwards.
  * logits [n][n_vocab] and hidden [n][n_embd] may be NULL. */

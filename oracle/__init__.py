@@ -119,6 +119,11 @@ def lib():
         L.orc_kv_pool_count.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32]
         L.orc_kv_export.restype = C.c_uint32
         L.orc_kv_export.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, i8p, f32p, i8p, f32p]
+        L.orc_kv_import.argtypes = [C.c_void_p] + [C.c_uint32] * 7 + [i8p, f32p, i8p, f32p]
+        L.orc_engine_set_state.argtypes = [C.c_void_p, C.c_uint32, f32p]
+        L.orc_generate_continue.restype = C.c_int32
+        L.orc_generate_continue.argtypes = [C.c_void_p, C.c_int32, C.c_uint32, C.POINTER(Sampling), C.c_uint64,
+                                            i32p, C.c_uint32, u32p, i32p, i32p]
         L.orc_engine_create.restype = C.c_void_p
         L.orc_engine_create.argtypes = [C.POINTER(ModelDesc)]
         L.orc_engine_destroy.argtypes = [C.c_void_p]
@@ -338,6 +343,41 @@ class Model:
                                 ptr(toks, i32p), cap, C.byref(n), C.byref(acc), C.byref(rej))
         assert rc == 0
         return toks[: n.value].copy(), acc.value, rej.value
+
+    def kv_import(self, layer, head, counts, win_pos0, k, ks, v, vs):
+        kv_import(lib().orc_engine_kv(self.h), layer, head, counts, win_pos0, k, ks, v, vs)
+
+    def set_state(self, pos, hidden=None):
+        """Next position and (optionally) the last hidden state, after
+        kv_import of every plane."""
+        h = None if hidden is None else np.ascontiguousarray(hidden, np.float32)
+        lib().orc_engine_set_state(self.h, int(pos), ptr(h, f32p) if h is not None else None)
+
+    def generate_continue(self, cur, max_new, sampling=None, seed=7):
+        """Engine::generate's decode loop from the current state with current
+        token `cur`; returns (generated tokens, accepted, rejected)."""
+        s = sampling or Sampling(0.8, 0.95, 40, 1)
+        cap = max_new + 8
+        toks = np.zeros(cap, np.int32)
+        n = C.c_uint32(0)
+        acc = C.c_int32(0)
+        rej = C.c_int32(0)
+        rc = lib().orc_generate_continue(self.h, int(cur), max_new, C.byref(s), seed, ptr(toks, i32p), cap,
+                                         C.byref(n), C.byref(acc), C.byref(rej))
+        assert rc == 0
+        return toks[: n.value].copy(), acc.value, rej.value
+
+
+def kv_import(kv, layer, head, counts, win_pos0, k, ks, v, vs):
+    """orc_kv_import on an orc_kv handle: counts = (sink, pooled, window,
+    pending) rows, stacked in that order in k/ks/v/vs."""
+    k = np.ascontiguousarray(k, np.int8)
+    v = np.ascontiguousarray(v, np.int8)
+    ks = np.ascontiguousarray(ks, np.float32)
+    vs = np.ascontiguousarray(vs, np.float32)
+    assert k.shape[0] == sum(counts)
+    lib().orc_kv_import(kv, layer, head, counts[0], counts[1], counts[2], int(win_pos0), counts[3],
+                        ptr(k, i8p), ptr(ks, f32p), ptr(v, i8p), ptr(vs, f32p))
 
 
 def philox4x32_10(ctr, key):

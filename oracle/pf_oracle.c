@@ -746,6 +746,49 @@ uint32_t orc_kv_export(const orc_kv* kv, uint32_t layer, uint32_t head,
     return n;
 }
 
+/* Sets plane (layer, head) to a state given in KVCache's own terms: n_sink
+ * sink rows, n_pool pooled rows, n_win window rows oldest first (the oldest
+ * at position win_pos0), then n_pend evicted rows not yet folded, in
+ * eviction order, whose running double sum (src/kv_cache.cpp:77-90) is
+ * rebuilt here.  Rows [n][head_dim] with their scales, in that order.  A
+ * full window is laid out oldest first from slot 0, the next slot to evict,
+ * which is the ring state src/kv_cache.cpp:92-127 reaches up to rotation. */
+void orc_kv_import(orc_kv* kv, uint32_t layer, uint32_t head, uint32_t n_sink, uint32_t n_pool, uint32_t n_win,
+                   uint32_t win_pos0, uint32_t n_pend, const int8_t* k, const float* ks, const int8_t* v,
+                   const float* vs) {
+    orc_head* c = &kv->h[(size_t)layer * kv->n_heads + head];
+    const uint32_t hd = kv->hd, ws = kv->window;
+    uint32_t r = 0;
+    for (uint32_t j = 0; j < n_sink && j < 8; j++, r++) {
+        memcpy(c->sink_k + (size_t)j * hd, k + (size_t)r * hd, hd); c->sink_ks[j] = ks[r];
+        memcpy(c->sink_v + (size_t)j * hd, v + (size_t)r * hd, hd); c->sink_vs[j] = vs[r];
+    }
+    c->sink_count = n_sink;
+    pool_reserve(c, hd, n_pool);
+    for (uint32_t j = 0; j < n_pool; j++, r++) {
+        memcpy(c->pool_k + (size_t)j * hd, k + (size_t)r * hd, hd); c->pool_ks[j] = ks[r];
+        memcpy(c->pool_v + (size_t)j * hd, v + (size_t)r * hd, hd); c->pool_vs[j] = vs[r];
+    }
+    c->pool_count = n_pool;
+    for (uint32_t j = 0; j < n_win && j < ws; j++, r++) {
+        memcpy(c->win_k + (size_t)j * hd, k + (size_t)r * hd, hd); c->win_ks[j] = ks[r];
+        memcpy(c->win_v + (size_t)j * hd, v + (size_t)r * hd, hd); c->win_vs[j] = vs[r];
+        c->win_pos[j] = win_pos0 + j;
+    }
+    c->win_count = n_win;
+    c->win_head = n_win % ws;
+    memset(c->acc_k, 0, sizeof(double) * hd);
+    memset(c->acc_v, 0, sizeof(double) * hd);
+    for (uint32_t j = 0; j < n_pend; j++, r++) {
+        for (uint32_t i = 0; i < hd; i++) {
+            c->acc_k[i] += (double)k[(size_t)r * hd + i] * (double)ks[r];
+            c->acc_v[i] += (double)v[(size_t)r * hd + i] * (double)vs[r];
+        }
+    }
+    c->acc_count = n_pend;
+    c->acc_start = win_pos0 - n_pend;
+}
+
 /* src/kv_cache.cpp:200-219 */
 void orc_kv_clear(orc_kv* kv) {
     for (size_t i = 0; i < (size_t)kv->n_layers * kv->n_heads; i++) {
@@ -870,6 +913,17 @@ void orc_engine_reset(orc_engine* e) {
     e->skips = 0;
 }
 uint32_t orc_engine_pos(const orc_engine* e) { return e->pos; }
+
+/* After orc_kv_import of every plane: the next position and, when hidden is
+ * not NULL, the last forward's hidden state (the MTP heads' input). */
+void orc_engine_set_state(orc_engine* e, uint32_t pos, const float* hidden) {
+    e->pos = pos;
+    e->kv->total_stored = pos < e->kv->max_context ? pos : e->kv->max_context;
+    if (hidden) {
+        memcpy(e->last_hidden, hidden, sizeof(float) * e->d.n_embd);
+        e->hidden_valid = 1;
+    }
+}
 orc_kv* orc_engine_kv(orc_engine* e) { return e->kv; }
 
 /* RoPE angles of src/engine.cpp:656-682 (theta 5e6) for one position:
@@ -1231,23 +1285,22 @@ double orc_last_decode_seconds(void) { return g_last_decode_seconds; }
  * configuration is passed explicitly (the reference can only use its
  * defaults, :311, 324, 355, 383).  Returns 0, or -1 when tokens_cap is too
  * small. */
-int32_t orc_generate_ops(const orc_gen_ops* ops, const int32_t* prompt, uint32_t n_prompt,
-                         uint32_t max_new, const orc_sampling* cfg, uint64_t seed,
-                         int32_t* tokens, uint32_t cap, uint32_t* n_tokens,
-                         int32_t* mtp_accepted, int32_t* mtp_rejected) {
+/* The decode loop of Engine::generate (src/engine.cpp:294-389) from the
+ * current token `cur`, appending to tokens[*n_io ..]; -1 once `cap` tokens
+ * would be exceeded. */
+static int32_t gen_loop(const orc_gen_ops* ops, int32_t cur, uint32_t max_new, const orc_sampling* cfg,
+                        uint64_t seed, int32_t* tokens, uint32_t cap, uint32_t* n_io, int32_t* mtp_accepted,
+                        int32_t* mtp_rejected) {
     uint32_t V = ops->n_vocab, NH = ops->n_mtp;
     uint64_t draw = 0;
-    uint32_t nt = 0;
+    uint32_t nt = *n_io;
     int32_t acc_total = 0, rej_total = 0;
     float* logits = (float*)malloc(sizeof(float) * V);
     float* mtp_logits = (float*)malloc(sizeof(float) * V * (NH ? NH : 1));
     int32_t* preds = (int32_t*)malloc(sizeof(int32_t) * (NH ? NH : 1));
 #define PUSH(t) do { if (nt >= cap) { nt = cap + 1; goto done; } tokens[nt++] = (t); } while (0)
-    for (uint32_t i = 0; i < n_prompt; i++) ops->forward(ops->ctx, prompt[i], NULL);   /* :286-290 */
-    for (uint32_t i = 0; i < n_prompt; i++) PUSH(prompt[i]);
     double t_dec = now_s();
     uint32_t n_gen = 0;
-    int32_t cur = n_prompt ? prompt[n_prompt - 1] : 0;                     /* :294 */
     while (n_gen < max_new) {
         /* :304-305: MTP heads present, a hidden state, and n + 4 <= N */
         if (NH > 0 && ops->hidden_valid(ops->ctx) && n_gen + 4 <= max_new) {
@@ -1281,9 +1334,25 @@ done:
 #undef PUSH
     g_last_decode_seconds = now_s() - t_dec;
     free(logits); free(mtp_logits); free(preds);
-    *n_tokens = nt > cap ? cap : nt;
+    *n_io = nt > cap ? cap : nt;
     *mtp_accepted = acc_total; *mtp_rejected = rej_total;
     return nt > cap ? -1 : 0;
+}
+
+int32_t orc_generate_ops(const orc_gen_ops* ops, const int32_t* prompt, uint32_t n_prompt,
+                         uint32_t max_new, const orc_sampling* cfg, uint64_t seed,
+                         int32_t* tokens, uint32_t cap, uint32_t* n_tokens,
+                         int32_t* mtp_accepted, int32_t* mtp_rejected) {
+    for (uint32_t i = 0; i < n_prompt; i++) ops->forward(ops->ctx, prompt[i], NULL);   /* :286-290 */
+    uint32_t nt = 0;
+    for (uint32_t i = 0; i < n_prompt; i++) {
+        if (nt >= cap) { *n_tokens = cap; *mtp_accepted = 0; *mtp_rejected = 0; return -1; }
+        tokens[nt++] = prompt[i];
+    }
+    int32_t cur = n_prompt ? prompt[n_prompt - 1] : 0;                     /* :294 */
+    int32_t rc = gen_loop(ops, cur, max_new, cfg, seed, tokens, cap, &nt, mtp_accepted, mtp_rejected);
+    *n_tokens = nt;
+    return rc;
 }
 
 /* Engine::step_mtp, src/engine.cpp:402-448, over an abstract model: drafts
@@ -1348,6 +1417,16 @@ int32_t orc_generate(orc_engine* e, const int32_t* prompt, uint32_t n_prompt,
     orc_gen_ops o = engine_ops(e);
     return orc_generate_ops(&o, prompt, n_prompt, max_new, cfg, seed, tokens, cap, n_tokens, mtp_accepted,
                             mtp_rejected);
+}
+
+int32_t orc_generate_continue(orc_engine* e, int32_t cur, uint32_t max_new, const orc_sampling* cfg,
+                              uint64_t seed, int32_t* tokens, uint32_t cap, uint32_t* n_tokens,
+                              int32_t* mtp_accepted, int32_t* mtp_rejected) {
+    orc_gen_ops o = engine_ops(e);
+    uint32_t nt = 0;
+    int32_t rc = gen_loop(&o, cur, max_new, cfg, seed, tokens, cap, &nt, mtp_accepted, mtp_rejected);
+    *n_tokens = nt;
+    return rc;
 }
 
 int32_t orc_step_mtp(orc_engine* e, int32_t current_token, const float* hidden, int32_t has_table,

@@ -102,6 +102,12 @@ uint32_t orc_kv_pool_count(const orc_kv* kv, uint32_t layer, uint32_t head);
  * k/v [count][head_dim] int8 and their row scales.  Returns count. */
 uint32_t orc_kv_export(const orc_kv* kv, uint32_t layer, uint32_t head,
                        int8_t* k, float* ks, int8_t* v, float* vs);
+/* Sets (layer, head) to a state: sink, pooled and window rows (oldest
+ * first, the oldest at position win_pos0), then n_pend evicted rows not yet
+ * folded into a pooled row (eviction order). */
+void     orc_kv_import(orc_kv* kv, uint32_t layer, uint32_t head, uint32_t n_sink, uint32_t n_pool,
+                       uint32_t n_win, uint32_t win_pos0, uint32_t n_pend, const int8_t* k, const float* ks,
+                       const int8_t* v, const float* vs);
 
 /* ------------------------------------------------ model + engine */
 typedef struct {
@@ -127,6 +133,7 @@ void     orc_engine_destroy(orc_engine* e);
 void     orc_engine_reset(orc_engine* e);
 uint32_t orc_engine_pos(const orc_engine* e);
 orc_kv*  orc_engine_kv(orc_engine* e);
+void     orc_engine_set_state(orc_engine* e, uint32_t pos, const float* hidden);
 void     orc_rope_table(uint32_t head_dim, uint32_t pos, float* cos_out, float* sin_out);
 void     orc_rope_rotate(float* x, uint32_t head_dim, const float* cos_t, const float* sin_t);
 void     orc_forward(orc_engine* e, int32_t token, float* logits, float* hidden);
@@ -164,6 +171,12 @@ int32_t  orc_step_mtp_ops(const orc_gen_ops* ops, int32_t current_token, const f
 int32_t  orc_step_mtp(orc_engine* e, int32_t current_token, const float* hidden, int32_t has_table,
                       const orc_sampling* cfg, uint64_t seed, uint64_t* draw, float* logits_out,
                       uint32_t* n_logits, int32_t* acc_out, int32_t* rej_out);
+/* Engine::generate's decode loop (src/engine.cpp:294-389) from the engine's
+ * state with current token `cur`: tokens_out receives the generated tokens
+ * only. */
+int32_t  orc_generate_continue(orc_engine* e, int32_t cur, uint32_t max_new, const orc_sampling* cfg,
+                               uint64_t seed, int32_t* tokens_out, uint32_t tokens_cap, uint32_t* n_tokens,
+                               int32_t* mtp_accepted, int32_t* mtp_rejected);
 int32_t  orc_generate(orc_engine* e, const int32_t* prompt, uint32_t n_prompt,
                       uint32_t max_new, const orc_sampling* cfg, uint64_t seed,
                       int32_t* tokens_out, uint32_t tokens_cap, uint32_t* n_tokens,

@@ -108,6 +108,7 @@ SYMBOLS = {
     "pf_engine_destroy": (None, [vp]),
     "pf_engine_reset": (C.c_int32, [vp]),
     "pf_engine_position": (C.c_uint32, [vp]),
+    "pf_engine_kv_export": (C.c_int32, [vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, vp, vp, C.c_uint32, vp]),
     "pf_forward": (C.c_int32, [vp, i32p, C.c_uint32, f32p, f32p]),
     "pf_mtp_forward": (C.c_int32, [vp, f32p, f32p]),
     "pf_sample": (C.c_int32, [vp, f32p, C.POINTER(Sampling), C.c_uint64, C.POINTER(C.c_uint64), i32p]),
@@ -664,6 +665,21 @@ class Engine:
         by, ln, us = (C.c_double * k)(), (C.c_uint32 * k)(), (C.c_double * k)()
         self.ctx.check(lib().pf_engine_gemv_by_size(self.h, k, by, ln, us, C.byref(n)), "pf_engine_gemv_by_size")
         return [(by[i], ln[i], us[i]) for i in range(min(k, n.value))]
+
+    def kv_export(self, seq, layer, head, cap):
+        """One KV plane's state at the sequence's position: (k, ks, v, vs,
+        counts) with counts = (sink, pooled, window, pending) rows in that
+        order (see pf_engine_kv_export)."""
+        hd = self.cfg["n_embd"] // self.cfg["n_heads"]
+        k = np.zeros((cap, hd), np.int8)
+        v = np.zeros((cap, hd), np.int8)
+        ks = np.zeros(cap, np.float32)
+        vs = np.zeros(cap, np.float32)
+        counts = np.zeros(4, np.uint32)
+        self.ctx.check(lib().pf_engine_kv_export(self.h, seq, layer, head, P(k, vp), P(ks, vp), P(v, vp),
+                                                 P(vs, vp), cap, P(counts, vp)), "pf_engine_kv_export")
+        n = int(counts.sum())
+        return k[:n], ks[:n], v[:n], vs[:n], tuple(int(x) for x in counts)
 
     def attn_stats(self):
         n, us = C.c_uint32(0), C.c_double(0)

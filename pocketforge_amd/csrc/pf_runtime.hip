@@ -1400,6 +1400,56 @@ extern "C" pf_status pf_engine_layer_skip_count(pf_engine* e, uint64_t* count) {
 
 extern "C" uint32_t pf_engine_position(const pf_engine* e) { return e ? e->pos : 0; }
 
+// State snapshot of one (sequence, layer, head) plane at the sequence's
+// position P: the rows of KVCache's attention order (sink, pooled, window
+// oldest first; src/kv_cache.cpp:137-155) followed by the evicted window
+// rows the next pooled row will fold (src/kv_cache.cpp:77-109 keeps their
+// running sum).  The pooled rows P's view needs are folded first (the next
+// pass would write the same values).
+extern "C" pf_status pf_engine_kv_export(pf_engine* e, uint32_t seq, uint32_t layer, uint32_t head, int8_t* k,
+                                         float* ks, int8_t* v, float* vs, uint32_t cap, uint32_t* counts) {
+    if (!e || !k || !ks || !v || !vs || !counts) return PF_ERR_ARG;
+    pf_ctx* c = e->c;
+    const KvGeom& g = e->g;
+    if (seq >= e->nseq || layer >= g.n_layers || head >= g.n_heads) return fail(c, PF_ERR_ARG, "plane out of range");
+    const uint32_t P = seq == 0 ? e->pos : e->spos[seq];
+    const KvView vw = kv_view(g, P);
+    const uint32_t n_win = vw.win_hi - vw.win_lo, n_pend = vw.win_lo - vw.pool * g.pool_block;
+    const uint32_t total = vw.sink + vw.pool + n_win + n_pend;
+    if (total > cap) return fail(c, PF_ERR_ARG, "export capacity below the plane's row count");
+    const size_t plane = ((size_t)seq * g.n_layers + layer) * g.n_heads + head;
+    const uint32_t r_lo = kv_view(g, P > 0 ? P - 1 : 0).pool;
+    for (uint32_t r = r_lo; r < vw.pool && r < g.pool_cap; r++)
+        hipLaunchKernelGGL(k_pool_row_one, dim3(1), dim3(g.head_dim <= 64 ? 64 : 128), 0, c->stream, g, e->kv,
+                           (uint32_t)plane, r);
+    PF_LAUNCHED(c);
+    PF_HIP(c, hipStreamSynchronize(c->stream));
+    const uint32_t hd = g.head_dim;
+    std::vector<int8_t> hk((size_t)g.rows * hd), hv((size_t)g.rows * hd);
+    std::vector<float> hks(g.rows), hvs(g.rows);
+    PF_HIP(c, hipMemcpy(hk.data(), e->kv.k + plane * g.rows * hd, hk.size(), hipMemcpyDeviceToHost));
+    PF_HIP(c, hipMemcpy(hv.data(), e->kv.v + plane * g.rows * hd, hv.size(), hipMemcpyDeviceToHost));
+    PF_HIP(c, hipMemcpy(hks.data(), e->kv.ks + plane * g.rows, g.rows * 4, hipMemcpyDeviceToHost));
+    PF_HIP(c, hipMemcpy(hvs.data(), e->kv.vs + plane * g.rows, g.rows * 4, hipMemcpyDeviceToHost));
+    uint32_t o = 0;
+    auto put = [&](uint32_t row) {
+        std::memcpy(k + (size_t)o * hd, hk.data() + (size_t)row * hd, hd);
+        std::memcpy(v + (size_t)o * hd, hv.data() + (size_t)row * hd, hd);
+        ks[o] = hks[row];
+        vs[o] = hvs[row];
+        o++;
+    };
+    for (uint32_t j = 0; j < vw.sink; j++) put(j);
+    for (uint32_t j = 0; j < vw.pool; j++) put(KV_SINK_ROWS + g.ring + j);
+    for (uint32_t w = vw.win_lo; w < vw.win_hi; w++) put(KV_SINK_ROWS + w % g.ring);
+    for (uint32_t w = vw.pool * g.pool_block; w < vw.win_lo; w++) put(KV_SINK_ROWS + w % g.ring);
+    counts[0] = vw.sink;
+    counts[1] = vw.pool;
+    counts[2] = n_win;
+    counts[3] = n_pend;
+    return PF_OK;
+}
+
 extern "C" pf_status pf_engine_set_mtp_enabled(pf_engine* e, int32_t enabled) {
     if (!e) return PF_ERR_ARG;
     e->mtp_enabled = enabled != 0;
