@@ -82,8 +82,8 @@ struct GenerationResult {
 using TokenCallback = std::function<void(int32_t token, float prob)>;
 using ProgressCallback = std::function<void(float progress)>;
 
-// Weight formats of a layer's matrices (this build's extension for
-// Engine::load_random_model: the .squeeze loader is not part of it).
+// Weight formats of a layer's matrices (this build's extension for the
+// synthetic loader, Engine::load_random_model).
 enum class WeightFormat : int32_t { Q4 = 0, Q2 = 1, Q1_5 = 2 };
 struct WeightFormats {
     WeightFormat attention = WeightFormat::Q4;   // Q, K, V, O

@@ -12,6 +12,7 @@
 #include <string>
 #include <vector>
 
+#include "forge/batch_engine.hpp"
 #include "forge/engine.hpp"
 #include "forge/kv_cache.hpp"
 #include "forge/matmul_neon.hpp"
@@ -77,6 +78,85 @@ HostMatrix gen_matrix(uint64_t seed, uint32_t stream, uint32_t rows, uint32_t co
     check(nullptr, pf_gen_matrix(seed, stream, 0.02f, rows, cols, fmt, m.codes.data(), m.scales.data()),
           "pf_gen_matrix");
     return m;
+}
+
+// A device model of the seeded synthetic weights: layer l, matrix j from
+// stream 16 l + j, the tied embedding from 0x10000, MTP head k matrix j from
+// 0x20000 + 3 k + j (the benchmark's streams).  MHA only.
+bool make_random_model(pf_ctx* ctx, const ModelConfig& cfg, uint64_t seed, const WeightFormats& formats,
+                       pf_model** out, size_t* weight_bytes, size_t* mtp_bytes) {
+    *out = nullptr;
+    const uint32_t D = cfg.n_embd, F = cfg.n_ff, V = cfg.n_vocab;
+    if (cfg.n_kv_heads != cfg.n_heads) return false;
+    pf_model_desc d{cfg.n_layers, D, cfg.n_heads, cfg.head_dim(), F, V, cfg.mtp_heads};
+    pf_model* m = nullptr;
+    if (pf_model_create(ctx, &d, &m) != PF_OK) return false;
+    std::unique_ptr<pf_model, void (*)(pf_model*)> guard(m, pf_model_destroy);
+    const int32_t fa = (int32_t)formats.attention, fg = (int32_t)formats.ffn_gate_up, fd = (int32_t)formats.ffn_down;
+    const struct { uint32_t rows, cols; int32_t fmt; } shape[7] = {
+        {D, D, fa}, {D, D, fa}, {D, D, fa}, {D, D, fa}, {F, D, fg}, {F, D, fg}, {D, F, fd}};
+    *weight_bytes = 0;
+    for (uint32_t l = 0; l < cfg.n_layers; l++)
+        for (int32_t j = 0; j < 7; j++) {
+            HostMatrix h = gen_matrix(seed, l * 16u + (uint32_t)j, shape[j].rows, shape[j].cols, shape[j].fmt);
+            if (pf_model_set_matrix(m, l, j, shape[j].fmt, h.codes.data(), h.scales.data()) != PF_OK) return false;
+            *weight_bytes += h.codes.size() + h.scales.size() * 2;
+        }
+    {
+        HostMatrix h = gen_matrix(seed, 0x10000u, V, D, PF_FMT_Q4);
+        if (pf_model_set_embedding(m, h.codes.data(), h.scales.data()) != PF_OK) return false;
+        *weight_bytes += h.codes.size() + h.scales.size() * 2;
+    }
+    *mtp_bytes = 0;
+    for (uint32_t k = 0; k < cfg.mtp_heads; k++)
+        for (int32_t j = 0; j < 3; j++) {
+            HostMatrix h = gen_matrix(seed, 0x20000u + 3u * k + (uint32_t)j, D, D, PF_FMT_Q4);
+            if (pf_model_set_mtp(m, k, j, h.codes.data(), h.scales.data()) != PF_OK) return false;
+            *mtp_bytes += h.codes.size() + h.scales.size() * 2;
+        }
+    *out = guard.release();
+    return true;
+}
+
+// A device model of a .squeeze file (src/engine.cpp:48-201), every layer
+// resident; cfg takes the file's configuration.  The format holds no MTP
+// heads; the reference draws them at load time (MTPHeads::init_weights),
+// here they are the seeded heads of make_random_model with seed 0.
+bool make_squeeze_model(pf_ctx* ctx, const std::string& path, ModelConfig& cfg, pf_model** out,
+                        size_t* mtp_bytes) {
+    *out = nullptr;
+    pf_squeeze* sq = nullptr;
+    if (pf_squeeze_open(path.c_str(), &sq) != PF_OK) return false;
+    pf_squeeze_info info{};
+    pf_squeeze_get_info(sq, &info);
+    pf_model* m = nullptr;
+    const pf_status st = pf_squeeze_load_model(ctx, sq, &m);
+    pf_squeeze_close(sq);
+    if (st != PF_OK) return false;
+    std::unique_ptr<pf_model, void (*)(pf_model*)> guard(m, pf_model_destroy);
+    cfg.n_layers = info.n_layers;
+    cfg.n_embd = info.n_embd;
+    cfg.n_heads = info.n_heads;
+    cfg.n_kv_heads = info.n_kv_heads ? info.n_kv_heads : info.n_heads;
+    cfg.n_ff = info.n_ff;
+    cfg.n_vocab = info.n_vocab;
+    cfg.max_seq_len = info.max_seq_len;
+    cfg.mtp_heads = info.mtp_heads;
+    const uint32_t D = cfg.n_embd;
+    *mtp_bytes = 0;
+    for (uint32_t k = 0; k < cfg.mtp_heads; k++)
+        for (int32_t j = 0; j < 3; j++) {
+            HostMatrix h = gen_matrix(0, 0x20000u + 3u * k + (uint32_t)j, D, D, PF_FMT_Q4);
+            if (pf_model_set_mtp(m, k, j, h.codes.data(), h.scales.data()) != PF_OK) return false;
+            *mtp_bytes += h.codes.size() + h.scales.size() * 2;
+        }
+    *out = guard.release();
+    return true;
+}
+
+// The reference's KVCacheConfig from ModelConfig (src/engine.cpp:58-67).
+pf_cache_desc cache_of(const ModelConfig& cfg) {
+    return pf_cache_desc{4u, std::min(cfg.kv_cache_size, (uint32_t)8192), 64u, cfg.max_seq_len};
 }
 
 }  // namespace
@@ -325,41 +405,17 @@ size_t Engine::MemoryStats::total() const {
 }
 
 // src/engine.cpp:48-201: the .squeeze file's configuration and weights
-// (every layer resident in HBM).  The format holds no MTP heads; the
-// reference draws them at load time (MTPHeads::init_weights), here they are
-// the seeded N(0, 0.02) Q4 heads of load_random_model (seed 0).
+// (every layer resident in HBM), MTP heads as make_squeeze_model says.
 bool Engine::load_model(const std::string& path) {
     if (!dev_->ctx) dev_->ctx = shared_ctx();
-    pf_squeeze* sq = nullptr;
-    if (pf_squeeze_open(path.c_str(), &sq) != PF_OK) return false;
-    pf_squeeze_info info{};
-    pf_squeeze_get_info(sq, &info);
     pf_engine_destroy(dev_->eng);
     dev_->eng = nullptr;
     pf_model_destroy(dev_->model);
     dev_->model = nullptr;
-    const pf_status st = pf_squeeze_load_model(dev_->ctx.get(), sq, &dev_->model);
-    dev_->weight_bytes = 0;   // not tracked for loaded files
-    pf_squeeze_close(sq);
-    if (st != PF_OK) return false;
     ModelConfig cfg = config_;
-    cfg.n_layers = info.n_layers;
-    cfg.n_embd = info.n_embd;
-    cfg.n_heads = info.n_heads;
-    cfg.n_kv_heads = info.n_kv_heads ? info.n_kv_heads : info.n_heads;
-    cfg.n_ff = info.n_ff;
-    cfg.n_vocab = info.n_vocab;
-    cfg.max_seq_len = info.max_seq_len;
-    cfg.mtp_heads = info.mtp_heads;
+    dev_->weight_bytes = 0;   // not tracked for loaded files
+    if (!make_squeeze_model(dev_->ctx.get(), path, cfg, &dev_->model, &dev_->mtp_bytes)) return false;
     config_ = cfg;
-    const uint32_t D = cfg.n_embd;
-    dev_->mtp_bytes = 0;
-    for (uint32_t k = 0; k < cfg.mtp_heads; k++)
-        for (int32_t j = 0; j < 3; j++) {
-            HostMatrix m = gen_matrix(0, 0x20000u + 3u * k + (uint32_t)j, D, D, PF_FMT_Q4);
-            if (pf_model_set_mtp(dev_->model, k, j, m.codes.data(), m.scales.data()) != PF_OK) return false;
-            dev_->mtp_bytes += m.codes.size() + m.scales.size() * 2;
-        }
     dev_->mtp_enabled = cfg.mtp_enabled;
     return rebuild_engine();
 }
@@ -369,8 +425,7 @@ bool Engine::rebuild_engine() {
     pf_engine_destroy(dev_->eng);
     dev_->eng = nullptr;
     if (!dev_->model) return false;
-    pf_cache_desc kc{4u, std::min(config_.kv_cache_size, (uint32_t)8192), 64u, config_.max_seq_len};
-    // the reference's KVCacheConfig from ModelConfig (src/engine.cpp:58-67)
+    pf_cache_desc kc = cache_of(config_);
     if (pf_engine_create(dev_->model, &kc, &dev_->eng) != PF_OK) return false;
     pf_engine_set_mtp_enabled(dev_->eng, dev_->mtp_enabled ? 1 : 0);
     pf_engine_set_max_memory(dev_->eng, dev_->max_memory);
@@ -385,34 +440,8 @@ bool Engine::load_random_model(const ModelConfig& cfg, uint64_t seed, const Weig
     pf_model_destroy(dev_->model);
     dev_->model = nullptr;
     config_ = cfg;
-    const uint32_t D = cfg.n_embd, F = cfg.n_ff, V = cfg.n_vocab;
-    if (cfg.n_kv_heads != cfg.n_heads) return false;   // MHA only
-    pf_model_desc d{cfg.n_layers, D, cfg.n_heads, cfg.head_dim(), F, V, cfg.mtp_heads};
-    if (pf_model_create(dev_->ctx.get(), &d, &dev_->model) != PF_OK) return false;
-    const int32_t fa = (int32_t)formats.attention, fg = (int32_t)formats.ffn_gate_up, fd = (int32_t)formats.ffn_down;
-    const struct { uint32_t rows, cols; int32_t fmt; } shape[7] = {
-        {D, D, fa}, {D, D, fa}, {D, D, fa}, {D, D, fa}, {F, D, fg}, {F, D, fg}, {D, F, fd}};
-    dev_->weight_bytes = 0;
-    for (uint32_t l = 0; l < cfg.n_layers; l++)
-        for (int32_t j = 0; j < 7; j++) {
-            // the synthetic-weight streams of the benchmark: layer l, matrix j -> 16 l + j
-            HostMatrix m = gen_matrix(seed, l * 16u + (uint32_t)j, shape[j].rows, shape[j].cols, shape[j].fmt);
-            if (pf_model_set_matrix(dev_->model, l, j, shape[j].fmt, m.codes.data(), m.scales.data()) != PF_OK)
-                return false;
-            dev_->weight_bytes += m.codes.size() + m.scales.size() * 2;
-        }
-    {
-        HostMatrix m = gen_matrix(seed, 0x10000u, V, D, PF_FMT_Q4);
-        if (pf_model_set_embedding(dev_->model, m.codes.data(), m.scales.data()) != PF_OK) return false;
-        dev_->weight_bytes += m.codes.size() + m.scales.size() * 2;
-    }
-    dev_->mtp_bytes = 0;
-    for (uint32_t k = 0; k < cfg.mtp_heads; k++)
-        for (int32_t j = 0; j < 3; j++) {
-            HostMatrix m = gen_matrix(seed, 0x20000u + 3u * k + (uint32_t)j, D, D, PF_FMT_Q4);
-            if (pf_model_set_mtp(dev_->model, k, j, m.codes.data(), m.scales.data()) != PF_OK) return false;
-            dev_->mtp_bytes += m.codes.size() + m.scales.size() * 2;
-        }
+    if (!make_random_model(dev_->ctx.get(), cfg, seed, formats, &dev_->model, &dev_->weight_bytes, &dev_->mtp_bytes))
+        return false;
     dev_->mtp_enabled = cfg.mtp_enabled;
     return rebuild_engine();
 }
@@ -582,6 +611,118 @@ Engine::MemoryStats Engine::get_memory_stats() const {
     const size_t known = m.weights_decompressed + m.mtp_heads + m.kv_cache;
     m.activations = total > known ? total - known : 0;
     return m;
+}
+
+// ======================================================== batch_engine.hpp
+
+struct BatchEngine::Device {
+    std::shared_ptr<pf_ctx> ctx;
+    pf_model* model = nullptr;
+    pf_engine* eng = nullptr;
+    bool mtp_enabled = true;
+    size_t weight_bytes = 0, mtp_bytes = 0;
+    ~Device() {
+        pf_engine_destroy(eng);
+        pf_model_destroy(model);
+    }
+};
+
+BatchEngine::BatchEngine(uint32_t n_sequences) : n_seq_(n_sequences), dev_(new Device) {}
+BatchEngine::~BatchEngine() = default;
+
+bool BatchEngine::rebuild_engine() {
+    pf_engine_destroy(dev_->eng);
+    dev_->eng = nullptr;
+    if (!dev_->model || n_seq_ == 0) return false;
+    pf_cache_desc kc = cache_of(config_);
+    if (pf_batch_create(dev_->model, &kc, n_seq_, &dev_->eng) != PF_OK) return false;
+    pf_engine_set_mtp_enabled(dev_->eng, dev_->mtp_enabled ? 1 : 0);
+    return true;
+}
+
+bool BatchEngine::load_model(const std::string& path) {
+    if (!dev_->ctx) dev_->ctx = shared_ctx();
+    pf_engine_destroy(dev_->eng);
+    dev_->eng = nullptr;
+    pf_model_destroy(dev_->model);
+    dev_->model = nullptr;
+    ModelConfig cfg = config_;
+    if (!make_squeeze_model(dev_->ctx.get(), path, cfg, &dev_->model, &dev_->mtp_bytes)) return false;
+    config_ = cfg;
+    dev_->mtp_enabled = cfg.mtp_enabled;
+    return rebuild_engine();
+}
+
+bool BatchEngine::load_random_model(const ModelConfig& cfg, uint64_t seed, const WeightFormats& formats) {
+    if (!dev_->ctx) dev_->ctx = shared_ctx();
+    pf_engine_destroy(dev_->eng);
+    dev_->eng = nullptr;
+    pf_model_destroy(dev_->model);
+    dev_->model = nullptr;
+    config_ = cfg;
+    if (!make_random_model(dev_->ctx.get(), cfg, seed, formats, &dev_->model, &dev_->weight_bytes, &dev_->mtp_bytes))
+        return false;
+    dev_->mtp_enabled = cfg.mtp_enabled;
+    return rebuild_engine();
+}
+
+void BatchEngine::set_max_context(uint32_t tokens) {   // as Engine::set_max_context (src/engine.cpp:232-237)
+    config_.max_seq_len = std::min(tokens, (uint32_t)131072);
+    config_.kv_cache_size = std::min(tokens, (uint32_t)8192);
+    if (dev_->eng) rebuild_engine();
+}
+
+void BatchEngine::set_mtp_enabled(bool enabled) {
+    config_.mtp_enabled = enabled;
+    dev_->mtp_enabled = enabled;
+    if (dev_->eng) pf_engine_set_mtp_enabled(dev_->eng, enabled ? 1 : 0);
+}
+
+uint32_t BatchEngine::position(uint32_t seq) const { return dev_->eng ? pf_batch_position(dev_->eng, seq) : 0; }
+
+void BatchEngine::reset() {
+    if (dev_->eng) check(dev_->ctx.get(), pf_engine_reset(dev_->eng), "pf_engine_reset");
+}
+
+std::vector<GenerationResult> BatchEngine::generate(const std::vector<std::vector<int32_t>>& prompts,
+                                                    uint32_t max_new, const SamplingConfig& sc,
+                                                    const std::vector<uint64_t>& seeds,
+                                                    BatchTokenCallback callback) {
+    if (!dev_->eng) throw std::runtime_error("BatchEngine::generate: no model loaded");
+    if (prompts.size() != n_seq_) throw std::invalid_argument("BatchEngine::generate: one prompt per sequence");
+    if (!seeds.empty() && seeds.size() != n_seq_)
+        throw std::invalid_argument("BatchEngine::generate: one seed per sequence");
+    const auto t0 = std::chrono::steady_clock::now();
+    std::vector<uint32_t> lens(n_seq_);
+    std::vector<int32_t> flat;
+    size_t longest = 0;
+    for (uint32_t i = 0; i < n_seq_; i++) {
+        lens[i] = (uint32_t)prompts[i].size();
+        flat.insert(flat.end(), prompts[i].begin(), prompts[i].end());
+        longest = std::max(longest, prompts[i].size());
+    }
+    if (flat.empty()) flat.push_back(0);
+    std::vector<uint64_t> sd = seeds.empty() ? std::vector<uint64_t>(n_seq_, 42) : seeds;
+    const uint32_t cap = (uint32_t)longest + max_new + 8;
+    std::vector<int32_t> out((size_t)n_seq_ * cap);
+    std::vector<pf_gen_result> g(n_seq_);
+    pf_sampling s{sc.temperature, sc.top_p, sc.top_k, sc.greedy ? 1 : 0};
+    check(dev_->ctx.get(),
+          pf_batch_generate(dev_->eng, flat.data(), lens.data(), max_new, &s, sd.data(), out.data(), cap, g.data()),
+          "pf_batch_generate");
+    const float secs = std::chrono::duration<float>(std::chrono::steady_clock::now() - t0).count();
+    std::vector<GenerationResult> r(n_seq_);
+    for (uint32_t i = 0; i < n_seq_; i++) {
+        r[i].tokens.assign(out.begin() + (size_t)i * cap, out.begin() + (size_t)i * cap + g[i].n_tokens);
+        r[i].tokens_per_second = secs > 0.0f ? (float)r[i].tokens.size() / secs : 0.0f;
+        r[i].mtp_accepted = g[i].mtp_accepted;
+        r[i].mtp_rejected = g[i].mtp_rejected;
+        r[i].oom_protected = g[i].oom_protected != 0;
+        r[i].peak_memory_bytes = pf_device_bytes(dev_->ctx.get());
+        if (callback)
+            for (size_t k = prompts[i].size(); k < r[i].tokens.size(); k++) callback(i, r[i].tokens[k]);
+    }
+    return r;
 }
 
 }  // namespace forge

@@ -9,7 +9,7 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIBDIR = os.path.join(ROOT, "pocketforge_amd", "_lib")
 BIN = os.path.join(LIBDIR, "tests")
-TESTS = ["test_forge_matmul", "test_forge_kv_cache", "test_forge_mtp", "test_forge_engine"]
+TESTS = ["test_forge_matmul", "test_forge_kv_cache", "test_forge_mtp", "test_forge_engine", "test_forge_batch"]
 
 
 def _built(name):
@@ -28,7 +28,8 @@ def test_forge_library_exports_the_reference_api():
                 "forge::Engine::sample_top_p(", "forge::KVCache::attention_scores(",
                 "forge::KVCache::attention_weighted_sum(", "forge::MTPHeads::forward(",
                 "forge::MTPHeads::speculative_accept(", "forge::matmul_int8(", "forge::matmul_quantized(",
-                "forge::quantize_activation_row(", "forge::softmax(", "forge::rmsnorm(", "forge::dot_product("]:
+                "forge::quantize_activation_row(", "forge::softmax(", "forge::rmsnorm(", "forge::dot_product(",
+                "forge::BatchEngine::generate(", "forge::BatchEngine::load_random_model("]:
         assert sym in out, sym
 
 

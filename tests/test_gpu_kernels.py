@@ -163,11 +163,24 @@ SAMPLERS = {
 }
 
 
+@pytest.fixture(scope="module")
+def engine_v16k(gpu):
+    """A one-layer model with the benchmark vocabulary (16384), for the
+    sampler at the size where its radix sort holds 16 keys per thread."""
+    from pocketforge_amd import weights as W
+    cfg = dict(n_layers=1, n_embd=256, n_heads=4, head_dim=64, n_ff=512, n_vocab=16384, n_mtp=4)
+    m = pf.Model(gpu, cfg, W.make_weights(cfg, seed=1234))
+    e = pf.Engine(m, sink_size=4, window_size=64, pool_block=6, max_context=256)
+    yield e
+    e.close()
+    m.close()
+
+
 @pytest.mark.parametrize("name", sorted(SAMPLERS))
 @pytest.mark.parametrize("V", [1024, 16384])
-def test_sampler(gpu, tiny_engine, name, V):
-    if V != tiny_engine.cfg["n_vocab"]:
-        pytest.skip("engine vocabulary differs")
+def test_sampler(gpu, tiny_engine, engine_v16k, name, V):
+    eng = tiny_engine if V == 1024 else engine_v16k
+    assert eng.cfg["n_vocab"] == V
     cfg = SAMPLERS[name]
     ocfg = O.Sampling(cfg.temperature, cfg.top_p, cfg.top_k, cfg.greedy)
     rng = np.random.default_rng(V)
@@ -176,7 +189,7 @@ def test_sampler(gpu, tiny_engine, name, V):
         if trial == 3:
             logits[::7] = logits.max()           # ties at the maximum
         draw = trial * 3
-        t, d = tiny_engine.sample(logits, cfg, 7, draw)
+        t, d = eng.sample(logits, cfg, 7, draw)
         t2, d2 = O.sample(logits, ocfg, 7, draw)
         assert (t, d) == (t2, d2), (name, trial)
 
