@@ -16,7 +16,10 @@ generated tokens / decode wall time over the K timed steps.
 Also reported: the int8 GEMV kernel's achieved HBM bandwidth (HIP events
 around every GEMV launch of the verify passes, algorithmic bytes = packed
 weights + int8 activations + fp32 outputs), the verify pass as a whole, and
-the CPU restatement (oracle) timed on a bounded sample on the host cores.
+the CPU restatement (oracle) timed on the host cores on a bounded sample of
+the same call: generate([last prompt token], 64 tokens on all cores, 16 on
+one) from the GPU's
+prefilled state at the workload's context, imported into the oracle.
 """
 import argparse
 import json
@@ -80,33 +83,56 @@ def measured_traffic():
     return None
 
 
-def cpu_baseline(cfg, w, kv, prompt, samp, what, n_prompt=16, n_new=8, threads=0):
-    """The oracle's MTP decode on the host: all cores (threads=0), or a given
-    number of threads (1: the reference's single-threaded compute)."""
+def snapshot_planes(eng, cfg, kv):
+    """Every KV plane of the engine's sequence (pf_engine_kv_export) at its
+    position, with the first window position, for the oracle's import."""
+    P = eng.pos
+    cap = 8 + kv["window_size"] + kv["pool_block"] + P // kv["pool_block"] + 8
+    planes = []
+    for l in range(cfg["n_layers"]):
+        for h in range(cfg["n_heads"]):
+            k, ks, v, vs, counts = eng.kv_export(0, l, h, cap)
+            planes.append((l, h, counts, kv["sink_size"] + counts[1] * kv["pool_block"] + counts[3], k, ks, v, vs))
+    return P, planes
+
+
+def cpu_baseline(cfg, w, kv, snapshot, last, n_new, samp, what, gpu_tokens, threads=0):
+    """The oracle (C restatement) running a step's timed call,
+    generate([last prompt token], n_new), on the host cores from the GPU's
+    prefilled state at the workload's context (every KV plane exported and
+    imported): all cores (threads=0) or a given number of threads (1: the
+    reference's single-threaded compute).  Bounded by n_new."""
     import oracle as O
     c = dict(cfg)
     c.update(kv)
     all_threads = int(O.lib().orc_num_threads())
     O.lib().orc_set_num_threads(threads or all_threads)
     om = O.Model(c, w)
+    P, planes = snapshot
+    for l, h, counts, wpos0, k, ks, v, vs in planes:
+        om.kv_import(l, h, counts, wpos0, k, ks, v, vs)
+    om.set_state(P)
     t0 = time.perf_counter()
-    toks, acc, rej = om.generate(prompt[:n_prompt], n_new, O.Sampling(*samp), 7)
+    toks, acc, rej = om.generate([last], n_new, O.Sampling(*samp), 7)
     wall = time.perf_counter() - t0
-    dec = O.lib().orc_last_decode_seconds()
     om.close()
     used = int(O.lib().orc_num_threads())
     O.lib().orc_set_num_threads(all_threads)
-    gen = len(toks) - n_prompt
+    gen = len(toks) - 1
+    # the MTP rounds of both runs agree while n + 4 <= n_new
+    k = max(0, n_new - 4)
+    agree = None if gpu_tokens is None else bool(np.array_equal(toks[1:1 + k], gpu_tokens[1:1 + k]))
     par = "single thread" if used == 1 else f"OpenMP row-parallel GEMVs, {used} threads"
     return {
-        "value": round(gen / dec, 4),
+        "value": round(gen / wall, 4),
         "unit": "tok/s",
         "cores": used,
         "kind": "port",
-        "sample": (f"oracle (C restatement, {par}) MTP decode of {gen} tokens after a "
-                   f"{n_prompt}-token prompt on the same weights and sampling ({what}); decode time {dec:.2f}s of "
-                   f"{wall:.2f}s wall (prefill excluded); context {n_prompt}-{n_prompt + n_new} instead of the "
-                   f"workload's"),
+        "sample": (f"oracle (C restatement, {par}): generate([last prompt token], {n_new}) from the GPU's prefilled "
+                   f"state at context {P} (all {len(planes)} KV planes exported and imported), the same call, "
+                   f"weights and sampling as a timed step of {what}; {gen} tokens in {wall:.2f}s wall"),
+        "context": P,
+        "tokens_match_gpu": agree,
     }
 
 
@@ -281,10 +307,16 @@ def main():
         },
     }
     if not args.no_cpu:
-        log("cpu baseline ...")
-        out["cpu_baseline"] = cpu_baseline(cfg, w, kv, prompt, C["samp"], args.config)
+        # the prefilled state of a step, exported once for both oracle runs
+        eng.reset()
+        for i in range(0, args.prompt - 1, 256):
+            eng.prefill(prompt[i:min(i + 256, args.prompt - 1)])
+        snap = snapshot_planes(eng, cfg, kv)
+        log(f"cpu baseline from the state at context {snap[0]} ...")
+        out["cpu_baseline"] = cpu_baseline(cfg, w, kv, snap, int(prompt[-1]), 64, C["samp"], args.config, toks_p)
         log("cpu baseline, one thread ...")
-        out["cpu_baseline_1thread"] = cpu_baseline(cfg, w, kv, prompt, C["samp"], args.config, n_new=4, threads=1)
+        out["cpu_baseline_1thread"] = cpu_baseline(cfg, w, kv, snap, int(prompt[-1]), 16, C["samp"], args.config,
+                                                   toks_p, threads=1)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)
@@ -432,8 +464,13 @@ def bench_batch(args, C, cfg, w, ctx, dev, model):
         },
     }
     if not args.no_cpu:
-        log("cpu baseline ...")
-        out["cpu_baseline"] = cpu_baseline(cfg, w, kv, prompts[0], C["samp"], "E, one sequence")
+        # sequence 0's state after the steps; the next step forwards last[0]
+        snap = snapshot_planes(eng, cfg, kv)
+        log(f"cpu baseline from sequence 0's state at context {snap[0]} ...")
+        out["cpu_baseline"] = cpu_baseline(cfg, w, kv, snap, int(last[0][0]), 16, C["samp"], "E, one sequence",
+                                           None)
+        out["cpu_baseline_1thread"] = cpu_baseline(cfg, w, kv, snap, int(last[0][0]), 8, C["samp"],
+                                                   "E, one sequence", None, threads=1)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)
