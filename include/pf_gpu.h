@@ -282,6 +282,14 @@ pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n_prompt, ui
 /* Engine::set_mtp_enabled (engine.hpp:23): with 0, generate runs the
  * single-token loop only (src/engine.cpp:304, 367-386). */
 pf_status pf_engine_set_mtp_enabled(pf_engine* e, int32_t enabled);
+/* (new) How pf_generate verifies a round's drafts; tokens are the same
+ * either way.  The reference forwards the verify rows one at a time and
+ * stops at the first mismatch (src/engine.cpp:332-365).  By default (0) a
+ * round that follows a round with no accepted draft verifies its first
+ * draft with a one-row pass and, if that draft is accepted, the rest in a
+ * second pass; other rounds verify every draft in one (n_mtp + 1)-row pass.
+ * With 1, every round uses the one (n_mtp + 1)-row pass. */
+pf_status pf_engine_set_verify_full(pf_engine* e, int32_t full);
 /* Engine::set_max_memory (engine.hpp:25): generate stops with
  * oom_protected when the context's device bytes exceed this (0 = off). */
 pf_status pf_engine_set_max_memory(pf_engine* e, size_t bytes);

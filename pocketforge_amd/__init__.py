@@ -108,6 +108,7 @@ SYMBOLS = {
     "pf_engine_destroy": (None, [vp]),
     "pf_engine_reset": (C.c_int32, [vp]),
     "pf_engine_position": (C.c_uint32, [vp]),
+    "pf_engine_set_verify_full": (C.c_int32, [vp, C.c_int32]),
     "pf_engine_kv_export": (C.c_int32, [vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, vp, vp, C.c_uint32, vp]),
     "pf_forward": (C.c_int32, [vp, i32p, C.c_uint32, f32p, f32p]),
     "pf_mtp_forward": (C.c_int32, [vp, f32p, f32p]),
@@ -621,6 +622,11 @@ class Engine:
 
     def set_max_memory(self, nbytes):
         self.ctx.check(lib().pf_engine_set_max_memory(self.h, nbytes), "pf_engine_set_max_memory")
+
+    def set_verify_full(self, full):
+        """1: every MTP round verifies all drafts in one pass; 0 (default):
+        one-row first segment after a round with no accepted draft."""
+        self.ctx.check(lib().pf_engine_set_verify_full(self.h, int(full)), "pf_engine_set_verify_full")
 
     def set_mtp_enabled(self, enabled):
         self.ctx.check(lib().pf_engine_set_mtp_enabled(self.h, int(enabled)), "pf_engine_set_mtp_enabled")

@@ -7,11 +7,17 @@
 // Philox4x32-10 keyed by the run seed with the draw index as counter.
 //
 // The decode round (src/engine.cpp:304-373) runs as: sample T1 from the
-// base logits, sample one draft per MTP head, one verify pass over
-// [T1, d0..d{n-1}], greedy argmax of every verify row, accept the longest
-// matching prefix, sample the corrective from the first mismatching row.
-// Every token decision is made here; the host reads one 32-bit word per
-// round (accepted count | corrective pushed << 8).
+// base logits, sample one draft per MTP head, verify [T1, d0..d{n-1}] in
+// one or two passes (segments), greedy argmax of every verify row, accept
+// the longest matching prefix, sample the corrective from the first
+// mismatching row.  Row j of the verify rows checks draft j (row n, fed
+// d{n-1}, is the next round's F(cur)).  A segment covers rows k0 .. k0+m-1;
+// the reference verifies one row at a time and stops at the first
+// mismatch, so a segment that ends with a mismatch has done all the work
+// the reference does, and one that accepts every row it checked leaves the
+// rest to the next segment.  Every token decision is made here; the host
+// reads one 32-bit word per segment (accepted count | corrective pushed << 8
+// | next segment needed << 9).
 #include "pf_device.h"
 
 #include <rocprim/block/block_radix_sort.hpp>
@@ -271,10 +277,8 @@ __global__ __launch_bounds__(1024) void k_sample(const float* __restrict__ logit
                                                  int32_t* tokens, uint32_t cap, PassDesc* pdB, int32_t role,
                                                  int32_t k, int32_t* out) {
     __shared__ uint32_t skip;
-    if (threadIdx.x == 0) {
-        uint32_t n_mtp = pdB ? pdB->m - 1 : 0;
-        skip = (role == ROLE_CORRECTIVE && st->round_acc >= n_mtp) ? 1u : 0u;
-    }
+    if (threadIdx.x == 0)
+        skip = (role == ROLE_CORRECTIVE && (st->round_acc >= st->n_mtp || st->more)) ? 1u : 0u;
     __syncthreads();
     if (skip) return;
     const uint32_t r = row >= 0 ? (uint32_t)row : st->round_acc;
@@ -283,12 +287,15 @@ __global__ __launch_bounds__(1024) void k_sample(const float* __restrict__ logit
     if (threadIdx.x != 0) return;
     if (used) st->draw++;
     switch (role) {
-        case ROLE_T1:
+        case ROLE_T1:   // k: rows of the first verify segment
             push_token(st, tokens, cap, t);
             pdB->tok[0] = t;
             pdB->pos0 = st->pos;
+            pdB->m = (uint32_t)k;
             pdB->batch = 0;
             pdB->seq0 = 0;
+            st->seg_k0 = 0;
+            st->more = 0;
             break;
         case ROLE_DRAFT:
             st->draft[k] = t;
@@ -326,25 +333,46 @@ __global__ void k_ctl_reuse_row(DecodeState* st) {
     st->have_row4 = 0;
 }
 
-// Acceptance (src/engine.cpp:333-365) given the greedy argmax of every
-// verify row: accepted prefix pushed, positions committed.
+// Acceptance (src/engine.cpp:333-365) of one verify segment given the
+// greedy argmax of its rows (row r checks draft seg_k0 + r): accepted
+// drafts pushed, the positions of the rows the reference would have
+// forwarded committed.
 __global__ void k_ctl_accept(DecodeState* st, const PassDesc* pdB, int32_t* tokens, uint32_t cap) {
-    const uint32_t n_mtp = pdB->m - 1;
-    uint32_t a = 0;
-    while (a < n_mtp && st->row_argmax[a] == st->draft[a]) {
+    const uint32_t n_mtp = st->n_mtp, k0 = st->seg_k0, m = pdB->m;
+    uint32_t a = k0, r = 0;
+    while (r < m && a < n_mtp && st->row_argmax[r] == st->draft[a]) {
         push_token(st, tokens, cap, st->draft[a]);
         a++;
+        r++;
     }
     st->round_acc = a;
-    st->accepted += a;
-    if (a < n_mtp) {
-        st->pos = pdB->pos0 + a + 1;
-        st->have_row4 = 0;
-    } else {
-        st->pos = pdB->pos0 + n_mtp;
+    st->accepted += a - k0;
+    st->more = 0;
+    st->have_row4 = 0;
+    if (a < n_mtp && r < m) {         // mismatch at row r: rows 0..r were forwarded
+        st->pos = pdB->pos0 + r + 1;
+    } else if (a < n_mtp) {           // every row accepted, drafts remain: next segment
+        st->pos = pdB->pos0 + m;
+        st->seg_k0 = a;
+        st->more = 1;
+    } else if (r < m) {               // all drafts accepted; row r holds F(last draft)
+        st->pos = pdB->pos0 + r;
         st->have_row4 = 1;
+    } else {                          // all drafts accepted by the segment's last row
+        st->pos = pdB->pos0 + m;
     }
-    st->round_word = a;
+    st->round_word = a | (st->more << 9);
+}
+
+// Setup of a verify segment that continues a round: rows check drafts
+// k0 .. n_mtp - 1 (inputs d{k0-1} .. d{n-2}) and end with F(d{n-1}).
+__global__ void k_ctl_segment(DecodeState* st, PassDesc* pdB) {
+    const uint32_t k0 = st->seg_k0, m = st->n_mtp - k0 + 1;
+    pdB->pos0 = st->pos;
+    pdB->m = m;
+    pdB->batch = 0;
+    pdB->seq0 = 0;
+    for (uint32_t r = 0; r < m; r++) pdB->tok[r] = st->draft[k0 - 1 + r];
 }
 
 // ------------------------------------------- multi-sequence decode rounds

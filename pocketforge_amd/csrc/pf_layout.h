@@ -93,6 +93,9 @@ struct DecodeState {
     int32_t draft[8];      // drafts of the current round
     int32_t row_argmax[8]; // greedy argmax of each pass-B row
     uint32_t round_acc;    // accepted drafts in the current round
+    uint32_t n_mtp;        // drafts per MTP round (single-sequence engine)
+    uint32_t seg_k0;       // draft index checked by row 0 of the current verify segment
+    uint32_t more;         // the segment accepted every row it checked, drafts remain
     uint32_t pad;
 };
 

@@ -1168,7 +1168,10 @@ struct pf_engine {
     size_t timed_used = 0;
     // captured decode rounds: [reuse][mtp] -> graph exec, for one sampling
     // configuration / seed / profiling mode
-    hipGraphExec_t round_exec[2][2] = {{nullptr, nullptr}, {nullptr, nullptr}};
+    // [reuse][mtp][first verify segment: 1 row, or all n_mtp + 1 rows]
+    hipGraphExec_t round_exec[2][2][2] = {};
+    hipGraphExec_t cont_exec = nullptr;   // the verify segment that continues a round (drafts 1..n_mtp-1)
+    bool verify_full = false;             // always verify all drafts in one segment
     uint32_t round_ev[2][2][4] = {};   // pass-event and GEMV-event slot ranges of each variant
     hipEvent_t rev0 = nullptr, rev1 = nullptr;
     double round_us = 0;
@@ -1328,8 +1331,10 @@ extern "C" void pf_engine_destroy(pf_engine* e) {
     for (auto& t : e->kev) { (void)hipEventDestroy(t.a); (void)hipEventDestroy(t.b); }
     for (auto& t : e->aev) { (void)hipEventDestroy(t.a); (void)hipEventDestroy(t.b); }
     for (auto& row : e->round_exec)
-        for (auto& g : row)
-            if (g) (void)hipGraphExecDestroy(g);
+        for (auto& col : row)
+            for (auto& g : col)
+                if (g) (void)hipGraphExecDestroy(g);
+    if (e->cont_exec) (void)hipGraphExecDestroy(e->cont_exec);
     if (e->rev0) (void)hipEventDestroy(e->rev0);
     if (e->rev1) (void)hipEventDestroy(e->rev1);
     for (auto& p : e->owned) dfree(e->c, p.first, p.second);
@@ -1447,6 +1452,12 @@ extern "C" pf_status pf_engine_kv_export(pf_engine* e, uint32_t seq, uint32_t la
     counts[1] = vw.pool;
     counts[2] = n_win;
     counts[3] = n_pend;
+    return PF_OK;
+}
+
+extern "C" pf_status pf_engine_set_verify_full(pf_engine* e, int32_t full) {
+    if (!e) return PF_ERR_ARG;
+    e->verify_full = full != 0;
     return PF_OK;
 }
 
@@ -1796,9 +1807,11 @@ extern "C" pf_status pf_sample(pf_engine* e, const float* logits, const pf_sampl
 
 // One decode round, all on the engine's stream (capturable): the base pass
 // (or reuse of the last verify row), then either the MTP round
-// (src/engine.cpp:308-365: T1, drafts, verify pass, acceptance,
-// corrective) or the single-token step (src/engine.cpp:377-386).
-static pf_status round_body(pf_engine* e, bool reuse, bool mtp, const SamplingCfg& cfg, uint64_t seed) {
+// (src/engine.cpp:308-365: T1, drafts, the first verify segment of h rows,
+// acceptance, corrective) or the single-token step (src/engine.cpp:377-386).
+// Verify row j sits at row j of logitsB / hiddenB in every segment.
+static pf_status round_body(pf_engine* e, bool reuse, bool mtp, const SamplingCfg& cfg, uint64_t seed,
+                            uint32_t h) {
     pf_ctx* c = e->c;
     hipStream_t st = c->stream;
     const pf_model_desc& d = e->m->d;
@@ -1823,16 +1836,15 @@ static pf_status round_body(pf_engine* e, bool reuse, bool mtp, const SamplingCf
     }
     if (mtp) {
         hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, base_logits, V, 0, V, cfg, seed, e->st, e->tokens,
-                           e->tok_cap, e->pdB, (int32_t)ROLE_T1, 0, (int32_t*)nullptr);
+                           e->tok_cap, e->pdB, (int32_t)ROLE_T1, (int32_t)h, (int32_t*)nullptr);
         if ((s = mtp_chain(e, base_hidden, true, &cfg, seed))) return s;
         if ((s = timed_begin(e, true, &tp))) return s;
         e->in_verify = true;
-        s = run_pass(e, e->pdB, NM + 1, e->pos + 1, e->logitsB, e->hiddenB);
+        s = run_pass(e, e->pdB, h, e->pos + 1, e->logitsB, e->hiddenB);
         e->in_verify = false;
         if (s) return s;
         if (tp) PF_HIP(c, hipEventRecord(tp->b, st));
-        hipLaunchKernelGGL(k_argmax_rows, dim3(NM + 1), dim3(1024), 0, st, e->logitsB, V, V, e->pdB,
-                           e->st->row_argmax);
+        hipLaunchKernelGGL(k_argmax_rows, dim3(h), dim3(1024), 0, st, e->logitsB, V, V, e->pdB, e->st->row_argmax);
         hipLaunchKernelGGL(k_ctl_accept, dim3(1), dim3(1), 0, st, e->st, e->pdB, e->tokens, e->tok_cap);
         if (e->skip_on) launch_skip_commit(e, e->pdB, NM + 1, 0, 0, true);
         hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, e->logitsB, V, -1, V, cfg, seed, e->st, e->tokens,
@@ -1845,36 +1857,73 @@ static pf_status round_body(pf_engine* e, bool reuse, bool mtp, const SamplingCf
     return PF_OK;
 }
 
-// Captures the four round variants as graphs for this sampling
-// configuration and seed (kernel arguments are baked into the graphs; the
-// positions and tokens live in device memory).
-static pf_status ensure_round_graphs(pf_engine* e, const SamplingCfg& cfg, uint64_t seed) {
+// The verify segment that continues a round whose first segment (one row)
+// accepted its draft: rows 1 .. n_mtp (inputs d0 .. d{n-1}) at verify rows
+// 1 .. n_mtp of logitsB, acceptance and corrective.
+static pf_status segment_body(pf_engine* e, const SamplingCfg& cfg, uint64_t seed) {
     pf_ctx* c = e->c;
+    hipStream_t st = c->stream;
+    const pf_model_desc& d = e->m->d;
+    const uint32_t V = d.n_vocab, D = d.n_embd, NM = d.n_mtp;
+    pf_status s;
+    TimedPass* tp = nullptr;
+    hipLaunchKernelGGL(k_ctl_segment, dim3(1), dim3(1), 0, st, e->st, e->pdB);
+    if ((s = timed_begin(e, true, &tp))) return s;
+    e->in_verify = true;
+    s = run_pass(e, e->pdB, NM, e->pos, e->logitsB + V, e->hiddenB + D);
+    e->in_verify = false;
+    if (s) return s;
+    if (tp) PF_HIP(c, hipEventRecord(tp->b, st));
+    hipLaunchKernelGGL(k_argmax_rows, dim3(NM), dim3(1024), 0, st, e->logitsB + V, V, V, e->pdB, e->st->row_argmax);
+    hipLaunchKernelGGL(k_ctl_accept, dim3(1), dim3(1), 0, st, e->st, e->pdB, e->tokens, e->tok_cap);
+    hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, e->logitsB, V, -1, V, cfg, seed, e->st, e->tokens,
+                       e->tok_cap, e->pdB, (int32_t)ROLE_CORRECTIVE, 0, (int32_t*)nullptr);
+    PF_LAUNCHED(c);
+    return PF_OK;
+}
+
+// Captures the round variants (reuse x MTP x first-segment height) and the
+// continuation segment as graphs for this sampling configuration and seed
+// (kernel arguments are baked into the graphs; the positions and tokens
+// live in device memory).
+static pf_status capture(pf_engine* e, hipGraphExec_t* out, int which, bool reuse, bool mtp, uint32_t h,
+                         const SamplingCfg& cfg, uint64_t seed) {
+    pf_ctx* c = e->c;
+    hipGraph_t graph = nullptr;
+    PF_HIP(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    e->capturing = true;
+    pf_status s = which == 0 ? round_body(e, reuse, mtp, cfg, seed, h) : segment_body(e, cfg, seed);
+    e->capturing = false;
+    hipError_t ee = hipStreamEndCapture(c->stream, &graph);
+    if (s) { if (graph) (void)hipGraphDestroy(graph); return s; }
+    if (ee != hipSuccess) return fail(c, PF_ERR_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(ee));
+    ee = hipGraphInstantiate(out, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (ee != hipSuccess) return fail(c, PF_ERR_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(ee));
+    return PF_OK;
+}
+
+static pf_status ensure_round_graphs(pf_engine* e, const SamplingCfg& cfg, uint64_t seed) {
     if (e->graphs_valid && e->graph_seed == seed && e->graph_profile == e->profile &&
         std::memcmp(&e->graph_cfg, &cfg, sizeof(cfg)) == 0)
         return PF_OK;
     for (auto& row : e->round_exec)
-        for (auto& g : row)
-            if (g) { (void)hipGraphExecDestroy(g); g = nullptr; }
+        for (auto& col : row)
+            for (auto& g : col)
+                if (g) { (void)hipGraphExecDestroy(g); g = nullptr; }
+    if (e->cont_exec) { (void)hipGraphExecDestroy(e->cont_exec); e->cont_exec = nullptr; }
     e->graphs_valid = false;
     e->timed_used = 0;
     e->kev_used = 0;
+    const uint32_t NM = e->m->d.n_mtp;
     for (int reuse = 0; reuse < 2; reuse++)
-        for (int mtp = 0; mtp < 2; mtp++) {
-            hipGraph_t graph = nullptr;
-
-            PF_HIP(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-            e->capturing = true;
-            pf_status s = round_body(e, reuse != 0, mtp != 0, cfg, seed);
-            e->capturing = false;
-
-            hipError_t ee = hipStreamEndCapture(c->stream, &graph);
-            if (s) { if (graph) (void)hipGraphDestroy(graph); return s; }
-            if (ee != hipSuccess) return fail(c, PF_ERR_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(ee));
-            ee = hipGraphInstantiate(&e->round_exec[reuse][mtp], graph, nullptr, nullptr, 0);
-            (void)hipGraphDestroy(graph);
-            if (ee != hipSuccess) return fail(c, PF_ERR_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(ee));
-        }
+        for (int mtp = 0; mtp < 2; mtp++)
+            for (int full = 0; full < (mtp ? 2 : 1); full++)
+                if (pf_status s = capture(e, &e->round_exec[reuse][mtp][full], 0, reuse != 0, mtp != 0,
+                                          full ? NM + 1 : 1u, cfg, seed))
+                    return s;
+    if (NM > 1)
+        if (pf_status s = capture(e, &e->cont_exec, 1, false, true, NM, cfg, seed)) return s;
     e->graph_cfg = cfg;
     e->graph_seed = seed;
     e->graph_profile = e->profile;
@@ -1941,6 +1990,7 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
     s0.pos = e->pos;
     s0.cur = n_prompt ? prompt[n_prompt - 1] : 0;
     s0.n_tokens = n_prompt;
+    s0.n_mtp = NM;
     PF_HIP(c, hipMemcpyAsync(e->st, &s0, sizeof(s0), hipMemcpyHostToDevice, st));
     PF_HIP(c, hipStreamSynchronize(st));
     auto t1 = std::chrono::steady_clock::now();
@@ -1962,6 +2012,33 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
     }
     uint32_t n_gen = 0;
     bool have_row = false;
+    uint32_t last_acc = 0;   // drafts the previous MTP round accepted
+    // One segment (a graph or, in profiling mode, its kernels one by one)
+    // timed with the round events and its dispatch events harvested.
+    auto segment = [&](hipGraphExec_t g, bool cont, bool reuse, bool mtp, uint32_t h) -> pf_status {
+        size_t ev[4] = {0, 0, 0, 0};
+        PF_HIP(c, hipEventRecord(e->rev0, st));
+        if (graphs) {
+            PF_HIP(c, hipGraphLaunch(g, st));
+        } else {
+            e->timed_used = 0;
+            e->kev_used = 0;
+            pf_status s = cont ? segment_body(e, cfg, seed) : round_body(e, reuse, mtp, cfg, seed, h);
+            if (s) return s;
+            ev[1] = e->timed_used;
+            ev[3] = e->kev_used;
+        }
+        PF_HIP(c, hipEventRecord(e->rev1, st));
+        if (mtp) PF_HIP(c, hipMemcpyAsync(e->word, &e->st->round_word, 4, hipMemcpyDeviceToHost, st));
+        PF_HIP(c, hipStreamSynchronize(st));
+        if (pf_status s = harvest_events(e, ev[0], ev[1], ev[2], ev[3])) return s;
+        if (mtp) {
+            float rms = 0;
+            PF_HIP(c, hipEventElapsedTime(&rms, e->rev0, e->rev1));
+            e->round_us += rms * 1000.0;
+        }
+        return PF_OK;
+    };
     while (n_gen < max_new) {
         if (e->max_memory && c->bytes > e->max_memory) {   // src/engine.cpp:297-301
             res->oom_protected = 1;
@@ -1970,43 +2047,48 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
         const bool mtp_round = e->mtp_enabled && NM > 0 && e->hidden_valid && n_gen + 4 <= max_new;   // src/engine.cpp:304-305
         if (e->pos + NM + 2 > e->rope_pos)
             return fail(c, PF_ERR_CAPACITY, "position beyond the engine's max_context");
-        pf_status s;
-        size_t ev[4];
-        PF_HIP(c, hipEventRecord(e->rev0, st));
-        if (graphs) {
-            PF_HIP(c, hipGraphLaunch(e->round_exec[have_row][mtp_round], st));
-            for (int i = 0; i < 4; i++) ev[i] = 0;
-            e->hidden_valid = true;
-        } else {
-            e->timed_used = 0;
-            e->kev_used = 0;
-            if ((s = round_body(e, have_row, mtp_round, cfg, seed))) return s;
-            ev[0] = 0; ev[1] = e->timed_used; ev[2] = 0; ev[3] = e->kev_used;
-        }
-        PF_HIP(c, hipEventRecord(e->rev1, st));
+        // first verify segment: every row after a round that accepted a draft
+        // (or when asked for); one row, the reference's first verify forward,
+        // after a round whose first draft was rejected
+        const bool full = e->verify_full || e->skip_on || last_acc > 0 || NM < 2;
+        const uint32_t h = full ? NM + 1 : 1u;
+        if (pf_status s = segment(graphs ? e->round_exec[have_row][mtp_round][mtp_round && full] : nullptr, false,
+                                  have_row, mtp_round, h))
+            return s;
+        e->hidden_valid = true;
         res->passes += (have_row ? 0 : 1) + (mtp_round ? 1 : 0);
         e->pos += 1;   // the base position (pass A, or the reused verify row)
         if (mtp_round) {
-            PF_HIP(c, hipMemcpyAsync(e->word, &e->st->round_word, 4, hipMemcpyDeviceToHost, st));
-            PF_HIP(c, hipStreamSynchronize(st));
-            if ((s = harvest_events(e, ev[0], ev[1], ev[2], ev[3]))) return s;
-            float rms = 0;
-            PF_HIP(c, hipEventElapsedTime(&rms, e->rev0, e->rev1));
-            e->round_us += rms * 1000.0;
+            uint32_t w = e->word[0], a = w & 0xFFu, pushed = (w >> 8) & 1u, more = (w >> 9) & 1u;
+            uint32_t k0 = 0, m = h;
+            if (more) {   // the one-row segment accepted d0: rows for d1 .. d{n-1} and F(d{n-1})
+                if (a != 1 || h != 1) return fail(c, PF_ERR_STATE, "verify continuation from an unexpected draft");
+                e->pos += m;
+                if (pf_status s = segment(e->cont_exec, true, false, true, NM)) return s;
+                res->passes += 1;
+                w = e->word[0];
+                a = w & 0xFFu;
+                pushed = (w >> 8) & 1u;
+                if ((w >> 9) & 1u) return fail(c, PF_ERR_STATE, "verify segment left drafts unchecked");
+                k0 = 1;
+                m = NM;
+            }
             e->round_n++;
-            const uint32_t w = e->word[0], a = w & 0xFFu, pushed = (w >> 8) & 1u;
             n_gen += 1 + a + pushed;
             res->rounds++;
+            const uint32_t r = a - k0;   // rows of the last segment whose drafts were accepted
             if (a < NM) {
-                e->pos += a + 1;
+                e->pos += r + 1;
                 have_row = false;
+            } else if (r < m) {
+                e->pos += r;
+                have_row = true;         // that segment's last row holds F(cur)
             } else {
-                e->pos += NM;
-                have_row = true;
+                e->pos += m;
+                have_row = false;
             }
+            last_acc = a;
         } else {
-            PF_HIP(c, hipStreamSynchronize(st));
-            if ((s = harvest_events(e, ev[0], ev[1], ev[2], ev[3]))) return s;
             n_gen += 1;
             have_row = false;
         }

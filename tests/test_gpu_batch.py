@@ -102,6 +102,7 @@ def test_batch_generate_matches_single_engines(gpu, tiny_weights, which, samp):
     for s in range(n_seq):
         print(f"sequence {s}: prompt {lens[s]}", flush=True)
         e = pf.Engine(m, **KV)
+        e.set_verify_full(1)      # the batched rounds verify every draft in one pass
         t, r = e.generate(prompts[s], 23, samp, int(seeds[s]))
         e.close()
         np.testing.assert_array_equal(toks_b[s], t, err_msg=f"sequence {s}")

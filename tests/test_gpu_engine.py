@@ -122,6 +122,39 @@ def test_generate_greedy_matches_oracle(gpu, tiny_weights, case):
         print("mixed: accepted", oa, "rejected", orj)
 
 
+@pytest.mark.parametrize("case", ["full_accept", "mixed", "random"])
+@pytest.mark.parametrize("full", [0, 1])
+def test_generate_verify_segments(gpu, tiny_weights, case, full):
+    """Both verify policies give the oracle's stream: every draft in one
+    pass, or a one-row first segment after a round with no accepted draft,
+    continued by a second segment when that draft is accepted (the full
+    acceptance case starts that way: its first round accepts everything
+    through the continuation and hands F(cur) to the next round)."""
+    cfg, w = tiny_weights
+    if case == "full_accept":
+        w = _zero_mats(w)
+    elif case == "mixed":
+        w = _zero_mats(w, scale=0.004, seed=5)
+    prompt = W.prompt_ids(20, cfg["n_vocab"], seed=9)
+    m = pf.Model(gpu, cfg, w)
+    e = pf.Engine(m, **KV)
+    e.set_verify_full(full)
+    toks, res = e.generate(prompt, 70, GREEDY, 7)
+    om = _oracle(cfg, w, KV)
+    ot, oa, orj = om.generate(prompt, 70, O.Sampling(0.8, 0.95, 40, 1), 7)
+    om.close()
+    np.testing.assert_array_equal(toks, ot)
+    assert (res.mtp_accepted, res.mtp_rejected) == (oa, orj)
+    # passes: one base pass per round without a reused row, one verify
+    # segment per round, one more for every continued round, and the
+    # single-token steps of the last tokens (n + 4 > N)
+    assert res.passes >= res.rounds
+    if full:
+        assert res.passes <= 2 * res.rounds + 4
+    e.close()
+    m.close()
+
+
 @pytest.mark.parametrize("samp", [TOP_P, TEMP, TOP_K], ids=["top_p", "temperature", "top_k"])
 def test_generate_stochastic_matches_oracle(gpu, tiny_weights, samp):
     cfg, w = tiny_weights
