@@ -350,7 +350,9 @@ constexpr uint32_t ag_smem(uint32_t nr) { return 2u * 256u * 128u + (512u + nr *
 // first row), then its fp32 self entry at list index C + r.  A group of n
 // rows is served by ceil(n / NR) blocks of at most NR rows each.
 // Grid (heads * chunks, M), 256 threads: block (x, m) serves share
-// m - m0 of the group led by row m0 (if that share exists).
+// m - m0 of the group led by row m0 (if that share exists).  With pf.p set
+// the grid has one more row of blocks, which stream pf's bytes (the next
+// kernel's weights) through the cache hierarchy instead.
 //
 // FUSED (passes of at most 8 rows): the pass's own K/V rows are not yet in
 // the cache.  Entries at positions of this pass are quantized here from the
@@ -364,9 +366,13 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
                                                     uint32_t layer, uint32_t M, const float* __restrict__ q,
                                                     const float* __restrict__ kself, const float* __restrict__ vself,
                                                     float* __restrict__ S, uint32_t s_stride,
-                                                    float* __restrict__ Up, uint32_t cstride) {
+                                                    float* __restrict__ Up, uint32_t cstride, Prefetch pf) {
     constexpr uint32_t hd = 16 * PARTS;
     __shared__ __align__(16) uint8_t smem[ag_smem(NR)];
+    if (blockIdx.y >= M) {
+        prefetch_bytes(pf.p, pf.n, blockIdx.x, gridDim.x, pf.sink);
+        return;
+    }
     int4* kt = reinterpret_cast<int4*>(smem);                       // [PARTS][256], swizzled
     int8_t (*vt)[128] = reinterpret_cast<int8_t (*)[128]>(smem + 256u * 128u);
     float* ksc = reinterpret_cast<float*>(smem + 512u * 128u);      // [256]

@@ -29,7 +29,7 @@ namespace pf {
 typedef int pf_v4i __attribute__((ext_vector_type(4)));
 typedef int pf_v16i __attribute__((ext_vector_type(16)));
 
-enum Pro : int { PRO_NORM = 0, PRO_QUANT = 1, PRO_INT8 = 2, PRO_QPART = 3 };
+enum Pro : int { PRO_NORM = 0, PRO_QUANT = 1, PRO_INT8 = 2, PRO_QPART = 3, PRO_MERGE = 4 };
 enum Epi : int { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_SWIGLU = 3 };
 
 // Consumer step applied to the outputs.  Row n is a device row (pf_layout.h).
@@ -154,6 +154,11 @@ struct GemvArgs {
     const float* pin;          // QPART: row maxima partials of the input [M][np]
     uint32_t np;
     const uint32_t* gate;      // gated instances: 0 -> nothing to compute
+    const float* S;            // MERGE: per (head, chunk) maximum and sum [H][s_stride] of row 0
+    uint32_t s_stride;
+    const float* Up;           // MERGE: chunk-weighted V [H][cstride][hd] of row 0
+    uint32_t cstride;
+    KvGeom g;                  // MERGE: chunk count of row 0's list
     MmEpi e;
 };
 
@@ -165,6 +170,9 @@ __host__ __device__ constexpr uint32_t gemv_smem(uint32_t M, uint32_t K) {
     return (uint32_t)GEMV_WAVES * 64u * 4u * 8u + M * gemv_kp(K) + M * (K / 64u) * 4u +
            M * 4u * (uint32_t)GEMV_WAVES * 4u + 3u * 8u * 4u;
 }
+// MERGE adds the chunk maxima and sums [2][2048] (heads * chunks <= 2048),
+// the head maxima and 1 / T [2][128] and a block reduction [16].
+constexpr uint32_t GEMV_MERGE_SMEM = (2u * 2048u + 2u * 128u + 16u) * 4u;
 
 // Codes of four values with the row's 127 / amax.
 __device__ __forceinline__ uint32_t pack_codes(float4 v, float q) {
@@ -196,6 +204,11 @@ __device__ __forceinline__ float max4abs(float4 v) {
 //   QUANT: the row held (CPW float4 per thread and row), amax, codes.
 //   QPART: the same, amax from the producer's per-workgroup maxima.
 //   INT8 : rows quantized by another kernel, copied.
+//   MERGE: (M == 1, K = heads * head_dim <= 2048) the attention's chunk
+//          results of the row merged per head exactly as merge_quant_row
+//          does (max over the chunk maxima, f_c = exp(m_c - max), T and U
+//          fmaf chains over c in order, U * (1 / (T + 1e-10))), then the
+//          row quantized (quantize_activation_row).
 template <int FMT, int PRO, int EPI, bool GATED, int CPW, int MR>
 __global__ __launch_bounds__(64 * GEMV_WAVES) void k_gemv(GemvArgs a) {
     constexpr uint32_t TB = g32_tile_bytes(FMT), CODES = g32_code_bytes(FMT);
@@ -237,7 +250,42 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void k_gemv(GemvArgs a) {
             const uint32_t i = t + NT * k, m = min(i / per16, mlast), c = i % per16;
             iv[k] = *reinterpret_cast<const uint4*>(a.a8 + (size_t)m * xs + 16u * c);
         }
-    } else {
+    }
+    // MERGE: the row's (head, chunk) maxima and sums (entry i = h nc + c,
+    // heads * chunks <= 2048), and the first MG chunks of its columns
+    // 4t .. 4t + 3 (head 4t >> hs, elements 4t & (hd - 1) ..; head_dim is a
+    // power of two).  Chunk loads past the list repeat its last chunk, so
+    // every group issues the same loads and the waits stay exact.
+    constexpr int MK = 2048 / NT;
+    constexpr uint32_t MG = 8;
+    uint32_t nc = 1, hn = 1, hs = 0;
+    uint32_t sh[MK], sc[MK];                  // head and chunk of S entry t + NT k
+    float sm[MK], sv[MK];
+    float4 uc[MG];
+    const float* upc = nullptr;               // this thread's columns in chunk 0
+    if constexpr (PRO == PRO_MERGE) {
+        static_assert(MR == 1, "the merge prologue serves one row");
+        nc = (kv_view(a.g, row_pos(a.e.pd, 0)).count() + 1u + 255u) / 256u;
+        hn = a.g.n_heads * nc;
+        hs = (uint32_t)__builtin_ctz(a.e.hd);
+        const float rnc = 1.0f / (float)nc;
+#pragma unroll
+        for (int k = 0; k < MK; k++) {
+            const uint32_t i = min(t + NT * k, hn - 1u);
+            uint32_t hh = (uint32_t)((float)i * rnc);     // i / nc, corrected below
+            hh -= hh * nc > i ? 1u : 0u;
+            hh += (hh + 1u) * nc <= i ? 1u : 0u;
+            sh[k] = hh;
+            sc[k] = t + NT * k < hn ? i - hh * nc : 0xFFFFFFFFu;
+            sm[k] = a.S[(size_t)hh * a.s_stride + 2u * (i - hh * nc)];
+            sv[k] = a.S[(size_t)hh * a.s_stride + 2u * (i - hh * nc) + 1u];
+        }
+        const uint32_t i4 = min(4u * t, K - 4u);
+        upc = a.Up + (size_t)(i4 >> hs) * a.cstride * a.e.hd + (i4 & (a.e.hd - 1u));
+#pragma unroll
+        for (uint32_t u = 0; u < MG; u++)
+            uc[u] = *reinterpret_cast<const float4*>(upc + (size_t)min(u, nc - 1u) * a.e.hd);
+    } else if constexpr (PRO != PRO_INT8 && PRO != PRO_NORM) {
 #pragma unroll
         for (uint32_t m = 0; m < MR; m++)
 #pragma unroll
@@ -268,7 +316,82 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void k_gemv(GemvArgs a) {
     const EpiPre pre = epi_prefetch<EPI>(a.e, min(om, mlast), on);
 
     // ---- prologue arithmetic
-    if constexpr (PRO == PRO_INT8) {
+    if constexpr (PRO == PRO_MERGE) {
+        float* fsm = st + 24;                    // [2048] chunk maxima, then f_c
+        float* tsm = fsm + 2048;                 // [2048] chunk sums
+        float* hmx = tsm + 2048;                 // [128] head maxima
+        float* hiv = hmx + 128;                  // [128] 1 / (T + 1e-10) per head
+        float* mred = hiv + 128;                 // [16]
+        const uint32_t H = a.g.n_heads, hd = a.e.hd;
+#pragma unroll
+        for (int k = 0; k < MK; k++) {
+            if (sc[k] < nc) {
+                fsm[sh[k] * nc + sc[k]] = sm[k];
+                tsm[sh[k] * nc + sc[k]] = sv[k];
+            }
+        }
+        __syncthreads();
+        if (t < H) {
+            const float* f = fsm + t * nc;
+            float mx = f[0];
+            for (uint32_t c = 1; c < nc; c++) mx = fmaxf(mx, f[c]);
+            hmx[t] = mx;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < MK; k++)
+            if (sc[k] < nc) fsm[sh[k] * nc + sc[k]] = expf_c(sm[k] - hmx[sh[k]]);
+        __syncthreads();
+        // T per head (lane h) beside the U chains; read after the next barrier
+        if (t < H) {
+            const float* f = fsm + t * nc;
+            const float* ts = tsm + t * nc;
+            float T = 0.0f;
+            for (uint32_t c = 0; c < nc; c++) T = __builtin_fmaf(ts[c], f[c], T);
+            hiv[t] = 1.0f / (T + 1e-10f);
+        }
+        // U chains over c in order, MG chunks at a time, the next group's
+        // loads issued before this group's FMAs
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float* f0 = fsm + (min(4u * t, K - 4u) >> hs) * nc;
+        for (uint32_t c0 = 0; c0 < nc; c0 += MG) {
+            float4 un[MG];
+#pragma unroll
+            for (uint32_t u = 0; u < MG; u++)
+                un[u] = *reinterpret_cast<const float4*>(upc + (size_t)min(c0 + MG + u, nc - 1u) * hd);
+            const uint32_t nb = min(MG, nc - c0);
+#pragma unroll
+            for (uint32_t u = 0; u < MG; u++) {
+                if (u < nb) {
+                    const float f = f0[c0 + u];
+                    v.x = __builtin_fmaf(uc[u].x, f, v.x);
+                    v.y = __builtin_fmaf(uc[u].y, f, v.y);
+                    v.z = __builtin_fmaf(uc[u].z, f, v.z);
+                    v.w = __builtin_fmaf(uc[u].w, f, v.w);
+                }
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < MG; u++) uc[u] = un[u];
+        }
+        __syncthreads();
+        // the row's amax: wave maxima meet in LDS behind one barrier
+        const bool own = 4u * t < K;
+        const float hv4 = hiv[min(4u * t, K - 4u) >> hs];
+        v.x *= hv4;
+        v.y *= hv4;
+        v.z *= hv4;
+        v.w *= hv4;
+        float amax = own ? max4abs(v) : 0.0f;
+        amax = wave_max(amax);
+        if (lane == 0) mred[wid] = amax;
+        __syncthreads();
+        amax = mred[0];
+#pragma unroll
+        for (uint32_t w = 1; w < GEMV_WAVES; w++) amax = fmaxf(amax, mred[w]);
+        const float qq = amax == 0.0f ? 1.0f : 127.0f / amax;
+        if (own) *reinterpret_cast<uint32_t*>(act + 4u * t) = pack_codes(v, qq);
+        if (t == 0) st_as[0] = amax == 0.0f ? 1.0f : amax / 127.0f;
+    } else if constexpr (PRO == PRO_INT8) {
 #pragma unroll
         for (int k = 0; k < 2; k++) {
             const uint32_t i = t + NT * k, m = i / per16, c = i % per16;

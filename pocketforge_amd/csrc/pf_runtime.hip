@@ -361,11 +361,12 @@ enum MmKind : int {
     MM_DOWN = 4,      // QPART -> RESID              (down)
     MM_DOWN_SKIP = 5, // QPART -> RESID, gated       (down, layer skip)
     MM_STORE = 6,     // QUANT -> STORE              (kernel-level entry point)
+    MM_O_MERGE = 7,   // MERGE -> RESID              (O projection of a one-row pass, chunk merge fused)
 };
 
 template <int F, int PRO, int EPI, bool G, int CPW, int MR>
 static void gemv_one(hipStream_t st, const GemvArgs& a, hipEvent_t ev0, hipEvent_t ev1) {
-    const uint32_t smem = gemv_smem(a.M, a.K);
+    const uint32_t smem = gemv_smem(a.M, a.K) + (PRO == PRO_MERGE ? GEMV_MERGE_SMEM : 0u);
     static bool attr = false;   // LDS beyond 64 KiB is granted per kernel
     if (!attr) {
         (void)hipFuncSetAttribute((const void*)k_gemv<F, PRO, EPI, G, CPW, MR>,
@@ -420,6 +421,7 @@ static void launch_gemv(hipStream_t st, const pf_matrix* W, MmKind kind, const G
     switch (kind) {
         case MM_QKV: PF_MM_FMT(W->fmt, (gemv_mr<F, PRO_NORM, EPI_QKV, false, 1>(st, a, ev0, ev1))) break;
         case MM_O: PF_MM_FMT(W->fmt, (gemv_mr<F, PRO_INT8, EPI_RESID, false, 1>(st, a, ev0, ev1))) break;
+        case MM_O_MERGE: PF_MM_FMT(W->fmt, (gemv_one<F, PRO_MERGE, EPI_RESID, false, 1, 1>(st, a, ev0, ev1))) break;
         case MM_GU: PF_MM_FMT(W->fmt, (gemv_mr<F, PRO_NORM, EPI_SWIGLU, false, 1>(st, a, ev0, ev1))) break;
         case MM_GU_SKIP: PF_MM_FMT(W->fmt, (gemv_mr<F, PRO_QUANT, EPI_SWIGLU, true, 1>(st, a, ev0, ev1))) break;
         case MM_DOWN: PF_MM_FMT(W->fmt, (gemv_cpw<F, PRO_QPART, EPI_RESID, false>(st, a, ev0, ev1))) break;
@@ -511,16 +513,17 @@ static int per_for(uint32_t K) {
 static bool attn_fused(uint32_t M) { return M <= AG_MAX_ROWS; }
 static void launch_attn(hipStream_t st, uint32_t hd, uint32_t M, uint32_t tasks, const PassDesc* pd,
                         const KvGeom& g, const KvPlanes& kv, uint32_t l, const float* q, const float* k,
-                        const float* v, float* S, uint32_t s_stride, float* Wp, uint32_t cstride,
+                        const float* v, float* S, uint32_t s_stride, float* Wp, uint32_t cstride, Prefetch pf,
                         hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr) {
+    const uint32_t gy = M + (pf.p ? 1u : 0u);   // one more row of blocks prefetches pf
 #define PF_ATTN_LAUNCH(P, F, NR)                                                                              \
     do {                                                                                                      \
         if (ev0)                                                                                              \
-            hipExtLaunchKernelGGL((k_attn_group<P, F, NR>), dim3(tasks, M), dim3(256), 0, st, ev0, ev1, 0, pd, g, \
-                                  kv, l, M, q, k, v, S, s_stride, Wp, cstride);                              \
+            hipExtLaunchKernelGGL((k_attn_group<P, F, NR>), dim3(tasks, gy), dim3(256), 0, st, ev0, ev1, 0, pd, \
+                                  g, kv, l, M, q, k, v, S, s_stride, Wp, cstride, pf);                       \
         else                                                                                                  \
-            hipLaunchKernelGGL((k_attn_group<P, F, NR>), dim3(tasks, M), dim3(256), 0, st, pd, g, kv, l, M, q, k, \
-                               v, S, s_stride, Wp, cstride);                                                  \
+            hipLaunchKernelGGL((k_attn_group<P, F, NR>), dim3(tasks, gy), dim3(256), 0, st, pd, g, kv, l, M, q, \
+                               k, v, S, s_stride, Wp, cstride, pf);                                           \
     } while (0)
 #define PF_ATTN_ROWS(P)                              \
     switch (M) {                                     \
@@ -1615,6 +1618,7 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
     const uint32_t attn_tasks = H * ((cmax + 1 + 255) / 256);
     const uint32_t ks = e->kmax;
     const bool tall = M > GEMV_MAX_M;
+    const bool merge_in_o = M == 1 && D <= 2048;
     // activation scales [4][rows] of the tall passes' row kernels
     float* as0 = e->as;                   // attention-norm act
     float* as1 = e->as + e->rows;         // attention output act
@@ -1654,18 +1658,25 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
             aev1 = e->aev[e->aev_used].b;
             e->aev_used++;
         }
+        // one-row passes merge the chunks in the O product's prologue, and the
+        // attention's extra blocks stream the O weights through the cache
+        // hierarchy; other passes run the merge kernel, whose extra blocks do
         launch_attn(st, hd, M, attn_tasks, pd, g, e->kv, l, e->q, e->k, e->v, e->S, e->s_stride, e->Wp,
-                    e->cstride, aev0, aev1);
-        // chunk merge and the O input's quantization; the extra blocks stream
-        // the O weights through the cache hierarchy
-        PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_attn_merge_quant<PER>, dim3(M + e->pf_blocks), dim3(1024), 0, st, pd,
-                                                g, (const float*)e->S, e->s_stride, (const float*)e->Wp, e->cstride,
-                                                e->act, ks, as1, (int32_t*)nullptr, 0u, M, prefetch_of(e, m->o[l])));
+                    e->cstride, merge_in_o ? prefetch_of(e, m->o[l]) : Prefetch{nullptr, 0, e->sink}, aev0, aev1);
+        if (!merge_in_o)
+            PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_attn_merge_quant<PER>, dim3(M + e->pf_blocks), dim3(1024), 0, st,
+                                                    pd, g, (const float*)e->S, e->s_stride, (const float*)e->Wp,
+                                                    e->cstride, e->act, ks, as1, (int32_t*)nullptr, 0u, M,
+                                                    prefetch_of(e, m->o[l])));
         // O projection + residual (src/engine.cpp:789-800)
         a = GemvArgs{};
         a.a8 = e->act; a.a8s = as1; a.xs = ks;
         a.e.y = e->x; a.e.y_stride = D;
-        if (pf_status s = pass_mm(e, m->o[l], MM_O, M, a, as1)) return s;
+        if (merge_in_o) {
+            a.S = e->S; a.s_stride = e->s_stride; a.Up = e->Wp; a.cstride = e->cstride; a.g = g;
+            a.e.pd = pd; a.e.hd = hd; a.e.D = D;
+        }
+        if (pf_status s = pass_mm(e, m->o[l], merge_in_o ? MM_O_MERGE : MM_O, M, a, as1)) return s;
         // FFN (src/engine.cpp:526-541, 805-854); with layer skip on, the
         // normed rows are staged for the skip decisions and the products run
         // only if some row needs them (gate word)
