@@ -10,6 +10,8 @@
 //                  extend each other): scores, chunk max, exp, chunk sum and
 //                  chunk-weighted V of each row; passes of at most 8 rows
 //                  also quantize and store their own K/V rows here
+//   k_attn_chunk   the same per (row, head, chunk), for batched passes of
+//                  more than 8 rows
 //   k_attn_merge_quant  per row: chunks rescaled to the row max and merged,
 //                  then the O projection's quantize_activation_row
 // The KVCache API (raw scores; weighted sum of caller probabilities) runs
@@ -280,6 +282,160 @@ __global__ void k_wsum_combine_one(const float* __restrict__ Wp, uint32_t nch, u
 // v_scale_j), or of e_j * v_self for the self entry.  Writes
 // S[(m*H + h)*s_stride + 2c] = m_c, [.. + 2c + 1] = T_c and
 // Up[((m*H + h)*cstride + c)*hd + i] = U_c[i].
+
+// Per-row attention, for batched passes of more than 8 rows (many
+// sequences, a few rows each): one block per (row, head, chunk) with the
+// first stage's arithmetic, every thread loading its own entry's K and V
+// rows.  Shared memory of one block (bytes): V rows of the chunk first,
+// VROW = 136 bytes each (8 bytes of padding), which keeps the block under
+// 40 KB, so four blocks fit in a CU's 160 KB.
+constexpr uint32_t att_vt(uint32_t vrow) { return 256 * vrow; }
+constexpr uint32_t att_smem(uint32_t vrow) { return att_vt(vrow) + (128 + 128 + 256 + 256 + 512 + 4) * 4; }
+
+template <int PARTS, uint32_t VROW = 144>
+__device__ __forceinline__ void attn_one_row(const PassDesc* __restrict__ pd, const KvGeom& g, const KvPlanes& kv,
+                                             uint32_t layer, uint32_t m, uint32_t h, uint32_t c,
+                                             const float* __restrict__ q, const float* __restrict__ kself,
+                                             const float* __restrict__ vself, float* __restrict__ S,
+                                             uint32_t s_stride, float* __restrict__ Up, uint32_t cstride,
+                                             uint8_t* smem) {
+    constexpr uint32_t hd = 16 * PARTS;
+    int8_t (*vt)[VROW] = reinterpret_cast<int8_t (*)[VROW]>(smem);
+    float* qs = reinterpret_cast<float*>(smem + att_vt(VROW));
+    float* kss = qs + 128;
+    float* vsc = kss + 128;
+    float* pe = vsc + 256;
+    float* wp = pe + 256;                           // [4][128]
+    float* red = wp + 512;
+    const uint32_t t = threadIdx.x;
+    const uint32_t D = g.n_heads * hd;
+    const KvView v = kv_view(g, row_pos(pd, m));
+    const uint32_t C = v.count(), n = C + 1, j0 = c * 256u;
+    if (j0 >= n) return;
+    const uint32_t j = j0 + t;
+    const size_t plane = plane_index(g, row_seq(pd, m), layer, h);
+    const size_t qrow = (size_t)m * D + h * hd;
+    const uint32_t nvis = j0 < C ? min(256u, C - j0) : 0u;
+    // every load first: the query, the fp32 self key, this thread's K and V rows
+    if (t < hd) {
+        qs[t] = q[qrow + t];
+        kss[t] = kself[qrow + t];
+    }
+    int4 kw[PARTS];
+    float ks = 0.0f, vs = 0.0f;
+    if (t < nvis) {
+        const size_t row = plane * g.rows + kv_row(g, v, j);
+        const int4* kr = reinterpret_cast<const int4*>(kv.k + row * hd);
+        const int4* vr = reinterpret_cast<const int4*>(kv.v + row * hd);
+        int4 vw[PARTS];
+#pragma unroll
+        for (int p = 0; p < PARTS; p++) {
+            kw[p] = kr[p];
+            vw[p] = vr[p];
+        }
+        ks = kv.ks[row];
+        vs = kv.vs[row];
+#pragma unroll
+        for (int p = 0; p < PARTS; p++) {
+            if constexpr (VROW % 16 == 0) {
+                *reinterpret_cast<int4*>(&vt[t][p * 16]) = vw[p];
+                continue;
+            }
+            *reinterpret_cast<int2*>(&vt[t][p * 16]) = make_int2(vw[p].x, vw[p].y);
+            *reinterpret_cast<int2*>(&vt[t][p * 16 + 8]) = make_int2(vw[p].z, vw[p].w);
+        }
+    }
+    vsc[t] = vs;                 // 0 past the visible entries: their terms below add exactly 0
+    __syncthreads();
+    const float scale = 1.0f / __builtin_sqrtf((float)hd);
+    float s = -__builtin_inff();
+    if (t < nvis) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int p = 0; p < PARTS; p++) {
+            const int wv[4] = {kw[p].x, kw[p].y, kw[p].z, kw[p].w};
+#pragma unroll
+            for (int b = 0; b < 16; b++) {
+                const int8_t cb = (int8_t)((wv[b >> 2] >> (8 * (b & 3))) & 0xFF);
+                acc = __builtin_fmaf(qs[p * 16 + b], (float)cb * ks, acc);
+            }
+        }
+        s = acc * scale;
+    } else if (j == C) {
+        float self = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < hd; i++) self = self + qs[i] * kss[i];
+        s = self * scale;
+    }
+    const float mx = block_max<4>(s, red);
+    const float ex = j < n ? expf_c(s - mx) : 0.0f;
+    pe[t] = ex;
+    const float T = block_canon_sum<4>(ex, red);       // its barriers publish pe
+    const uint32_t sc = t >> 6, i0 = 2u * (t & 63u);
+    if (i0 < hd) {
+        float w0 = 0.0f, w1 = 0.0f;
+        // entries [64sc, min(64sc + 64, nvis)) in groups of 8; the padding
+        // entries up to the next multiple of 8 have v_scale 0 and finite
+        // codes and weights, so fmaf(e, code * 0, w) == w
+        const uint32_t e_end = min(64u * sc + 64u, (nvis + 7u) & ~7u);
+        for (uint32_t e = 64u * sc; e < e_end; e += 8) {
+            float pp[8], vv[8];
+            uint32_t cc[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                pp[u] = pe[e + u];
+                vv[u] = vsc[e + u];
+                cc[u] = *reinterpret_cast<const uint16_t*>(&vt[e + u][i0]);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                w0 = __builtin_fmaf(pp[u], (float)(int8_t)(cc[u] & 0xFFu) * vv[u], w0);
+                w1 = __builtin_fmaf(pp[u], (float)(int8_t)(cc[u] >> 8) * vv[u], w1);
+            }
+        }
+        const uint32_t js = C - j0;                     // list index of the self entry in the chunk
+        if (js < 256u && (js >> 6) == sc) {
+            const float p = pe[js];
+            w0 = __builtin_fmaf(p, vself[qrow + i0], w0);
+            w1 = __builtin_fmaf(p, vself[qrow + i0 + 1], w1);
+        }
+        wp[sc * 128 + i0] = w0;
+        wp[sc * 128 + i0 + 1] = w1;
+    }
+    __syncthreads();
+    const size_t mh = (size_t)m * g.n_heads + h;
+    if (t < hd) {
+        float u = 0.0f;
+        u = u + wp[t];
+        u = u + wp[128 + t];
+        u = u + wp[256 + t];
+        u = u + wp[384 + t];
+        Up[(mh * cstride + c) * hd + t] = u;
+    }
+    if (t == 0) {
+        S[mh * s_stride + 2 * c] = mx;
+        S[mh * s_stride + 2 * c + 1] = T;
+    }
+}
+
+// 1-D grid of 8 * M * ceil(G / 8) blocks, G = H * chunks, task group
+// grp = c * H + h.  Blocks are dealt to the 8 XCDs round-robin, so block b
+// runs on XCD b mod 8: group grp's M rows get blocks with b mod 8 = grp mod
+// 8, and after the first row a chunk's K/V rows come from that XCD's L2.
+// 256 threads; head_dim = 16 * PARTS; V rows of VROW bytes in LDS.
+template <int PARTS, uint32_t VROW>
+__global__ __launch_bounds__(256) void k_attn_chunk(const PassDesc* __restrict__ pd, KvGeom g, KvPlanes kv,
+                                                    uint32_t layer, uint32_t M, uint32_t n_groups,
+                                                    const float* __restrict__ q, const float* __restrict__ kself,
+                                                    const float* __restrict__ vself, float* __restrict__ S,
+                                                    uint32_t s_stride, float* __restrict__ Up, uint32_t cstride) {
+    __shared__ __align__(16) uint8_t smem[att_smem(VROW)];
+    const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
+    const uint32_t grp = (slot / M) * 8u + xcd, m = slot % M;
+    if (grp >= n_groups || m >= pd->m) return;
+    attn_one_row<PARTS, VROW>(pd, g, kv, layer, m, grp % g.n_heads, grp / g.n_heads, q, kself, vself, S, s_stride,
+                              Up, cstride, smem);
+}
 
 // ------------------------------------------------- grouped attention
 

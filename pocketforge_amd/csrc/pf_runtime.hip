@@ -507,14 +507,36 @@ static int per_for(uint32_t K) {
 // creation): one block per (head, 256-entry chunk, share of a group of
 // aligned rows), grid (heads * chunks, M); groups of more than 3 rows are
 // split over two or three blocks (two blocks fit on a CU), so that the
-// chip's CUs share the work.  Passes of at most 8 rows quantize and store
+// chip's CUs share the work.  Batched passes of more than 8 rows (many
+// sequences of a few rows) take the per-row kernel.  Passes of at most 8 rows quantize and store
 // their own K/V rows inside the attention kernel (FUSED); taller passes have
 // them stored by k_kv_store_pass first.
 static bool attn_fused(uint32_t M) { return M <= AG_MAX_ROWS; }
 static void launch_attn(hipStream_t st, uint32_t hd, uint32_t M, uint32_t tasks, const PassDesc* pd,
                         const KvGeom& g, const KvPlanes& kv, uint32_t l, const float* q, const float* k,
                         const float* v, float* S, uint32_t s_stride, float* Wp, uint32_t cstride, Prefetch pf,
-                        hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr) {
+                        bool batch, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr) {
+    if (batch && M > AG_MAX_ROWS) {
+        // many sequences of a few rows each: one block per (row, head, chunk),
+        // the M rows of one (head, chunk) on one XCD (blocks b with equal b mod 8)
+        const uint32_t blocks = 8 * M * ((tasks + 7) / 8);
+        if (hd == 64) {
+            if (ev0)
+                hipExtLaunchKernelGGL((k_attn_chunk<4, 136u>), dim3(blocks), dim3(256), 0, st, ev0, ev1, 0, pd, g, kv,
+                                      l, M, tasks, q, k, v, S, s_stride, Wp, cstride);
+            else
+                hipLaunchKernelGGL((k_attn_chunk<4, 136u>), dim3(blocks), dim3(256), 0, st, pd, g, kv, l, M, tasks, q,
+                                   k, v, S, s_stride, Wp, cstride);
+        } else {
+            if (ev0)
+                hipExtLaunchKernelGGL((k_attn_chunk<8, 136u>), dim3(blocks), dim3(256), 0, st, ev0, ev1, 0, pd, g, kv,
+                                      l, M, tasks, q, k, v, S, s_stride, Wp, cstride);
+            else
+                hipLaunchKernelGGL((k_attn_chunk<8, 136u>), dim3(blocks), dim3(256), 0, st, pd, g, kv, l, M, tasks, q,
+                                   k, v, S, s_stride, Wp, cstride);
+        }
+        return;
+    }
     const uint32_t gy = M + (pf.p ? 1u : 0u);   // one more row of blocks prefetches pf
 #define PF_ATTN_LAUNCH(P, F, NR)                                                                              \
     do {                                                                                                      \
@@ -1662,7 +1684,8 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         // attention's extra blocks stream the O weights through the cache
         // hierarchy; other passes run the merge kernel, whose extra blocks do
         launch_attn(st, hd, M, attn_tasks, pd, g, e->kv, l, e->q, e->k, e->v, e->S, e->s_stride, e->Wp,
-                    e->cstride, merge_in_o ? prefetch_of(e, m->o[l]) : Prefetch{nullptr, 0, e->sink}, aev0, aev1);
+                    e->cstride, merge_in_o ? prefetch_of(e, m->o[l]) : Prefetch{nullptr, 0, e->sink}, batch, aev0,
+                    aev1);
         if (!merge_in_o)
             PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_attn_merge_quant<PER>, dim3(M + e->pf_blocks), dim3(1024), 0, st,
                                                     pd, g, (const float*)e->S, e->s_stride, (const float*)e->Wp,
