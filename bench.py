@@ -153,6 +153,35 @@ def copy_probe(nbytes):
     ctx.close()
 
 
+def gemm_probe(M):
+    """The int8 MFMA GEMM alone: pf_gemv_q on M activation rows (rows
+    quantized, then k_gemm) for the four products of one 1B layer (QKV,
+    O, gate|up, down; Q4 weights N(0, 0.02)), 10 launches each, with the
+    host time per call (synchronized) beside it.  The workload of the
+    GEMM's kernel-trace and hardware-counter passes."""
+    import pocketforge_amd as pf
+    from pocketforge_amd import weights as W
+    cfg = W.ONE_B
+    D, F = cfg["n_embd"], cfg["n_ff"]
+    ctx = pf.Context(0)
+    rng = np.random.default_rng(5)
+    out = {"gemm_probe_rows": M, "products": []}
+    for name, (N, K) in (("qkv", (3 * D, D)), ("o", (D, D)), ("gate_up", (2 * F, D)), ("down", (D, F))):
+        codes, scales = pf.gen_matrix(1234, 77, 0.02, N, K, pf.FMT_Q4)
+        Wm = ctx.upload_matrix(pf.FMT_Q4, codes, scales)
+        x = ctx.to_device(rng.normal(0.0, 1.0, (M, K)).astype(np.float32))
+        ctx.gemv_q(Wm, x)
+        t0 = time.perf_counter()
+        for _ in range(10):
+            ctx.gemv_q(Wm, x)
+        us = (time.perf_counter() - t0) / 10 * 1e6
+        out["products"].append({"name": name, "N": N, "K": K, "host_us_per_call": round(us, 1),
+                                "ops": 2 * M * N * K})
+        Wm.close()
+    print(json.dumps(out), flush=True)
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -167,9 +196,14 @@ def main():
                     help="layer-skip threshold (0: off, the default; single-sequence configurations)")
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only run 3 device-to-device copies of this many bytes (hardware-counter calibration)")
+    ap.add_argument("--gemm-probe", type=int, default=0,
+                    help="only run the int8 GEMM on this many rows for the four 1B layer products (counter passes)")
     args = ap.parse_args()
     if args.copy_probe:
         copy_probe(args.copy_probe)
+        return
+    if args.gemm_probe:
+        gemm_probe(args.gemm_probe)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is a design note only "
@@ -431,7 +465,7 @@ def bench_batch(args, C, cfg, w, ctx, dev, model):
         # the step's dominant kernel: verify-pass attention (78% of the decode's
         # kernel time), bound by HBM
         "roofline": {
-            "kernel": f"k_attn_group<8> (verify-pass attention, {M} rows over {N} sequences' int8 K/V)",
+            "kernel": f"k_attn_chunk<8> (verify-pass attention, {M} rows over {N} sequences' int8 K/V)",
             "bound": "hbm",
             "achieved": round(attn_gbps, 1),
             "peak": HBM_PEAK_GBPS,
@@ -445,7 +479,7 @@ def bench_batch(args, C, cfg, w, ctx, dev, model):
                       "(hipExtLaunchKernelGGL) on the engine stream, in one extra step of the same workload",
         },
         "gemm_roofline": {
-            "kernel": f"k_gemm_i8<Q4> (verify-pass int8 x Q4 GEMM, M={M})",
+            "kernel": f"k_gemm<Q4> (verify-pass int8 x Q4 MFMA GEMM, M={M}; average over QKV, O, gate|up, down)",
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": GEMM_PEAK_TOPS,

@@ -12,14 +12,16 @@
 //            SwiGLU of interleaved gate/up rows).
 //  * k_gemm  M > 8 rows (prompt passes, many-sequence verify): the same
 //            exact arithmetic over 32-row activation tiles quantized by the
-//            row kernels, with the same epilogues.
+//            row kernels, with the same epilogues; a workgroup shares each
+//            activation tile among its waves through LDS.
 //
 // Arithmetic: v_mfma_i32_32x32x32_i8 gives the exact int32 dot p of one
 // 32-element block of an activation row and a weight row; the output is
 // y = (float)(a_s * sum_b d_b * p_b) with the sum exact in fp64 (every term is
 // a multiple of the smallest block-scale ulp of the row and the row's scales
 // span at most 15 binades, checked at upload), so any association order
-// gives the same bits.  The activation quantization and RMSNorm follow
+// gives the same bits; k_gemm keeps the same sum as an exact int64 multiple
+// of the row's smallest scale binade.  The activation quantization and RMSNorm follow
 // src/matmul_neon.cpp:16-29 and :231-239 in the canonical orders of
 // pf_gemv.hip.
 #include "pf_device.h"
@@ -555,65 +557,163 @@ struct GemmArgs {
     uint32_t act_stride;
     const float* as;           // [M]
     const uint32_t* gate;
+    const uint8_t* xmin;       // [device rows]: smallest binade of the row's nonzero block scales
     MmEpi e;
 };
 
-// Grid (N / 32, ceil(M / 128)), 256 threads: wave w of workgroup (g, y)
-// computes M tile 4y + w (32 activation rows) against row group g over all
-// of K.  Each lane keeps the 16 outputs of its MFMA tile in fp64.  The next
-// chunk's weight words and activation tiles load while the current chunk
-// runs (every load is issued unconditionally, so the waits are exact).
-template <int FMT, int EPI, bool GATED = false>
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
-    constexpr uint32_t TB = g32_tile_bytes(FMT), CODES = g32_code_bytes(FMT);
-    constexpr int SETS = sets_of<FMT>();
-    if constexpr (GATED)
-        if (*a.gate == 0u) return;
-    const uint32_t lane = threadIdx.x & 63u, r = lane & 31u, h = lane >> 5;
-    const uint32_t mt = blockIdx.y * 4u + (threadIdx.x >> 6);
-    if (mt * 32u >= a.M) return;
-    const uint32_t nch = a.K >> 8;
-    const uint8_t* tiles = a.W + (size_t)blockIdx.x * nch * TB;
-    const int8_t* arow = a.act + (size_t)(mt * 32u + r) * a.act_stride + 16u * h;
-    double S[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++) S[i] = 0.0;
+// Integer form of a block scale for exact int64 sums: the fp16 scale d
+// (low 16 bits of h) is M * 2^(X - 25) with M = significand (hidden bit
+// included, 0 for zero) and X = max(biased exponent, 1); relative to the
+// row's smallest binade xmin (nonzero scales only, so X >= xmin whenever
+// M != 0) d = c * 2^(xmin - 25) with c = M << (X - xmin) < 2^26 (the
+// upload keeps nonzero scales of a row within 15 binades).
+__device__ __forceinline__ int32_t scale_multiplier(uint32_t h, uint32_t xmin) {
+    const uint32_t e = (h >> 10) & 31u, mt = h & 1023u;
+    const uint32_t mag = (e ? (mt | 1024u) : mt) << (((e ? e : 1u) - xmin) & 31u);
+    return (h & 0x8000u) ? -(int32_t)mag : (int32_t)mag;
+}
+
+// One 256-column chunk of one wave's 32 x 32 output tile: eight blocks'
+// exact int32 dots (MFMA) times the blocks' integer scale multipliers into
+// int64 sums (|c p| < 2^41, so the sums of up to 8192 columns stay exact).
+// The MFMAs of DI blocks are issued before their products are added, so
+// the matrix core works while the adds of earlier blocks run.
+template <int FMT, int DI>
+__device__ __forceinline__ void gemm_chunk(int64_t (&S)[16], const uint8_t* arow, const uint4 (&cw)[sets_of<FMT>()],
+                                           const uint4& sw, uint32_t xmin) {
     const pf_v16i zero = {};
-    uint4 cwn[SETS], swn;
-    pf_v4i an[8];
-    auto load = [&](uint32_t c) {
-        const uint8_t* tile = tiles + (size_t)c * TB;
+    pf_v4i A[8];
 #pragma unroll
-        for (int s = 0; s < SETS; s++) cwn[s] = *reinterpret_cast<const uint4*>(tile + s * 1024 + lane * 16);
-        swn = *reinterpret_cast<const uint4*>(tile + CODES + r * 16);
+    for (uint32_t u = 0; u < 8; u++) A[u] = *reinterpret_cast<const pf_v4i*>(arow + 32u * u);
+    const uint32_t sx[4] = {sw.x, sw.y, sw.z, sw.w};
 #pragma unroll
-        for (int t = 0; t < 8; t++) an[t] = *reinterpret_cast<const pf_v4i*>(arow + 256u * c + 32u * t);
-    };
-    load(0);
-    for (uint32_t c = 0; c < nch; c++) {
-        uint4 cw[SETS], sw = swn;
-        pf_v4i A[8];
+    for (uint32_t u0 = 0; u0 < 8; u0 += DI) {
+        pf_v16i D[DI];
 #pragma unroll
-        for (int s = 0; s < SETS; s++) cw[s] = cwn[s];
+        for (uint32_t j = 0; j < (uint32_t)DI; j++)
+            D[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[u0 + j], b_operand<FMT>(cw, u0 + j), zero, 0, 0, 0);
 #pragma unroll
-        for (int t = 0; t < 8; t++) A[t] = an[t];
-        load(c + 1 < nch ? c + 1 : c);
-        const uint16_t* sc = reinterpret_cast<const uint16_t*>(&sw);
+        for (uint32_t j = 0; j < (uint32_t)DI; j++) {
+            const uint32_t u = u0 + j;
+            const int32_t c = scale_multiplier(sx[u >> 1] >> (16u * (u & 1u)), xmin);
 #pragma unroll
-        for (uint32_t t = 0; t < 8; t++) {
-            const pf_v16i D = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[t], b_operand<FMT>(cw, t), zero, 0, 0, 0);
-            const double d = (double)h2f(sc[t]);
-#pragma unroll
-            for (int i = 0; i < 16; i++) S[i] = __builtin_fma(d, (double)D[i], S[i]);
+            for (int i = 0; i < 16; i++) S[i] += (int64_t)c * (int64_t)D[j][i];
         }
     }
+}
+
+// Grid (ceil(N / 32 / NW), ceil(M / 32 / MW)), 512 threads: 8 waves, wave
+// w takes M tile mw = w % MW (32 activation rows),
+// weight group nw = (w / MW) % NW of the workgroup's NW groups, and K slice
+// kw = w / (MW NW) (chunks c with c % KW == kw).  Step s covers chunks
+// KW s .. KW s + KW - 1: the workgroup copies their activation tiles
+// (32 MW rows x 256 B each) once into LDS (double buffer, rows padded to
+// 272 B) and every wave reads its rows from there, so a tile is fetched
+// once per workgroup instead of once per wave; one barrier per step.  Loads
+// run one step ahead (clamped, issued unconditionally), the weights into
+// two register sets used on alternate steps, so that no copy waits for
+// them.
+// K slices meet in LDS (exact int64 sums).  Two waves per SIMD (up to 256
+// VGPRs per lane): a 128-register budget spills.  Each lane keeps the 16
+// outputs of its MFMA tile as int64 multiples of its row's 2^(xmin - 25);
+// the epilogue converts them to fp64 exactly (|sum| < 2^53) and applies
+// y = (float)(sum * 2^(xmin - 25) * a_s), the value of the fp64 block sum.
+template <int MW, int KW>
+constexpr uint32_t gemm_smem() { return 2u * KW * 32u * MW * 272u; }
+
+template <int FMT, int EPI, bool GATED, int MW, int NW, int KW, int DI>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm(GemmArgs a) {
+    static_assert(MW * NW * KW == 8, "eight waves");
+    constexpr uint32_t TB = g32_tile_bytes(FMT), CODES = g32_code_bytes(FMT);
+    constexpr int SETS = sets_of<FMT>();
+    constexpr uint32_t ROWS = 32u * MW, AROW = 272u, STEP = KW * ROWS * AROW;
+    constexpr uint32_t APT = KW * MW;                  // 16-byte activation pieces per thread and step
+    static_assert((KW > 1 ? (KW - 1) * MW * NW * 64 * 16 * 8 : 0) <= 2 * STEP, "slice partials fit the buffers");
+    __shared__ __align__(16) uint8_t smem[2 * STEP];
+    if constexpr (GATED)
+        if (*a.gate == 0u) return;
+    const uint32_t t = threadIdx.x, lane = t & 63u, r = lane & 31u, h = lane >> 5;
+    const uint32_t wid = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t mw = wid % MW, nw = (wid / MW) % NW, kw = wid / (MW * NW);
+    const uint32_t m0 = blockIdx.y * ROWS, ng = a.N >> 5, g = blockIdx.x * NW + nw, gc = min(g, ng - 1u);
+    const uint32_t nch = a.K >> 8, nsteps = (nch + KW - 1) / KW, mlast = a.M - 1u;
+    const uint8_t* tiles = a.W + (size_t)gc * nch * TB;
+    // piece u of thread t: row (t >> 4) + 32 (u % MW) of the tile, 16 bytes
+    // at 16 (t & 15) of chunk KW s + u / MW
+    const int8_t* abase[MW];
+#pragma unroll
+    for (uint32_t u = 0; u < (uint32_t)MW; u++)
+        abase[u] = a.act + (size_t)min(m0 + (t >> 4) + 32u * u, mlast) * a.act_stride + 16u * (t & 15u);
+    const uint32_t sbase = (t >> 4) * AROW + 16u * (t & 15u);
+    pf_v4i av[APT];
+#pragma unroll
+    for (uint32_t u = 0; u < APT; u++)
+        av[u] = *reinterpret_cast<const pf_v4i*>(abase[u % MW] + 256u * min(u / MW, nch - 1u));
+    uint4 cw0[SETS], cw1[SETS], sw0, sw1;
+    {
+        const uint8_t* tile = tiles + (size_t)min(kw, nch - 1u) * TB;
+#pragma unroll
+        for (int q = 0; q < SETS; q++) cw0[q] = *reinterpret_cast<const uint4*>(tile + q * 1024 + lane * 16);
+        sw0 = *reinterpret_cast<const uint4*>(tile + CODES + r * 16);
+    }
+    int64_t S[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) S[i] = 0;
+    const uint32_t xmin = a.xmin[32u * gc + r];
+    const uint32_t aoff = (kw * ROWS + 32u * mw + r) * AROW + 16u * h;
+    for (uint32_t st = 0; st < nsteps; st += 2) {
+#pragma unroll
+        for (uint32_t ph = 0; ph < 2; ph++) {
+            const uint32_t s = st + ph;
+            if (ph == 1 && s >= nsteps) break;
+            uint8_t* buf = smem + ph * STEP;
+#pragma unroll
+            for (uint32_t u = 0; u < APT; u++)
+                *reinterpret_cast<pf_v4i*>(buf + (u / MW) * ROWS * AROW + 32u * (u % MW) * AROW + sbase) = av[u];
+            __syncthreads();
+            const uint32_t nx = s + 1u < nsteps ? s + 1u : s;
+            const uint8_t* tile = tiles + (size_t)min(KW * nx + kw, nch - 1u) * TB;
+            // two register sets: step s uses set s & 1, the loads fill the other
+#pragma unroll
+            for (int q = 0; q < SETS; q++) {
+                const uint4 w = *reinterpret_cast<const uint4*>(tile + q * 1024 + lane * 16);
+                if (ph == 0) cw1[q] = w; else cw0[q] = w;
+            }
+            const uint4 w = *reinterpret_cast<const uint4*>(tile + CODES + r * 16);
+            if (ph == 0) sw1 = w; else sw0 = w;
+#pragma unroll
+            for (uint32_t u = 0; u < APT; u++)
+                av[u] = *reinterpret_cast<const pf_v4i*>(abase[u % MW] + 256u * min(KW * nx + u / MW, nch - 1u));
+            if (KW * s + kw < nch) {
+                if (ph == 0) gemm_chunk<FMT, DI>(S, buf + aoff, cw0, sw0, xmin);
+                else gemm_chunk<FMT, DI>(S, buf + aoff, cw1, sw1, xmin);
+            }
+        }
+    }
+    if constexpr (KW > 1) {
+        int64_t* red = reinterpret_cast<int64_t*>(smem);   // [KW - 1][MW NW][16][64]: lanes on consecutive banks
+        __syncthreads();
+        if (kw > 0) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) red[(((kw - 1u) * MW * NW + mw + MW * nw) * 16u + i) * 64u + lane] = S[i];
+        }
+        __syncthreads();
+        if (kw == 0) {
+#pragma unroll
+            for (uint32_t k = 1; k < (uint32_t)KW; k++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) S[i] += red[(((k - 1u) * MW * NW + mw + MW * nw) * 16u + i) * 64u + lane];
+        }
+    }
+    if (kw != 0u || g >= ng) return;   // whole waves
     // output i of lane (r, h): activation row 8 (i / 4) + 4 h + i % 4 of the
-    // tile, device row r of the group
-    const uint32_t n = 32u * blockIdx.x + r;
+    // wave's M tile, device row r of group g
+    const uint32_t n = 32u * g + r;
+    const double unit = __builtin_ldexp(1.0, (int)xmin - 25);
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-        const uint32_t m = mt * 32u + 8u * (i / 4) + 4u * h + (i % 4);
-        const float y = m < a.M ? (float)(S[i] * (double)a.as[m]) : 0.0f;
+        const uint32_t m = m0 + 32u * mw + 8u * (i / 4) + 4u * h + (i % 4);
+        const float y = m < a.M ? (float)(((double)S[i] * unit) * (double)a.as[m]) : 0.0f;
         const float y1 = __shfl_xor(y, 1, 64), y16 = __shfl_xor(y, 16, 64);
         if (m < a.M) {
             const EpiPre pre = epi_prefetch<EPI>(a.e, m, n);

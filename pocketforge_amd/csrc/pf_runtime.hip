@@ -199,8 +199,22 @@ struct pf_matrix {
     bool ilv = false;           // halves [0, rows/2) and [rows/2, rows) interleaved by 16 rows
     uint8_t* data = nullptr;    // 32-row group tiles; row-major: codes
     uint16_t* scales = nullptr; // row-major only
+    uint8_t* xmin = nullptr;    // tiled only: per device row, smallest binade of its nonzero block scales
+    std::vector<uint8_t> xmin_host;
     size_t bytes = 0;
 };
+
+// Smallest binade max(biased exponent, 1) of a row's nonzero fp16 block
+// scales (1 for a row of zero scales): the unit of the GEMM's integer sums.
+static uint8_t row_xmin(const uint16_t* sc, uint32_t nb) {
+    int xm = 31;
+    for (uint32_t b = 0; b < nb; b++) {
+        if ((sc[b] & 0x7FFF) == 0) continue;
+        const int e = (sc[b] >> 10) & 31;
+        xm = std::min(xm, e ? e : 1);
+    }
+    return (uint8_t)(xm == 31 ? 1 : xm);
+}
 
 static uint32_t interchange_code(int fmt, const uint8_t* blk, uint32_t e) {
     if (fmt == FMT_Q4) return (e & 1u) ? (blk[e >> 1] >> 4) : (blk[e >> 1] & 15u);
@@ -289,7 +303,13 @@ static pf_status matrix_alloc(pf_ctx* c, int32_t fmt, uint32_t rows, uint32_t co
     } else {
         M->bytes = (size_t)(rows / 32) * (cols / 256) * g32_tile_bytes(fmt);
         pf_status s = dalloc_t(c, &M->data, M->bytes);
-        if (s) { delete M; return s; }
+        if (!s) s = dalloc_t(c, &M->xmin, rows);
+        if (s) {
+            if (M->data) dfree(c, M->data, M->bytes);
+            delete M;
+            return s;
+        }
+        M->xmin_host.assign(rows, 1);
     }
     *out = M;
     return PF_OK;
@@ -326,8 +346,10 @@ static pf_status matrix_put(pf_matrix* M, uint32_t r0, uint32_t n, const uint8_t
         const uint32_t dr = device_row(M, r);
         pack_row(M->fmt, M->cols, codes + (size_t)(r - r0) * nb * bb, scales + (size_t)(r - r0) * nb, dr % 32,
                  buf.data() + (size_t)(dr / 32 - g_lo) * gbytes);
+        M->xmin_host[dr] = row_xmin(scales + (size_t)(r - r0) * nb, nb);
     }
     PF_HIP(c, hipMemcpy(M->data + g_lo * gbytes, buf.data(), buf.size(), hipMemcpyHostToDevice));
+    PF_HIP(c, hipMemcpy(M->xmin, M->xmin_host.data(), M->rows, hipMemcpyHostToDevice));
     return PF_OK;
 }
 
@@ -347,6 +369,7 @@ extern "C" void pf_matrix_free(pf_matrix* M) {
     if (!M) return;
     dfree(M->ctx, M->data, M->bytes);
     if (M->scales) dfree(M->ctx, M->scales, (size_t)M->rows * (M->cols / 32) * 2);
+    if (M->xmin) dfree(M->ctx, M->xmin, M->rows);
     delete M;
 }
 
@@ -400,11 +423,22 @@ static void gemv_cpw(hipStream_t st, const GemvArgs& a, hipEvent_t ev0, hipEvent
     else gemv_mr<F, PRO, EPI, G, 4>(st, a, ev0, ev1);
 }
 
+template <int F, int EPI, bool G, int MW, int NW, int KW, int DI>
+static void gemm_tiled(hipStream_t st, const GemmArgs& a, hipEvent_t ev0, hipEvent_t ev1) {
+    const dim3 grid((a.N / 32 + NW - 1) / NW, (a.M + 32 * MW - 1) / (32 * MW));
+    if (ev0) hipExtLaunchKernelGGL((k_gemm<F, EPI, G, MW, NW, KW, DI>), grid, dim3(512), 0, st, ev0, ev1, 0, a);
+    else hipLaunchKernelGGL((k_gemm<F, EPI, G, MW, NW, KW, DI>), grid, dim3(512), 0, st, a);
+}
+
+// Workgroup shapes measured at M = 320 on the 1B products: matrices of at
+// least 4096 rows take 32 activation rows x 8 row groups per workgroup;
+// narrower ones split K over two wave sets (32 x 4 x 2) so that the chip
+// still gets enough workgroups.  Every wave issues its chunk's 8 MFMAs
+// before their integer scaling.
 template <int F, int EPI, bool G>
 static void gemm_one(hipStream_t st, const GemmArgs& a, hipEvent_t ev0, hipEvent_t ev1) {
-    const dim3 grid(a.N / 32, (a.M + 127) / 128);
-    if (ev0) hipExtLaunchKernelGGL((k_gemm<F, EPI, G>), grid, dim3(256), 0, st, ev0, ev1, 0, a);
-    else hipLaunchKernelGGL((k_gemm<F, EPI, G>), grid, dim3(256), 0, st, a);
+    if (a.N >= 4096) gemm_tiled<F, EPI, G, 1, 8, 1, 8>(st, a, ev0, ev1);
+    else gemm_tiled<F, EPI, G, 1, 4, 2, 8>(st, a, ev0, ev1);
 }
 
 #define PF_MM_FMT(fmt, CALL)                                  \
@@ -439,8 +473,9 @@ static void launch_gemv(hipStream_t st, const pf_matrix* W, MmKind kind, const G
 }
 
 // M > 8 rows: activation rows quantized beforehand (int8 + scales).
-static void launch_gemm(hipStream_t st, const pf_matrix* W, MmKind kind, const GemmArgs& a, hipEvent_t ev0 = nullptr,
+static void launch_gemm(hipStream_t st, const pf_matrix* W, MmKind kind, GemmArgs a, hipEvent_t ev0 = nullptr,
                         hipEvent_t ev1 = nullptr) {
+    a.xmin = W->xmin;
     switch (kind) {
         case MM_QKV: PF_MM_FMT(W->fmt, (gemm_one<F, EPI_QKV, false>(st, a, ev0, ev1))) break;
         case MM_O:
