@@ -314,7 +314,7 @@ def main():
                 "ffn_blocks_skipped_last_step": eng.layer_skip_count()} if args.layer_skip else {}),
         },
         "roofline": {
-            "kernel": "k_gemv_i8<fmt,M=5> (verify-pass int8 x block-quantized GEMV)",
+            "kernel": "k_gemv<fmt,...> (verify-pass int8 x block-quantized GEMV: QKV, merge + O, gate|up, down)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,

@@ -175,6 +175,8 @@ typedef struct {
     uint32_t n_layers, n_embd, n_heads, head_dim, n_ff, n_vocab, n_mtp;
 } pf_model_desc;  /* ModelConfig subset, include/forge/types.hpp:220-254 (MHA) */
 
+/* n_vocab <= 16384 (the on-chip sampler's limit): larger vocabularies,
+ * such as ModelConfig's default 130560, return PF_ERR_UNSUPPORTED. */
 pf_status pf_model_create(pf_ctx* ctx, const pf_model_desc* desc, pf_model** out);
 void pf_model_destroy(pf_model* m);
 /* Layer matrix `id` (PF_MAT_*), interchange layout.  Q/K/V must share a
@@ -298,7 +300,8 @@ pf_status pf_engine_set_max_memory(pf_engine* e, size_t bytes);
  * types.hpp): LayerSkipController (src/layer_skip.cpp:22-67) on the FFN
  * input of every layer of every pass.  On while threshold > 0 (default off;
  * the reference's ModelConfig default is 0.01); switching it on starts from
- * zeroed caches.  Passes run kernel-per-step while it is on. */
+ * zeroed caches.  While it is on, every MTP round verifies all drafts in
+ * one (n_mtp + 1)-row pass. */
 pf_status pf_engine_set_layer_skip(pf_engine* e, float threshold, uint32_t interval);
 /* FFN blocks skipped since creation or pf_engine_reset (the reference's
  * GenerationResult::layers_skipped reads a counter that is never
