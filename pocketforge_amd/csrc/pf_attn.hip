@@ -293,7 +293,7 @@ constexpr uint32_t att_vt(uint32_t vrow) { return 256 * vrow; }
 constexpr uint32_t att_smem(uint32_t vrow) { return att_vt(vrow) + (128 + 128 + 256 + 256 + 512 + 4) * 4; }
 
 template <int PARTS, uint32_t VROW = 144>
-__device__ __forceinline__ void attn_one_row(const PassDesc* __restrict__ pd, const KvGeom& g, const KvPlanes& kv,
+__device__ __forceinline__ void attn_one_row(const PassHead& pd, const KvGeom& g, const KvPlanes& kv,
                                              uint32_t layer, uint32_t m, uint32_t h, uint32_t c,
                                              const float* __restrict__ q, const float* __restrict__ kself,
                                              const float* __restrict__ vself, float* __restrict__ S,
@@ -432,8 +432,9 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const PassDesc* __restrict__
     __shared__ __align__(16) uint8_t smem[att_smem(VROW)];
     const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
     const uint32_t grp = (slot / M) * 8u + xcd, m = slot % M;
-    if (grp >= n_groups || m >= pd->m) return;
-    attn_one_row<PARTS, VROW>(pd, g, kv, layer, m, grp % g.n_heads, grp / g.n_heads, q, kself, vself, S, s_stride,
+    const PassHead ph = pass_head(pd);
+    if (grp >= n_groups || m >= ph.m) return;
+    attn_one_row<PARTS, VROW>(ph, g, kv, layer, m, grp % g.n_heads, grp / g.n_heads, q, kself, vself, S, s_stride,
                               Up, cstride, smem);
 }
 
@@ -443,7 +444,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const PassDesc* __restrict__
 // entries plus one more, the store of a's position (same sink and pooled
 // counts, same oldest window entry).  Chunk c then holds the same entries
 // for both, so one block serves both rows.
-__device__ __forceinline__ bool rows_aligned(const KvGeom& g, const PassDesc* pd, uint32_t a, uint32_t b) {
+__device__ __forceinline__ bool rows_aligned(const KvGeom& g, const PassHead& pd, uint32_t a, uint32_t b) {
     if (row_seq(pd, a) != row_seq(pd, b)) return false;
     const uint32_t pa = row_pos(pd, a), pb = row_pos(pd, b);
     if (pb != pa + 1u) return false;
@@ -543,12 +544,13 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
 
     const uint32_t H = g.n_heads, h = blockIdx.x % H, c = blockIdx.x / H, m0 = blockIdx.y;
     const uint32_t t = threadIdx.x, lane = t & 63u, wid = t >> 6;
-    const uint32_t Mp = min(M, pd->m);
+    const PassHead ph = pass_head(pd);
+    const uint32_t Mp = min(M, ph.m);
     if (m0 >= Mp) return;
     // lane l < 8: row base + l starts a group (not aligned with row base + l - 1)
     const uint32_t base = m0 & ~7u;
     bool st = true;
-    if (lane >= 1u && lane < 8u && base + lane < Mp) st = !rows_aligned(g, pd, base + lane - 1u, base + lane);
+    if (lane >= 1u && lane < 8u && base + lane < Mp) st = !rows_aligned(g, ph, base + lane - 1u, base + lane);
     const uint32_t starts = (uint32_t)__ballot(st) & 0xFFu;
     const uint32_t k = m0 - base;                                   // this block's row in the slice
     const uint32_t lead = 31u - (uint32_t)__builtin_clz(starts & ((2u << k) - 1u));
@@ -559,10 +561,10 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
     const uint32_t per = (glen + nsh - 1u) / nsh;
     const uint32_t mb = base + lead + share * per;                  // first row of this block
     const uint32_t G = min(per, glen - share * per);
-    const KvView vL = kv_view(g, row_pos(pd, mb + G - 1u));         // the longest list
+    const KvView vL = kv_view(g, row_pos(ph, mb + G - 1u));         // the longest list
     const uint32_t CL = vL.count(), C0 = CL - (G - 1u), j0 = 256u * c;
     if (j0 > CL) return;                                            // past the last row's self entry
-    const uint32_t D = H * hd, seq = row_seq(pd, mb);
+    const uint32_t D = H * hd, seq = row_seq(ph, mb);
     const size_t plane = plane_index(g, seq, layer, h);
     const uint32_t nvis = j0 < CL ? min(256u, CL - j0) : 0u;
     const uint32_t wstart = max(j0, vL.sink + vL.pool), wb = (vL.win_lo + (wstart - vL.sink - vL.pool)) % g.ring;
@@ -570,8 +572,8 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
     // or later are the pass's own rows
     uint32_t first = mb, p_first = 0xFFFFFFFFu;
     if constexpr (FUSED) {
-        while (first > 0 && row_seq(pd, first - 1u) == seq) first--;
-        p_first = row_pos(pd, first);
+        while (first > 0 && row_seq(ph, first - 1u) == seq) first--;
+        p_first = row_pos(ph, first);
     }
 
     // ---- loads, all issued before any is used
@@ -773,27 +775,29 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
         // entries [64 sub, min(64 sub + 64, nvis)) in groups of 4; entries
         // past nvis up to the next multiple of 8 have v_scale 0 and finite
         // codes, and entries past a row's list have weight 0
-        const uint32_t e_end = min(64u * sub + 64u, (nvis + 7u) & ~7u);
-        for (uint32_t e = 64u * sub; e < e_end; e += 4) {
-            float a0[4], a1[4];
+        const uint32_t e_end = min(64u * sub + 64u, (nvis + 7u) & ~7u);   // both multiples of 8
+#pragma unroll 2
+        for (uint32_t e = 64u * sub; e < e_end; e += 8) {
+            float a0[8], a1[8];
+            const float4 s0 = *reinterpret_cast<const float4*>(&vsc[e]);
+            const float4 s1 = *reinterpret_cast<const float4*>(&vsc[e + 4]);
+            const float vv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
+            for (int u = 0; u < 8; u++) {
                 const uint32_t cc = *reinterpret_cast<const uint16_t*>(&vt[e + u][i0]);
-                const float vv = vsc[e + u];
-                a0[u] = (float)(int8_t)(cc & 0xFFu) * vv;
-                a1[u] = (float)(int8_t)(cc >> 8) * vv;
+                a0[u] = (float)(int8_t)(cc & 0xFFu) * vv[u];
+                a1[u] = (float)(int8_t)(cc >> 8) * vv[u];
             }
 #pragma unroll
             for (int r = 0; r < NR; r++) {
-                const float4 pp = *reinterpret_cast<const float4*>(&pe[r * 256 + e]);
-                w0[r] = __builtin_fmaf(pp.x, a0[0], w0[r]);
-                w1[r] = __builtin_fmaf(pp.x, a1[0], w1[r]);
-                w0[r] = __builtin_fmaf(pp.y, a0[1], w0[r]);
-                w1[r] = __builtin_fmaf(pp.y, a1[1], w1[r]);
-                w0[r] = __builtin_fmaf(pp.z, a0[2], w0[r]);
-                w1[r] = __builtin_fmaf(pp.z, a1[2], w1[r]);
-                w0[r] = __builtin_fmaf(pp.w, a0[3], w0[r]);
-                w1[r] = __builtin_fmaf(pp.w, a1[3], w1[r]);
+                const float4 p0 = *reinterpret_cast<const float4*>(&pe[r * 256 + e]);
+                const float4 p1 = *reinterpret_cast<const float4*>(&pe[r * 256 + e + 4]);
+                const float pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    w0[r] = __builtin_fmaf(pp[u], a0[u], w0[r]);
+                    w1[r] = __builtin_fmaf(pp[u], a1[u], w1[r]);
+                }
             }
         }
 #pragma unroll

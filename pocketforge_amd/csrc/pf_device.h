@@ -203,6 +203,25 @@ __device__ __forceinline__ uint32_t row_seq(const PassDesc* pd, uint32_t m) {
     return pd->batch ? pd->rseq[m] : pd->seq0;
 }
 
+// The descriptor's first four words (pos0, m, batch, seq0) read with one
+// 16-byte load at a kernel's start, so that the positions and sequences of
+// a single-sequence pass's rows need no further memory round trip (each
+// dependent descriptor read costs one on the kernel's critical path).
+struct PassHead {
+    uint32_t pos0, m, batch, seq0;
+    const PassDesc* pd;
+};
+__device__ __forceinline__ PassHead pass_head(const PassDesc* pd) {
+    const uint4 w = *reinterpret_cast<const uint4*>(pd);
+    return PassHead{w.x, w.y, w.z, w.w, pd};
+}
+__device__ __forceinline__ uint32_t row_pos(const PassHead& p, uint32_t m) {
+    return p.batch ? p.pd->rpos[m] : p.pos0 + m;
+}
+__device__ __forceinline__ uint32_t row_seq(const PassHead& p, uint32_t m) {
+    return p.batch ? p.pd->rseq[m] : p.seq0;
+}
+
 // Row index (within one (layer, head) plane) of visible entry j.
 __device__ __forceinline__ uint32_t kv_row(const KvGeom& g, const KvView& v, uint32_t j) {
     if (j < v.sink) return j;

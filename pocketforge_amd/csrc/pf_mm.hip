@@ -267,7 +267,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void k_gemv(GemvArgs a) {
     const float* upc = nullptr;               // this thread's columns in chunk 0
     if constexpr (PRO == PRO_MERGE) {
         static_assert(MR == 1, "the merge prologue serves one row");
-        nc = (kv_view(a.g, row_pos(a.e.pd, 0)).count() + 1u + 255u) / 256u;
+        nc = (kv_view(a.g, row_pos(pass_head(a.e.pd), 0)).count() + 1u + 255u) / 256u;
         hn = a.g.n_heads * nc;
         hs = (uint32_t)__builtin_ctz(a.e.hd);
         const float rnc = 1.0f / (float)nc;
