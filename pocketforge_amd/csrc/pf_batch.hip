@@ -124,9 +124,7 @@ static pf_status batch_mtp_chain(pf_engine* e, const float* h0, uint32_t n, cons
     const uint32_t D = d.n_embd, V = d.n_vocab, R = d.n_mtp + 1, nd = n * D;
     hipLaunchKernelGGL(k_copy_f32, dim3((nd + 255) / 256), dim3(256), 0, st, h0, e->mcur, nd);
     for (uint32_t k = 0; k < d.n_mtp; k++) {
-        launch_gemv_f32(st, m->mtp[k * 3 + 0], n, e->mcur, D, e->mg, D, nullptr);
-        launch_gemv_f32(st, m->mtp[k * 3 + 1], n, e->mcur, D, e->mu, D, nullptr);
-        hipLaunchKernelGGL(k_silu_mul, dim3((nd + 255) / 256), dim3(256), 0, st, e->mg, e->mu, e->ma, nd);
+        launch_gemv_f32_glu(st, m->mtp[k * 3 + 0], m->mtp[k * 3 + 1], n, e->mcur, D, e->ma, D);
         launch_gemv_f32(st, m->mtp[k * 3 + 2], n, e->ma, D, e->mcur, D, e->mcur);
         launch_gemv_f32(st, m->emb, n, e->mcur, D, e->mlogb, V, nullptr);
         hipLaunchKernelGGL(k_bsample, dim3(n), dim3(1024), 0, st, (const float*)e->mlogb, V, V, cfg,

@@ -1,7 +1,9 @@
 // fp32-activation GEMV and the row kernels of the gfx950 path.
 //
 //  * k_gemv_f32    fp32 activations x dequantized Q4 row-major matrix (tied
-//                  unembedding, MTP heads) in the canonical 64-lane order.
+//                  unembedding, MTP heads) in the canonical 64-lane order;
+//                  k_gemv_f32_glu: a head's gate and up products and their
+//                  SiLU product in one launch.
 //  * row kernels   quantize_activation_row of whole rows, layer-skip
 //                  decisions and cache commits, embedding, small copies.
 //  * k_matmul_int8 / k_mm_epilogue: the reference's plain int8 matmul API.
@@ -65,6 +67,68 @@ __global__ __launch_bounds__(256) void k_gemv_f32(const uint8_t* __restrict__ co
             if (lane == 0) {
                 size_t o = (size_t)m * y_stride + n;
                 y[o] = y_in ? (y_in[o] + t) : t;
+            }
+        }
+    }
+}
+
+// One MTP head's gate and up products with the SiLU product fused
+// (src/mtp.cpp:63-127): a[m][n] = silu(g) * u, g and u the canonical dots
+// of h[m] with row n of Wg and Wu (k_gemv_f32's order), silu(g) =
+// g / (1 + exp(-g)) as k_silu_mul computes it, so a equals the three
+// separate launches bit for bit.
+template <int M>
+__global__ __launch_bounds__(256) void k_gemv_f32_glu(const uint8_t* __restrict__ gcodes,
+                                                      const uint16_t* __restrict__ gscales,
+                                                      const uint8_t* __restrict__ ucodes,
+                                                      const uint16_t* __restrict__ uscales, uint32_t N, uint32_t K,
+                                                      const float* __restrict__ h, uint32_t h_stride,
+                                                      float* __restrict__ a, uint32_t a_stride) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
+    const uint32_t nb = K >> 5;
+    const bool live = lane < nb;
+    float hv[M][32];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+            float4 v = live ? *reinterpret_cast<const float4*>(h + (size_t)m * h_stride + lane * 32u + i)
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+            hv[m][i] = v.x; hv[m][i + 1] = v.y; hv[m][i + 2] = v.z; hv[m][i + 3] = v.w;
+        }
+    }
+    for (uint32_t n = wave; n < N; n += nwaves) {
+        float ag[M], au[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) ag[m] = au[m] = 0.0f;
+        if (live) {
+            const uint4 cg = *reinterpret_cast<const uint4*>(gcodes + ((size_t)n * nb + lane) * 16u);
+            const uint4 cu = *reinterpret_cast<const uint4*>(ucodes + ((size_t)n * nb + lane) * 16u);
+            const float dg = h2f(gscales[(size_t)n * nb + lane]), du = h2f(uscales[(size_t)n * nb + lane]);
+            const float ndg = -8.0f * dg, ndu = -8.0f * du;
+            const uint32_t gw[4] = {cg.x, cg.y, cg.z, cg.w}, uw[4] = {cu.x, cu.y, cu.z, cu.w};
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const uint32_t bg = (gw[j >> 2] >> (8 * (j & 3))) & 0xFFu, bu = (uw[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+                const float g0 = __builtin_fmaf((float)(bg & 15u), dg, ndg), g1 = __builtin_fmaf((float)(bg >> 4), dg, ndg);
+                const float u0 = __builtin_fmaf((float)(bu & 15u), du, ndu), u1 = __builtin_fmaf((float)(bu >> 4), du, ndu);
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+                    ag[m] = __builtin_fmaf(hv[m][2 * j], g0, ag[m]);
+                    ag[m] = __builtin_fmaf(hv[m][2 * j + 1], g1, ag[m]);
+                    au[m] = __builtin_fmaf(hv[m][2 * j], u0, au[m]);
+                    au[m] = __builtin_fmaf(hv[m][2 * j + 1], u1, au[m]);
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const float g = wave_tree_sum(ag[m]), u = wave_tree_sum(au[m]);
+            if (lane == 0) {
+                const float sg = g / (1.0f + expf_c(-g));
+                a[(size_t)m * a_stride + n] = sg * u;
             }
         }
     }

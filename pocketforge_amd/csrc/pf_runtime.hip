@@ -514,6 +514,29 @@ static void launch_gemv_f32(hipStream_t st, const pf_matrix* W, uint32_t M, cons
     }
 }
 
+// Gate and up products of one MTP head with the SiLU product fused:
+// a[m] = silu(Wg h[m]) * (Wu h[m]), rows in chunks of 8.
+static void launch_gemv_f32_glu(hipStream_t st, const pf_matrix* Wg, const pf_matrix* Wu, uint32_t M, const float* h,
+                                uint32_t h_stride, float* a, uint32_t a_stride) {
+    uint32_t waves = std::min<uint32_t>(Wg->rows, 2048);
+    dim3 grid((waves + 3) / 4);
+    for (uint32_t r0 = 0; r0 < M; r0 += 8) {
+        const uint32_t mb = std::min(8u, M - r0);
+        const float* hr = h + (size_t)r0 * h_stride;
+        float* ar = a + (size_t)r0 * a_stride;
+#define PF_GLU_CASE(MM)                                                                                          \
+    case MM:                                                                                                     \
+        hipLaunchKernelGGL(k_gemv_f32_glu<MM>, grid, dim3(256), 0, st, Wg->data, Wg->scales, Wu->data, Wu->scales, \
+                           Wg->rows, Wg->cols, hr, h_stride, ar, a_stride);                                      \
+        break;
+        switch (mb) {
+            PF_GLU_CASE(1) PF_GLU_CASE(2) PF_GLU_CASE(3) PF_GLU_CASE(4)
+            PF_GLU_CASE(5) PF_GLU_CASE(6) PF_GLU_CASE(7) PF_GLU_CASE(8)
+        }
+#undef PF_GLU_CASE
+    }
+}
+
 static int per_for(uint32_t K) {
     uint32_t per = (K + 255) / 256;
     for (int p : {4, 8, 12, 16, 24, 32})
@@ -825,9 +848,7 @@ extern "C" pf_status pf_mtp_heads_forward(pf_mtp* m, const float* hidden, float*
     const uint32_t D = m->D, V = m->V;
     PF_HIP(c, hipMemcpyAsync(m->cur, hidden, (size_t)D * 4, hipMemcpyHostToDevice, st));
     for (uint32_t k = 0; k < m->H; k++) {            // src/mtp.cpp:63-127
-        launch_gemv_f32(st, m->mats[k * 3 + 0], 1, m->cur, D, m->g, D, nullptr);
-        launch_gemv_f32(st, m->mats[k * 3 + 1], 1, m->cur, D, m->u, D, nullptr);
-        hipLaunchKernelGGL(k_silu_mul, dim3((D + 255) / 256), dim3(256), 0, st, m->g, m->u, m->a, D);
+        launch_gemv_f32_glu(st, m->mats[k * 3 + 0], m->mats[k * 3 + 1], 1, m->cur, D, m->a, D);
         launch_gemv_f32(st, m->mats[k * 3 + 2], 1, m->a, D, m->cur, D, m->cur);
         float* lk = m->logits + (size_t)k * V;
         if (m->table)
@@ -1822,9 +1843,7 @@ static pf_status mtp_chain(pf_engine* e, const float* h0, bool sample, const Sam
     const uint32_t D = d.n_embd, V = d.n_vocab;
     hipLaunchKernelGGL(k_copy_f32, dim3((D + 255) / 256), dim3(256), 0, st, h0, e->mcur, D);
     for (uint32_t k = 0; k < d.n_mtp; k++) {
-        launch_gemv_f32(st, m->mtp[k * 3 + 0], 1, e->mcur, D, e->mg, D, nullptr);
-        launch_gemv_f32(st, m->mtp[k * 3 + 1], 1, e->mcur, D, e->mu, D, nullptr);
-        hipLaunchKernelGGL(k_silu_mul, dim3((D + 255) / 256), dim3(256), 0, st, e->mg, e->mu, e->ma, D);
+        launch_gemv_f32_glu(st, m->mtp[k * 3 + 0], m->mtp[k * 3 + 1], 1, e->mcur, D, e->ma, D);
         launch_gemv_f32(st, m->mtp[k * 3 + 2], 1, e->ma, D, e->mcur, D, e->mcur);
         float* lk = e->mlogits + (size_t)k * V;
         launch_gemv_f32(st, m->emb, 1, e->mcur, D, lk, V, nullptr);
