@@ -465,7 +465,7 @@ def bench_batch(args, C, cfg, w, ctx, dev, model):
         # the step's dominant kernel: verify-pass attention (78% of the decode's
         # kernel time), bound by HBM
         "roofline": {
-            "kernel": f"k_attn_chunk<8> (verify-pass attention, {M} rows over {N} sequences' int8 K/V)",
+            "kernel": f"k_attn_seq<8> (verify-pass attention, {M} rows over {N} sequences' int8 K/V)",
             "bound": "hbm",
             "achieved": round(attn_gbps, 1),
             "peak": HBM_PEAK_GBPS,

@@ -12,6 +12,8 @@
 //                  also quantize and store their own K/V rows here
 //   k_attn_chunk   the same per (row, head, chunk), for batched passes of
 //                  more than 8 rows
+//   k_attn_seq     the same per (head, chunk, group of a sequence's rows)
+//                  for batched verify passes, whose rows' windows may slide
 //   k_attn_merge_quant  per row: chunks rescaled to the row max and merged,
 //                  then the O projection's quantize_activation_row
 // The KVCache API (raw scores; weighted sum of caller probabilities) runs
@@ -436,6 +438,358 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const PassDesc* __restrict__
     if (grp >= n_groups || m >= ph.m) return;
     attn_one_row<PARTS, VROW>(ph, g, kv, layer, m, grp % g.n_heads, grp / g.n_heads, q, kself, vself, S, s_stride,
                               Up, cstride, smem);
+}
+
+// ------------------------------------------- sequence-group attention
+
+// LDS of k_attn_seq (bytes): K and V tiles of AS_TILE entries (the K tile
+// is reused after the dots for the dots [NR][AS_TILE], the probabilities
+// [NR][256] and the V partials [NR][4][128]), the tile's scales [2][AS_TILE],
+// queries and self keys [NR][128] fp32 each, wave maxima and sums [2][NR][4],
+// self scores and self weights [2][NR].
+constexpr uint32_t AS_EXTRA = 16;                  // extra tile entries for the rows' shifts
+constexpr uint32_t AS_TILE = 256 + AS_EXTRA;
+constexpr uint32_t AS_NR = 5;                      // rows of one group at most
+constexpr uint32_t as_smem() {
+    return 2u * AS_TILE * 128u + (2u * AS_TILE + 2u * AS_NR * 128u + 8u * AS_NR + 2u * AS_NR) * 4u;
+}
+static_assert((AS_NR * AS_TILE + AS_NR * 256u + AS_NR * 4u * 128u) * 4u <= AS_TILE * 128u, "K tile reuse");
+
+// Engine attention (the first stage above) of batched passes whose rows
+// come in groups of gsize (<= AS_NR) consecutive positions of one
+// sequence (a batched verify pass: each sequence's n_mtp + 1 rows).  Unlike
+// k_attn_group the rows' lists need not extend each other: when the window
+// slides (or a pooled row completes, or the sink fills) between the rows,
+// row r's list index j names a different entry than row 0's.  The block
+// for (head h, chunk c, group y) therefore loads the union of the rows'
+// chunk-c entries once, in a unified order: the S_max sink entries, the
+// pool_max pooled rows, then the window from the first row's oldest entry
+// (the counts of the group's last row are the largest).  Row r's entry j
+// sits at unified index u = j + shift_r(j), shift 0 in the sink part,
+// S_max - S_r in the pooled part, and D_r = (S_max - S_r) + (pool_max -
+// pool_r) + (win_lo_r - win_lo_0) in the window part, so chunk c of every
+// row lies in unified [256 c, 256 c + 256 + max D_r) (D_r <= 12 for 5
+// consecutive positions).  Each row's arithmetic is k_attn_group's: the
+// per-entry fmaf dot, the self score as a sequential mul+add, chunk max,
+// exp, CANON(4) sum, and 64-entry V chains in list order (zero-weight
+// terms past a row's list are left out, which changes no bit).  The K/V
+// conversions of the dots are shared by the rows.  Grid (heads * chunks,
+// ceil(M / gsize)), 512 threads: waves 0-4 compute the tile's dots (one
+// entry per thread), wave 7 the self dots; for the softmax and V chains
+// waves 0-3 serve rows 0-2 and waves 4-7 rows 3-4.
+template <int PARTS>
+__global__ __launch_bounds__(512) void k_attn_seq(const PassDesc* __restrict__ pd, KvGeom g, KvPlanes kv,
+                                                  uint32_t layer, uint32_t M, uint32_t gsize,
+                                                  const float* __restrict__ q, const float* __restrict__ kself,
+                                                  const float* __restrict__ vself, float* __restrict__ S,
+                                                  uint32_t s_stride, float* __restrict__ Up, uint32_t cstride) {
+    constexpr uint32_t hd = 16 * PARTS, NR = AS_NR;
+    __shared__ __align__(16) uint8_t smem[as_smem()];
+    int4* kt = reinterpret_cast<int4*>(smem);                                // [PARTS][AS_TILE], swizzled
+    int8_t (*vt)[128] = reinterpret_cast<int8_t (*)[128]>(smem + AS_TILE * 128u);
+    float* ksc = reinterpret_cast<float*>(smem + 2u * AS_TILE * 128u);     // [AS_TILE]
+    float* vsc = ksc + AS_TILE;                                             // [AS_TILE]
+    float* qs = vsc + AS_TILE;                                              // [NR][128]
+    float* kss = qs + NR * 128;                                             // [NR][128]
+    float* rmx = kss + NR * 128;                                            // [NR][4]
+    float* rsm = rmx + NR * 4;                                              // [NR][4]
+    float* selfs = rsm + NR * 4;                                            // [NR] self dots
+    float* pself = selfs + NR;                                              // [NR]
+    float* dot = reinterpret_cast<float*>(smem);                            // [NR][AS_TILE], after the dots
+    float* pe = dot + NR * AS_TILE;                                         // [NR][256]
+    float* wp = pe + NR * 256;                                              // [NR][4][128]
+
+    const uint32_t H = g.n_heads, h = blockIdx.x % H, c = blockIdx.x / H;
+    const uint32_t t = threadIdx.x, lane = t & 63u, wid = t >> 6;
+    const PassHead ph = pass_head(pd);
+    const uint32_t Mp = min(M, ph.m), mb = blockIdx.y * gsize;
+    if (mb >= Mp) return;
+    const uint32_t G = min(min(gsize, NR), Mp - mb);
+    // the rows' views (positions consecutive, so every count is nondecreasing)
+    uint32_t Sr[NR], Pr[NR], Cr[NR], Dr[NR];
+    const KvView v0 = kv_view(g, row_pos(ph, mb));
+    const KvView vl = kv_view(g, row_pos(ph, mb + G - 1u));
+    const uint32_t Smax = vl.sink, Pmax = vl.pool, wl0 = v0.win_lo;
+    uint32_t Cmax = 0, Dmax = 0;
+#pragma unroll
+    for (uint32_t r = 0; r < NR; r++) {
+        const KvView v = kv_view(g, row_pos(ph, mb + min(r, G - 1u)));
+        Sr[r] = v.sink;
+        Pr[r] = v.pool;
+        Cr[r] = v.count();
+        Dr[r] = (Smax - v.sink) + (Pmax - v.pool) + (v.win_lo - wl0);
+        Cmax = max(Cmax, Cr[r]);
+        Dmax = max(Dmax, Dr[r]);
+    }
+    const uint32_t j0 = 256u * c;
+    if (j0 > Cmax) return;                                   // past every row's self entry
+    const uint32_t U = Smax + Pmax + (vl.win_hi - wl0);      // unified entries
+    const uint32_t ntile = U > j0 ? min(min(AS_TILE, 256u + Dmax), U - j0) : 0u;
+    const uint32_t D = H * hd, seq = row_seq(ph, mb);
+    const size_t plane = plane_index(g, seq, layer, h);
+    const uint32_t wb0 = wl0 % g.ring;
+    // physical row of unified entry u
+    auto urow = [&](uint32_t u) -> uint32_t {
+        if (u < Smax) return u;
+        if (u < Smax + Pmax) return KV_SINK_ROWS + g.ring + (u - Smax);
+        uint32_t x = wb0 + (u - Smax - Pmax);
+        x = x >= g.ring ? x - g.ring : x;
+        return KV_SINK_ROWS + x;
+    };
+
+    // ---- loads, all issued before any is used
+    constexpr uint32_t QPT = (NR * hd + 511u) / 512u;
+    float qv[QPT], kvv[QPT];
+#pragma unroll
+    for (uint32_t k = 0; k < QPT; k++) {
+        const uint32_t i = t + 512u * k, r = i / hd, d = i - r * hd;
+        qv[k] = 0.0f;
+        kvv[k] = 0.0f;
+        if (r < G) {
+            const size_t o = (size_t)(mb + r) * D + h * hd + d;
+            qv[k] = q[o];
+            kvv[k] = kself[o];
+        }
+    }
+    // K and V of the tile: 16-byte piece pi = t + 512 i is part pi % PARTS
+    // of tile entry pi / PARTS
+    constexpr uint32_t LPT = (AS_TILE * PARTS + 511u) / 512u;
+    int4 kw[LPT], vw[LPT];
+#pragma unroll
+    for (uint32_t i = 0; i < LPT; i++) {
+        const uint32_t pi = t + 512u * i, e = pi / PARTS, part = pi % PARTS;
+        kw[i] = make_int4(0, 0, 0, 0);
+        vw[i] = make_int4(0, 0, 0, 0);
+        if (e < ntile) {
+            const size_t row = plane * g.rows + urow(j0 + e);
+            kw[i] = reinterpret_cast<const int4*>(kv.k + row * hd)[part];
+            vw[i] = reinterpret_cast<const int4*>(kv.v + row * hd)[part];
+        }
+    }
+    float ks = 0.0f, vs = 0.0f;
+    if (t < ntile) {
+        const size_t row = plane * g.rows + urow(j0 + t);
+        ks = kv.ks[row];
+        vs = kv.vs[row];
+    }
+
+    // ---- LDS
+#pragma unroll
+    for (uint32_t k = 0; k < QPT; k++) {
+        const uint32_t i = t + 512u * k, r = i / hd, d = i - r * hd;
+        if (r < NR) {
+            qs[r * 128 + d] = qv[k];
+            kss[r * 128 + d] = kvv[k];
+        }
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < LPT; i++) {
+        const uint32_t pi = t + 512u * i, e = pi / PARTS, part = pi % PARTS;
+        if (e < AS_TILE) {
+            kt[part * AS_TILE + (e ^ part)] = kw[i];
+            *reinterpret_cast<int4*>(&vt[e][16 * part]) = vw[i];
+        }
+    }
+    if (t < AS_TILE) {
+        ksc[t] = ks;                                         // 0 past the tile: those terms add exactly 0
+        vsc[t] = vs;
+    }
+    __syncthreads();
+
+    // ---- dots of tile entry t (waves 0-4) with every row's query (the
+    // converted key shared by the rows); wave 7 lane r: row r's self dot
+    float acc[NR];
+#pragma unroll
+    for (uint32_t r = 0; r < NR; r++) acc[r] = 0.0f;
+    if (t < ntile) {
+        const float ksv = ksc[t];
+#pragma unroll
+        for (int p = 0; p < PARTS; p++) {
+            const int4 w4 = kt[p * AS_TILE + (t ^ (uint32_t)p)];
+            const int wv4[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+            for (int b = 0; b < 16; b++) {
+                const float kf = (float)(int8_t)((wv4[b >> 2] >> (8 * (b & 3))) & 0xFF) * ksv;
+#pragma unroll
+                for (uint32_t r = 0; r < NR; r++) acc[r] = __builtin_fmaf(qs[r * 128 + p * 16 + b], kf, acc[r]);
+            }
+        }
+    }
+    {
+        const uint32_t rs = wid == 7u ? lane : NR;
+        if (rs < G) {
+            float sd = 0.0f;
+#pragma unroll 16
+            for (uint32_t i = 0; i < hd; i++) sd = sd + qs[rs * 128 + i] * kss[rs * 128 + i];
+            selfs[rs] = sd;
+        }
+    }
+    __syncthreads();                                         // the K tile is read; dot reuses it
+    if (t < AS_TILE)
+#pragma unroll
+        for (uint32_t r = 0; r < NR; r++) dot[r * AS_TILE + t] = acc[r];
+    __syncthreads();
+
+    // ---- per row: scores by list index j = j0 + tt, chunk max, exp and the
+    // CANON(4) chunk sum; waves 0-3 serve rows 0-2, waves 4-7 rows 3-4
+    // (wave w & 3 holds list indices 64 (w & 3) ..)
+    const float scale = 1.0f / __builtin_sqrtf((float)hd);
+    const uint32_t half = wid >> 2, tt = t & 255u, wq = wid & 3u;
+    const uint32_t j = j0 + tt;
+    float sc[NR];
+#pragma unroll
+    for (uint32_t r = 0; r < NR; r++) {
+        sc[r] = -__builtin_inff();
+        if ((r >= 3u ? 1u : 0u) != half) continue;
+        if (r < G) {
+            if (j < Cr[r]) {
+                const uint32_t sh = j < Sr[r] ? 0u : (j < Sr[r] + Pr[r] ? Smax - Sr[r] : Dr[r]);
+                sc[r] = dot[r * AS_TILE + tt + sh] * scale;
+            } else if (j == Cr[r]) {
+                sc[r] = selfs[r] * scale;
+            }
+        }
+        const float w = wave_max(sc[r]);
+        if (lane == 0) rmx[r * 4 + wq] = w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t r = 0; r < NR; r++) {
+        if ((r >= 3u ? 1u : 0u) != half) continue;
+        const float* rr = rmx + r * 4;
+        const float mx = fmaxf(fmaxf(rr[0], rr[1]), fmaxf(rr[2], rr[3]));
+        const bool in = r < G && j <= Cr[r];
+        const float ex = in ? expf_c(sc[r] - mx) : 0.0f;
+        pe[r * 256 + tt] = r < G && j < Cr[r] ? ex : 0.0f;
+        if (in && j == Cr[r]) pself[r] = ex;
+        const float w = wave_tree_sum(ex);
+        if (lane == 0) rsm[r * 4 + wq] = w;
+    }
+    __syncthreads();
+
+    // ---- V: per row and 64-entry sub-chunk an fmaf chain in list order
+    // (entries in groups of 8, the rows' chains interleaved; entries past a
+    // row's list up to the next multiple of 8 have weight 0 and read finite
+    // tile values, so fmaf(0, a, w) == w)
+    const uint32_t sub = wq, i0 = 2u * lane;
+    if (i0 < hd) {
+        float w0[NR], w1[NR];
+        uint32_t e_end[NR], b1[NR], b2[NR];
+        uint32_t e_max = 64u * sub;
+#pragma unroll
+        for (uint32_t r = 0; r < NR; r++) {
+            w0[r] = 0.0f;
+            w1[r] = 0.0f;
+            const bool mine = (r >= 3u ? 1u : 0u) == half;
+            const uint32_t nvis = mine && r < G && j0 < Cr[r] ? min(256u, Cr[r] - j0) : 0u;
+            e_end[r] = min(64u * sub + 64u, (nvis + 7u) & ~7u);
+            e_max = max(e_max, e_end[r]);
+            b1[r] = Sr[r] > j0 ? Sr[r] - j0 : 0u;                    // first pooled offset
+            b2[r] = Sr[r] + Pr[r] > j0 ? Sr[r] + Pr[r] - j0 : 0u;    // first window offset
+        }
+        // rows whose chunk lies in the window part with shift D_r = r (the
+        // window sliding by one entry per row, no pooled row completed in
+        // the group) read slots e + u + r: the conversions of slots e ..
+        // are shared by the rows
+        bool fast = true;
+#pragma unroll
+        for (uint32_t r = 0; r < NR; r++)
+            if (r < G && (r >= 3u ? 1u : 0u) == half) fast = fast && Dr[r] == r && b2[r] == 0u;
+#define PF_ATTN_SEQ_VFAST(R0, NRH)                                                                         \
+    for (uint32_t e = 64u * sub; e < e_max; e += 8) {                                                      \
+        float a0[8 + NRH - 1], a1[8 + NRH - 1];                                                            \
+        _Pragma("unroll") for (uint32_t k = 0; k < 8u + NRH - 1u; k++) {                                   \
+            const uint32_t sl = e + R0 + k;                                                                \
+            const uint32_t cc = *reinterpret_cast<const uint16_t*>(&vt[sl][i0]);                           \
+            const float vv = vsc[sl];                                                                      \
+            a0[k] = (float)(int8_t)(cc & 0xFFu) * vv;                                                      \
+            a1[k] = (float)(int8_t)(cc >> 8) * vv;                                                         \
+        }                                                                                                  \
+        _Pragma("unroll") for (uint32_t rr = 0; rr < NRH; rr++) {                                          \
+            const uint32_t r = R0 + rr;                                                                    \
+            if (e >= e_end[r]) continue;                                                                   \
+            const float4 p0 = *reinterpret_cast<const float4*>(&pe[r * 256 + e]);                          \
+            const float4 p1 = *reinterpret_cast<const float4*>(&pe[r * 256 + e + 4]);                      \
+            const float pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};                          \
+            _Pragma("unroll") for (uint32_t u = 0; u < 8; u++) {                                           \
+                w0[r] = __builtin_fmaf(pp[u], a0[u + rr], w0[r]);                                          \
+                w1[r] = __builtin_fmaf(pp[u], a1[u + rr], w1[r]);                                          \
+            }                                                                                              \
+        }                                                                                                  \
+    }
+        if (fast && half == 0u) {
+            PF_ATTN_SEQ_VFAST(0u, 3u)
+        } else if (fast) {
+            PF_ATTN_SEQ_VFAST(3u, 2u)
+        } else
+        for (uint32_t e = 64u * sub; e < e_max; e += 8) {
+#pragma unroll
+            for (uint32_t r = 0; r < NR; r++) {
+                if (e >= e_end[r]) continue;
+                uint32_t sl[8];
+                if (e >= b2[r]) {
+#pragma unroll
+                    for (int u = 0; u < 8; u++) sl[u] = e + u + Dr[r];
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        const uint32_t x = e + u;
+                        sl[u] = x + (x < b1[r] ? 0u : (x < b2[r] ? Smax - Sr[r] : Dr[r]));
+                    }
+                }
+                float vv[8];
+                uint32_t cc[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    cc[u] = *reinterpret_cast<const uint16_t*>(&vt[sl[u]][i0]);
+                    vv[u] = vsc[sl[u]];
+                }
+                const float4 p0 = *reinterpret_cast<const float4*>(&pe[r * 256 + e]);
+                const float4 p1 = *reinterpret_cast<const float4*>(&pe[r * 256 + e + 4]);
+                const float pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    w0[r] = __builtin_fmaf(pp[u], (float)(int8_t)(cc[u] & 0xFFu) * vv[u], w0[r]);
+                    w1[r] = __builtin_fmaf(pp[u], (float)(int8_t)(cc[u] >> 8) * vv[u], w1[r]);
+                }
+            }
+        }
+#pragma unroll
+        for (uint32_t r = 0; r < NR; r++) {
+            if (r >= G) break;
+            if ((r >= 3u ? 1u : 0u) != half) continue;
+            const uint32_t js = Cr[r] - j0;                  // the row's self entry in the chunk
+            if (js < 256u && (js >> 6) == sub) {
+                const float ps = pself[r];
+                const size_t o = (size_t)(mb + r) * D + h * hd + i0;
+                w0[r] = __builtin_fmaf(ps, vself[o], w0[r]);
+                w1[r] = __builtin_fmaf(ps, vself[o + 1], w1[r]);
+            }
+            wp[(r * 4 + sub) * 128 + i0] = w0[r];
+            wp[(r * 4 + sub) * 128 + i0 + 1] = w1[r];
+        }
+#undef PF_ATTN_SEQ_VFAST
+    }
+    __syncthreads();
+    // ---- outputs of the rows whose list reaches this chunk
+    for (uint32_t i = t; i < G * hd; i += 512u) {
+        const uint32_t r = i / hd, d = i - r * hd;
+        if (j0 > Cr[r]) continue;
+        const size_t mh = (size_t)(mb + r) * H + h;
+        float u = 0.0f;
+        u = u + wp[(r * 4 + 0) * 128 + d];
+        u = u + wp[(r * 4 + 1) * 128 + d];
+        u = u + wp[(r * 4 + 2) * 128 + d];
+        u = u + wp[(r * 4 + 3) * 128 + d];
+        Up[(mh * cstride + c) * hd + d] = u;
+    }
+    if (t < G && j0 <= Cr[t]) {
+        const float* mm = rmx + t * 4;
+        const float* ss = rsm + t * 4;
+        const size_t mh = (size_t)(mb + t) * H + h;
+        S[mh * s_stride + 2 * c] = fmaxf(fmaxf(mm[0], mm[1]), fmaxf(mm[2], mm[3]));
+        S[mh * s_stride + 2 * c + 1] = (ss[0] + ss[2]) + (ss[1] + ss[3]);   // CANON(4) over the wave totals
+    }
 }
 
 // ------------------------------------------------- grouped attention

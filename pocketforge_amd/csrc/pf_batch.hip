@@ -100,8 +100,10 @@ extern "C" pf_status pf_batch_forward(pf_engine* e, const uint32_t* seqs, uint32
     PF_HIP(c, hipMemcpyAsync(e->pdP, &pd, sizeof(PassDesc), hipMemcpyHostToDevice, c->stream));
     PF_HIP(c, hipStreamSynchronize(c->stream));
     pd.batch = 0;
+    e->batch_group = rows_per_seq;           // each sequence's rows_per_seq consecutive positions
     pf_status s = run_pass(e, e->pdP, rows, 0, logits ? e->logitsB : nullptr, hidden ? e->hiddenB : nullptr, true,
                            pos_last);
+    e->batch_group = 0;
     if (s) return s;
     for (uint32_t i = 0; i < n; i++) e->spos[seqs[i]] += rows_per_seq;
     batch_sync_out(e);
@@ -278,7 +280,9 @@ extern "C" pf_status pf_batch_generate(pf_engine* e, const int32_t* prompts, con
             if ((s = batch_mtp_chain(e, e->hiddenA, nm, cfg))) return s;
             if ((s = timed_begin(e, true, &tp))) return s;
             e->in_verify = true;
+            e->batch_group = R;                      // each MTP sequence's R verify rows
             s = run_pass(e, e->pdB, nm * R, 0, e->logitsB, nullptr, true, pos_hi + R);
+            e->batch_group = 0;
             e->in_verify = false;
             if (s) return s;
             if (tp) PF_HIP(c, hipEventRecord(tp->b, st));

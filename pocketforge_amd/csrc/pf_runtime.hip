@@ -573,7 +573,29 @@ static bool attn_fused(uint32_t M) { return M <= AG_MAX_ROWS; }
 static void launch_attn(hipStream_t st, uint32_t hd, uint32_t M, uint32_t tasks, const PassDesc* pd,
                         const KvGeom& g, const KvPlanes& kv, uint32_t l, const float* q, const float* k,
                         const float* v, float* S, uint32_t s_stride, float* Wp, uint32_t cstride, Prefetch pf,
-                        bool batch, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr) {
+                        bool batch, uint32_t gsize, hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr) {
+    if (batch && M > AG_MAX_ROWS && gsize >= 2 && gsize <= AS_NR) {
+        // groups of gsize consecutive positions of one sequence (a batched
+        // verify pass): one block per (head, chunk, group) loads the union
+        // of the rows' chunk entries once
+        const dim3 grid(tasks, (M + gsize - 1) / gsize);
+        if (hd == 64) {
+            if (ev0)
+                hipExtLaunchKernelGGL((k_attn_seq<4>), grid, dim3(512), 0, st, ev0, ev1, 0, pd, g, kv, l, M, gsize, q,
+                                      k, v, S, s_stride, Wp, cstride);
+            else
+                hipLaunchKernelGGL((k_attn_seq<4>), grid, dim3(512), 0, st, pd, g, kv, l, M, gsize, q, k, v, S,
+                                   s_stride, Wp, cstride);
+        } else {
+            if (ev0)
+                hipExtLaunchKernelGGL((k_attn_seq<8>), grid, dim3(512), 0, st, ev0, ev1, 0, pd, g, kv, l, M, gsize, q,
+                                      k, v, S, s_stride, Wp, cstride);
+            else
+                hipLaunchKernelGGL((k_attn_seq<8>), grid, dim3(512), 0, st, pd, g, kv, l, M, gsize, q, k, v, S,
+                                   s_stride, Wp, cstride);
+        }
+        return;
+    }
     if (batch && M > AG_MAX_ROWS) {
         // many sequences of a few rows each: one block per (row, head, chunk),
         // the M rows of one (head, chunk) on one XCD (blocks b with equal b mod 8)
@@ -1266,6 +1288,7 @@ struct pf_engine {
     // per-launch timing of the int8 GEMVs of verify passes (profiling mode)
     bool profile = false;
     bool in_verify = false;
+    uint32_t batch_group = 0;     // batched pass: rows come in groups of this many consecutive positions of one sequence
     std::vector<TimedPass> kev;
     std::vector<double> kev_bytes;
     size_t kev_used = 0;
@@ -1740,8 +1763,8 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         // attention's extra blocks stream the O weights through the cache
         // hierarchy; other passes run the merge kernel, whose extra blocks do
         launch_attn(st, hd, M, attn_tasks, pd, g, e->kv, l, e->q, e->k, e->v, e->S, e->s_stride, e->Wp,
-                    e->cstride, merge_in_o ? prefetch_of(e, m->o[l]) : Prefetch{nullptr, 0, e->sink}, batch, aev0,
-                    aev1);
+                    e->cstride, merge_in_o ? prefetch_of(e, m->o[l]) : Prefetch{nullptr, 0, e->sink}, batch,
+                    batch ? e->batch_group : 0u, aev0, aev1);
         if (!merge_in_o)
             PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_attn_merge_quant<PER>, dim3(M + e->pf_blocks), dim3(1024), 0, st,
                                                     pd, g, (const float*)e->S, e->s_stride, (const float*)e->Wp,

@@ -119,3 +119,34 @@ def test_e_64x8k_snapshot_batched_verify(one_b):
         np.testing.assert_array_equal(gl[s], ol, err_msg=f"logits, sequence {s}")
         oms[s].close()
     e.close()
+
+
+def test_e_sliding_window_snapshot_batched_verify(one_b):
+    """E's shape once decoding has slid the window: 8 sequences of the 1B
+    model after 8318 + s tokens (window 8192, pool 64: one pooled row and
+    a window sliding by one entry per verify row), one batched pass of 5
+    rows per sequence.  The attention of that pass serves each sequence's
+    rows together although their lists differ by one entry per row; for
+    sequences 2-5 a pooled row completes between two of the rows."""
+    cfg, w, m = one_b
+    S, L = 8, 8318
+    kv = dict(sink_size=4, window_size=8192, pool_block=64, max_context=L + S + 64)
+    e = pf.BatchEngine(m, S, **kv)
+    for s in range(S):
+        e.prefill_seq(s, W.prompt_ids(L + s, cfg["n_vocab"], seed=700 + s))
+    c = dict(cfg)
+    c.update(kv)
+    checked = (0, 3, 7)
+    oms = {}
+    for s in checked:
+        print(f"E sliding snapshot: importing sequence {s}", flush=True)
+        oms[s] = O.Model(c, w)
+        _import_state(e, s, oms[s], cfg, kv)
+    rows = np.stack([W.prompt_ids(5, cfg["n_vocab"], seed=900 + s) for s in range(S)]).astype(np.int32)
+    gl, gh = e.forward_batch(np.arange(S, dtype=np.uint32), rows)
+    for s in checked:
+        ol, oh = _oracle_rows(oms[s], rows[s])
+        np.testing.assert_array_equal(gh[s], oh, err_msg=f"hidden, sequence {s}")
+        np.testing.assert_array_equal(gl[s], ol, err_msg=f"logits, sequence {s}")
+        oms[s].close()
+    e.close()
