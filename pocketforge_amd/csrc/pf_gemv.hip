@@ -14,6 +14,31 @@ namespace pf {
 
 // ============================================ fp32 x dequantized Q4 GEMV
 
+// The M activation rows (K <= 2048 floats each) staged once per workgroup
+// in LDS, then lane l's 32 elements of every row (block l) in registers
+// (zeros for lanes past the row's blocks): one copy of the rows per
+// workgroup from L2 instead of one per wave.
+template <int M>
+__device__ __forceinline__ void stage_rows(const float* __restrict__ h, uint32_t h_stride, uint32_t K, uint32_t lane,
+                                           bool live, float (&hv)[M][32]) {
+    __shared__ __align__(16) float hsm[M * 2048];
+    const uint32_t n4 = K >> 2;
+    for (uint32_t i = threadIdx.x; i < M * n4; i += blockDim.x) {
+        const uint32_t m = i / n4, c = i - m * n4;
+        reinterpret_cast<float4*>(hsm)[m * 512u + c] = *reinterpret_cast<const float4*>(h + (size_t)m * h_stride + 4u * c);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+            const float4 v = live ? *reinterpret_cast<const float4*>(hsm + m * 2048 + lane * 32u + i)
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+            hv[m][i] = v.x; hv[m][i + 1] = v.y; hv[m][i + 2] = v.z; hv[m][i + 3] = v.w;
+        }
+    }
+}
+
 // y[m][n] (+= y_in[m][n] when resid) = canonical fp32 dot of h[m] with row n:
 // lane l holds block l (K <= 2048), fmaf chain over the block's elements,
 // halving tree over the 64 lanes.  Each wave walks rows n = wave, wave +
@@ -31,15 +56,7 @@ __global__ __launch_bounds__(256) void k_gemv_f32(const uint8_t* __restrict__ co
     const uint32_t nb = K >> 5;
     const bool live = lane < nb;
     float hv[M][32];
-#pragma unroll
-    for (int m = 0; m < M; m++) {
-#pragma unroll
-        for (int i = 0; i < 32; i += 4) {
-            float4 v = live ? *reinterpret_cast<const float4*>(h + (size_t)m * h_stride + lane * 32u + i)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
-            hv[m][i] = v.x; hv[m][i + 1] = v.y; hv[m][i + 2] = v.z; hv[m][i + 3] = v.w;
-        }
-    }
+    stage_rows<M>(h, h_stride, K, lane, live, hv);
     for (uint32_t n = wave; n < N; n += nwaves) {
         float acc[M];
 #pragma unroll
@@ -90,15 +107,7 @@ __global__ __launch_bounds__(256) void k_gemv_f32_glu(const uint8_t* __restrict_
     const uint32_t nb = K >> 5;
     const bool live = lane < nb;
     float hv[M][32];
-#pragma unroll
-    for (int m = 0; m < M; m++) {
-#pragma unroll
-        for (int i = 0; i < 32; i += 4) {
-            float4 v = live ? *reinterpret_cast<const float4*>(h + (size_t)m * h_stride + lane * 32u + i)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
-            hv[m][i] = v.x; hv[m][i + 1] = v.y; hv[m][i + 2] = v.z; hv[m][i + 3] = v.w;
-        }
-    }
+    stage_rows<M>(h, h_stride, K, lane, live, hv);
     for (uint32_t n = wave; n < N; n += nwaves) {
         float ag[M], au[M];
 #pragma unroll
