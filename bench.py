@@ -274,10 +274,15 @@ def main():
     n_l, gemv_us, gemv_bytes = eng.gemv_stats()
     gemv_groups = eng.gemv_by_size()
     a_n, attn_us = eng.attn_stats()
+    v_ev, b_ev, _, _ = eng.pass_times()
+    log(f"profiled step: {dt_p * 1e3:.1f} ms, verify pass {v_ev:.1f} us, base pass {b_ev:.1f} us (with dispatch "
+        f"events), gemv {gemv_us:.2f} us avg x{n_l}")
+    # and one more, issued the same way with events around each pass only:
+    # the pass times without the dispatch events' own cost
+    step(2)
     v_us, b_us, vn, bn = eng.pass_times()
     eng.profile(False)
-    log(f"profiled step: {dt_p * 1e3:.1f} ms, verify pass {v_us:.1f} us x{vn}, base pass {b_us:.1f} us x{bn}, "
-        f"gemv {gemv_us:.2f} us avg x{n_l}")
+    log(f"pass-timed step: verify pass {v_us:.1f} us x{vn}, base pass {b_us:.1f} us x{bn}")
     achieved = gemv_bytes / gemv_us / 1e3
     r_avg = sum(r[0] * r[1] for r in round_us) / max(1, sum(r[1] for r in round_us))
     # verify pass algorithmic bytes: every packed weight once (incl. the tied
@@ -338,6 +343,9 @@ def main():
             "frac": round(pass_bytes / v_us / 1e3 / HBM_PEAK_GBPS, 4),
             "attention_avg_us": round(attn_us, 2),
             "attention_launches": a_n,
+            "timing": "HIP events around each verify pass on the engine stream, in one more decode step of the same "
+                      "workload issued without graphs and without per-dispatch events",
+            "with_dispatch_events_us": round(v_ev, 2),
         },
     }
     if not args.no_cpu:
@@ -419,14 +427,18 @@ def bench_batch(args, C, cfg, w, ctx, dev, model):
     dt_p, toks_p, res_p = step(True)
     n_l, gemm_us, gemm_bytes = eng.gemv_stats()
     a_n, attn_us = eng.attn_stats()
+    v_ev, b_ev, _, _ = eng.pass_times()
+    # one more step with events around each pass only (undisturbed pass times)
+    step(2)
     v_us, b_us, vn, bn = eng.pass_times()
     eng.profile(False)
     M = N * (cfg["n_mtp"] + 1)
     D, F = cfg["n_embd"], cfg["n_ff"]
     nk = [(3 * D, D), (D, D), (2 * F, D), (D, F)]    # QKV, O, gate|up, down (N x K) of every layer
     gemm_ops = 2.0 * M * sum(n * k for n, k in nk) / len(nk)
-    log(f"profiled step: {dt_p * 1e3:.1f} ms, verify pass {v_us:.1f} us x{vn}, base pass {b_us:.1f} us x{bn}, "
-        f"gemm {gemm_us:.2f} us avg x{n_l}")
+    log(f"profiled step: {dt_p * 1e3:.1f} ms, verify pass {v_ev:.1f} us (with dispatch events), "
+        f"gemm {gemm_us:.2f} us avg x{n_l}; pass-timed step: verify pass {v_us:.1f} us x{vn}, "
+        f"base pass {b_us:.1f} us x{bn}")
     achieved = gemm_ops / gemm_us / 1e6
     r_avg = sum(r[0] * r[1] for r in round_us) / max(1, sum(r[1] for r in round_us))
     wbytes = W.packed_bytes(w) + w["emb"][1].nbytes + w["emb"][2].nbytes
@@ -495,6 +507,8 @@ def bench_batch(args, C, cfg, w, ctx, dev, model):
             "bytes": round(wbytes + kv_bytes),
             "achieved_GBps": round((wbytes + kv_bytes) / v_us / 1e3, 1),
             "frac": round((wbytes + kv_bytes) / v_us / 1e3 / HBM_PEAK_GBPS, 4),
+            "timing": "HIP events around each verify pass on the engine stream, in one more step of the same "
+                      "workload issued without graphs and without per-dispatch events",
         },
     }
     if not args.no_cpu:

@@ -311,16 +311,19 @@ pf_status pf_engine_layer_skip_count(pf_engine* e, uint64_t* count);
 /* Average device time (us, HIP events on the engine's stream) of the MTP
  * rounds of the last pf_generate: base pass + draft + verify + accept. */
 pf_status pf_engine_round_time(const pf_engine* e, double* round_us, uint32_t* rounds);
-/* Average device time in microseconds of the verify passes (M = n_mtp + 1)
- * and base passes (M = 1) of the last pf_generate run without captured
- * graphs (profiling mode), measured with HIP events on the engine's
- * stream. */
+/* Average device time in microseconds of the verify passes (every verify
+ * segment) and base passes of the last pf_generate run without captured
+ * graphs (profiling modes 1 and 2), measured with HIP events around each
+ * pass on the engine's stream.  Mode 2 adds no events inside a pass, so
+ * its pass times are the undisturbed ones. */
 pf_status pf_engine_pass_times(const pf_engine* e, double* verify_us, double* base_us,
                                uint32_t* verify_n, uint32_t* base_n);
 
-/* Profiling mode: pf_generate issues its kernels one by one (no captured
- * graphs) and every int8 GEMV dispatch of the verify passes carries HIP
- * start/stop events. */
+/* Profiling mode.  0: off (captured graphs).  1: pf_generate issues its
+ * kernels one by one (no captured graphs) and every int8 GEMV and attention
+ * dispatch of the verify passes carries HIP start/stop events.  2: kernels
+ * one by one with events around each pass only.  Other values:
+ * PF_ERR_ARG. */
 pf_status pf_engine_profile(pf_engine* e, int32_t enable);
 /* Launch count, average duration (us) and average algorithmic bytes
  * (packed weights + int8 activations + fp32 outputs) of the GEMV launches

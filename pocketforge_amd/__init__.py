@@ -648,6 +648,9 @@ class Engine:
         return v.value, b.value, vn.value, bn.value
 
     def profile(self, enable=True):
+        """Profiling level (pf_engine_profile): False/0 captured graphs, True/1
+        kernels one by one with per-dispatch events on the verify passes, 2
+        kernels one by one with events around each pass only."""
         self.ctx.check(lib().pf_engine_profile(self.h, int(enable)), "pf_engine_profile")
 
     def round_time(self):

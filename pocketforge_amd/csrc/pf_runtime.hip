@@ -1281,12 +1281,14 @@ struct pf_engine {
     uint32_t round_n = 0;
     SamplingCfg graph_cfg{};
     uint64_t graph_seed = 0;
-    bool graph_profile = false;
+    int32_t graph_profile = 0;
     bool graphs_valid = false;
     bool capturing = false;
     bool use_graphs = true;
-    // per-launch timing of the int8 GEMVs of verify passes (profiling mode)
-    bool profile = false;
+    // profiling mode: 0 off (captured graphs), 1 kernels one by one with
+    // pass events and per-dispatch events on the verify passes' GEMVs and
+    // attention, 2 kernels one by one with pass events only
+    int32_t profile = 0;
     bool in_verify = false;
     uint32_t batch_group = 0;     // batched pass: rows come in groups of this many consecutive positions of one sequence
     std::vector<TimedPass> kev;
@@ -1633,7 +1635,7 @@ static pf_status pass_mm(pf_engine* e, const pf_matrix* W, MmKind kind, uint32_t
     a.K = W->cols;
     a.M = M;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
-    if (e->profile && e->in_verify && !e->capturing) {
+    if (e->profile == 1 && e->in_verify && !e->capturing) {
         if (e->kev_used == e->kev.size()) {
             TimedPass n{};
             PF_HIP(e->c, hipEventCreate(&n.a));
@@ -1748,7 +1750,7 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
             hipLaunchKernelGGL(k_kv_store_pass, dim3(M, H), dim3(64), 0, st, (const PassDesc*)pd, g, e->kv, l,
                                (const float*)e->k, (const float*)e->v);
         hipEvent_t aev0 = nullptr, aev1 = nullptr;
-        if (e->profile && e->in_verify && !e->capturing) {
+        if (e->profile == 1 && e->in_verify && !e->capturing) {
             if (e->aev_used == e->aev.size()) {
                 TimedPass n{};
                 PF_HIP(c, hipEventCreate(&n.a));
@@ -2221,7 +2223,8 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
 
 extern "C" pf_status pf_engine_profile(pf_engine* e, int32_t enable) {
     if (!e) return PF_ERR_ARG;
-    e->profile = enable != 0;
+    if (enable < 0 || enable > 2) return PF_ERR_ARG;
+    e->profile = enable;
     return PF_OK;
 }
 
