@@ -283,6 +283,17 @@ def main():
     v_us, b_us, vn, bn = eng.pass_times()
     eng.profile(False)
     log(f"pass-timed step: verify pass {v_us:.1f} us x{vn}, base pass {b_us:.1f} us x{bn}")
+    # the same workload with every round verifying all n_mtp + 1 rows in one
+    # pass (pf_engine_set_verify_full): one timed step in graphs, one
+    # pass-timed step
+    eng.set_verify_full(True)
+    dt_f, toks_f, res_f = step(False)
+    step(2)
+    vf_us, _, vf_n, _ = eng.pass_times()
+    eng.profile(False)
+    eng.set_verify_full(False)
+    log(f"full-verify step: {len(toks_f) - 1} tokens in {dt_f * 1e3:.1f} ms ({(len(toks_f) - 1) / dt_f:.1f} tok/s), "
+        f"verify pass ({cfg['n_mtp'] + 1} rows) {vf_us:.1f} us x{vf_n}")
     achieved = gemv_bytes / gemv_us / 1e3
     r_avg = sum(r[0] * r[1] for r in round_us) / max(1, sum(r[1] for r in round_us))
     # verify pass algorithmic bytes: every packed weight once (incl. the tied
@@ -346,6 +357,15 @@ def main():
             "timing": "HIP events around each verify pass on the engine stream, in one more decode step of the same "
                       "workload issued without graphs and without per-dispatch events",
             "with_dispatch_events_us": round(v_ev, 2),
+        },
+        # every round verifying all n_mtp + 1 rows in one pass (the segment
+        # policy's alternative): throughput and the undisturbed pass time
+        "verify_full": {
+            "value": round((len(toks_f) - 1) / dt_f, 3),
+            "rows": cfg["n_mtp"] + 1,
+            "verify_pass_us": round(vf_us, 2),
+            "achieved_GBps": round(pass_bytes / vf_us / 1e3, 1),
+            "frac": round(pass_bytes / vf_us / 1e3 / HBM_PEAK_GBPS, 4),
         },
     }
     if not args.no_cpu:
