@@ -92,8 +92,8 @@ __global__ __launch_bounds__(256) void k_gemv_f32(const uint8_t* __restrict__ co
 // One MTP head's gate and up products with the SiLU product fused
 // (src/mtp.cpp:63-127): a[m][n] = silu(g) * u, g and u the canonical dots
 // of h[m] with row n of Wg and Wu (k_gemv_f32's order), silu(g) =
-// g / (1 + exp(-g)) as k_silu_mul computes it, so a equals the three
-// separate launches bit for bit.
+// g / (1 + exp(-g)) (src/mtp.cpp:89-91, 157-159): the bits of two
+// k_gemv_f32 products followed by that elementwise step.
 template <int M>
 __global__ __launch_bounds__(256) void k_gemv_f32_glu(const uint8_t* __restrict__ gcodes,
                                                       const uint16_t* __restrict__ gscales,
@@ -365,15 +365,6 @@ __global__ __launch_bounds__(256) void k_skip_commit(const PassDesc* __restrict_
 __global__ void k_copy_f32(const float* __restrict__ src, float* __restrict__ dst, uint32_t n) {
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) dst[i] = src[i];
-}
-
-// MTP activation: a = silu(g) * u with silu(x) = x / (1 + exp(-x))
-// (src/mtp.cpp:89-91, 157-159).
-__global__ void k_silu_mul(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ a, uint32_t n) {
-    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    float s = g[i] / (1.0f + expf_c(-g[i]));
-    a[i] = s * u[i];
 }
 
 // Token embedding: x[m] = dequantized row tok[m] of the tied Q4 table.
