@@ -2126,6 +2126,9 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
     uint32_t n_gen = 0;
     bool have_row = false;
     uint32_t last_acc = 0;   // drafts the previous MTP round accepted
+    // MTP rounds that followed a round with no accepted draft, and those of
+    // them that accepted d0 (observed under either segment height)
+    uint32_t z_rounds = 0, z_d0 = 0;
     // One segment (a graph or, in profiling mode, its kernels one by one)
     // timed with the round events and its dispatch events harvested.
     auto segment = [&](hipGraphExec_t g, bool cont, bool reuse, bool mtp, uint32_t h) -> pf_status {
@@ -2162,8 +2165,12 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
             return fail(c, PF_ERR_CAPACITY, "position beyond the engine's max_context");
         // first verify segment: every row after a round that accepted a draft
         // (or when asked for); one row, the reference's first verify forward,
-        // after a round whose first draft was rejected
-        const bool full = e->verify_full || e->skip_on || last_acc > 0 || NM < 2;
+        // after a round whose first draft was rejected, unless d0 was accepted
+        // in more than 3 of 10 such rounds so far.  A one-row segment saves the
+        // other rows' work only when d0 is rejected (accepted, it needs a second
+        // segment), and a one-row pass costs about 0.7 of a five-row pass.
+        const bool d0_likely = z_rounds >= 2 && 10u * z_d0 > 3u * z_rounds;
+        const bool full = e->verify_full || e->skip_on || last_acc > 0 || NM < 2 || d0_likely;
         const uint32_t h = full ? NM + 1 : 1u;
         if (pf_status s = segment(graphs ? e->round_exec[have_row][mtp_round][mtp_round && full] : nullptr, false,
                                   have_row, mtp_round, h))
@@ -2199,6 +2206,10 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
             } else {
                 e->pos += m;
                 have_row = false;
+            }
+            if (last_acc == 0) {
+                z_rounds++;
+                z_d0 += a > 0 ? 1u : 0u;
             }
             last_acc = a;
         } else {
