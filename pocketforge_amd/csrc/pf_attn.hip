@@ -454,6 +454,10 @@ constexpr uint32_t as_smem() {
     return 2u * AS_TILE * 128u + (2u * AS_TILE + 2u * AS_NR * 128u + 8u * AS_NR + 2u * AS_NR) * 4u;
 }
 static_assert((AS_NR * AS_TILE + AS_NR * 256u + AS_NR * 4u * 128u) * 4u <= AS_TILE * 128u, "K tile reuse");
+// Over AS_NR consecutive positions the sink count, the pooled count and the
+// oldest window entry each move by at most one per position, so a row's
+// shift D_r stays within the tile's extra entries.
+static_assert(3u * (AS_NR - 1u) <= AS_EXTRA, "row shifts fit the tile");
 
 // Engine attention (the first stage above) of batched passes whose rows
 // come in groups of gsize (<= AS_NR) consecutive positions of one

@@ -565,10 +565,11 @@ static int per_for(uint32_t K) {
 // creation): one block per (head, 256-entry chunk, share of a group of
 // aligned rows), grid (heads * chunks, M); groups of more than 3 rows are
 // split over two or three blocks (two blocks fit on a CU), so that the
-// chip's CUs share the work.  Batched passes of more than 8 rows (many
-// sequences of a few rows) take the per-row kernel.  Passes of at most 8 rows quantize and store
-// their own K/V rows inside the attention kernel (FUSED); taller passes have
-// them stored by k_kv_store_pass first.
+// chip's CUs share the work.  Batched passes of more than 8 rows take the
+// sequence-group kernel (rows in groups of 2-5 consecutive positions) or the
+// per-row kernel.  Passes of at most 8 rows quantize and store their own K/V
+// rows inside the attention kernel (FUSED); taller passes have them stored by
+// k_kv_store_pass first.
 static bool attn_fused(uint32_t M) { return M <= AG_MAX_ROWS; }
 static void launch_attn(hipStream_t st, uint32_t hd, uint32_t M, uint32_t tasks, const PassDesc* pd,
                         const KvGeom& g, const KvPlanes& kv, uint32_t l, const float* q, const float* k,
