@@ -123,11 +123,11 @@ static pf_status batch_mtp_chain(pf_engine* e, const float* h0, uint32_t n, cons
     const pf_model* m = e->m;
     const pf_model_desc& d = m->d;
     hipStream_t st = c->stream;
-    const uint32_t D = d.n_embd, V = d.n_vocab, R = d.n_mtp + 1, nd = n * D;
-    hipLaunchKernelGGL(k_copy_f32, dim3((nd + 255) / 256), dim3(256), 0, st, h0, e->mcur, nd);
+    const uint32_t D = d.n_embd, V = d.n_vocab, R = d.n_mtp + 1;
     for (uint32_t k = 0; k < d.n_mtp; k++) {
-        launch_gemv_f32_glu(st, m->mtp[k * 3 + 0], m->mtp[k * 3 + 1], n, e->mcur, D, e->ma, D);
-        launch_gemv_f32(st, m->mtp[k * 3 + 2], n, e->ma, D, e->mcur, D, e->mcur);
+        const float* hin = k == 0 ? h0 : e->mcur;   // head 0 reads the rows of h0 (stride d) itself
+        launch_gemv_f32_glu(st, m->mtp[k * 3 + 0], m->mtp[k * 3 + 1], n, hin, D, e->ma, D);
+        launch_gemv_f32(st, m->mtp[k * 3 + 2], n, e->ma, D, e->mcur, D, hin);
         launch_gemv_f32(st, m->emb, n, e->mcur, D, e->mlogb, V, nullptr);
         hipLaunchKernelGGL(k_bsample, dim3(n), dim3(1024), 0, st, (const float*)e->mlogb, V, V, cfg,
                            (const uint64_t*)e->seeds, e->st, (const uint32_t*)e->sel, 0u, e->tokens, e->tok_cap,

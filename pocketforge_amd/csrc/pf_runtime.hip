@@ -1232,7 +1232,7 @@ struct pf_engine {
     uint32_t prefill_rows = 8;    // rows of a prompt pass
     PassDesc pd_host{};           // staging of the prompt passes' descriptors
     float *logitsA = nullptr, *hiddenA = nullptr, *logitsB = nullptr, *hiddenB = nullptr;
-    float *mcur = nullptr, *mg = nullptr, *mu = nullptr, *ma = nullptr, *mlogits = nullptr;
+    float *mcur = nullptr, *ma = nullptr, *mlogits = nullptr;
     PassDesc *pdA = nullptr, *pdB = nullptr, *pdP = nullptr;
     DecodeState* st = nullptr;
     int32_t* tokens = nullptr;
@@ -1395,8 +1395,6 @@ static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t ns
     if (!s) s = ealloc(e, &e->logitsB, (size_t)MR * V);
     if (!s) s = ealloc(e, &e->hiddenB, (size_t)MR * D);
     if (!s) s = ealloc(e, &e->mcur, (size_t)nseq * D);
-    if (!s) s = ealloc(e, &e->mg, (size_t)nseq * D);
-    if (!s) s = ealloc(e, &e->mu, (size_t)nseq * D);
     if (!s) s = ealloc(e, &e->ma, (size_t)nseq * D);
     if (!s) s = ealloc(e, &e->mlogits, (size_t)std::max(1u, d.n_mtp) * V);
     if (!s) s = ealloc(e, &e->mlogb, (size_t)nseq * V);
@@ -1860,17 +1858,18 @@ extern "C" pf_status pf_forward(pf_engine* e, const int32_t* tokens, uint32_t n,
 
 // MTPHeads::forward chain on the device hidden state h0 (src/mtp.cpp:63-127):
 // gate, up, silu(gate) * up, down + residual, tied unembed, per head; with
-// `sample` the draft of head k is sampled right after its logits.
+// `sample` the draft of head k is sampled right after its logits.  Head 0
+// reads h0 itself; its down product writes the running row mcur.
 static pf_status mtp_chain(pf_engine* e, const float* h0, bool sample, const SamplingCfg* cfg, uint64_t seed) {
     pf_ctx* c = e->c;
     const pf_model* m = e->m;
     const pf_model_desc& d = m->d;
     hipStream_t st = c->stream;
     const uint32_t D = d.n_embd, V = d.n_vocab;
-    hipLaunchKernelGGL(k_copy_f32, dim3((D + 255) / 256), dim3(256), 0, st, h0, e->mcur, D);
     for (uint32_t k = 0; k < d.n_mtp; k++) {
-        launch_gemv_f32_glu(st, m->mtp[k * 3 + 0], m->mtp[k * 3 + 1], 1, e->mcur, D, e->ma, D);
-        launch_gemv_f32(st, m->mtp[k * 3 + 2], 1, e->ma, D, e->mcur, D, e->mcur);
+        const float* hin = k == 0 ? h0 : e->mcur;
+        launch_gemv_f32_glu(st, m->mtp[k * 3 + 0], m->mtp[k * 3 + 1], 1, hin, D, e->ma, D);
+        launch_gemv_f32(st, m->mtp[k * 3 + 2], 1, e->ma, D, e->mcur, D, hin);
         float* lk = e->mlogits + (size_t)k * V;
         launch_gemv_f32(st, m->emb, 1, e->mcur, D, lk, V, nullptr);
         if (sample)
