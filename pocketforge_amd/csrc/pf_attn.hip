@@ -866,8 +866,8 @@ constexpr uint32_t ag_smem(uint32_t nr) { return 2u * 256u * 128u + (512u + nr *
 // rows is served by ceil(n / NR) blocks of at most NR rows each.
 // Grid (heads * chunks, M), 256 threads: block (x, m) serves share
 // m - m0 of the group led by row m0 (if that share exists).  With pf.p set
-// the grid has one more row of blocks, which stream pf's bytes (the next
-// kernel's weights) through the cache hierarchy instead.
+// the grid has one more row of blocks, which load pf's groups (the next
+// kernel's weights) into the L2 of the XCDs that will read them instead.
 //
 // FUSED (passes of at most 8 rows): the pass's own K/V rows are not yet in
 // the cache.  Entries at positions of this pass are quantized here from the
@@ -885,7 +885,7 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
     constexpr uint32_t hd = 16 * PARTS;
     __shared__ __align__(16) uint8_t smem[ag_smem(NR)];
     if (blockIdx.y >= M) {
-        prefetch_bytes(pf.p, pf.n, blockIdx.x, gridDim.x, pf.sink);
+        prefetch_groups(pf, blockIdx.x + blockIdx.y * gridDim.x, blockIdx.x, gridDim.x);
         return;
     }
     int4* kt = reinterpret_cast<int4*>(smem);                       // [PARTS][256], swizzled
@@ -1326,7 +1326,7 @@ __global__ __launch_bounds__(1024) void k_attn_merge_quant(const PassDesc* __res
     __shared__ float red[16];
     const uint32_t m = blockIdx.x;
     if (m >= rows) {
-        prefetch_bytes(pf.p, pf.n, m - rows, gridDim.x - rows, pf.sink);
+        prefetch_groups(pf, m, m - rows, gridDim.x - rows);
         return;
     }
     if (m >= pd->m) return;

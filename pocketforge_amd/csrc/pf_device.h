@@ -233,30 +233,46 @@ __device__ __forceinline__ uint32_t kv_row(const KvGeom& g, const KvView& v, uin
 
 // ---------------------------------------------------------- prefetch
 
-// Streams bytes [p, p + n) (n a multiple of 16) through the cache hierarchy
-// so that the next kernel finds them in the MALL.  Block b of nb prefetching
-// blocks takes every nb-th stripe of blockDim.x * 16 bytes.  The loaded
-// words feed a value that is stored only if it equals a constant, so the
-// loads stay.
-__device__ __forceinline__ void prefetch_bytes(const uint8_t* __restrict__ p, size_t n, uint32_t b, uint32_t nb,
-                                               uint32_t* __restrict__ sink) {
-    const uint4* q = reinterpret_cast<const uint4*>(p);
-    const size_t n16 = n >> 4, stride = (size_t)nb * blockDim.x;
-    uint32_t x = 0;
-    size_t i = (size_t)b * blockDim.x + threadIdx.x;
-    for (; i + 3 * stride < n16; i += 4 * stride) {
-        const uint4 v0 = q[i], v1 = q[i + stride], v2 = q[i + 2 * stride], v3 = q[i + 3 * stride];
-        x ^= v0.x ^ v1.y ^ v2.z ^ v3.w;
-    }
-    for (; i < n16; i += stride) x ^= q[i].x;
-    if (x == 0x7A5C3E1Fu) sink[0] = x;
-}
-
+// The weights of the next kernel in the stream, loaded by extra blocks of
+// the current one so that the next kernel finds them in its L2.  The matrix
+// is stored as `groups` contiguous runs of `gbytes` bytes (the 32-row groups
+// of the tiled layout) and the next kernel's workgroup g reads group g.
+// Every dispatch deals its workgroups to the 8 XCDs round-robin from XCD 0
+// (workgroup b runs on XCD b mod 8, measured with the XCC_ID register on
+// consecutive dispatches and graph replays), and each XCD has its own L2:
+// group g is wanted in the L2 of XCD g mod 8.
 struct Prefetch {
-    const uint8_t* p;   // bytes the next kernel reads first (null: none)
-    size_t n;
+    const uint8_t* p;   // null: nothing to prefetch
+    uint32_t gbytes;    // bytes per group, a multiple of 16
+    uint32_t groups;
+    uint32_t blocks;    // prefetch workgroups a GEMV launch adds to its grid
     uint32_t* sink;
 };
+
+// Prefetch block x of T, whose linear block id is lin (the prefetch blocks
+// of a launch have consecutive ids), loads the groups g = lin mod 8 (mod 8)
+// into its XCD's L2, sharing them with the other prefetch blocks of that
+// XCD (those with the same x mod 8).  The loaded words feed a value that is
+// stored only if it equals a constant, so the loads stay.
+__device__ __forceinline__ void prefetch_groups(const Prefetch& pf, uint32_t lin, uint32_t x, uint32_t T) {
+    const uint32_t xcd = lin & 7u;
+    if (!pf.p || xcd >= pf.groups) return;
+    const uint32_t rank = x >> 3, cnt = (T - (x & 7u) + 7u) >> 3;
+    const uint32_t gb16 = pf.gbytes >> 4, n16 = ((pf.groups - xcd + 7u) >> 3) * gb16;
+    const uint32_t stride = cnt * blockDim.x;
+    const uint4* q = reinterpret_cast<const uint4*>(pf.p);
+    uint32_t acc = 0;
+    for (uint32_t u = rank * blockDim.x + threadIdx.x; u < n16; u += 4u * stride) {
+        uint4 v[4];
+#pragma unroll
+        for (uint32_t k = 0; k < 4; k++) {
+            const uint32_t w = min(u + k * stride, n16 - 1u), i = w / gb16;   // i-th group of this XCD
+            v[k] = q[(size_t)(xcd + 8u * i) * gb16 + (w - i * gb16)];
+        }
+        acc ^= v[0].x ^ v[1].y ^ v[2].z ^ v[3].w;
+    }
+    if (acc == 0x7A5C3E1Fu) pf.sink[0] = acc;
+}
 
 // ------------------------------------------------------ quantized rows
 

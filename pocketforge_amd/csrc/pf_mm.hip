@@ -162,6 +162,7 @@ struct GemvArgs {
     uint32_t cstride;
     KvGeom g;                  // MERGE: chunk count of row 0's list
     MmEpi e;
+    Prefetch nx;               // the next product's weights: nx.blocks more workgroups load them
 };
 
 // Dynamic LDS of k_gemv (bytes), laid out as: fp64 partials [waves][64][4],
@@ -187,9 +188,10 @@ __device__ __forceinline__ float max4abs(float4 v) {
     return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 }
 
-// Grid N / 32 (one 32-row group per workgroup), 64 * GEMV_WAVES threads,
-// gemv_smem(M, K) bytes of dynamic LDS.  K % 256 == 0, K <= 1024 CPW
-// (CPW chunks of 256 columns per wave, held in registers), M <= MR <= 8.
+// Grid N / 32 (one 32-row group per workgroup) + nx.blocks prefetch
+// workgroups, 64 * GEMV_WAVES threads, gemv_smem(M, K) bytes of dynamic LDS.
+// K % 256 == 0, K <= 1024 CPW (CPW chunks of 256 columns per wave, held in
+// registers), M <= MR <= 8.
 //
 // The workgroup first loads everything its prologue needs, then its weight
 // words (wave w takes chunks [nch w / W, nch (w + 1) / W)), then the
@@ -216,6 +218,10 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void k_gemv(GemvArgs a) {
     constexpr uint32_t TB = g32_tile_bytes(FMT), CODES = g32_code_bytes(FMT);
     constexpr int SETS = sets_of<FMT>();
     constexpr uint32_t NT = 64u * GEMV_WAVES;
+    if (blockIdx.x >= (a.N >> 5)) {   // workgroups past the groups prefetch the next product's weights
+        prefetch_groups(a.nx, blockIdx.x, blockIdx.x - (a.N >> 5), gridDim.x - (a.N >> 5));
+        return;
+    }
     if constexpr (GATED)
         if (*a.gate == 0u) return;   // no row of the pass needs this product
     extern __shared__ __align__(16) uint8_t smem[];

@@ -396,11 +396,11 @@ static void gemv_one(hipStream_t st, const GemvArgs& a, hipEvent_t ev0, hipEvent
                                   hipFuncAttributeMaxDynamicSharedMemorySize, gemv_smem(GEMV_MAX_M, 8192));
         attr = true;
     }
+    const dim3 grid(a.N / 32 + (a.nx.p ? a.nx.blocks : 0u));
     if (ev0)
-        hipExtLaunchKernelGGL((k_gemv<F, PRO, EPI, G, CPW, MR>), dim3(a.N / 32), dim3(64 * GEMV_WAVES), smem, st, ev0,
-                              ev1, 0, a);
+        hipExtLaunchKernelGGL((k_gemv<F, PRO, EPI, G, CPW, MR>), grid, dim3(64 * GEMV_WAVES), smem, st, ev0, ev1, 0, a);
     else
-        hipLaunchKernelGGL((k_gemv<F, PRO, EPI, G, CPW, MR>), dim3(a.N / 32), dim3(64 * GEMV_WAVES), smem, st, a);
+        hipLaunchKernelGGL((k_gemv<F, PRO, EPI, G, CPW, MR>), grid, dim3(64 * GEMV_WAVES), smem, st, a);
 }
 
 // Rows held in registers: 1 (base passes), 5 (verify passes of four
@@ -1253,7 +1253,8 @@ struct pf_engine {
     uint32_t pool_rows_max = 1;
     bool hidden_valid = false;
     size_t max_memory = 0;
-    uint32_t pf_blocks = 128;     // blocks of the attention merge that stream the O weights (PF_PREFETCH_BLOCKS)
+    uint32_t pf_blocks = 128;     // blocks of the attention merge that prefetch the O weights (PF_PREFETCH_BLOCKS)
+    uint32_t l2_blocks = 64;      // blocks of a decode GEMV that prefetch the next product's weights (PF_L2_BLOCKS)
     uint32_t* sink = nullptr;     // 4 bytes the prefetch loops never write in practice
     bool mtp_enabled = true;      // ModelConfig::mtp_enabled, include/forge/types.hpp
     // layer skip (LayerSkipController, src/layer_skip.cpp): on while the
@@ -1379,6 +1380,7 @@ static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t ns
     e->s_stride = 2 * ((cmax + 1 + 255) / 256) + 8;    // per (row, head): chunk max and sum
     e->cstride = (cmax + 1 + 255) / 256 + 1;          // per (row, head): chunk partials
     if (const char* v = std::getenv("PF_PREFETCH_BLOCKS")) e->pf_blocks = (uint32_t)std::strtoul(v, nullptr, 10);
+    if (const char* v = std::getenv("PF_L2_BLOCKS")) e->l2_blocks = 8u * ((uint32_t)std::strtoul(v, nullptr, 10) / 8u);
     if (!s) s = ealloc(e, &e->sink, 1);
     if (!s) s = ealloc(e, &e->x, (size_t)PR * D);
     if (!s) s = ealloc(e, &e->act, (size_t)PR * e->kmax);
@@ -1660,9 +1662,17 @@ static pf_status pass_mm(pf_engine* e, const pf_matrix* W, MmKind kind, uint32_t
     return PF_OK;
 }
 
-static Prefetch prefetch_of(const pf_engine* e, const pf_matrix* W) {
-    if (!e->pf_blocks) return Prefetch{nullptr, 0, e->sink};
-    return Prefetch{W->data, W->bytes & ~(size_t)15, e->sink};
+// The tiled matrix W as the next kernel's weights, loaded into the L2 of
+// the XCD whose workgroups read each group by `blocks` prefetch blocks of
+// the current kernel (none when blocks is 0 or W is not tiled).
+static bool prefetchable(const pf_matrix* W) {
+    const uint32_t groups = W ? W->rows / 32 : 0u;
+    return W && !W->rowmajor && groups && W->bytes % groups == 0 && (W->bytes / groups) % 16 == 0;
+}
+static Prefetch prefetch_of(const pf_engine* e, const pf_matrix* W, uint32_t blocks) {
+    if (!blocks || !prefetchable(W)) return Prefetch{nullptr, 0, 0, 0, e->sink};
+    const uint32_t groups = W->rows / 32;
+    return Prefetch{W->data, (uint32_t)(W->bytes / groups), groups, blocks, e->sink};
 }
 
 // LayerSkipController's threshold for layer l (src/layer_skip.cpp:43-55):
@@ -1761,20 +1771,23 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
             e->aev_used++;
         }
         // one-row passes merge the chunks in the O product's prologue, and the
-        // attention's extra blocks stream the O weights through the cache
-        // hierarchy; other passes run the merge kernel, whose extra blocks do
+        // attention's extra blocks load the O weights into the L2 of the XCDs
+        // whose O workgroups read them; other passes run the merge kernel,
+        // whose extra blocks do.  Each decode GEMV's extra blocks do the same
+        // for the next product (O -> gate|up -> down -> next layer's QKV).
         launch_attn(st, hd, M, attn_tasks, pd, g, e->kv, l, e->q, e->k, e->v, e->S, e->s_stride, e->Wp,
-                    e->cstride, merge_in_o ? prefetch_of(e, m->o[l]) : Prefetch{nullptr, 0, e->sink}, batch,
+                    e->cstride, merge_in_o ? prefetch_of(e, m->o[l], e->pf_blocks) : prefetch_of(e, nullptr, 0), batch,
                     batch ? e->batch_group : 0u, aev0, aev1);
         if (!merge_in_o)
             PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_attn_merge_quant<PER>, dim3(M + e->pf_blocks), dim3(1024), 0, st,
                                                     pd, g, (const float*)e->S, e->s_stride, (const float*)e->Wp,
                                                     e->cstride, e->act, ks, as1, (int32_t*)nullptr, 0u, M,
-                                                    prefetch_of(e, m->o[l])));
+                                                    prefetch_of(e, m->o[l], e->pf_blocks)));
         // O projection + residual (src/engine.cpp:789-800)
         a = GemvArgs{};
         a.a8 = e->act; a.a8s = as1; a.xs = ks;
         a.e.y = e->x; a.e.y_stride = D;
+        a.nx = prefetch_of(e, m->gu[l], e->l2_blocks);
         if (merge_in_o) {
             a.S = e->S; a.s_stride = e->s_stride; a.Up = e->Wp; a.cstride = e->cstride; a.g = g;
             a.e.pd = pd; a.e.hd = hd; a.e.D = D;
@@ -1786,6 +1799,7 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         a = GemvArgs{};
         a.e.y = e->sg; a.e.y_stride = F;
         a.e.pmax = tall ? nullptr : e->pmax;
+        a.nx = prefetch_of(e, m->down[l], e->l2_blocks);
         if (e->skip_on) {
             float* nout = e->skip_stage + (size_t)l * e->rows * D;
             PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_norm_rows<PER>, dim3(M), dim3(1024), 0, st, (const float*)e->x, D,
@@ -1810,6 +1824,7 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         a = GemvArgs{};
         a.x = e->sg; a.xs = F; a.pin = e->pmax; a.np = 2 * F / 32;
         a.e.y = e->x; a.e.y_stride = D;
+        a.nx = prefetch_of(e, l + 1 < d.n_layers ? m->qkv[l + 1] : nullptr, e->l2_blocks);
         if (e->skip_on) {
             a.gate = e->skip_nrun + l;
             a.e.skipm = e->skip_flags + (size_t)l * e->rows;
