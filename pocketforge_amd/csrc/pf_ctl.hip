@@ -37,7 +37,30 @@ __device__ ArgBest block_argmax(const float* __restrict__ x, uint32_t V) {
     __shared__ float sv[16];
     __shared__ int32_t si[16];
     ArgBest b{-__builtin_inff(), 0x7FFFFFFF};
-    for (uint32_t i = threadIdx.x; i < V; i += blockDim.x) b = arg_better(b, ArgBest{x[i], (int32_t)i});
+    // 16-byte loads, four per thread in flight (the whole row at V = 16384),
+    // then the elements past the last aligned quad; arg_better picks the
+    // same element in any order
+    const uint32_t V4 = ((uintptr_t)x & 15u) == 0u ? V / 4u : 0u;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    for (uint32_t i0 = threadIdx.x; i0 < V4; i0 += 4u * blockDim.x) {
+        float4 v[4];
+#pragma unroll
+        for (uint32_t u = 0; u < 4; u++) {
+            const uint32_t i = i0 + u * blockDim.x;
+            v[u] = x4[i < V4 ? i : V4 - 1u];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 4; u++) {
+            const uint32_t i = i0 + u * blockDim.x;
+            if (i < V4) {
+                b = arg_better(b, ArgBest{v[u].x, (int32_t)(4u * i)});
+                b = arg_better(b, ArgBest{v[u].y, (int32_t)(4u * i + 1u)});
+                b = arg_better(b, ArgBest{v[u].z, (int32_t)(4u * i + 2u)});
+                b = arg_better(b, ArgBest{v[u].w, (int32_t)(4u * i + 3u)});
+            }
+        }
+    }
+    for (uint32_t i = 4u * V4 + threadIdx.x; i < V; i += blockDim.x) b = arg_better(b, ArgBest{x[i], (int32_t)i});
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
         ArgBest o{__shfl_xor(b.v, off, 64), __shfl_xor(b.i, off, 64)};
@@ -279,11 +302,19 @@ __global__ __launch_bounds__(1024) void k_sample(const float* __restrict__ logit
     __shared__ uint32_t skip;
     if (threadIdx.x == 0)
         skip = (role == ROLE_CORRECTIVE && (st->round_acc >= st->n_mtp || st->more)) ? 1u : 0u;
-    __syncthreads();
-    if (skip) return;
+    // a row given by the caller is ranked while thread 0 reads the skip
+    // condition; a row chosen by the round's acceptance waits for it
+    if (row < 0) {
+        __syncthreads();
+        if (skip) return;
+    }
     const uint32_t r = row >= 0 ? (uint32_t)row : st->round_acc;
     bool used = false;
     const int32_t t = sample_row(logits + (size_t)r * stride, V, cfg, seed, st->draw, &used);
+    if (row >= 0) {
+        __syncthreads();
+        if (skip) return;
+    }
     if (threadIdx.x != 0) return;
     if (used) st->draw++;
     switch (role) {

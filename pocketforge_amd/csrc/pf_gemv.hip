@@ -42,7 +42,8 @@ __device__ __forceinline__ void stage_rows(const float* __restrict__ h, uint32_t
 // y[m][n] (+= y_in[m][n] when resid) = canonical fp32 dot of h[m] with row n:
 // lane l holds block l (K <= 2048), fmaf chain over the block's elements,
 // halving tree over the 64 lanes.  Each wave walks rows n = wave, wave +
-// total_waves, ...
+// total_waves, ..., loading the codes and scales of RB rows before their
+// products (the tied unembedding gives each wave 8 rows).
 template <int M>
 __global__ __launch_bounds__(256) void k_gemv_f32(const uint8_t* __restrict__ codes,
                                                   const uint16_t* __restrict__ scales,
@@ -57,33 +58,49 @@ __global__ __launch_bounds__(256) void k_gemv_f32(const uint8_t* __restrict__ co
     const bool live = lane < nb;
     float hv[M][32];
     stage_rows<M>(h, h_stride, K, lane, live, hv);
-    for (uint32_t n = wave; n < N; n += nwaves) {
-        float acc[M];
+    constexpr uint32_t RB = M == 1 ? 8u : (M <= 4 ? 4u : 2u);
+    for (uint32_t n0 = wave; n0 < N; n0 += RB * nwaves) {
+        uint4 cr[RB];
+        float dr[RB];
 #pragma unroll
-        for (int m = 0; m < M; m++) acc[m] = 0.0f;
-        if (live) {
-            uint4 c = *reinterpret_cast<const uint4*>(codes + ((size_t)n * nb + lane) * 16u);
-            float d = h2f(scales[(size_t)n * nb + lane]);
-            float nd = -8.0f * d;
-            uint32_t cw[4] = {c.x, c.y, c.z, c.w};
-#pragma unroll
-            for (int j = 0; j < 16; j++) {
-                uint32_t byte = (cw[j >> 2] >> (8 * (j & 3))) & 0xFFu;
-                float w0 = __builtin_fmaf((float)(byte & 15u), d, nd);
-                float w1 = __builtin_fmaf((float)(byte >> 4), d, nd);
-#pragma unroll
-                for (int m = 0; m < M; m++) {
-                    acc[m] = __builtin_fmaf(hv[m][2 * j], w0, acc[m]);
-                    acc[m] = __builtin_fmaf(hv[m][2 * j + 1], w1, acc[m]);
-                }
+        for (uint32_t q = 0; q < RB; q++) {
+            const uint32_t n = n0 + q * nwaves;
+            cr[q] = make_uint4(0u, 0u, 0u, 0u);
+            dr[q] = 0.0f;
+            if (live && n < N) {
+                cr[q] = *reinterpret_cast<const uint4*>(codes + ((size_t)n * nb + lane) * 16u);
+                dr[q] = h2f(scales[(size_t)n * nb + lane]);
             }
         }
 #pragma unroll
-        for (int m = 0; m < M; m++) {
-            float t = wave_tree_sum(acc[m]);
-            if (lane == 0) {
-                size_t o = (size_t)m * y_stride + n;
-                y[o] = y_in ? (y_in[o] + t) : t;
+        for (uint32_t q = 0; q < RB; q++) {
+            const uint32_t n = n0 + q * nwaves;
+            if (n >= N) break;
+            float acc[M];
+#pragma unroll
+            for (int m = 0; m < M; m++) acc[m] = 0.0f;
+            if (live) {
+                const float d = dr[q], nd = -8.0f * d;
+                const uint32_t cw[4] = {cr[q].x, cr[q].y, cr[q].z, cr[q].w};
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    uint32_t byte = (cw[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+                    float w0 = __builtin_fmaf((float)(byte & 15u), d, nd);
+                    float w1 = __builtin_fmaf((float)(byte >> 4), d, nd);
+#pragma unroll
+                    for (int m = 0; m < M; m++) {
+                        acc[m] = __builtin_fmaf(hv[m][2 * j], w0, acc[m]);
+                        acc[m] = __builtin_fmaf(hv[m][2 * j + 1], w1, acc[m]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                float t = wave_tree_sum(acc[m]);
+                if (lane == 0) {
+                    size_t o = (size_t)m * y_stride + n;
+                    y[o] = y_in ? (y_in[o] + t) : t;
+                }
             }
         }
     }
