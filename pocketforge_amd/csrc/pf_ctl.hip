@@ -119,8 +119,10 @@ static_assert(sizeof(SampleSort::storage_type) <= SAMPLE_MAX_V * sizeof(uint64_t
 // a stable ascending sort of ~ord(x) over the indices in ascending order,
 // so equal logits keep ascending indices.  Slots past V hold ~0 keys and
 // sort last.  1024 threads; `a` doubles as the sort's scratch.
-__device__ uint32_t sort_desc(const float* __restrict__ x, uint32_t V, uint64_t* a) {
-    uint32_t key[SAMPLE_IPT], idx[SAMPLE_IPT];
+// The sort itself, leaving sorted positions 16 t .. 16 t + 15 in thread t's
+// registers (`a` is the sort's scratch, free again after the call).
+__device__ void sort_desc_regs(const float* __restrict__ x, uint32_t V, uint64_t* a, uint32_t (&key)[SAMPLE_IPT],
+                               uint32_t (&idx)[SAMPLE_IPT]) {
 #pragma unroll
     for (uint32_t j = 0; j < SAMPLE_IPT; j++) {
         const uint32_t i = threadIdx.x * SAMPLE_IPT + j;
@@ -129,6 +131,11 @@ __device__ uint32_t sort_desc(const float* __restrict__ x, uint32_t V, uint64_t*
     }
     SampleSort().sort(key, idx, *reinterpret_cast<SampleSort::storage_type*>(a));
     __syncthreads();
+}
+
+__device__ uint32_t sort_desc(const float* __restrict__ x, uint32_t V, uint64_t* a) {
+    uint32_t key[SAMPLE_IPT], idx[SAMPLE_IPT];
+    sort_desc_regs(x, V, a, key, idx);
 #pragma unroll
     for (uint32_t j = 0; j < SAMPLE_IPT; j++)
         a[threadIdx.x * SAMPLE_IPT + j] = ((uint64_t)key[j] << 32) | idx[j];
@@ -142,18 +149,28 @@ __device__ __forceinline__ float key_val(uint64_t k) {
     return __uint_as_float(u);
 }
 
-// Chunk-of-64 sum and scan over p[0..n) held in the high words of `a`
-// (float bits) by wave 0: chunk totals left to right, running prefix from
-// the chunk's offset.  Returns the first index with cum >= thr1 (or n) and
-// the first index with thr2 <= cum (or n).  Valid in wave 0.
+// Chunk-of-64 sum and scan (the canonical order of the oracle's sampler):
+// element s of n belongs to chunk L = s / cl (cl = ceil(n / 64)); each chunk
+// is summed left to right from 0, the chunk totals left to right; the scan
+// runs from the chunk's offset (the totals before it, left to right).  The
+// scan returns the first index with cum >= thr1 (or n) and the first index
+// with thr2 <= cum (or n).
 struct ScanHit { uint32_t first_ge1, first_ge2; };
 
-__device__ __forceinline__ float slot_f(uint64_t k) { return __uint_as_float((uint32_t)(k >> 32)); }
-
-__device__ float chunk64_total(const uint64_t* a, uint32_t n, float* tot_lds) {
-    const uint32_t lane = threadIdx.x, cl = (n + 63u) / 64u;
+// The values live transposed in LDS: element s at (s - L cl) * 64 + L, so
+// that the 64 lanes of wave 0, one per chunk, read consecutive words (in the
+// plain layout every lane's word falls in the same bank).
+__device__ __forceinline__ uint32_t tpos(uint32_t s, uint32_t cl) {
+    const uint32_t L = s / cl;
+    return (s - L * cl) * 64u + L;
+}
+__device__ __forceinline__ uint32_t chunk_len(uint32_t lane, uint32_t n, uint32_t cl) {
+    return lane * cl < n ? min(cl, n - lane * cl) : 0u;
+}
+__device__ float chunk64_total_t(const float* P, uint32_t n, float* tot_lds) {
+    const uint32_t lane = threadIdx.x, cl = (n + 63u) / 64u, len = chunk_len(lane, n, cl);
     float t = 0.0f;
-    for (uint32_t i = lane * cl; i < n && i < (lane + 1) * cl; i++) t = t + slot_f(a[i]);
+    for (uint32_t o = 0; o < len; o++) t = t + P[o * 64u + lane];
     tot_lds[lane] = t;
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -161,11 +178,10 @@ __device__ float chunk64_total(const uint64_t* a, uint32_t n, float* tot_lds) {
     for (uint32_t b = 0; b < 64; b++) s = s + tot_lds[b];
     return s;
 }
-
-__device__ ScanHit chunk64_scan(const uint64_t* a, uint32_t n, float thr1, float thr2, float* tot_lds) {
-    const uint32_t lane = threadIdx.x, cl = (n + 63u) / 64u;
+__device__ ScanHit chunk64_scan_t(const float* P, uint32_t n, float thr1, float thr2, float* tot_lds) {
+    const uint32_t lane = threadIdx.x, cl = (n + 63u) / 64u, len = chunk_len(lane, n, cl);
     float t = 0.0f;
-    for (uint32_t i = lane * cl; i < n && i < (lane + 1) * cl; i++) t = t + slot_f(a[i]);
+    for (uint32_t o = 0; o < len; o++) t = t + P[o * 64u + lane];
     tot_lds[lane] = t;
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -173,10 +189,10 @@ __device__ ScanHit chunk64_scan(const uint64_t* a, uint32_t n, float thr1, float
     for (uint32_t b = 0; b < lane; b++) off = off + tot_lds[b];
     uint32_t h1 = n, h2 = n;
     float c = off;
-    for (uint32_t i = lane * cl; i < n && i < (lane + 1) * cl; i++) {
-        c = c + slot_f(a[i]);
-        if (h1 == n && c >= thr1) h1 = i;
-        if (h2 == n && thr2 <= c) h2 = i;
+    for (uint32_t o = 0; o < len; o++) {
+        c = c + P[o * 64u + lane];
+        if (h1 == n && c >= thr1) h1 = lane * cl + o;
+        if (h2 == n && thr2 <= c) h2 = lane * cl + o;
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
@@ -200,32 +216,46 @@ __device__ int32_t sample_row(const float* __restrict__ x, uint32_t V, const Sam
     const float r = uniform(seed, draw);
     int32_t result = 0;
     if (cfg.top_p < 1.0f && cfg.top_p > 0.0f) {            // src/engine.cpp:961-1003
-        sort_desc(x, V, arena);
-        const float mx = key_val(arena[0]);
-        __syncthreads();   // every thread has read slot 0 before it is rewritten
-        for (uint32_t i = threadIdx.x; i < V; i += blockDim.x) {
-            uint64_t k = arena[i];
-            float p = expf_c((key_val(k) - mx) / temp);
-            arena[i] = ((uint64_t)__float_as_uint(p) << 32) | (uint32_t)k;
+        // sorted positions 16 t + j in thread t's registers; then the
+        // probabilities of the sorted order in the transposed chunk layout
+        // P (at most 16,448 words) and the sorted indices IX (16-bit, V <=
+        // 16384) in the arena
+        uint32_t key[SAMPLE_IPT], idx[SAMPLE_IPT];
+        sort_desc_regs(x, V, arena, key, idx);
+        float* P = reinterpret_cast<float*>(arena);
+        uint16_t* IX = reinterpret_cast<uint16_t*>(P + SAMPLE_MAX_V + 64u);
+        const uint32_t cl = (V + 63u) / 64u;
+        if (threadIdx.x == 0) bcast[1] = key_val(((uint64_t)key[0]) << 32);
+        __syncthreads();
+        const float mx = bcast[1];
+        float pv[SAMPLE_IPT];
+#pragma unroll
+        for (uint32_t j = 0; j < SAMPLE_IPT; j++) {
+            const uint32_t sp = threadIdx.x * SAMPLE_IPT + j;
+            pv[j] = expf_c((key_val(((uint64_t)key[j]) << 32) - mx) / temp);
+            if (sp < V) {
+                P[tpos(sp, cl)] = pv[j];
+                IX[sp] = (uint16_t)idx[j];
+            }
         }
         __syncthreads();
         if (threadIdx.x < 64) {
-            float sum = chunk64_total(arena, V, tot);
+            float sum = chunk64_total_t(P, V, tot);
             if (threadIdx.x == 0) bcast[0] = sum;
         }
         __syncthreads();
         const float sum = bcast[0];
-        for (uint32_t i = threadIdx.x; i < V; i += blockDim.x) {
-            uint64_t k = arena[i];
-            float p = slot_f(k) / sum;
-            arena[i] = ((uint64_t)__float_as_uint(p) << 32) | (uint32_t)k;
+#pragma unroll
+        for (uint32_t j = 0; j < SAMPLE_IPT; j++) {
+            const uint32_t sp = threadIdx.x * SAMPLE_IPT + j;
+            if (sp < V) P[tpos(sp, cl)] = pv[j] / sum;
         }
         __syncthreads();
         if (threadIdx.x < 64) {
-            ScanHit h = chunk64_scan(arena, V, cfg.top_p, r, tot);
+            ScanHit h = chunk64_scan_t(P, V, cfg.top_p, r, tot);
             uint32_t cutoff = h.first_ge1 < V ? h.first_ge1 + 1 : V;
             uint32_t pick = h.first_ge2 < cutoff ? h.first_ge2 : cutoff - 1;
-            if (threadIdx.x == 0) result = (int32_t)(uint32_t)arena[pick];
+            if (threadIdx.x == 0) result = (int32_t)IX[pick];
         }
     } else if (cfg.top_k > 0 && cfg.top_k < V) {           // src/engine.cpp:930-959
         sort_desc(x, V, arena);
@@ -250,28 +280,33 @@ __device__ int32_t sample_row(const float* __restrict__ x, uint32_t V, const Sam
             __syncthreads();
             mx = bcast[1];
         }
-        for (uint32_t i = threadIdx.x; i < V; i += blockDim.x) {
-            float p = expf_c((x[i] - mx) / temp);
-            arena[i] = ((uint64_t)__float_as_uint(p) << 32) | i;
+        // index order: element i = t + 1024 k in thread t's registers and in
+        // the transposed chunk layout
+        const uint32_t cl = (V + 63u) / 64u;
+        float pv[SAMPLE_IPT];
+#pragma unroll
+        for (uint32_t k = 0; k < SAMPLE_IPT; k++) {
+            const uint32_t i = threadIdx.x + 1024u * k;
+            pv[k] = i < V ? expf_c((x[i] - mx) / temp) : 0.0f;
+            if (i < V) fa[tpos(i, cl)] = pv[k];
         }
         __syncthreads();
         if (threadIdx.x < 64) {
-            float sum = chunk64_total(arena, V, tot);
+            float sum = chunk64_total_t(fa, V, tot);
             if (threadIdx.x == 0) bcast[0] = sum;
         }
         __syncthreads();
         const float sum = bcast[0];
-        for (uint32_t i = threadIdx.x; i < V; i += blockDim.x) {
-            uint64_t k = arena[i];
-            float p = slot_f(k) / sum;
-            arena[i] = ((uint64_t)__float_as_uint(p) << 32) | (uint32_t)k;
+#pragma unroll
+        for (uint32_t k = 0; k < SAMPLE_IPT; k++) {
+            const uint32_t i = threadIdx.x + 1024u * k;
+            if (i < V) fa[tpos(i, cl)] = pv[k] / sum;
         }
         __syncthreads();
         if (threadIdx.x < 64) {
-            ScanHit h = chunk64_scan(arena, V, 2.0f, r, tot);
+            ScanHit h = chunk64_scan_t(fa, V, 2.0f, r, tot);
             if (threadIdx.x == 0) result = h.first_ge2 < V ? (int32_t)h.first_ge2 : (int32_t)V - 1;
         }
-        (void)fa;
     }
     __syncthreads();
     return result;
