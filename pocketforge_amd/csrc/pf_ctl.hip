@@ -164,6 +164,20 @@ __device__ __forceinline__ uint32_t tpos(uint32_t s, uint32_t cl) {
     const uint32_t L = s / cl;
     return (s - L * cl) * 64u + L;
 }
+// tpos for s = s0 + j (j < 16) from the chunk of s0, cl >= 16: consecutive
+// positions cross at most one chunk boundary.
+__device__ __forceinline__ uint32_t tpos_next(uint32_t s, uint32_t L0, uint32_t cl) {
+    const uint32_t L = s >= (L0 + 1u) * cl ? L0 + 1u : L0;
+    return (s - L * cl) * 64u + L;
+}
+// Chunk of element s with a float reciprocal of cl, corrected to the exact
+// quotient (s < 2^24).
+__device__ __forceinline__ uint32_t tpos_r(uint32_t s, uint32_t cl, float rcl) {
+    uint32_t L = (uint32_t)((float)s * rcl);
+    L -= L * cl > s ? 1u : 0u;
+    L += (L + 1u) * cl <= s ? 1u : 0u;
+    return (s - L * cl) * 64u + L;
+}
 __device__ __forceinline__ uint32_t chunk_len(uint32_t lane, uint32_t n, uint32_t cl) {
     return lane * cl < n ? min(cl, n - lane * cl) : 0u;
 }
@@ -228,13 +242,20 @@ __device__ int32_t sample_row(const float* __restrict__ x, uint32_t V, const Sam
         if (threadIdx.x == 0) bcast[1] = key_val(((uint64_t)key[0]) << 32);
         __syncthreads();
         const float mx = bcast[1];
+        // this thread's positions' slots in P (one division per thread)
+        uint32_t ps[SAMPLE_IPT];
+        {
+            const uint32_t s0 = threadIdx.x * SAMPLE_IPT, L0 = s0 / cl;
+#pragma unroll
+            for (uint32_t j = 0; j < SAMPLE_IPT; j++) ps[j] = cl >= SAMPLE_IPT ? tpos_next(s0 + j, L0, cl) : tpos(s0 + j, cl);
+        }
         float pv[SAMPLE_IPT];
 #pragma unroll
         for (uint32_t j = 0; j < SAMPLE_IPT; j++) {
             const uint32_t sp = threadIdx.x * SAMPLE_IPT + j;
             pv[j] = expf_c((key_val(((uint64_t)key[j]) << 32) - mx) / temp);
             if (sp < V) {
-                P[tpos(sp, cl)] = pv[j];
+                P[ps[j]] = pv[j];
                 IX[sp] = (uint16_t)idx[j];
             }
         }
@@ -248,7 +269,7 @@ __device__ int32_t sample_row(const float* __restrict__ x, uint32_t V, const Sam
 #pragma unroll
         for (uint32_t j = 0; j < SAMPLE_IPT; j++) {
             const uint32_t sp = threadIdx.x * SAMPLE_IPT + j;
-            if (sp < V) P[tpos(sp, cl)] = pv[j] / sum;
+            if (sp < V) P[ps[j]] = pv[j] / sum;
         }
         __syncthreads();
         if (threadIdx.x < 64) {
@@ -283,12 +304,15 @@ __device__ int32_t sample_row(const float* __restrict__ x, uint32_t V, const Sam
         // index order: element i = t + 1024 k in thread t's registers and in
         // the transposed chunk layout
         const uint32_t cl = (V + 63u) / 64u;
+        const float rcl = 1.0f / (float)cl;
+        uint32_t ps[SAMPLE_IPT];
         float pv[SAMPLE_IPT];
 #pragma unroll
         for (uint32_t k = 0; k < SAMPLE_IPT; k++) {
             const uint32_t i = threadIdx.x + 1024u * k;
+            ps[k] = tpos_r(i, cl, rcl);
             pv[k] = i < V ? expf_c((x[i] - mx) / temp) : 0.0f;
-            if (i < V) fa[tpos(i, cl)] = pv[k];
+            if (i < V) fa[ps[k]] = pv[k];
         }
         __syncthreads();
         if (threadIdx.x < 64) {
@@ -300,7 +324,7 @@ __device__ int32_t sample_row(const float* __restrict__ x, uint32_t V, const Sam
 #pragma unroll
         for (uint32_t k = 0; k < SAMPLE_IPT; k++) {
             const uint32_t i = threadIdx.x + 1024u * k;
-            if (i < V) fa[tpos(i, cl)] = pv[k] / sum;
+            if (i < V) fa[ps[k]] = pv[k] / sum;
         }
         __syncthreads();
         if (threadIdx.x < 64) {
@@ -328,12 +352,13 @@ __device__ __forceinline__ void push_token(DecodeState* st, int32_t* tokens, uin
     st->cur = t;
 }
 
-// One Engine::sample call.  Row `row` of `logits` (row < 0: the verify row
-// of the first mismatch, st->round_acc).  Grid 1, 1024 threads.
+// One Engine::sample call outside the round's first samples (the
+// corrective, the single-token fallback, a plain call).  Row `row` of
+// `logits` (row < 0: the verify row of the first mismatch, st->round_acc).
+// Grid 1, 1024 threads.
 __global__ __launch_bounds__(1024) void k_sample(const float* __restrict__ logits, uint32_t stride, int32_t row,
                                                  uint32_t V, SamplingCfg cfg, uint64_t seed, DecodeState* st,
-                                                 int32_t* tokens, uint32_t cap, PassDesc* pdB, int32_t role,
-                                                 int32_t k, int32_t* out) {
+                                                 int32_t* tokens, uint32_t cap, int32_t role, int32_t* out) {
     __shared__ uint32_t skip;
     if (threadIdx.x == 0)
         skip = (role == ROLE_CORRECTIVE && (st->round_acc >= st->n_mtp || st->more)) ? 1u : 0u;
@@ -353,20 +378,6 @@ __global__ __launch_bounds__(1024) void k_sample(const float* __restrict__ logit
     if (threadIdx.x != 0) return;
     if (used) st->draw++;
     switch (role) {
-        case ROLE_T1:   // k: rows of the first verify segment
-            push_token(st, tokens, cap, t);
-            pdB->tok[0] = t;
-            pdB->pos0 = st->pos;
-            pdB->m = (uint32_t)k;
-            pdB->batch = 0;
-            pdB->seq0 = 0;
-            st->seg_k0 = 0;
-            st->more = 0;
-            break;
-        case ROLE_DRAFT:
-            st->draft[k] = t;
-            pdB->tok[k + 1] = t;
-            break;
         case ROLE_CORRECTIVE: {
             uint32_t a = st->round_acc;
             uint32_t pushed = 0;
@@ -379,6 +390,47 @@ __global__ __launch_bounds__(1024) void k_sample(const float* __restrict__ logit
             break;
         default:
             if (out) *out = t;
+    }
+}
+
+// The first samples of an MTP round in one launch: block 0 samples T1 from
+// the base row (ROLE_T1: pushed, row 0 of the verify pass, `h` rows in its
+// first segment), block 1 + k the draft of head k from its logits
+// (ROLE_DRAFT), every block on its own CU at once.  Draw indices follow the
+// reference's order, T1 then the drafts by head (src/engine.cpp:311, 318-330):
+// block j draws st->draw + j when sampling is stochastic, and the last block
+// to finish (every block has read st->draw by then) advances it past them.
+// Grid 1 + n_mtp, 1024 threads.
+__global__ __launch_bounds__(1024) void k_sample_round(const float* __restrict__ base_logits,
+                                                       const float* __restrict__ mlogits, uint32_t V, SamplingCfg cfg,
+                                                       uint64_t seed, DecodeState* st, int32_t* tokens, uint32_t cap,
+                                                       PassDesc* pdB, int32_t h) {
+    __shared__ uint64_t base_s;
+    if (threadIdx.x == 0) base_s = st->draw;
+    __syncthreads();
+    const uint64_t base = base_s;
+    const uint32_t j = blockIdx.x;
+    bool used = false;
+    const float* row = j == 0 ? base_logits : mlogits + (size_t)(j - 1u) * V;
+    const int32_t t = sample_row(row, V, cfg, seed, base + j, &used);
+    if (threadIdx.x != 0) return;
+    if (j == 0) {
+        push_token(st, tokens, cap, t);
+        pdB->tok[0] = t;
+        pdB->pos0 = st->pos;
+        pdB->m = (uint32_t)h;
+        pdB->batch = 0;
+        pdB->seq0 = 0;
+        st->seg_k0 = 0;
+        st->more = 0;
+    } else {
+        st->draft[j - 1u] = t;
+        pdB->tok[j] = t;
+    }
+    const uint32_t done = __hip_atomic_fetch_add(&st->blocks_done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (done == gridDim.x - 1u) {
+        if (used) st->draw = base + gridDim.x;
+        st->blocks_done = 0u;
     }
 }
 

@@ -1872,10 +1872,10 @@ extern "C" pf_status pf_forward(pf_engine* e, const int32_t* tokens, uint32_t n,
 }
 
 // MTPHeads::forward chain on the device hidden state h0 (src/mtp.cpp:63-127):
-// gate, up, silu(gate) * up, down + residual, tied unembed, per head; with
-// `sample` the draft of head k is sampled right after its logits.  Head 0
-// reads h0 itself; its down product writes the running row mcur.
-static pf_status mtp_chain(pf_engine* e, const float* h0, bool sample, const SamplingCfg* cfg, uint64_t seed) {
+// gate, up, silu(gate) * up, down + residual, tied unembed, per head, the
+// logits of head k in row k of mlogits.  Head 0 reads h0 itself; its down
+// product writes the running row mcur.
+static pf_status mtp_chain(pf_engine* e, const float* h0) {
     pf_ctx* c = e->c;
     const pf_model* m = e->m;
     const pf_model_desc& d = m->d;
@@ -1887,9 +1887,6 @@ static pf_status mtp_chain(pf_engine* e, const float* h0, bool sample, const Sam
         launch_gemv_f32(st, m->mtp[k * 3 + 2], 1, e->ma, D, e->mcur, D, hin);
         float* lk = e->mlogits + (size_t)k * V;
         launch_gemv_f32(st, m->emb, 1, e->mcur, D, lk, V, nullptr);
-        if (sample)
-            hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, lk, V, 0, V, *cfg, seed, e->st, e->tokens,
-                               e->tok_cap, e->pdB, (int32_t)ROLE_DRAFT, (int32_t)k, (int32_t*)nullptr);
     }
     PF_LAUNCHED(c);
     return PF_OK;
@@ -1900,7 +1897,7 @@ extern "C" pf_status pf_mtp_forward(pf_engine* e, const float* hidden, float* lo
     pf_ctx* c = e->c;
     const pf_model_desc& d = e->m->d;
     PF_HIP(c, hipMemcpyAsync(e->hiddenA, hidden, d.n_embd * 4, hipMemcpyHostToDevice, c->stream));
-    pf_status s = mtp_chain(e, e->hiddenA, false, nullptr, 0);
+    pf_status s = mtp_chain(e, e->hiddenA);
     if (s) return s;
     PF_HIP(c, hipMemcpyAsync(logits, e->mlogits, (size_t)d.n_mtp * d.n_vocab * 4, hipMemcpyDeviceToHost, c->stream));
     PF_HIP(c, hipStreamSynchronize(c->stream));
@@ -1923,8 +1920,7 @@ extern "C" pf_status pf_sample(pf_engine* e, const float* logits, const pf_sampl
     PF_HIP(c, hipMemcpyAsync(e->st, &st, sizeof(st), hipMemcpyHostToDevice, c->stream));
     PF_HIP(c, hipMemcpyAsync(e->logitsA, logits, (size_t)V * 4, hipMemcpyHostToDevice, c->stream));
     hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, c->stream, e->logitsA, V, 0, V, to_cfg(cfg), seed, e->st,
-                       (int32_t*)nullptr, 0u, (PassDesc*)nullptr, (int32_t)ROLE_PLAIN, 0,
-                       (int32_t*)&e->st->round_word);
+                       (int32_t*)nullptr, 0u, (int32_t)ROLE_PLAIN, (int32_t*)&e->st->round_word);
     PF_LAUNCHED(c);
     PF_HIP(c, hipMemcpyAsync(&st, e->st, sizeof(st), hipMemcpyDeviceToHost, c->stream));
     PF_HIP(c, hipStreamSynchronize(c->stream));
@@ -1963,9 +1959,11 @@ static pf_status round_body(pf_engine* e, bool reuse, bool mtp, const SamplingCf
         base_hidden = e->hiddenA;
     }
     if (mtp) {
-        hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, base_logits, V, 0, V, cfg, seed, e->st, e->tokens,
-                           e->tok_cap, e->pdB, (int32_t)ROLE_T1, (int32_t)h, (int32_t*)nullptr);
-        if ((s = mtp_chain(e, base_hidden, true, &cfg, seed))) return s;
+        // the heads run from the base row's hidden state; T1 and the drafts
+        // are then sampled together, one block each
+        if ((s = mtp_chain(e, base_hidden))) return s;
+        hipLaunchKernelGGL(k_sample_round, dim3(1 + NM), dim3(1024), 0, st, base_logits, (const float*)e->mlogits, V,
+                           cfg, seed, e->st, e->tokens, e->tok_cap, e->pdB, (int32_t)h);
         if ((s = timed_begin(e, true, &tp))) return s;
         e->in_verify = true;
         s = run_pass(e, e->pdB, h, e->pos + 1, e->logitsB, e->hiddenB);
@@ -1976,10 +1974,10 @@ static pf_status round_body(pf_engine* e, bool reuse, bool mtp, const SamplingCf
         hipLaunchKernelGGL(k_ctl_accept, dim3(1), dim3(1), 0, st, e->st, e->pdB, e->tokens, e->tok_cap);
         if (e->skip_on) launch_skip_commit(e, e->pdB, NM + 1, 0, 0, true);
         hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, e->logitsB, V, -1, V, cfg, seed, e->st, e->tokens,
-                           e->tok_cap, e->pdB, (int32_t)ROLE_CORRECTIVE, 0, (int32_t*)nullptr);
+                           e->tok_cap, (int32_t)ROLE_CORRECTIVE, (int32_t*)nullptr);
     } else {
         hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, base_logits, V, 0, V, cfg, seed, e->st, e->tokens,
-                           e->tok_cap, e->pdB, (int32_t)ROLE_FALLBACK, 0, (int32_t*)nullptr);
+                           e->tok_cap, (int32_t)ROLE_FALLBACK, (int32_t*)nullptr);
     }
     PF_LAUNCHED(c);
     return PF_OK;
@@ -2005,7 +2003,7 @@ static pf_status segment_body(pf_engine* e, const SamplingCfg& cfg, uint64_t see
     hipLaunchKernelGGL(k_argmax_rows, dim3(NM), dim3(1024), 0, st, e->logitsB + V, V, V, e->pdB, e->st->row_argmax);
     hipLaunchKernelGGL(k_ctl_accept, dim3(1), dim3(1), 0, st, e->st, e->pdB, e->tokens, e->tok_cap);
     hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, e->logitsB, V, -1, V, cfg, seed, e->st, e->tokens,
-                       e->tok_cap, e->pdB, (int32_t)ROLE_CORRECTIVE, 0, (int32_t*)nullptr);
+                       e->tok_cap, (int32_t)ROLE_CORRECTIVE, (int32_t*)nullptr);
     PF_LAUNCHED(c);
     return PF_OK;
 }
