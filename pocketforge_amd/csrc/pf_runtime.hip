@@ -1396,7 +1396,7 @@ static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t ns
     if (!s) s = ealloc(e, &e->hiddenA, (size_t)MA * D);
     if (!s) s = ealloc(e, &e->logitsB, (size_t)MR * V);
     if (!s) s = ealloc(e, &e->hiddenB, (size_t)MR * D);
-    if (!s) s = ealloc(e, &e->mcur, (size_t)nseq * D);
+    if (!s) s = ealloc(e, &e->mcur, (size_t)std::max(nseq, d.n_mtp) * D);
     if (!s) s = ealloc(e, &e->ma, (size_t)nseq * D);
     if (!s) s = ealloc(e, &e->mlogits, (size_t)std::max(1u, d.n_mtp) * V);
     if (!s) s = ealloc(e, &e->mlogb, (size_t)nseq * V);
@@ -1872,9 +1872,10 @@ extern "C" pf_status pf_forward(pf_engine* e, const int32_t* tokens, uint32_t n,
 }
 
 // MTPHeads::forward chain on the device hidden state h0 (src/mtp.cpp:63-127):
-// gate, up, silu(gate) * up, down + residual, tied unembed, per head, the
-// logits of head k in row k of mlogits.  Head 0 reads h0 itself; its down
-// product writes the running row mcur.
+// gate, up, silu(gate) * up, down + residual per head, head k's state in row
+// k of mcur (head 0 reads h0 itself, head k > 0 row k - 1), then the tied
+// unembedding of all the heads' rows in one product (each row's logits are
+// those of its own product), the logits of head k in row k of mlogits.
 static pf_status mtp_chain(pf_engine* e, const float* h0) {
     pf_ctx* c = e->c;
     const pf_model* m = e->m;
@@ -1882,12 +1883,11 @@ static pf_status mtp_chain(pf_engine* e, const float* h0) {
     hipStream_t st = c->stream;
     const uint32_t D = d.n_embd, V = d.n_vocab;
     for (uint32_t k = 0; k < d.n_mtp; k++) {
-        const float* hin = k == 0 ? h0 : e->mcur;
+        const float* hin = k == 0 ? h0 : e->mcur + (size_t)(k - 1) * D;
         launch_gemv_f32_glu(st, m->mtp[k * 3 + 0], m->mtp[k * 3 + 1], 1, hin, D, e->ma, D);
-        launch_gemv_f32(st, m->mtp[k * 3 + 2], 1, e->ma, D, e->mcur, D, hin);
-        float* lk = e->mlogits + (size_t)k * V;
-        launch_gemv_f32(st, m->emb, 1, e->mcur, D, lk, V, nullptr);
+        launch_gemv_f32(st, m->mtp[k * 3 + 2], 1, e->ma, D, e->mcur + (size_t)k * D, D, hin);
     }
+    if (d.n_mtp) launch_gemv_f32(st, m->emb, d.n_mtp, e->mcur, D, e->mlogits, V, nullptr);
     PF_LAUNCHED(c);
     return PF_OK;
 }
