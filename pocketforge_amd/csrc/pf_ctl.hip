@@ -85,15 +85,6 @@ __global__ __launch_bounds__(1024) void k_argmax_one(const float* __restrict__ x
     if (threadIdx.x == 0) *out = b.i;
 }
 
-// row_argmax[m] for every row of a pass.  Grid M, 1024 threads.
-__global__ __launch_bounds__(1024) void k_argmax_rows(const float* __restrict__ logits, uint32_t stride,
-                                                      uint32_t V, const PassDesc* __restrict__ pd,
-                                                      int32_t* __restrict__ out) {
-    if (blockIdx.x >= pd->m) return;
-    ArgBest b = block_argmax(logits + (size_t)blockIdx.x * stride, V);
-    if (threadIdx.x == 0) out[blockIdx.x] = b.i;
-}
-
 // ----------------------------------------------------- stochastic sampler
 
 __device__ __forceinline__ uint32_t ord_f(float f) {
@@ -451,12 +442,29 @@ __global__ void k_ctl_reuse_row(DecodeState* st) {
     st->have_row4 = 0;
 }
 
-// Acceptance (src/engine.cpp:333-365) of one verify segment given the
-// greedy argmax of its rows (row r checks draft seg_k0 + r): accepted
-// drafts pushed, the positions of the rows the reference would have
-// forwarded committed.
-__global__ void k_ctl_accept(DecodeState* st, const PassDesc* pdB, int32_t* tokens, uint32_t cap) {
-    const uint32_t n_mtp = st->n_mtp, k0 = st->seg_k0, m = pdB->m;
+// Acceptance (src/engine.cpp:333-365) of one verify segment in one launch:
+// block r ranks verify row r (the first index of its maximum) into
+// row_argmax, row r checking draft seg_k0 + r; the last block to finish
+// (counted with a device-scope atomic; every block's row is visible to it)
+// pushes the drafts while the rows' argmax equal them, commits the
+// positions of the rows the reference would have forwarded, sets the next
+// segment, and with greedy sampling also
+// takes the corrective: Engine::sample of the first mismatching row is its
+// argmax, pushed when it differs from the draft (k_sample's corrective
+// without a draw).  Grid rows of the segment's largest height, 1024 threads.
+__global__ __launch_bounds__(1024) void k_verify_accept(const float* __restrict__ logits, uint32_t stride, uint32_t V,
+                                                        DecodeState* st, const PassDesc* __restrict__ pdB,
+                                                        int32_t* tokens, uint32_t cap, int32_t greedy) {
+    const uint32_t m = pdB->m, rb = blockIdx.x;
+    if (rb < m) {
+        const ArgBest b = block_argmax(logits + (size_t)rb * stride, V);
+        if (threadIdx.x == 0) st->row_argmax[rb] = b.i;
+    }
+    if (threadIdx.x != 0) return;
+    const uint32_t done = __hip_atomic_fetch_add(&st->blocks_done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (done != gridDim.x - 1u) return;
+    st->blocks_done = 0u;
+    const uint32_t n_mtp = st->n_mtp, k0 = st->seg_k0;
     uint32_t a = k0, r = 0;
     while (r < m && a < n_mtp && st->row_argmax[r] == st->draft[a]) {
         push_token(st, tokens, cap, st->draft[a]);
@@ -480,6 +488,12 @@ __global__ void k_ctl_accept(DecodeState* st, const PassDesc* pdB, int32_t* toke
         st->pos = pdB->pos0 + m;
     }
     st->round_word = a | (st->more << 9);
+    if (greedy && a < n_mtp && r < m) {   // the corrective of row r (draft a)
+        const int32_t t = st->row_argmax[r];
+        uint32_t pushed = 0;
+        if (t != st->draft[a]) { push_token(st, tokens, cap, t); st->rejected++; pushed = 1; }
+        st->round_word = a | (pushed << 8);
+    }
 }
 
 // Setup of a verify segment that continues a round: rows check drafts
@@ -585,7 +599,7 @@ __global__ __launch_bounds__(1024) void k_bargmax_rows(const float* __restrict__
     if (threadIdx.x == 0) st[sel[r / R]].row_argmax[r % R] = b.i;
 }
 
-// Acceptance of k_ctl_accept for the nm MTP sequences of a batched round.
+// Acceptance of k_verify_accept for the nm MTP sequences of a batched round.
 __global__ void k_bctl_accept(DecodeState* st, const uint32_t* __restrict__ sel, uint32_t nm,
                               const PassDesc* __restrict__ pdB, uint32_t R, int32_t* tokens, uint32_t cap) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;

@@ -1936,6 +1936,7 @@ extern "C" pf_status pf_sample(pf_engine* e, const float* logits, const pf_sampl
 // Verify row j sits at row j of logitsB / hiddenB in every segment.
 static pf_status round_body(pf_engine* e, bool reuse, bool mtp, const SamplingCfg& cfg, uint64_t seed,
                             uint32_t h) {
+    const bool greedy = cfg.greedy || cfg.temperature <= 0.0f;   // Engine::sample's greedy branch
     pf_ctx* c = e->c;
     hipStream_t st = c->stream;
     const pf_model_desc& d = e->m->d;
@@ -1970,11 +1971,12 @@ static pf_status round_body(pf_engine* e, bool reuse, bool mtp, const SamplingCf
         e->in_verify = false;
         if (s) return s;
         if (tp) PF_HIP(c, hipEventRecord(tp->b, st));
-        hipLaunchKernelGGL(k_argmax_rows, dim3(h), dim3(1024), 0, st, e->logitsB, V, V, e->pdB, e->st->row_argmax);
-        hipLaunchKernelGGL(k_ctl_accept, dim3(1), dim3(1), 0, st, e->st, e->pdB, e->tokens, e->tok_cap);
+        hipLaunchKernelGGL(k_verify_accept, dim3(h), dim3(1024), 0, st, (const float*)e->logitsB, V, V, e->st,
+                           (const PassDesc*)e->pdB, e->tokens, e->tok_cap, greedy ? 1 : 0);
         if (e->skip_on) launch_skip_commit(e, e->pdB, NM + 1, 0, 0, true);
-        hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, e->logitsB, V, -1, V, cfg, seed, e->st, e->tokens,
-                           e->tok_cap, (int32_t)ROLE_CORRECTIVE, (int32_t*)nullptr);
+        if (!greedy)
+            hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, e->logitsB, V, -1, V, cfg, seed, e->st,
+                               e->tokens, e->tok_cap, (int32_t)ROLE_CORRECTIVE, (int32_t*)nullptr);
     } else {
         hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, base_logits, V, 0, V, cfg, seed, e->st, e->tokens,
                            e->tok_cap, (int32_t)ROLE_FALLBACK, (int32_t*)nullptr);
@@ -2000,10 +2002,12 @@ static pf_status segment_body(pf_engine* e, const SamplingCfg& cfg, uint64_t see
     e->in_verify = false;
     if (s) return s;
     if (tp) PF_HIP(c, hipEventRecord(tp->b, st));
-    hipLaunchKernelGGL(k_argmax_rows, dim3(NM), dim3(1024), 0, st, e->logitsB + V, V, V, e->pdB, e->st->row_argmax);
-    hipLaunchKernelGGL(k_ctl_accept, dim3(1), dim3(1), 0, st, e->st, e->pdB, e->tokens, e->tok_cap);
-    hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, e->logitsB, V, -1, V, cfg, seed, e->st, e->tokens,
-                       e->tok_cap, (int32_t)ROLE_CORRECTIVE, (int32_t*)nullptr);
+    const bool greedy = cfg.greedy || cfg.temperature <= 0.0f;   // Engine::sample's greedy branch
+    hipLaunchKernelGGL(k_verify_accept, dim3(NM), dim3(1024), 0, st, (const float*)(e->logitsB + V), V, V, e->st,
+                       (const PassDesc*)e->pdB, e->tokens, e->tok_cap, greedy ? 1 : 0);
+    if (!greedy)
+        hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, e->logitsB, V, -1, V, cfg, seed, e->st, e->tokens,
+                           e->tok_cap, (int32_t)ROLE_CORRECTIVE, (int32_t*)nullptr);
     PF_LAUNCHED(c);
     return PF_OK;
 }
