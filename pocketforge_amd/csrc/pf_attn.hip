@@ -864,7 +864,8 @@ constexpr uint32_t ag_smem(uint32_t nr) { return 2u * 256u * 128u + (512u + nr *
 // row's list: row r of the group sees C + r entries (C the count of its
 // first row), then its fp32 self entry at list index C + r.  A group of n
 // rows is served by ceil(n / NR) blocks of at most NR rows each.
-// Grid (heads * chunks, M), 256 threads: block (x, m) serves share
+// Grid (heads * chunks, M), 512 threads (waves 4-7 join only the V chains,
+// one element each): block (x, m) serves share
 // m - m0 of the group led by row m0 (if that share exists).  With pf.p set
 // the grid has one more row of blocks, which load pf's groups (the next
 // kernel's weights) into the L2 of the XCDs that will read them instead.
@@ -877,7 +878,7 @@ constexpr uint32_t ag_smem(uint32_t nr) { return 2u * 256u * 128u + (512u + nr *
 // of every list of the pass, so blocks still reading other chunks never see
 // them change.  Otherwise k_kv_store_pass has stored the pass's rows.
 template <int PARTS, bool FUSED, int NR>
-__global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__ pd, KvGeom g, KvPlanes kv,
+__global__ __launch_bounds__(512) void k_attn_group(const PassDesc* __restrict__ pd, KvGeom g, KvPlanes kv,
                                                     uint32_t layer, uint32_t M, const float* __restrict__ q,
                                                     const float* __restrict__ kself, const float* __restrict__ vself,
                                                     float* __restrict__ S, uint32_t s_stride,
@@ -902,6 +903,7 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
 
     const uint32_t H = g.n_heads, h = blockIdx.x % H, c = blockIdx.x / H, m0 = blockIdx.y;
     const uint32_t t = threadIdx.x, lane = t & 63u, wid = t >> 6;
+    const bool hi = t >= 256u;   // waves 4-7 join the V chains only
     const PassHead ph = pass_head(pd);
     const uint32_t Mp = min(M, ph.m);
     if (m0 >= Mp) return;
@@ -943,7 +945,7 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
         const uint32_t i = t + 256u * k, r = i / hd, d = i - r * hd;
         qv[k] = 0.0f;
         kvv[k] = 0.0f;
-        if (r < G) {
+        if (!hi && r < G) {
             const size_t o = (size_t)(mb + r) * D + h * hd + d;
             qv[k] = q[o];
             kvv[k] = kself[o];
@@ -957,7 +959,7 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
     for (uint32_t u = 0; u < 2; u++) {
         const uint32_t i = wid + 4u * u;
         fk[u][0] = fk[u][1] = fv[u][0] = fv[u][1] = 0.0f;
-        if (i < nq && 2u * lane < hd) {
+        if (!hi && i < nq && 2u * lane < hd) {
             const size_t o = (size_t)(first + i) * D + h * hd + 2u * lane;
             fk[u][0] = kself[o];
             fk[u][1] = kself[o + 1];
@@ -973,7 +975,7 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
         const uint32_t pi = t + 256u * i, e = pi / PARTS, part = pi % PARTS;
         kw[i] = make_int4(0, 0, 0, 0);
         vw[i] = make_int4(0, 0, 0, 0);
-        if (e < nvis) {
+        if (!hi && e < nvis) {
             const uint32_t pos = FUSED ? entry_pos(g, vL, j0 + e) : 0xFFFFFFFFu;
             if (pos == 0xFFFFFFFFu || pos < p_first) {
                 const size_t row = plane * g.rows + chunk_row(g, vL, j0 + e, wstart, wb);
@@ -998,7 +1000,7 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
 #pragma unroll
     for (uint32_t k = 0; k < QPT; k++) {
         const uint32_t i = t + 256u * k, r = i / hd, d = i - r * hd;
-        if (r < (uint32_t)NR) {
+        if (!hi && r < (uint32_t)NR) {
             qs[r * 128 + d] = qv[k];
             kss[r * 128 + d] = kvv[k];
         }
@@ -1007,7 +1009,7 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
 #pragma unroll
         for (uint32_t u = 0; u < 2; u++) {
             const uint32_t i = wid + 4u * u;
-            if (i >= nq) continue;
+            if (hi || i >= nq) continue;
             const float ak = wave_max(fmaxf(fabsf(fk[u][0]), fabsf(fk[u][1])));
             const float av = wave_max(fmaxf(fabsf(fv[u][0]), fabsf(fv[u][1])));
             const float ik = ak == 0.0f ? 1.0f : 127.0f / ak, iv = av == 0.0f ? 1.0f : 127.0f / av;
@@ -1052,7 +1054,7 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
 #pragma unroll
     for (uint32_t i = 0; i < (uint32_t)PARTS; i++) {
         const uint32_t pi = t + 256u * i, e = pi / PARTS, part = pi % PARTS;
-        if (e < nvis) {
+        if (!hi && e < nvis) {
             const uint32_t pos = FUSED ? entry_pos(g, vL, j0 + e) : 0xFFFFFFFFu;
             if (pos == 0xFFFFFFFFu || pos < p_first) {
                 kt[part * 256u + (e ^ part)] = kw[i];
@@ -1060,7 +1062,7 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
             }
         }
     }
-    if (!pend) {                      // 0 past the visible entries: their terms below add exactly 0
+    if (!hi && !pend) {               // 0 past the visible entries: their terms below add exactly 0
         ksc[t] = ks;
         vsc[t] = vs;
     }
@@ -1089,7 +1091,7 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
     // the self score of row j - C0, when this thread holds that row's self entry
     float selfd = 0.0f;
     const uint32_t rs = j - C0;
-    if (rs < G) {
+    if (!hi && rs < G) {
 #pragma unroll 16
         for (uint32_t i = 0; i < hd; i++) selfd = selfd + qs[rs * 128 + i] * kss[rs * 128 + i];
     }
@@ -1104,7 +1106,7 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
 #pragma unroll
     for (int r = 0; r < NR; r++) {
         const float w = wave_max(sc[r]);
-        if (lane == 0) rmx[r * 4 + wid] = w;
+        if (!hi && lane == 0) rmx[r * 4 + wid] = w;
     }
     __syncthreads();
     float ex[NR];
@@ -1112,50 +1114,41 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
     for (int r = 0; r < NR; r++) {
         const float* rr = rmx + r * 4;
         const float mx = fmaxf(fmaxf(rr[0], rr[1]), fmaxf(rr[2], rr[3]));
-        const bool in = (uint32_t)r < G && j <= C0 + r;
+        const bool in = !hi && (uint32_t)r < G && j <= C0 + r;
         ex[r] = in ? expf_c(sc[r] - mx) : 0.0f;
         // the V chains take cached and pending entries; the self term is added apart
-        pe[r * 256 + t] = j < C0 + r ? ex[r] : 0.0f;
+        if (!hi) pe[r * 256 + t] = j < C0 + r ? ex[r] : 0.0f;
         if (in && j == C0 + r) pself[r] = ex[r];
         const float w = wave_tree_sum(ex[r]);
-        if (lane == 0) rsm[r * 4 + wid] = w;
+        if (!hi && lane == 0) rsm[r * 4 + wid] = w;
     }
     __syncthreads();
-    // ---- V: per row and 64-entry sub-chunk an fmaf chain, conversions shared
-    const uint32_t sub = wid, i0 = 2u * lane;
-    if (i0 < hd) {
-        float w0[NR], w1[NR];
+    // ---- V: per row and 64-entry sub-chunk an fmaf chain; wave w takes
+    // sub-chunk w & 3 and element lane + 64 (w >> 2) of every row
+    const uint32_t sub = wid & 3u, iv = lane + 64u * (wid >> 2);
+    if (iv < hd) {
+        float w0[NR];
 #pragma unroll
-        for (int r = 0; r < NR; r++) {
-            w0[r] = 0.0f;
-            w1[r] = 0.0f;
-        }
-        // entries [64 sub, min(64 sub + 64, nvis)) in groups of 4; entries
+        for (int r = 0; r < NR; r++) w0[r] = 0.0f;
+        // entries [64 sub, min(64 sub + 64, nvis)) in groups of 8; entries
         // past nvis up to the next multiple of 8 have v_scale 0 and finite
         // codes, and entries past a row's list have weight 0
         const uint32_t e_end = min(64u * sub + 64u, (nvis + 7u) & ~7u);   // both multiples of 8
 #pragma unroll 2
         for (uint32_t e = 64u * sub; e < e_end; e += 8) {
-            float a0[8], a1[8];
+            float a0[8];
             const float4 s0 = *reinterpret_cast<const float4*>(&vsc[e]);
             const float4 s1 = *reinterpret_cast<const float4*>(&vsc[e + 4]);
             const float vv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const uint32_t cc = *reinterpret_cast<const uint16_t*>(&vt[e + u][i0]);
-                a0[u] = (float)(int8_t)(cc & 0xFFu) * vv[u];
-                a1[u] = (float)(int8_t)(cc >> 8) * vv[u];
-            }
+            for (int u = 0; u < 8; u++) a0[u] = (float)vt[e + u][iv] * vv[u];
 #pragma unroll
             for (int r = 0; r < NR; r++) {
                 const float4 p0 = *reinterpret_cast<const float4*>(&pe[r * 256 + e]);
                 const float4 p1 = *reinterpret_cast<const float4*>(&pe[r * 256 + e + 4]);
                 const float pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    w0[r] = __builtin_fmaf(pp[u], a0[u], w0[r]);
-                    w1[r] = __builtin_fmaf(pp[u], a1[u], w1[r]);
-                }
+                for (int u = 0; u < 8; u++) w0[r] = __builtin_fmaf(pp[u], a0[u], w0[r]);
             }
         }
 #pragma unroll
@@ -1164,17 +1157,15 @@ __global__ __launch_bounds__(256) void k_attn_group(const PassDesc* __restrict__
             const uint32_t js = C0 + r - j0;          // row r's self entry in the chunk
             if (js < 256u && (js >> 6) == sub) {
                 const float ps = pself[r];
-                const size_t o = (size_t)(mb + r) * D + h * hd + i0;
+                const size_t o = (size_t)(mb + r) * D + h * hd + iv;
                 w0[r] = __builtin_fmaf(ps, vself[o], w0[r]);
-                w1[r] = __builtin_fmaf(ps, vself[o + 1], w1[r]);
             }
-            wp[(r * 4 + sub) * 128 + i0] = w0[r];
-            wp[(r * 4 + sub) * 128 + i0 + 1] = w1[r];
+            wp[(r * 4 + sub) * 128 + iv] = w0[r];
         }
     }
     __syncthreads();
     // ---- outputs of the rows whose list reaches this chunk
-    for (uint32_t i = t; i < G * hd; i += 256u) {
+    for (uint32_t i = t; i < G * hd; i += 512u) {
         const uint32_t r = i / hd, d = i - r * hd;
         if (j0 > C0 + r) continue;
         const size_t mh = (size_t)(mb + r) * H + h;

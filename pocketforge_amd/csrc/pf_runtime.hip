@@ -622,10 +622,10 @@ static void launch_attn(hipStream_t st, uint32_t hd, uint32_t M, uint32_t tasks,
 #define PF_ATTN_LAUNCH(P, F, NR)                                                                              \
     do {                                                                                                      \
         if (ev0)                                                                                              \
-            hipExtLaunchKernelGGL((k_attn_group<P, F, NR>), dim3(tasks, gy), dim3(256), 0, st, ev0, ev1, 0, pd, \
+            hipExtLaunchKernelGGL((k_attn_group<P, F, NR>), dim3(tasks, gy), dim3(512), 0, st, ev0, ev1, 0, pd, \
                                   g, kv, l, M, q, k, v, S, s_stride, Wp, cstride, pf);                       \
         else                                                                                                  \
-            hipLaunchKernelGGL((k_attn_group<P, F, NR>), dim3(tasks, gy), dim3(256), 0, st, pd, g, kv, l, M, q, \
+            hipLaunchKernelGGL((k_attn_group<P, F, NR>), dim3(tasks, gy), dim3(512), 0, st, pd, g, kv, l, M, q, \
                                k, v, S, s_stride, Wp, cstride, pf);                                           \
     } while (0)
 #define PF_ATTN_ROWS(P)                              \
