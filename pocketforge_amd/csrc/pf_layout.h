@@ -96,7 +96,7 @@ struct DecodeState {
     uint32_t n_mtp;        // drafts per MTP round (single-sequence engine)
     uint32_t seg_k0;       // draft index checked by row 0 of the current verify segment
     uint32_t more;         // the segment accepted every row it checked, drafts remain
-    uint32_t blocks_done;  // blocks of the current k_sample_round that have finished
+    uint32_t blocks_done;  // finished blocks of the running k_sample_round / k_verify_accept (0 between launches)
 };
 
 struct SamplingCfg {
