@@ -43,7 +43,8 @@ __device__ __forceinline__ void stage_rows(const float* __restrict__ h, uint32_t
 // lane l holds block l (K <= 2048), fmaf chain over the block's elements,
 // halving tree over the 64 lanes.  Each wave walks rows n = wave, wave +
 // total_waves, ..., loading the codes and scales of RB rows before their
-// products (the tied unembedding gives each wave 8 rows).
+// products (the tied unembedding gives each wave 8 rows).  Grid y takes
+// the activation rows M at a time: slice y serves rows M y .. M y + M - 1.
 template <int M>
 __global__ __launch_bounds__(256) void k_gemv_f32(const uint8_t* __restrict__ codes,
                                                   const uint16_t* __restrict__ scales,
@@ -51,6 +52,9 @@ __global__ __launch_bounds__(256) void k_gemv_f32(const uint8_t* __restrict__ co
                                                   const float* __restrict__ h, uint32_t h_stride,
                                                   float* __restrict__ y, uint32_t y_stride,
                                                   const float* __restrict__ y_in) {
+    h += (size_t)blockIdx.y * M * h_stride;
+    y += (size_t)blockIdx.y * M * y_stride;
+    if (y_in) y_in += (size_t)blockIdx.y * M * y_stride;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
@@ -118,6 +122,8 @@ __global__ __launch_bounds__(256) void k_gemv_f32_glu(const uint8_t* __restrict_
                                                       const uint16_t* __restrict__ uscales, uint32_t N, uint32_t K,
                                                       const float* __restrict__ h, uint32_t h_stride,
                                                       float* __restrict__ a, uint32_t a_stride) {
+    h += (size_t)blockIdx.y * M * h_stride;   // grid y: activation rows M at a time
+    a += (size_t)blockIdx.y * M * a_stride;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);

@@ -495,9 +495,10 @@ static_assert(NOALLOC_SCALE_BYTES >= MAX_GEMM_ROWS * 4, "one scale per GEMM row"
 static void launch_gemv_f32(hipStream_t st, const pf_matrix* W, uint32_t M, const float* h, uint32_t h_stride,
                             float* y, uint32_t y_stride, const float* y_in) {
     uint32_t waves = std::min<uint32_t>(W->rows, 2048);
-    dim3 grid((waves + 3) / 4);
-    for (uint32_t r0 = 0; r0 < M; r0 += 8) {
+    // whole groups of 8 rows in one launch (grid y), then the rest
+    for (uint32_t r0 = 0; r0 < M;) {
         const uint32_t mb = std::min(8u, M - r0);
+        const dim3 grid((waves + 3) / 4, mb == 8u ? (M - r0) / 8u : 1u);
         const float* hr = h + (size_t)r0 * h_stride;
         float* yr = y + (size_t)r0 * y_stride;
         const float* yi = y_in ? y_in + (size_t)r0 * y_stride : nullptr;
@@ -511,6 +512,7 @@ static void launch_gemv_f32(hipStream_t st, const pf_matrix* W, uint32_t M, cons
             PF_F32_CASE(5) PF_F32_CASE(6) PF_F32_CASE(7) PF_F32_CASE(8)
         }
 #undef PF_F32_CASE
+        r0 += mb * grid.y;
     }
 }
 
@@ -519,9 +521,9 @@ static void launch_gemv_f32(hipStream_t st, const pf_matrix* W, uint32_t M, cons
 static void launch_gemv_f32_glu(hipStream_t st, const pf_matrix* Wg, const pf_matrix* Wu, uint32_t M, const float* h,
                                 uint32_t h_stride, float* a, uint32_t a_stride) {
     uint32_t waves = std::min<uint32_t>(Wg->rows, 2048);
-    dim3 grid((waves + 3) / 4);
-    for (uint32_t r0 = 0; r0 < M; r0 += 8) {
+    for (uint32_t r0 = 0; r0 < M;) {
         const uint32_t mb = std::min(8u, M - r0);
+        const dim3 grid((waves + 3) / 4, mb == 8u ? (M - r0) / 8u : 1u);
         const float* hr = h + (size_t)r0 * h_stride;
         float* ar = a + (size_t)r0 * a_stride;
 #define PF_GLU_CASE(MM)                                                                                          \
@@ -534,6 +536,7 @@ static void launch_gemv_f32_glu(hipStream_t st, const pf_matrix* Wg, const pf_ma
             PF_GLU_CASE(5) PF_GLU_CASE(6) PF_GLU_CASE(7) PF_GLU_CASE(8)
         }
 #undef PF_GLU_CASE
+        r0 += mb * grid.y;
     }
 }
 
