@@ -45,6 +45,7 @@ struct MmEpi {
     const PassDesc* pd;        // QKV: positions of the pass rows
     uint32_t D, hd;
     float* pmax;               // SWIGLU (GEMV): per-workgroup row maxima of |output| [M][N / 32], or null
+    float* y2;                 // RESID: a copy of the updated rows (a pass's hidden output), or null
 };
 
 // Logical row of device row n of a matrix whose halves [0, N/2) and
@@ -87,6 +88,7 @@ __device__ __forceinline__ float epi_apply(const MmEpi& e, const EpiPre& p, uint
         e.y[(size_t)m * e.y_stride + (e.ilv ? ilv_logical(n, N) : n)] = y;
     } else if constexpr (EPI == EPI_RESID) {
         if (p.b == 0.0f) e.y[(size_t)m * e.y_stride + n] = p.a + y;
+        if (e.y2) e.y2[(size_t)m * e.y_stride + n] = p.b == 0.0f ? p.a + y : p.a;
     } else if constexpr (EPI == EPI_QKV) {
         // src/engine.cpp:693-715 (Q, K, V rows of the fused matrix) and the
         // RoPE of :732-749 for Q and K: pair (2t, 2t+1) of a head

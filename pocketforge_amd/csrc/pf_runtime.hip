@@ -1836,6 +1836,9 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         a.x = e->sg; a.xs = F; a.pin = e->pmax; a.np = 2 * F / 32;
         a.e.y = e->x; a.e.y_stride = D;
         a.nx = prefetch_of(e, l + 1 < d.n_layers ? m->qkv[l + 1] : nullptr, e->l2_blocks);
+        // the last down product also writes the pass's hidden output (a
+        // gated launch may write nothing, so layer skip keeps the copy)
+        if (l + 1 == d.n_layers && hidden && !e->skip_on) a.e.y2 = hidden;
         if (e->skip_on) {
             a.gate = e->skip_nrun + l;
             a.e.skipm = e->skip_flags + (size_t)l * e->rows;
@@ -1848,7 +1851,7 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
     // every row of a pass counts for the skip caches except in verify passes,
     // whose caller commits the rows the acceptance keeps
     if (e->skip_on && !e->in_verify) launch_skip_commit(e, pd, M, 0, 0xFFFFFFFFu, false);
-    if (hidden)
+    if (hidden && (e->skip_on || d.n_layers == 0))
         hipLaunchKernelGGL(k_copy_f32, dim3((M * D + 255) / 256), dim3(256), 0, st, (const float*)e->x, hidden, M * D);
     if (logits) launch_gemv_f32(st, m->emb, M, e->x, D, logits, d.n_vocab, nullptr);
     PF_LAUNCHED(c);
