@@ -37,6 +37,7 @@ typedef int32_t pf_status;
 #define PF_ERR_STATE -5        /* call out of order (e.g. model incomplete) */
 #define PF_ERR_CAPACITY -6     /* position/token capacity exceeded */
 #define PF_ERR_FORMAT -7       /* malformed or unsupported file contents */
+#define PF_ERR_DEVICE -8       /* a bounded device-side wait timed out (results of that call are invalid) */
 
 typedef struct pf_ctx pf_ctx;
 typedef struct pf_model pf_model;

@@ -853,6 +853,55 @@ constexpr uint32_t AG_MAX_ROWS = 8;   // rows of one attention group
 // 8 lanes writing one row and the lanes reading part p of consecutive rows
 // both fall on distinct banks.  V rows are plain [256][128].
 constexpr uint32_t ag_smem(uint32_t nr) { return 2u * 256u * 128u + (512u + nr * (256u + 256u + 8u + 1u)) * 4u; }
+// With the rows' q/k/v taken from LL words, their self values [NR][128]
+// follow (the V stage reads them from LDS).
+constexpr uint32_t ag_smem_ll(uint32_t nr) { return ag_smem(nr) + nr * 128u * 4u; }
+
+// The pass's q/k/v rows as written by the QKV workgroups of the same launch
+// (pf_mm.hip, EPI_QKV with ll set): 8-byte words (value bits, flag) at
+// ll[row][3 D] (q, then k, then v), flag = ep[0] * fmul + fadd.  A reader
+// loads its words with device-scope loads and loads again the ones whose
+// flag is not yet the pass's.  A wait longer than LL_SPIN_MAX rounds sets
+// *err (the host reports it) and goes on, so every block ends.
+struct LLIn {
+    const unsigned long long* ll;
+    const uint32_t* ep;
+    uint32_t fmul, fadd;
+    uint32_t* err;
+};
+constexpr uint32_t LL_SPIN_MAX = 1u << 20;
+
+__device__ __forceinline__ unsigned long long ll_load(const unsigned long long* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Values of the N words base[off[i]] (off[i] == LL_NONE: 0) once each
+// carries `flag`.
+constexpr uint32_t LL_NONE = 0xFFFFFFFFu;
+template <int N>
+__device__ __forceinline__ void ll_wait(const unsigned long long* base, const uint32_t (&off)[N], float (&out)[N],
+                                        uint32_t flag, uint32_t* err) {
+    unsigned long long w[N];
+    const unsigned long long done = (unsigned long long)flag << 32;
+#pragma unroll
+    for (int i = 0; i < N; i++) w[i] = off[i] != LL_NONE ? ll_load(base + off[i]) : done;
+    for (uint32_t spins = 0;; spins++) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < N; i++) ok = ok && (uint32_t)(w[i] >> 32) == flag;
+        if (ok) break;
+        if (spins >= LL_SPIN_MAX) {
+            atomicOr(err, 1u);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int i = 0; i < N; i++)
+            if ((uint32_t)(w[i] >> 32) != flag) w[i] = ll_load(base + off[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++) out[i] = __uint_as_float((uint32_t)w[i]);
+}
 
 // Engine attention of every row of a pass (the first stage above), one
 // block per (head h, 256-entry chunk c, share of a group of rows), with the
@@ -877,18 +926,24 @@ constexpr uint32_t ag_smem(uint32_t nr) { return 2u * 256u * 128u + (512u + nr *
 // cache (src/kv_cache.cpp:59-127).  The ring's slack keeps those rows out
 // of every list of the pass, so blocks still reading other chunks never see
 // them change.  Otherwise k_kv_store_pass has stored the pass's rows.
-template <int PARTS, bool FUSED, int NR>
-__global__ __launch_bounds__(512) void k_attn_group(const PassDesc* __restrict__ pd, KvGeom g, KvPlanes kv,
-                                                    uint32_t layer, uint32_t M, const float* __restrict__ q,
-                                                    const float* __restrict__ kself, const float* __restrict__ vself,
-                                                    float* __restrict__ S, uint32_t s_stride,
-                                                    float* __restrict__ Up, uint32_t cstride, Prefetch pf) {
+//
+// LL: the pass's q/k/v rows come from LL words written by the QKV
+// workgroups of the same launch (k_qkv_attn); the cached K/V rows, which do
+// not depend on them, are loaded first.  attn_group_body is block (bx, by)
+// of a grid gx wide, linear workgroup id lin.
+template <int PARTS, bool FUSED, int NR, bool LL>
+__device__ __forceinline__ void attn_group_body(const PassDesc* __restrict__ pd, const KvGeom& g, const KvPlanes& kv,
+                                                uint32_t layer, uint32_t M, const float* __restrict__ q,
+                                                const float* __restrict__ kself, const float* __restrict__ vself,
+                                                float* __restrict__ S, uint32_t s_stride, float* __restrict__ Up,
+                                                uint32_t cstride, const Prefetch& pf, const LLIn& lli, uint32_t bx,
+                                                uint32_t by, uint32_t lin, uint32_t gx, uint8_t* smem) {
     constexpr uint32_t hd = 16 * PARTS;
-    __shared__ __align__(16) uint8_t smem[ag_smem(NR)];
-    if (blockIdx.y >= M) {
-        prefetch_groups(pf, blockIdx.x + blockIdx.y * gridDim.x, blockIdx.x, gridDim.x);
+    if (by >= M) {
+        prefetch_groups(pf, lin, bx, gx);
         return;
     }
+    const uint32_t epoch = LL ? lli.ep[0] : 0u;
     int4* kt = reinterpret_cast<int4*>(smem);                       // [PARTS][256], swizzled
     int8_t (*vt)[128] = reinterpret_cast<int8_t (*)[128]>(smem + 256u * 128u);
     float* ksc = reinterpret_cast<float*>(smem + 512u * 128u);      // [256]
@@ -899,9 +954,10 @@ __global__ __launch_bounds__(512) void k_attn_group(const PassDesc* __restrict__
     float* rmx = pe + NR * 256;                                     // [NR][4] wave maxima
     float* rsm = rmx + NR * 4;                                      // [NR][4] wave sums
     float* pself = rsm + NR * 4;                                    // [NR]
+    float* vss = pself + NR;                                        // LL: [NR][128] self values
     float* wp = reinterpret_cast<float*>(smem);                     // [NR][4][128], after the scores
 
-    const uint32_t H = g.n_heads, h = blockIdx.x % H, c = blockIdx.x / H, m0 = blockIdx.y;
+    const uint32_t H = g.n_heads, h = bx % H, c = bx / H, m0 = by;
     const uint32_t t = threadIdx.x, lane = t & 63u, wid = t >> 6;
     const bool hi = t >= 256u;   // waves 4-7 join the V chains only
     const PassHead ph = pass_head(pd);
@@ -939,13 +995,14 @@ __global__ __launch_bounds__(512) void k_attn_group(const PassDesc* __restrict__
     // ---- loads, all issued before any is used
     // the group's queries and self keys: element i = t + 256 k of [NR][hd]
     constexpr uint32_t QPT = (NR * hd + 255u) / 256u;
-    float qv[QPT], kvv[QPT];
+    float qv[QPT], kvv[QPT], vvv[QPT];
 #pragma unroll
     for (uint32_t k = 0; k < QPT; k++) {
         const uint32_t i = t + 256u * k, r = i / hd, d = i - r * hd;
         qv[k] = 0.0f;
         kvv[k] = 0.0f;
-        if (!hi && r < G) {
+        vvv[k] = 0.0f;
+        if (!LL && !hi && r < G) {
             const size_t o = (size_t)(mb + r) * D + h * hd + d;
             qv[k] = q[o];
             kvv[k] = kself[o];
@@ -959,7 +1016,7 @@ __global__ __launch_bounds__(512) void k_attn_group(const PassDesc* __restrict__
     for (uint32_t u = 0; u < 2; u++) {
         const uint32_t i = wid + 4u * u;
         fk[u][0] = fk[u][1] = fv[u][0] = fv[u][1] = 0.0f;
-        if (!hi && i < nq && 2u * lane < hd) {
+        if (!LL && !hi && i < nq && 2u * lane < hd) {
             const size_t o = (size_t)(first + i) * D + h * hd + 2u * lane;
             fk[u][0] = kself[o];
             fk[u][1] = kself[o + 1];
@@ -995,6 +1052,83 @@ __global__ __launch_bounds__(512) void k_attn_group(const PassDesc* __restrict__
             vs = kv.vs[row];
         }
     }
+    // the cached rows into LDS (pass rows quantized here take other slots)
+    auto stage_cached = [&]() {
+#pragma unroll
+        for (uint32_t i = 0; i < (uint32_t)PARTS; i++) {
+            const uint32_t pi = t + 256u * i, e = pi / PARTS, part = pi % PARTS;
+            if (!hi && e < nvis) {
+                const uint32_t pos = FUSED ? entry_pos(g, vL, j0 + e) : 0xFFFFFFFFu;
+                if (pos == 0xFFFFFFFFu || pos < p_first) {
+                    kt[part * 256u + (e ^ part)] = kw[i];
+                    *reinterpret_cast<int4*>(&vt[e][16 * part]) = vw[i];
+                }
+            }
+        }
+        if (!hi && !pend) {               // 0 past the visible entries: their terms below add exactly 0
+            ksc[t] = ks;
+            vsc[t] = vs;
+        }
+    };
+    if constexpr (LL) {
+        // staged before the wait, so that no register holds them meanwhile
+        stage_cached();
+        // the rows' q, self k and self v (element i = t + 256 k of [G][hd]),
+        // and for FUSED the k / v of pass rows first + w, first + w + 4
+        // (elements 2 lane, 2 lane + 1), once their QKV workgroups wrote them
+        constexpr int NW = 3 * (int)QPT + 8;
+        uint32_t wa[NW];
+        float wv_[NW];
+        const uint32_t rs3 = 3u * D;
+#pragma unroll
+        for (uint32_t k = 0; k < QPT; k++) {
+            const uint32_t i = t + 256u * k, r = i / hd, d = i - r * hd;
+            const bool use = !hi && r < G;
+            const uint32_t b = (mb + r) * rs3 + h * hd + d;
+            wa[3 * k] = use ? b : LL_NONE;
+            wa[3 * k + 1] = use ? b + D : LL_NONE;
+            wa[3 * k + 2] = use ? b + 2u * D : LL_NONE;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 2; u++) {
+            const uint32_t i = wid + 4u * u;
+            const bool use = !hi && i < nq && 2u * lane < hd;
+            const uint32_t b = (first + i) * rs3 + D + h * hd + 2u * lane;
+            wa[3 * QPT + 4 * u] = use ? b : LL_NONE;
+            wa[3 * QPT + 4 * u + 1] = use ? b + 1u : LL_NONE;
+            wa[3 * QPT + 4 * u + 2] = use ? b + D : LL_NONE;
+            wa[3 * QPT + 4 * u + 3] = use ? b + D + 1u : LL_NONE;
+        }
+        // one thread first waits for a word of each of the head's producer
+        // workgroups (32 output rows each of q, k and v), so that the block
+        // does not keep the memory system busy with all its words' polls
+        const uint32_t flag = epoch * lli.fmul + lli.fadd;
+        if (t == 0) {
+            uint32_t sp[12];
+            float sv_[12];
+#pragma unroll
+            for (uint32_t j = 0; j < 4; j++)
+#pragma unroll
+                for (uint32_t sec = 0; sec < 3; sec++)
+                    sp[3 * j + sec] = 32u * j < hd ? mb * rs3 + sec * D + h * hd + 32u * j : LL_NONE;
+            ll_wait<12>(lli.ll, sp, sv_, flag, lli.err);
+        }
+        __syncthreads();
+        ll_wait<NW>(lli.ll, wa, wv_, flag, lli.err);
+#pragma unroll
+        for (uint32_t k = 0; k < QPT; k++) {
+            qv[k] = wv_[3 * k];
+            kvv[k] = wv_[3 * k + 1];
+            vvv[k] = wv_[3 * k + 2];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 2; u++) {
+            fk[u][0] = wv_[3 * QPT + 4 * u];
+            fk[u][1] = wv_[3 * QPT + 4 * u + 1];
+            fv[u][0] = wv_[3 * QPT + 4 * u + 2];
+            fv[u][1] = wv_[3 * QPT + 4 * u + 3];
+        }
+    }
 
     // ---- LDS: queries, self keys, pass rows quantized here, cached rows
 #pragma unroll
@@ -1003,6 +1137,7 @@ __global__ __launch_bounds__(512) void k_attn_group(const PassDesc* __restrict__
         if (!hi && r < (uint32_t)NR) {
             qs[r * 128 + d] = qv[k];
             kss[r * 128 + d] = kvv[k];
+            if (LL) vss[r * 128 + d] = vvv[k];
         }
     }
     if constexpr (FUSED) {
@@ -1051,21 +1186,7 @@ __global__ __launch_bounds__(512) void k_attn_group(const PassDesc* __restrict__
             }
         }
     }
-#pragma unroll
-    for (uint32_t i = 0; i < (uint32_t)PARTS; i++) {
-        const uint32_t pi = t + 256u * i, e = pi / PARTS, part = pi % PARTS;
-        if (!hi && e < nvis) {
-            const uint32_t pos = FUSED ? entry_pos(g, vL, j0 + e) : 0xFFFFFFFFu;
-            if (pos == 0xFFFFFFFFu || pos < p_first) {
-                kt[part * 256u + (e ^ part)] = kw[i];
-                *reinterpret_cast<int4*>(&vt[e][16 * part]) = vw[i];
-            }
-        }
-    }
-    if (!hi && !pend) {               // 0 past the visible entries: their terms below add exactly 0
-        ksc[t] = ks;
-        vsc[t] = vs;
-    }
+    if constexpr (!LL) stage_cached();
     __syncthreads();
 
     // ---- scores: per row an fmaf chain over the converted key
@@ -1158,7 +1279,7 @@ __global__ __launch_bounds__(512) void k_attn_group(const PassDesc* __restrict__
             if (js < 256u && (js >> 6) == sub) {
                 const float ps = pself[r];
                 const size_t o = (size_t)(mb + r) * D + h * hd + iv;
-                w0[r] = __builtin_fmaf(ps, vself[o], w0[r]);
+                w0[r] = __builtin_fmaf(ps, LL ? vss[r * 128 + iv] : vself[o], w0[r]);
             }
             wp[(r * 4 + sub) * 128 + iv] = w0[r];
         }
@@ -1183,6 +1304,18 @@ __global__ __launch_bounds__(512) void k_attn_group(const PassDesc* __restrict__
         S[mh * s_stride + 2 * c] = fmaxf(fmaxf(mm[0], mm[1]), fmaxf(mm[2], mm[3]));
         S[mh * s_stride + 2 * c + 1] = (ss[0] + ss[2]) + (ss[1] + ss[3]);   // CANON(4) over the wave totals
     }
+}
+
+template <int PARTS, bool FUSED, int NR>
+__global__ __launch_bounds__(512) void k_attn_group(const PassDesc* __restrict__ pd, KvGeom g, KvPlanes kv,
+                                                    uint32_t layer, uint32_t M, const float* __restrict__ q,
+                                                    const float* __restrict__ kself, const float* __restrict__ vself,
+                                                    float* __restrict__ S, uint32_t s_stride,
+                                                    float* __restrict__ Up, uint32_t cstride, Prefetch pf) {
+    __shared__ __align__(16) uint8_t smem[ag_smem(NR)];
+    attn_group_body<PARTS, FUSED, NR, false>(pd, g, kv, layer, M, q, kself, vself, S, s_stride, Up, cstride, pf,
+                                             LLIn{}, blockIdx.x, blockIdx.y, blockIdx.x + blockIdx.y * gridDim.x,
+                                             gridDim.x, smem);
 }
 
 // Engine attention, second stage: the chunks of (row m, head h) merged left

@@ -63,7 +63,7 @@ extern "C" pf_status pf_batch_prefill(pf_engine* e, uint32_t seq, const int32_t*
     batch_sync_out(e);
     if (s) return s;
     PF_HIP(e->c, hipStreamSynchronize(e->c->stream));
-    return PF_OK;
+    return ll_check(e);
 }
 
 extern "C" pf_status pf_batch_forward(pf_engine* e, const uint32_t* seqs, uint32_t n, uint32_t rows_per_seq,
@@ -112,7 +112,7 @@ extern "C" pf_status pf_batch_forward(pf_engine* e, const uint32_t* seqs, uint32
     if (hidden)
         PF_HIP(c, hipMemcpyAsync(hidden, e->hiddenB, (size_t)rows * d.n_embd * 4, hipMemcpyDeviceToHost, c->stream));
     PF_HIP(c, hipStreamSynchronize(c->stream));
-    return PF_OK;
+    return ll_check(e);
 }
 
 // MTPHeads::forward chain (src/mtp.cpp:63-127) for rows 0..n-1 of h0 (the
@@ -339,5 +339,5 @@ extern "C" pf_status pf_batch_generate(pf_engine* e, const int32_t* prompts, con
         res[s].prefill_seconds = ps;
         res[s].decode_seconds = ds;
     }
-    return PF_OK;
+    return ll_check(e);
 }

@@ -391,9 +391,13 @@ __global__ void k_copy_f32(const float* __restrict__ src, float* __restrict__ ds
 }
 
 // Token embedding: x[m] = dequantized row tok[m] of the tied Q4 table.
+// The first kernel of every pass also advances the pass epoch `ep`, which
+// names the pass in the flags of the LL words its QKV products write.
 __global__ void k_embed(const uint8_t* __restrict__ codes, const uint16_t* __restrict__ scales,
-                        uint32_t V, uint32_t D, const PassDesc* __restrict__ pd, float* __restrict__ x) {
+                        uint32_t V, uint32_t D, const PassDesc* __restrict__ pd, float* __restrict__ x,
+                        uint32_t* __restrict__ ep) {
     uint32_t m = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (ep && m == 0 && i == 0) ep[0] += 1u;
     if (m >= pd->m || i >= D) return;
     int32_t tok = pd->tok[m];
     float val = 0.0f;

@@ -46,6 +46,13 @@ struct MmEpi {
     uint32_t D, hd;
     float* pmax;               // SWIGLU (GEMV): per-workgroup row maxima of |output| [M][N / 32], or null
     float* y2;                 // RESID: a copy of the updated rows (a pass's hidden output), or null
+    // QKV of a one-launch QKV + attention pass: instead of q/k/v, the rows
+    // go to ll[m][3 D] as 8-byte words (value bits, flag) written with one
+    // device-scope store each, flag = ep[0] * fmul + fadd (the pass epoch
+    // and the layer), so a reader that sees the flag sees the value
+    unsigned long long* ll;
+    const uint32_t* ep;
+    uint32_t fmul, fadd;
 };
 
 // Logical row of device row n of a matrix whose halves [0, N/2) and
@@ -58,11 +65,11 @@ __device__ __forceinline__ uint32_t ilv_logical(uint32_t n, uint32_t N) {
 // Operands of the epilogue that come from memory, loaded before the
 // product so that their latency overlaps it: RESID the old value (a) and
 // the skip flag (b != 0: no residual); QKV the RoPE cos (a) and sin (b).
-struct EpiPre { float a, b; };
+struct EpiPre { float a, b; uint32_t f; };
 
 template <int EPI>
 __device__ __forceinline__ EpiPre epi_prefetch(const MmEpi& e, uint32_t m, uint32_t n) {
-    EpiPre p{0.0f, 0.0f};
+    EpiPre p{0.0f, 0.0f, 0u};
     if constexpr (EPI == EPI_RESID) {
         p.a = e.y[(size_t)m * e.y_stride + n];
         p.b = (e.skipm && e.skipm[m]) ? 1.0f : 0.0f;
@@ -74,6 +81,7 @@ __device__ __forceinline__ EpiPre epi_prefetch(const MmEpi& e, uint32_t m, uint3
             p.a = e.rc[(size_t)pos * half + t];
             p.b = e.rs[(size_t)pos * half + t];
         }
+        if (e.ll) p.f = e.ep[0] * e.fmul + e.fadd;
     }
     return p;
 }
@@ -95,8 +103,13 @@ __device__ __forceinline__ float epi_apply(const MmEpi& e, const EpiPre& p, uint
         const uint32_t sec = n / e.D, i = n - sec * e.D;
         float out = y;
         if (sec < 2u) out = (n & 1u) ? __builtin_fmaf(y1, p.b, y * p.a) : __builtin_fmaf(y, p.a, -(y1 * p.b));
-        float* dst = sec == 0u ? e.q : (sec == 1u ? e.k : e.v);
-        dst[(size_t)m * e.D + i] = out;
+        if (e.ll) {
+            __hip_atomic_store(e.ll + (size_t)m * 3u * e.D + n, ((unsigned long long)p.f << 32) | f2u(out),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            float* dst = sec == 0u ? e.q : (sec == 1u ? e.k : e.v);
+            dst[(size_t)m * e.D + i] = out;
+        }
     } else {
         // SwiGLU of src/engine.cpp:832-838 on gate row j (group rows 0-15)
         // and up row j (rows 16-31): g * (1 / (1 + exp(-g))) * u
@@ -215,18 +228,20 @@ __device__ __forceinline__ float max4abs(float4 v) {
 //          does (max over the chunk maxima, f_c = exp(m_c - max), T and U
 //          fmaf chains over c in order, U * (1 / (T + 1e-10))), then the
 //          row quantized (quantize_activation_row).
+//
+// gemv_body is the workgroup's work as workgroup bx of gx; k_gemv runs it
+// as its own grid, k_qkv_attn as the first workgroups of a wider one.
 template <int FMT, int PRO, int EPI, bool GATED, int CPW, int MR>
-__global__ __launch_bounds__(64 * GEMV_WAVES) void k_gemv(GemvArgs a) {
+__device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32_t gx, uint8_t* smem) {
     constexpr uint32_t TB = g32_tile_bytes(FMT), CODES = g32_code_bytes(FMT);
     constexpr int SETS = sets_of<FMT>();
     constexpr uint32_t NT = 64u * GEMV_WAVES;
-    if (blockIdx.x >= (a.N >> 5)) {   // workgroups past the groups prefetch the next product's weights
-        prefetch_groups(a.nx, blockIdx.x, blockIdx.x - (a.N >> 5), gridDim.x - (a.N >> 5));
+    if (bx >= (a.N >> 5)) {   // workgroups past the groups prefetch the next product's weights
+        prefetch_groups(a.nx, bx, bx - (a.N >> 5), gx - (a.N >> 5));
         return;
     }
     if constexpr (GATED)
         if (*a.gate == 0u) return;   // no row of the pass needs this product
-    extern __shared__ __align__(16) uint8_t smem[];
     double* red = reinterpret_cast<double*>(smem);
     int8_t* act = reinterpret_cast<int8_t*>(smem + GEMV_WAVES * 64 * 4 * 8);
     const uint32_t K = a.K, M = a.M, kp = gemv_kp(K), nt = K / 64u, xs = a.xs, mlast = M - 1u;
@@ -312,7 +327,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void k_gemv(GemvArgs a) {
 
     // ---- weight loads
     const uint32_t nch = K >> 8, c0 = nch * wid / GEMV_WAVES, c1 = nch * (wid + 1) / GEMV_WAVES;
-    const uint8_t* tiles = a.W + (size_t)blockIdx.x * nch * TB;
+    const uint8_t* tiles = a.W + (size_t)bx * nch * TB;
     uint4 cw[CPW][SETS], sw[CPW];
 #pragma unroll
     for (int j = 0; j < CPW; j++) {
@@ -322,7 +337,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void k_gemv(GemvArgs a) {
         sw[j] = *reinterpret_cast<const uint4*>(tile + CODES + r * 16);
     }
     // ---- epilogue operands: thread t outputs row om of device row on
-    const uint32_t om = t >> 5, on = 32u * blockIdx.x + (t & 31u);
+    const uint32_t om = t >> 5, on = 32u * bx + (t & 31u);
     const EpiPre pre = epi_prefetch<EPI>(a.e, min(om, mlast), on);
 
     // ---- prologue arithmetic
@@ -552,8 +567,14 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void k_gemv(GemvArgs a) {
         float mx = fabsf(f);
 #pragma unroll
         for (int off = 16; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-        if (a.e.pmax && om < M && (t & 31u) == 0) a.e.pmax[(size_t)om * (a.N / 32u) + blockIdx.x] = mx;
+        if (a.e.pmax && om < M && (t & 31u) == 0) a.e.pmax[(size_t)om * (a.N / 32u) + bx] = mx;
     }
+}
+
+template <int FMT, int PRO, int EPI, bool GATED, int CPW, int MR>
+__global__ __launch_bounds__(64 * GEMV_WAVES) void k_gemv(GemvArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    gemv_body<FMT, PRO, EPI, GATED, CPW, MR>(a, blockIdx.x, gridDim.x, smem);
 }
 
 // =============================================================== GEMM

@@ -3,6 +3,7 @@
 #include "pf_gemv.hip"
 #include "pf_mm.hip"
 #include "pf_attn.hip"
+#include "pf_pass.hip"
 #include "pf_ctl.hip"
 
 #include <hip/hip_ext.h>
@@ -658,6 +659,41 @@ static void launch_attn(hipStream_t st, uint32_t hd, uint32_t M, uint32_t tasks,
     }
 #undef PF_ATTN_ROWS
 #undef PF_ATTN_LAUNCH
+}
+
+// The QKV product and the attention of a pass of at most 8 rows in one
+// launch (k_qkv_attn, pf_pass.hip), for Q4 attention matrices: rows held
+// per QKV workgroup as gemv_mr chooses (1, 5 or 8), attention rows per
+// block as launch_attn's table (M = 1 -> 1, 2 -> 2, 3 -> 3, 4-5 -> 2,
+// 6 -> 3, 7-8 -> 4).
+template <int MR, int P, int NR>
+static void qkv_attn_one(hipStream_t st, const GemvArgs& a, const AttnGroupArgs& b, uint32_t tasks, hipEvent_t ev0,
+                         hipEvent_t ev1) {
+    const uint32_t nq = a.N / 32;
+    static bool attr = false;   // LDS beyond 64 KiB is granted per kernel
+    if (!attr) {
+        (void)hipFuncSetAttribute((const void*)k_qkv_attn<FMT_Q4, MR, P, NR>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, qkv_attn_smem(GEMV_MAX_M, 2048, NR));
+        attr = true;
+    }
+    const uint32_t smem = qkv_attn_smem(a.M, a.K, NR);
+    const dim3 grid(nq + tasks * (b.M + (b.pf.p ? 1u : 0u)));
+    if (ev0)
+        hipExtLaunchKernelGGL((k_qkv_attn<FMT_Q4, MR, P, NR>), grid, dim3(512), smem, st, ev0, ev1, 0, a, b, nq, tasks);
+    else
+        hipLaunchKernelGGL((k_qkv_attn<FMT_Q4, MR, P, NR>), grid, dim3(512), smem, st, a, b, nq, tasks);
+}
+
+template <int P>
+static void qkv_attn_rows(hipStream_t st, const GemvArgs& a, const AttnGroupArgs& b, uint32_t tasks, hipEvent_t ev0,
+                          hipEvent_t ev1) {
+    switch (a.M) {
+        case 1: qkv_attn_one<1, P, 1>(st, a, b, tasks, ev0, ev1); break;
+        case 2: case 4: case 5: qkv_attn_one<5, P, 2>(st, a, b, tasks, ev0, ev1); break;
+        case 3: qkv_attn_one<5, P, 3>(st, a, b, tasks, ev0, ev1); break;
+        case 6: qkv_attn_one<8, P, 3>(st, a, b, tasks, ev0, ev1); break;
+        default: qkv_attn_one<8, P, 4>(st, a, b, tasks, ev0, ev1); break;
+    }
 }
 
 extern "C" pf_status pf_quantize_activation_rows(pf_ctx* c, const float* src, int8_t* dst, float* scales,
@@ -1316,6 +1352,14 @@ struct pf_engine {
     std::map<double, std::pair<double, uint32_t>> kev_by_size;   // bytes -> (us sum, launches)
     double verify_us = 0, base_us = 0;
     uint32_t verify_n = 0, base_n = 0;
+    // one launch for the QKV product and the attention of passes of at most
+    // 8 rows (k_qkv_attn, pf_pass.hip): the rows' q/k/v as LL words
+    // [MAX_PASS_ROWS][3 D], the pass epoch k_embed advances, and the flag a
+    // timed-out wait sets.  PF_QKV_ATTN=0 launches the two separately.
+    unsigned long long* ll = nullptr;
+    uint32_t* ep = nullptr;
+    uint32_t* ll_err = nullptr;
+    bool qkv_attn = true;
 };
 
 template <class T>
@@ -1417,7 +1461,13 @@ static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t ns
     if (!s) s = ealloc(e, &e->pdB, 1);
     if (!s) s = ealloc(e, &e->pdP, 1);
     if (!s) s = ealloc(e, &e->st, nseq);
+    if (!s) s = ealloc(e, &e->ll, (size_t)MAX_PASS_ROWS * 3 * D);
+    if (!s) s = ealloc(e, &e->ep, 2);
     if (s) { pf_engine_destroy(e); return s; }
+    e->ll_err = e->ep + 1;
+    PF_HIP(c, hipMemset(e->ll, 0, (size_t)MAX_PASS_ROWS * 3 * D * 8));
+    PF_HIP(c, hipMemset(e->ep, 0, 8));
+    if (const char* v = std::getenv("PF_QKV_ATTN")) e->qkv_attn = !(v[0] == '0');
     if (hipHostMalloc((void**)&e->word, 64, hipHostMallocDefault) != hipSuccess) {
         pf_engine_destroy(e);
         return fail(c, PF_ERR_HIP, "hipHostMalloc failed");
@@ -1711,6 +1761,20 @@ static void launch_skip_commit(pf_engine* e, const PassDesc* pd, uint32_t M, uin
                        e->skip_ctr);
 }
 
+// A wait of k_qkv_attn's attention blocks that ran out of rounds (its
+// results are invalid): reported by the call that ran the passes, and
+// cleared.  Waits end within microseconds in practice; the bound only keeps a
+// launch from running forever.
+static pf_status ll_check(pf_engine* e) {
+    uint32_t v = 0;
+    PF_HIP(e->c, hipMemcpyAsync(&v, e->ll_err, 4, hipMemcpyDeviceToHost, e->c->stream));
+    PF_HIP(e->c, hipStreamSynchronize(e->c->stream));
+    if (!v) return PF_OK;
+    PF_HIP(e->c, hipMemsetAsync(e->ll_err, 0, 4, e->c->stream));
+    PF_HIP(e->c, hipStreamSynchronize(e->c->stream));
+    return fail(e->c, PF_ERR_DEVICE, "a wait for the QKV product's rows timed out inside k_qkv_attn");
+}
+
 // One forward pass of M rows (the PassDesc at `pd` holds positions and
 // tokens; pos0 is the host's copy of the first position).  hidden/logits
 // outputs are device [M][D] / [M][V]; either may be null.  A batched pass
@@ -1753,7 +1817,7 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
     hipLaunchKernelGGL(k_pool_rows, dim3(g.n_layers * g.n_heads, batch ? M : e->pool_rows_max), tb, 0, st, g, e->kv,
                        pd);
     hipLaunchKernelGGL(k_embed, dim3((D + 255) / 256, M), dim3(256), 0, st, m->emb->data, m->emb->scales, d.n_vocab, D,
-                       pd, e->x);
+                       pd, e->x, e->ep);
     for (uint32_t l = 0; l < d.n_layers; l++) {
         const float* an = m->attn_norm + (size_t)l * D;
         const float* fn = m->ffn_norm + (size_t)l * D;
@@ -1765,7 +1829,12 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         if (tall)
             PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_norm_quant<PER>, dim3(M), dim3(1024), 0, st, (const float*)e->x,
                                                     D, an, e->act, ks, as0));
-        if (pf_status s = pass_mm(e, m->qkv[l], MM_QKV, M, a, as0)) return s;
+        // passes of at most 8 rows: the QKV product and the attention in one
+        // launch (its attention blocks load the cached K/V rows while the
+        // product runs)
+        const bool qa = e->qkv_attn && !tall && attn_fused(M) && m->qkv[l]->fmt == FMT_Q4 && (hd == 64 || hd == 128);
+        if (!qa)
+            if (pf_status s = pass_mm(e, m->qkv[l], MM_QKV, M, a, as0)) return s;
         if (!attn_fused(M))
             hipLaunchKernelGGL(k_kv_store_pass, dim3(M, H), dim3(64), 0, st, (const PassDesc*)pd, g, e->kv, l,
                                (const float*)e->k, (const float*)e->v);
@@ -1786,9 +1855,24 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         // whose O workgroups read them; other passes run the merge kernel,
         // whose extra blocks do.  Each decode GEMV's extra blocks do the same
         // for the next product (O -> gate|up -> down -> next layer's QKV).
-        launch_attn(st, hd, M, attn_tasks, pd, g, e->kv, l, e->q, e->k, e->v, e->S, e->s_stride, e->Wp,
-                    e->cstride, merge_in_o ? prefetch_of(e, m->o[l], e->pf_blocks) : prefetch_of(e, nullptr, 0), batch,
-                    batch ? e->batch_group : 0u, aev0, aev1);
+        const Prefetch opf = merge_in_o ? prefetch_of(e, m->o[l], e->pf_blocks) : prefetch_of(e, nullptr, 0);
+        if (qa) {
+            a.W = m->qkv[l]->data;
+            a.N = m->qkv[l]->rows;
+            a.K = m->qkv[l]->cols;
+            a.M = M;
+            a.e.ll = e->ll;
+            a.e.ep = e->ep;
+            a.e.fmul = d.n_layers;
+            a.e.fadd = l;
+            const AttnGroupArgs b{pd, g, e->kv, l, M, e->S, e->s_stride, e->Wp, e->cstride, opf,
+                                  LLIn{e->ll, e->ep, d.n_layers, l, e->ll_err}};
+            if (hd == 64) qkv_attn_rows<4>(st, a, b, attn_tasks, aev0, aev1);
+            else qkv_attn_rows<8>(st, a, b, attn_tasks, aev0, aev1);
+        } else {
+            launch_attn(st, hd, M, attn_tasks, pd, g, e->kv, l, e->q, e->k, e->v, e->S, e->s_stride, e->Wp,
+                        e->cstride, opf, batch, batch ? e->batch_group : 0u, aev0, aev1);
+        }
         if (!merge_in_o)
             PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_attn_merge_quant<PER>, dim3(M + e->pf_blocks), dim3(1024), 0, st,
                                                     pd, g, (const float*)e->S, e->s_stride, (const float*)e->Wp,
@@ -1882,7 +1966,7 @@ extern "C" pf_status pf_forward(pf_engine* e, const int32_t* tokens, uint32_t n,
         PF_HIP(c, hipMemcpyAsync(logits, e->logitsA, (size_t)n * d.n_vocab * 4, hipMemcpyDeviceToHost, c->stream));
     if (hidden) PF_HIP(c, hipMemcpyAsync(hidden, e->hiddenA, (size_t)n * d.n_embd * 4, hipMemcpyDeviceToHost, c->stream));
     PF_HIP(c, hipStreamSynchronize(c->stream));
-    return PF_OK;
+    return ll_check(e);
 }
 
 // MTPHeads::forward chain on the device hidden state h0 (src/mtp.cpp:63-127):
@@ -2252,6 +2336,7 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
     PF_HIP(c, hipMemcpyAsync(&sf, e->st, sizeof(sf), hipMemcpyDeviceToHost, st));
     PF_HIP(c, hipStreamSynchronize(st));
     auto t2 = std::chrono::steady_clock::now();
+    if (pf_status s = ll_check(e)) return s;
     if (sf.pos != e->pos) return fail(c, PF_ERR_STATE, "device and host positions diverged");
     const uint32_t nt = std::min(sf.n_tokens, tokens_cap);
     PF_HIP(c, hipMemcpy(tokens_out, e->tokens, (size_t)nt * 4, hipMemcpyDeviceToHost));
