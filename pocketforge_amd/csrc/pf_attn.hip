@@ -1026,31 +1026,29 @@ __device__ __forceinline__ void attn_group_body(const PassDesc* __restrict__ pd,
     }
     // K and V rows: 16-byte piece pi = t + 256 i is part pi % PARTS of
     // entry pi / PARTS, so a wave reads 64 / PARTS whole rows per load
+    // (waves 0-3 only).  Every load of a wave is issued unconditionally:
+    // list index j0 + e past the visible entries still names a valid row of
+    // the plane (chunk_row stays inside the sink, pooled or ring rows), and
+    // the staging below keeps only the entries it needs, so no wait
+    // separates the loads.
     int4 kw[PARTS], vw[PARTS];
 #pragma unroll
-    for (uint32_t i = 0; i < (uint32_t)PARTS; i++) {
-        const uint32_t pi = t + 256u * i, e = pi / PARTS, part = pi % PARTS;
-        kw[i] = make_int4(0, 0, 0, 0);
-        vw[i] = make_int4(0, 0, 0, 0);
-        if (!hi && e < nvis) {
-            const uint32_t pos = FUSED ? entry_pos(g, vL, j0 + e) : 0xFFFFFFFFu;
-            if (pos == 0xFFFFFFFFu || pos < p_first) {
-                const size_t row = plane * g.rows + chunk_row(g, vL, j0 + e, wstart, wb);
-                kw[i] = reinterpret_cast<const int4*>(kv.k + row * hd)[part];
-                vw[i] = reinterpret_cast<const int4*>(kv.v + row * hd)[part];
-            }
-        }
-    }
+    for (uint32_t i = 0; i < (uint32_t)PARTS; i++) kw[i] = vw[i] = make_int4(0, 0, 0, 0);
     float ks = 0.0f, vs = 0.0f;
     bool pend = false;
-    if (t < nvis) {
-        const uint32_t pos = FUSED ? entry_pos(g, vL, j0 + t) : 0xFFFFFFFFu;
-        pend = pos != 0xFFFFFFFFu && pos >= p_first;
-        if (!pend) {
-            const size_t row = plane * g.rows + chunk_row(g, vL, j0 + t, wstart, wb);
-            ks = kv.ks[row];
-            vs = kv.vs[row];
+    if (!hi) {
+#pragma unroll
+        for (uint32_t i = 0; i < (uint32_t)PARTS; i++) {
+            const uint32_t pi = t + 256u * i, e = pi / PARTS, part = pi % PARTS;
+            const size_t row = plane * g.rows + chunk_row(g, vL, j0 + e, wstart, wb);
+            kw[i] = reinterpret_cast<const int4*>(kv.k + row * hd)[part];
+            vw[i] = reinterpret_cast<const int4*>(kv.v + row * hd)[part];
         }
+        const uint32_t pos = FUSED ? entry_pos(g, vL, j0 + t) : 0xFFFFFFFFu;
+        pend = t < nvis && pos != 0xFFFFFFFFu && pos >= p_first;
+        const size_t row = plane * g.rows + chunk_row(g, vL, j0 + t, wstart, wb);
+        ks = kv.ks[row];
+        vs = kv.vs[row];
     }
     // the cached rows into LDS (pass rows quantized here take other slots)
     auto stage_cached = [&]() {
@@ -1066,8 +1064,8 @@ __device__ __forceinline__ void attn_group_body(const PassDesc* __restrict__ pd,
             }
         }
         if (!hi && !pend) {               // 0 past the visible entries: their terms below add exactly 0
-            ksc[t] = ks;
-            vsc[t] = vs;
+            ksc[t] = t < nvis ? ks : 0.0f;
+            vsc[t] = t < nvis ? vs : 0.0f;
         }
     };
     if constexpr (LL) {
