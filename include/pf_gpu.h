@@ -242,6 +242,7 @@ typedef struct {
     int32_t oom_protected;
     uint32_t rounds;          /* MTP rounds */
     uint32_t passes;          /* forward passes issued (prefill excluded) */
+    uint32_t continued;       /* rounds whose one-row first verify segment was continued by a second one */
     double prefill_seconds;
     double decode_seconds;
 } pf_gen_result;  /* GenerationResult, include/forge/types.hpp:260-268 */

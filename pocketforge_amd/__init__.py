@@ -46,7 +46,7 @@ class Sampling(C.Structure):
 class GenResult(C.Structure):
     _fields_ = [("n_tokens", C.c_uint32), ("mtp_accepted", C.c_int32), ("mtp_rejected", C.c_int32),
                 ("oom_protected", C.c_int32), ("rounds", C.c_uint32), ("passes", C.c_uint32),
-                ("prefill_seconds", C.c_double), ("decode_seconds", C.c_double)]
+                ("continued", C.c_uint32), ("prefill_seconds", C.c_double), ("decode_seconds", C.c_double)]
 
 
 class SqueezeInfo(C.Structure):

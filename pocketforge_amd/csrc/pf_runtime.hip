@@ -2301,6 +2301,7 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
                 e->pos += m;
                 if (pf_status s = segment(e->cont_exec, true, false, true, NM)) return s;
                 res->passes += 1;
+                res->continued += 1;
                 w = e->word[0];
                 a = w & 0xFFu;
                 pushed = (w >> 8) & 1u;

@@ -46,6 +46,51 @@ def test_config_s_full_greedy_stream(gpu):
     assert (res.mtp_accepted, res.mtp_rejected) == (oa, orj)
 
 
+def _repeating_1b():
+    """The 1B shapes with layer matrices N(0, 0.016^2), the Q4 tied embedding
+    N(0, 0.02^2) and zero MTP heads: the residual stream stays close to the
+    token's embedding, so the model mostly repeats its input and most greedy
+    drafts are accepted (the oracle accepts 29 and rejects 3 over 40 tokens
+    after a 16-token prompt).  Random N(0, 0.02^2) weights accept none."""
+    cfg = W.ONE_B
+    w = W.make_weights(cfg, seed=1234, std=0.016)
+    codes, scales = pf.gen_matrix(1234, 0x10000, 0.02, cfg["n_vocab"], cfg["n_embd"], pf.FMT_Q4)
+    w["emb"] = (pf.FMT_Q4, codes, scales)
+    for hw in w["mtp"]:
+        for n in ("gate", "up", "down"):
+            fmt, c, sc = hw[n]
+            hw[n] = (fmt, np.full_like(c, 0x88), np.zeros_like(sc))
+    return cfg, w
+
+
+def test_config_b_accepted_drafts_stream(gpu):
+    """Acceptance at the 1B shape: the rounds that commit every row of a
+    verify pass, reuse its last row as the next base pass, and continue a
+    one-row first segment with a second one, under both verify policies,
+    against the oracle's stream and counters."""
+    cfg, w = _repeating_1b()
+    prompt = W.prompt_ids(16, cfg["n_vocab"], seed=42)
+    kv = dict(sink_size=4, window_size=8192, pool_block=64, max_context=256)
+    samp = pf.Sampling(0.8, 0.95, 40, 1)
+    c = dict(cfg)
+    c.update(kv)
+    om = O.Model(c, w)
+    ot, oa, orj = om.generate(prompt, 40, O.Sampling(0.8, 0.95, 40, 1), 7)
+    om.close()
+    assert oa > 20 and orj > 0
+    m = pf.Model(gpu, cfg, w)
+    for full in (0, 1):
+        e = pf.Engine(m, **kv)
+        e.set_verify_full(full)
+        toks, res = e.generate(prompt, 40, samp, 7)
+        np.testing.assert_array_equal(toks, ot, err_msg=f"verify_full={full}")
+        assert (res.mtp_accepted, res.mtp_rejected) == (oa, orj)
+        if not full:
+            assert res.continued > 0
+        e.close()
+    m.close()
+
+
 def test_config_bmix_top_p_prefix(gpu):
     cfg = W.ONE_B
     w = W.make_weights(cfg, seed=1234, fmts=W.MIXED)

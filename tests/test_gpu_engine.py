@@ -155,6 +155,40 @@ def test_generate_verify_segments(gpu, tiny_weights, case, full):
     m.close()
 
 
+@pytest.mark.parametrize("samp,std", [(TOP_P, 0.15), (TEMP, 0.18)], ids=["top_p", "temperature"])
+@pytest.mark.parametrize("full", [0, 1])
+def test_generate_verify_segments_stochastic(gpu, tiny_weights, samp, std, full):
+    """Stochastic sampling through both verify policies, on weights whose
+    drafts are accepted often but not always: every layer and head matrix
+    zero and an embedding of std 0.15 / 0.18, so that a token's logits peak
+    at the token itself (the oracle accepts 23 and rejects 17 drafts with
+    top-p, 28 and 13 with temperature sampling).  Under the default policy a
+    round after one with no accepted draft verifies d0 alone; when d0 is
+    accepted the round continues with a second segment, and a draft
+    rejected there takes its corrective from that segment's row
+    (k_sample reads row round_acc of the verify logits)."""
+    cfg, _ = tiny_weights
+    w = _zero_mats(W.make_weights(cfg, seed=31, std=std))
+    prompt = W.prompt_ids(12, cfg["n_vocab"], seed=4)
+    m = pf.Model(gpu, cfg, w)
+    e = pf.Engine(m, **KV)
+    e.set_verify_full(full)
+    toks, res = e.generate(prompt, 60, samp, 99)
+    om = _oracle(cfg, w, KV)
+    ot, oa, orj = om.generate(prompt, 60, O.Sampling(samp.temperature, samp.top_p, samp.top_k, samp.greedy), 99)
+    om.close()
+    np.testing.assert_array_equal(toks, ot)
+    assert (res.mtp_accepted, res.mtp_rejected) == (oa, orj)
+    assert oa > 10 and orj > 10
+    if full:
+        assert res.continued == 0
+    else:
+        assert res.continued > 0            # second segments ran
+        assert res.passes > res.rounds + res.continued
+    e.close()
+    m.close()
+
+
 @pytest.mark.parametrize("samp", [TOP_P, TEMP, TOP_K], ids=["top_p", "temperature", "top_k"])
 def test_generate_stochastic_matches_oracle(gpu, tiny_weights, samp):
     cfg, w = tiny_weights
