@@ -46,14 +46,17 @@ typedef struct pf_kv pf_kv;
 typedef struct pf_matrix pf_matrix;
 
 /* Weight formats: 32-element blocks with an fp16 scale d.
- * Interchange layout (host): codes [rows][cols/32][16 (Q4) | 8 (Q2, Q1.5)]
- * with the reference's element order (Q4: byte j = elements 2j (low
- * nibble) and 2j+1, code = nibble - 8; Q2: byte j = elements 4j..4j+3 at
- * bits 0,2,4,6, code = c - 2; Q1.5: same packing, code = c - 1 for
- * c in {0,1,2}), scales [rows][cols/32] as IEEE binary16 bits. */
+ * Interchange layout (host): codes [rows][cols/32][16 (Q4) | 8 (Q2, Q1.5)
+ * | 32 (Q8)] with the reference's element order (Q4: byte j = elements 2j
+ * (low nibble) and 2j+1, code = nibble - 8; Q2: byte j = elements
+ * 4j..4j+3 at bits 0,2,4,6, code = c - 2; Q1.5: same packing, code = c - 1
+ * for c in {0,1,2}; Q8: byte j = element j, code = the signed byte, as
+ * Q8_0 of include/forge/types.hpp:17-20), scales [rows][cols/32] as IEEE
+ * binary16 bits. */
 #define PF_FMT_Q4 0
 #define PF_FMT_Q2 1
 #define PF_FMT_Q15 2
+#define PF_FMT_Q8 3
 
 /* Matrix ids within a layer follow the .squeeze matrix ids of
  * src/quant_tool.cpp (0-6 = Q K V O gate up down). */
@@ -186,6 +189,9 @@ pf_status pf_model_set_matrix(pf_model* m, uint32_t layer, int32_t id, int32_t f
                               const uint16_t* scales);
 /* Tied embedding / unembedding table [n_vocab][n_embd], Q4. */
 pf_status pf_model_set_embedding(pf_model* m, const uint8_t* codes, const uint16_t* scales);
+/* The same in format fmt: PF_FMT_Q4 or PF_FMT_Q8 (the .squeeze default,
+ * src/quant_tool.cpp:193-194). */
+pf_status pf_model_set_embedding_fmt(pf_model* m, int32_t fmt, const uint8_t* codes, const uint16_t* scales);
 /* MTP head k matrix which (0 gate, 1 up, 2 down), n_embd x n_embd Q4. */
 pf_status pf_model_set_mtp(pf_model* m, uint32_t head, int32_t which, const uint8_t* codes,
                            const uint16_t* scales);

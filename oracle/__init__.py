@@ -15,7 +15,7 @@ _LIB = os.path.join(_HERE, "_build", "liboracle.so")
 _REF = os.path.join(_HERE, "_ref", "libforge_ref.so")
 _REF_NOFMA = os.path.join(_HERE, "_ref", "libforge_ref_nofma.so")
 
-Q4, Q2, Q15 = 0, 1, 2
+Q4, Q2, Q15, Q8 = 0, 1, 2, 3
 
 f32p = C.POINTER(C.c_float)
 i8p = C.POINTER(C.c_int8)
@@ -211,7 +211,7 @@ def qmat(fmt, codes, scales):
 def quantize_matrix(w, fmt):
     w = np.ascontiguousarray(w, dtype=np.float32)
     rows, cols = w.shape
-    bb = 16 if fmt == Q4 else 8
+    bb = {Q4: 16, Q8: 32}.get(fmt, 8)
     codes = np.zeros((rows, cols // 32, bb), np.uint8)
     scales = np.zeros((rows, cols // 32), np.uint16)
     lib().orc_quantize_matrix(ptr(w, f32p), rows, cols, fmt, ptr(codes, u8p), ptr(scales, u16p))

@@ -338,12 +338,13 @@ void orc_engine_rmsnorm(float* out, const float* x, const float* w, uint32_t n) 
 
 /* ============================================== block-quantized matrices */
 
-uint32_t orc_block_bytes(int32_t fmt) { return fmt == ORC_Q4 ? 16u : 8u; }
+uint32_t orc_block_bytes(int32_t fmt) { return fmt == ORC_Q8 ? 32u : (fmt == ORC_Q4 ? 16u : 8u); }
 
 /* Code of element (row, col) as the signed integer multiplier of d. */
 int orc_block_code(const orc_qmat* W, uint32_t row, uint32_t col) {
     uint32_t nb = W->cols / 32, b = col / 32, i = col % 32;
     const uint8_t* blk = W->codes + ((size_t)row * nb + b) * orc_block_bytes(W->fmt);
+    if (W->fmt == ORC_Q8) return (int)(int8_t)blk[i];   /* Q8_0, include/forge/types.hpp:17-20 */
     if (W->fmt == ORC_Q4) {
         uint8_t byte = blk[i / 2];
         return (int)((i & 1) ? (byte >> 4) : (byte & 15)) - 8;
@@ -372,7 +373,17 @@ void orc_quantize_matrix(const float* w, uint32_t rows, uint32_t cols, int32_t f
             for (int i = 0; i < 32; i++) { float a = fabsf(x[i]); if (a > amax) amax = a; }
             memset(q, 0, bb);
             uint16_t d16 = 0;
-            if (fmt == ORC_Q4) {
+            if (fmt == ORC_Q8) {
+                /* symmetric, as the activation rows: code = round(x * 127 / amax)
+                 * (the reference's round(x s + 0.5) of src/quant_format.cpp:68
+                 * is kept only for codes read from its files) */
+                float inv = (amax == 0.0f) ? 0.0f : 127.0f / amax;
+                for (int i = 0; i < 32; i++) {
+                    int v = (int)roundf(x[i] * inv);
+                    q[i] = (uint8_t)(int8_t)(v < -127 ? -127 : (v > 127 ? 127 : v));
+                }
+                d16 = orc_f32_to_f16(amax / 127.0f);
+            } else if (fmt == ORC_Q4) {
                 float inv = (amax == 0.0f) ? 0.0f : 7.0f / amax;
                 for (int i = 0; i < 32; i += 2) {
                     int v0 = (int)(int8_t)roundf(x[i] * inv);
@@ -409,7 +420,7 @@ void orc_quantize_matrix(const float* w, uint32_t rows, uint32_t cols, int32_t f
             int e = (d16 >> 10) & 31; if (e == 0) e = 1;
             if ((d16 & 0x7FFF) && e < emax - 15) {
                 uint8_t* q = codes + ((size_t)r * nb + b) * bb;
-                uint8_t zero = fmt == ORC_Q4 ? 0x88 : (fmt == ORC_Q2 ? 0xAA : 0x55);
+                uint8_t zero = fmt == ORC_Q8 ? 0x00 : (fmt == ORC_Q4 ? 0x88 : (fmt == ORC_Q2 ? 0xAA : 0x55));
                 memset(q, zero, bb);
                 scales[(size_t)r * nb + b] = 0;
             }
@@ -421,7 +432,9 @@ void orc_quantize_matrix(const float* w, uint32_t rows, uint32_t cols, int32_t f
 static void decode_block(const orc_qmat* W, uint32_t row, uint32_t b, int8_t* w) {
     uint32_t nb = W->cols / 32;
     const uint8_t* blk = W->codes + ((size_t)row * nb + b) * orc_block_bytes(W->fmt);
-    if (W->fmt == ORC_Q4) {
+    if (W->fmt == ORC_Q8) {
+        for (int j = 0; j < 32; j++) w[j] = (int8_t)blk[j];
+    } else if (W->fmt == ORC_Q4) {
         for (int j = 0; j < 16; j++) {
             w[2 * j] = (int8_t)((blk[j] & 15) - 8);
             w[2 * j + 1] = (int8_t)((blk[j] >> 4) - 8);
@@ -436,7 +449,7 @@ static void decode_block(const orc_qmat* W, uint32_t row, uint32_t b, int8_t* w)
     }
 }
 
-/* Dequantized row: (float)code * d, exact in fp32 (4-bit x 11-bit). */
+/* Dequantized row: (float)code * d, exact in fp32 (8-bit x 11-bit). */
 void orc_dequant_row(const orc_qmat* W, uint32_t row, float* out) {
     uint32_t nb = W->cols / 32;
     int8_t w[32];

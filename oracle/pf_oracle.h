@@ -51,10 +51,10 @@ void  orc_rmsnorm(float* out, const float* x, const float* w, uint32_t n);
 void  orc_engine_rmsnorm(float* out, const float* x, const float* w, uint32_t n);
 
 /* ------------------------------------------------- block-quant matrices */
-enum { ORC_Q4 = 0, ORC_Q2 = 1, ORC_Q15 = 2 };
+enum { ORC_Q4 = 0, ORC_Q2 = 1, ORC_Q15 = 2, ORC_Q8 = 3 };
 
 typedef struct {
-    int32_t         fmt;     /* ORC_Q4 / ORC_Q2 / ORC_Q15 */
+    int32_t         fmt;     /* ORC_Q4 / ORC_Q2 / ORC_Q15 / ORC_Q8 */
     uint32_t        rows;    /* N: output features */
     uint32_t        cols;    /* K: input features, multiple of 32 */
     const uint8_t*  codes;   /* [rows][cols/32][16 (Q4) | 8 (Q2, Q1.5)] */

@@ -14,7 +14,12 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_lib", "libpocketforge_amd.so")
 
-FMT_Q4, FMT_Q2, FMT_Q15 = 0, 1, 2
+FMT_Q4, FMT_Q2, FMT_Q15, FMT_Q8 = 0, 1, 2, 3
+
+
+def block_bytes(fmt):
+    """Code bytes of one 32-element block in the interchange layout."""
+    return {FMT_Q4: 16, FMT_Q8: 32}.get(fmt, 8)
 MAT_Q, MAT_K, MAT_V, MAT_O, MAT_GATE, MAT_UP, MAT_DOWN = range(7)
 
 f32p = C.POINTER(C.c_float)
@@ -102,6 +107,7 @@ SYMBOLS = {
     "pf_model_destroy": (None, [vp]),
     "pf_model_set_matrix": (C.c_int32, [vp, C.c_uint32, C.c_int32, C.c_int32, u8p, u16p]),
     "pf_model_set_embedding": (C.c_int32, [vp, u8p, u16p]),
+    "pf_model_set_embedding_fmt": (C.c_int32, [vp, C.c_int32, u8p, u16p]),
     "pf_model_set_mtp": (C.c_int32, [vp, C.c_uint32, C.c_int32, u8p, u16p]),
     "pf_model_set_norm": (C.c_int32, [vp, C.c_uint32, C.c_int32, f32p]),
     "pf_engine_create": (C.c_int32, [vp, C.POINTER(CacheDesc), C.POINTER(vp)]),
@@ -214,7 +220,7 @@ class DeviceArray:
 
 def gen_matrix(seed, stream, std, rows, cols, fmt):
     """N(0, std^2) weights quantized to a 32-block format (interchange layout)."""
-    bb = 16 if fmt == FMT_Q4 else 8
+    bb = block_bytes(fmt)
     codes = np.zeros((rows, cols // 32, bb), np.uint8)
     scales = np.zeros((rows, cols // 32), np.uint16)
     rc = lib().pf_gen_matrix(seed, stream, std, rows, cols, fmt, P(codes, u8p), P(scales, u16p))
@@ -226,7 +232,7 @@ def gen_matrix(seed, stream, std, rows, cols, fmt):
 def quantize_matrix(w, fmt):
     w = np.ascontiguousarray(w, np.float32)
     rows, cols = w.shape
-    bb = 16 if fmt == FMT_Q4 else 8
+    bb = block_bytes(fmt)
     codes = np.zeros((rows, cols // 32, bb), np.uint8)
     scales = np.zeros((rows, cols // 32), np.uint16)
     rc = lib().pf_quantize_matrix(P(w, f32p), rows, cols, fmt, P(codes, u8p), P(scales, u16p))
@@ -543,7 +549,8 @@ class Model:
                 ctx.check(lib().pf_model_set_matrix(self.h, l, j, fmt, P(codes, u8p), P(scales, u16p)),
                           f"pf_model_set_matrix({l},{n})")
         fmt, codes, scales = weights["emb"]
-        ctx.check(lib().pf_model_set_embedding(self.h, P(codes, u8p), P(scales, u16p)), "pf_model_set_embedding")
+        ctx.check(lib().pf_model_set_embedding_fmt(self.h, fmt, P(codes, u8p), P(scales, u16p)),
+                  "pf_model_set_embedding_fmt")
         for k in range(cfg["n_mtp"]):
             for j, n in enumerate(["gate", "up", "down"]):
                 fmt, codes, scales = weights["mtp"][k][n]

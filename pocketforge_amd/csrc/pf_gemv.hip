@@ -45,7 +45,9 @@ __device__ __forceinline__ void stage_rows(const float* __restrict__ h, uint32_t
 // total_waves, ..., loading the codes and scales of RB rows before their
 // products (the tied unembedding gives each wave 8 rows).  Grid y takes
 // the activation rows M at a time: slice y serves rows M y .. M y + M - 1.
-template <int M>
+// FMT: Q4 (16 code bytes per block: weight (nibble - 8) d, formed as
+// fmaf(nibble, d, -8 d), exact) or Q8 (32: weight (float)code * d, exact).
+template <int M, int FMT>
 __global__ __launch_bounds__(256) void k_gemv_f32(const uint8_t* __restrict__ codes,
                                                   const uint16_t* __restrict__ scales,
                                                   uint32_t N, uint32_t K,
@@ -64,15 +66,19 @@ __global__ __launch_bounds__(256) void k_gemv_f32(const uint8_t* __restrict__ co
     stage_rows<M>(h, h_stride, K, lane, live, hv);
     constexpr uint32_t RB = M == 1 ? 8u : (M <= 4 ? 4u : 2u);
     for (uint32_t n0 = wave; n0 < N; n0 += RB * nwaves) {
-        uint4 cr[RB];
+        constexpr uint32_t CB = FMT == FMT_Q8 ? 2u : 1u;   // 16-byte code words per block
+        uint4 cr[RB][CB];
         float dr[RB];
 #pragma unroll
         for (uint32_t q = 0; q < RB; q++) {
             const uint32_t n = n0 + q * nwaves;
-            cr[q] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+            for (uint32_t u = 0; u < CB; u++) cr[q][u] = make_uint4(0u, 0u, 0u, 0u);
             dr[q] = 0.0f;
             if (live && n < N) {
-                cr[q] = *reinterpret_cast<const uint4*>(codes + ((size_t)n * nb + lane) * 16u);
+#pragma unroll
+                for (uint32_t u = 0; u < CB; u++)
+                    cr[q][u] = *reinterpret_cast<const uint4*>(codes + ((size_t)n * nb + lane) * (16u * CB) + 16u * u);
                 dr[q] = h2f(scales[(size_t)n * nb + lane]);
             }
         }
@@ -85,16 +91,27 @@ __global__ __launch_bounds__(256) void k_gemv_f32(const uint8_t* __restrict__ co
             for (int m = 0; m < M; m++) acc[m] = 0.0f;
             if (live) {
                 const float d = dr[q], nd = -8.0f * d;
-                const uint32_t cw[4] = {cr[q].x, cr[q].y, cr[q].z, cr[q].w};
+                if constexpr (FMT == FMT_Q8) {
+                    const uint32_t cw[8] = {cr[q][0].x, cr[q][0].y, cr[q][0].z, cr[q][0].w,
+                                            cr[q][1].x, cr[q][1].y, cr[q][1].z, cr[q][1].w};
 #pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    uint32_t byte = (cw[j >> 2] >> (8 * (j & 3))) & 0xFFu;
-                    float w0 = __builtin_fmaf((float)(byte & 15u), d, nd);
-                    float w1 = __builtin_fmaf((float)(byte >> 4), d, nd);
+                    for (int j = 0; j < 32; j++) {
+                        const float wj = (float)(int8_t)((cw[j >> 2] >> (8 * (j & 3))) & 0xFFu) * d;
 #pragma unroll
-                    for (int m = 0; m < M; m++) {
-                        acc[m] = __builtin_fmaf(hv[m][2 * j], w0, acc[m]);
-                        acc[m] = __builtin_fmaf(hv[m][2 * j + 1], w1, acc[m]);
+                        for (int m = 0; m < M; m++) acc[m] = __builtin_fmaf(hv[m][j], wj, acc[m]);
+                    }
+                } else {
+                    const uint32_t cw[4] = {cr[q][0].x, cr[q][0].y, cr[q][0].z, cr[q][0].w};
+#pragma unroll
+                    for (int j = 0; j < 16; j++) {
+                        uint32_t byte = (cw[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+                        float w0 = __builtin_fmaf((float)(byte & 15u), d, nd);
+                        float w1 = __builtin_fmaf((float)(byte >> 4), d, nd);
+#pragma unroll
+                        for (int m = 0; m < M; m++) {
+                            acc[m] = __builtin_fmaf(hv[m][2 * j], w0, acc[m]);
+                            acc[m] = __builtin_fmaf(hv[m][2 * j + 1], w1, acc[m]);
+                        }
                     }
                 }
             }
@@ -390,12 +407,13 @@ __global__ void k_copy_f32(const float* __restrict__ src, float* __restrict__ ds
     if (i < n) dst[i] = src[i];
 }
 
-// Token embedding: x[m] = dequantized row tok[m] of the tied Q4 table.
+// Token embedding: x[m] = dequantized row tok[m] of the tied table (Q4 or
+// Q8, fmt).
 // The first kernel of every pass also advances the pass epoch `ep`, which
 // names the pass in the flags of the LL words its QKV products write.
 __global__ void k_embed(const uint8_t* __restrict__ codes, const uint16_t* __restrict__ scales,
                         uint32_t V, uint32_t D, const PassDesc* __restrict__ pd, float* __restrict__ x,
-                        uint32_t* __restrict__ ep) {
+                        uint32_t* __restrict__ ep, int32_t fmt) {
     uint32_t m = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
     if (ep && m == 0 && i == 0) ep[0] += 1u;
     if (m >= pd->m || i >= D) return;
@@ -403,10 +421,14 @@ __global__ void k_embed(const uint8_t* __restrict__ codes, const uint16_t* __res
     float val = 0.0f;
     if (tok >= 0 && (uint32_t)tok < V) {
         uint32_t nb = D >> 5, b = i >> 5, e = i & 31u;
-        uint8_t byte = codes[((size_t)tok * nb + b) * 16u + (e >> 1)];
-        uint32_t nib = (e & 1u) ? (byte >> 4) : (byte & 15u);
         float d = h2f(scales[(size_t)tok * nb + b]);
-        val = (float)((int)nib - 8) * d;
+        if (fmt == FMT_Q8) {
+            val = (float)(int8_t)codes[((size_t)tok * nb + b) * 32u + e] * d;
+        } else {
+            uint8_t byte = codes[((size_t)tok * nb + b) * 16u + (e >> 1)];
+            uint32_t nib = (e & 1u) ? (byte >> 4) : (byte & 15u);
+            val = (float)((int)nib - 8) * d;
+        }
     }
     x[(size_t)m * D + i] = val;
 }

@@ -63,8 +63,11 @@ int half_exponent(uint16_t h) {
 int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
 // One row of blocks.  Returns nothing; codes/scales advance by the row.
+uint32_t block_bytes(int fmt) { return fmt == PF_FMT_Q8 ? 32 : (fmt == PF_FMT_Q4 ? 16 : 8); }
+uint8_t zero_code(int fmt) { return fmt == PF_FMT_Q8 ? 0x00 : (fmt == PF_FMT_Q4 ? 0x88 : (fmt == PF_FMT_Q2 ? 0xAA : 0x55)); }
+
 void quantize_row(const float* x, uint32_t cols, int fmt, uint8_t* codes, uint16_t* scales) {
-    const uint32_t nb = cols / 32, bb = fmt == PF_FMT_Q4 ? 16 : 8;
+    const uint32_t nb = cols / 32, bb = block_bytes(fmt);
     int emax = 0;
     for (uint32_t b = 0; b < nb; b++) {
         const float* v = x + 32 * b;
@@ -73,7 +76,12 @@ void quantize_row(const float* x, uint32_t cols, int fmt, uint8_t* codes, uint16
         float amax = 0.0f;
         for (int i = 0; i < 32; i++) amax = std::max(amax, std::fabs(v[i]));
         uint16_t d = 0;
-        if (fmt == PF_FMT_Q4) {
+        if (fmt == PF_FMT_Q8) {
+            // symmetric: code = round(x * 127 / amax), d = amax / 127
+            const float s = amax == 0.0f ? 0.0f : 127.0f / amax;
+            for (int i = 0; i < 32; i++) q[i] = (uint8_t)(int8_t)clampi((int)std::round(v[i] * s), -127, 127);
+            d = to_half(amax / 127.0f);
+        } else if (fmt == PF_FMT_Q4) {
             const float s = amax == 0.0f ? 0.0f : 7.0f / amax;
             for (int i = 0; i < 32; i += 2) {
                 int a = clampi((int)(int8_t)std::round(v[i] * s), -8, 7);
@@ -107,7 +115,7 @@ void quantize_row(const float* x, uint32_t cols, int fmt, uint8_t* codes, uint16
     // largest block), which keeps the fp64 block sums of the GEMV exact.
     for (uint32_t b = 0; b < nb; b++) {
         if ((scales[b] & 0x7FFF) && half_exponent(scales[b]) < emax - 15) {
-            std::memset(codes + (size_t)b * bb, fmt == PF_FMT_Q4 ? 0x88 : (fmt == PF_FMT_Q2 ? 0xAA : 0x55), bb);
+            std::memset(codes + (size_t)b * bb, zero_code(fmt), bb);
             scales[b] = 0;
         }
     }
@@ -130,7 +138,7 @@ void parallel_rows(uint32_t rows, F f) {
     for (auto& t : th) t.join();
 }
 
-bool valid_fmt(int fmt) { return fmt == PF_FMT_Q4 || fmt == PF_FMT_Q2 || fmt == PF_FMT_Q15; }
+bool valid_fmt(int fmt) { return fmt == PF_FMT_Q4 || fmt == PF_FMT_Q2 || fmt == PF_FMT_Q15 || fmt == PF_FMT_Q8; }
 
 }  // namespace
 
@@ -141,7 +149,7 @@ uint16_t half_rne(float f) { return to_half(f); }
 extern "C" pf_status pf_quantize_matrix(const float* w, uint32_t rows, uint32_t cols, int32_t fmt,
                                         uint8_t* codes, uint16_t* scales) {
     if (!w || !codes || !scales || cols % 32 || !valid_fmt(fmt)) return PF_ERR_ARG;
-    const uint32_t nb = cols / 32, bb = fmt == PF_FMT_Q4 ? 16 : 8;
+    const uint32_t nb = cols / 32, bb = block_bytes(fmt);
     parallel_rows(rows, [&](uint32_t a, uint32_t b) {
         for (uint32_t r = a; r < b; r++)
             quantize_row(w + (size_t)r * cols, cols, fmt, codes + (size_t)r * nb * bb, scales + (size_t)r * nb);
@@ -152,7 +160,7 @@ extern "C" pf_status pf_quantize_matrix(const float* w, uint32_t rows, uint32_t 
 extern "C" pf_status pf_gen_matrix(uint64_t seed, uint32_t stream, float stddev, uint32_t rows, uint32_t cols,
                                    int32_t fmt, uint8_t* codes, uint16_t* scales) {
     if (!codes || !scales || cols % 32 || !valid_fmt(fmt)) return PF_ERR_ARG;
-    const uint32_t nb = cols / 32, bb = fmt == PF_FMT_Q4 ? 16 : 8;
+    const uint32_t nb = cols / 32, bb = block_bytes(fmt);
     const double two_pi = 6.283185307179586476925286766559;
     parallel_rows(rows, [&](uint32_t a, uint32_t b) {
         std::vector<float> row(cols);

@@ -5,7 +5,7 @@
 namespace pf {
 
 // ---------------------------------------------------------- weight formats
-enum Fmt : int32_t { FMT_Q4 = 0, FMT_Q2 = 1, FMT_Q15 = 2 };
+enum Fmt : int32_t { FMT_Q4 = 0, FMT_Q2 = 1, FMT_Q15 = 2, FMT_Q8 = 3 };
 
 // Int8-activation matrices (fused QKV, O, fused gate|up, down) are stored
 // in tiles of 32 output rows x 256 input columns (8 blocks of 32), the
@@ -18,21 +18,25 @@ enum Fmt : int32_t { FMT_Q4 = 0, FMT_Q2 = 1, FMT_Q15 = 2 };
 //           byte j holds element 16h + j (low nibble) and 16h + j + 8 (high).
 //   Q2/Q15: 2 sets; set s covers blocks 4s .. 4s + 3, one dword each, where
 //           bits 2u, 2u + 1 of byte j hold element 16h + 4u + j.
+//   Q8    : 8 sets; set s is block s, 16 bytes: byte j holds element 16h + j
+//           (the MFMA operand as stored, no unpacking).
 // Code values: Q4 = nibble - 8, Q2 = code - 2, Q1.5 = code - 1 (code 3 is
-// rejected at upload).  The fused gate|up matrix interleaves its halves by
-// 16 rows: group g holds gate rows 16g .. 16g + 15, then up rows 16g ..
-// 16g + 15, so the SwiGLU pairs meet in one group.
+// rejected at upload), Q8 = the signed byte.  The fused gate|up matrix
+// interleaves its halves by 16 rows: group g holds gate rows 16g .. 16g + 15,
+// then up rows 16g .. 16g + 15, so the SwiGLU pairs meet in one group.
 constexpr int GROUP_ROWS = 32;
-__host__ __device__ constexpr uint32_t code_bytes(int fmt) { return fmt == FMT_Q4 ? 16u : 8u; }
-__host__ __device__ constexpr uint32_t g32_code_bytes(int fmt) { return fmt == FMT_Q4 ? 4096u : 2048u; }
+__host__ __device__ constexpr uint32_t code_bytes(int fmt) { return fmt == FMT_Q8 ? 32u : (fmt == FMT_Q4 ? 16u : 8u); }
+__host__ __device__ constexpr uint32_t g32_code_bytes(int fmt) { return 256u * code_bytes(fmt); }
 __host__ __device__ constexpr uint32_t g32_tile_bytes(int fmt) { return g32_code_bytes(fmt) + 512u; }
-__host__ __device__ constexpr int code_offset(int fmt) { return fmt == FMT_Q4 ? 8 : (fmt == FMT_Q2 ? 2 : 1); }
+__host__ __device__ constexpr int code_offset(int fmt) {
+    return fmt == FMT_Q8 ? 0 : (fmt == FMT_Q4 ? 8 : (fmt == FMT_Q2 ? 2 : 1));
+}
 
 // fp32-activation GEMV matrices (tied embedding / unembedding, MTP heads)
 // are row-major: codes [rows][cols/32][code_bytes] in the interchange
 // element order (Q4: byte j = elements 2j (low nibble), 2j+1 (high);
-// Q2/Q1.5: byte j = elements 4j..4j+3 at bits 0,2,4,6), scales separate
-// [rows][cols/32] fp16.
+// Q2/Q1.5: byte j = elements 4j..4j+3 at bits 0,2,4,6; Q8: byte j =
+// element j), scales separate [rows][cols/32] fp16.  Q4 and Q8 only.
 
 // ------------------------------------------------------------- KV cache
 // One (layer, head) plane holds KV_SINK_ROWS sink rows, then `ring` window

@@ -133,7 +133,10 @@ template <int FMT>
 __device__ __forceinline__ pf_v4i b_operand(const uint4* cw, uint32_t t) {
     constexpr uint32_t ADD = (0x80u - (uint32_t)code_offset(FMT)) * 0x01010101u;
     pf_v4i v;
-    if constexpr (FMT == FMT_Q4) {
+    if constexpr (FMT == FMT_Q8) {
+        const uint4 c = cw[t];
+        v.x = (int)c.x; v.y = (int)c.y; v.z = (int)c.z; v.w = (int)c.w;
+    } else if constexpr (FMT == FMT_Q4) {
         const uint4 c = cw[t >> 1];
         const uint32_t x0 = (t & 1u) ? c.z : c.x, x1 = (t & 1u) ? c.w : c.y, mk = 0x0F0F0F0Fu;
         v.x = (int)(((x0 & mk) + ADD) ^ 0x80808080u);
@@ -153,7 +156,7 @@ __device__ __forceinline__ pf_v4i b_operand(const uint4* cw, uint32_t t) {
 }
 
 template <int FMT>
-constexpr int sets_of() { return FMT == FMT_Q4 ? 4 : 2; }
+constexpr int sets_of() { return FMT == FMT_Q8 ? 8 : (FMT == FMT_Q4 ? 4 : 2); }
 
 // =============================================================== GEMV
 

@@ -268,7 +268,9 @@ static void pack_row(int fmt, uint32_t cols, const uint8_t* codes, const uint16_
         std::memcpy(tile + CODES + r * 16 + t * 2, &scales[b], 2);
         for (uint32_t h = 0; h < 2; h++) {
             const uint32_t lane = r + 32 * h;
-            if (fmt == FMT_Q4) {
+            if (fmt == FMT_Q8) {
+                std::memcpy(tile + t * 1024 + lane * 16, blk + 16 * h, 16);
+            } else if (fmt == FMT_Q4) {
                 uint8_t* dst = tile + (t >> 1) * 1024 + lane * 16 + (t & 1) * 8;
                 for (uint32_t j = 0; j < 8; j++)
                     dst[j] = (uint8_t)(interchange_code(fmt, blk, 16 * h + j) |
@@ -287,17 +289,17 @@ static void pack_row(int fmt, uint32_t cols, const uint8_t* codes, const uint16_
 
 static pf_status matrix_alloc(pf_ctx* c, int32_t fmt, uint32_t rows, uint32_t cols, bool rowmajor, pf_matrix** out,
                               bool ilv = false) {
-    if (fmt != FMT_Q4 && fmt != FMT_Q2 && fmt != FMT_Q15) return fail(c, PF_ERR_ARG, "unknown format");
+    if (fmt != FMT_Q4 && fmt != FMT_Q2 && fmt != FMT_Q15 && fmt != FMT_Q8) return fail(c, PF_ERR_ARG, "unknown format");
     if (cols % 256 || rows % 64 || rows == 0 || cols == 0)
         return fail(c, PF_ERR_UNSUPPORTED, "matrix shape must have rows % 64 == 0 and cols % 256 == 0");
-    if (rowmajor && (fmt != FMT_Q4 || cols > 2048))
-        return fail(c, PF_ERR_UNSUPPORTED, "fp32-activation matrices must be Q4 with cols <= 2048");
+    if (rowmajor && ((fmt != FMT_Q4 && fmt != FMT_Q8) || cols > 2048))
+        return fail(c, PF_ERR_UNSUPPORTED, "fp32-activation matrices must be Q4 or Q8 with cols <= 2048");
     if (!rowmajor && cols > 8192) return fail(c, PF_ERR_UNSUPPORTED, "int8-activation matrices need cols <= 8192");
     pf_matrix* M = new pf_matrix();
     M->ctx = c; M->fmt = fmt; M->rows = rows; M->cols = cols; M->rowmajor = rowmajor; M->ilv = ilv;
     const uint32_t nb = cols / 32;
     if (rowmajor) {
-        M->bytes = (size_t)rows * nb * 16;
+        M->bytes = (size_t)rows * nb * code_bytes(fmt);
         pf_status s = dalloc_t(c, &M->data, M->bytes);
         if (!s) s = dalloc_t(c, &M->scales, (size_t)rows * nb);
         if (s) { delete M; return s; }
@@ -329,7 +331,7 @@ static pf_status matrix_put(pf_matrix* M, uint32_t r0, uint32_t n, const uint8_t
         if (s) return s;
     }
     if (M->rowmajor) {
-        PF_HIP(c, hipMemcpy(M->data + (size_t)r0 * nb * 16, codes, (size_t)n * nb * 16, hipMemcpyHostToDevice));
+        PF_HIP(c, hipMemcpy(M->data + (size_t)r0 * nb * bb, codes, (size_t)n * nb * bb, hipMemcpyHostToDevice));
         PF_HIP(c, hipMemcpy(M->scales + (size_t)r0 * nb, scales, (size_t)n * nb * 2, hipMemcpyHostToDevice));
         return PF_OK;
     }
@@ -446,6 +448,7 @@ static void gemm_one(hipStream_t st, const GemmArgs& a, hipEvent_t ev0, hipEvent
     switch (fmt) {                                            \
         case FMT_Q4: { constexpr int F = FMT_Q4; CALL; } break; \
         case FMT_Q2: { constexpr int F = FMT_Q2; CALL; } break; \
+        case FMT_Q8: { constexpr int F = FMT_Q8; CALL; } break; \
         default: { constexpr int F = FMT_Q15; CALL; } break;    \
     }
 
@@ -512,8 +515,12 @@ static void launch_gemv_f32(hipStream_t st, const pf_matrix* W, uint32_t M, cons
         const float* yi = y_in ? y_in + (size_t)r0 * y_stride : nullptr;
 #define PF_F32_CASE(MM)                                                                                       \
     case MM:                                                                                                  \
-        hipLaunchKernelGGL(k_gemv_f32<MM>, grid, dim3(256), 0, st, W->data, W->scales, W->rows, W->cols, hr,  \
-                           h_stride, yr, y_stride, yi);                                                       \
+        if (W->fmt == FMT_Q8)                                                                                 \
+            hipLaunchKernelGGL((k_gemv_f32<MM, FMT_Q8>), grid, dim3(256), 0, st, W->data, W->scales, W->rows,   \
+                               W->cols, hr, h_stride, yr, y_stride, yi);                                      \
+        else                                                                                                  \
+            hipLaunchKernelGGL((k_gemv_f32<MM, FMT_Q4>), grid, dim3(256), 0, st, W->data, W->scales, W->rows,   \
+                               W->cols, hr, h_stride, yr, y_stride, yi);                                      \
         break;
         switch (mb) {
             PF_F32_CASE(1) PF_F32_CASE(2) PF_F32_CASE(3) PF_F32_CASE(4)
@@ -1210,16 +1217,27 @@ extern "C" pf_status pf_model_set_matrix(pf_model* m, uint32_t layer, int32_t id
     return PF_OK;
 }
 
-extern "C" pf_status pf_model_set_embedding(pf_model* m, const uint8_t* codes, const uint16_t* scales) {
+extern "C" pf_status pf_model_set_embedding_fmt(pf_model* m, int32_t fmt, const uint8_t* codes,
+                                                 const uint16_t* scales) {
     if (!m || !codes || !scales) return PF_ERR_ARG;
+    if (fmt != FMT_Q4 && fmt != FMT_Q8) return fail(m->ctx, PF_ERR_UNSUPPORTED, "the embedding table must be Q4 or Q8");
+    if (m->emb && m->emb->fmt != fmt) {
+        pf_matrix_free(m->emb);
+        m->emb = nullptr;
+        m->emb_set = false;
+    }
     if (!m->emb) {
-        pf_status s = matrix_alloc(m->ctx, FMT_Q4, m->d.n_vocab, m->d.n_embd, true, &m->emb);
+        pf_status s = matrix_alloc(m->ctx, fmt, m->d.n_vocab, m->d.n_embd, true, &m->emb);
         if (s) return s;
     }
     pf_status s = matrix_put(m->emb, 0, m->d.n_vocab, codes, scales);
     if (s) return s;
     m->emb_set = true;
     return PF_OK;
+}
+
+extern "C" pf_status pf_model_set_embedding(pf_model* m, const uint8_t* codes, const uint16_t* scales) {
+    return pf_model_set_embedding_fmt(m, FMT_Q4, codes, scales);
 }
 
 extern "C" pf_status pf_model_set_mtp(pf_model* m, uint32_t head, int32_t which, const uint8_t* codes,
@@ -1817,7 +1835,7 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
     hipLaunchKernelGGL(k_pool_rows, dim3(g.n_layers * g.n_heads, batch ? M : e->pool_rows_max), tb, 0, st, g, e->kv,
                        pd);
     hipLaunchKernelGGL(k_embed, dim3((D + 255) / 256, M), dim3(256), 0, st, m->emb->data, m->emb->scales, d.n_vocab, D,
-                       pd, e->x, e->ep);
+                       pd, e->x, e->ep, (int32_t)m->emb->fmt);
     for (uint32_t l = 0; l < d.n_layers; l++) {
         const float* an = m->attn_norm + (size_t)l * D;
         const float* fn = m->ffn_norm + (size_t)l * D;

@@ -258,8 +258,10 @@ extern "C" pf_status pf_squeeze_load_block(pf_squeeze* s, uint32_t layer, uint32
 }
 
 // Device interchange layout of one matrix from decoded codes and block
-// multipliers: fmt PF_FMT_Q4 (quant type 1), PF_FMT_Q2 (2) or PF_FMT_Q15
-// (3); codes [rows][cols/32][16 | 8], fp16 scales [rows][cols/32].
+// multipliers: fmt PF_FMT_Q8 (quant type 0, codes kept as stored, the
+// reference's round(x s + 0.5) rule included), PF_FMT_Q4 (1), PF_FMT_Q2 (2)
+// or PF_FMT_Q15 (3); codes [rows][cols/32][32 | 16 | 8], fp16 scales
+// [rows][cols/32].
 static pf_status repack(pf_squeeze* s, uint32_t layer, uint32_t matrix, uint32_t want_rows, uint32_t want_cols,
                         int32_t* fmt, std::vector<uint8_t>& codes, std::vector<uint16_t>& scales) {
     uint32_t rows, cols, qt;
@@ -269,12 +271,11 @@ static pf_status repack(pf_squeeze* s, uint32_t layer, uint32_t matrix, uint32_t
     if (rows != want_rows || cols != want_cols || cols % 32)
         return sq_fail(s, PF_ERR_FORMAT, "matrix " + std::to_string(matrix) + " of layer " + std::to_string(layer) +
                                              " has the wrong shape");
-    if (qt == 0) return sq_fail(s, PF_ERR_UNSUPPORTED, "Q8 layer matrices have no device format");
     std::vector<int8_t> c((size_t)rows * cols);
     std::vector<float> d((size_t)rows * cols / 32);
     if (pf_status st = pf_squeeze_load_block(s, layer, matrix, c.data(), d.data())) return st;
-    *fmt = qt == 1 ? PF_FMT_Q4 : (qt == 2 ? PF_FMT_Q2 : PF_FMT_Q15);
-    const uint32_t bb = qt == 1 ? 16 : 8;
+    *fmt = qt == 0 ? PF_FMT_Q8 : (qt == 1 ? PF_FMT_Q4 : (qt == 2 ? PF_FMT_Q2 : PF_FMT_Q15));
+    const uint32_t bb = qt == 0 ? 32 : (qt == 1 ? 16 : 8);
     codes.assign(d.size() * bb, 0);
     scales.resize(d.size());
     for (size_t k = 0; k < d.size(); k++) {
@@ -282,7 +283,8 @@ static pf_status repack(pf_squeeze* s, uint32_t layer, uint32_t matrix, uint32_t
         uint8_t* o = codes.data() + k * bb;
         for (uint32_t j = 0; j < 32; j++) {
             const int v = c[32 * k + j];
-            if (qt == 1) o[j / 2] |= (uint8_t)((v + 8) << (4 * (j & 1)));
+            if (qt == 0) o[j] = (uint8_t)(int8_t)v;
+            else if (qt == 1) o[j / 2] |= (uint8_t)((v + 8) << (4 * (j & 1)));
             else if (qt == 2) o[j / 4] |= (uint8_t)((v + 2) << (2 * (j & 3)));
             else o[j / 4] |= (uint8_t)((v + 1) << (2 * (j & 3)));
         }
@@ -307,7 +309,7 @@ static pf_status load_norm(pf_squeeze* s, pf_model* m, uint32_t layer, uint32_t 
 
 // Engine::load_model + load_layer_weights (src/engine.cpp:48-201, 606-640)
 // with every layer resident in HBM: layer matrices 0-6 (Q K V O gate up
-// down), norms 7 and 8, the tied embedding (layer 0, matrix 10, Q4).  MTP
+// down), norms 7 and 8, the tied embedding (layer 0, matrix 10, Q4 or Q8).  MTP
 // heads are not in the file format; set them with pf_model_set_mtp (n_mtp of
 // the model is the header's mtp_heads).
 extern "C" pf_status pf_squeeze_load_model(pf_ctx* ctx, pf_squeeze* s, pf_model** out) {
@@ -338,8 +340,10 @@ extern "C" pf_status pf_squeeze_load_model(pf_ctx* ctx, pf_squeeze* s, pf_model*
     if (!st) {
         int32_t fmt = 0;
         st = repack(s, 0, 10, I.n_vocab, D, &fmt, codes, scales);
-        if (!st && fmt != PF_FMT_Q4) st = sq_fail(s, PF_ERR_UNSUPPORTED, "the embedding table must be Q4");
-        if (!st && (st = pf_model_set_embedding(m, codes.data(), scales.data()))) sq_fail(s, st, pf_last_error(ctx));
+        if (!st && fmt != PF_FMT_Q4 && fmt != PF_FMT_Q8)
+            st = sq_fail(s, PF_ERR_UNSUPPORTED, "the embedding table must be Q4 or Q8");
+        if (!st && (st = pf_model_set_embedding_fmt(m, fmt, codes.data(), scales.data())))
+            sq_fail(s, st, pf_last_error(ctx));
     }
     if (st) {
         pf_model_destroy(m);

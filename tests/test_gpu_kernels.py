@@ -69,7 +69,7 @@ def test_matmul_reference_golden(gpu):
     np.testing.assert_array_equal(got, K["mq_Cas_fma"])
 
 
-@pytest.mark.parametrize("fmt", [pf.FMT_Q4, pf.FMT_Q2, pf.FMT_Q15])
+@pytest.mark.parametrize("fmt", [pf.FMT_Q4, pf.FMT_Q2, pf.FMT_Q15, pf.FMT_Q8])
 @pytest.mark.parametrize("shape", [(128, 512), (320, 2048), (64, 1792)])
 def test_gemv_int8_block(gpu, fmt, shape):
     N, K = shape
@@ -100,17 +100,18 @@ def test_gemv_rejects_out_of_range_scales(gpu):
         gpu.upload_matrix(pf.FMT_Q15, codes, scales)
 
 
+@pytest.mark.parametrize("fmt", [pf.FMT_Q4, pf.FMT_Q8])
 @pytest.mark.parametrize("K", [256, 768, 2048])
-def test_gemv_f32(gpu, K):
+def test_gemv_f32(gpu, K, fmt):
     N = 640
-    codes, scales = pf.gen_matrix(7, K, 0.02, N, K, pf.FMT_Q4)
-    W = gpu.upload_matrix(pf.FMT_Q4, codes, scales, rowmajor=True)
+    codes, scales = pf.gen_matrix(7, K, 0.02, N, K, fmt)
+    W = gpu.upload_matrix(fmt, codes, scales, rowmajor=True)
     rng = np.random.default_rng(K)
     for M in (1, 5):
         h = (rng.standard_normal((M, K))).astype(np.float32)
         y = gpu.gemv_f32(W, _t(h)).numpy()
         for m in range(M):
-            np.testing.assert_array_equal(y[m], O.gemv_f32(pf.FMT_Q4, codes, scales, h[m]))
+            np.testing.assert_array_equal(y[m], O.gemv_f32(fmt, codes, scales, h[m]))
     W.close()
 
 
@@ -261,7 +262,7 @@ def test_mtp_heads_standalone(gpu, with_table):
     m.close()
 
 
-@pytest.mark.parametrize("fmt", [pf.FMT_Q4, pf.FMT_Q2, pf.FMT_Q15])
+@pytest.mark.parametrize("fmt", [pf.FMT_Q4, pf.FMT_Q2, pf.FMT_Q15, pf.FMT_Q8])
 @pytest.mark.parametrize("shape", [(128, 512), (320, 2048), (64, 1792)])
 def test_gemm_int8_block(gpu, fmt, shape):
     """The int8 MFMA GEMM (M > 8 rows: many-sequence verify, batched prefill)

@@ -38,7 +38,7 @@ def test_init_without_gpu_fails_cleanly():
         pf.Context(0)
 
 
-@pytest.mark.parametrize("fmt", [pf.FMT_Q4, pf.FMT_Q2, pf.FMT_Q15])
+@pytest.mark.parametrize("fmt", [pf.FMT_Q4, pf.FMT_Q2, pf.FMT_Q15, pf.FMT_Q8])
 def test_quantizer_matches_oracle(fmt):
     rng = np.random.default_rng(5)
     w = (rng.standard_normal((96, 512)) * 0.02).astype(np.float32)
@@ -67,6 +67,11 @@ def test_quantizer_code_rules():
     codes, scales = pf.quantize_matrix(w, pf.FMT_Q15)
     assert codes[0, 0, 0] == (2 | (0 << 2) | (2 << 4) | (1 << 6))
     np.testing.assert_allclose(scales[0, 0:1].view(np.float16).astype(np.float32), [0.5833], rtol=1e-3)
+    # Q8: v = clamp(round(x * 127/amax), -127, 127), one signed byte per element, d = amax/127
+    codes, scales = pf.quantize_matrix(w, pf.FMT_Q8)
+    assert codes.shape == (64, 8, 32)
+    assert list(codes[0, 0, :4].view(np.int8)) == [127, -127, 64, 0]      # round(63.5) = 64
+    assert np.float16(scales[0, 0].view(np.float16)) == np.float16(0.7 / 127)
 
 
 def test_gen_matrix_deterministic_and_normal():

@@ -59,6 +59,8 @@ def decode_interchange(fmt, codes):
     holds elements 4j..4j+3 at bits 0, 2, 4, 6, value code - 2; Q1.5 the same
     positions with value code - 1."""
     rows, nb, _ = codes.shape
+    if fmt == O.Q8:     # Q8_0 (include/forge/types.hpp:17-20): one signed byte per element
+        return codes.view(np.int8).astype(np.int64).reshape(rows, nb * 32)
     if fmt == O.Q4:
         lo = (codes & 15).astype(np.int64) - 8
         hi = (codes >> 4).astype(np.int64) - 8
@@ -73,7 +75,7 @@ def f16(bits):
     return np.asarray(bits, np.uint16).view(np.float16).astype(np.float64)
 
 
-@pytest.mark.parametrize("fmt", [O.Q4, O.Q2, O.Q15])
+@pytest.mark.parametrize("fmt", [O.Q4, O.Q2, O.Q15, O.Q8])
 @pytest.mark.parametrize("rows,cols,seed", [(7, 256, 1), (33, 1024, 2), (5, 5632, 3)])
 def test_gemv_i8_against_float64_brute_force(fmt, rows, cols, seed):
     # y[n] = (float)(S_n * (double)a_s) with S_n the exact sum over k of
@@ -98,7 +100,7 @@ def test_gemv_i8_decoder_agrees_with_reference_dequantizers():
     # the brute force's decoder against the oracle's block decoder, which is
     # itself pinned to the reference dequantizer goldens
     rng = np.random.default_rng(9)
-    for fmt in (O.Q4, O.Q2, O.Q15):
+    for fmt in (O.Q4, O.Q2, O.Q15, O.Q8):
         w = rng.normal(0, 0.02, (3, 96)).astype(np.float32)
         codes, scales = O.quantize_matrix(w, fmt)
         q = O.qmat(fmt, codes, scales)
