@@ -370,7 +370,8 @@ def main():
                 "ffn_blocks_skipped_last_step": eng.layer_skip_count()} if args.layer_skip else {}),
         },
         "roofline": {
-            "kernel": "k_gemv<fmt,...> (verify-pass int8 x block-quantized GEMV: QKV, merge + O, gate|up, down)",
+            "kernel": ("k_o_ffn<Q4,3> (one-row verify pass: the attention's chunk merge and the O, gate|up and down "
+                       "int8 x Q4 products of a layer in one launch; bytes = the three matrices + fp32 rows)"),
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,

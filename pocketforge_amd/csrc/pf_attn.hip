@@ -857,52 +857,6 @@ constexpr uint32_t ag_smem(uint32_t nr) { return 2u * 256u * 128u + (512u + nr *
 // follow (the V stage reads them from LDS).
 constexpr uint32_t ag_smem_ll(uint32_t nr) { return ag_smem(nr) + nr * 128u * 4u; }
 
-// The pass's q/k/v rows as written by the QKV workgroups of the same launch
-// (pf_mm.hip, EPI_QKV with ll set): 8-byte words (value bits, flag) at
-// ll[row][3 D] (q, then k, then v), flag = ep[0] * fmul + fadd.  A reader
-// loads its words with device-scope loads and loads again the ones whose
-// flag is not yet the pass's.  A wait longer than LL_SPIN_MAX rounds sets
-// *err (the host reports it) and goes on, so every block ends.
-struct LLIn {
-    const unsigned long long* ll;
-    const uint32_t* ep;
-    uint32_t fmul, fadd;
-    uint32_t* err;
-};
-constexpr uint32_t LL_SPIN_MAX = 1u << 20;
-
-__device__ __forceinline__ unsigned long long ll_load(const unsigned long long* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Values of the N words base[off[i]] (off[i] == LL_NONE: 0) once each
-// carries `flag`.
-constexpr uint32_t LL_NONE = 0xFFFFFFFFu;
-template <int N>
-__device__ __forceinline__ void ll_wait(const unsigned long long* base, const uint32_t (&off)[N], float (&out)[N],
-                                        uint32_t flag, uint32_t* err) {
-    unsigned long long w[N];
-    const unsigned long long done = (unsigned long long)flag << 32;
-#pragma unroll
-    for (int i = 0; i < N; i++) w[i] = off[i] != LL_NONE ? ll_load(base + off[i]) : done;
-    for (uint32_t spins = 0;; spins++) {
-        bool ok = true;
-#pragma unroll
-        for (int i = 0; i < N; i++) ok = ok && (uint32_t)(w[i] >> 32) == flag;
-        if (ok) break;
-        if (spins >= LL_SPIN_MAX) {
-            atomicOr(err, 1u);
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-        for (int i = 0; i < N; i++)
-            if ((uint32_t)(w[i] >> 32) != flag) w[i] = ll_load(base + off[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < N; i++) out[i] = __uint_as_float((uint32_t)w[i]);
-}
-
 // Engine attention of every row of a pass (the first stage above), one
 // block per (head h, 256-entry chunk c, share of a group of rows), with the
 // chunk's K and V rows loaded once, coalesced, into LDS for all the rows

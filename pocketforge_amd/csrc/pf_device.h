@@ -317,4 +317,59 @@ __device__ __forceinline__ void quantize_row_block(const float (&x)[PER], uint32
     if (threadIdx.x == 0) *scale_out = (amax == 0.0f) ? 1.0f : amax / 127.0f;
 }
 
+// ------------------------------------------------------------- LL words
+// Values handed from workgroups of one launch to later workgroups of the
+// same launch: 8-byte words (value bits, flag) written with one device-scope
+// store each, flag = ep[0] * fmul + fadd (the pass epoch kept in device
+// memory and the layer), so a reader that sees the flag sees the value and
+// a word of an earlier pass or layer is never taken for the current one.  A
+// reader loads its words with device-scope loads and loads again the ones
+// whose flag is not yet the current one.  A wait longer than LL_SPIN_MAX
+// rounds sets *err (the host reports it) and goes on, so every workgroup
+// ends.
+struct LLIn {
+    const unsigned long long* ll;
+    const uint32_t* ep;
+    uint32_t fmul, fadd;
+    uint32_t* err;
+};
+constexpr uint32_t LL_SPIN_MAX = 1u << 20;
+
+__device__ __forceinline__ unsigned long long ll_load(const unsigned long long* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void ll_store(unsigned long long* p, float v, uint32_t flag) {
+    __hip_atomic_store(p, ((unsigned long long)flag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Values of the N words base[off[i]] (off[i] == LL_NONE: 0) once each
+// carries `flag`.
+constexpr uint32_t LL_NONE = 0xFFFFFFFFu;
+template <int N>
+__device__ __forceinline__ void ll_wait(const unsigned long long* base, const uint32_t (&off)[N], float (&out)[N],
+                                        uint32_t flag, uint32_t* err) {
+    unsigned long long w[N];
+    const unsigned long long done = (unsigned long long)flag << 32;
+#pragma unroll
+    for (int i = 0; i < N; i++) w[i] = off[i] != LL_NONE ? ll_load(base + off[i]) : done;
+    for (uint32_t spins = 0;; spins++) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < N; i++) ok = ok && (uint32_t)(w[i] >> 32) == flag;
+        if (ok) break;
+        if (spins >= LL_SPIN_MAX) {
+            atomicOr(err, 1u);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int i = 0; i < N; i++)
+            if ((uint32_t)(w[i] >> 32) != flag) w[i] = ll_load(base + off[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++) out[i] = __uint_as_float((uint32_t)w[i]);
+}
+
 }  // namespace pf

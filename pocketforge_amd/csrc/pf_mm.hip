@@ -33,6 +33,11 @@ typedef int pf_v16i __attribute__((ext_vector_type(16)));
 
 enum Pro : int { PRO_NORM = 0, PRO_QUANT = 1, PRO_INT8 = 2, PRO_QPART = 3, PRO_MERGE = 4 };
 enum Epi : int { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_SWIGLU = 3 };
+// Hand-offs through LL words (pf_device.h) inside one launch:
+//   LL_IN : the NORM / QUANT prologue's input rows are LL words, lli.ll[m xs + col]
+//   LL_OLD: the RESID epilogue's old values are LL words, e.llold[m y_stride + n]
+//   LL_OUT: the RESID / SWIGLU epilogue writes LL words to e.ll instead of e.y
+enum LLMode : int { LL_IN = 1, LL_OLD = 2, LL_OUT = 4 };
 
 // Consumer step applied to the outputs.  Row n is a device row (pf_layout.h).
 struct MmEpi {
@@ -53,6 +58,7 @@ struct MmEpi {
     unsigned long long* ll;
     const uint32_t* ep;
     uint32_t fmul, fadd;
+    const unsigned long long* llold;   // RESID with LL_OLD
 };
 
 // Logical row of device row n of a matrix whose halves [0, N/2) and
@@ -67,10 +73,16 @@ __device__ __forceinline__ uint32_t ilv_logical(uint32_t n, uint32_t N) {
 // the skip flag (b != 0: no residual); QKV the RoPE cos (a) and sin (b).
 struct EpiPre { float a, b; uint32_t f; };
 
-template <int EPI>
-__device__ __forceinline__ EpiPre epi_prefetch(const MmEpi& e, uint32_t m, uint32_t n) {
-    EpiPre p{0.0f, 0.0f, 0u};
-    if constexpr (EPI == EPI_RESID) {
+template <int EPI, int LLM = 0>
+__device__ __forceinline__ EpiPre epi_prefetch(const MmEpi& e, uint32_t m, uint32_t n, uint32_t flag = 0u,
+                                               uint32_t* err = nullptr) {
+    EpiPre p{0.0f, 0.0f, flag};
+    if constexpr (EPI == EPI_RESID && (LLM & LL_OLD)) {
+        const uint32_t off[1] = {m * e.y_stride + n};
+        float v[1];
+        ll_wait<1>(e.llold, off, v, flag, err);
+        p.a = v[0];
+    } else if constexpr (EPI == EPI_RESID) {
         p.a = e.y[(size_t)m * e.y_stride + n];
         p.b = (e.skipm && e.skipm[m]) ? 1.0f : 0.0f;
     } else if constexpr (EPI == EPI_QKV) {
@@ -89,11 +101,13 @@ __device__ __forceinline__ EpiPre epi_prefetch(const MmEpi& e, uint32_t m, uint3
 // y is this lane's output for (row m, device row n); y1 and y16 are the
 // outputs of rows n ^ 1 and n ^ 16 of the same m (lane partners).  Returns
 // the value a SWIGLU lane stores (0 for the others).
-template <int EPI>
+template <int EPI, int LLM = 0>
 __device__ __forceinline__ float epi_apply(const MmEpi& e, const EpiPre& p, uint32_t N, uint32_t m, uint32_t n,
                                            float y, float y1, float y16) {
     if constexpr (EPI == EPI_STORE) {
         e.y[(size_t)m * e.y_stride + (e.ilv ? ilv_logical(n, N) : n)] = y;
+    } else if constexpr (EPI == EPI_RESID && (LLM & LL_OUT)) {
+        ll_store(e.ll + (size_t)m * e.y_stride + n, p.a + y, p.f);
     } else if constexpr (EPI == EPI_RESID) {
         if (p.b == 0.0f) e.y[(size_t)m * e.y_stride + n] = p.a + y;
         if (e.y2) e.y2[(size_t)m * e.y_stride + n] = p.b == 0.0f ? p.a + y : p.a;
@@ -117,7 +131,8 @@ __device__ __forceinline__ float epi_apply(const MmEpi& e, const EpiPre& p, uint
             const uint32_t j = 16u * (n >> 5) + (n & 31u);
             const float sig = 1.0f / (1.0f + expf_c(-y));
             const float f = y * sig * y16;
-            e.y[(size_t)m * e.y_stride + j] = f;
+            if constexpr ((LLM & LL_OUT) != 0) ll_store(e.ll + (size_t)m * e.y_stride + j, f, p.f);
+            else e.y[(size_t)m * e.y_stride + j] = f;
             return f;
         }
     }
@@ -178,9 +193,11 @@ struct GemvArgs {
     uint32_t s_stride;
     const float* Up;           // MERGE: chunk-weighted V [H][cstride][hd] of row 0
     uint32_t cstride;
+    uint32_t ncap;             // MERGE: chunks the loads cover without reading the pass (heads * ncap <= 2048), or 0
     KvGeom g;                  // MERGE: chunk count of row 0's list
     MmEpi e;
     Prefetch nx;               // the next product's weights: nx.blocks more workgroups load them
+    LLIn lli;                  // LL_IN / LL_OLD / LL_OUT: input words, epoch, flag terms, timeout flag
 };
 
 // Dynamic LDS of k_gemv (bytes), laid out as: fp64 partials [waves][64][4],
@@ -233,9 +250,13 @@ __device__ __forceinline__ float max4abs(float4 v) {
 //          row quantized (quantize_activation_row).
 //
 // gemv_body is the workgroup's work as workgroup bx of gx; k_gemv runs it
-// as its own grid, k_qkv_attn as the first workgroups of a wider one.
-template <int FMT, int PRO, int EPI, bool GATED, int CPW, int MR>
+// as its own grid, k_qkv_attn and k_o_ffn as workgroups of a wider one.
+// With LL_IN the prologue's input words are waited for after the weight
+// loads have been issued, so the weights stream in during the wait.
+template <int FMT, int PRO, int EPI, bool GATED, int CPW, int MR, int LLM = 0>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32_t gx, uint8_t* smem) {
+    static_assert(!(LLM & LL_IN) || (MR == 1 && (PRO == PRO_NORM || PRO == PRO_QUANT)),
+                  "LL input rows: one row, NORM or QUANT prologue");
     constexpr uint32_t TB = g32_tile_bytes(FMT), CODES = g32_code_bytes(FMT);
     constexpr int SETS = sets_of<FMT>();
     constexpr uint32_t NT = 64u * GEMV_WAVES;
@@ -256,6 +277,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
     const uint32_t t = threadIdx.x, lane = t & 63u, r = lane & 31u, h = lane >> 5;
     const uint32_t wid = __builtin_amdgcn_readfirstlane(t >> 6);
     const float* __restrict__ xg = a.x;
+    const uint32_t llflag = LLM ? a.lli.ep[0] * a.lli.fmul + a.lli.fadd : 0u;
 
     // ---- prologue loads
     const uint32_t li = lane & 15u, q = lane >> 4, T = wid + GEMV_WAVES * q;   // NORM tile of this lane
@@ -268,10 +290,12 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
         const uint32_t col = 64u * min(T, nt - 1u) + li;
 #pragma unroll
         for (int k = 0; k < 4; k++) wv[k] = a.nw[col + 16u * k];
+        if constexpr (!(LLM & LL_IN)) {
 #pragma unroll
-        for (uint32_t m = 0; m < MR; m++)
+            for (uint32_t m = 0; m < MR; m++)
 #pragma unroll
-            for (int k = 0; k < 4; k++) xv[m][k] = xg[(size_t)min(m, mlast) * xs + col + 16u * k];
+                for (int k = 0; k < 4; k++) xv[m][k] = xg[(size_t)min(m, mlast) * xs + col + 16u * k];
+        }
     } else if constexpr (PRO == PRO_INT8) {
 #pragma unroll
         for (int k = 0; k < 2; k++) {
@@ -279,41 +303,45 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
             iv[k] = *reinterpret_cast<const uint4*>(a.a8 + (size_t)m * xs + 16u * c);
         }
     }
-    // MERGE: the row's (head, chunk) maxima and sums (entry i = h nc + c,
-    // heads * chunks <= 2048), and the first MG chunks of its columns
+    // MERGE: the row's (head, chunk) maxima and sums (entry i = h ncl + c,
+    // heads * ncl <= 2048), and the first MG chunks of its columns
     // 4t .. 4t + 3 (head 4t >> hs, elements 4t & (hd - 1) ..; head_dim is a
-    // power of two).  Chunk loads past the list repeat its last chunk, so
-    // every group issues the same loads and the waits stay exact.
+    // power of two).  With ncap set the loads cover ncl = ncap chunks, the
+    // capacity, whatever the pass's count nc, so they issue without waiting
+    // for the pass descriptor; entries past nc are never used.  Otherwise
+    // ncl = nc.  Chunk loads past ncl repeat its last chunk, so every group
+    // issues the same loads and the waits stay exact.
     constexpr int MK = 2048 / NT;
-    constexpr uint32_t MG = 8;
-    uint32_t nc = 1, hn = 1, hs = 0;
+    constexpr uint32_t MG = 12;
+    uint32_t nc = 1, ncl = 1, hs = 0;
     uint32_t sh[MK], sc[MK];                  // head and chunk of S entry t + NT k
     float sm[MK], sv[MK];
     float4 uc[MG];
     const float* upc = nullptr;               // this thread's columns in chunk 0
     if constexpr (PRO == PRO_MERGE) {
         static_assert(MR == 1, "the merge prologue serves one row");
-        nc = (kv_view(a.g, row_pos(pass_head(a.e.pd), 0)).count() + 1u + 255u) / 256u;
-        hn = a.g.n_heads * nc;
+        if (a.ncap) ncl = a.ncap;
+        else ncl = (kv_view(a.g, row_pos(pass_head(a.e.pd), 0)).count() + 1u + 255u) / 256u;
+        const uint32_t hn = a.g.n_heads * ncl;
         hs = (uint32_t)__builtin_ctz(a.e.hd);
-        const float rnc = 1.0f / (float)nc;
+        const float rnc = 1.0f / (float)ncl;
 #pragma unroll
         for (int k = 0; k < MK; k++) {
             const uint32_t i = min(t + NT * k, hn - 1u);
-            uint32_t hh = (uint32_t)((float)i * rnc);     // i / nc, corrected below
-            hh -= hh * nc > i ? 1u : 0u;
-            hh += (hh + 1u) * nc <= i ? 1u : 0u;
+            uint32_t hh = (uint32_t)((float)i * rnc);     // i / ncl, corrected below
+            hh -= hh * ncl > i ? 1u : 0u;
+            hh += (hh + 1u) * ncl <= i ? 1u : 0u;
             sh[k] = hh;
-            sc[k] = t + NT * k < hn ? i - hh * nc : 0xFFFFFFFFu;
-            sm[k] = a.S[(size_t)hh * a.s_stride + 2u * (i - hh * nc)];
-            sv[k] = a.S[(size_t)hh * a.s_stride + 2u * (i - hh * nc) + 1u];
+            sc[k] = t + NT * k < hn ? i - hh * ncl : 0xFFFFFFFFu;
+            sm[k] = a.S[(size_t)hh * a.s_stride + 2u * (i - hh * ncl)];
+            sv[k] = a.S[(size_t)hh * a.s_stride + 2u * (i - hh * ncl) + 1u];
         }
         const uint32_t i4 = min(4u * t, K - 4u);
         upc = a.Up + (size_t)(i4 >> hs) * a.cstride * a.e.hd + (i4 & (a.e.hd - 1u));
 #pragma unroll
         for (uint32_t u = 0; u < MG; u++)
-            uc[u] = *reinterpret_cast<const float4*>(upc + (size_t)min(u, nc - 1u) * a.e.hd);
-    } else if constexpr (PRO != PRO_INT8 && PRO != PRO_NORM) {
+            uc[u] = *reinterpret_cast<const float4*>(upc + (size_t)min(u, ncl - 1u) * a.e.hd);
+    } else if constexpr (PRO != PRO_INT8 && PRO != PRO_NORM && !(LLM & LL_IN)) {
 #pragma unroll
         for (uint32_t m = 0; m < MR; m++)
 #pragma unroll
@@ -339,54 +367,76 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
         for (int s = 0; s < SETS; s++) cw[j][s] = *reinterpret_cast<const uint4*>(tile + s * 1024 + lane * 16);
         sw[j] = *reinterpret_cast<const uint4*>(tile + CODES + r * 16);
     }
+    // ---- LL input rows (row 0), after the weight loads
+    if constexpr ((LLM & LL_IN) && PRO == PRO_NORM) {
+        const uint32_t col = 64u * min(T, nt - 1u) + li;
+        uint32_t off[4];
+        float v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) off[k] = col + 16u * k;
+        ll_wait<4>(a.lli.ll, off, v, llflag, a.lli.err);
+#pragma unroll
+        for (int k = 0; k < 4; k++) xv[0][k] = v[k];
+    } else if constexpr ((LLM & LL_IN) && PRO == PRO_QUANT) {
+        uint32_t off[4 * CPW];
+        float v[4 * CPW];
+#pragma unroll
+        for (int k = 0; k < CPW; k++) {
+            const uint32_t c = min(t + NT * k, per4 - 1u);
+#pragma unroll
+            for (int j = 0; j < 4; j++) off[4 * k + j] = 4u * c + j;
+        }
+        ll_wait<4 * CPW>(a.lli.ll, off, v, llflag, a.lli.err);
+#pragma unroll
+        for (int k = 0; k < CPW; k++) hv[0][k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+    }
     // ---- epilogue operands: thread t outputs row om of device row on
     const uint32_t om = t >> 5, on = 32u * bx + (t & 31u);
-    const EpiPre pre = epi_prefetch<EPI>(a.e, min(om, mlast), on);
+    const EpiPre pre = epi_prefetch<EPI, LLM>(a.e, min(om, mlast), on, llflag, a.lli.err);
 
     // ---- prologue arithmetic
     if constexpr (PRO == PRO_MERGE) {
         float* fsm = st + 24;                    // [2048] chunk maxima, then f_c
         float* tsm = fsm + 2048;                 // [2048] chunk sums
-        float* hmx = tsm + 2048;                 // [128] head maxima
-        float* hiv = hmx + 128;                  // [128] 1 / (T + 1e-10) per head
+        float* hiv = tsm + 2048 + 128;           // [128] 1 / (T + 1e-10) per head
         float* mred = hiv + 128;                 // [16]
         const uint32_t H = a.g.n_heads, hd = a.e.hd;
+        if (a.ncap) nc = (kv_view(a.g, row_pos(pass_head(a.e.pd), 0)).count() + 1u + 255u) / 256u;
+        else nc = ncl;
 #pragma unroll
         for (int k = 0; k < MK; k++) {
             if (sc[k] < nc) {
-                fsm[sh[k] * nc + sc[k]] = sm[k];
-                tsm[sh[k] * nc + sc[k]] = sv[k];
+                fsm[sh[k] * ncl + sc[k]] = sm[k];
+                tsm[sh[k] * ncl + sc[k]] = sv[k];
             }
         }
         __syncthreads();
+        // per head (thread h): the maximum over the chunk maxima, then
+        // f_c = exp(m_c - max) in place and the T chain over c in order
         if (t < H) {
-            const float* f = fsm + t * nc;
+            float* f = fsm + t * ncl;
+            const float* ts = tsm + t * ncl;
             float mx = f[0];
             for (uint32_t c = 1; c < nc; c++) mx = fmaxf(mx, f[c]);
-            hmx[t] = mx;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < MK; k++)
-            if (sc[k] < nc) fsm[sh[k] * nc + sc[k]] = expf_c(sm[k] - hmx[sh[k]]);
-        __syncthreads();
-        // T per head (lane h) beside the U chains; read after the next barrier
-        if (t < H) {
-            const float* f = fsm + t * nc;
-            const float* ts = tsm + t * nc;
             float T = 0.0f;
-            for (uint32_t c = 0; c < nc; c++) T = __builtin_fmaf(ts[c], f[c], T);
+            for (uint32_t c = 0; c < nc; c++) {
+                const float fc = expf_c(f[c] - mx);
+                f[c] = fc;
+                T = __builtin_fmaf(ts[c], fc, T);
+            }
             hiv[t] = 1.0f / (T + 1e-10f);
         }
-        // U chains over c in order, MG chunks at a time, the next group's
-        // loads issued before this group's FMAs
+        __syncthreads();
+        // U chains over c in order: the first MG chunks are held, later
+        // groups (more than MG chunks) are loaded group by group
         float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        const float* f0 = fsm + (min(4u * t, K - 4u) >> hs) * nc;
+        const float* f0 = fsm + (min(4u * t, K - 4u) >> hs) * ncl;
         for (uint32_t c0 = 0; c0 < nc; c0 += MG) {
-            float4 un[MG];
+            if (c0) {
 #pragma unroll
-            for (uint32_t u = 0; u < MG; u++)
-                un[u] = *reinterpret_cast<const float4*>(upc + (size_t)min(c0 + MG + u, nc - 1u) * hd);
+                for (uint32_t u = 0; u < MG; u++)
+                    uc[u] = *reinterpret_cast<const float4*>(upc + (size_t)min(c0 + u, nc - 1u) * hd);
+            }
             const uint32_t nb = min(MG, nc - c0);
 #pragma unroll
             for (uint32_t u = 0; u < MG; u++) {
@@ -398,10 +448,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
                     v.w = __builtin_fmaf(uc[u].w, f, v.w);
                 }
             }
-#pragma unroll
-            for (uint32_t u = 0; u < MG; u++) uc[u] = un[u];
         }
-        __syncthreads();
         // the row's amax: wave maxima meet in LDS behind one barrier
         const bool own = 4u * t < K;
         const float hv4 = hiv[min(4u * t, K - 4u) >> hs];
@@ -522,6 +569,54 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
     __syncthreads();
 
     // ---- product
+    if constexpr (MR == 1) {
+        // One row: lane (r, h) takes the 16 codes 16h .. 16h + 15 of each
+        // block of weight row r with the row's matching activation bytes
+        // (the same LDS words for every lane of a half, a broadcast), four
+        // v_dot4 give the exact int32 partial p, and d_b * p accumulates in
+        // fp64; the halves and waves meet in LDS.  Every partial sum is a
+        // sum of some of the exact terms d_b * p_b, so the result is the
+        // same sum as the MFMA path's.
+        double S1 = 0.0;
+        const int8_t* a0 = act + 16u * h;
+#pragma unroll
+        for (int j = 0; j < CPW; j++) {
+            if (c0 + j >= c1) break;
+            const uint32_t c = c0 + j;
+            const uint16_t* sc = reinterpret_cast<const uint16_t*>(&sw[j]);
+            pf_v4i A[8];
+#pragma unroll
+            for (uint32_t u = 0; u < 8; u++) A[u] = *reinterpret_cast<const pf_v4i*>(a0 + 32u * (8u * c + u));
+#pragma unroll
+            for (uint32_t u = 0; u < 8; u++) {
+                const pf_v4i B = b_operand<FMT>(cw[j], u);
+                int pp = __builtin_amdgcn_sdot4(A[u].x, B.x, 0, false);
+                pp = __builtin_amdgcn_sdot4(A[u].y, B.y, pp, false);
+                pp = __builtin_amdgcn_sdot4(A[u].z, B.z, pp, false);
+                pp = __builtin_amdgcn_sdot4(A[u].w, B.w, pp, false);
+                S1 = __builtin_fma((double)h2f(sc[u]), (double)pp, S1);
+            }
+        }
+        red[wid * 64 + lane] = S1;
+        __syncthreads();
+        float y = 0.0f;
+        if (t < 32u) {
+            double v = red[t] + red[t + 32u];
+#pragma unroll
+            for (uint32_t w = 1; w < GEMV_WAVES; w++) v += red[w * 64 + t] + red[w * 64 + t + 32u];
+            y = (float)(v * (double)st_as[0]);
+        }
+        const float y1 = __shfl_xor(y, 1, 64), y16 = __shfl_xor(y, 16, 64);
+        float f = 0.0f;
+        if (om < M) f = epi_apply<EPI, LLM>(a.e, pre, a.N, om, on, y, y1, y16);
+        if constexpr (EPI == EPI_SWIGLU) {
+            float mx = fabsf(f);
+#pragma unroll
+            for (int off = 16; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+            if (a.e.pmax && om < M && (t & 31u) == 0) a.e.pmax[(size_t)om * (a.N / 32u) + bx] = mx;
+        }
+        return;
+    }
     double S[4] = {0.0, 0.0, 0.0, 0.0};
     const pf_v16i zero = {};
     const pf_v4i za = {0, 0, 0, 0};
@@ -563,7 +658,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
     }
     const float y1 = __shfl_xor(y, 1, 64), y16 = __shfl_xor(y, 16, 64);
     float f = 0.0f;
-    if (om < M) f = epi_apply<EPI>(a.e, pre, a.N, om, on, y, y1, y16);
+    if (om < M) f = epi_apply<EPI, LLM>(a.e, pre, a.N, om, on, y, y1, y16);
     if constexpr (EPI == EPI_SWIGLU) {
         // row maximum of |f| over the group's 16 outputs (lanes of one m
         // are a half wave), for the consumer's quantization

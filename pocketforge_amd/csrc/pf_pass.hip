@@ -1,5 +1,6 @@
-// One launch for a decode pass's Q/K/V product and its attention (passes of
-// at most 8 rows), for gfx950.
+// One-launch stages of a decode pass, for gfx950: the Q/K/V product with
+// the attention (passes of at most 8 rows), and the O, gate|up and down
+// products (one-row passes).
 //
 // The attention of a one-row pass reads about 9.5 MB of cached K/V rows per
 // layer at the 1B model's 2K context, and none of them depends on the pass's
@@ -60,6 +61,98 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     attn_group_body<PARTS, true, NR, true>(b.pd, b.g, b.kv, b.layer, b.M, nullptr, nullptr, nullptr, b.S,
                                            b.s_stride, b.Up, b.cstride, b.pf, b.lli, x % tasks, x / tasks,
                                            blockIdx.x, tasks, smem);
+}
+
+// LDS of k_o_ffn: the largest of its GEMV roles' needs.
+__host__ __device__ constexpr uint32_t o_ffn_smem(uint32_t D, uint32_t F) {
+    return gemv_smem(1, D) > gemv_smem(1, F) ? gemv_smem(1, D) : gemv_smem(1, F);
+}
+
+// The chunk merge of a one-row pass's attention output for the columns
+// 512 mb .. 512 mb + 511 of the row, one column per thread, as LL words to
+// a.lli.ll: for column j of head h, with the chunks' maxima m_c, sums T_c
+// and weighted values U_c (the attention's S and Up), f_c = exp(m_c - max_c
+// m_c), T and U fmaf chains over c in order, U * (1 / (T + 1e-10)), the
+// arithmetic of merge_quant_row before its quantization.  Loads cover
+// ncap chunks (a.ncap, the buffers' capacity) so they issue before the
+// pass descriptor gives the count nc; lists of more than MC chunks read
+// their chunks again in a loop.
+__device__ __forceinline__ void merge_cols_ll(const GemvArgs& a, uint32_t mb) {
+    constexpr uint32_t MC = 16;
+    const uint32_t D = a.K, hd = a.e.hd, hs = (uint32_t)__builtin_ctz(hd);
+    const uint32_t j0 = 512u * mb + threadIdx.x, j = min(j0, D - 1u), h = j >> hs, e = j & (hd - 1u);
+    const uint32_t flag = a.lli.ep[0] * a.lli.fmul + a.lli.fadd;
+    const float* sp = a.S + (size_t)h * a.s_stride;
+    const float* up = a.Up + (size_t)h * a.cstride * hd + e;
+    const uint32_t ncl = a.ncap;
+    float m[MC], ts[MC], u[MC];
+#pragma unroll
+    for (uint32_t c = 0; c < MC; c++) {
+        const uint32_t cc = min(c, ncl - 1u);
+        m[c] = sp[2u * cc];
+        ts[c] = sp[2u * cc + 1u];
+        u[c] = up[(size_t)cc * hd];
+    }
+    const uint32_t nc = (kv_view(a.g, row_pos(pass_head(a.e.pd), 0)).count() + 1u + 255u) / 256u;
+    float T = 0.0f, U = 0.0f;
+    if (nc <= MC && nc <= ncl) {
+        float mx = m[0];
+#pragma unroll
+        for (uint32_t c = 1; c < MC; c++)
+            if (c < nc) mx = fmaxf(mx, m[c]);
+#pragma unroll
+        for (uint32_t c = 0; c < MC; c++) {
+            if (c < nc) {
+                const float f = expf_c(m[c] - mx);
+                T = __builtin_fmaf(ts[c], f, T);
+                U = __builtin_fmaf(u[c], f, U);
+            }
+        }
+    } else {
+        float mx = sp[0];
+        for (uint32_t c = 1; c < nc; c++) mx = fmaxf(mx, sp[2u * c]);
+        for (uint32_t c = 0; c < nc; c++) {
+            const float f = expf_c(sp[2u * c] - mx);
+            T = __builtin_fmaf(sp[2u * c + 1u], f, T);
+            U = __builtin_fmaf(up[(size_t)c * hd], f, U);
+        }
+    }
+    if (j0 < D) ll_store(const_cast<unsigned long long*>(a.lli.ll) + j0, U * (1.0f / (T + 1e-10f)), flag);
+}
+
+// The rest of a one-row pass's layer after the attention, in one launch:
+// workgroups [0, n_mg) merge the attention's chunks into the row (LL words
+// at o.lli.ll), [n_mg, n_mg + n_o) are the O product's (quantize prologue
+// over the merged row, residual epilogue), the next n_gu the gate|up
+// product's (RMSNorm + quantize prologue, SwiGLU epilogue), the last N / 32
+// the down product's (quantize prologue, residual epilogue).  Stage outputs
+// are LL words: O writes the updated residual row to o.e.ll (D words),
+// gate|up its SwiGLU row to gu.e.ll (F words); gate|up reads the residual
+// row and down reads both.  The GEMV workgroups issue their weight loads as
+// they start, before they wait, so the weights stream in while the earlier
+// stages run; the O workgroups, once done, load the next layer's QKV
+// weights (o.nx) into the L2 of the XCDs whose workgroups will read them.
+// Only down writes the residual row itself (dn.e.y) and the pass's hidden
+// output.
+//
+// Progress, as for k_qkv_attn: each XCD receives its workgroups in id order
+// and a workgroup waits only for workgroups of earlier stages (lower ids),
+// and the first stage waits for nothing; every wait is bounded.
+template <int FMT, int CPWD>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_o_ffn(uint32_t n_mg, uint32_t n_o, uint32_t n_gu, GemvArgs o, GemvArgs gu, GemvArgs dn) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t b = blockIdx.x;
+    if (b < n_mg) {
+        merge_cols_ll(o, b);
+    } else if (b < n_mg + n_o) {
+        gemv_body<FMT, PRO_QUANT, EPI_RESID, false, 1, 1, LL_IN | LL_OUT>(o, b - n_mg, n_o, smem);
+        prefetch_groups(o.nx, b, b - n_mg, n_o);
+    } else if (b < n_mg + n_o + n_gu) {
+        gemv_body<FMT, PRO_NORM, EPI_SWIGLU, false, 1, 1, LL_IN | LL_OUT>(gu, b - n_mg - n_o, n_gu, smem);
+    } else {
+        const uint32_t x = b - n_mg - n_o - n_gu;
+        gemv_body<FMT, PRO_QUANT, EPI_RESID, false, CPWD, 1, LL_IN | LL_OLD>(dn, x, dn.N / 32u, smem);
+    }
 }
 
 }  // namespace pf

@@ -1378,6 +1378,12 @@ struct pf_engine {
     uint32_t* ep = nullptr;
     uint32_t* ll_err = nullptr;
     bool qkv_attn = true;
+    // one launch for the O, gate|up and down products of one-row passes
+    // (k_o_ffn, pf_pass.hip): the residual row after O (D words), the
+    // SwiGLU row (F words) and the merged attention row (D words), as LL
+    // words.  PF_O_FFN=0 launches them separately.
+    unsigned long long* llt = nullptr;
+    bool o_ffn = true;
 };
 
 template <class T>
@@ -1481,11 +1487,14 @@ static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t ns
     if (!s) s = ealloc(e, &e->st, nseq);
     if (!s) s = ealloc(e, &e->ll, (size_t)MAX_PASS_ROWS * 3 * D);
     if (!s) s = ealloc(e, &e->ep, 2);
+    if (!s) s = ealloc(e, &e->llt, (size_t)2 * D + d.n_ff);
     if (s) { pf_engine_destroy(e); return s; }
     e->ll_err = e->ep + 1;
     PF_HIP(c, hipMemset(e->ll, 0, (size_t)MAX_PASS_ROWS * 3 * D * 8));
+    PF_HIP(c, hipMemset(e->llt, 0, ((size_t)2 * D + d.n_ff) * 8));
     PF_HIP(c, hipMemset(e->ep, 0, 8));
     if (const char* v = std::getenv("PF_QKV_ATTN")) e->qkv_attn = !(v[0] == '0');
+    if (const char* v = std::getenv("PF_O_FFN")) e->o_ffn = !(v[0] == '0');
     if (hipHostMalloc((void**)&e->word, 64, hipHostMallocDefault) != hipSuccess) {
         pf_engine_destroy(e);
         return fail(c, PF_ERR_HIP, "hipHostMalloc failed");
@@ -1793,6 +1802,46 @@ static pf_status ll_check(pf_engine* e) {
     return fail(e->c, PF_ERR_DEVICE, "a wait for the QKV product's rows timed out inside k_qkv_attn");
 }
 
+// Chunk capacity of the merge prologue's loads: the chunks of the largest
+// list the engine's buffers hold, if heads * chunks fits its LDS tables.
+static uint32_t merge_ncap(const pf_engine* e) {
+    const uint32_t n = e->cstride - 1;
+    return e->m->d.n_heads * n <= 2048 ? n : 0u;
+}
+
+// k_o_ffn serves layer l of a one-row pass: three Q4 matrices, F a
+// multiple of 256 up to 6144 (at most three 256-column chunks per wave of
+// the down product, held in registers without spills), D <= 2048 (one
+// 256-column chunk per wave of the O and gate|up products), no layer skip.
+static bool o_ffn_ok(const pf_engine* e, uint32_t l) {
+    const pf_model* m = e->m;
+    const uint32_t F = m->d.n_ff;
+    return e->o_ffn && !e->skip_on && m->o[l]->fmt == FMT_Q4 && m->gu[l]->fmt == FMT_Q4 &&
+           m->down[l]->fmt == FMT_Q4 && F % 256 == 0 && F <= 6144 && m->d.n_embd <= 2048;
+}
+
+template <int CPWD>
+static void o_ffn_one(hipStream_t st, const GemvArgs& ao, const GemvArgs& ag, const GemvArgs& ad, hipEvent_t ev0,
+                      hipEvent_t ev1) {
+    const uint32_t n_mg = (ao.K + 511) / 512, n_o = ao.N / 32, n_gu = ag.N / 32, n_dn = ad.N / 32;
+    const uint32_t smem = o_ffn_smem(ao.K, ad.K);
+    const dim3 grid(n_mg + n_o + n_gu + n_dn);
+    if (ev0)
+        hipExtLaunchKernelGGL((k_o_ffn<FMT_Q4, CPWD>), grid, dim3(512), smem, st, ev0, ev1, 0, n_mg, n_o, n_gu, ao, ag,
+                              ad);
+    else
+        hipLaunchKernelGGL((k_o_ffn<FMT_Q4, CPWD>), grid, dim3(512), smem, st, n_mg, n_o, n_gu, ao, ag, ad);
+}
+
+static void launch_o_ffn(hipStream_t st, const GemvArgs& ao, const GemvArgs& ag, const GemvArgs& ad, hipEvent_t ev0,
+                         hipEvent_t ev1) {
+    switch ((ad.K / 256 + GEMV_WAVES - 1) / GEMV_WAVES) {
+        case 1: o_ffn_one<1>(st, ao, ag, ad, ev0, ev1); break;
+        case 2: o_ffn_one<2>(st, ao, ag, ad, ev0, ev1); break;
+        default: o_ffn_one<3>(st, ao, ag, ad, ev0, ev1); break;
+    }
+}
+
 // One forward pass of M rows (the PassDesc at `pd` holds positions and
 // tokens; pos0 is the host's copy of the first position).  hidden/logits
 // outputs are device [M][D] / [M][V]; either may be null.  A batched pass
@@ -1896,6 +1945,51 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
                                                     pd, g, (const float*)e->S, e->s_stride, (const float*)e->Wp,
                                                     e->cstride, e->act, ks, as1, (int32_t*)nullptr, 0u, M,
                                                     prefetch_of(e, m->o[l], e->pf_blocks)));
+        // one-row passes without layer skip: O, gate|up and down in one launch
+        if (merge_in_o && o_ffn_ok(e, l)) {
+            const LLIn li{nullptr, e->ep, d.n_layers, l, e->ll_err};
+            GemvArgs ao{}, ag{}, ad{};
+            ao.W = m->o[l]->data; ao.N = D; ao.K = D; ao.M = 1;
+            ao.xs = D;
+            ao.S = e->S; ao.s_stride = e->s_stride; ao.Up = e->Wp; ao.cstride = e->cstride; ao.g = g;
+            ao.ncap = e->cstride - 1;
+            ao.e.pd = pd; ao.e.hd = hd; ao.e.D = D;
+            ao.e.y = e->x; ao.e.y_stride = D; ao.e.ll = e->llt;
+            ao.nx = prefetch_of(e, l + 1 < d.n_layers ? m->qkv[l + 1] : nullptr, D / 32);
+            ao.lli = li;
+            ao.lli.ll = e->llt + D + F;
+            ag.W = m->gu[l]->data; ag.N = m->gu[l]->rows; ag.K = D; ag.M = 1;
+            ag.xs = D; ag.nw = fn;
+            ag.e.y_stride = F; ag.e.ll = e->llt + D;
+            ag.lli = li;
+            ag.lli.ll = e->llt;
+            ad.W = m->down[l]->data; ad.N = D; ad.K = F; ad.M = 1;
+            ad.xs = F;
+            ad.e.y = e->x; ad.e.y_stride = D; ad.e.llold = e->llt;
+            if (l + 1 == d.n_layers && hidden) ad.e.y2 = hidden;
+            ad.lli = li;
+            ad.lli.ll = e->llt + D;
+            hipEvent_t ev0 = nullptr, ev1 = nullptr;
+            if (e->profile == 1 && e->in_verify && !e->capturing) {
+                if (e->kev_used == e->kev.size()) {
+                    TimedPass n{};
+                    PF_HIP(c, hipEventCreate(&n.a));
+                    PF_HIP(c, hipEventCreate(&n.b));
+                    e->kev.push_back(n);
+                    e->kev_bytes.push_back(0.0);
+                }
+                // the three matrices, their fp32 input rows and outputs
+                double b = 0.0;
+                for (const pf_matrix* W : {m->o[l], m->gu[l], m->down[l]})
+                    b += (double)W->bytes + 4.0 * W->cols + 4.0 * W->rows;
+                e->kev_bytes[e->kev_used] = b;
+                ev0 = e->kev[e->kev_used].a;
+                ev1 = e->kev[e->kev_used].b;
+                e->kev_used++;
+            }
+            launch_o_ffn(st, ao, ag, ad, ev0, ev1);
+            continue;
+        }
         // O projection + residual (src/engine.cpp:789-800)
         a = GemvArgs{};
         a.a8 = e->act; a.a8s = as1; a.xs = ks;
@@ -1903,6 +1997,7 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         a.nx = prefetch_of(e, m->gu[l], e->l2_blocks);
         if (merge_in_o) {
             a.S = e->S; a.s_stride = e->s_stride; a.Up = e->Wp; a.cstride = e->cstride; a.g = g;
+            a.ncap = merge_ncap(e);
             a.e.pd = pd; a.e.hd = hd; a.e.D = D;
         }
         if (pf_status s = pass_mm(e, m->o[l], merge_in_o ? MM_O_MERGE : MM_O, M, a, as1)) return s;
