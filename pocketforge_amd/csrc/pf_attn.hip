@@ -897,7 +897,7 @@ __device__ __forceinline__ void attn_group_body(const PassDesc* __restrict__ pd,
         prefetch_groups(pf, lin, bx, gx);
         return;
     }
-    const uint32_t epoch = LL ? lli.ep[0] : 0u;
+    const uint32_t epoch = LL ? ll_epoch(lli.ep) : 0u;
     int4* kt = reinterpret_cast<int4*>(smem);                       // [PARTS][256], swizzled
     int8_t (*vt)[128] = reinterpret_cast<int8_t (*)[128]>(smem + 256u * 128u);
     float* ksc = reinterpret_cast<float*>(smem + 512u * 128u);      // [256]

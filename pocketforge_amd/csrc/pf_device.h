@@ -215,6 +215,16 @@ __device__ __forceinline__ PassHead pass_head(const PassDesc* pd) {
     const uint4 w = *reinterpret_cast<const uint4*>(pd);
     return PassHead{w.x, w.y, w.z, w.w, pd};
 }
+// The same words with vector loads, for a kernel that needs them only after
+// its main loads: a scalar load issued early would hold up every later
+// kernel-argument read (scalar loads return out of order, so a wait for one
+// is a wait for all).
+__device__ __forceinline__ PassHead pass_head_late(const PassDesc* pd) {
+    const unsigned long long* q = reinterpret_cast<const unsigned long long*>(pd);
+    const unsigned long long a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return PassHead{(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32), pd};
+}
 __device__ __forceinline__ uint32_t row_pos(const PassHead& p, uint32_t m) {
     return p.batch ? p.pd->rpos[m] : p.pos0 + m;
 }
@@ -247,18 +257,20 @@ struct Prefetch {
     uint32_t groups;
     uint32_t blocks;    // prefetch workgroups a GEMV launch adds to its grid
     uint32_t* sink;
+    uint32_t xoff;      // the consumer reads group g on XCD (g + xoff) mod 8
 };
 
 // Prefetch block x of T, whose linear block id is lin (the prefetch blocks
-// of a launch have consecutive ids), loads the groups g = lin mod 8 (mod 8)
-// into its XCD's L2, sharing them with the other prefetch blocks of that
-// XCD (those with the same x mod 8).  The loaded words feed a value that is
-// stored only if it equals a constant, so the loads stay.
+// of a launch have consecutive ids), loads the groups g with
+// g + xoff = lin (mod 8) into its XCD's L2, sharing them with the other
+// prefetch blocks of that XCD (those with the same x mod 8).  The loaded
+// words feed a value that is stored only if it equals a constant, so the
+// loads stay.
 __device__ __forceinline__ void prefetch_groups(const Prefetch& pf, uint32_t lin, uint32_t x, uint32_t T) {
-    const uint32_t xcd = lin & 7u;
-    if (!pf.p || xcd >= pf.groups) return;
+    const uint32_t g0 = (lin - pf.xoff) & 7u;
+    if (!pf.p || g0 >= pf.groups) return;
     const uint32_t rank = x >> 3, cnt = (T - (x & 7u) + 7u) >> 3;
-    const uint32_t gb16 = pf.gbytes >> 4, n16 = ((pf.groups - xcd + 7u) >> 3) * gb16;
+    const uint32_t gb16 = pf.gbytes >> 4, n16 = ((pf.groups - g0 + 7u) >> 3) * gb16;
     const uint32_t stride = cnt * blockDim.x;
     const uint4* q = reinterpret_cast<const uint4*>(pf.p);
     uint32_t acc = 0;
@@ -267,7 +279,7 @@ __device__ __forceinline__ void prefetch_groups(const Prefetch& pf, uint32_t lin
 #pragma unroll
         for (uint32_t k = 0; k < 4; k++) {
             const uint32_t w = min(u + k * stride, n16 - 1u), i = w / gb16;   // i-th group of this XCD
-            v[k] = q[(size_t)(xcd + 8u * i) * gb16 + (w - i * gb16)];
+            v[k] = q[(size_t)(g0 + 8u * i) * gb16 + (w - i * gb16)];
         }
         acc ^= v[0].x ^ v[1].y ^ v[2].z ^ v[3].w;
     }
@@ -332,8 +344,18 @@ struct LLIn {
     const uint32_t* ep;
     uint32_t fmul, fadd;
     uint32_t* err;
+    // a word of the input that an early producer writes: a waiting wave
+    // polls it alone (one request per round) before it polls its own words,
+    // which keeps the memory traffic of long waits small
+    uint32_t sent;
 };
 constexpr uint32_t LL_SPIN_MAX = 1u << 20;
+
+// The pass epoch, with a vector load: it is needed only when the first LL
+// word is written or checked, after the kernel's main loads are issued.
+__device__ __forceinline__ uint32_t ll_epoch(const uint32_t* ep) {
+    return __hip_atomic_load(ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 __device__ __forceinline__ unsigned long long ll_load(const unsigned long long* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -347,6 +369,13 @@ __device__ __forceinline__ void ll_store(unsigned long long* p, float v, uint32_
 // Values of the N words base[off[i]] (off[i] == LL_NONE: 0) once each
 // carries `flag`.
 constexpr uint32_t LL_NONE = 0xFFFFFFFFu;
+//
+// One word per thread (a sentinel) is polled with two rounds of loads in
+// flight: while the older round is checked the newer one travels, so the
+// word is seen about half a memory round trip after it lands instead of up
+// to a whole one.  A round issued later sees every word an earlier round saw
+// (a word, once written for this pass and layer, keeps its flag until the
+// launch ends), so the newest completed round decides.
 template <int N>
 __device__ __forceinline__ void ll_wait(const unsigned long long* base, const uint32_t (&off)[N], float (&out)[N],
                                         uint32_t flag, uint32_t* err) {
@@ -354,6 +383,37 @@ __device__ __forceinline__ void ll_wait(const unsigned long long* base, const ui
     const unsigned long long done = (unsigned long long)flag << 32;
 #pragma unroll
     for (int i = 0; i < N; i++) w[i] = off[i] != LL_NONE ? ll_load(base + off[i]) : done;
+    if constexpr (N == 1) {
+        unsigned long long v[N];
+        __builtin_amdgcn_s_sleep(8);
+#pragma unroll
+        for (int i = 0; i < N; i++) v[i] = off[i] != LL_NONE ? ll_load(base + off[i]) : done;
+        for (uint32_t spins = 0;; spins++) {
+            bool ok = true;
+#pragma unroll
+            for (int i = 0; i < N; i++) ok = ok && (uint32_t)(w[i] >> 32) == flag;
+            if (ok) break;
+#pragma unroll
+            for (int i = 0; i < N; i++) w[i] = off[i] != LL_NONE ? ll_load(base + off[i]) : done;
+            ok = true;
+#pragma unroll
+            for (int i = 0; i < N; i++) ok = ok && (uint32_t)(v[i] >> 32) == flag;
+            if (ok) {
+#pragma unroll
+                for (int i = 0; i < N; i++) out[i] = __uint_as_float((uint32_t)v[i]);
+                return;
+            }
+            if (spins >= LL_SPIN_MAX) {
+                atomicOr(err, 1u);
+                break;
+            }
+#pragma unroll
+            for (int i = 0; i < N; i++) v[i] = off[i] != LL_NONE ? ll_load(base + off[i]) : done;
+        }
+#pragma unroll
+        for (int i = 0; i < N; i++) out[i] = __uint_as_float((uint32_t)w[i]);
+        return;
+    }
     for (uint32_t spins = 0;; spins++) {
         bool ok = true;
 #pragma unroll

@@ -93,7 +93,7 @@ __device__ __forceinline__ EpiPre epi_prefetch(const MmEpi& e, uint32_t m, uint3
             p.a = e.rc[(size_t)pos * half + t];
             p.b = e.rs[(size_t)pos * half + t];
         }
-        if (e.ll) p.f = e.ep[0] * e.fmul + e.fadd;
+        if (e.ll) p.f = ll_epoch(e.ep) * e.fmul + e.fadd;
     }
     return p;
 }
@@ -277,7 +277,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
     const uint32_t t = threadIdx.x, lane = t & 63u, r = lane & 31u, h = lane >> 5;
     const uint32_t wid = __builtin_amdgcn_readfirstlane(t >> 6);
     const float* __restrict__ xg = a.x;
-    const uint32_t llflag = LLM ? a.lli.ep[0] * a.lli.fmul + a.lli.fadd : 0u;
+    const uint32_t llflag = LLM ? ll_epoch(a.lli.ep) * a.lli.fmul + a.lli.fadd : 0u;
 
     // ---- prologue loads
     const uint32_t li = lane & 15u, q = lane >> 4, T = wid + GEMV_WAVES * q;   // NORM tile of this lane
@@ -367,7 +367,14 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
         for (int s = 0; s < SETS; s++) cw[j][s] = *reinterpret_cast<const uint4*>(tile + s * 1024 + lane * 16);
         sw[j] = *reinterpret_cast<const uint4*>(tile + CODES + r * 16);
     }
-    // ---- LL input rows (row 0), after the weight loads
+    // ---- LL input rows (row 0), after the weight loads: the sentinel word
+    // first (every lane of a wave loads the same word, one request), then the
+    // thread's own words
+    if constexpr ((LLM & LL_IN) != 0) {
+        const uint32_t so[1] = {a.lli.sent};
+        float sv[1];
+        ll_wait<1>(a.lli.ll, so, sv, llflag, a.lli.err);
+    }
     if constexpr ((LLM & LL_IN) && PRO == PRO_NORM) {
         const uint32_t col = 64u * min(T, nt - 1u) + li;
         uint32_t off[4];

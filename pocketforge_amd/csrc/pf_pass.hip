@@ -17,7 +17,8 @@
 // block (x mod tasks, x / tasks)); a block polls only the words it needs
 // (its rows' q, self k and self v in its head, and the pass rows' k and v it
 // quantizes) until every flag is the pass's, so a word it sees is a word
-// written in this pass.  The last `tasks` workgroups load the O weights into
+// written in this pass.  The last `tasks` workgroups load the next launch's
+// weights (b.pf, b.pf2, b.pf3: O, and with k_o_ffn gate|up and down) into
 // the L2 of the XCDs that will read them.
 //
 // Progress: each XCD receives its workgroups in id order, and the QKV
@@ -41,6 +42,7 @@ struct AttnGroupArgs {
     uint32_t cstride;
     Prefetch pf;
     LLIn lli;
+    Prefetch pf2, pf3;   // more weights the prefetch blocks load after pf's
 };
 
 // LDS of k_qkv_attn: the larger of the two roles' needs.
@@ -58,6 +60,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         return;
     }
     const uint32_t x = blockIdx.x - nq;
+    if (x / tasks >= b.M) {
+        // the prefetch row: the next launch's weights into L2, once the QKV
+        // product is done (its last word written), so that these loads run
+        // beside the attention's arithmetic rather than its K/V loads
+        const uint32_t last[1] = {3u * b.g.n_heads * b.g.head_dim - 1u};
+        float lv[1];
+        ll_wait<1>(b.lli.ll, last, lv, ll_epoch(b.lli.ep) * b.lli.fmul + b.lli.fadd, b.lli.err);
+        prefetch_groups(b.pf, blockIdx.x, x % tasks, tasks);
+        prefetch_groups(b.pf2, blockIdx.x, x % tasks, tasks);
+        prefetch_groups(b.pf3, blockIdx.x, x % tasks, tasks);
+        return;
+    }
     attn_group_body<PARTS, true, NR, true>(b.pd, b.g, b.kv, b.layer, b.M, nullptr, nullptr, nullptr, b.S,
                                            b.s_stride, b.Up, b.cstride, b.pf, b.lli, x % tasks, x / tasks,
                                            blockIdx.x, tasks, smem);
@@ -81,7 +95,7 @@ __device__ __forceinline__ void merge_cols_ll(const GemvArgs& a, uint32_t mb) {
     constexpr uint32_t MC = 16;
     const uint32_t D = a.K, hd = a.e.hd, hs = (uint32_t)__builtin_ctz(hd);
     const uint32_t j0 = 512u * mb + threadIdx.x, j = min(j0, D - 1u), h = j >> hs, e = j & (hd - 1u);
-    const uint32_t flag = a.lli.ep[0] * a.lli.fmul + a.lli.fadd;
+    const uint32_t flag = ll_epoch(a.lli.ep) * a.lli.fmul + a.lli.fadd;
     const float* sp = a.S + (size_t)h * a.s_stride;
     const float* up = a.Up + (size_t)h * a.cstride * hd + e;
     const uint32_t ncl = a.ncap;
@@ -93,7 +107,7 @@ __device__ __forceinline__ void merge_cols_ll(const GemvArgs& a, uint32_t mb) {
         ts[c] = sp[2u * cc + 1u];
         u[c] = up[(size_t)cc * hd];
     }
-    const uint32_t nc = (kv_view(a.g, row_pos(pass_head(a.e.pd), 0)).count() + 1u + 255u) / 256u;
+    const uint32_t nc = (kv_view(a.g, row_pos(pass_head_late(a.e.pd), 0)).count() + 1u + 255u) / 256u;
     float T = 0.0f, U = 0.0f;
     if (nc <= MC && nc <= ncl) {
         float mx = m[0];

@@ -1757,10 +1757,10 @@ static bool prefetchable(const pf_matrix* W) {
     const uint32_t groups = W ? W->rows / 32 : 0u;
     return W && !W->rowmajor && groups && W->bytes % groups == 0 && (W->bytes / groups) % 16 == 0;
 }
-static Prefetch prefetch_of(const pf_engine* e, const pf_matrix* W, uint32_t blocks) {
-    if (!blocks || !prefetchable(W)) return Prefetch{nullptr, 0, 0, 0, e->sink};
+static Prefetch prefetch_of(const pf_engine* e, const pf_matrix* W, uint32_t blocks, uint32_t xoff = 0) {
+    if (!blocks || !prefetchable(W)) return Prefetch{nullptr, 0, 0, 0, e->sink, 0};
     const uint32_t groups = W->rows / 32;
-    return Prefetch{W->data, (uint32_t)(W->bytes / groups), groups, blocks, e->sink};
+    return Prefetch{W->data, (uint32_t)(W->bytes / groups), groups, blocks, e->sink, xoff};
 }
 
 // LayerSkipController's threshold for layer l (src/layer_skip.cpp:43-55):
@@ -1922,7 +1922,12 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         // whose O workgroups read them; other passes run the merge kernel,
         // whose extra blocks do.  Each decode GEMV's extra blocks do the same
         // for the next product (O -> gate|up -> down -> next layer's QKV).
-        const Prefetch opf = merge_in_o ? prefetch_of(e, m->o[l], e->pf_blocks) : prefetch_of(e, nullptr, 0);
+        // with k_o_ffn the O, gate|up and down workgroups follow the merge
+        // workgroups in its grid, so their XCDs are offset by those before them
+        const bool tail = merge_in_o && o_ffn_ok(e, l);
+        const uint32_t n_mg = (D + 511) / 512, n_gu = m->gu[l]->rows / 32;
+        const Prefetch opf = merge_in_o ? prefetch_of(e, m->o[l], e->pf_blocks, tail ? n_mg : 0u)
+                                        : prefetch_of(e, nullptr, 0);
         if (qa) {
             a.W = m->qkv[l]->data;
             a.N = m->qkv[l]->rows;
@@ -1932,8 +1937,12 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
             a.e.ep = e->ep;
             a.e.fmul = d.n_layers;
             a.e.fadd = l;
-            const AttnGroupArgs b{pd, g, e->kv, l, M, e->S, e->s_stride, e->Wp, e->cstride, opf,
-                                  LLIn{e->ll, e->ep, d.n_layers, l, e->ll_err}};
+            AttnGroupArgs b{pd, g, e->kv, l, M, e->S, e->s_stride, e->Wp, e->cstride, opf,
+                            LLIn{e->ll, e->ep, d.n_layers, l, e->ll_err}};
+            if (tail) {
+                b.pf2 = prefetch_of(e, m->gu[l], e->pf_blocks, n_mg + D / 32);
+                b.pf3 = prefetch_of(e, m->down[l], e->pf_blocks, n_mg + D / 32 + n_gu);
+            }
             if (hd == 64) qkv_attn_rows<4>(st, a, b, attn_tasks, aev0, aev1);
             else qkv_attn_rows<8>(st, a, b, attn_tasks, aev0, aev1);
         } else {
@@ -1946,7 +1955,7 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
                                                     e->cstride, e->act, ks, as1, (int32_t*)nullptr, 0u, M,
                                                     prefetch_of(e, m->o[l], e->pf_blocks)));
         // one-row passes without layer skip: O, gate|up and down in one launch
-        if (merge_in_o && o_ffn_ok(e, l)) {
+        if (tail) {
             const LLIn li{nullptr, e->ep, d.n_layers, l, e->ll_err};
             GemvArgs ao{}, ag{}, ad{};
             ao.W = m->o[l]->data; ao.N = D; ao.K = D; ao.M = 1;
