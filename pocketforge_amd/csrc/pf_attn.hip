@@ -1051,21 +1051,14 @@ __device__ __forceinline__ void attn_group_body(const PassDesc* __restrict__ pd,
             wa[3 * QPT + 4 * u + 2] = use ? b + D : LL_NONE;
             wa[3 * QPT + 4 * u + 3] = use ? b + D + 1u : LL_NONE;
         }
-        // one thread first waits for a word of each of the head's producer
-        // workgroups (32 output rows each of q, k and v), so that the block
-        // does not keep the memory system busy with all its words' polls
+        // each wave first waits for one word of the head's v rows (every
+        // lane loads the same word: one request per round), so that the
+        // block does not keep the memory system busy with all its words'
+        // polls, then for its own words
         const uint32_t flag = epoch * lli.fmul + lli.fadd;
-        if (t == 0) {
-            uint32_t sp[12];
-            float sv_[12];
-#pragma unroll
-            for (uint32_t j = 0; j < 4; j++)
-#pragma unroll
-                for (uint32_t sec = 0; sec < 3; sec++)
-                    sp[3 * j + sec] = 32u * j < hd ? mb * rs3 + sec * D + h * hd + 32u * j : LL_NONE;
-            ll_wait<12>(lli.ll, sp, sv_, flag, lli.err);
-        }
-        __syncthreads();
+        const uint32_t sp[1] = {mb * rs3 + 2u * D + h * hd + hd - 1u};
+        float sv_[1];
+        ll_wait<1>(lli.ll, sp, sv_, flag, lli.err);
         ll_wait<NW>(lli.ll, wa, wv_, flag, lli.err);
 #pragma unroll
         for (uint32_t k = 0; k < QPT; k++) {
