@@ -67,7 +67,7 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_i8_traffic_1b_q4.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "o_ffn_traffic_1b_q4.md")
 
 
 def measured_traffic():
@@ -378,12 +378,12 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": measured_traffic() if headline else None,
-            "traffic_source": "profiles/gemv_i8_traffic_1b_q4.md (rocprofv3 FETCH_SIZE x 1.99978 + WRITE_SIZE x 1.0, "
-                              "factors from a copy kernel of known size)",
+            "traffic_source": "profiles/o_ffn_traffic_1b_q4.md (rocprofv3 FETCH_SIZE x 1.99978 + WRITE_SIZE x 1.0, "
+                              "factors from a copy kernel of known size; prefetch off)",
             "avg_launch_us": round(gemv_us, 3),
             "avg_bytes_per_launch": round(gemv_bytes),
             "launches": n_l,
-            "timing": "HIP start/stop events attached to each GEMV dispatch (hipExtLaunchKernelGGL) on the engine "
+            "timing": "HIP start/stop events attached to each k_o_ffn dispatch (hipExtLaunchKernelGGL) on the engine "
                       "stream, in one extra decode step of the same workload issued without graphs",
             "by_matrix": [{"bytes": round(b), "launches": n, "avg_us": round(u, 3),
                            "GBps": round(b / u / 1e3, 1)} for b, n, u in gemv_groups],

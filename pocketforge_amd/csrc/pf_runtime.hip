@@ -1964,7 +1964,7 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
             ao.ncap = e->cstride - 1;
             ao.e.pd = pd; ao.e.hd = hd; ao.e.D = D;
             ao.e.y = e->x; ao.e.y_stride = D; ao.e.ll = e->llt;
-            ao.nx = prefetch_of(e, l + 1 < d.n_layers ? m->qkv[l + 1] : nullptr, D / 32);
+            ao.nx = prefetch_of(e, l + 1 < d.n_layers ? m->qkv[l + 1] : nullptr, e->l2_blocks ? D / 32 : 0u);
             ao.lli = li;
             ao.lli.ll = e->llt + D + F;
             ag.W = m->gu[l]->data; ag.N = m->gu[l]->rows; ag.K = D; ag.M = 1;
