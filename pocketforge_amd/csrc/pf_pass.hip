@@ -89,8 +89,9 @@ __host__ __device__ constexpr uint32_t o_ffn_smem(uint32_t D, uint32_t F) {
 // m_c), T and U fmaf chains over c in order, U * (1 / (T + 1e-10)), the
 // arithmetic of merge_quant_row before its quantization.  Loads cover
 // ncap chunks (a.ncap, the buffers' capacity) so they issue before the
-// pass descriptor gives the count nc; lists of more than MC chunks read
-// their chunks again in a loop.
+// pass descriptor gives the count nc; lists of more than MC chunks load the
+// later chunks MC at a time (one round trip per group for the maximum and
+// one for the chains).
 __device__ __forceinline__ void merge_cols_ll(const GemvArgs& a, uint32_t mb) {
     constexpr uint32_t MC = 16;
     const uint32_t D = a.K, hd = a.e.hd, hs = (uint32_t)__builtin_ctz(hd);
@@ -108,27 +109,44 @@ __device__ __forceinline__ void merge_cols_ll(const GemvArgs& a, uint32_t mb) {
         u[c] = up[(size_t)cc * hd];
     }
     const uint32_t nc = (kv_view(a.g, row_pos(pass_head_late(a.e.pd), 0)).count() + 1u + 255u) / 256u;
+    // the maximum over the chunk maxima (exact in any order), later groups of
+    // MC chunks loaded together, one round trip per group
+    float mx = m[0];
+#pragma unroll
+    for (uint32_t c = 1; c < MC; c++)
+        if (c < nc) mx = fmaxf(mx, m[c]);
+    for (uint32_t c0 = MC; c0 < nc; c0 += MC) {
+        float mm[MC];
+#pragma unroll
+        for (uint32_t k = 0; k < MC; k++) mm[k] = sp[2u * min(c0 + k, nc - 1u)];
+#pragma unroll
+        for (uint32_t k = 0; k < MC; k++) mx = fmaxf(mx, mm[k]);
+    }
+    // T and U chains over c in order
     float T = 0.0f, U = 0.0f;
-    if (nc <= MC && nc <= ncl) {
-        float mx = m[0];
 #pragma unroll
-        for (uint32_t c = 1; c < MC; c++)
-            if (c < nc) mx = fmaxf(mx, m[c]);
-#pragma unroll
-        for (uint32_t c = 0; c < MC; c++) {
-            if (c < nc) {
-                const float f = expf_c(m[c] - mx);
-                T = __builtin_fmaf(ts[c], f, T);
-                U = __builtin_fmaf(u[c], f, U);
-            }
+    for (uint32_t c = 0; c < MC; c++) {
+        if (c < nc) {
+            const float f = expf_c(m[c] - mx);
+            T = __builtin_fmaf(ts[c], f, T);
+            U = __builtin_fmaf(u[c], f, U);
         }
-    } else {
-        float mx = sp[0];
-        for (uint32_t c = 1; c < nc; c++) mx = fmaxf(mx, sp[2u * c]);
-        for (uint32_t c = 0; c < nc; c++) {
-            const float f = expf_c(sp[2u * c] - mx);
-            T = __builtin_fmaf(sp[2u * c + 1u], f, T);
-            U = __builtin_fmaf(up[(size_t)c * hd], f, U);
+    }
+    for (uint32_t c0 = MC; c0 < nc; c0 += MC) {
+#pragma unroll
+        for (uint32_t k = 0; k < MC; k++) {
+            const uint32_t cc = min(c0 + k, nc - 1u);
+            m[k] = sp[2u * cc];
+            ts[k] = sp[2u * cc + 1u];
+            u[k] = up[(size_t)cc * hd];
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < MC; k++) {
+            if (c0 + k < nc) {
+                const float f = expf_c(m[k] - mx);
+                T = __builtin_fmaf(ts[k], f, T);
+                U = __builtin_fmaf(u[k], f, U);
+            }
         }
     }
     if (j0 < D) ll_store(const_cast<unsigned long long*>(a.lli.ll) + j0, U * (1.0f / (T + 1e-10f)), flag);
