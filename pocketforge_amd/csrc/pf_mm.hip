@@ -250,11 +250,15 @@ __device__ __forceinline__ float max4abs(float4 v) {
 //          row quantized (quantize_activation_row).
 //
 // gemv_body is the workgroup's work as workgroup bx of gx; k_gemv runs it
-// as its own grid, k_qkv_attn and k_o_ffn as workgroups of a wider one.
+// as its own grid, k_qkv_attn and k_o_ffn as workgroups of a wider one.  The
+// weights, input rows and norm weights come as parameters (a kernel may
+// pass them as preloaded arguments), the rest from a.
 // With LL_IN the prologue's input words are waited for after the weight
 // loads have been issued, so the weights stream in during the wait.
 template <int FMT, int PRO, int EPI, bool GATED, int CPW, int MR, int LLM = 0>
-__device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32_t gx, uint8_t* smem) {
+__device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32_t gx, uint8_t* smem,
+                                          const uint8_t* __restrict__ Wm, const float* __restrict__ xin,
+                                          const float* __restrict__ nwv) {
     static_assert(!(LLM & LL_IN) || (MR == 1 && (PRO == PRO_NORM || PRO == PRO_QUANT)),
                   "LL input rows: one row, NORM or QUANT prologue");
     constexpr uint32_t TB = g32_tile_bytes(FMT), CODES = g32_code_bytes(FMT);
@@ -276,7 +280,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
     float* st_as = st + 16;                    // amax / 127
     const uint32_t t = threadIdx.x, lane = t & 63u, r = lane & 31u, h = lane >> 5;
     const uint32_t wid = __builtin_amdgcn_readfirstlane(t >> 6);
-    const float* __restrict__ xg = a.x;
+    const float* __restrict__ xg = xin;
     const uint32_t llflag = LLM ? ll_epoch(a.lli.ep) * a.lli.fmul + a.lli.fadd : 0u;
 
     // ---- prologue loads
@@ -289,7 +293,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
     if constexpr (PRO == PRO_NORM) {
         const uint32_t col = 64u * min(T, nt - 1u) + li;
 #pragma unroll
-        for (int k = 0; k < 4; k++) wv[k] = a.nw[col + 16u * k];
+        for (int k = 0; k < 4; k++) wv[k] = nwv[col + 16u * k];
         if constexpr (!(LLM & LL_IN)) {
 #pragma unroll
             for (uint32_t m = 0; m < MR; m++)
@@ -358,7 +362,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
 
     // ---- weight loads
     const uint32_t nch = K >> 8, c0 = nch * wid / GEMV_WAVES, c1 = nch * (wid + 1) / GEMV_WAVES;
-    const uint8_t* tiles = a.W + (size_t)bx * nch * TB;
+    const uint8_t* tiles = Wm + (size_t)bx * nch * TB;
     uint4 cw[CPW][SETS], sw[CPW];
 #pragma unroll
     for (int j = 0; j < CPW; j++) {
@@ -679,7 +683,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
 template <int FMT, int PRO, int EPI, bool GATED, int CPW, int MR>
 __global__ __launch_bounds__(64 * GEMV_WAVES) void k_gemv(GemvArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    gemv_body<FMT, PRO, EPI, GATED, CPW, MR>(a, blockIdx.x, gridDim.x, smem);
+    gemv_body<FMT, PRO, EPI, GATED, CPW, MR>(a, blockIdx.x, gridDim.x, smem, a.W, a.x, a.nw);
 }
 
 // =============================================================== GEMM

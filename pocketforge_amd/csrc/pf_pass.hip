@@ -53,10 +53,12 @@ __host__ __device__ constexpr uint32_t qkv_attn_smem(uint32_t M, uint32_t K, uin
 // Two blocks per CU (at most 128 VGPRs: 4 waves per SIMD), so that the
 // attention blocks are resident beside the QKV workgroups.
 template <int FMT, int MR, int PARTS, int NR>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_qkv_attn(GemvArgs a, AttnGroupArgs b, uint32_t nq, uint32_t tasks) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_qkv_attn(uint32_t nq, uint32_t tasks, const PassDesc* pd, const uint8_t* W, const float* xr,
+                                      const float* nw, GemvArgs a, AttnGroupArgs b) {
     extern __shared__ __align__(16) uint8_t smem[];
     if (blockIdx.x < nq) {
-        gemv_body<FMT, PRO_NORM, EPI_QKV, false, 1, MR>(a, blockIdx.x, nq, smem);
+        // the operands of its first loads come preloaded into SGPRs
+        gemv_body<FMT, PRO_NORM, EPI_QKV, false, 1, MR>(a, blockIdx.x, nq, smem, W, xr, nw);
         return;
     }
     const uint32_t x = blockIdx.x - nq;
@@ -72,7 +74,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         prefetch_groups(b.pf3, blockIdx.x, x % tasks, tasks);
         return;
     }
-    attn_group_body<PARTS, true, NR, true>(b.pd, b.g, b.kv, b.layer, b.M, nullptr, nullptr, nullptr, b.S,
+    attn_group_body<PARTS, true, NR, true>(pd, b.g, b.kv, b.layer, b.M, nullptr, nullptr, nullptr, b.S,
                                            b.s_stride, b.Up, b.cstride, b.pf, b.lli, x % tasks, x / tasks,
                                            blockIdx.x, tasks, smem);
 }
@@ -92,14 +94,18 @@ __host__ __device__ constexpr uint32_t o_ffn_smem(uint32_t D, uint32_t F) {
 // pass descriptor gives the count nc; lists of more than MC chunks load the
 // later chunks MC at a time (one round trip per group for the maximum and
 // one for the chains).
-__device__ __forceinline__ void merge_cols_ll(const GemvArgs& a, uint32_t mb) {
+// The inputs its loads need come as separate kernel arguments (preloaded
+// into SGPRs), the rest from a.
+__device__ __forceinline__ void merge_cols_ll(const GemvArgs& a, uint32_t mb, const float* S, const float* Up,
+                                              const uint32_t* ep, const PassDesc* pd, uint32_t s_stride,
+                                              uint32_t cstride, uint32_t D, uint32_t hd, uint32_t ncap) {
     constexpr uint32_t MC = 16;
-    const uint32_t D = a.K, hd = a.e.hd, hs = (uint32_t)__builtin_ctz(hd);
+    const uint32_t hs = (uint32_t)__builtin_ctz(hd);
     const uint32_t j0 = 512u * mb + threadIdx.x, j = min(j0, D - 1u), h = j >> hs, e = j & (hd - 1u);
-    const uint32_t flag = ll_epoch(a.lli.ep) * a.lli.fmul + a.lli.fadd;
-    const float* sp = a.S + (size_t)h * a.s_stride;
-    const float* up = a.Up + (size_t)h * a.cstride * hd + e;
-    const uint32_t ncl = a.ncap;
+    const uint32_t epoch = ll_epoch(ep);
+    const float* sp = S + (size_t)h * s_stride;
+    const float* up = Up + (size_t)h * cstride * hd + e;
+    const uint32_t ncl = ncap;
     float m[MC], ts[MC], u[MC];
 #pragma unroll
     for (uint32_t c = 0; c < MC; c++) {
@@ -108,7 +114,8 @@ __device__ __forceinline__ void merge_cols_ll(const GemvArgs& a, uint32_t mb) {
         ts[c] = sp[2u * cc + 1u];
         u[c] = up[(size_t)cc * hd];
     }
-    const uint32_t nc = (kv_view(a.g, row_pos(pass_head_late(a.e.pd), 0)).count() + 1u + 255u) / 256u;
+    const uint32_t nc = (kv_view(a.g, row_pos(pass_head_late(pd), 0)).count() + 1u + 255u) / 256u;
+    const uint32_t flag = epoch * a.lli.fmul + a.lli.fadd;
     // the maximum over the chunk maxima (exact in any order), later groups of
     // MC chunks loaded together, one round trip per group
     float mx = m[0];
@@ -171,19 +178,22 @@ __device__ __forceinline__ void merge_cols_ll(const GemvArgs& a, uint32_t mb) {
 // and a workgroup waits only for workgroups of earlier stages (lower ids),
 // and the first stage waits for nothing; every wait is bounded.
 template <int FMT, int CPWD>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_o_ffn(uint32_t n_mg, uint32_t n_o, uint32_t n_gu, GemvArgs o, GemvArgs gu, GemvArgs dn) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_o_ffn(uint32_t n_mg, uint32_t n_o, uint32_t n_gu, const float* mS, const float* mUp, uint32_t s_stride,
+             uint32_t cstride, uint32_t D, uint32_t hd, uint32_t ncap, const uint32_t* ep, const PassDesc* pd,
+             GemvArgs o, GemvArgs gu, GemvArgs dn) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t b = blockIdx.x;
     if (b < n_mg) {
-        merge_cols_ll(o, b);
+        merge_cols_ll(o, b, mS, mUp, ep, pd, s_stride, cstride, D, hd, ncap);
     } else if (b < n_mg + n_o) {
-        gemv_body<FMT, PRO_QUANT, EPI_RESID, false, 1, 1, LL_IN | LL_OUT>(o, b - n_mg, n_o, smem);
+        gemv_body<FMT, PRO_QUANT, EPI_RESID, false, 1, 1, LL_IN | LL_OUT>(o, b - n_mg, n_o, smem, o.W, o.x, o.nw);
         prefetch_groups(o.nx, b, b - n_mg, n_o);
     } else if (b < n_mg + n_o + n_gu) {
-        gemv_body<FMT, PRO_NORM, EPI_SWIGLU, false, 1, 1, LL_IN | LL_OUT>(gu, b - n_mg - n_o, n_gu, smem);
+        gemv_body<FMT, PRO_NORM, EPI_SWIGLU, false, 1, 1, LL_IN | LL_OUT>(gu, b - n_mg - n_o, n_gu, smem, gu.W, gu.x,
+                                                                          gu.nw);
     } else {
         const uint32_t x = b - n_mg - n_o - n_gu;
-        gemv_body<FMT, PRO_QUANT, EPI_RESID, false, CPWD, 1, LL_IN | LL_OLD>(dn, x, dn.N / 32u, smem);
+        gemv_body<FMT, PRO_QUANT, EPI_RESID, false, CPWD, 1, LL_IN | LL_OLD>(dn, x, dn.N / 32u, smem, dn.W, dn.x, dn.nw);
     }
 }
 

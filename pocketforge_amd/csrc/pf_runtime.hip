@@ -686,9 +686,11 @@ static void qkv_attn_one(hipStream_t st, const GemvArgs& a, const AttnGroupArgs&
     const uint32_t smem = qkv_attn_smem(a.M, a.K, NR);
     const dim3 grid(nq + tasks * (b.M + (b.pf.p ? 1u : 0u)));
     if (ev0)
-        hipExtLaunchKernelGGL((k_qkv_attn<FMT_Q4, MR, P, NR>), grid, dim3(512), smem, st, ev0, ev1, 0, a, b, nq, tasks);
+        hipExtLaunchKernelGGL((k_qkv_attn<FMT_Q4, MR, P, NR>), grid, dim3(512), smem, st, ev0, ev1, 0, nq, tasks, b.pd,
+                              a.W, a.x, a.nw, a, b);
     else
-        hipLaunchKernelGGL((k_qkv_attn<FMT_Q4, MR, P, NR>), grid, dim3(512), smem, st, a, b, nq, tasks);
+        hipLaunchKernelGGL((k_qkv_attn<FMT_Q4, MR, P, NR>), grid, dim3(512), smem, st, nq, tasks, b.pd, a.W, a.x, a.nw,
+                           a, b);
 }
 
 template <int P>
@@ -1826,11 +1828,13 @@ static void o_ffn_one(hipStream_t st, const GemvArgs& ao, const GemvArgs& ag, co
     const uint32_t n_mg = (ao.K + 511) / 512, n_o = ao.N / 32, n_gu = ag.N / 32, n_dn = ad.N / 32;
     const uint32_t smem = o_ffn_smem(ao.K, ad.K);
     const dim3 grid(n_mg + n_o + n_gu + n_dn);
+    // the merge workgroups' inputs lead the argument list (preloaded into SGPRs)
     if (ev0)
-        hipExtLaunchKernelGGL((k_o_ffn<FMT_Q4, CPWD>), grid, dim3(512), smem, st, ev0, ev1, 0, n_mg, n_o, n_gu, ao, ag,
-                              ad);
+        hipExtLaunchKernelGGL((k_o_ffn<FMT_Q4, CPWD>), grid, dim3(512), smem, st, ev0, ev1, 0, n_mg, n_o, n_gu, ao.S,
+                              ao.Up, ao.s_stride, ao.cstride, ao.K, ao.e.hd, ao.ncap, ao.lli.ep, ao.e.pd, ao, ag, ad);
     else
-        hipLaunchKernelGGL((k_o_ffn<FMT_Q4, CPWD>), grid, dim3(512), smem, st, n_mg, n_o, n_gu, ao, ag, ad);
+        hipLaunchKernelGGL((k_o_ffn<FMT_Q4, CPWD>), grid, dim3(512), smem, st, n_mg, n_o, n_gu, ao.S, ao.Up, ao.s_stride,
+                           ao.cstride, ao.K, ao.e.hd, ao.ncap, ao.lli.ep, ao.e.pd, ao, ag, ad);
 }
 
 static void launch_o_ffn(hipStream_t st, const GemvArgs& ao, const GemvArgs& ag, const GemvArgs& ad, hipEvent_t ev0,
