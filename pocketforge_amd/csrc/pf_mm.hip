@@ -37,7 +37,8 @@ enum Epi : int { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_SWIGLU = 3 };
 //   LL_IN : the NORM / QUANT prologue's input rows are LL words, lli.ll[m xs + col]
 //   LL_OLD: the RESID epilogue's old values are LL words, e.llold[m y_stride + n]
 //   LL_OUT: the RESID / SWIGLU epilogue writes LL words to e.ll instead of e.y
-enum LLMode : int { LL_IN = 1, LL_OLD = 2, LL_OUT = 4 };
+//   LL_COPY: with LL_OUT, RESID also stores the rows to e.y2 (for a later launch)
+enum LLMode : int { LL_IN = 1, LL_OLD = 2, LL_OUT = 4, LL_COPY = 8 };
 
 // Consumer step applied to the outputs.  Row n is a device row (pf_layout.h).
 struct MmEpi {
@@ -50,7 +51,7 @@ struct MmEpi {
     const PassDesc* pd;        // QKV: positions of the pass rows
     uint32_t D, hd;
     float* pmax;               // SWIGLU (GEMV): per-workgroup row maxima of |output| [M][N / 32], or null
-    float* y2;                 // RESID: a copy of the updated rows (a pass's hidden output), or null
+    float* y2;                 // RESID: a copy of the updated rows (a pass's hidden output, or with LL_OUT the rows for a later launch), or null
     // QKV of a one-launch QKV + attention pass: instead of q/k/v, the rows
     // go to ll[m][3 D] as 8-byte words (value bits, flag) written with one
     // device-scope store each, flag = ep[0] * fmul + fadd (the pass epoch
@@ -108,6 +109,7 @@ __device__ __forceinline__ float epi_apply(const MmEpi& e, const EpiPre& p, uint
         e.y[(size_t)m * e.y_stride + (e.ilv ? ilv_logical(n, N) : n)] = y;
     } else if constexpr (EPI == EPI_RESID && (LLM & LL_OUT)) {
         ll_store(e.ll + (size_t)m * e.y_stride + n, p.a + y, p.f);
+        if constexpr ((LLM & LL_COPY) != 0) e.y2[(size_t)m * e.y_stride + n] = p.a + y;
     } else if constexpr (EPI == EPI_RESID) {
         if (p.b == 0.0f) e.y[(size_t)m * e.y_stride + n] = p.a + y;
         if (e.y2) e.y2[(size_t)m * e.y_stride + n] = p.b == 0.0f ? p.a + y : p.a;
@@ -259,8 +261,7 @@ template <int FMT, int PRO, int EPI, bool GATED, int CPW, int MR, int LLM = 0>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32_t gx, uint8_t* smem,
                                           const uint8_t* __restrict__ Wm, const float* __restrict__ xin,
                                           const float* __restrict__ nwv) {
-    static_assert(!(LLM & LL_IN) || (MR == 1 && (PRO == PRO_NORM || PRO == PRO_QUANT)),
-                  "LL input rows: one row, NORM or QUANT prologue");
+    static_assert(!(LLM & LL_IN) || PRO == PRO_NORM || PRO == PRO_QUANT, "LL input rows: NORM or QUANT prologue");
     constexpr uint32_t TB = g32_tile_bytes(FMT), CODES = g32_code_bytes(FMT);
     constexpr int SETS = sets_of<FMT>();
     constexpr uint32_t NT = 64u * GEMV_WAVES;
@@ -371,9 +372,9 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
         for (int s = 0; s < SETS; s++) cw[j][s] = *reinterpret_cast<const uint4*>(tile + s * 1024 + lane * 16);
         sw[j] = *reinterpret_cast<const uint4*>(tile + CODES + r * 16);
     }
-    // ---- LL input rows (row 0), after the weight loads: the sentinel word
-    // first (every lane of a wave loads the same word, one request), then the
-    // thread's own words
+    // ---- LL input rows, after the weight loads: the sentinel word first
+    // (every lane of a wave loads the same word, one request), then the
+    // thread's own words row by row (rows past M repeat row M - 1)
     if constexpr ((LLM & LL_IN) != 0) {
         const uint32_t so[1] = {a.lli.sent};
         float sv[1];
@@ -381,25 +382,31 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
     }
     if constexpr ((LLM & LL_IN) && PRO == PRO_NORM) {
         const uint32_t col = 64u * min(T, nt - 1u) + li;
-        uint32_t off[4];
-        float v[4];
 #pragma unroll
-        for (int k = 0; k < 4; k++) off[k] = col + 16u * k;
-        ll_wait<4>(a.lli.ll, off, v, llflag, a.lli.err);
+        for (uint32_t m = 0; m < MR; m++) {
+            uint32_t off[4];
+            float v[4];
 #pragma unroll
-        for (int k = 0; k < 4; k++) xv[0][k] = v[k];
-    } else if constexpr ((LLM & LL_IN) && PRO == PRO_QUANT) {
-        uint32_t off[4 * CPW];
-        float v[4 * CPW];
+            for (int k = 0; k < 4; k++) off[k] = (MR == 1 ? 0u : min(m, mlast) * xs) + col + 16u * k;
+            ll_wait<4>(a.lli.ll, off, v, llflag, a.lli.err);
 #pragma unroll
-        for (int k = 0; k < CPW; k++) {
-            const uint32_t c = min(t + NT * k, per4 - 1u);
-#pragma unroll
-            for (int j = 0; j < 4; j++) off[4 * k + j] = 4u * c + j;
+            for (int k = 0; k < 4; k++) xv[m][k] = v[k];
         }
-        ll_wait<4 * CPW>(a.lli.ll, off, v, llflag, a.lli.err);
+    } else if constexpr ((LLM & LL_IN) && PRO == PRO_QUANT) {
 #pragma unroll
-        for (int k = 0; k < CPW; k++) hv[0][k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+        for (uint32_t m = 0; m < MR; m++) {
+            uint32_t off[4 * CPW];
+            float v[4 * CPW];
+#pragma unroll
+            for (int k = 0; k < CPW; k++) {
+                const uint32_t c = min(t + NT * k, per4 - 1u);
+#pragma unroll
+                for (int j = 0; j < 4; j++) off[4 * k + j] = (MR == 1 ? 0u : min(m, mlast) * xs) + 4u * c + j;
+            }
+            ll_wait<4 * CPW>(a.lli.ll, off, v, llflag, a.lli.err);
+#pragma unroll
+            for (int k = 0; k < CPW; k++) hv[m][k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+        }
     }
     // ---- epilogue operands: thread t outputs row om of device row on
     const uint32_t om = t >> 5, on = 32u * bx + (t & 31u);

@@ -1,6 +1,6 @@
-// One-launch stages of a decode pass, for gfx950: the Q/K/V product with
-// the attention (passes of at most 8 rows), and the O, gate|up and down
-// products (one-row passes).
+// One-launch stages of a decode pass (at most 8 rows), for gfx950: the
+// Q/K/V product with the attention, and the chunk merge with the O, gate|up
+// and down products.
 //
 // The attention of a one-row pass reads about 9.5 MB of cached K/V rows per
 // layer at the 1B model's 2K context, and none of them depends on the pass's
@@ -79,14 +79,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
                                            blockIdx.x, tasks, smem);
 }
 
-// LDS of k_o_ffn: the largest of its GEMV roles' needs.
-__host__ __device__ constexpr uint32_t o_ffn_smem(uint32_t D, uint32_t F) {
-    return gemv_smem(1, D) > gemv_smem(1, F) ? gemv_smem(1, D) : gemv_smem(1, F);
+// LDS of k_o_ffn for M rows: the largest of its GEMV roles' needs.
+__host__ __device__ constexpr uint32_t o_ffn_smem(uint32_t M, uint32_t D, uint32_t F) {
+    return gemv_smem(M, D) > gemv_smem(M, F) ? gemv_smem(M, D) : gemv_smem(M, F);
 }
 
-// The chunk merge of a one-row pass's attention output for the columns
-// 512 mb .. 512 mb + 511 of the row, one column per thread, as LL words to
-// a.lli.ll: for column j of head h, with the chunks' maxima m_c, sums T_c
+// The chunk merge of a decode pass's attention output for the columns
+// 512 cb .. 512 cb + 511 of row `row`, one column per thread, as LL words to
+// a.lli.ll[row D ..]: for column j of head h, with the chunks' maxima m_c, sums T_c
 // and weighted values U_c (the attention's S and Up), f_c = exp(m_c - max_c
 // m_c), T and U fmaf chains over c in order, U * (1 / (T + 1e-10)), the
 // arithmetic of merge_quant_row before its quantization.  Loads cover
@@ -96,15 +96,16 @@ __host__ __device__ constexpr uint32_t o_ffn_smem(uint32_t D, uint32_t F) {
 // one for the chains).
 // The inputs its loads need come as separate kernel arguments (preloaded
 // into SGPRs), the rest from a.
-__device__ __forceinline__ void merge_cols_ll(const GemvArgs& a, uint32_t mb, const float* S, const float* Up,
-                                              const uint32_t* ep, const PassDesc* pd, uint32_t s_stride,
-                                              uint32_t cstride, uint32_t D, uint32_t hd, uint32_t ncap) {
+__device__ __forceinline__ void merge_cols_ll(const GemvArgs& a, uint32_t row, uint32_t cb, const float* S,
+                                              const float* Up, const uint32_t* ep, const PassDesc* pd,
+                                              uint32_t s_stride, uint32_t cstride, uint32_t D, uint32_t hd,
+                                              uint32_t ncap) {
     constexpr uint32_t MC = 16;
-    const uint32_t hs = (uint32_t)__builtin_ctz(hd);
-    const uint32_t j0 = 512u * mb + threadIdx.x, j = min(j0, D - 1u), h = j >> hs, e = j & (hd - 1u);
+    const uint32_t hs = (uint32_t)__builtin_ctz(hd), H = D >> hs;
+    const uint32_t j0 = 512u * cb + threadIdx.x, j = min(j0, D - 1u), h = j >> hs, e = j & (hd - 1u);
     const uint32_t epoch = ll_epoch(ep);
-    const float* sp = S + (size_t)h * s_stride;
-    const float* up = Up + (size_t)h * cstride * hd + e;
+    const float* sp = S + ((size_t)row * H + h) * s_stride;
+    const float* up = Up + ((size_t)row * H + h) * cstride * hd + e;
     const uint32_t ncl = ncap;
     float m[MC], ts[MC], u[MC];
 #pragma unroll
@@ -114,7 +115,7 @@ __device__ __forceinline__ void merge_cols_ll(const GemvArgs& a, uint32_t mb, co
         ts[c] = sp[2u * cc + 1u];
         u[c] = up[(size_t)cc * hd];
     }
-    const uint32_t nc = (kv_view(a.g, row_pos(pass_head_late(pd), 0)).count() + 1u + 255u) / 256u;
+    const uint32_t nc = (kv_view(a.g, row_pos(pass_head_late(pd), row)).count() + 1u + 255u) / 256u;
     const uint32_t flag = epoch * a.lli.fmul + a.lli.fadd;
     // the maximum over the chunk maxima (exact in any order), later groups of
     // MC chunks loaded together, one round trip per group
@@ -156,20 +157,23 @@ __device__ __forceinline__ void merge_cols_ll(const GemvArgs& a, uint32_t mb, co
             }
         }
     }
-    if (j0 < D) ll_store(const_cast<unsigned long long*>(a.lli.ll) + j0, U * (1.0f / (T + 1e-10f)), flag);
+    if (j0 < D)
+        ll_store(const_cast<unsigned long long*>(a.lli.ll) + (size_t)row * D + j0, U * (1.0f / (T + 1e-10f)), flag);
 }
 
-// The rest of a one-row pass's layer after the attention, in one launch:
-// workgroups [0, n_mg) merge the attention's chunks into the row (LL words
-// at o.lli.ll), [n_mg, n_mg + n_o) are the O product's (quantize prologue
-// over the merged row, residual epilogue), the next n_gu the gate|up
-// product's (RMSNorm + quantize prologue, SwiGLU epilogue), the last N / 32
-// the down product's (quantize prologue, residual epilogue).  Stage outputs
-// are LL words: O writes the updated residual row to o.e.ll (D words),
-// gate|up its SwiGLU row to gu.e.ll (F words); gate|up reads the residual
-// row and down reads both.  The GEMV workgroups issue their weight loads as
-// they start, before they wait, so the weights stream in while the earlier
-// stages run; the O workgroups, once done, load the next layer's QKV
+// The rest of a decode pass's layer after the attention (M <= MR rows), in
+// one launch: workgroups [0, n_mg) merge the attention's chunks into the
+// rows (ceil(D / 512) per row; LL words at o.lli.ll), [n_mg, n_mg + n_o)
+// are the O product's (quantize prologue over the merged rows, residual
+// epilogue), the next n_gu the gate|up product's (RMSNorm + quantize
+// prologue, SwiGLU epilogue), the last N / 32 the down product's (quantize
+// prologue, residual epilogue).  Stage outputs are LL words: O writes the
+// updated residual rows to o.e.ll ([M][D] words), gate|up its SwiGLU rows
+// to gu.e.ll ([M][F] words); gate|up reads the residual rows and down
+// reads both (passes of several rows stop after gate|up, which then writes
+// plain rows and row maxima for a separate down launch).  The GEMV
+// workgroups issue their weight loads as they start, before they wait, so
+// the weights stream in while the earlier stages run; the O workgroups, once done, load the next layer's QKV
 // weights (o.nx) into the L2 of the XCDs whose workgroups will read them.
 // Only down writes the residual row itself (dn.e.y) and the pass's hidden
 // output.
@@ -177,23 +181,40 @@ __device__ __forceinline__ void merge_cols_ll(const GemvArgs& a, uint32_t mb, co
 // Progress, as for k_qkv_attn: each XCD receives its workgroups in id order
 // and a workgroup waits only for workgroups of earlier stages (lower ids),
 // and the first stage waits for nothing; every wait is bounded.
-template <int FMT, int CPWD>
+template <int FMT, int CPWD, int MR>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_o_ffn(uint32_t n_mg, uint32_t n_o, uint32_t n_gu, const float* mS, const float* mUp, uint32_t s_stride,
              uint32_t cstride, uint32_t D, uint32_t hd, uint32_t ncap, const uint32_t* ep, const PassDesc* pd,
              GemvArgs o, GemvArgs gu, GemvArgs dn) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t b = blockIdx.x;
     if (b < n_mg) {
-        merge_cols_ll(o, b, mS, mUp, ep, pd, s_stride, cstride, D, hd, ncap);
+        const uint32_t nmr = (D + 511u) / 512u;   // merge workgroups per row (at most 4)
+        uint32_t row = 0, cb = b;
+        while (cb >= nmr) {   // at most 8 rows: no division on the merge's critical path
+            cb -= nmr;
+            row++;
+        }
+        merge_cols_ll(o, row, cb, mS, mUp, ep, pd, s_stride, cstride, D, hd, ncap);
     } else if (b < n_mg + n_o) {
-        gemv_body<FMT, PRO_QUANT, EPI_RESID, false, 1, 1, LL_IN | LL_OUT>(o, b - n_mg, n_o, smem, o.W, o.x, o.nw);
+        // several rows: O also stores the residual rows for the down launch
+        constexpr int LO = MR == 1 ? (LL_IN | LL_OUT) : (LL_IN | LL_OUT | LL_COPY);
+        gemv_body<FMT, PRO_QUANT, EPI_RESID, false, 1, MR, LO>(o, b - n_mg, n_o, smem, o.W, o.x, o.nw);
         prefetch_groups(o.nx, b, b - n_mg, n_o);
-    } else if (b < n_mg + n_o + n_gu) {
-        gemv_body<FMT, PRO_NORM, EPI_SWIGLU, false, 1, 1, LL_IN | LL_OUT>(gu, b - n_mg - n_o, n_gu, smem, gu.W, gu.x,
-                                                                          gu.nw);
+    } else if constexpr (MR == 1) {
+        if (b < n_mg + n_o + n_gu) {
+            gemv_body<FMT, PRO_NORM, EPI_SWIGLU, false, 1, 1, LL_IN | LL_OUT>(gu, b - n_mg - n_o, n_gu, smem, gu.W,
+                                                                              gu.x, gu.nw);
+        } else {
+            const uint32_t x = b - n_mg - n_o - n_gu;
+            gemv_body<FMT, PRO_QUANT, EPI_RESID, false, CPWD, 1, LL_IN | LL_OLD>(dn, x, dn.N / 32u, smem, dn.W, dn.x,
+                                                                                 dn.nw);
+        }
     } else {
-        const uint32_t x = b - n_mg - n_o - n_gu;
-        gemv_body<FMT, PRO_QUANT, EPI_RESID, false, CPWD, 1, LL_IN | LL_OLD>(dn, x, dn.N / 32u, smem, dn.W, dn.x, dn.nw);
+        // several rows: the gate|up workgroups write the SwiGLU rows and their
+        // row maxima to memory for a separate down launch (the down role's
+        // rows and weights together exceed the registers of two workgroups
+        // per CU)
+        gemv_body<FMT, PRO_NORM, EPI_SWIGLU, false, 1, MR, LL_IN>(gu, b - n_mg - n_o, n_gu, smem, gu.W, gu.x, gu.nw);
     }
 }
 

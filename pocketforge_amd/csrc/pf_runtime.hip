@@ -1381,9 +1381,9 @@ struct pf_engine {
     uint32_t* ll_err = nullptr;
     bool qkv_attn = true;
     // one launch for the O, gate|up and down products of one-row passes
-    // (k_o_ffn, pf_pass.hip): the residual row after O (D words), the
-    // SwiGLU row (F words) and the merged attention row (D words), as LL
-    // words.  PF_O_FFN=0 launches them separately.
+    // (k_o_ffn, pf_pass.hip): the residual rows after O [8][D], the SwiGLU
+    // rows [8][F] and the merged attention rows [8][D], as LL words.
+    // PF_O_FFN=0 launches them separately.
     unsigned long long* llt = nullptr;
     bool o_ffn = true;
 };
@@ -1489,11 +1489,11 @@ static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t ns
     if (!s) s = ealloc(e, &e->st, nseq);
     if (!s) s = ealloc(e, &e->ll, (size_t)MAX_PASS_ROWS * 3 * D);
     if (!s) s = ealloc(e, &e->ep, 2);
-    if (!s) s = ealloc(e, &e->llt, (size_t)2 * D + d.n_ff);
+    if (!s) s = ealloc(e, &e->llt, (size_t)MAX_PASS_ROWS * (2 * D + d.n_ff));
     if (s) { pf_engine_destroy(e); return s; }
     e->ll_err = e->ep + 1;
     PF_HIP(c, hipMemset(e->ll, 0, (size_t)MAX_PASS_ROWS * 3 * D * 8));
-    PF_HIP(c, hipMemset(e->llt, 0, ((size_t)2 * D + d.n_ff) * 8));
+    PF_HIP(c, hipMemset(e->llt, 0, (size_t)MAX_PASS_ROWS * (2 * D + d.n_ff) * 8));
     PF_HIP(c, hipMemset(e->ep, 0, 8));
     if (const char* v = std::getenv("PF_QKV_ATTN")) e->qkv_attn = !(v[0] == '0');
     if (const char* v = std::getenv("PF_O_FFN")) e->o_ffn = !(v[0] == '0');
@@ -1811,10 +1811,10 @@ static uint32_t merge_ncap(const pf_engine* e) {
     return e->m->d.n_heads * n <= 2048 ? n : 0u;
 }
 
-// k_o_ffn serves layer l of a one-row pass: three Q4 matrices, F a
-// multiple of 256 up to 6144 (at most three 256-column chunks per wave of
-// the down product, held in registers without spills), D <= 2048 (one
-// 256-column chunk per wave of the O and gate|up products), no layer skip.
+// k_o_ffn serves layer l of a decode pass of at most 8 rows: three Q4
+// matrices, F a multiple of 256 up to 6144 (at most three 256-column chunks
+// per wave of the down product), D <= 2048 (one 256-column chunk per wave
+// of the O and gate|up products), no layer skip.
 static bool o_ffn_ok(const pf_engine* e, uint32_t l) {
     const pf_model* m = e->m;
     const uint32_t F = m->d.n_ff;
@@ -1822,28 +1822,46 @@ static bool o_ffn_ok(const pf_engine* e, uint32_t l) {
            m->down[l]->fmt == FMT_Q4 && F % 256 == 0 && F <= 6144 && m->d.n_embd <= 2048;
 }
 
-template <int CPWD>
+template <int CPWD, int MR>
 static void o_ffn_one(hipStream_t st, const GemvArgs& ao, const GemvArgs& ag, const GemvArgs& ad, hipEvent_t ev0,
                       hipEvent_t ev1) {
-    const uint32_t n_mg = (ao.K + 511) / 512, n_o = ao.N / 32, n_gu = ag.N / 32, n_dn = ad.N / 32;
-    const uint32_t smem = o_ffn_smem(ao.K, ad.K);
+    const uint32_t n_mg = ao.M * ((ao.K + 511) / 512), n_o = ao.N / 32, n_gu = ag.N / 32;
+    const uint32_t n_dn = MR == 1 ? ad.N / 32 : 0u;
+    static bool attr = false;   // LDS beyond 64 KiB is granted per kernel
+    if (!attr) {
+        (void)hipFuncSetAttribute((const void*)k_o_ffn<FMT_Q4, CPWD, MR>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  o_ffn_smem(MR, 2048, 6144));
+        attr = true;
+    }
+    const uint32_t smem = o_ffn_smem(ao.M, ao.K, ad.K);
     const dim3 grid(n_mg + n_o + n_gu + n_dn);
     // the merge workgroups' inputs lead the argument list (preloaded into SGPRs)
     if (ev0)
-        hipExtLaunchKernelGGL((k_o_ffn<FMT_Q4, CPWD>), grid, dim3(512), smem, st, ev0, ev1, 0, n_mg, n_o, n_gu, ao.S,
-                              ao.Up, ao.s_stride, ao.cstride, ao.K, ao.e.hd, ao.ncap, ao.lli.ep, ao.e.pd, ao, ag, ad);
+        hipExtLaunchKernelGGL((k_o_ffn<FMT_Q4, CPWD, MR>), grid, dim3(512), smem, st, ev0, ev1, 0, n_mg, n_o, n_gu,
+                              ao.S, ao.Up, ao.s_stride, ao.cstride, ao.K, ao.e.hd, ao.ncap, ao.lli.ep, ao.e.pd, ao, ag,
+                              ad);
     else
-        hipLaunchKernelGGL((k_o_ffn<FMT_Q4, CPWD>), grid, dim3(512), smem, st, n_mg, n_o, n_gu, ao.S, ao.Up, ao.s_stride,
-                           ao.cstride, ao.K, ao.e.hd, ao.ncap, ao.lli.ep, ao.e.pd, ao, ag, ad);
+        hipLaunchKernelGGL((k_o_ffn<FMT_Q4, CPWD, MR>), grid, dim3(512), smem, st, n_mg, n_o, n_gu, ao.S, ao.Up,
+                           ao.s_stride, ao.cstride, ao.K, ao.e.hd, ao.ncap, ao.lli.ep, ao.e.pd, ao, ag, ad);
 }
 
+template <int MR>
+static void o_ffn_rows(hipStream_t st, const GemvArgs& ao, const GemvArgs& ag, const GemvArgs& ad, hipEvent_t ev0,
+                       hipEvent_t ev1) {
+    switch ((ad.K / 256 + GEMV_WAVES - 1) / GEMV_WAVES) {
+        case 1: o_ffn_one<1, MR>(st, ao, ag, ad, ev0, ev1); break;
+        case 2: o_ffn_one<2, MR>(st, ao, ag, ad, ev0, ev1); break;
+        default: o_ffn_one<3, MR>(st, ao, ag, ad, ev0, ev1); break;
+    }
+}
+
+// Rows held in registers: 1, 5 (verify passes of four heads), else 8.  With
+// more than one row the launch ends with gate|up (no down role).
 static void launch_o_ffn(hipStream_t st, const GemvArgs& ao, const GemvArgs& ag, const GemvArgs& ad, hipEvent_t ev0,
                          hipEvent_t ev1) {
-    switch ((ad.K / 256 + GEMV_WAVES - 1) / GEMV_WAVES) {
-        case 1: o_ffn_one<1>(st, ao, ag, ad, ev0, ev1); break;
-        case 2: o_ffn_one<2>(st, ao, ag, ad, ev0, ev1); break;
-        default: o_ffn_one<3>(st, ao, ag, ad, ev0, ev1); break;
-    }
+    if (ao.M == 1) o_ffn_rows<1>(st, ao, ag, ad, ev0, ev1);
+    else if (ao.M <= 5) o_ffn_one<1, 5>(st, ao, ag, ad, ev0, ev1);
+    else o_ffn_one<1, 8>(st, ao, ag, ad, ev0, ev1);
 }
 
 // One forward pass of M rows (the PassDesc at `pd` holds positions and
@@ -1928,10 +1946,10 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         // for the next product (O -> gate|up -> down -> next layer's QKV).
         // with k_o_ffn the O, gate|up and down workgroups follow the merge
         // workgroups in its grid, so their XCDs are offset by those before them
-        const bool tail = merge_in_o && o_ffn_ok(e, l);
-        const uint32_t n_mg = (D + 511) / 512, n_gu = m->gu[l]->rows / 32;
-        const Prefetch opf = merge_in_o ? prefetch_of(e, m->o[l], e->pf_blocks, tail ? n_mg : 0u)
-                                        : prefetch_of(e, nullptr, 0);
+        const bool tail = !tall && D <= 2048 && o_ffn_ok(e, l);
+        const uint32_t n_mg = M * ((D + 511) / 512), n_gu = m->gu[l]->rows / 32;
+        const Prefetch opf = tail ? prefetch_of(e, m->o[l], e->pf_blocks, n_mg)
+                                  : (merge_in_o ? prefetch_of(e, m->o[l], e->pf_blocks) : prefetch_of(e, nullptr, 0));
         if (qa) {
             a.W = m->qkv[l]->data;
             a.N = m->qkv[l]->rows;
@@ -1943,7 +1961,10 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
             a.e.fadd = l;
             AttnGroupArgs b{pd, g, e->kv, l, M, e->S, e->s_stride, e->Wp, e->cstride, opf,
                             LLIn{e->ll, e->ep, d.n_layers, l, e->ll_err}};
-            if (tail) {
+            // one-row passes: the gate|up and down weights too (with more rows
+            // the heavier attention is slowed more by those loads than
+            // k_o_ffn gains: 5 rows 18.9 -> 21.5 us against 24.3 -> 20.7 us)
+            if (tail && M == 1) {
                 b.pf2 = prefetch_of(e, m->gu[l], e->pf_blocks, n_mg + D / 32);
                 b.pf3 = prefetch_of(e, m->down[l], e->pf_blocks, n_mg + D / 32 + n_gu);
             }
@@ -1953,35 +1974,47 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
             launch_attn(st, hd, M, attn_tasks, pd, g, e->kv, l, e->q, e->k, e->v, e->S, e->s_stride, e->Wp,
                         e->cstride, opf, batch, batch ? e->batch_group : 0u, aev0, aev1);
         }
-        if (!merge_in_o)
+        if (!merge_in_o && !tail)
             PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_attn_merge_quant<PER>, dim3(M + e->pf_blocks), dim3(1024), 0, st,
                                                     pd, g, (const float*)e->S, e->s_stride, (const float*)e->Wp,
                                                     e->cstride, e->act, ks, as1, (int32_t*)nullptr, 0u, M,
                                                     prefetch_of(e, m->o[l], e->pf_blocks)));
-        // one-row passes without layer skip: O, gate|up and down in one launch
+        // decode passes without layer skip: the merge, O, gate|up and down in
+        // one launch; LL words in llt: residual rows [M][D], SwiGLU rows
+        // [M][F], merged attention rows [M][D]
         if (tail) {
             const LLIn li{nullptr, e->ep, d.n_layers, l, e->ll_err};
+            unsigned long long* const lx = e->llt;
+            unsigned long long* const lsg = e->llt + (size_t)M * D;
+            unsigned long long* const lmg = lsg + (size_t)M * F;
             GemvArgs ao{}, ag{}, ad{};
-            ao.W = m->o[l]->data; ao.N = D; ao.K = D; ao.M = 1;
+            ao.W = m->o[l]->data; ao.N = D; ao.K = D; ao.M = M;
             ao.xs = D;
             ao.S = e->S; ao.s_stride = e->s_stride; ao.Up = e->Wp; ao.cstride = e->cstride; ao.g = g;
             ao.ncap = e->cstride - 1;
             ao.e.pd = pd; ao.e.hd = hd; ao.e.D = D;
-            ao.e.y = e->x; ao.e.y_stride = D; ao.e.ll = e->llt;
+            ao.e.y = e->x; ao.e.y_stride = D; ao.e.ll = lx;
             ao.nx = prefetch_of(e, l + 1 < d.n_layers ? m->qkv[l + 1] : nullptr, e->l2_blocks ? D / 32 : 0u);
             ao.lli = li;
-            ao.lli.ll = e->llt + D + F;
-            ag.W = m->gu[l]->data; ag.N = m->gu[l]->rows; ag.K = D; ag.M = 1;
+            ao.lli.ll = lmg;
+            ag.W = m->gu[l]->data; ag.N = m->gu[l]->rows; ag.K = D; ag.M = M;
             ag.xs = D; ag.nw = fn;
-            ag.e.y_stride = F; ag.e.ll = e->llt + D;
+            ag.e.y_stride = F; ag.e.ll = lsg;
+            if (M > 1) {   // rows and maxima for the separate down launch
+                ag.e.y = e->sg;
+                ag.e.pmax = e->pmax;
+                ao.e.y2 = e->x;   // and the residual rows after O, which it adds to
+                // the O workgroups then load that launch's weights into L2
+                ao.nx = prefetch_of(e, m->down[l], e->l2_blocks ? D / 32 : 0u);
+            }
             ag.lli = li;
-            ag.lli.ll = e->llt;
-            ad.W = m->down[l]->data; ad.N = D; ad.K = F; ad.M = 1;
+            ag.lli.ll = lx;
+            ad.W = m->down[l]->data; ad.N = D; ad.K = F; ad.M = M;
             ad.xs = F;
-            ad.e.y = e->x; ad.e.y_stride = D; ad.e.llold = e->llt;
+            ad.e.y = e->x; ad.e.y_stride = D; ad.e.llold = lx;
             if (l + 1 == d.n_layers && hidden) ad.e.y2 = hidden;
             ad.lli = li;
-            ad.lli.ll = e->llt + D;
+            ad.lli.ll = lsg;
             hipEvent_t ev0 = nullptr, ev1 = nullptr;
             if (e->profile == 1 && e->in_verify && !e->capturing) {
                 if (e->kev_used == e->kev.size()) {
@@ -1994,52 +2027,54 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
                 // the three matrices, their fp32 input rows and outputs
                 double b = 0.0;
                 for (const pf_matrix* W : {m->o[l], m->gu[l], m->down[l]})
-                    b += (double)W->bytes + 4.0 * W->cols + 4.0 * W->rows;
+                    if (M == 1 || W != m->down[l]) b += (double)W->bytes + 4.0 * M * W->cols + 4.0 * M * W->rows;
                 e->kev_bytes[e->kev_used] = b;
                 ev0 = e->kev[e->kev_used].a;
                 ev1 = e->kev[e->kev_used].b;
                 e->kev_used++;
             }
             launch_o_ffn(st, ao, ag, ad, ev0, ev1);
-            continue;
-        }
-        // O projection + residual (src/engine.cpp:789-800)
-        a = GemvArgs{};
-        a.a8 = e->act; a.a8s = as1; a.xs = ks;
-        a.e.y = e->x; a.e.y_stride = D;
-        a.nx = prefetch_of(e, m->gu[l], e->l2_blocks);
-        if (merge_in_o) {
-            a.S = e->S; a.s_stride = e->s_stride; a.Up = e->Wp; a.cstride = e->cstride; a.g = g;
-            a.ncap = merge_ncap(e);
-            a.e.pd = pd; a.e.hd = hd; a.e.D = D;
-        }
-        if (pf_status s = pass_mm(e, m->o[l], merge_in_o ? MM_O_MERGE : MM_O, M, a, as1)) return s;
-        // FFN (src/engine.cpp:526-541, 805-854); with layer skip on, the
-        // normed rows are staged for the skip decisions and the products run
-        // only if some row needs them (gate word)
-        a = GemvArgs{};
-        a.e.y = e->sg; a.e.y_stride = F;
-        a.e.pmax = tall ? nullptr : e->pmax;
-        a.nx = prefetch_of(e, m->down[l], e->l2_blocks);
-        if (e->skip_on) {
-            float* nout = e->skip_stage + (size_t)l * e->rows * D;
-            PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_norm_rows<PER>, dim3(M), dim3(1024), 0, st, (const float*)e->x, D,
-                                                    fn, nout, e->skip_nrun + l));
-            hipLaunchKernelGGL(k_layer_skip, dim3(e->nseq), dim3(1024), 0, st, (const PassDesc*)pd, M,
-                               (const float*)nout, (const float*)e->skip_cache + (size_t)l * D,
-                               (size_t)d.n_layers * D, D, skip_threshold(e, l), e->skip_flags + (size_t)l * e->rows,
-                               e->skip_nrun + l);
-            a.x = nout; a.xs = D; a.gate = e->skip_nrun + l;
-            if (tall)
-                PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_quant_rows_wide<PER>, dim3(M), dim3(1024), 0, st,
-                                                        (const float*)nout, D, e->act, ks, as2, (int32_t*)nullptr, 0u));
-            if (pf_status s = pass_mm(e, m->gu[l], MM_GU_SKIP, M, a, as2)) return s;
+            if (M == 1) continue;
         } else {
-            a.x = e->x; a.xs = D; a.nw = fn;
-            if (tall)
-                PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_norm_quant<PER>, dim3(M), dim3(1024), 0, st,
-                                                        (const float*)e->x, D, fn, e->act, ks, as2));
-            if (pf_status s = pass_mm(e, m->gu[l], MM_GU, M, a, as2)) return s;
+            // O projection + residual (src/engine.cpp:789-800)
+            a = GemvArgs{};
+            a.a8 = e->act; a.a8s = as1; a.xs = ks;
+            a.e.y = e->x; a.e.y_stride = D;
+            a.nx = prefetch_of(e, m->gu[l], e->l2_blocks);
+            if (merge_in_o) {
+                a.S = e->S; a.s_stride = e->s_stride; a.Up = e->Wp; a.cstride = e->cstride; a.g = g;
+                a.ncap = merge_ncap(e);
+                a.e.pd = pd; a.e.hd = hd; a.e.D = D;
+            }
+            if (pf_status s = pass_mm(e, m->o[l], merge_in_o ? MM_O_MERGE : MM_O, M, a, as1)) return s;
+            // FFN (src/engine.cpp:526-541, 805-854); with layer skip on, the
+            // normed rows are staged for the skip decisions and the products run
+            // only if some row needs them (gate word)
+            a = GemvArgs{};
+            a.e.y = e->sg; a.e.y_stride = F;
+            a.e.pmax = tall ? nullptr : e->pmax;
+            a.nx = prefetch_of(e, m->down[l], e->l2_blocks);
+            if (e->skip_on) {
+                float* nout = e->skip_stage + (size_t)l * e->rows * D;
+                PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_norm_rows<PER>, dim3(M), dim3(1024), 0, st,
+                                                        (const float*)e->x, D, fn, nout, e->skip_nrun + l));
+                hipLaunchKernelGGL(k_layer_skip, dim3(e->nseq), dim3(1024), 0, st, (const PassDesc*)pd, M,
+                                   (const float*)nout, (const float*)e->skip_cache + (size_t)l * D,
+                                   (size_t)d.n_layers * D, D, skip_threshold(e, l), e->skip_flags + (size_t)l * e->rows,
+                                   e->skip_nrun + l);
+                a.x = nout; a.xs = D; a.gate = e->skip_nrun + l;
+                if (tall)
+                    PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_quant_rows_wide<PER>, dim3(M), dim3(1024), 0, st,
+                                                            (const float*)nout, D, e->act, ks, as2,
+                                                            (int32_t*)nullptr, 0u));
+                if (pf_status s = pass_mm(e, m->gu[l], MM_GU_SKIP, M, a, as2)) return s;
+            } else {
+                a.x = e->x; a.xs = D; a.nw = fn;
+                if (tall)
+                    PF_PER1024_SWITCH(D, hipLaunchKernelGGL(k_norm_quant<PER>, dim3(M), dim3(1024), 0, st,
+                                                            (const float*)e->x, D, fn, e->act, ks, as2));
+                if (pf_status s = pass_mm(e, m->gu[l], MM_GU, M, a, as2)) return s;
+            }
         }
         // down + residual; rows whose FFN was skipped take no residual
         a = GemvArgs{};
