@@ -1141,16 +1141,42 @@ __device__ __forceinline__ void attn_group_body(const PassDesc* __restrict__ pd,
 #pragma unroll
     for (int r = 0; r < NR; r++) acc[r] = 0.0f;
     if (t < nvis) {
+        // part p + 1's key words and query elements are read from LDS while
+        // part p's fmaf steps run (the order of the steps is unchanged)
         const float ksv = ksc[t];
+        int4 wn = kt[t];
+        float4 qn[NR][4];
+#pragma unroll
+        for (int r = 0; r < NR; r++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) qn[r][i] = *reinterpret_cast<const float4*>(&qs[r * 128 + 4 * i]);
 #pragma unroll
         for (int p = 0; p < PARTS; p++) {
-            const int4 w4 = kt[p * 256u + (t ^ (uint32_t)p)];
+            const int4 w4 = wn;
+            float qc[NR][16];
+#pragma unroll
+            for (int r = 0; r < NR; r++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    qc[r][4 * i] = qn[r][i].x;
+                    qc[r][4 * i + 1] = qn[r][i].y;
+                    qc[r][4 * i + 2] = qn[r][i].z;
+                    qc[r][4 * i + 3] = qn[r][i].w;
+                }
+            if (p + 1 < PARTS) {
+                wn = kt[(p + 1) * 256u + (t ^ (uint32_t)(p + 1))];
+#pragma unroll
+                for (int r = 0; r < NR; r++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        qn[r][i] = *reinterpret_cast<const float4*>(&qs[r * 128 + (p + 1) * 16 + 4 * i]);
+            }
             const int wv4[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
             for (int b = 0; b < 16; b++) {
                 const float kf = (float)(int8_t)((wv4[b >> 2] >> (8 * (b & 3))) & 0xFF) * ksv;
 #pragma unroll
-                for (int r = 0; r < NR; r++) acc[r] = __builtin_fmaf(qs[r * 128 + p * 16 + b], kf, acc[r]);
+                for (int r = 0; r < NR; r++) acc[r] = __builtin_fmaf(qc[r][b], kf, acc[r]);
             }
         }
     }
@@ -1200,22 +1226,42 @@ __device__ __forceinline__ void attn_group_body(const PassDesc* __restrict__ pd,
         // past nvis up to the next multiple of 8 have v_scale 0 and finite
         // codes, and entries past a row's list have weight 0
         const uint32_t e_end = min(64u * sub + 64u, (nvis + 7u) & ~7u);   // both multiples of 8
-#pragma unroll 2
-        for (uint32_t e = 64u * sub; e < e_end; e += 8) {
-            float a0[8];
-            const float4 s0 = *reinterpret_cast<const float4*>(&vsc[e]);
-            const float4 s1 = *reinterpret_cast<const float4*>(&vsc[e + 4]);
-            const float vv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        // the next group's scales, codes and weights are read from LDS while
+        // the current group's fmaf steps run (the order of the steps is
+        // unchanged; a group past e_end reads in-bounds slots it never uses)
+        float4 ns0, ns1, np0[NR], np1[NR];
+        int nb[8];
+        auto load_group = [&](uint32_t e) {
+            ns0 = *reinterpret_cast<const float4*>(&vsc[e]);
+            ns1 = *reinterpret_cast<const float4*>(&vsc[e + 4]);
 #pragma unroll
-            for (int u = 0; u < 8; u++) a0[u] = (float)vt[e + u][iv] * vv[u];
+            for (int u = 0; u < 8; u++) nb[u] = vt[e + u][iv];
 #pragma unroll
             for (int r = 0; r < NR; r++) {
-                const float4 p0 = *reinterpret_cast<const float4*>(&pe[r * 256 + e]);
-                const float4 p1 = *reinterpret_cast<const float4*>(&pe[r * 256 + e + 4]);
-                const float pp[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-#pragma unroll
-                for (int u = 0; u < 8; u++) w0[r] = __builtin_fmaf(pp[u], a0[u], w0[r]);
+                np0[r] = *reinterpret_cast<const float4*>(&pe[r * 256 + e]);
+                np1[r] = *reinterpret_cast<const float4*>(&pe[r * 256 + e + 4]);
             }
+        };
+        load_group(min(64u * sub, 248u));
+        for (uint32_t e = 64u * sub; e < e_end; e += 8) {
+            const float vv[8] = {ns0.x, ns0.y, ns0.z, ns0.w, ns1.x, ns1.y, ns1.z, ns1.w};
+            int cb[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) cb[u] = nb[u];
+            float pc[NR][8];
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                pc[r][0] = np0[r].x; pc[r][1] = np0[r].y; pc[r][2] = np0[r].z; pc[r][3] = np0[r].w;
+                pc[r][4] = np1[r].x; pc[r][5] = np1[r].y; pc[r][6] = np1[r].z; pc[r][7] = np1[r].w;
+            }
+            load_group(min(e + 8u, 248u));
+            float a0[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) a0[u] = (float)cb[u] * vv[u];
+#pragma unroll
+            for (int r = 0; r < NR; r++)
+#pragma unroll
+                for (int u = 0; u < 8; u++) w0[r] = __builtin_fmaf(pc[r][u], a0[u], w0[r]);
         }
 #pragma unroll
         for (int r = 0; r < NR; r++) {
