@@ -1286,14 +1286,23 @@ __device__ __forceinline__ void attn_group_body(const PassDesc* __restrict__ pd,
         u = u + wp[(r * 4 + 1) * 128 + d];
         u = u + wp[(r * 4 + 2) * 128 + d];
         u = u + wp[(r * 4 + 3) * 128 + d];
-        Up[(mh * cstride + c) * hd + d] = u;
+        if (LL && lli.out) ll_store(lli.out + lli.sreg + (mh * cstride + c) * hd + d, u, epoch * lli.fmul + lli.fadd);
+        else Up[(mh * cstride + c) * hd + d] = u;
     }
     if (t < G && j0 <= C0 + t) {
         const float* mm = rmx + t * 4;
         const float* ss = rsm + t * 4;
         const size_t mh = (size_t)(mb + t) * H + h;
-        S[mh * s_stride + 2 * c] = fmaxf(fmaxf(mm[0], mm[1]), fmaxf(mm[2], mm[3]));
-        S[mh * s_stride + 2 * c + 1] = (ss[0] + ss[2]) + (ss[1] + ss[3]);   // CANON(4) over the wave totals
+        const float smx = fmaxf(fmaxf(mm[0], mm[1]), fmaxf(mm[2], mm[3]));
+        const float ssm = (ss[0] + ss[2]) + (ss[1] + ss[3]);   // CANON(4) over the wave totals
+        if (LL && lli.out) {
+            const uint32_t flag = epoch * lli.fmul + lli.fadd;
+            ll_store(lli.out + mh * s_stride + 2 * c, smx, flag);
+            ll_store(lli.out + mh * s_stride + 2 * c + 1, ssm, flag);
+        } else {
+            S[mh * s_stride + 2 * c] = smx;
+            S[mh * s_stride + 2 * c + 1] = ssm;
+        }
     }
 }
 

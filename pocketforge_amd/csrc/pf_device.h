@@ -348,6 +348,15 @@ struct LLIn {
     // polls it alone (one request per round) before it polls its own words,
     // which keeps the memory traffic of long waits small
     uint32_t sent;
+    // attention blocks with out set write their chunk results as LL words:
+    // S pairs at out[(row H + h) s_stride + 2 c ..], U at
+    // out[sreg + ((row H + h) cstride + c) hd + d]
+    unsigned long long* out;
+    uint32_t sreg;
+    // LL_GATE (GEMV): the word gate[gate_off] a workgroup waits for before its
+    // weight loads
+    const unsigned long long* gate;
+    uint32_t gate_off;
 };
 constexpr uint32_t LL_SPIN_MAX = 1u << 20;
 

@@ -38,7 +38,9 @@ enum Epi : int { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_SWIGLU = 3 };
 //   LL_OLD: the RESID epilogue's old values are LL words, e.llold[m y_stride + n]
 //   LL_OUT: the RESID / SWIGLU epilogue writes LL words to e.ll instead of e.y
 //   LL_COPY: with LL_OUT, RESID also stores the rows to e.y2 (for a later launch)
-enum LLMode : int { LL_IN = 1, LL_OLD = 2, LL_OUT = 4, LL_COPY = 8 };
+//   LL_GATE: the weight loads wait for the word lli.gate[lli.gate_off], so that
+//            they start after an earlier stage's own loads
+enum LLMode : int { LL_IN = 1, LL_OLD = 2, LL_OUT = 4, LL_COPY = 8, LL_GATE = 16 };
 
 // Consumer step applied to the outputs.  Row n is a device row (pf_layout.h).
 struct MmEpi {
@@ -361,7 +363,12 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
         }
     }
 
-    // ---- weight loads
+    // ---- weight loads (after the gate word, with LL_GATE)
+    if constexpr ((LLM & LL_GATE) != 0) {
+        const uint32_t go[1] = {a.lli.gate_off};
+        float gv[1];
+        ll_wait<1>(a.lli.gate, go, gv, llflag, a.lli.err);
+    }
     const uint32_t nch = K >> 8, c0 = nch * wid / GEMV_WAVES, c1 = nch * (wid + 1) / GEMV_WAVES;
     const uint8_t* tiles = Wm + (size_t)bx * nch * TB;
     uint4 cw[CPW][SETS], sw[CPW];

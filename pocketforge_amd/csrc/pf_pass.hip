@@ -218,4 +218,106 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     }
 }
 
+// The chunk merge of a one-row pass from the attention blocks of the same
+// launch (k_layer): their chunk results are LL words at ain (S pairs, then U
+// from ain + sreg), the arithmetic that of merge_cols_ll.  Lane L of a wave
+// (the wave's 64 columns lie in one head) waits for chunk L's maximum and sum
+// and its column's U of the first UC chunks in one round of polls; the
+// maximum over the chunk maxima is a wave reduction (exact in any order) and
+// the T and U chains take chunk c's f_c and sum from lane c in order.  At
+// most 64 chunks.  Written to a.lli.ll like merge_cols_ll's row.
+__device__ __forceinline__ void merge_cols_poll(const GemvArgs& a, uint32_t cb, const unsigned long long* ain,
+                                                uint32_t sreg, uint32_t s_stride, uint32_t cstride, uint32_t D,
+                                                uint32_t hd, const uint32_t* ep, const PassDesc* pd) {
+    constexpr uint32_t UC = 16;
+    const uint32_t lane = threadIdx.x & 63u, hs = (uint32_t)__builtin_ctz(hd);
+    const uint32_t j0 = 512u * cb + threadIdx.x, j = min(j0, D - 1u), h = j >> hs, e = j & (hd - 1u);
+    const uint32_t flag = ll_epoch(ep) * a.lli.fmul + a.lli.fadd;
+    const uint32_t nc = (kv_view(a.g, row_pos(pass_head_late(pd), 0)).count() + 1u + 255u) / 256u;
+    uint32_t off[2 + UC];
+    float v[2 + UC];
+    const uint32_t cl = min(lane, nc - 1u);
+    off[0] = h * s_stride + 2u * cl;
+    off[1] = off[0] + 1u;
+#pragma unroll
+    for (uint32_t k = 0; k < UC; k++) off[2 + k] = sreg + (h * cstride + min(k, nc - 1u)) * hd + e;
+    ll_wait<2 + UC>(ain, off, v, flag, a.lli.err);
+    const float mx = wave_max(lane < nc ? v[0] : -__builtin_inff());
+    const int fL = __float_as_int(expf_c(v[0] - mx)), tL = __float_as_int(v[1]);
+    float uc[UC];
+#pragma unroll
+    for (uint32_t k = 0; k < UC; k++) uc[k] = v[2 + k];
+    float T = 0.0f, U = 0.0f;
+    for (uint32_t c0 = 0; c0 < nc; c0 += UC) {
+        if (c0) {   // lists of more than UC chunks: the next UC chunks' U
+            uint32_t o2[UC];
+#pragma unroll
+            for (uint32_t k = 0; k < UC; k++) o2[k] = sreg + (h * cstride + min(c0 + k, nc - 1u)) * hd + e;
+            ll_wait<UC>(ain, o2, uc, flag, a.lli.err);
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < UC; k++) {
+            if (c0 + k < nc) {
+                const float fc = __int_as_float(__builtin_amdgcn_readlane(fL, c0 + k));
+                const float tc = __int_as_float(__builtin_amdgcn_readlane(tL, c0 + k));
+                T = __builtin_fmaf(tc, fc, T);
+                U = __builtin_fmaf(uc[k], fc, U);
+            }
+        }
+    }
+    if (j0 < D) ll_store(const_cast<unsigned long long*>(a.lli.ll) + j0, U * (1.0f / (T + 1e-10f)), flag);
+}
+
+// One launch for a whole layer of a one-row pass: workgroups [0, nq) are
+// k_qkv_attn's QKV GEMV, the next `tasks` its attention blocks (their chunk
+// results as LL words at b.lli.out), then k_o_ffn's roles for one row with
+// the merge reading those words (merge_cols_poll): n_mg merge, n_o O, n_gu
+// gate|up, the rest down.  The O, gate|up and down workgroups wait for the
+// QKV product's last word (LL_GATE) before their weight loads, so that those
+// run beside the attention's arithmetic rather than its K/V loads.  At most
+// 64 chunks per list.  Progress as for k_qkv_attn and k_o_ffn: every wait is
+// for workgroups of lower ids, and bounded.
+template <int FMT, int PARTS, int CPWD>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_layer(
+    uint32_t nq, uint32_t tasks, uint32_t n_mg, uint32_t n_o, uint32_t n_gu, const PassDesc* pd, const uint8_t* W,
+    const float* xr, const float* nw, GemvArgs a, AttnGroupArgs b, GemvArgs o, GemvArgs gu, GemvArgs dn) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t bid = blockIdx.x;
+    if (bid < nq) {
+        gemv_body<FMT, PRO_NORM, EPI_QKV, false, 1, 1>(a, bid, nq, smem, W, xr, nw);
+        return;
+    }
+    uint32_t x = bid - nq;
+    if (x < tasks) {
+        attn_group_body<PARTS, true, 1, true>(pd, b.g, b.kv, b.layer, b.M, nullptr, nullptr, nullptr, b.S,
+                                              b.s_stride, b.Up, b.cstride, b.pf, b.lli, x, 0, bid, tasks, smem);
+        return;
+    }
+    x -= tasks;
+    if (x < n_mg) {
+        merge_cols_poll(o, x, b.lli.out, b.lli.sreg, b.s_stride, b.cstride, o.K, o.e.hd, o.lli.ep, pd);
+        return;
+    }
+    x -= n_mg;
+    if (x < n_o) {
+        gemv_body<FMT, PRO_QUANT, EPI_RESID, false, 1, 1, LL_IN | LL_OUT | LL_GATE>(o, x, n_o, smem, o.W, o.x, o.nw);
+        prefetch_groups(o.nx, bid, x, n_o);
+        return;
+    }
+    x -= n_o;
+    if (x < n_gu) {
+        gemv_body<FMT, PRO_NORM, EPI_SWIGLU, false, 1, 1, LL_IN | LL_OUT | LL_GATE>(gu, x, n_gu, smem, gu.W, gu.x,
+                                                                                    gu.nw);
+        return;
+    }
+    x -= n_gu;
+    gemv_body<FMT, PRO_QUANT, EPI_RESID, false, CPWD, 1, LL_IN | LL_OLD | LL_GATE>(dn, x, dn.N / 32u, smem, dn.W,
+                                                                                   dn.x, dn.nw);
+}
+
+// LDS of k_layer: the attention blocks' need is the largest.
+__host__ __device__ constexpr uint32_t layer_smem(uint32_t D, uint32_t F) {
+    return qkv_attn_smem(1, D, 1) > o_ffn_smem(1, D, F) ? qkv_attn_smem(1, D, 1) : o_ffn_smem(1, D, F);
+}
+
 }  // namespace pf

@@ -1386,6 +1386,11 @@ struct pf_engine {
     // PF_O_FFN=0 launches them separately.
     unsigned long long* llt = nullptr;
     bool o_ffn = true;
+    // one launch per layer of a one-row pass (k_layer, pf_pass.hip): the
+    // attention's chunk results as LL words (one row: S pairs [H][s_stride],
+    // then U [H][cstride][hd]).  PF_LAYER=0 keeps the two launches.
+    unsigned long long* lla = nullptr;
+    bool layer_fuse = true;
 };
 
 template <class T>
@@ -1490,13 +1495,16 @@ static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t ns
     if (!s) s = ealloc(e, &e->ll, (size_t)MAX_PASS_ROWS * 3 * D);
     if (!s) s = ealloc(e, &e->ep, 2);
     if (!s) s = ealloc(e, &e->llt, (size_t)MAX_PASS_ROWS * (2 * D + d.n_ff));
+    if (!s) s = ealloc(e, &e->lla, (size_t)d.n_heads * (e->s_stride + (size_t)e->cstride * d.head_dim));
     if (s) { pf_engine_destroy(e); return s; }
     e->ll_err = e->ep + 1;
     PF_HIP(c, hipMemset(e->ll, 0, (size_t)MAX_PASS_ROWS * 3 * D * 8));
     PF_HIP(c, hipMemset(e->llt, 0, (size_t)MAX_PASS_ROWS * (2 * D + d.n_ff) * 8));
+    PF_HIP(c, hipMemset(e->lla, 0, (size_t)d.n_heads * (e->s_stride + (size_t)e->cstride * d.head_dim) * 8));
     PF_HIP(c, hipMemset(e->ep, 0, 8));
     if (const char* v = std::getenv("PF_QKV_ATTN")) e->qkv_attn = !(v[0] == '0');
     if (const char* v = std::getenv("PF_O_FFN")) e->o_ffn = !(v[0] == '0');
+    if (const char* v = std::getenv("PF_LAYER")) e->layer_fuse = !(v[0] == '0');
     if (hipHostMalloc((void**)&e->word, 64, hipHostMallocDefault) != hipSuccess) {
         pf_engine_destroy(e);
         return fail(c, PF_ERR_HIP, "hipHostMalloc failed");
@@ -1864,6 +1872,42 @@ static void launch_o_ffn(hipStream_t st, const GemvArgs& ao, const GemvArgs& ag,
     else o_ffn_one<1, 8>(st, ao, ag, ad, ev0, ev1);
 }
 
+template <int P, int CPWD>
+static void layer_one(hipStream_t st, const GemvArgs& a, const AttnGroupArgs& b, const GemvArgs& ao,
+                      const GemvArgs& ag, const GemvArgs& ad, uint32_t tasks, hipEvent_t ev0, hipEvent_t ev1) {
+    static bool attr = false;   // LDS beyond 64 KiB is granted per kernel
+    if (!attr) {
+        (void)hipFuncSetAttribute((const void*)k_layer<FMT_Q4, P, CPWD>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  layer_smem(2048, 6144));
+        attr = true;
+    }
+    const uint32_t nq = a.N / 32, n_mg = (ao.K + 511) / 512, n_o = ao.N / 32, n_gu = ag.N / 32, n_dn = ad.N / 32;
+    const uint32_t smem = layer_smem(ao.K, ad.K);
+    const dim3 grid(nq + tasks + n_mg + n_o + n_gu + n_dn);
+    if (ev0)
+        hipExtLaunchKernelGGL((k_layer<FMT_Q4, P, CPWD>), grid, dim3(512), smem, st, ev0, ev1, 0, nq, tasks, n_mg, n_o,
+                              n_gu, b.pd, a.W, a.x, a.nw, a, b, ao, ag, ad);
+    else
+        hipLaunchKernelGGL((k_layer<FMT_Q4, P, CPWD>), grid, dim3(512), smem, st, nq, tasks, n_mg, n_o, n_gu, b.pd,
+                           a.W, a.x, a.nw, a, b, ao, ag, ad);
+}
+
+template <int P>
+static void layer_cpw(hipStream_t st, const GemvArgs& a, const AttnGroupArgs& b, const GemvArgs& ao,
+                      const GemvArgs& ag, const GemvArgs& ad, uint32_t tasks, hipEvent_t ev0, hipEvent_t ev1) {
+    switch ((ad.K / 256 + GEMV_WAVES - 1) / GEMV_WAVES) {
+        case 1: layer_one<P, 1>(st, a, b, ao, ag, ad, tasks, ev0, ev1); break;
+        case 2: layer_one<P, 2>(st, a, b, ao, ag, ad, tasks, ev0, ev1); break;
+        default: layer_one<P, 3>(st, a, b, ao, ag, ad, tasks, ev0, ev1); break;
+    }
+}
+
+static void launch_layer(hipStream_t st, uint32_t hd, const GemvArgs& a, const AttnGroupArgs& b, const GemvArgs& ao,
+                         const GemvArgs& ag, const GemvArgs& ad, uint32_t tasks, hipEvent_t ev0, hipEvent_t ev1) {
+    if (hd == 64) layer_cpw<4>(st, a, b, ao, ag, ad, tasks, ev0, ev1);
+    else layer_cpw<8>(st, a, b, ao, ag, ad, tasks, ev0, ev1);
+}
+
 // One forward pass of M rows (the PassDesc at `pd` holds positions and
 // tokens; pos0 is the host's copy of the first position).  hidden/logits
 // outputs are device [M][D] / [M][V]; either may be null.  A batched pass
@@ -1922,6 +1966,67 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         // launch (its attention blocks load the cached K/V rows while the
         // product runs)
         const bool qa = e->qkv_attn && !tall && attn_fused(M) && m->qkv[l]->fmt == FMT_Q4 && (hd == 64 || hd == 128);
+        // one-row passes: the whole layer in one launch (k_layer)
+        if (M == 1 && qa && e->layer_fuse && D <= 2048 && o_ffn_ok(e, l) && e->cstride - 1 <= 64) {
+            const LLIn li{nullptr, e->ep, d.n_layers, l, e->ll_err};
+            a.W = m->qkv[l]->data;
+            a.N = m->qkv[l]->rows;
+            a.K = m->qkv[l]->cols;
+            a.M = 1;
+            a.e.ll = e->ll;
+            a.e.ep = e->ep;
+            a.e.fmul = d.n_layers;
+            a.e.fadd = l;
+            AttnGroupArgs b{pd, g, e->kv, l, 1, e->S, e->s_stride, e->Wp, e->cstride, prefetch_of(e, nullptr, 0),
+                            LLIn{e->ll, e->ep, d.n_layers, l, e->ll_err}};
+            b.lli.out = e->lla;
+            b.lli.sreg = H * e->s_stride;
+            unsigned long long* const lx = e->llt;
+            unsigned long long* const lsg = e->llt + D;
+            unsigned long long* const lmg = lsg + F;
+            GemvArgs ao{}, ag{}, ad{};
+            ao.W = m->o[l]->data; ao.N = D; ao.K = D; ao.M = 1; ao.xs = D; ao.g = g;
+            ao.e.pd = pd; ao.e.hd = hd; ao.e.D = D;
+            ao.e.y = e->x; ao.e.y_stride = D; ao.e.ll = lx;
+            ao.nx = prefetch_of(e, l + 1 < d.n_layers ? m->qkv[l + 1] : nullptr, e->l2_blocks ? D / 32 : 0u);
+            ao.lli = li;
+            ao.lli.ll = lmg;
+            ag.W = m->gu[l]->data; ag.N = m->gu[l]->rows; ag.K = D; ag.M = 1; ag.xs = D; ag.nw = fn;
+            ag.e.y_stride = F; ag.e.ll = lsg;
+            ag.lli = li;
+            ag.lli.ll = lx;
+            ad.W = m->down[l]->data; ad.N = D; ad.K = F; ad.M = 1; ad.xs = F;
+            ad.e.y = e->x; ad.e.y_stride = D; ad.e.llold = lx;
+            if (l + 1 == d.n_layers && hidden) ad.e.y2 = hidden;
+            ad.lli = li;
+            ad.lli.ll = lsg;
+            for (GemvArgs* x : {&ao, &ag, &ad}) {   // weight loads after the QKV product's last word
+                x->lli.gate = e->ll;
+                x->lli.gate_off = 3 * D - 1;
+            }
+            hipEvent_t ev0 = nullptr, ev1 = nullptr;
+            if (e->profile == 1 && e->in_verify && !e->capturing) {
+                if (e->kev_used == e->kev.size()) {
+                    TimedPass n{};
+                    PF_HIP(c, hipEventCreate(&n.a));
+                    PF_HIP(c, hipEventCreate(&n.b));
+                    e->kev.push_back(n);
+                    e->kev_bytes.push_back(0.0);
+                }
+                // the four matrices with their fp32 input and output rows, and
+                // the visible K/V rows with their scales
+                double bytes = 0.0;
+                for (const pf_matrix* W : {m->qkv[l], m->o[l], m->gu[l], m->down[l]})
+                    bytes += (double)W->bytes + 4.0 * W->cols + 4.0 * W->rows;
+                bytes += 2.0 * H * (hd + 4.0) * kv_view(g, pos_last).count();
+                e->kev_bytes[e->kev_used] = bytes;
+                ev0 = e->kev[e->kev_used].a;
+                ev1 = e->kev[e->kev_used].b;
+                e->kev_used++;
+            }
+            launch_layer(st, hd, a, b, ao, ag, ad, attn_tasks, ev0, ev1);
+            continue;
+        }
         if (!qa)
             if (pf_status s = pass_mm(e, m->qkv[l], MM_QKV, M, a, as0)) return s;
         if (!attn_fused(M))
