@@ -1051,14 +1051,15 @@ __device__ __forceinline__ void attn_group_body(const PassDesc* __restrict__ pd,
             wa[3 * QPT + 4 * u + 2] = use ? b + D : LL_NONE;
             wa[3 * QPT + 4 * u + 3] = use ? b + D + 1u : LL_NONE;
         }
-        // each wave first waits for one word of the head's v rows (every
-        // lane loads the same word: one request per round), so that the
-        // block does not keep the memory system busy with all its words'
-        // polls, then for its own words
+        // wave 0 first waits for one word of the head's v rows (every lane
+        // loads the same word: one request per round) while the other waves
+        // wait at a barrier, so that the block does not keep the memory
+        // system busy with its polls; then each wave waits for its own words
         const uint32_t flag = epoch * lli.fmul + lli.fadd;
         const uint32_t sp[1] = {mb * rs3 + 2u * D + h * hd + hd - 1u};
         float sv_[1];
-        ll_wait<1>(lli.ll, sp, sv_, flag, lli.err);
+        if (wid == 0) ll_wait<1>(lli.ll, sp, sv_, flag, lli.err);
+        __syncthreads();
         ll_wait<NW>(lli.ll, wa, wv_, flag, lli.err);
 #pragma unroll
         for (uint32_t k = 0; k < QPT; k++) {

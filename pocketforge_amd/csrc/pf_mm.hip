@@ -40,7 +40,9 @@ enum Epi : int { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_SWIGLU = 3 };
 //   LL_COPY: with LL_OUT, RESID also stores the rows to e.y2 (for a later launch)
 //   LL_GATE: the weight loads wait for the word lli.gate[lli.gate_off], so that
 //            they start after an earlier stage's own loads
-enum LLMode : int { LL_IN = 1, LL_OLD = 2, LL_OUT = 4, LL_COPY = 8, LL_GATE = 16 };
+//   LL_NEXT: with LL_OUT, the words carry the next layer's flag (the residual
+//            rows a layer hands to the next one in a launch of several layers)
+enum LLMode : int { LL_IN = 1, LL_OLD = 2, LL_OUT = 4, LL_COPY = 8, LL_GATE = 16, LL_NEXT = 32 };
 
 // Consumer step applied to the outputs.  Row n is a device row (pf_layout.h).
 struct MmEpi {
@@ -78,8 +80,8 @@ struct EpiPre { float a, b; uint32_t f; };
 
 template <int EPI, int LLM = 0>
 __device__ __forceinline__ EpiPre epi_prefetch(const MmEpi& e, uint32_t m, uint32_t n, uint32_t flag = 0u,
-                                               uint32_t* err = nullptr) {
-    EpiPre p{0.0f, 0.0f, flag};
+                                               uint32_t* err = nullptr, uint32_t lay = 0u) {
+    EpiPre p{0.0f, 0.0f, (LLM & LL_NEXT) ? flag + 1u : flag};
     if constexpr (EPI == EPI_RESID && (LLM & LL_OLD)) {
         const uint32_t off[1] = {m * e.y_stride + n};
         float v[1];
@@ -96,7 +98,7 @@ __device__ __forceinline__ EpiPre epi_prefetch(const MmEpi& e, uint32_t m, uint3
             p.a = e.rc[(size_t)pos * half + t];
             p.b = e.rs[(size_t)pos * half + t];
         }
-        if (e.ll) p.f = ll_epoch(e.ep) * e.fmul + e.fadd;
+        if (e.ll) p.f = ll_epoch(e.ep) * e.fmul + e.fadd + lay;
     }
     return p;
 }
@@ -258,12 +260,14 @@ __device__ __forceinline__ float max4abs(float4 v) {
 // weights, input rows and norm weights come as parameters (a kernel may
 // pass them as preloaded arguments), the rest from a.
 // With LL_IN the prologue's input words are waited for after the weight
-// loads have been issued, so the weights stream in during the wait.
+// loads have been issued, so the weights stream in during the wait.  `lay`
+// adds to every flag (the layer of a launch of several layers).
 template <int FMT, int PRO, int EPI, bool GATED, int CPW, int MR, int LLM = 0>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32_t gx, uint8_t* smem,
                                           const uint8_t* __restrict__ Wm, const float* __restrict__ xin,
-                                          const float* __restrict__ nwv) {
+                                          const float* __restrict__ nwv, uint32_t lay = 0u) {
     static_assert(!(LLM & LL_IN) || PRO == PRO_NORM || PRO == PRO_QUANT, "LL input rows: NORM or QUANT prologue");
+    static_assert(!(LLM & LL_OLD) || (LLM & LL_IN), "LL old values come with LL input rows");
     constexpr uint32_t TB = g32_tile_bytes(FMT), CODES = g32_code_bytes(FMT);
     constexpr int SETS = sets_of<FMT>();
     constexpr uint32_t NT = 64u * GEMV_WAVES;
@@ -284,7 +288,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
     const uint32_t t = threadIdx.x, lane = t & 63u, r = lane & 31u, h = lane >> 5;
     const uint32_t wid = __builtin_amdgcn_readfirstlane(t >> 6);
     const float* __restrict__ xg = xin;
-    const uint32_t llflag = LLM ? ll_epoch(a.lli.ep) * a.lli.fmul + a.lli.fadd : 0u;
+    const uint32_t llflag = LLM ? ll_epoch(a.lli.ep) * a.lli.fmul + a.lli.fadd + lay : 0u;
 
     // ---- prologue loads
     const uint32_t li = lane & 15u, q = lane >> 4, T = wid + GEMV_WAVES * q;   // NORM tile of this lane
@@ -363,11 +367,14 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
         }
     }
 
-    // ---- weight loads (after the gate word, with LL_GATE)
+    // ---- weight loads (after the gate word, with LL_GATE: wave 0 polls it
+    // and the others wait at a barrier, so that a workgroup keeps one poll
+    // in flight rather than eight)
     if constexpr ((LLM & LL_GATE) != 0) {
         const uint32_t go[1] = {a.lli.gate_off};
         float gv[1];
-        ll_wait<1>(a.lli.gate, go, gv, llflag, a.lli.err);
+        if (wid == 0) ll_wait<1>(a.lli.gate, go, gv, llflag, a.lli.err);
+        __syncthreads();
     }
     const uint32_t nch = K >> 8, c0 = nch * wid / GEMV_WAVES, c1 = nch * (wid + 1) / GEMV_WAVES;
     const uint8_t* tiles = Wm + (size_t)bx * nch * TB;
@@ -379,14 +386,26 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
         for (int s = 0; s < SETS; s++) cw[j][s] = *reinterpret_cast<const uint4*>(tile + s * 1024 + lane * 16);
         sw[j] = *reinterpret_cast<const uint4*>(tile + CODES + r * 16);
     }
+    // ---- epilogue operands from memory (thread t outputs row om of device
+    // row on), issued before the LL input wait so that their latency overlaps
+    // it; an LL old value is loaded beside the input words (below)
+    const uint32_t om = t >> 5, on = 32u * bx + (t & 31u);
+    EpiPre pre{};
+    if constexpr (!(LLM & LL_OLD)) pre = epi_prefetch<EPI, LLM>(a.e, min(om, mlast), on, llflag, a.lli.err, lay);
     // ---- LL input rows, after the weight loads: the sentinel word first
-    // (every lane of a wave loads the same word, one request), then the
-    // thread's own words row by row (rows past M repeat row M - 1)
+    // (wave 0 polls it, one request per round, while the others wait at a
+    // barrier), then the
+    // thread's own words row by row (rows past M repeat row M - 1); the old
+    // value's word (LL_OLD, written by an earlier stage than the input's) is
+    // loaded with them and waited for only if its flag is not yet there
+    unsigned long long wold = 0;
     if constexpr ((LLM & LL_IN) != 0) {
         const uint32_t so[1] = {a.lli.sent};
         float sv[1];
-        ll_wait<1>(a.lli.ll, so, sv, llflag, a.lli.err);
+        if (wid == 0) ll_wait<1>(a.lli.ll, so, sv, llflag, a.lli.err);
+        __syncthreads();
     }
+    if constexpr ((LLM & LL_OLD) != 0) wold = ll_load(a.e.llold + (size_t)min(om, mlast) * a.e.y_stride + on);
     if constexpr ((LLM & LL_IN) && PRO == PRO_NORM) {
         const uint32_t col = 64u * min(T, nt - 1u) + li;
 #pragma unroll
@@ -415,9 +434,14 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
             for (int k = 0; k < CPW; k++) hv[m][k] = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
         }
     }
-    // ---- epilogue operands: thread t outputs row om of device row on
-    const uint32_t om = t >> 5, on = 32u * bx + (t & 31u);
-    const EpiPre pre = epi_prefetch<EPI, LLM>(a.e, min(om, mlast), on, llflag, a.lli.err);
+    if constexpr ((LLM & LL_OLD) != 0) {
+        if ((uint32_t)(wold >> 32) == llflag) {
+            pre.a = __uint_as_float((uint32_t)wold);
+            pre.f = (LLM & LL_NEXT) ? llflag + 1u : llflag;
+        } else {
+            pre = epi_prefetch<EPI, LLM>(a.e, min(om, mlast), on, llflag, a.lli.err, lay);
+        }
+    }
 
     // ---- prologue arithmetic
     if constexpr (PRO == PRO_MERGE) {

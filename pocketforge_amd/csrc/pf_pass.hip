@@ -228,11 +228,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 // most 64 chunks.  Written to a.lli.ll like merge_cols_ll's row.
 __device__ __forceinline__ void merge_cols_poll(const GemvArgs& a, uint32_t cb, const unsigned long long* ain,
                                                 uint32_t sreg, uint32_t s_stride, uint32_t cstride, uint32_t D,
-                                                uint32_t hd, const uint32_t* ep, const PassDesc* pd) {
+                                                uint32_t hd, const uint32_t* ep, const PassDesc* pd,
+                                                uint32_t lay = 0u) {
     constexpr uint32_t UC = 16;
     const uint32_t lane = threadIdx.x & 63u, hs = (uint32_t)__builtin_ctz(hd);
     const uint32_t j0 = 512u * cb + threadIdx.x, j = min(j0, D - 1u), h = j >> hs, e = j & (hd - 1u);
-    const uint32_t flag = ll_epoch(ep) * a.lli.fmul + a.lli.fadd;
+    const uint32_t flag = ll_epoch(ep) * a.lli.fmul + a.lli.fadd + lay;
     const uint32_t nc = (kv_view(a.g, row_pos(pass_head_late(pd), 0)).count() + 1u + 255u) / 256u;
     uint32_t off[2 + UC];
     float v[2 + UC];
@@ -315,7 +316,76 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
                                                                                    dn.x, dn.nw);
 }
 
-// LDS of k_layer: the attention blocks' need is the largest.
+// Per-layer operands of k_stack.
+struct StackLayer {
+    const uint8_t *qkv, *o, *gu, *dn;   // packed matrices
+    const float *an, *fn;               // attention and FFN norm weights [D]
+};
+
+// Every layer of a one-row pass in one launch: layer l's workgroups are
+// [l G, (l + 1) G), laid out as k_layer's (QKV, attention, merge, O,
+// gate|up, down).  Layer l's down product hands the updated residual row to
+// layer l + 1 as LL words (dn.e.ll, flagged for layer l + 1): its QKV
+// workgroups read them as the prologue's input and its O workgroups as the
+// residual; layer 0 reads the embedded row a.x / o.e.y from memory and the
+// last layer's down writes dn.e.y (and dn.e.y2) to memory.  A layer's
+// workgroups start while the layer before runs, so their weight loads (and
+// the attention's cached K/V loads) overlap its arithmetic.  Flags are
+// epoch * layers + layer (the args carry fadd = 0; each role adds its layer).
+// Progress as for k_layer: every wait is for workgroups of lower ids (the
+// layer before, or earlier roles of the layer), and bounded.
+template <int FMT, int PARTS, int CPWD>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_stack(
+    uint32_t nq, uint32_t tasks, uint32_t n_mg, uint32_t n_o, uint32_t n_gu, uint32_t G, const PassDesc* pd,
+    const StackLayer* lw, GemvArgs a, AttnGroupArgs b, GemvArgs o, GemvArgs gu, GemvArgs dn) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t bid = blockIdx.x, l = bid / G;
+    uint32_t x = bid - l * G;
+    const StackLayer& w = lw[l];
+    if (x < nq) {
+        if (l == 0) gemv_body<FMT, PRO_NORM, EPI_QKV, false, 1, 1>(a, x, nq, smem, w.qkv, a.x, w.an, 0u);
+        else gemv_body<FMT, PRO_NORM, EPI_QKV, false, 1, 1, LL_IN>(a, x, nq, smem, w.qkv, a.x, w.an, l);
+        return;
+    }
+    x -= nq;
+    if (x < tasks) {
+        LLIn li = b.lli;
+        li.fadd = l;
+        attn_group_body<PARTS, true, 1, true>(pd, b.g, b.kv, l, b.M, nullptr, nullptr, nullptr, b.S, b.s_stride,
+                                              b.Up, b.cstride, b.pf, li, x, 0, bid, tasks, smem);
+        return;
+    }
+    x -= tasks;
+    if (x < n_mg) {
+        merge_cols_poll(o, x, b.lli.out, b.lli.sreg, b.s_stride, b.cstride, o.K, o.e.hd, o.lli.ep, pd, l);
+        return;
+    }
+    x -= n_mg;
+    if (x < n_o) {
+        if (l == 0)
+            gemv_body<FMT, PRO_QUANT, EPI_RESID, false, 1, 1, LL_IN | LL_OUT | LL_GATE>(o, x, n_o, smem, w.o, o.x,
+                                                                                        o.nw, 0u);
+        else
+            gemv_body<FMT, PRO_QUANT, EPI_RESID, false, 1, 1, LL_IN | LL_OLD | LL_OUT | LL_GATE>(o, x, n_o, smem, w.o,
+                                                                                                 o.x, o.nw, l);
+        return;
+    }
+    x -= n_o;
+    if (x < n_gu) {
+        gemv_body<FMT, PRO_NORM, EPI_SWIGLU, false, 1, 1, LL_IN | LL_OUT | LL_GATE>(gu, x, n_gu, smem, w.gu, gu.x,
+                                                                                    w.fn, l);
+        return;
+    }
+    x -= n_gu;
+    if (l + 1 < a.e.fmul)
+        gemv_body<FMT, PRO_QUANT, EPI_RESID, false, CPWD, 1, LL_IN | LL_OLD | LL_OUT | LL_NEXT | LL_GATE>(
+            dn, x, dn.N / 32u, smem, w.dn, dn.x, dn.nw, l);
+    else
+        gemv_body<FMT, PRO_QUANT, EPI_RESID, false, CPWD, 1, LL_IN | LL_OLD | LL_GATE>(dn, x, dn.N / 32u, smem, w.dn,
+                                                                                       dn.x, dn.nw, l);
+}
+
+// LDS of k_layer and k_stack: the attention blocks' need is the largest.
 __host__ __device__ constexpr uint32_t layer_smem(uint32_t D, uint32_t F) {
     return qkv_attn_smem(1, D, 1) > o_ffn_smem(1, D, F) ? qkv_attn_smem(1, D, 1) : o_ffn_smem(1, D, F);
 }

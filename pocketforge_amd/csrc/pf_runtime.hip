@@ -1391,6 +1391,13 @@ struct pf_engine {
     // then U [H][cstride][hd]).  PF_LAYER=0 keeps the two launches.
     unsigned long long* lla = nullptr;
     bool layer_fuse = true;
+    // one launch for every layer of a one-row pass (k_stack, pf_pass.hip):
+    // the per-layer operand table, whether every layer suits the fused
+    // roles, and PF_STACK=1 to use it (off by default: one launch per layer
+    // measures faster)
+    StackLayer* lw = nullptr;
+    bool stack_ok = false;
+    bool stack = false;
 };
 
 template <class T>
@@ -1496,7 +1503,22 @@ static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t ns
     if (!s) s = ealloc(e, &e->ep, 2);
     if (!s) s = ealloc(e, &e->llt, (size_t)MAX_PASS_ROWS * (2 * D + d.n_ff));
     if (!s) s = ealloc(e, &e->lla, (size_t)d.n_heads * (e->s_stride + (size_t)e->cstride * d.head_dim));
+    if (!s) s = ealloc(e, &e->lw, std::max(1u, d.n_layers));
     if (s) { pf_engine_destroy(e); return s; }
+    {
+        const pf_model* m = e->m;
+        std::vector<StackLayer> lw(d.n_layers);
+        bool ok = d.n_layers > 0 && D <= 2048 && (hd == 64 || hd == 128);
+        for (uint32_t l = 0; l < d.n_layers; l++) {
+            lw[l] = StackLayer{m->qkv[l]->data, m->o[l]->data, m->gu[l]->data, m->down[l]->data,
+                               m->attn_norm + (size_t)l * D, m->ffn_norm + (size_t)l * D};
+            ok = ok && m->qkv[l]->fmt == FMT_Q4 && m->o[l]->fmt == FMT_Q4 && m->gu[l]->fmt == FMT_Q4 &&
+                 m->down[l]->fmt == FMT_Q4;
+        }
+        e->stack_ok = ok && F % 256 == 0 && F <= 6144 && e->cstride - 1 <= 64;
+        if (d.n_layers)
+            PF_HIP(c, hipMemcpy(e->lw, lw.data(), lw.size() * sizeof(StackLayer), hipMemcpyHostToDevice));
+    }
     e->ll_err = e->ep + 1;
     PF_HIP(c, hipMemset(e->ll, 0, (size_t)MAX_PASS_ROWS * 3 * D * 8));
     PF_HIP(c, hipMemset(e->llt, 0, (size_t)MAX_PASS_ROWS * (2 * D + d.n_ff) * 8));
@@ -1505,6 +1527,7 @@ static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t ns
     if (const char* v = std::getenv("PF_QKV_ATTN")) e->qkv_attn = !(v[0] == '0');
     if (const char* v = std::getenv("PF_O_FFN")) e->o_ffn = !(v[0] == '0');
     if (const char* v = std::getenv("PF_LAYER")) e->layer_fuse = !(v[0] == '0');
+    if (const char* v = std::getenv("PF_STACK")) e->stack = v[0] == '1';
     if (hipHostMalloc((void**)&e->word, 64, hipHostMallocDefault) != hipSuccess) {
         pf_engine_destroy(e);
         return fail(c, PF_ERR_HIP, "hipHostMalloc failed");
@@ -1908,6 +1931,43 @@ static void launch_layer(hipStream_t st, uint32_t hd, const GemvArgs& a, const A
     else layer_cpw<8>(st, a, b, ao, ag, ad, tasks, ev0, ev1);
 }
 
+template <int P, int CPWD>
+static void stack_one(hipStream_t st, uint32_t nl, const StackLayer* lw, const GemvArgs& a, const AttnGroupArgs& b,
+                      const GemvArgs& ao, const GemvArgs& ag, const GemvArgs& ad, uint32_t tasks, hipEvent_t ev0,
+                      hipEvent_t ev1) {
+    static bool attr = false;   // LDS beyond 64 KiB is granted per kernel
+    if (!attr) {
+        (void)hipFuncSetAttribute((const void*)k_stack<FMT_Q4, P, CPWD>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  layer_smem(2048, 6144));
+        attr = true;
+    }
+    const uint32_t nq = a.N / 32, n_mg = (ao.K + 511) / 512, n_o = ao.N / 32, n_gu = ag.N / 32, n_dn = ad.N / 32;
+    const uint32_t G = nq + tasks + n_mg + n_o + n_gu + n_dn;
+    const uint32_t smem = layer_smem(ao.K, ad.K);
+    const dim3 grid(G * nl);
+    if (ev0)
+        hipExtLaunchKernelGGL((k_stack<FMT_Q4, P, CPWD>), grid, dim3(512), smem, st, ev0, ev1, 0, nq, tasks, n_mg, n_o,
+                              n_gu, G, b.pd, lw, a, b, ao, ag, ad);
+    else
+        hipLaunchKernelGGL((k_stack<FMT_Q4, P, CPWD>), grid, dim3(512), smem, st, nq, tasks, n_mg, n_o, n_gu, G, b.pd,
+                           lw, a, b, ao, ag, ad);
+}
+
+static void launch_stack(hipStream_t st, uint32_t hd, uint32_t nl, const StackLayer* lw, const GemvArgs& a,
+                         const AttnGroupArgs& b, const GemvArgs& ao, const GemvArgs& ag, const GemvArgs& ad,
+                         uint32_t tasks, hipEvent_t ev0, hipEvent_t ev1) {
+    const uint32_t cpw = (ad.K / 256 + GEMV_WAVES - 1) / GEMV_WAVES;
+    if (hd == 64) {
+        if (cpw == 1) stack_one<4, 1>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
+        else if (cpw == 2) stack_one<4, 2>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
+        else stack_one<4, 3>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
+    } else {
+        if (cpw == 1) stack_one<8, 1>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
+        else if (cpw == 2) stack_one<8, 2>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
+        else stack_one<8, 3>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
+    }
+}
+
 // One forward pass of M rows (the PassDesc at `pd` holds positions and
 // tokens; pos0 is the host's copy of the first position).  hidden/logits
 // outputs are device [M][D] / [M][V]; either may be null.  A batched pass
@@ -1951,7 +2011,71 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
                        pd);
     hipLaunchKernelGGL(k_embed, dim3((D + 255) / 256, M), dim3(256), 0, st, m->emb->data, m->emb->scales, d.n_vocab, D,
                        pd, e->x, e->ep, (int32_t)m->emb->fmt);
-    for (uint32_t l = 0; l < d.n_layers; l++) {
+    // one-row passes: every layer in one launch (k_stack); LL words of the
+    // residual rows between layers after the three of k_layer in llt
+    const bool stack = M == 1 && e->stack && e->stack_ok && e->qkv_attn && e->o_ffn && !e->skip_on;
+    if (stack) {
+        const uint32_t nl = d.n_layers;
+        unsigned long long* const lx = e->llt;
+        unsigned long long* const lsg = e->llt + D;
+        unsigned long long* const lmg = lsg + F;
+        unsigned long long* const lxo = lmg + D;
+        const LLIn li{nullptr, e->ep, nl, 0u, e->ll_err};
+        GemvArgs a{};
+        a.e.rc = e->rope_c; a.e.rs = e->rope_s; a.e.pd = pd; a.e.D = D; a.e.hd = hd;
+        a.e.ll = e->ll; a.e.ep = e->ep; a.e.fmul = nl; a.e.fadd = 0;
+        a.x = e->x; a.xs = D;
+        a.N = m->qkv[0]->rows; a.K = D; a.M = 1;
+        a.lli = li;
+        a.lli.ll = lxo;
+        a.lli.sent = D - 1;
+        AttnGroupArgs b{pd, g, e->kv, 0u, 1, e->S, e->s_stride, e->Wp, e->cstride, prefetch_of(e, nullptr, 0),
+                        LLIn{e->ll, e->ep, nl, 0u, e->ll_err}};
+        b.lli.out = e->lla;
+        b.lli.sreg = H * e->s_stride;
+        GemvArgs ao{}, ag{}, ad{};
+        ao.N = D; ao.K = D; ao.M = 1; ao.xs = D; ao.g = g;
+        ao.e.pd = pd; ao.e.hd = hd; ao.e.D = D;
+        ao.e.y = e->x; ao.e.y_stride = D; ao.e.ll = lx; ao.e.llold = lxo;
+        ao.lli = li;
+        ao.lli.ll = lmg;
+        ag.N = m->gu[0]->rows; ag.K = D; ag.M = 1; ag.xs = D;
+        ag.e.y_stride = F; ag.e.ll = lsg;
+        ag.lli = li;
+        ag.lli.ll = lx;
+        ad.N = D; ad.K = F; ad.M = 1; ad.xs = F;
+        ad.e.y = e->x; ad.e.y_stride = D; ad.e.llold = lx; ad.e.ll = lxo;
+        if (hidden) ad.e.y2 = hidden;
+        ad.lli = li;
+        ad.lli.ll = lsg;
+        for (GemvArgs* x : {&ao, &ag, &ad}) {   // weight loads after the layer's QKV product
+            x->lli.gate = e->ll;
+            x->lli.gate_off = 3 * D - 1;
+        }
+        hipEvent_t ev0 = nullptr, ev1 = nullptr;
+        if (e->profile == 1 && e->in_verify && !e->capturing) {
+            if (e->kev_used == e->kev.size()) {
+                TimedPass n{};
+                PF_HIP(c, hipEventCreate(&n.a));
+                PF_HIP(c, hipEventCreate(&n.b));
+                e->kev.push_back(n);
+                e->kev_bytes.push_back(0.0);
+            }
+            // every layer's four matrices with their fp32 input and output
+            // rows, and the visible K/V rows with their scales
+            double bytes = 0.0;
+            for (uint32_t l = 0; l < nl; l++)
+                for (const pf_matrix* W : {m->qkv[l], m->o[l], m->gu[l], m->down[l]})
+                    bytes += (double)W->bytes + 4.0 * W->cols + 4.0 * W->rows;
+            bytes += 2.0 * nl * H * (hd + 4.0) * kv_view(g, pos_last).count();
+            e->kev_bytes[e->kev_used] = bytes;
+            ev0 = e->kev[e->kev_used].a;
+            ev1 = e->kev[e->kev_used].b;
+            e->kev_used++;
+        }
+        launch_stack(st, hd, nl, e->lw, a, b, ao, ag, ad, attn_tasks, ev0, ev1);
+    }
+    for (uint32_t l = 0; l < (stack ? 0u : d.n_layers); l++) {
         const float* an = m->attn_norm + (size_t)l * D;
         const float* fn = m->ffn_norm + (size_t)l * D;
         // Q/K/V with RoPE (src/engine.cpp:515-523, 693-749)
