@@ -985,6 +985,14 @@ __device__ __forceinline__ void attn_group_body(const PassDesc* __restrict__ pd,
     // the plane (chunk_row stays inside the sink, pooled or ring rows), and
     // the staging below keeps only the entries it needs, so no wait
     // separates the loads.
+    if constexpr (LL) {
+        if (lli.gate) {   // the K/V loads wait for an earlier stage's word
+            const uint32_t go[1] = {lli.gate_off};
+            float gv[1];
+            if (wid == 0) ll_wait<1>(lli.gate, go, gv, epoch * lli.fmul + lli.fadd - lli.gate_back, lli.err);
+            __syncthreads();
+        }
+    }
     int4 kw[PARTS], vw[PARTS];
 #pragma unroll
     for (uint32_t i = 0; i < (uint32_t)PARTS; i++) kw[i] = vw[i] = make_int4(0, 0, 0, 0);

@@ -353,10 +353,11 @@ struct LLIn {
     // out[sreg + ((row H + h) cstride + c) hd + d]
     unsigned long long* out;
     uint32_t sreg;
-    // LL_GATE (GEMV): the word gate[gate_off] a workgroup waits for before its
-    // weight loads
+    // LL_GATE (GEMV), or attention blocks with gate set: the word
+    // gate[gate_off] a workgroup waits for before its weight (or cached K/V)
+    // loads, flagged gate_back layers before the workgroup's own
     const unsigned long long* gate;
-    uint32_t gate_off;
+    uint32_t gate_off, gate_back;
 };
 constexpr uint32_t LL_SPIN_MAX = 1u << 20;
 

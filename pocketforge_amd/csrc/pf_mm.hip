@@ -373,7 +373,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
     if constexpr ((LLM & LL_GATE) != 0) {
         const uint32_t go[1] = {a.lli.gate_off};
         float gv[1];
-        if (wid == 0) ll_wait<1>(a.lli.gate, go, gv, llflag, a.lli.err);
+        if (wid == 0) ll_wait<1>(a.lli.gate, go, gv, llflag - a.lli.gate_back, a.lli.err);
         __syncthreads();
     }
     const uint32_t nch = K >> 8, c0 = nch * wid / GEMV_WAVES, c1 = nch * (wid + 1) / GEMV_WAVES;

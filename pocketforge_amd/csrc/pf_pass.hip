@@ -344,13 +344,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     const StackLayer& w = lw[l];
     if (x < nq) {
         if (l == 0) gemv_body<FMT, PRO_NORM, EPI_QKV, false, 1, 1>(a, x, nq, smem, w.qkv, a.x, w.an, 0u);
-        else gemv_body<FMT, PRO_NORM, EPI_QKV, false, 1, 1, LL_IN>(a, x, nq, smem, w.qkv, a.x, w.an, l);
+        else gemv_body<FMT, PRO_NORM, EPI_QKV, false, 1, 1, LL_IN | LL_GATE>(a, x, nq, smem, w.qkv, a.x, w.an, l);
         return;
     }
     x -= nq;
     if (x < tasks) {
         LLIn li = b.lli;
         li.fadd = l;
+        if (l == 0) li.gate = nullptr;
         attn_group_body<PARTS, true, 1, true>(pd, b.g, b.kv, l, b.M, nullptr, nullptr, nullptr, b.S, b.s_stride,
                                               b.Up, b.cstride, b.pf, li, x, 0, bid, tasks, smem);
         return;

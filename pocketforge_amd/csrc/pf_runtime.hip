@@ -1393,11 +1393,10 @@ struct pf_engine {
     bool layer_fuse = true;
     // one launch for every layer of a one-row pass (k_stack, pf_pass.hip):
     // the per-layer operand table, whether every layer suits the fused
-    // roles, and PF_STACK=1 to use it (off by default: one launch per layer
-    // measures faster)
+    // roles, and PF_STACK=0 to keep one launch per layer (k_layer)
     StackLayer* lw = nullptr;
     bool stack_ok = false;
-    bool stack = false;
+    bool stack = true;
 };
 
 template <class T>
@@ -1527,7 +1526,7 @@ static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t ns
     if (const char* v = std::getenv("PF_QKV_ATTN")) e->qkv_attn = !(v[0] == '0');
     if (const char* v = std::getenv("PF_O_FFN")) e->o_ffn = !(v[0] == '0');
     if (const char* v = std::getenv("PF_LAYER")) e->layer_fuse = !(v[0] == '0');
-    if (const char* v = std::getenv("PF_STACK")) e->stack = v[0] == '1';
+    if (const char* v = std::getenv("PF_STACK")) e->stack = !(v[0] == '0');
     if (hipHostMalloc((void**)&e->word, 64, hipHostMallocDefault) != hipSuccess) {
         pf_engine_destroy(e);
         return fail(c, PF_ERR_HIP, "hipHostMalloc failed");
@@ -2029,10 +2028,18 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
         a.lli = li;
         a.lli.ll = lxo;
         a.lli.sent = D - 1;
+        // layers after the first: the QKV weight loads wait for the layer
+        // before's O product, the attention's cached K/V loads for its down
+        // product, so that neither competes with that layer's hand-offs
+        a.lli.gate = lx;
+        a.lli.gate_off = D - 1;
+        a.lli.gate_back = 1;
         AttnGroupArgs b{pd, g, e->kv, 0u, 1, e->S, e->s_stride, e->Wp, e->cstride, prefetch_of(e, nullptr, 0),
                         LLIn{e->ll, e->ep, nl, 0u, e->ll_err}};
         b.lli.out = e->lla;
         b.lli.sreg = H * e->s_stride;
+        b.lli.gate = lxo;
+        b.lli.gate_off = D - 1;
         GemvArgs ao{}, ag{}, ad{};
         ao.N = D; ao.K = D; ao.M = 1; ao.xs = D; ao.g = g;
         ao.e.pd = pd; ao.e.hd = hd; ao.e.D = D;
