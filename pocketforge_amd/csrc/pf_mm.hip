@@ -176,6 +176,33 @@ __device__ __forceinline__ pf_v4i b_operand(const uint4* cw, uint32_t t) {
     return v;
 }
 
+// The same block's codes as stored (0 .. 15 for Q4, 0 .. 3 for the 2-bit
+// formats), without the offset: v_dot4 over them gives the block's dot plus
+// offset x the activation codes' sum, which the one-row product removes by
+// starting its v_dot4 chain at -offset x that sum (integers: exact).
+template <int FMT>
+__device__ __forceinline__ pf_v4i b_operand_raw(const uint4* cw, uint32_t t) {
+    static_assert(FMT != FMT_Q8, "Q8 codes are signed bytes");
+    pf_v4i v;
+    if constexpr (FMT == FMT_Q4) {
+        const uint4 c = cw[t >> 1];
+        const uint32_t x0 = (t & 1u) ? c.z : c.x, x1 = (t & 1u) ? c.w : c.y, mk = 0x0F0F0F0Fu;
+        v.x = (int)(x0 & mk);
+        v.y = (int)(x1 & mk);
+        v.z = (int)((x0 >> 4) & mk);
+        v.w = (int)((x1 >> 4) & mk);
+    } else {
+        const uint4 c = cw[t >> 2];
+        const uint32_t s = t & 3u;
+        const uint32_t x = s == 0u ? c.x : (s == 1u ? c.y : (s == 2u ? c.z : c.w)), mk = 0x03030303u;
+        v.x = (int)(x & mk);
+        v.y = (int)((x >> 2) & mk);
+        v.z = (int)((x >> 4) & mk);
+        v.w = (int)((x >> 6) & mk);
+    }
+    return v;
+}
+
 template <int FMT>
 constexpr int sets_of() { return FMT == FMT_Q8 ? 8 : (FMT == FMT_Q4 ? 4 : 2); }
 
@@ -208,11 +235,12 @@ struct GemvArgs {
 
 // Dynamic LDS of k_gemv (bytes), laid out as: fp64 partials [waves][64][4],
 // int8 rows [M][K + 16], tile sums [M][K / 64], maxima [M][4 waves], row
-// statistics [3][8].
+// statistics [3][8], and for one row the offset terms of the raw-code
+// products [2][K / 32] (int32).
 __host__ __device__ constexpr uint32_t gemv_kp(uint32_t K) { return K + 16u; }
 __host__ __device__ constexpr uint32_t gemv_smem(uint32_t M, uint32_t K) {
     return (uint32_t)GEMV_WAVES * 64u * 4u * 8u + M * gemv_kp(K) + M * (K / 64u) * 4u +
-           M * 4u * (uint32_t)GEMV_WAVES * 4u + 3u * 8u * 4u;
+           M * 4u * (uint32_t)GEMV_WAVES * 4u + 3u * 8u * 4u + (M == 1u ? K / 16u * 4u : 0u);
 }
 // MERGE adds the chunk maxima and sums [2][2048] (heads * chunks <= 2048),
 // the head maxima and 1 / T [2][128] and a block reduction [16].
@@ -616,6 +644,20 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
         }
     }
     __syncthreads();
+    // one row of a sub-byte format: -offset x the sum of each half block's
+    // 16 activation codes, [half][block], the start of the product's chains
+    int* nsum = reinterpret_cast<int*>(st + 24);
+    if constexpr (MR == 1 && FMT != FMT_Q8) {
+        for (uint32_t i = t; i < K / 16u; i += NT) {
+            const pf_v4i v = *reinterpret_cast<const pf_v4i*>(act + 16u * i);
+            int s = __builtin_amdgcn_sdot4(v.x, 0x01010101, 0, false);
+            s = __builtin_amdgcn_sdot4(v.y, 0x01010101, s, false);
+            s = __builtin_amdgcn_sdot4(v.z, 0x01010101, s, false);
+            s = __builtin_amdgcn_sdot4(v.w, 0x01010101, s, false);
+            nsum[(i & 1u) * (K / 32u) + (i >> 1)] = -code_offset(FMT) * s;
+        }
+        __syncthreads();
+    }
 
     // ---- product
     if constexpr (MR == 1) {
@@ -625,7 +667,8 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
         // v_dot4 give the exact int32 partial p, and d_b * p accumulates in
         // fp64; the halves and waves meet in LDS.  Every partial sum is a
         // sum of some of the exact terms d_b * p_b, so the result is the
-        // same sum as the MFMA path's.
+        // same sum as the MFMA path's.  Sub-byte codes enter the v_dot4 as
+        // stored, the chain starting at the half block's offset term.
         double S1 = 0.0;
         const int8_t* a0 = act + 16u * h;
 #pragma unroll
@@ -634,12 +677,27 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, uint32_t bx, uint32
             const uint32_t c = c0 + j;
             const uint16_t* sc = reinterpret_cast<const uint16_t*>(&sw[j]);
             pf_v4i A[8];
+            int n0[8];
 #pragma unroll
             for (uint32_t u = 0; u < 8; u++) A[u] = *reinterpret_cast<const pf_v4i*>(a0 + 32u * (8u * c + u));
+            if constexpr (FMT != FMT_Q8) {
+                const int4 p0 = *reinterpret_cast<const int4*>(nsum + h * (K / 32u) + 8u * c);
+                const int4 p1 = *reinterpret_cast<const int4*>(nsum + h * (K / 32u) + 8u * c + 4u);
+                n0[0] = p0.x; n0[1] = p0.y; n0[2] = p0.z; n0[3] = p0.w;
+                n0[4] = p1.x; n0[5] = p1.y; n0[6] = p1.z; n0[7] = p1.w;
+            }
 #pragma unroll
             for (uint32_t u = 0; u < 8; u++) {
-                const pf_v4i B = b_operand<FMT>(cw[j], u);
-                int pp = __builtin_amdgcn_sdot4(A[u].x, B.x, 0, false);
+                pf_v4i B;
+                int pp;
+                if constexpr (FMT == FMT_Q8) {
+                    B = b_operand<FMT>(cw[j], u);
+                    pp = 0;
+                } else {
+                    B = b_operand_raw<FMT>(cw[j], u);
+                    pp = n0[u];
+                }
+                pp = __builtin_amdgcn_sdot4(A[u].x, B.x, pp, false);
                 pp = __builtin_amdgcn_sdot4(A[u].y, B.y, pp, false);
                 pp = __builtin_amdgcn_sdot4(A[u].z, B.z, pp, false);
                 pp = __builtin_amdgcn_sdot4(A[u].w, B.w, pp, false);
