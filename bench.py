@@ -13,9 +13,11 @@ is resident in HBM); the timed call is generate([last prompt token], 512),
 which forwards the last prompt token and runs the MTP rounds.  value =
 generated tokens / decode wall time over the K timed steps.
 
-Also reported: the int8 GEMV kernel's achieved HBM bandwidth (HIP events
-around every GEMV launch of the verify passes, algorithmic bytes = packed
-weights + int8 activations + fp32 outputs), the verify pass as a whole, and
+Also reported: the one-row pass's layer launch (k_stack: every layer in one
+launch) and its achieved HBM bandwidth (HIP events around every dispatch,
+algorithmic bytes = every layer's packed matrices with their fp32 input and
+output rows + the visible int8 K/V rows with scales), the verify pass as a
+whole, and
 the CPU restatement (oracle) timed on the host cores on a bounded sample of
 the same call: generate([last prompt token], 64 tokens on all cores, 16 on
 one) from the GPU's
@@ -67,13 +69,13 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "o_ffn_traffic_1b_q4.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "stack_traffic_1b_q4.md")
 
 
 def measured_traffic():
-    """HBM bytes per verify-pass GEMV launch from the committed hardware-
-    counter profile (FETCH_SIZE and WRITE_SIZE, scaled by a copy kernel of
-    known size), or None when the profile is absent."""
+    """HBM bytes per k_stack dispatch of the headline workload from the
+    committed hardware-counter profile (FETCH_SIZE and WRITE_SIZE, scaled by
+    a copy kernel of known size), or None when the profile is absent."""
     try:
         for line in open(TRAFFIC_PROFILE):
             if line.startswith("traffic_bytes_per_launch_avg:"):
@@ -139,7 +141,7 @@ def cpu_baseline(cfg, w, kv, snapshot, last, n_new, samp, what, gpu_tokens, thre
 def copy_probe(nbytes):
     """Three device-to-device copies of nbytes through the runtime's copy
     kernel: the known-size reference that scales the FETCH_SIZE and
-    WRITE_SIZE counters of the GEMV kernels."""
+    WRITE_SIZE counters of the decode kernels."""
     import pocketforge_amd as pf
     ctx = pf.Context(0)
     a = pf.DeviceArray(ctx, (nbytes,), np.uint8)
@@ -269,14 +271,15 @@ def main():
             f"accepted {res.mtp_accepted}, device time per MTP round {r_us:.1f} us")
     value = sum(gens) / sum(times)
     # one more decode of the same workload, kernels issued one by one with
-    # HIP start/stop events attached to every verify-pass GEMV dispatch
+    # HIP start/stop events attached to every layer launch of the decode
+    # passes (k_stack for one row)
     dt_p, toks_p, res_p = step(True)
     n_l, gemv_us, gemv_bytes = eng.gemv_stats()
     gemv_groups = eng.gemv_by_size()
     a_n, attn_us = eng.attn_stats()
     v_ev, b_ev, _, _ = eng.pass_times()
     log(f"profiled step: {dt_p * 1e3:.1f} ms, verify pass {v_ev:.1f} us, base pass {b_ev:.1f} us (with dispatch "
-        f"events), gemv {gemv_us:.2f} us avg x{n_l}")
+        f"events), layer launch {gemv_us:.2f} us avg x{n_l}")
     # and one more, issued the same way with events around each pass only:
     # the pass times without the dispatch events' own cost
     step(2)
@@ -370,23 +373,26 @@ def main():
                 "ffn_blocks_skipped_last_step": eng.layer_skip_count()} if args.layer_skip else {}),
         },
         "roofline": {
-            "kernel": ("k_o_ffn<Q4,3> (one-row verify pass: the attention's chunk merge and the O, gate|up and down "
-                       "int8 x Q4 products of a layer in one launch; bytes = the three matrices + fp32 rows)"),
+            "kernel": ("k_stack<Q4,8,3> (one-row decode pass: every layer's QKV product, attention, chunk merge, "
+                       "O, gate|up and down products in one launch; bytes = every layer's four matrices with their "
+                       "fp32 input and output rows + the visible int8 K/V rows with scales)"),
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": measured_traffic() if headline else None,
-            "traffic_source": "profiles/o_ffn_traffic_1b_q4.md (rocprofv3 FETCH_SIZE x 1.99978 + WRITE_SIZE x 1.0, "
-                              "factors from a copy kernel of known size; prefetch off)",
+            "traffic_source": "profiles/stack_traffic_1b_q4.md (rocprofv3 FETCH_SIZE and WRITE_SIZE per k_stack "
+                              "dispatch of this workload, scaled by a copy kernel of known size)",
             "avg_launch_us": round(gemv_us, 3),
             "avg_bytes_per_launch": round(gemv_bytes),
             "launches": n_l,
-            "timing": "HIP start/stop events attached to each k_o_ffn dispatch (hipExtLaunchKernelGGL) on the engine "
+            "timing": "HIP start/stop events attached to each k_stack dispatch (hipExtLaunchKernelGGL) on the engine "
                       "stream, in one extra decode step of the same workload issued without graphs",
-            "by_matrix": [{"bytes": round(b), "launches": n, "avg_us": round(u, 3),
-                           "GBps": round(b / u / 1e3, 1)} for b, n, u in gemv_groups],
+            "range": ({"min_bytes": round(min(b for b, _, _ in gemv_groups)),
+                       "max_bytes": round(max(b for b, _, _ in gemv_groups)),
+                       "min_us": round(min(u for _, _, u in gemv_groups), 3),
+                       "max_us": round(max(u for _, _, u in gemv_groups), 3)} if gemv_groups else None),
         },
         "verify_pass": {
             "avg_us": round(v_us, 2),
