@@ -322,6 +322,12 @@ struct StackLayer {
     const float *an, *fn;               // attention and FFN norm weights [D]
 };
 
+// The gate|up and down formats k_stack is built for: all Q4, or Q2 gate|up
+// with Q1.5 down (the QKV and O matrices Q4 in both).
+inline bool stack_fmts(int32_t fg, int32_t fd) {
+    return (fg == FMT_Q4 && fd == FMT_Q4) || (fg == FMT_Q2 && fd == FMT_Q15);
+}
+
 // Every layer of a one-row pass in one launch: layer l's workgroups are
 // [l G, (l + 1) G), laid out as k_layer's (QKV, attention, merge, O,
 // gate|up, down).  Layer l's down product hands the updated residual row to
@@ -333,8 +339,9 @@ struct StackLayer {
 // the attention's cached K/V loads) overlap its arithmetic.  Flags are
 // epoch * layers + layer (the args carry fadd = 0; each role adds its layer).
 // Progress as for k_layer: every wait is for workgroups of lower ids (the
-// layer before, or earlier roles of the layer), and bounded.
-template <int FMT, int PARTS, int CPWD>
+// layer before, or earlier roles of the layer), and bounded.  FMT is the
+// format of the QKV and O matrices, FG of gate|up, FD of down.
+template <int FMT, int FG, int FD, int PARTS, int CPWD>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void k_stack(
     uint32_t nq, uint32_t tasks, uint32_t n_mg, uint32_t n_o, uint32_t n_gu, uint32_t G, const PassDesc* pd,
     const StackLayer* lw, GemvArgs a, AttnGroupArgs b, GemvArgs o, GemvArgs gu, GemvArgs dn) {
@@ -373,17 +380,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     }
     x -= n_o;
     if (x < n_gu) {
-        gemv_body<FMT, PRO_NORM, EPI_SWIGLU, false, 1, 1, LL_IN | LL_OUT | LL_GATE>(gu, x, n_gu, smem, w.gu, gu.x,
-                                                                                    w.fn, l);
+        gemv_body<FG, PRO_NORM, EPI_SWIGLU, false, 1, 1, LL_IN | LL_OUT | LL_GATE>(gu, x, n_gu, smem, w.gu, gu.x,
+                                                                                   w.fn, l);
         return;
     }
     x -= n_gu;
     if (l + 1 < a.e.fmul)
-        gemv_body<FMT, PRO_QUANT, EPI_RESID, false, CPWD, 1, LL_IN | LL_OLD | LL_OUT | LL_NEXT | LL_GATE>(
+        gemv_body<FD, PRO_QUANT, EPI_RESID, false, CPWD, 1, LL_IN | LL_OLD | LL_OUT | LL_NEXT | LL_GATE>(
             dn, x, dn.N / 32u, smem, w.dn, dn.x, dn.nw, l);
     else
-        gemv_body<FMT, PRO_QUANT, EPI_RESID, false, CPWD, 1, LL_IN | LL_OLD | LL_GATE>(dn, x, dn.N / 32u, smem, w.dn,
-                                                                                       dn.x, dn.nw, l);
+        gemv_body<FD, PRO_QUANT, EPI_RESID, false, CPWD, 1, LL_IN | LL_OLD | LL_GATE>(dn, x, dn.N / 32u, smem, w.dn,
+                                                                                      dn.x, dn.nw, l);
 }
 
 // LDS of k_layer and k_stack: the attention blocks' need is the largest.

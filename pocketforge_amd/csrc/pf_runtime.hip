@@ -1511,9 +1511,10 @@ static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t ns
         for (uint32_t l = 0; l < d.n_layers; l++) {
             lw[l] = StackLayer{m->qkv[l]->data, m->o[l]->data, m->gu[l]->data, m->down[l]->data,
                                m->attn_norm + (size_t)l * D, m->ffn_norm + (size_t)l * D};
-            ok = ok && m->qkv[l]->fmt == FMT_Q4 && m->o[l]->fmt == FMT_Q4 && m->gu[l]->fmt == FMT_Q4 &&
-                 m->down[l]->fmt == FMT_Q4;
+            ok = ok && m->qkv[l]->fmt == FMT_Q4 && m->o[l]->fmt == FMT_Q4 && m->gu[l]->fmt == m->gu[0]->fmt &&
+                 m->down[l]->fmt == m->down[0]->fmt;
         }
+        ok = ok && stack_fmts(m->gu[0]->fmt, m->down[0]->fmt);
         e->stack_ok = ok && F % 256 == 0 && F <= 6144 && e->cstride - 1 <= 64;
         if (d.n_layers)
             PF_HIP(c, hipMemcpy(e->lw, lw.data(), lw.size() * sizeof(StackLayer), hipMemcpyHostToDevice));
@@ -1930,14 +1931,14 @@ static void launch_layer(hipStream_t st, uint32_t hd, const GemvArgs& a, const A
     else layer_cpw<8>(st, a, b, ao, ag, ad, tasks, ev0, ev1);
 }
 
-template <int P, int CPWD>
+template <int FG, int FD, int P, int CPWD>
 static void stack_one(hipStream_t st, uint32_t nl, const StackLayer* lw, const GemvArgs& a, const AttnGroupArgs& b,
                       const GemvArgs& ao, const GemvArgs& ag, const GemvArgs& ad, uint32_t tasks, hipEvent_t ev0,
                       hipEvent_t ev1) {
     static bool attr = false;   // LDS beyond 64 KiB is granted per kernel
     if (!attr) {
-        (void)hipFuncSetAttribute((const void*)k_stack<FMT_Q4, P, CPWD>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  layer_smem(2048, 6144));
+        (void)hipFuncSetAttribute((const void*)k_stack<FMT_Q4, FG, FD, P, CPWD>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, layer_smem(2048, 6144));
         attr = true;
     }
     const uint32_t nq = a.N / 32, n_mg = (ao.K + 511) / 512, n_o = ao.N / 32, n_gu = ag.N / 32, n_dn = ad.N / 32;
@@ -1945,26 +1946,34 @@ static void stack_one(hipStream_t st, uint32_t nl, const StackLayer* lw, const G
     const uint32_t smem = layer_smem(ao.K, ad.K);
     const dim3 grid(G * nl);
     if (ev0)
-        hipExtLaunchKernelGGL((k_stack<FMT_Q4, P, CPWD>), grid, dim3(512), smem, st, ev0, ev1, 0, nq, tasks, n_mg, n_o,
-                              n_gu, G, b.pd, lw, a, b, ao, ag, ad);
+        hipExtLaunchKernelGGL((k_stack<FMT_Q4, FG, FD, P, CPWD>), grid, dim3(512), smem, st, ev0, ev1, 0, nq, tasks,
+                              n_mg, n_o, n_gu, G, b.pd, lw, a, b, ao, ag, ad);
     else
-        hipLaunchKernelGGL((k_stack<FMT_Q4, P, CPWD>), grid, dim3(512), smem, st, nq, tasks, n_mg, n_o, n_gu, G, b.pd,
-                           lw, a, b, ao, ag, ad);
+        hipLaunchKernelGGL((k_stack<FMT_Q4, FG, FD, P, CPWD>), grid, dim3(512), smem, st, nq, tasks, n_mg, n_o, n_gu,
+                           G, b.pd, lw, a, b, ao, ag, ad);
 }
 
-static void launch_stack(hipStream_t st, uint32_t hd, uint32_t nl, const StackLayer* lw, const GemvArgs& a,
-                         const AttnGroupArgs& b, const GemvArgs& ao, const GemvArgs& ag, const GemvArgs& ad,
-                         uint32_t tasks, hipEvent_t ev0, hipEvent_t ev1) {
+template <int FG, int FD>
+static void stack_fmt(hipStream_t st, uint32_t hd, uint32_t nl, const StackLayer* lw, const GemvArgs& a,
+                      const AttnGroupArgs& b, const GemvArgs& ao, const GemvArgs& ag, const GemvArgs& ad,
+                      uint32_t tasks, hipEvent_t ev0, hipEvent_t ev1) {
     const uint32_t cpw = (ad.K / 256 + GEMV_WAVES - 1) / GEMV_WAVES;
     if (hd == 64) {
-        if (cpw == 1) stack_one<4, 1>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
-        else if (cpw == 2) stack_one<4, 2>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
-        else stack_one<4, 3>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
+        if (cpw == 1) stack_one<FG, FD, 4, 1>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
+        else if (cpw == 2) stack_one<FG, FD, 4, 2>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
+        else stack_one<FG, FD, 4, 3>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
     } else {
-        if (cpw == 1) stack_one<8, 1>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
-        else if (cpw == 2) stack_one<8, 2>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
-        else stack_one<8, 3>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
+        if (cpw == 1) stack_one<FG, FD, 8, 1>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
+        else if (cpw == 2) stack_one<FG, FD, 8, 2>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
+        else stack_one<FG, FD, 8, 3>(st, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
     }
+}
+
+static void launch_stack(hipStream_t st, int32_t fg, uint32_t hd, uint32_t nl, const StackLayer* lw,
+                         const GemvArgs& a, const AttnGroupArgs& b, const GemvArgs& ao, const GemvArgs& ag,
+                         const GemvArgs& ad, uint32_t tasks, hipEvent_t ev0, hipEvent_t ev1) {
+    if (fg == FMT_Q4) stack_fmt<FMT_Q4, FMT_Q4>(st, hd, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
+    else stack_fmt<FMT_Q2, FMT_Q15>(st, hd, nl, lw, a, b, ao, ag, ad, tasks, ev0, ev1);
 }
 
 // One forward pass of M rows (the PassDesc at `pd` holds positions and
@@ -2080,7 +2089,7 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
             ev1 = e->kev[e->kev_used].b;
             e->kev_used++;
         }
-        launch_stack(st, hd, nl, e->lw, a, b, ao, ag, ad, attn_tasks, ev0, ev1);
+        launch_stack(st, m->gu[0]->fmt, hd, nl, e->lw, a, b, ao, ag, ad, attn_tasks, ev0, ev1);
     }
     for (uint32_t l = 0; l < (stack ? 0u : d.n_layers); l++) {
         const float* an = m->attn_norm + (size_t)l * D;

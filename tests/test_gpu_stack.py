@@ -1,8 +1,9 @@
 """One-row passes through each of the fused launch layouts, bit-exact
 against the oracle: every layer in one launch (the default), one launch per
 layer (PF_STACK=0) and the QKV + attention and O + FFN launches
-(PF_STACK=0 PF_LAYER=0).  Models of 1, 2 and 12 layers, hidden sizes 256 and 768, and
-attention lists of one and three 256-entry chunks."""
+(PF_STACK=0 PF_LAYER=0).  Models of 1, 2 and 12 layers, hidden sizes 256 and 768, all
+Q4 or with Q2 gate|up and Q1.5 down, and attention lists of one and three 256-entry
+chunks."""
 import numpy as np
 import pytest
 
@@ -51,6 +52,29 @@ def test_one_row_forwards(gpu, monkeypatch, mode, layers, kv, n):
         lg, hg = e.forward([t])
         lo, ho = om.forward(t)
         if i < 8 or i % 23 == 0 or i >= n - 4:
+            np.testing.assert_array_equal(hg[0], ho, err_msg=f"{mode} row {i}")
+            np.testing.assert_array_equal(lg[0], lo, err_msg=f"{mode} row {i}")
+    om.close()
+    e.close()
+    m.close()
+
+
+@pytest.mark.parametrize("mode", list(MODES))
+def test_one_row_forwards_mixed_formats(gpu, monkeypatch, mode):
+    """Q4 attention matrices with Q2 gate|up and Q1.5 down (the layer stack's
+    second format set; the other layouts run these as separate products)."""
+    _setenv(monkeypatch, mode)
+    cfg = W.TINY
+    kv = dict(sink_size=4, window_size=64, pool_block=6, max_context=512)
+    w = W.make_weights(cfg, seed=321, fmts=W.MIXED)
+    m = pf.Model(gpu, cfg, w)
+    e = pf.Engine(m, **kv)
+    om = _oracle(cfg, w, kv)
+    toks = W.prompt_ids(80, cfg["n_vocab"], seed=8)
+    for i, t in enumerate(toks):
+        lg, hg = e.forward([t])
+        lo, ho = om.forward(t)
+        if i < 8 or i % 13 == 0 or i >= 76:
             np.testing.assert_array_equal(hg[0], ho, err_msg=f"{mode} row {i}")
             np.testing.assert_array_equal(lg[0], lo, err_msg=f"{mode} row {i}")
     om.close()
