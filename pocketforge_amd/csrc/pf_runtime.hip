@@ -504,7 +504,7 @@ constexpr uint32_t F32_GROUP = 4;
 
 static void launch_gemv_f32(hipStream_t st, const pf_matrix* W, uint32_t M, const float* h, uint32_t h_stride,
                             float* y, uint32_t y_stride, const float* y_in) {
-    uint32_t waves = std::min<uint32_t>(W->rows, 2048);
+    uint32_t waves = std::min<uint32_t>(W->rows, 4096);
     // whole groups of F32_GROUP rows in one launch (grid y), then the rest
     constexpr uint32_t GR = F32_GROUP;
     for (uint32_t r0 = 0; r0 < M;) {
