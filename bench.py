@@ -373,9 +373,12 @@ def main():
                 "ffn_blocks_skipped_last_step": eng.layer_skip_count()} if args.layer_skip else {}),
         },
         "roofline": {
-            "kernel": ("k_stack<Q4,8,3> (one-row decode pass: every layer's QKV product, attention, chunk merge, "
-                       "O, gate|up and down products in one launch; bytes = every layer's four matrices with their "
-                       "fp32 input and output rows + the visible int8 K/V rows with scales)"),
+            "kernel": ("k_stack (one-row decode pass: every layer's QKV product, attention, chunk merge, O, "
+                       "gate|up and down products in one launch; bytes = every layer's four matrices with their fp32 "
+                       "input and output rows + the visible int8 K/V rows with scales)" if headline else
+                       "the decode passes' layer launches: k_stack for one-row passes, k_o_ffn (merge, O, gate|up) "
+                       "for passes of 2-8 rows; bytes = the launch's matrices with their fp32 rows (+ K/V rows for "
+                       "k_stack)"),
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
