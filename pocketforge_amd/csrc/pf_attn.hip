@@ -143,8 +143,9 @@ __global__ __launch_bounds__(128) void k_pool_row_one(KvGeom g, KvPlanes kv, uin
 // a single-sequence pass, or over the pass rows of a batched pass: row m at
 // position p folds [pool(p - 1), pool(p)), at most one row, since the
 // pooled count grows by at most one per position.
-__global__ __launch_bounds__(128) void k_pool_rows(KvGeom g, KvPlanes kv, const PassDesc* __restrict__ pd) {
-    uint32_t p_first, p_last, seq, y = blockIdx.y;
+__device__ __forceinline__ void pool_rows_block(const KvGeom& g, const KvPlanes& kv, const PassDesc* __restrict__ pd,
+                                                uint32_t bx, uint32_t y) {
+    uint32_t p_first, p_last, seq;
     if (pd->batch) {
         if (y >= pd->m) return;
         p_first = p_last = pd->rpos[y];
@@ -159,7 +160,10 @@ __global__ __launch_bounds__(128) void k_pool_rows(KvGeom g, KvPlanes kv, const 
     const uint32_t r_hi = kv_view(g, p_last).pool;
     const uint32_t r = r_lo + y;
     if (r >= r_hi || r >= g.pool_cap) return;
-    pool_row(g, kv, (size_t)seq * g.n_layers * g.n_heads + blockIdx.x, r);
+    pool_row(g, kv, (size_t)seq * g.n_layers * g.n_heads + bx, r);
+}
+__global__ __launch_bounds__(128) void k_pool_rows(KvGeom g, KvPlanes kv, const PassDesc* __restrict__ pd) {
+    pool_rows_block(g, kv, pd, blockIdx.x, blockIdx.y);
 }
 
 // ------------------------------------------------------------ attention

@@ -411,10 +411,10 @@ __global__ void k_copy_f32(const float* __restrict__ src, float* __restrict__ ds
 // Q8, fmt).
 // The first kernel of every pass also advances the pass epoch `ep`, which
 // names the pass in the flags of the LL words its QKV products write.
-__global__ void k_embed(const uint8_t* __restrict__ codes, const uint16_t* __restrict__ scales,
-                        uint32_t V, uint32_t D, const PassDesc* __restrict__ pd, float* __restrict__ x,
-                        uint32_t* __restrict__ ep, int32_t fmt) {
-    uint32_t m = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void embed_elem(const uint8_t* __restrict__ codes, const uint16_t* __restrict__ scales,
+                                           uint32_t V, uint32_t D, const PassDesc* __restrict__ pd,
+                                           float* __restrict__ x, uint32_t* __restrict__ ep, int32_t fmt, uint32_t m,
+                                           uint32_t i) {
     if (ep && m == 0 && i == 0) ep[0] += 1u;
     if (m >= pd->m || i >= D) return;
     int32_t tok = pd->tok[m];
@@ -431,6 +431,11 @@ __global__ void k_embed(const uint8_t* __restrict__ codes, const uint16_t* __res
         }
     }
     x[(size_t)m * D + i] = val;
+}
+__global__ void k_embed(const uint8_t* __restrict__ codes, const uint16_t* __restrict__ scales,
+                        uint32_t V, uint32_t D, const PassDesc* __restrict__ pd, float* __restrict__ x,
+                        uint32_t* __restrict__ ep, int32_t fmt) {
+    embed_elem(codes, scales, V, D, pd, x, ep, fmt, blockIdx.y, blockIdx.x * blockDim.x + threadIdx.x);
 }
 
 // ============================================ reference plain-int8 matmul

@@ -316,6 +316,23 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
                                                                                    dn.x, dn.nw);
 }
 
+// A pass's first launch: the pooled rows it can see (k_pool_rows, blocks
+// [0, n_pool): layers * heads per pooled-row slot ny) and its embedded rows
+// with the epoch advance (k_embed, 128 columns per block), two independent
+// jobs in one launch.  128 threads.
+__global__ __launch_bounds__(128) void k_pass_prep(KvGeom g, KvPlanes kv, const PassDesc* __restrict__ pd,
+                                                   uint32_t n_pool, const uint8_t* __restrict__ codes,
+                                                   const uint16_t* __restrict__ scales, uint32_t V, uint32_t D,
+                                                   float* __restrict__ x, uint32_t* __restrict__ ep, int32_t fmt) {
+    const uint32_t b = blockIdx.x, lh = g.n_layers * g.n_heads;
+    if (b < n_pool) {
+        pool_rows_block(g, kv, pd, b % lh, b / lh);
+        return;
+    }
+    const uint32_t e = b - n_pool, nbx = (D + 127u) / 128u, m = e / nbx;
+    embed_elem(codes, scales, V, D, pd, x, ep, fmt, m, (e - m * nbx) * 128u + threadIdx.x);
+}
+
 // Per-layer operands of k_stack.
 struct StackLayer {
     const uint8_t *qkv, *o, *gu, *dn;   // packed matrices

@@ -2012,13 +2012,14 @@ static pf_status run_pass(pf_engine* e, PassDesc* pd, uint32_t M, uint32_t pos0,
     float* as1 = e->as + e->rows;         // attention output act
     float* as2 = e->as + 2 * e->rows;     // ffn-norm act
     float* as3 = e->as + 3 * e->rows;     // swiglu act
-    const dim3 tb(hd <= 64 ? 64 : 128);
 
     // pooled rows the pass can see (folded from window entries still in the ring)
-    hipLaunchKernelGGL(k_pool_rows, dim3(g.n_layers * g.n_heads, batch ? M : e->pool_rows_max), tb, 0, st, g, e->kv,
-                       pd);
-    hipLaunchKernelGGL(k_embed, dim3((D + 255) / 256, M), dim3(256), 0, st, m->emb->data, m->emb->scales, d.n_vocab, D,
-                       pd, e->x, e->ep, (int32_t)m->emb->fmt);
+    // and the embedded rows, in one launch (k_pass_prep)
+    {
+        const uint32_t n_pool = g.n_layers * g.n_heads * (batch ? M : e->pool_rows_max);
+        hipLaunchKernelGGL(k_pass_prep, dim3(n_pool + (D + 127) / 128 * M), dim3(128), 0, st, g, e->kv, pd, n_pool,
+                           m->emb->data, m->emb->scales, d.n_vocab, D, e->x, e->ep, (int32_t)m->emb->fmt);
+    }
     // one-row passes: every layer in one launch (k_stack); LL words of the
     // residual rows between layers after the three of k_layer in llt
     const bool stack = M == 1 && e->stack && e->stack_ok && e->qkv_attn && e->o_ffn && !e->skip_on;
