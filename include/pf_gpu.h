@@ -280,6 +280,20 @@ pf_status pf_forward(pf_engine* e, const int32_t* tokens, uint32_t n, float* log
 /* MTPHeads::forward (mtp.hpp:40-43) with the tied table: logits
  * [n_mtp][n_vocab] from a pre-norm hidden state. */
 pf_status pf_mtp_forward(pf_engine* e, const float* hidden, float* logits);
+/* Engine::step_mtp (src/engine.cpp:402-448) with the heads present, on the
+ * device: MTPHeads::forward from `hidden` (pre-norm, [n_embd]), one sample per
+ * head (cfg, seed, draws from *draw_index, advanced like pf_sample's), one
+ * pass over [current_token, d0 .. d{n-2}] at the engine's next positions,
+ * and the greedy check of row k against draft k up to the first mismatch.
+ * The engine's position advances by the rows the reference forwards
+ * (accepted + 1 on a rejection, n_mtp otherwise).  *accepted_out is the
+ * count; on a rejection *acc_out = 0, *rej_out = n_mtp - accepted and
+ * logits_out [n_vocab] (may be NULL) receives the rejecting row's logits
+ * with *has_logits = 1; when every draft is accepted *acc_out = accepted,
+ * *rej_out = 0 and *has_logits = 0.  PF_ERR_STATE without heads. */
+pf_status pf_step_mtp(pf_engine* e, int32_t current_token, const float* hidden, const pf_sampling* cfg,
+                      uint64_t seed, uint64_t* draw_index, int32_t* accepted_out, int32_t* acc_out,
+                      int32_t* rej_out, float* logits_out, int32_t* has_logits);
 /* Engine::sample (engine.hpp:54-60) on a host logits row; *draw_index is
  * the stochastic draw counter (incremented when a uniform is used). */
 pf_status pf_sample(pf_engine* e, const float* logits, const pf_sampling* cfg, uint64_t seed,

@@ -331,6 +331,20 @@ class Model:
         lib().orc_mtp_forward(self.h, ptr(hidden, f32p), ptr(out, f32p))
         return out
 
+    def step_mtp(self, token, hidden, has_table, sampling, seed=42, draw=0):
+        """orc_step_mtp (Engine::step_mtp, src/engine.cpp:402-448) on this
+        engine: (accepted, rejecting forward's logits or None,
+        mtp_accepted_out, mtp_rejected_out, draw counter after)."""
+        h = np.ascontiguousarray(hidden, np.float32)
+        lg = np.zeros(self.cfg["n_vocab"], np.float32)
+        d = C.c_uint64(draw)
+        nl = C.c_uint32(0)
+        a = C.c_int32(0)
+        r = C.c_int32(0)
+        k = lib().orc_step_mtp(self.h, int(token), ptr(h, f32p), int(has_table), C.byref(sampling), seed,
+                               C.byref(d), ptr(lg, f32p), C.byref(nl), C.byref(a), C.byref(r))
+        return k, (lg if nl.value else None), a.value, r.value, d.value
+
     def generate(self, prompt, max_new, sampling=None, seed=7):
         s = sampling or Sampling(0.8, 0.95, 40, 1)
         prompt = np.ascontiguousarray(prompt, np.int32)

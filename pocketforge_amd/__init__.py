@@ -119,6 +119,8 @@ SYMBOLS = {
     "pf_forward": (C.c_int32, [vp, i32p, C.c_uint32, f32p, f32p]),
     "pf_mtp_forward": (C.c_int32, [vp, f32p, f32p]),
     "pf_sample": (C.c_int32, [vp, f32p, C.POINTER(Sampling), C.c_uint64, C.POINTER(C.c_uint64), i32p]),
+    "pf_step_mtp": (C.c_int32, [vp, C.c_int32, f32p, C.POINTER(Sampling), C.c_uint64, C.POINTER(C.c_uint64), i32p,
+                                i32p, i32p, f32p, i32p]),
     "pf_generate": (C.c_int32, [vp, i32p, C.c_uint32, C.c_uint32, C.POINTER(Sampling), C.c_uint64, i32p,
                                 C.c_uint32, C.POINTER(GenResult)]),
     "pf_engine_set_max_memory": (C.c_int32, [vp, C.c_size_t]),
@@ -608,6 +610,18 @@ class Engine:
         out = np.zeros((self.cfg["n_mtp"], self.cfg["n_vocab"]), np.float32)
         self.ctx.check(lib().pf_mtp_forward(self.h, P(hidden, f32p), P(out, f32p)), "pf_mtp_forward")
         return out
+
+    def step_mtp(self, token, hidden, sampling, seed=42, draw=0):
+        """Engine::step_mtp on the device: (accepted, rejecting row's logits
+        or None, mtp_accepted_out, mtp_rejected_out, draw counter after)."""
+        hidden = np.ascontiguousarray(hidden, np.float32)
+        lg = np.zeros(self.cfg["n_vocab"], np.float32)
+        d = C.c_uint64(draw)
+        a, acc, rej, has = C.c_int32(0), C.c_int32(0), C.c_int32(0), C.c_int32(0)
+        self.ctx.check(lib().pf_step_mtp(self.h, int(token), P(hidden, f32p), C.byref(sampling), seed, C.byref(d),
+                                         C.byref(a), C.byref(acc), C.byref(rej), P(lg, f32p), C.byref(has)),
+                       "pf_step_mtp")
+        return a.value, (lg if has.value else None), acc.value, rej.value, d.value
 
     def sample(self, logits, sampling, seed, draw_idx):
         logits = np.ascontiguousarray(logits, np.float32)

@@ -425,6 +425,47 @@ __global__ __launch_bounds__(1024) void k_sample_round(const float* __restrict__
     }
 }
 
+// Engine::step_mtp's samples (src/engine.cpp:418-423): block j samples head
+// j's logits with draw st->draw + j when sampling is stochastic (the order of
+// the reference's calls), keeps it as draft j and, for j < n - 1, makes it
+// row j + 1 of the verify pass `pd`; the last block to finish advances the
+// draw counter.  Grid n_mtp, 1024 threads.
+__global__ __launch_bounds__(1024) void k_step_drafts(const float* __restrict__ mlogits, uint32_t V, SamplingCfg cfg,
+                                                      uint64_t seed, DecodeState* st, PassDesc* pd) {
+    __shared__ uint64_t base_s;
+    if (threadIdx.x == 0) base_s = st->draw;
+    __syncthreads();
+    const uint64_t base = base_s;
+    const uint32_t j = blockIdx.x;
+    bool used = false;
+    const int32_t t = sample_row(mlogits + (size_t)j * V, V, cfg, seed, base + j, &used);
+    if (threadIdx.x != 0) return;
+    st->draft[j] = t;
+    if (j + 1u < gridDim.x) pd->tok[j + 1u] = t;
+    const uint32_t done = __hip_atomic_fetch_add(&st->blocks_done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (done == gridDim.x - 1u) {
+        if (used) st->draw = base + gridDim.x;
+        st->blocks_done = 0u;
+    }
+}
+
+// Engine::step_mtp's verification (src/engine.cpp:426-447) of the pass over
+// [current, d0 .. d{n-2}]: block r ranks row r (the first index of its
+// maximum, sample_greedy); the last block to finish counts the rows whose
+// argmax equals draft r up to the first mismatch into round_word.  Grid
+// n_mtp, 1024 threads.
+__global__ __launch_bounds__(1024) void k_step_accept(const float* __restrict__ logits, uint32_t V, DecodeState* st) {
+    const ArgBest b = block_argmax(logits + (size_t)blockIdx.x * V, V);
+    if (threadIdx.x != 0) return;
+    st->row_argmax[blockIdx.x] = b.i;
+    const uint32_t done = __hip_atomic_fetch_add(&st->blocks_done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (done != gridDim.x - 1u) return;
+    st->blocks_done = 0u;
+    uint32_t a = 0;
+    while (a < gridDim.x && st->row_argmax[a] == st->draft[a]) a++;
+    st->round_word = a;
+}
+
 // Pass A setup: forward `cur` at the next position.
 __global__ void k_ctl_pass_a(DecodeState* st, PassDesc* pdA) {
     pdA->pos0 = st->pos;

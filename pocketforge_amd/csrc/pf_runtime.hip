@@ -2415,6 +2415,60 @@ static SamplingCfg to_cfg(const pf_sampling* s) {
     return c;
 }
 
+// Engine::step_mtp (src/engine.cpp:402-448) on the device: the head chain,
+// the drafts (k_step_drafts writes them into the pass descriptor), one pass
+// of n_mtp rows, and the greedy check (k_step_accept); 4 bytes and the draw
+// counter come back, and the rejecting row's logits when a draft fails.
+extern "C" pf_status pf_step_mtp(pf_engine* e, int32_t current_token, const float* hidden, const pf_sampling* cfg,
+                                 uint64_t seed, uint64_t* draw_index, int32_t* accepted_out, int32_t* acc_out,
+                                 int32_t* rej_out, float* logits_out, int32_t* has_logits) {
+    if (!e || !hidden || !accepted_out || !acc_out || !rej_out || !has_logits) return PF_ERR_ARG;
+    pf_ctx* c = e->c;
+    const pf_model_desc& d = e->m->d;
+    const uint32_t NH = d.n_mtp, V = d.n_vocab;
+    if (NH == 0 || NH > MAX_PASS_ROWS) return fail(c, PF_ERR_STATE, "step_mtp needs MTP heads (at most 8)");
+    if (e->nseq != 1) return fail(c, PF_ERR_STATE, "multi-sequence engine: step_mtp serves one sequence");
+    if (current_token < 0 || (uint32_t)current_token >= V) return fail(c, PF_ERR_ARG, "token id out of range");
+    if (e->pos + NH > e->rope_pos) return fail(c, PF_ERR_CAPACITY, "position beyond the engine's max_context");
+    hipStream_t st = c->stream;
+    DecodeState ds{};
+    ds.draw = draw_index ? *draw_index : 0;
+    PassDesc pd{};
+    pd.pos0 = e->pos;
+    pd.m = NH;
+    pd.tok[0] = current_token;
+    PF_HIP(c, hipMemcpyAsync(e->st, &ds, sizeof(ds), hipMemcpyHostToDevice, st));
+    PF_HIP(c, hipMemcpyAsync(e->pdP, &pd, sizeof(pd), hipMemcpyHostToDevice, st));
+    PF_HIP(c, hipMemcpyAsync(e->hiddenA, hidden, (size_t)d.n_embd * 4, hipMemcpyHostToDevice, st));
+    if (pf_status s = mtp_chain(e, e->hiddenA)) return s;
+    hipLaunchKernelGGL(k_step_drafts, dim3(NH), dim3(1024), 0, st, (const float*)e->mlogits, V, to_cfg(cfg), seed,
+                       e->st, e->pdP);
+    if (pf_status s = run_pass(e, e->pdP, NH, e->pos, e->logitsB, nullptr)) return s;
+    hipLaunchKernelGGL(k_step_accept, dim3(NH), dim3(1024), 0, st, (const float*)e->logitsB, V, e->st);
+    PF_LAUNCHED(c);
+    PF_HIP(c, hipMemcpyAsync(&ds, e->st, sizeof(ds), hipMemcpyDeviceToHost, st));
+    PF_HIP(c, hipStreamSynchronize(st));
+    if (pf_status s = ll_check(e)) return s;
+    const uint32_t a = ds.round_word;
+    *accepted_out = (int32_t)a;
+    if (draw_index) *draw_index = ds.draw;
+    if (a < NH) {   // rows 0 .. a were forwarded; row a rejected draft a
+        e->pos += a + 1;
+        *acc_out = 0;
+        *rej_out = (int32_t)(NH - a);
+        *has_logits = 1;
+        if (logits_out)
+            PF_HIP(c, hipMemcpy(logits_out, e->logitsB + (size_t)a * V, (size_t)V * 4, hipMemcpyDeviceToHost));
+    } else {
+        e->pos += NH;
+        *acc_out = (int32_t)a;
+        *rej_out = 0;
+        *has_logits = 0;
+    }
+    e->hidden_valid = false;
+    return PF_OK;
+}
+
 extern "C" pf_status pf_sample(pf_engine* e, const float* logits, const pf_sampling* cfg, uint64_t seed,
                                uint64_t* draw_index, int32_t* token) {
     if (!e || !logits || !token) return PF_ERR_ARG;

@@ -546,26 +546,19 @@ std::pair<int, std::vector<float>> Engine::step_mtp(int32_t current_token, const
     // The heads run on the engine's device-resident tied table; the caller's
     // fp32 table is only checked for emptiness.  Engine::generate passes the
     // dequantized tied table itself (src/engine.cpp:318-319), so the two agree
-    // for the reference's own caller.
-    const uint32_t V = config_.n_vocab, NH = config_.mtp_heads;
-    std::vector<float> mtp_logits((size_t)NH * V);
-    check(dev_->ctx.get(), pf_mtp_forward(dev_->eng, hidden_state.data(), mtp_logits.data()), "pf_mtp_forward");
-    std::vector<int32_t> preds(NH);
-    for (uint32_t h = 0; h < NH; h++) preds[h] = sample(mtp_logits.data() + (size_t)h * V, V);
-    int accepted = 0;
-    for (uint32_t h = 0; h < NH; h++) {
-        const int32_t in = h == 0 ? current_token : preds[h - 1];
-        std::vector<float> hid;
-        std::vector<float> logits = forward_with_hidden({in}, hid);
-        if (sample_greedy(logits.data(), V) == preds[h]) {
-            accepted++;
-        } else {
-            rej_out = (int)NH - accepted;
-            return {accepted, logits};
-        }
-    }
-    acc_out = accepted;
-    return {accepted, {}};
+    // for the reference's own caller.  The drafts are sampled with
+    // Engine::sample's defaults (seed 42, the engine's draw counter) and
+    // verified in one pass on the device (pf_step_mtp).
+    const SamplingConfig dflt;
+    const pf_sampling s{dflt.temperature, dflt.top_p, dflt.top_k, dflt.greedy ? 1 : 0};
+    std::vector<float> logits(config_.n_vocab);
+    int32_t accepted = 0, has = 0;
+    check(dev_->ctx.get(),
+          pf_step_mtp(dev_->eng, current_token, hidden_state.data(), &s, 42, &dev_->draw, &accepted, &acc_out,
+                      &rej_out, logits.data(), &has),
+          "pf_step_mtp");
+    if (!has) logits.clear();
+    return {accepted, logits};
 }
 
 int32_t Engine::sample(const float* logits, uint32_t n_vocab, const SamplingConfig& cfg) {
