@@ -391,6 +391,26 @@ pf_status pf_batch_forward(pf_engine* e, const uint32_t* seqs, uint32_t n, uint3
 pf_status pf_batch_generate(pf_engine* e, const int32_t* prompts, const uint32_t* prompt_lens,
                             uint32_t max_new_tokens, const pf_sampling* cfg, const uint64_t* seeds,
                             int32_t* tokens_out, uint32_t tokens_cap, pf_gen_result* results);
+/* (new) Continuous batching: requests join and leave between rounds.  The
+ * reference serves each request with its own Engine::generate call
+ * (src/forge_server.cpp:280, 398); here every admitted sequence's tokens
+ * and counters equal that call's for its prompt and seed (src/engine.cpp:
+ * 276-396), whatever else runs beside it.  pf_batch_open starts a session
+ * (every slot free; cfg for every request, tokens_cap per slot; it replaces
+ * the token buffers of an earlier pf_batch_generate); pf_batch_admit
+ * prefills a prompt (n_prompt >= 1) into a free slot from an empty cache,
+ * with its own budget and seed; pf_batch_step runs one round (base pass,
+ * drafts, one verify pass, acceptance and corrective, batched over the
+ * generating slots) and lists in finished[] (n_seq entries, may be NULL)
+ * the slots that reached their budget; pf_batch_take copies a slot's
+ * tokens (prompt included) and counters and frees it (a slot still
+ * generating leaves the batch).  Layer skip must be off. */
+pf_status pf_batch_open(pf_engine* e, const pf_sampling* cfg, uint32_t tokens_cap);
+pf_status pf_batch_admit(pf_engine* e, uint32_t seq, const int32_t* prompt, uint32_t n_prompt,
+                         uint32_t max_new_tokens, uint64_t seed);
+pf_status pf_batch_step(pf_engine* e, uint32_t* finished, uint32_t* n_finished);
+pf_status pf_batch_take(pf_engine* e, uint32_t seq, int32_t* tokens_out, uint32_t tokens_cap,
+                        pf_gen_result* result);
 
 #ifdef __cplusplus
 }

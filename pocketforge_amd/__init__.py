@@ -148,6 +148,10 @@ SYMBOLS = {
     "pf_batch_forward": (C.c_int32, [vp, u32p, C.c_uint32, C.c_uint32, i32p, f32p, f32p]),
     "pf_batch_generate": (C.c_int32, [vp, i32p, u32p, C.c_uint32, C.POINTER(Sampling), C.POINTER(C.c_uint64), i32p,
                                       C.c_uint32, C.POINTER(GenResult)]),
+    "pf_batch_open": (C.c_int32, [vp, C.POINTER(Sampling), C.c_uint32]),
+    "pf_batch_admit": (C.c_int32, [vp, C.c_uint32, i32p, C.c_uint32, C.c_uint32, C.c_uint64]),
+    "pf_batch_step": (C.c_int32, [vp, u32p, u32p]),
+    "pf_batch_take": (C.c_int32, [vp, C.c_uint32, i32p, C.c_uint32, C.POINTER(GenResult)]),
 }
 
 _lib = None
@@ -775,3 +779,27 @@ class BatchEngine(Engine):
                                                seeds.ctypes.data_as(C.POINTER(C.c_uint64)), P(toks, i32p), cap,
                                                res), "pf_batch_generate")
         return [toks[i, : res[i].n_tokens].copy() for i in range(self.n_seq)], list(res)
+
+    # continuous batching: requests join and leave between rounds
+    def open(self, sampling=None, tokens_cap=1024):
+        s = sampling or Sampling(0.8, 0.95, 40, 1)
+        self._cap = tokens_cap
+        self.ctx.check(lib().pf_batch_open(self.h, C.byref(s), tokens_cap), "pf_batch_open")
+
+    def admit(self, seq, prompt, max_new, seed=7):
+        p = np.ascontiguousarray(prompt, np.int32)
+        self.ctx.check(lib().pf_batch_admit(self.h, seq, P(p, i32p), len(p), max_new, seed), "pf_batch_admit")
+
+    def step(self):
+        """One round of every generating slot; returns the slots that finished."""
+        fin = np.zeros(self.n_seq, np.uint32)
+        n = C.c_uint32(0)
+        self.ctx.check(lib().pf_batch_step(self.h, P(fin, u32p), C.byref(n)), "pf_batch_step")
+        return [int(x) for x in fin[: n.value]]
+
+    def take(self, seq):
+        """(tokens, GenResult) of a slot, which becomes free."""
+        toks = np.zeros(self._cap, np.int32)
+        r = GenResult()
+        self.ctx.check(lib().pf_batch_take(self.h, seq, P(toks, i32p), self._cap, C.byref(r)), "pf_batch_take")
+        return toks[: r.n_tokens].copy(), r

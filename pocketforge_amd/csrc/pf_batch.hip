@@ -147,6 +147,208 @@ static pf_status batch_mtp_chain(pf_engine* e, const float* h0, uint32_t n, cons
 // verify pass over their [T1, drafts] rows, acceptance and correctives, and
 // the single-token step of the others.  The host reads the decode states
 // back once per round.
+// One decode round of the sequences in `cand` that still generate
+// (n_gen < lim and not stopped by the memory guard): the MTP sequences
+// (src/engine.cpp:304-305: heads on, a stored position, 4 tokens of budget
+// left) take the base pass, T1 and drafts, one verify pass of n_mtp + 1 rows
+// each, acceptance and the corrective; the others a single-token step; all
+// in the same passes.  hs receives every sequence's device state; n_gen,
+// have_row, oom and res[q] are updated for the sequences that ran, and
+// *ran tells whether any did.
+static pf_status batch_round(pf_engine* e, const SamplingCfg& cfg, const std::vector<uint32_t>& cand,
+                             const std::vector<uint32_t>& lim, std::vector<uint32_t>& n_gen,
+                             std::vector<uint8_t>& have_row, std::vector<uint8_t>& oom, pf_gen_result* res,
+                             std::vector<DecodeState>& hs, bool* ran) {
+    pf_ctx* c = e->c;
+    const pf_model_desc& d = e->m->d;
+    hipStream_t st = c->stream;
+    const uint32_t N = e->nseq, V = d.n_vocab, NM = d.n_mtp, R = NM + 1;
+    std::vector<uint32_t> sel(N);
+    *ran = false;
+    // MTP sequences first (src/engine.cpp:304-305), then single-token steps
+    uint32_t nm = 0, na = 0, pos_hi = 0;
+    const bool out_of_memory = e->max_memory && c->bytes > e->max_memory;   // src/engine.cpp:297-301
+    for (int pass = 0; pass < 2; pass++)
+        for (const uint32_t s : cand) {
+            if (n_gen[s] >= lim[s] || oom[s]) continue;
+            if (out_of_memory) { oom[s] = 1; continue; }
+            const bool mtp = e->mtp_enabled && NM > 0 && e->spos[s] > 0 && n_gen[s] + 4 <= lim[s];
+            if (mtp != (pass == 0)) continue;
+            sel[na++] = s;
+            if (mtp) nm++;
+            pos_hi = std::max(pos_hi, e->spos[s]);
+        }
+    if (na == 0) return PF_OK;
+    *ran = true;
+    if ((uint64_t)pos_hi + NM + 2 > e->rope_pos) return fail(c, PF_ERR_CAPACITY, "position beyond the engine's max_context");
+    e->timed_used = 0;
+    e->kev_used = 0;
+    PF_HIP(c, hipMemcpyAsync(e->sel, sel.data(), (size_t)na * 4, hipMemcpyHostToDevice, st));
+    PF_HIP(c, hipEventRecord(e->rev0, st));
+    hipLaunchKernelGGL(k_bctl_pass_a, dim3(1), dim3(256), 0, st, e->st, (const uint32_t*)e->sel, na, e->pdA);
+    TimedPass* tp = nullptr;
+    pf_status s;
+    if ((s = timed_begin(e, false, &tp))) return s;
+    if ((s = run_pass(e, e->pdA, na, 0, e->logitsA, e->hiddenA, true, pos_hi))) return s;
+    if (tp) PF_HIP(c, hipEventRecord(tp->b, st));
+    if (nm) {
+        hipLaunchKernelGGL(k_bsample, dim3(nm), dim3(1024), 0, st, (const float*)e->logitsA, V, V, cfg,
+                           (const uint64_t*)e->seeds, e->st, (const uint32_t*)e->sel, 0u, e->tokens, e->tok_cap,
+                           e->pdB, R, (int32_t)ROLE_T1, 0);
+        if ((s = batch_mtp_chain(e, e->hiddenA, nm, cfg))) return s;
+        if ((s = timed_begin(e, true, &tp))) return s;
+        e->in_verify = true;
+        e->batch_group = R;                      // each MTP sequence's R verify rows
+        s = run_pass(e, e->pdB, nm * R, 0, e->logitsB, nullptr, true, pos_hi + R);
+        e->batch_group = 0;
+        e->in_verify = false;
+        if (s) return s;
+        if (tp) PF_HIP(c, hipEventRecord(tp->b, st));
+        hipLaunchKernelGGL(k_bargmax_rows, dim3(nm * R), dim3(1024), 0, st, (const float*)e->logitsB, V, R,
+                           (const uint32_t*)e->sel, e->st);
+        hipLaunchKernelGGL(k_bctl_accept, dim3((nm + 63) / 64), dim3(64), 0, st, e->st, (const uint32_t*)e->sel,
+                           nm, (const PassDesc*)e->pdB, R, e->tokens, e->tok_cap);
+        if (e->skip_on) launch_skip_commit(e, e->pdB, nm * R, 0, 0, true);
+        hipLaunchKernelGGL(k_bsample, dim3(nm), dim3(1024), 0, st, (const float*)e->logitsB, V, V, cfg,
+                           (const uint64_t*)e->seeds, e->st, (const uint32_t*)e->sel, 0u, e->tokens, e->tok_cap,
+                           e->pdB, R, (int32_t)ROLE_CORRECTIVE, 0);
+    }
+    if (na > nm)
+        hipLaunchKernelGGL(k_bsample, dim3(na - nm), dim3(1024), 0, st, (const float*)e->logitsA, V, V, cfg,
+                           (const uint64_t*)e->seeds, e->st, (const uint32_t*)e->sel, nm, e->tokens, e->tok_cap,
+                           e->pdB, R, (int32_t)ROLE_FALLBACK, 0);
+    PF_LAUNCHED(c);
+    PF_HIP(c, hipEventRecord(e->rev1, st));
+    PF_HIP(c, hipMemcpyAsync(hs.data(), e->st, (size_t)N * sizeof(DecodeState), hipMemcpyDeviceToHost, st));
+    PF_HIP(c, hipStreamSynchronize(st));
+    if ((s = harvest_events(e, 0, e->timed_used, 0, e->kev_used))) return s;
+    if (nm) {
+        float ms = 0;
+        PF_HIP(c, hipEventElapsedTime(&ms, e->rev0, e->rev1));
+        e->round_us += ms * 1000.0;
+        e->round_n++;
+    }
+    for (uint32_t i = 0; i < na; i++) {
+        const uint32_t q = sel[i];
+        const bool mtp = i < nm;
+        res[q].passes += (have_row[q] ? 0 : 1) + (mtp ? 1 : 0);
+        if (mtp) {
+            res[q].rounds++;
+            have_row[q] = (hs[q].round_word & 0xFFu) >= NM;
+        } else {
+            have_row[q] = 0;
+        }
+        n_gen[q] = hs[q].n_gen;
+        e->spos[q] = hs[q].pos;
+    }
+    return PF_OK;
+}
+
+// ---------------------------------------------------- continuous batching
+
+// A session of sequences that join and leave between rounds; each one's
+// tokens equal Engine::generate for its prompt and seed (src/engine.cpp:
+// 276-396) whatever else runs beside it.
+extern "C" pf_status pf_batch_open(pf_engine* e, const pf_sampling* cfg, uint32_t tokens_cap) {
+    if (!e || tokens_cap == 0) return PF_ERR_ARG;
+    const uint32_t N = e->nseq;
+    if (e->tok_cap != tokens_cap || e->tok_alloc < (size_t)N * tokens_cap)
+        if (pf_status s = ensure_tokens(e, tokens_cap)) return s;
+    e->bs_cfg = to_cfg(cfg);
+    e->bs_state.assign(N, 0);
+    e->bs_have.assign(N, 0);
+    e->bs_oom.assign(N, 0);
+    e->bs_ngen.assign(N, 0);
+    e->bs_lim.assign(N, 0);
+    e->bs_res.assign(N, pf_gen_result{});
+    e->bs_hs.assign(N, DecodeState{});
+    e->round_us = 0;
+    e->round_n = 0;
+    e->bs_open = true;
+    return PF_OK;
+}
+
+extern "C" pf_status pf_batch_admit(pf_engine* e, uint32_t seq, const int32_t* prompt, uint32_t n_prompt,
+                                    uint32_t max_new, uint64_t seed) {
+    if (!e || !prompt || n_prompt == 0) return PF_ERR_ARG;
+    pf_ctx* c = e->c;
+    if (!e->bs_open) return fail(c, PF_ERR_STATE, "pf_batch_open first");
+    if (seq >= e->nseq) return fail(c, PF_ERR_ARG, "sequence slot out of range");
+    if (e->bs_state[seq] != 0) return fail(c, PF_ERR_STATE, "sequence slot in use (pf_batch_take frees it)");
+    if (e->skip_on) return fail(c, PF_ERR_UNSUPPORTED, "continuous batching with layer skip on");
+    if (pf_status s = check_tokens(e, prompt, n_prompt)) return s;
+    if ((uint64_t)n_prompt + max_new + 1 > e->tok_cap) return fail(c, PF_ERR_CAPACITY, "tokens_cap < prompt + max_new + 1");
+    if ((uint64_t)n_prompt + max_new + MAX_PASS_ROWS > e->rope_pos)
+        return fail(c, PF_ERR_CAPACITY, "prompt + max_new_tokens exceed the engine's max_context");
+    hipStream_t st = c->stream;
+    batch_sync_in(e);
+    e->spos[seq] = 0;   // a new request starts an empty cache in this slot
+    PF_HIP(c, hipMemcpyAsync(e->tokens + (size_t)seq * e->tok_cap, prompt, (size_t)n_prompt * 4,
+                             hipMemcpyHostToDevice, st));
+    PF_HIP(c, hipMemcpyAsync(e->seeds + seq, &seed, 8, hipMemcpyHostToDevice, st));
+    pf_status s = batch_prefill_seq(e, seq, prompt, n_prompt);
+    if (s) { batch_sync_out(e); return s; }
+    DecodeState h{};
+    h.pos = e->spos[seq];
+    h.cur = prompt[n_prompt - 1];
+    h.n_tokens = n_prompt;
+    e->bs_hs[seq] = h;
+    PF_HIP(c, hipMemcpyAsync(e->st + seq, &e->bs_hs[seq], sizeof(DecodeState), hipMemcpyHostToDevice, st));
+    PF_HIP(c, hipStreamSynchronize(st));
+    batch_sync_out(e);
+    e->bs_state[seq] = 1;
+    e->bs_have[seq] = 0;
+    e->bs_oom[seq] = 0;
+    e->bs_ngen[seq] = 0;
+    e->bs_lim[seq] = max_new;
+    e->bs_res[seq] = pf_gen_result{};
+    return ll_check(e);
+}
+
+extern "C" pf_status pf_batch_step(pf_engine* e, uint32_t* finished, uint32_t* n_finished) {
+    if (!e || !n_finished) return PF_ERR_ARG;
+    pf_ctx* c = e->c;
+    *n_finished = 0;
+    if (!e->bs_open) return fail(c, PF_ERR_STATE, "pf_batch_open first");
+    std::vector<uint32_t> cand;
+    for (uint32_t q = 0; q < e->nseq; q++)
+        if (e->bs_state[q] == 1) cand.push_back(q);
+    bool ran = false;
+    if (!cand.empty()) {
+        batch_sync_in(e);
+        pf_status s = batch_round(e, e->bs_cfg, cand, e->bs_lim, e->bs_ngen, e->bs_have, e->bs_oom, e->bs_res.data(),
+                                  e->bs_hs, &ran);
+        batch_sync_out(e);
+        if (s) return s;
+    }
+    for (const uint32_t q : cand) {
+        if (e->bs_ngen[q] >= e->bs_lim[q] || e->bs_oom[q]) {
+            e->bs_state[q] = 2;
+            if (finished) finished[*n_finished] = q;
+            (*n_finished)++;
+        }
+    }
+    return ran ? ll_check(e) : PF_OK;
+}
+
+extern "C" pf_status pf_batch_take(pf_engine* e, uint32_t seq, int32_t* tokens_out, uint32_t tokens_cap,
+                                   pf_gen_result* res) {
+    if (!e || !tokens_out || !res) return PF_ERR_ARG;
+    pf_ctx* c = e->c;
+    if (!e->bs_open) return fail(c, PF_ERR_STATE, "pf_batch_open first");
+    if (seq >= e->nseq || e->bs_state[seq] == 0) return fail(c, PF_ERR_STATE, "no sequence in that slot");
+    const DecodeState& h = e->bs_hs[seq];
+    const uint32_t nt = std::min(std::min(h.n_tokens, e->tok_cap), tokens_cap);
+    PF_HIP(c, hipMemcpy(tokens_out, e->tokens + (size_t)seq * e->tok_cap, (size_t)nt * 4, hipMemcpyDeviceToHost));
+    *res = e->bs_res[seq];
+    res->n_tokens = nt;
+    res->mtp_accepted = (int32_t)h.accepted;
+    res->mtp_rejected = (int32_t)h.rejected;
+    res->oom_protected = e->bs_oom[seq];
+    e->bs_state[seq] = 0;
+    return PF_OK;
+}
+
 extern "C" pf_status pf_batch_generate(pf_engine* e, const int32_t* prompts, const uint32_t* prompt_lens,
                                        uint32_t max_new, const pf_sampling* scfg, const uint64_t* seeds,
                                        int32_t* tokens_out, uint32_t tokens_cap, pf_gen_result* res) {
@@ -242,87 +444,16 @@ extern "C" pf_status pf_batch_generate(pf_engine* e, const int32_t* prompts, con
     e->aev_used = 0;
     e->round_us = 0;
     e->round_n = 0;
-    std::vector<uint32_t> n_gen(N, 0), sel(N);
+    std::vector<uint32_t> n_gen(N, 0), lim(N, max_new), cand(N);
     std::vector<uint8_t> have_row(N, 0), oom(N, 0);
+    for (uint32_t q = 0; q < N; q++) cand[q] = q;
     for (;;) {
-        // MTP sequences first (src/engine.cpp:304-305), then single-token steps
-        uint32_t nm = 0, na = 0, pos_hi = 0;
-        bool out_of_memory = e->max_memory && c->bytes > e->max_memory;   // src/engine.cpp:297-301
-        for (int pass = 0; pass < 2; pass++)
-            for (uint32_t s = 0; s < N; s++) {
-                if (n_gen[s] >= max_new || oom[s]) continue;
-                if (out_of_memory) { oom[s] = 1; continue; }
-                const bool mtp = e->mtp_enabled && NM > 0 && e->spos[s] > 0 && n_gen[s] + 4 <= max_new;
-                if (mtp != (pass == 0)) continue;
-                sel[na++] = s;
-                if (mtp) nm++;
-                pos_hi = std::max(pos_hi, e->spos[s]);
-            }
-        if (na == 0) break;
-        if ((uint64_t)pos_hi + NM + 2 > e->rope_pos) {
+        bool ran = false;
+        if (pf_status s = batch_round(e, cfg, cand, lim, n_gen, have_row, oom, res, hs, &ran)) {
             batch_sync_out(e);
-            return fail(c, PF_ERR_CAPACITY, "position beyond the engine's max_context");
+            return s;
         }
-        e->timed_used = 0;
-        e->kev_used = 0;
-        PF_HIP(c, hipMemcpyAsync(e->sel, sel.data(), (size_t)na * 4, hipMemcpyHostToDevice, st));
-        PF_HIP(c, hipEventRecord(e->rev0, st));
-        hipLaunchKernelGGL(k_bctl_pass_a, dim3(1), dim3(256), 0, st, e->st, (const uint32_t*)e->sel, na, e->pdA);
-        TimedPass* tp = nullptr;
-        pf_status s;
-        if ((s = timed_begin(e, false, &tp))) return s;
-        if ((s = run_pass(e, e->pdA, na, 0, e->logitsA, e->hiddenA, true, pos_hi))) return s;
-        if (tp) PF_HIP(c, hipEventRecord(tp->b, st));
-        if (nm) {
-            hipLaunchKernelGGL(k_bsample, dim3(nm), dim3(1024), 0, st, (const float*)e->logitsA, V, V, cfg,
-                               (const uint64_t*)e->seeds, e->st, (const uint32_t*)e->sel, 0u, e->tokens, e->tok_cap,
-                               e->pdB, R, (int32_t)ROLE_T1, 0);
-            if ((s = batch_mtp_chain(e, e->hiddenA, nm, cfg))) return s;
-            if ((s = timed_begin(e, true, &tp))) return s;
-            e->in_verify = true;
-            e->batch_group = R;                      // each MTP sequence's R verify rows
-            s = run_pass(e, e->pdB, nm * R, 0, e->logitsB, nullptr, true, pos_hi + R);
-            e->batch_group = 0;
-            e->in_verify = false;
-            if (s) return s;
-            if (tp) PF_HIP(c, hipEventRecord(tp->b, st));
-            hipLaunchKernelGGL(k_bargmax_rows, dim3(nm * R), dim3(1024), 0, st, (const float*)e->logitsB, V, R,
-                               (const uint32_t*)e->sel, e->st);
-            hipLaunchKernelGGL(k_bctl_accept, dim3((nm + 63) / 64), dim3(64), 0, st, e->st, (const uint32_t*)e->sel,
-                               nm, (const PassDesc*)e->pdB, R, e->tokens, e->tok_cap);
-            if (e->skip_on) launch_skip_commit(e, e->pdB, nm * R, 0, 0, true);
-            hipLaunchKernelGGL(k_bsample, dim3(nm), dim3(1024), 0, st, (const float*)e->logitsB, V, V, cfg,
-                               (const uint64_t*)e->seeds, e->st, (const uint32_t*)e->sel, 0u, e->tokens, e->tok_cap,
-                               e->pdB, R, (int32_t)ROLE_CORRECTIVE, 0);
-        }
-        if (na > nm)
-            hipLaunchKernelGGL(k_bsample, dim3(na - nm), dim3(1024), 0, st, (const float*)e->logitsA, V, V, cfg,
-                               (const uint64_t*)e->seeds, e->st, (const uint32_t*)e->sel, nm, e->tokens, e->tok_cap,
-                               e->pdB, R, (int32_t)ROLE_FALLBACK, 0);
-        PF_LAUNCHED(c);
-        PF_HIP(c, hipEventRecord(e->rev1, st));
-        PF_HIP(c, hipMemcpyAsync(hs.data(), e->st, (size_t)N * sizeof(DecodeState), hipMemcpyDeviceToHost, st));
-        PF_HIP(c, hipStreamSynchronize(st));
-        if ((s = harvest_events(e, 0, e->timed_used, 0, e->kev_used))) return s;
-        if (nm) {
-            float ms = 0;
-            PF_HIP(c, hipEventElapsedTime(&ms, e->rev0, e->rev1));
-            e->round_us += ms * 1000.0;
-            e->round_n++;
-        }
-        for (uint32_t i = 0; i < na; i++) {
-            const uint32_t q = sel[i];
-            const bool mtp = i < nm;
-            res[q].passes += (have_row[q] ? 0 : 1) + (mtp ? 1 : 0);
-            if (mtp) {
-                res[q].rounds++;
-                have_row[q] = (hs[q].round_word & 0xFFu) >= NM;
-            } else {
-                have_row[q] = 0;
-            }
-            n_gen[q] = hs[q].n_gen;
-            e->spos[q] = hs[q].pos;
-        }
+        if (!ran) break;
     }
     auto t2 = std::chrono::steady_clock::now();
     batch_sync_out(e);

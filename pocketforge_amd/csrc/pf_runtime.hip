@@ -1397,6 +1397,16 @@ struct pf_engine {
     StackLayer* lw = nullptr;
     bool stack_ok = false;
     bool stack = true;
+    // continuous batching (pf_batch_open / admit / step / take, pf_batch.hip):
+    // per sequence slot its state (0 free, 1 generating, 2 finished), token
+    // budget, generated count, verify-row reuse, memory-guard stop, counters
+    // and the last device state read back
+    bool bs_open = false;
+    SamplingCfg bs_cfg{};
+    std::vector<uint8_t> bs_state, bs_have, bs_oom;
+    std::vector<uint32_t> bs_ngen, bs_lim;
+    std::vector<pf_gen_result> bs_res;
+    std::vector<DecodeState> bs_hs;
 };
 
 template <class T>
