@@ -698,8 +698,8 @@ static void qkv_attn_rows(hipStream_t st, const GemvArgs& a, const AttnGroupArgs
                           hipEvent_t ev1) {
     switch (a.M) {
         case 1: qkv_attn_one<1, P, 1>(st, a, b, tasks, ev0, ev1); break;
-        case 2: case 4: case 5: qkv_attn_one<5, P, 2>(st, a, b, tasks, ev0, ev1); break;
-        case 3: qkv_attn_one<5, P, 3>(st, a, b, tasks, ev0, ev1); break;
+        case 2: case 4: qkv_attn_one<5, P, 2>(st, a, b, tasks, ev0, ev1); break;
+        case 3: case 5: qkv_attn_one<5, P, 3>(st, a, b, tasks, ev0, ev1); break;   // 5 rows: groups of 3 and 2
         case 6: qkv_attn_one<8, P, 3>(st, a, b, tasks, ev0, ev1); break;
         default: qkv_attn_one<8, P, 4>(st, a, b, tasks, ev0, ev1); break;
     }
