@@ -391,16 +391,18 @@ __global__ __launch_bounds__(1024) void k_sample(const float* __restrict__ logit
 // reference's order, T1 then the drafts by head (src/engine.cpp:311, 318-330):
 // block j draws st->draw + j when sampling is stochastic, and the last block
 // to finish (every block has read st->draw by then) advances it past them.
-// Grid 1 + n_mtp, 1024 threads.
+// Grid 1 + n_mtp, 1024 threads; or the same samples in two launches, T1
+// (grid 1, j0 = 0, advance = 0) and then the drafts (grid n_mtp, j0 = 1,
+// advance = 1), which read the same st->draw and take the same draws.
 __global__ __launch_bounds__(1024) void k_sample_round(const float* __restrict__ base_logits,
                                                        const float* __restrict__ mlogits, uint32_t V, SamplingCfg cfg,
                                                        uint64_t seed, DecodeState* st, int32_t* tokens, uint32_t cap,
-                                                       PassDesc* pdB, int32_t h) {
+                                                       PassDesc* pdB, int32_t h, uint32_t j0, int32_t advance) {
     __shared__ uint64_t base_s;
     if (threadIdx.x == 0) base_s = st->draw;
     __syncthreads();
     const uint64_t base = base_s;
-    const uint32_t j = blockIdx.x;
+    const uint32_t j = blockIdx.x + j0;
     bool used = false;
     const float* row = j == 0 ? base_logits : mlogits + (size_t)(j - 1u) * V;
     const int32_t t = sample_row(row, V, cfg, seed, base + j, &used);
@@ -420,7 +422,7 @@ __global__ __launch_bounds__(1024) void k_sample_round(const float* __restrict__
     }
     const uint32_t done = __hip_atomic_fetch_add(&st->blocks_done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     if (done == gridDim.x - 1u) {
-        if (used) st->draw = base + gridDim.x;
+        if (used && advance) st->draw = base + j0 + gridDim.x;
         st->blocks_done = 0u;
     }
 }

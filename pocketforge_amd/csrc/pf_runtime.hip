@@ -503,8 +503,8 @@ static_assert(NOALLOC_SCALE_BYTES >= MAX_GEMM_ROWS * 4, "one scale per GEMM row"
 constexpr uint32_t F32_GROUP = 4;
 
 static void launch_gemv_f32(hipStream_t st, const pf_matrix* W, uint32_t M, const float* h, uint32_t h_stride,
-                            float* y, uint32_t y_stride, const float* y_in) {
-    uint32_t waves = std::min<uint32_t>(W->rows, 4096);
+                            float* y, uint32_t y_stride, const float* y_in, uint32_t max_waves = 4096) {
+    uint32_t waves = std::min<uint32_t>(W->rows, max_waves);
     // whole groups of F32_GROUP rows in one launch (grid y), then the rest
     constexpr uint32_t GR = F32_GROUP;
     for (uint32_t r0 = 0; r0 < M;) {
@@ -534,8 +534,8 @@ static void launch_gemv_f32(hipStream_t st, const pf_matrix* W, uint32_t M, cons
 // Gate and up products of one MTP head with the SiLU product fused:
 // a[m] = silu(Wg h[m]) * (Wu h[m]), rows in chunks of 8.
 static void launch_gemv_f32_glu(hipStream_t st, const pf_matrix* Wg, const pf_matrix* Wu, uint32_t M, const float* h,
-                                uint32_t h_stride, float* a, uint32_t a_stride) {
-    uint32_t waves = std::min<uint32_t>(Wg->rows, 2048);
+                                uint32_t h_stride, float* a, uint32_t a_stride, uint32_t max_waves = 2048) {
+    uint32_t waves = std::min<uint32_t>(Wg->rows, max_waves);
     constexpr uint32_t GR = F32_GROUP;
     for (uint32_t r0 = 0; r0 < M;) {
         const uint32_t mb = std::min(GR, M - r0);
@@ -1397,6 +1397,14 @@ struct pf_engine {
     StackLayer* lw = nullptr;
     bool stack_ok = false;
     bool stack = true;
+    // a second stream for the MTP head chain beside a one-row verify pass
+    // (fork and join events), its launches limited to mtp_side_waves waves
+    // so that they leave the CUs to the verify pass (PF_MTP_SIDE_WAVES);
+    // PF_MTP_OVERLAP=0 keeps them in sequence
+    hipStream_t st2 = nullptr;
+    hipEvent_t evf = nullptr, evj = nullptr;
+    bool mtp_overlap = true;
+    uint32_t mtp_side_waves = 256;
     // continuous batching (pf_batch_open / admit / step / take, pf_batch.hip):
     // per sequence slot its state (0 free, 1 generating, 2 finished), token
     // budget, generated count, verify-row reuse, memory-guard stop, counters
@@ -1545,6 +1553,11 @@ static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t ns
     if (const char* ng = std::getenv("PF_NO_GRAPHS")) e->use_graphs = !(ng[0] == '1');
     PF_HIP(c, hipEventCreate(&e->rev0));
     PF_HIP(c, hipEventCreate(&e->rev1));
+    PF_HIP(c, hipStreamCreateWithFlags(&e->st2, hipStreamNonBlocking));   // default priority
+    PF_HIP(c, hipEventCreateWithFlags(&e->evf, hipEventDisableTiming));
+    PF_HIP(c, hipEventCreateWithFlags(&e->evj, hipEventDisableTiming));
+    if (const char* v = std::getenv("PF_MTP_OVERLAP")) e->mtp_overlap = !(v[0] == '0');
+    if (const char* v = std::getenv("PF_MTP_SIDE_WAVES")) e->mtp_side_waves = std::max(4u, (uint32_t)std::strtoul(v, nullptr, 10));
     // every field of the pass descriptors defined (single-sequence passes of
     // sequence 0) before any kernel reads them
     PassDesc pb{};
@@ -1575,6 +1588,12 @@ extern "C" void pf_engine_destroy(pf_engine* e) {
     if (e->cont_exec) (void)hipGraphExecDestroy(e->cont_exec);
     if (e->rev0) (void)hipEventDestroy(e->rev0);
     if (e->rev1) (void)hipEventDestroy(e->rev1);
+    if (e->st2) {
+        (void)hipStreamSynchronize(e->st2);
+        (void)hipStreamDestroy(e->st2);
+    }
+    if (e->evf) (void)hipEventDestroy(e->evf);
+    if (e->evj) (void)hipEventDestroy(e->evj);
     for (auto& p : e->owned) dfree(e->c, p.first, p.second);
     if (e->tokens) dfree(e->c, e->tokens, e->tok_alloc * 4);
     kv_free(e->c, e->g, &e->kv);
@@ -2391,18 +2410,19 @@ extern "C" pf_status pf_forward(pf_engine* e, const int32_t* tokens, uint32_t n,
 // k of mcur (head 0 reads h0 itself, head k > 0 row k - 1), then the tied
 // unembedding of all the heads' rows in one product (each row's logits are
 // those of its own product), the logits of head k in row k of mlogits.
-static pf_status mtp_chain(pf_engine* e, const float* h0) {
+// waves: at most this many waves per launch (few when the chain runs beside
+// a verify pass, whose launch it should leave the CUs to)
+static pf_status mtp_chain(pf_engine* e, const float* h0, hipStream_t st, uint32_t waves = 4096) {
     pf_ctx* c = e->c;
     const pf_model* m = e->m;
     const pf_model_desc& d = m->d;
-    hipStream_t st = c->stream;
     const uint32_t D = d.n_embd, V = d.n_vocab;
     for (uint32_t k = 0; k < d.n_mtp; k++) {
         const float* hin = k == 0 ? h0 : e->mcur + (size_t)(k - 1) * D;
-        launch_gemv_f32_glu(st, m->mtp[k * 3 + 0], m->mtp[k * 3 + 1], 1, hin, D, e->ma, D);
-        launch_gemv_f32(st, m->mtp[k * 3 + 2], 1, e->ma, D, e->mcur + (size_t)k * D, D, hin);
+        launch_gemv_f32_glu(st, m->mtp[k * 3 + 0], m->mtp[k * 3 + 1], 1, hin, D, e->ma, D, std::min(waves, 2048u));
+        launch_gemv_f32(st, m->mtp[k * 3 + 2], 1, e->ma, D, e->mcur + (size_t)k * D, D, hin, waves);
     }
-    if (d.n_mtp) launch_gemv_f32(st, m->emb, d.n_mtp, e->mcur, D, e->mlogits, V, nullptr);
+    if (d.n_mtp) launch_gemv_f32(st, m->emb, d.n_mtp, e->mcur, D, e->mlogits, V, nullptr, waves);
     PF_LAUNCHED(c);
     return PF_OK;
 }
@@ -2412,7 +2432,7 @@ extern "C" pf_status pf_mtp_forward(pf_engine* e, const float* hidden, float* lo
     pf_ctx* c = e->c;
     const pf_model_desc& d = e->m->d;
     PF_HIP(c, hipMemcpyAsync(e->hiddenA, hidden, d.n_embd * 4, hipMemcpyHostToDevice, c->stream));
-    pf_status s = mtp_chain(e, e->hiddenA);
+    pf_status s = mtp_chain(e, e->hiddenA, c->stream);
     if (s) return s;
     PF_HIP(c, hipMemcpyAsync(logits, e->mlogits, (size_t)d.n_mtp * d.n_vocab * 4, hipMemcpyDeviceToHost, c->stream));
     PF_HIP(c, hipStreamSynchronize(c->stream));
@@ -2450,7 +2470,7 @@ extern "C" pf_status pf_step_mtp(pf_engine* e, int32_t current_token, const floa
     PF_HIP(c, hipMemcpyAsync(e->st, &ds, sizeof(ds), hipMemcpyHostToDevice, st));
     PF_HIP(c, hipMemcpyAsync(e->pdP, &pd, sizeof(pd), hipMemcpyHostToDevice, st));
     PF_HIP(c, hipMemcpyAsync(e->hiddenA, hidden, (size_t)d.n_embd * 4, hipMemcpyHostToDevice, st));
-    if (pf_status s = mtp_chain(e, e->hiddenA)) return s;
+    if (pf_status s = mtp_chain(e, e->hiddenA, st)) return s;
     hipLaunchKernelGGL(k_step_drafts, dim3(NH), dim3(1024), 0, st, (const float*)e->mlogits, V, to_cfg(cfg), seed,
                        e->st, e->pdP);
     if (pf_status s = run_pass(e, e->pdP, NH, e->pos, e->logitsB, nullptr)) return s;
@@ -2530,16 +2550,34 @@ static pf_status round_body(pf_engine* e, bool reuse, bool mtp, const SamplingCf
     }
     if (mtp) {
         // the heads run from the base row's hidden state; T1 and the drafts
-        // are then sampled together, one block each
-        if ((s = mtp_chain(e, base_hidden))) return s;
-        hipLaunchKernelGGL(k_sample_round, dim3(1 + NM), dim3(1024), 0, st, base_logits, (const float*)e->mlogits, V,
-                           cfg, seed, e->st, e->tokens, e->tok_cap, e->pdB, (int32_t)h);
+        // are sampled together, one block each.  A one-row verify segment
+        // needs only T1: T1 is sampled first, and the heads and the drafts
+        // run on the second stream beside the verify pass, joined before the
+        // acceptance (the same draws either way)
+        const bool ovl = e->mtp_overlap && h == 1 && !e->skip_on;
+        if (ovl) {
+            hipLaunchKernelGGL(k_sample_round, dim3(1), dim3(1024), 0, st, base_logits, (const float*)e->mlogits, V,
+                               cfg, seed, e->st, e->tokens, e->tok_cap, e->pdB, (int32_t)h, 0u, 0);
+            PF_HIP(c, hipEventRecord(e->evf, st));
+            PF_HIP(c, hipStreamWaitEvent(e->st2, e->evf, 0));
+            if ((s = mtp_chain(e, base_hidden, e->st2, e->mtp_side_waves))) return s;
+            hipLaunchKernelGGL(k_sample_round, dim3(NM), dim3(1024), 0, e->st2, base_logits,
+                               (const float*)e->mlogits, V, cfg, seed, e->st, e->tokens, e->tok_cap, e->pdB,
+                               (int32_t)h, 1u, 1);
+            PF_HIP(c, hipEventRecord(e->evj, e->st2));
+        } else {
+            if ((s = mtp_chain(e, base_hidden, st))) return s;
+            hipLaunchKernelGGL(k_sample_round, dim3(1 + NM), dim3(1024), 0, st, base_logits,
+                               (const float*)e->mlogits, V, cfg, seed, e->st, e->tokens, e->tok_cap, e->pdB,
+                               (int32_t)h, 0u, 1);
+        }
         if ((s = timed_begin(e, true, &tp))) return s;
         e->in_verify = true;
         s = run_pass(e, e->pdB, h, e->pos + 1, e->logitsB, e->hiddenB);
         e->in_verify = false;
         if (s) return s;
         if (tp) PF_HIP(c, hipEventRecord(tp->b, st));
+        if (ovl) PF_HIP(c, hipStreamWaitEvent(st, e->evj, 0));
         hipLaunchKernelGGL(k_verify_accept, dim3(h), dim3(1024), 0, st, (const float*)e->logitsB, V, V, e->st,
                            (const PassDesc*)e->pdB, e->tokens, e->tok_cap, greedy ? 1 : 0);
         if (e->skip_on) launch_skip_commit(e, e->pdB, NM + 1, 0, 0, true);
