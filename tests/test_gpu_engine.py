@@ -242,6 +242,26 @@ def test_generate_without_graphs_matches(gpu, tiny_weights, monkeypatch):
     assert (res.mtp_accepted, res.mtp_rejected) == (oa, orj)
 
 
+@pytest.mark.parametrize("overlap", ["1", "0"])
+@pytest.mark.parametrize("graphs", ["1", "0"])
+def test_generate_mtp_overlap(gpu, tiny_weights, monkeypatch, overlap, graphs):
+    """The MTP head chain and the drafts' sampling on a second stream beside
+    a one-row verify segment (PF_MTP_OVERLAP=1, the default) or after it
+    (0), replayed from graphs or issued one by one: with top-p sampling and
+    drafts both accepted and rejected, the draws, tokens and counters equal
+    the oracle's."""
+    cfg, _ = tiny_weights
+    w = _zero_mats(W.make_weights(cfg, seed=31, std=0.15))
+    monkeypatch.setenv("PF_MTP_OVERLAP", overlap)
+    if graphs == "0":
+        monkeypatch.setenv("PF_NO_GRAPHS", "1")
+    prompt = W.prompt_ids(12, cfg["n_vocab"], seed=4)
+    toks, res, ot, oa, orj = _gen_both(gpu, cfg, w, prompt, 60, TOP_P, seed=99)
+    np.testing.assert_array_equal(toks, ot)
+    assert (res.mtp_accepted, res.mtp_rejected) == (oa, orj)
+    assert oa > 10 and orj > 10
+
+
 def test_profiled_generate_matches(gpu, tiny_weights):
     cfg, w = tiny_weights
     m = pf.Model(gpu, cfg, w)
