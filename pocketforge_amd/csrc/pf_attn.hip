@@ -611,15 +611,28 @@ __global__ __launch_bounds__(512) void k_attn_seq(const PassDesc* __restrict__ p
     for (uint32_t r = 0; r < NR; r++) acc[r] = 0.0f;
     if (t < ntile) {
         const float ksv = ksc[t];
+        const float* qo = lds_opaque(qs);
 #pragma unroll
         for (int p = 0; p < PARTS; p++) {
             const int4 w4 = kt[p * AS_TILE + (t ^ (uint32_t)p)];
             const int wv4[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
-            for (int b = 0; b < 16; b++) {
-                const float kf = (float)(int8_t)((wv4[b >> 2] >> (8 * (b & 3))) & 0xFF) * ksv;
+            for (int b4 = 0; b4 < 4; b4++) {
+                float qc[NR][4];
 #pragma unroll
-                for (uint32_t r = 0; r < NR; r++) acc[r] = __builtin_fmaf(qs[r * 128 + p * 16 + b], kf, acc[r]);
+                for (uint32_t r = 0; r < NR; r++) {
+                    const float4 q4 = *reinterpret_cast<const float4*>(&qo[r * 128 + p * 16 + 4 * b4]);
+                    qc[r][0] = q4.x;
+                    qc[r][1] = q4.y;
+                    qc[r][2] = q4.z;
+                    qc[r][3] = q4.w;
+                }
+#pragma unroll
+                for (int bb = 0; bb < 4; bb++) {
+                    const float kf = (float)(int8_t)((wv4[b4] >> (8 * bb)) & 0xFF) * ksv;
+#pragma unroll
+                    for (uint32_t r = 0; r < NR; r++) acc[r] = __builtin_fmaf(qc[r][bb], kf, acc[r]);
+                }
             }
         }
     }
@@ -1158,11 +1171,12 @@ __device__ __forceinline__ void attn_group_body(const PassDesc* __restrict__ pd,
         // part p's fmaf steps run (the order of the steps is unchanged)
         const float ksv = ksc[t];
         int4 wn = kt[t];
+        const float* qo = lds_opaque(qs);
         float4 qn[NR][4];
 #pragma unroll
         for (int r = 0; r < NR; r++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) qn[r][i] = *reinterpret_cast<const float4*>(&qs[r * 128 + 4 * i]);
+            for (int i = 0; i < 4; i++) qn[r][i] = *reinterpret_cast<const float4*>(&qo[r * 128 + 4 * i]);
 #pragma unroll
         for (int p = 0; p < PARTS; p++) {
             const int4 w4 = wn;
@@ -1182,7 +1196,7 @@ __device__ __forceinline__ void attn_group_body(const PassDesc* __restrict__ pd,
                 for (int r = 0; r < NR; r++)
 #pragma unroll
                     for (int i = 0; i < 4; i++)
-                        qn[r][i] = *reinterpret_cast<const float4*>(&qs[r * 128 + (p + 1) * 16 + 4 * i]);
+                        qn[r][i] = *reinterpret_cast<const float4*>(&qo[r * 128 + (p + 1) * 16 + 4 * i]);
             }
             const int wv4[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll

@@ -329,6 +329,17 @@ __device__ __forceinline__ void quantize_row_block(const float (&x)[PER], uint32
     if (threadIdx.x == 0) *scale_out = (amax == 0.0f) ? 1.0f : amax / 127.0f;
 }
 
+// An LDS pointer (16-byte aligned) whose address sits in a VGPR the
+// compiler cannot fold: reads at constant offsets from it carry the offset
+// in the instruction instead of materialising each address in a register of
+// its own.
+template <typename T>
+__device__ __forceinline__ const T* lds_opaque(const T* p) {
+    uint32_t z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    return reinterpret_cast<const T*>(__builtin_assume_aligned(reinterpret_cast<const uint8_t*>(p) + z, 16));
+}
+
 // ------------------------------------------------------------- LL words
 // Values handed from workgroups of one launch to later workgroups of the
 // same launch: 8-byte words (value bits, flag) written with one device-scope
