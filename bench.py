@@ -260,16 +260,23 @@ def main():
     times, gens, accs, rejs, rounds, round_us = [], [], [], [], [], []
     for i in range(args.steps):
         dt, toks, res = step(False)
-        r_us, r_n = eng.round_time()
         times.append(dt)
         gens.append(len(toks) - 1)
         accs.append(res.mtp_accepted)
         rejs.append(res.mtp_rejected)
         rounds.append(res.rounds)
-        round_us.append((r_us, r_n))
         log(f"step {i}: {gens[-1]} tokens in {dt * 1e3:.1f} ms ({gens[-1] / dt:.1f} tok/s), rounds {res.rounds}, "
-            f"accepted {res.mtp_accepted}, device time per MTP round {r_us:.1f} us")
+            f"accepted {res.mtp_accepted}")
     value = sum(gens) / sum(times)
+    # the device time per round from one more step of the same decode with
+    # HIP events around every round (pf_engine_set_round_timing; the timed
+    # steps run without them, whose recording costs wall time)
+    eng.set_round_timing(True)
+    step(False)
+    r_us, r_n = eng.round_time()
+    eng.set_round_timing(False)
+    round_us.append((r_us, r_n))
+    log(f"round-timed step: device time per MTP round {r_us:.1f} us over {r_n} rounds")
     # one more decode of the same workload, kernels issued one by one with
     # HIP start/stop events attached to every layer launch of the decode
     # passes (k_stack for one row)

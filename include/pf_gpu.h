@@ -330,8 +330,15 @@ pf_status pf_engine_set_layer_skip(pf_engine* e, float threshold, uint32_t inter
  * incremented, src/engine.cpp:393). */
 pf_status pf_engine_layer_skip_count(pf_engine* e, uint64_t* count);
 
+/* HIP events around every decode segment of pf_generate (on: 1), which
+ * pf_engine_round_time reports; off by default, since recording them costs
+ * about 10 us of wall time per round.  No counterpart in the reference:
+ * instrumentation for benchmarks and profilers. */
+pf_status pf_engine_set_round_timing(pf_engine* e, int32_t on);
 /* Average device time (us, HIP events on the engine's stream) of the MTP
- * rounds of the last pf_generate: base pass + draft + verify + accept. */
+ * rounds of the last pf_generate run with round timing on: base pass +
+ * draft + verify + accept (0 with it off; rounds counts the rounds either
+ * way). */
 pf_status pf_engine_round_time(const pf_engine* e, double* round_us, uint32_t* rounds);
 /* Average device time in microseconds of the verify passes (every verify
  * segment) and base passes of the last pf_generate run without captured

@@ -137,6 +137,7 @@ SYMBOLS = {
     "pf_engine_pass_times": (C.c_int32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_double), u32p, u32p]),
     "pf_engine_profile": (C.c_int32, [vp, C.c_int32]),
     "pf_engine_round_time": (C.c_int32, [vp, C.POINTER(C.c_double), u32p]),
+    "pf_engine_set_round_timing": (C.c_int32, [vp, C.c_int32]),
     "pf_engine_gemv_stats": (C.c_int32, [vp, u32p, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "pf_engine_attn_stats": (C.c_int32, [vp, u32p, C.POINTER(C.c_double)]),
     "pf_engine_gemv_by_size": (C.c_int32, [vp, C.c_uint32, C.POINTER(C.c_double), u32p, C.POINTER(C.c_double),
@@ -677,6 +678,11 @@ class Engine:
         kernels one by one with per-dispatch events on the verify passes, 2
         kernels one by one with events around each pass only."""
         self.ctx.check(lib().pf_engine_profile(self.h, int(enable)), "pf_engine_profile")
+
+    def set_round_timing(self, on=True):
+        """HIP events around every decode segment (pf_engine_set_round_timing),
+        for round_time(); off by default."""
+        self.ctx.check(lib().pf_engine_set_round_timing(self.h, int(bool(on))), "pf_engine_set_round_timing")
 
     def round_time(self):
         us, n = C.c_double(0), C.c_uint32(0)
