@@ -480,6 +480,13 @@ __global__ void k_ctl_pass_a(DecodeState* st, PassDesc* pdA) {
 }
 
 // The last verify row already holds F(cur) at position st->pos.
+// The round word into the pinned host word the host reads after a decode
+// segment (fine-grained host memory, one system-scope store), as the
+// segment's last command.
+__global__ void k_word_out(const DecodeState* st, uint32_t* out) {
+    if (threadIdx.x == 0) __hip_atomic_store(out, st->round_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 __global__ void k_ctl_reuse_row(DecodeState* st) {
     st->pos += 1;
     st->have_row4 = 0;

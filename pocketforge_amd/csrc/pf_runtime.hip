@@ -1305,7 +1305,8 @@ struct pf_engine {
     int32_t* tokens = nullptr;
     uint32_t tok_cap = 0;         // token-buffer capacity of each sequence
     size_t tok_alloc = 0;         // elements allocated (nseq * tok_cap)
-    uint32_t* word = nullptr;   // pinned readback
+    uint32_t* word = nullptr;   // pinned readback (fine-grained), written by k_word_out
+    uint32_t* word_dev = nullptr;   // its device address
     // multi-sequence engines (pf_batch_*): nseq sequences, each with its own
     // KV planes, decode state (st[s]) and token buffer (tokens + s * tok_cap)
     uint32_t nseq = 1;
@@ -1549,7 +1550,8 @@ static pf_status engine_create(pf_model* m, const pf_cache_desc* cd, uint32_t ns
     if (const char* v = std::getenv("PF_O_FFN")) e->o_ffn = !(v[0] == '0');
     if (const char* v = std::getenv("PF_LAYER")) e->layer_fuse = !(v[0] == '0');
     if (const char* v = std::getenv("PF_STACK")) e->stack = !(v[0] == '0');
-    if (hipHostMalloc((void**)&e->word, 64, hipHostMallocDefault) != hipSuccess) {
+    if (hipHostMalloc((void**)&e->word, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
+        hipHostGetDevicePointer((void**)&e->word_dev, e->word, 0) != hipSuccess) {
         pf_engine_destroy(e);
         return fail(c, PF_ERR_HIP, "hipHostMalloc failed");
     }
@@ -2587,6 +2589,7 @@ static pf_status round_body(pf_engine* e, bool reuse, bool mtp, const SamplingCf
         if (!greedy)
             hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, e->logitsB, V, -1, V, cfg, seed, e->st,
                                e->tokens, e->tok_cap, (int32_t)ROLE_CORRECTIVE, (int32_t*)nullptr);
+        hipLaunchKernelGGL(k_word_out, dim3(1), dim3(64), 0, st, (const DecodeState*)e->st, e->word_dev);
     } else {
         hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, base_logits, V, 0, V, cfg, seed, e->st, e->tokens,
                            e->tok_cap, (int32_t)ROLE_FALLBACK, (int32_t*)nullptr);
@@ -2618,6 +2621,7 @@ static pf_status segment_body(pf_engine* e, const SamplingCfg& cfg, uint64_t see
     if (!greedy)
         hipLaunchKernelGGL(k_sample, dim3(1), dim3(1024), 0, st, e->logitsB, V, -1, V, cfg, seed, e->st, e->tokens,
                            e->tok_cap, (int32_t)ROLE_CORRECTIVE, (int32_t*)nullptr);
+    hipLaunchKernelGGL(k_word_out, dim3(1), dim3(64), 0, st, (const DecodeState*)e->st, e->word_dev);
     PF_LAUNCHED(c);
     return PF_OK;
 }
@@ -2772,7 +2776,6 @@ extern "C" pf_status pf_generate(pf_engine* e, const int32_t* prompt, uint32_t n
             ev[3] = e->kev_used;
         }
         if (e->round_timing) PF_HIP(c, hipEventRecord(e->rev1, st));
-        if (mtp) PF_HIP(c, hipMemcpyAsync(e->word, &e->st->round_word, 4, hipMemcpyDeviceToHost, st));
         PF_HIP(c, hipStreamSynchronize(st));
         if (pf_status s = harvest_events(e, ev[0], ev[1], ev[2], ev[3])) return s;
         if (mtp && e->round_timing) {
